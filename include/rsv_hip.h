@@ -1,0 +1,303 @@
+/*
+ * rsv_hip.h -- C-ABI of librsv_hip.so, the MI355X (gfx950) backend of the
+ * rwkv-rsv RWKV-7 forward step.
+ *
+ * Each entry point replaces one method of the reference's backend trait
+ * `ComputeBackend` (reference: src/backend.rs:48-985); the cited line is the
+ * trait method it implements.  A Rust `backend_hip.rs` binds these symbols
+ * one-to-one: TensorId is a uint32_t, Int8Handle is
+ * `rsv_int8`, slices are (pointer, length) pairs, and every call returns 0 on
+ * success or a non-zero status whose text is `rsv_last_error()`; the Rust
+ * side turns that into `Err(Box<dyn Error>)`.
+ *
+ * Conventions shared by every op:
+ *  - One in-order HIP stream per context; ops are enqueued, downloads
+ *    synchronise (backend_cuda.rs:1140-1151 semantics).
+ *  - Per-session tensors are [batch, ...] slot-major; weights are shared.
+ *  - Linear weights are [out, in] row-major ("A[m,k]"): int8 as the reference
+ *    format (idx = u8[m,k] packed 4 per u32 low byte first, sz = u32[m,k/128]
+ *    with fp16 scale in the low half and fp16 zero in the high half), fp16 as
+ *    F16 tensors.  LoRA matrices are F16 [out, in].
+ *  - Token slots hold u32 bit patterns (F32 or U32 tensors).
+ */
+#ifndef RSV_HIP_H
+#define RSV_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct rsv_ctx rsv_ctx;
+
+enum rsv_dtype { RSV_F32 = 0, RSV_F16 = 1, RSV_U32 = 2 };
+
+/* Int8Handle (backend.rs:36-44). */
+typedef struct rsv_int8 {
+    uint32_t idx; /* U32 tensor, m*k/4 words */
+    uint32_t sz;  /* U32 tensor, m*k/128 words */
+    uint64_t m;
+    uint64_t k;
+} rsv_int8;
+
+/* ---- context, errors (create_backend backend.rs:1019; R<T> runtime.rs:18) */
+int rsv_create(int device, rsv_ctx **out);
+int rsv_destroy(rsv_ctx *ctx);
+const char *rsv_last_error(void); /* thread-local text of the last failure */
+int rsv_device_name(rsv_ctx *ctx, char *buf, size_t len);
+
+/* ---- tensors (backend.rs:50-60, 671-679) */
+int rsv_tensor_create(rsv_ctx *ctx, uint64_t len, int dtype, uint32_t *id);  /* :50 */
+int rsv_tensor_free(rsv_ctx *ctx, uint32_t id);                              /* :675 */
+int rsv_drop_host(rsv_ctx *ctx, uint32_t id);                                /* :673 (no host copy is kept: no-op) */
+int rsv_clear_cache(rsv_ctx *ctx);                                           /* :671 */
+int rsv_tensor_len(rsv_ctx *ctx, uint32_t id, uint64_t *len, int *dtype);
+/* F16 tensors convert from f32 with round-to-nearest-even. */
+int rsv_upload(rsv_ctx *ctx, uint32_t id, const float *data, uint64_t len);                  /* :51 */
+int rsv_upload_part(rsv_ctx *ctx, uint32_t id, uint64_t offset, const float *data, uint64_t len); /* :54 */
+int rsv_upload_u32(rsv_ctx *ctx, uint32_t id, const uint32_t *data, uint64_t len);           /* :58 */
+/* Raw-byte upload (u8 int8_idx payloads, fp16 bit patterns); no conversion. */
+int rsv_upload_bytes(rsv_ctx *ctx, uint32_t id, const void *data, uint64_t nbytes);
+int rsv_download(rsv_ctx *ctx, uint32_t id, float *out, uint64_t len);                      /* :59 */
+int rsv_download_u32(rsv_ctx *ctx, uint32_t id, uint32_t *out, uint64_t len);                /* :60 */
+int rsv_copy_device(rsv_ctx *ctx, uint32_t src, uint32_t dst);                              /* :679 */
+int rsv_copy_device_f16(rsv_ctx *ctx, uint32_t src, uint32_t dst);                          /* :155 */
+/* Share another context's tensors (same device, not freed by this ctx). :141 */
+int rsv_import_tensors(rsv_ctx *ctx, rsv_ctx *src);
+int rsv_synchronize(rsv_ctx *ctx);
+
+/* ---- batching and graphs (backend.rs:63-109) */
+int rsv_begin_batch(rsv_ctx *ctx);        /* :63 */
+int rsv_end_batch(rsv_ctx *ctx);          /* :64 (enqueue only; download syncs) */
+int rsv_graph_begin(rsv_ctx *ctx);        /* :75 */
+int rsv_graph_end(rsv_ctx *ctx);          /* :79 */
+int rsv_graph_replay(rsv_ctx *ctx);       /* :83 */
+int rsv_supports_graph_capture(rsv_ctx *ctx); /* :88, returns 1 */
+int rsv_prefill_graph_valid(rsv_ctx *ctx, uint64_t t, int *valid); /* :95 */
+int rsv_prefill_graph_begin(rsv_ctx *ctx, uint64_t t);             /* :99 */
+int rsv_prefill_graph_end(rsv_ctx *ctx);                           /* :103 */
+int rsv_prefill_graph_replay(rsv_ctx *ctx);                        /* :107 */
+
+/* ---- token / sampler slots (backend.rs:113-135, 634, 954) */
+int rsv_store_token(rsv_ctx *ctx, uint32_t tok, uint32_t token);   /* :113, stream-ordered */
+int rsv_store_tokens(rsv_ctx *ctx, uint32_t tok, const uint32_t *tokens, uint64_t batch);
+int rsv_store_sampler(rsv_ctx *ctx, uint32_t sampler, float temperature, uint32_t top_k, float top_p,
+                      uint32_t seed, float repetition_penalty, float frequency_penalty,
+                      float presence_penalty, uint32_t hist_len);                      /* :954 */
+int rsv_store_sampler_async(rsv_ctx *ctx, uint32_t sampler, uint64_t row, float temperature,
+                            uint32_t top_k, float top_p, uint32_t seed, float repetition_penalty,
+                            float frequency_penalty, float presence_penalty, uint32_t hist_len); /* :119 */
+int rsv_store_sampler_async_batch(rsv_ctx *ctx, uint32_t sampler, uint64_t row, float temperature,
+                                  uint32_t top_k, float top_p, const uint32_t *seeds, uint64_t batch,
+                                  float repetition_penalty, float frequency_penalty,
+                                  float presence_penalty, uint32_t hist_len);            /* :634 */
+uint64_t rsv_sampler_async_rows(rsv_ctx *ctx);                                          /* :135 */
+
+/* ---- embedding gather (backend.rs:147, 449).  src may be F16 or F32. */
+int rsv_gather_row_device_f16(rsv_ctx *ctx, uint32_t src, uint32_t dst, uint32_t tok, uint64_t c);
+int rsv_gather_rows_device_f16(rsv_ctx *ctx, uint32_t src, uint32_t dst, uint32_t tok, uint64_t c,
+                               uint64_t batch);
+
+/* ---- normalisation (backend.rs:171, 185, 209, 461, 487) */
+int rsv_norm(rsv_ctx *ctx, uint32_t x, uint32_t gamma, uint32_t beta, uint32_t y, uint64_t c,
+             uint64_t h, float eps, uint64_t rows);
+int rsv_norm_lerp6(rsv_ctx *ctx, uint32_t x, uint32_t state, uint32_t gamma, uint32_t beta,
+                   uint32_t x_r, uint32_t x_w, uint32_t x_k, uint32_t x_v, uint32_t x_a, uint32_t x_g,
+                   uint32_t o_r, uint32_t o_w, uint32_t o_k, uint32_t o_v, uint32_t o_a, uint32_t o_g,
+                   uint64_t c, float eps);
+int rsv_norm_lerp6_batch(rsv_ctx *ctx, uint32_t x, uint32_t state, uint32_t gamma, uint32_t beta,
+                         uint32_t x_r, uint32_t x_w, uint32_t x_k, uint32_t x_v, uint32_t x_a,
+                         uint32_t x_g, uint32_t o_r, uint32_t o_w, uint32_t o_k, uint32_t o_v,
+                         uint32_t o_a, uint32_t o_g, uint64_t c, float eps, uint64_t batch);
+int rsv_cmix_norm_lerp(rsv_ctx *ctx, uint32_t x, uint32_t state, uint32_t gamma, uint32_t beta,
+                       uint32_t x_k, uint32_t out_xb, uint64_t c, float eps);
+int rsv_cmix_norm_lerp_batch(rsv_ctx *ctx, uint32_t x, uint32_t state, uint32_t gamma, uint32_t beta,
+                             uint32_t x_k, uint32_t out_xb, uint64_t c, float eps, uint64_t batch);
+
+/* ---- WKV7 time-mix state update (backend.rs:223, 566) */
+int rsv_fuse_ka_dplr_norm(rsv_ctx *ctx, uint32_t s, uint32_t k, uint32_t k_k, uint32_t a, uint32_t k_a,
+                          uint32_t r, uint32_t v, uint32_t w, uint32_t ln_x_w, uint32_t ln_x_b,
+                          uint32_t r_k, uint32_t k_mod, uint32_t y, uint32_t y_norm, uint64_t h,
+                          uint64_t n, float eps, float gn_eps);
+int rsv_fuse_ka_dplr_norm_batch(rsv_ctx *ctx, uint32_t s, uint32_t k, uint32_t k_k, uint32_t a,
+                                uint32_t k_a, uint32_t r, uint32_t v, uint32_t w, uint32_t ln_x_w,
+                                uint32_t ln_x_b, uint32_t r_k, uint32_t k_mod, uint32_t y,
+                                uint32_t y_norm, uint64_t h, uint64_t n, float eps, float gn_eps,
+                                uint64_t batch);
+
+/* ---- fused stage-1 projections (backend.rs:247, 278, 503):
+ * r,k,v = x{r,k,v} W^T; v_mid = xv V1^T; w_mid = tanh(xw W1^T); a_mid = xa A1^T;
+ * g_mid = xg G1^T. */
+int rsv_gemv_rkv_stage1(rsv_ctx *ctx, uint32_t rw, uint32_t kw, uint32_t vw, uint32_t v1, uint32_t w1,
+                        uint32_t a1, uint32_t g1, uint32_t xr, uint32_t xk, uint32_t xv, uint32_t xw,
+                        uint32_t xa, uint32_t xg, uint32_t r, uint32_t k, uint32_t v, uint32_t v_mid,
+                        uint32_t w_mid, uint32_t a_mid, uint32_t g_mid, uint64_t c, uint64_t vm,
+                        uint64_t wm, uint64_t am, uint64_t gm);
+int rsv_gemv_int8_rkv_stage1(rsv_ctx *ctx, const rsv_int8 *rw, const rsv_int8 *kw, const rsv_int8 *vw,
+                             uint32_t v1, uint32_t w1, uint32_t a1, uint32_t g1, uint32_t xr,
+                             uint32_t xk, uint32_t xv, uint32_t xw, uint32_t xa, uint32_t xg,
+                             uint32_t r, uint32_t k, uint32_t v, uint32_t v_mid, uint32_t w_mid,
+                             uint32_t a_mid, uint32_t g_mid, uint64_t c, uint64_t vm, uint64_t wm,
+                             uint64_t am, uint64_t gm);
+int rsv_gemv_int8_rkv_stage1_batch(rsv_ctx *ctx, const rsv_int8 *rw, const rsv_int8 *kw,
+                                   const rsv_int8 *vw, uint32_t v1, uint32_t w1, uint32_t a1,
+                                   uint32_t g1, uint32_t xr, uint32_t xk, uint32_t xv, uint32_t xw,
+                                   uint32_t xa, uint32_t xg, uint32_t r, uint32_t k, uint32_t v,
+                                   uint32_t v_mid, uint32_t w_mid, uint32_t a_mid, uint32_t g_mid,
+                                   uint64_t c, uint64_t vm, uint64_t wm, uint64_t am, uint64_t gm,
+                                   uint64_t batch);
+int rsv_gemv_rkv_stage1_batch(rsv_ctx *ctx, uint32_t rw, uint32_t kw, uint32_t vw, uint32_t v1,
+                              uint32_t w1, uint32_t a1, uint32_t g1, uint32_t xr, uint32_t xk,
+                              uint32_t xv, uint32_t xw, uint32_t xa, uint32_t xg, uint32_t r,
+                              uint32_t k, uint32_t v, uint32_t v_mid, uint32_t w_mid, uint32_t a_mid,
+                              uint32_t g_mid, uint64_t c, uint64_t vm, uint64_t wm, uint64_t am,
+                              uint64_t gm, uint64_t batch);
+
+/* ---- LoRA stage 2 (backend.rs:309, 536):
+ * w = exp(scale*sigmoid(w_mid W2^T + w0)); a = sigmoid(a_mid A2^T + a0);
+ * v += sigmoid(v_mid V2^T + v0) * (v_first - v); g = sigmoid(g_mid) G2^T.
+ * scale_w is a 1-element F32 tensor (-1/sqrt(e)). */
+int rsv_gemv_lowrank_chain4(rsv_ctx *ctx, uint32_t w2, uint32_t a2, uint32_t v2, uint32_t g2,
+                            uint32_t w_mid, uint32_t a_mid, uint32_t v_mid, uint32_t g_mid,
+                            uint32_t w0, uint32_t a0, uint32_t v0, uint32_t scale_w, uint32_t v_first,
+                            uint32_t w_out, uint32_t a_out, uint32_t v_inout, uint32_t g_out,
+                            uint64_t c, uint64_t wm, uint64_t am, uint64_t vm, uint64_t gm);
+int rsv_gemv_lowrank_chain4_batch(rsv_ctx *ctx, uint32_t w2, uint32_t a2, uint32_t v2, uint32_t g2,
+                                  uint32_t w_mid, uint32_t a_mid, uint32_t v_mid, uint32_t g_mid,
+                                  uint32_t w0, uint32_t a0, uint32_t v0, uint32_t scale_w,
+                                  uint32_t v_first, uint32_t w_out, uint32_t a_out, uint32_t v_inout,
+                                  uint32_t g_out, uint64_t c, uint64_t wm, uint64_t am, uint64_t vm,
+                                  uint64_t gm, uint64_t batch);
+
+/* ---- weight GEMV with fused dequant (backend.rs:160, 337-415).  Shapes:
+ * w = [m, k]; x = [n, k]; y = [n, m] (n = batch). */
+int rsv_gemv_f16(rsv_ctx *ctx, uint32_t w, uint32_t x, uint32_t y, uint64_t m, uint64_t k, uint64_t n);
+int rsv_gemv_f16_relu2(rsv_ctx *ctx, uint32_t w, uint32_t x, uint32_t y, uint64_t m, uint64_t k, uint64_t n);
+int rsv_gemv_f16_mul_add(rsv_ctx *ctx, uint32_t w, uint32_t x, uint32_t g, uint32_t y, uint64_t m,
+                         uint64_t k, uint64_t n);
+int rsv_gemv_f16_add(rsv_ctx *ctx, uint32_t w, uint32_t x, uint32_t y, uint64_t m, uint64_t k, uint64_t n);
+int rsv_gemv_int8_relu2(rsv_ctx *ctx, const rsv_int8 *w, uint32_t x, uint32_t y, uint64_t m, uint64_t k,
+                        uint64_t n);
+int rsv_gemv_int8_mul_add(rsv_ctx *ctx, const rsv_int8 *w, uint32_t x, uint32_t g, uint32_t y, uint64_t m,
+                          uint64_t k, uint64_t n);
+int rsv_gemv_int8_add(rsv_ctx *ctx, const rsv_int8 *w, uint32_t x, uint32_t y, uint64_t m, uint64_t k,
+                      uint64_t n);
+int rsv_gemv_int8_plain(rsv_ctx *ctx, const rsv_int8 *w, uint32_t x, uint32_t y, uint64_t m, uint64_t k,
+                        uint64_t n);
+int rsv_supports_sparse_ffn(rsv_ctx *ctx); /* :439, returns 0: the dense int8/fp16 path is used */
+
+/* ---- int8 dequant to f32 / f16 (model.rs:234-252; backend.rs:756) */
+int rsv_dequant_int8_f32(rsv_ctx *ctx, const rsv_int8 *a, uint32_t out);
+int rsv_dequant_int8_to_f16(rsv_ctx *ctx, const rsv_int8 *a, uint32_t out, uint64_t m, uint64_t k);
+
+/* ---- argmax / sampling / token records (backend.rs:606, 621, 651, 654, 969-984) */
+int rsv_argmax(rsv_ctx *ctx, uint32_t logits, uint32_t token, uint64_t n);
+int rsv_argmax_into_host(rsv_ctx *ctx, uint32_t logits, uint32_t token, uint64_t n);
+int rsv_argmax_batch(rsv_ctx *ctx, uint32_t logits, uint32_t token, uint64_t n, uint64_t batch);
+int rsv_sample(rsv_ctx *ctx, uint32_t logits, uint32_t token, uint64_t n, float temperature,
+               uint32_t top_k, float top_p, uint32_t seed, float repetition_penalty,
+               float frequency_penalty, float presence_penalty, const uint32_t *history,
+               uint64_t hist_len);
+int rsv_sample_into_host_seeded(rsv_ctx *ctx, uint32_t logits, uint32_t token, uint64_t n,
+                                uint32_t temp, uint32_t mask, uint32_t counter, uint32_t sampler,
+                                uint32_t hist);
+int rsv_sample_into_host_seeded_batch(rsv_ctx *ctx, uint32_t logits, uint32_t token, uint64_t n,
+                                      uint32_t temp, uint32_t mask, uint32_t counter,
+                                      uint32_t sampler, uint32_t hist, uint64_t batch);
+int rsv_record_token(rsv_ctx *ctx, uint32_t in_tok, uint32_t out_seq, uint32_t cnt);
+int rsv_record_tokens(rsv_ctx *ctx, uint32_t in_tok, uint32_t out_seq, uint32_t cnt, uint64_t stride,
+                      uint64_t batch);
+
+/* ---- sequence (prefill) ops (backend.rs:681-939) */
+int rsv_copy_token(rsv_ctx *ctx, uint32_t x, uint32_t y, uint64_t c, uint64_t stride, uint64_t token);
+int rsv_copy_token_batch(rsv_ctx *ctx, uint32_t x, uint32_t state, uint32_t lens, uint64_t c,
+                         uint64_t t, uint64_t batch);
+/* C[m,n] = A[m,k] B[n,k]^T (+bias[n] | +x[m,n] | relu^2 | tanh); A,B F16, C F32. */
+int rsv_gemm(rsv_ctx *ctx, uint32_t a, uint32_t b, uint32_t c, uint64_t m, uint64_t n, uint64_t k);
+int rsv_gemm_bias(rsv_ctx *ctx, uint32_t a, uint32_t b, uint32_t bias, uint32_t c, uint64_t m, uint64_t n,
+                  uint64_t k);
+int rsv_gemm_add(rsv_ctx *ctx, uint32_t a, uint32_t b, uint32_t x, uint32_t y, uint64_t m, uint64_t n,
+                 uint64_t k);
+int rsv_gemm_relu2(rsv_ctx *ctx, uint32_t a, uint32_t b, uint32_t c, uint64_t m, uint64_t n, uint64_t k);
+int rsv_gemm_tanh(rsv_ctx *ctx, uint32_t a, uint32_t b, uint32_t c, uint64_t m, uint64_t n, uint64_t k);
+/* C[m,n] (op)= A[m,k] W[n,k]^T with W int8 dequantised in the MFMA tile loader. */
+int rsv_gemm_int8(rsv_ctx *ctx, uint32_t a, const rsv_int8 *w, uint32_t c, uint64_t m, int epilogue);
+int rsv_to_f16(rsv_ctx *ctx, uint32_t x, uint32_t y, uint64_t c, uint64_t t, uint64_t m_pad,
+               uint64_t x_stride, uint64_t y_stride);
+int rsv_to_f16_triple(rsv_ctx *ctx, uint32_t xr, uint32_t xk, uint32_t xv, uint32_t yr, uint32_t yk,
+                      uint32_t yv, uint64_t c, uint64_t t, uint64_t m_pad, uint64_t x_stride,
+                      uint64_t y_stride);
+int rsv_elementwise_sigmoid(rsv_ctx *ctx, uint32_t a, uint32_t y, uint64_t c, uint64_t batch);
+int rsv_elementwise_sigmoid_inplace(rsv_ctx *ctx, uint32_t y, uint64_t c, uint64_t batch);
+int rsv_elementwise_scale_exp(rsv_ctx *ctx, uint32_t a, uint32_t b, uint32_t y, uint64_t c, uint64_t batch);
+int rsv_elementwise_mul(rsv_ctx *ctx, uint32_t a, uint32_t b, uint32_t y, uint64_t c, uint64_t batch);
+int rsv_v_first_lerp(rsv_ctx *ctx, uint32_t v, uint32_t gate, uint32_t v_first, uint64_t c, uint64_t t,
+                     uint64_t stride);
+int rsv_fuse_ka(rsv_ctx *ctx, uint32_t k, uint32_t k_k, uint32_t a, uint32_t k_a, uint32_t k_mod,
+                uint32_t kk_l2, uint32_t b, uint64_t h, uint64_t n, uint64_t batch);
+int rsv_sum_rk_rk(rsv_ctx *ctx, uint32_t r, uint32_t k_mod, uint32_t r_k, uint32_t v, uint32_t y,
+                  uint64_t h, uint64_t n, uint64_t batch);
+int rsv_seq_shift(rsv_ctx *ctx, uint32_t x, uint32_t state, uint32_t tm, uint32_t y, uint64_t c,
+                  uint64_t t, uint64_t stride_x, uint64_t stride_y);
+int rsv_seq_shift_batch(rsv_ctx *ctx, uint32_t x, uint32_t state, uint32_t tm, uint32_t y, uint64_t c,
+                        uint64_t t, uint64_t stride_x, uint64_t stride_y, uint64_t batch);
+/* Sequential WKV over t tokens: s [H,N,N] state; r,w,k(=k_mod),v,a(=kk_l2),b [t, c]; y [t, c]. */
+int rsv_dplr_seq(rsv_ctx *ctx, uint32_t s, uint32_t r, uint32_t w, uint32_t k, uint32_t v, uint32_t a,
+                 uint32_t b, uint32_t y, uint64_t h, uint64_t n, uint64_t t, uint64_t c);
+int rsv_dplr_seq_batch(rsv_ctx *ctx, uint32_t s, uint32_t r, uint32_t w, uint32_t k, uint32_t v,
+                       uint32_t a, uint32_t b, uint32_t y, uint32_t lens, uint64_t h, uint64_t n,
+                       uint64_t t, uint64_t c, uint64_t batch);
+int rsv_segmean(rsv_ctx *ctx, uint32_t x, uint32_t out, uint32_t lens, uint64_t c, uint64_t t_pad,
+                uint64_t batch);
+
+/* ---- fused ragged prefill WKV (no reference counterpart as one call; it
+ * composes fuse_ka + dplr_seq(_batch) + norm(GN) + sum_rk_rk of
+ * backend.rs:765-870 over packed ragged segments).  seg_start/seg_len/seg_slot
+ * are U32 [nseg]: token rows [start, start+len) of the packed [T, C] buffers
+ * belong to state slot seg_slot. */
+int rsv_wkv7_seq_ragged(rsv_ctx *ctx, uint32_t s, uint32_t r, uint32_t w, uint32_t k, uint32_t v,
+                        uint32_t a, uint32_t k_k, uint32_t k_a, uint32_t r_k, uint32_t ln_x_w,
+                        uint32_t ln_x_b, uint32_t y_norm, uint32_t seg_start, uint32_t seg_len,
+                        uint32_t seg_slot, uint64_t nseg, uint64_t h, uint64_t n, float gn_eps);
+
+/* ---- prefill building blocks.  These have no one-to-one trait method: they
+ * are the pieces the packed (ragged) prefill is built from, replacing the
+ * seq_shift, to_f16, gemm_* and elementwise_* chains of gpu_model.rs:2911-3255 with
+ * fewer, fused launches.
+ *
+ * rsv_seq_norm_mix: per token row t of x [T, C]: ln = LN(x[t]); prev = LN(x[p])
+ * when row_prev[t] = p, or state[slot] when row_prev[t] = 0x80000000|slot;
+ * out_j[t] = f16(ln + coef_j*(prev - ln)) for j < nout (out_j F16 [T, C]). */
+int rsv_seq_norm_mix(rsv_ctx *ctx, uint32_t x, uint32_t state, uint32_t gamma, uint32_t beta,
+                     const uint32_t *coef, const uint32_t *out_f16, uint64_t nout, uint32_t row_prev,
+                     uint64_t t, uint64_t c, float eps);
+/* state[seg_slot[g]] = LN(x[seg_last[g]]) for g < nseg. */
+int rsv_seq_state_store(rsv_ctx *ctx, uint32_t x, uint32_t state, uint32_t gamma, uint32_t beta,
+                        uint32_t seg_last, uint32_t seg_slot, uint64_t nseg, uint64_t c, float eps);
+/* dst[dst_rows[i]] = src[src_rows[i]] for i < n (rows of c f32). */
+int rsv_copy_rows(rsv_ctx *ctx, uint32_t src, uint32_t dst, uint32_t src_rows, uint32_t dst_rows,
+                  uint64_t n, uint64_t c);
+/* y = f16(a * b), n elements. */
+int rsv_mul_to_f16(rsv_ctx *ctx, uint32_t a, uint32_t b, uint32_t y, uint64_t n);
+/* General prefill GEMM: C[m,n] = epi(A[m,k] W[n,k]^T).  A is F16 [m, k];
+ * W is an F16 tensor [n, k] (w8 == NULL) or an int8 handle; C is F32 or F16
+ * [m, n].  epilogue: 0 store, 1 +bias[n], 2 +C (in place), 3 relu^2, 4 tanh,
+ * 5 exp(scale*sigmoid(acc+bias)), 6 sigmoid(acc+bias),
+ * 7 C + sigmoid(acc+bias)*(aux - C), 8 sigmoid(acc).  Unused ids: 0xFFFFFFFF. */
+int rsv_gemm_ex(rsv_ctx *ctx, uint32_t a, uint32_t w16, const rsv_int8 *w8, uint32_t c, uint64_t m,
+                uint64_t n, uint64_t k, int epilogue, uint32_t bias, uint32_t aux, uint32_t scale);
+
+/* ---- profiling hooks (backend.rs:67-70); kernel timing is done with rocprofv3 */
+int rsv_clear_kernel_prof(rsv_ctx *ctx);
+int rsv_dump_kernel_prof(rsv_ctx *ctx);
+
+/* ---- raw access for harnesses: device pointer and stream of a tensor/ctx */
+int rsv_tensor_ptr(rsv_ctx *ctx, uint32_t id, void **ptr);
+int rsv_stream(rsv_ctx *ctx, void **stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

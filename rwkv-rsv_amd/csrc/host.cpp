@@ -1,0 +1,1116 @@
+// librsv_host.so: the model driver above the HIP backend C-ABI.
+//
+// Restates the reference's GpuModel / Bundle / State (src/gpu_model.rs) in
+// C++ for hosts without a Rust toolchain.  Talks to the device only through
+// include/rsv_hip.h, exactly as a backend_hip.rs-backed GpuModel would.
+//
+//  - load:    safetensors (mmap) -> config from shapes (gpu_model.rs:401-546),
+//             LN0 applied to the embedding on the CPU (gpu_model.rs:450-460),
+//             linears int8 when `{key}.int8_idx` exists else fp16
+//             (gpu_model.rs:3405-3442), LoRA oriented [out, in] fp16.
+//  - decode:  per layer norm_lerp6 -> fused stage-1 -> v_first snapshot
+//             (layer 0) -> LoRA stage-2 chain -> WKV7 -> att.output ->
+//             cmix_norm_lerp -> ffn.key relu^2 -> ffn.value
+//             (gpu_model.rs:2060-2392), batched over B slots.
+//  - prefill: packed ragged segments through MFMA GEMMs and one sequential
+//             WKV scan per layer (replaces gpu_model.rs:2911-3255 and
+//             1041-1350).
+//  - self-loops: one step captured as a HIP graph and replayed n times
+//             (gpu_model.rs:1824-1874, 732-852, 1639-1803).
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "../../include/rsv_hip.h"
+#include "../../include/rsv_host.h"
+
+namespace {
+
+thread_local std::string g_herr;
+
+int herr(const char *fmt, ...) {
+    char buf[2048];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_herr = buf;
+    return -1;
+}
+
+// Propagate a backend failure with its text.
+#define CK(call)                                                              \
+    do {                                                                      \
+        if ((call) != 0) return herr("%s: %s", #call, rsv_last_error());       \
+    } while (0)
+#define HK(call)                         \
+    do {                                 \
+        if ((call) != 0) return -1;      \
+    } while (0)
+
+constexpr uint32_t NONE = 0xFFFFFFFFu;
+constexpr float LN_EPS = 1.0e-5f;  // model.rs:6
+constexpr float GN_EPS = 64.0e-5f; // model.rs:7
+constexpr float L2_EPS = 1.0e-12f; // model.rs:8
+
+// ------------------------------------------------------------ safetensors
+struct StEntry {
+    std::string dtype;
+    std::vector<uint64_t> shape;
+    uint64_t begin = 0, end = 0;
+    uint64_t numel() const {
+        uint64_t n = 1;
+        for (auto s : shape) n *= s;
+        return n;
+    }
+};
+
+struct SafeTensors {
+    int fd = -1;
+    uint8_t *base = nullptr;
+    size_t size = 0;
+    const uint8_t *data = nullptr;
+    std::map<std::string, StEntry> t;
+
+    ~SafeTensors() {
+        if (base) munmap(base, size);
+        if (fd >= 0) close(fd);
+    }
+
+    // Minimal JSON reader for the safetensors header: an object of objects
+    // holding "dtype" (string), "shape" (int array), "data_offsets" (2 ints).
+    struct P {
+        const char *s, *e;
+        void ws() { while (s < e && (*s == ' ' || *s == '\n' || *s == '\r' || *s == '\t')) s++; }
+        bool lit(char c) { ws(); if (s < e && *s == c) { s++; return true; } return false; }
+        bool str(std::string &out) {
+            ws();
+            if (s >= e || *s != '"') return false;
+            s++;
+            out.clear();
+            while (s < e && *s != '"') {
+                if (*s == '\\' && s + 1 < e) { out.push_back(s[1]); s += 2; continue; }
+                out.push_back(*s++);
+            }
+            if (s >= e) return false;
+            s++;
+            return true;
+        }
+        bool num(uint64_t &v) {
+            ws();
+            if (s >= e || *s < '0' || *s > '9') return false;
+            v = 0;
+            while (s < e && *s >= '0' && *s <= '9') v = v * 10 + (uint64_t)(*s++ - '0');
+            return true;
+        }
+        bool skip() {  // skip any JSON value
+            ws();
+            if (s >= e) return false;
+            if (*s == '"') { std::string d; return str(d); }
+            if (*s == '{' || *s == '[') {
+                const char open = *s, close = open == '{' ? '}' : ']';
+                int depth = 0;
+                bool in_str = false;
+                for (; s < e; s++) {
+                    if (in_str) { if (*s == '\\') s++; else if (*s == '"') in_str = false; continue; }
+                    if (*s == '"') in_str = true;
+                    else if (*s == open) depth++;
+                    else if (*s == close && --depth == 0) { s++; return true; }
+                }
+                return false;
+            }
+            while (s < e && *s != ',' && *s != '}' && *s != ']') s++;
+            return true;
+        }
+    };
+
+    int open_file(const char *path) {
+        fd = ::open(path, O_RDONLY);
+        if (fd < 0) return herr("cannot open %s", path);
+        struct stat st;
+        if (fstat(fd, &st) != 0) return herr("cannot stat %s", path);
+        size = (size_t)st.st_size;
+        if (size < 8) return herr("%s: too small for safetensors", path);
+        base = (uint8_t *)mmap(nullptr, size, PROT_READ, MAP_PRIVATE, fd, 0);
+        if (base == MAP_FAILED) { base = nullptr; return herr("mmap %s failed", path); }
+        uint64_t hl = 0;
+        memcpy(&hl, base, 8);
+        if (hl > size - 8) return herr("%s: bad header length", path);
+        data = base + 8 + hl;
+        const uint64_t dsize = size - 8 - hl;
+        P p{(const char *)base + 8, (const char *)base + 8 + hl};
+        if (!p.lit('{')) return herr("%s: header is not an object", path);
+        if (p.lit('}')) return 0;
+        do {
+            std::string name;
+            if (!p.str(name) || !p.lit(':')) return herr("%s: bad header key", path);
+            if (name == "__metadata__") { if (!p.skip()) return herr("%s: bad metadata", path); continue; }
+            StEntry ent;
+            if (!p.lit('{')) return herr("%s: bad entry %s", path, name.c_str());
+            if (!p.lit('}')) {
+                do {
+                    std::string k;
+                    if (!p.str(k) || !p.lit(':')) return herr("%s: bad field in %s", path, name.c_str());
+                    if (k == "dtype") {
+                        if (!p.str(ent.dtype)) return herr("%s: bad dtype", path);
+                    } else if (k == "shape" || k == "data_offsets") {
+                        std::vector<uint64_t> v;
+                        if (!p.lit('[')) return herr("%s: bad array", path);
+                        if (!p.lit(']')) {
+                            do {
+                                uint64_t x;
+                                if (!p.num(x)) return herr("%s: bad number", path);
+                                v.push_back(x);
+                            } while (p.lit(','));
+                            if (!p.lit(']')) return herr("%s: unterminated array", path);
+                        }
+                        if (k == "shape") ent.shape = v;
+                        else if (v.size() == 2) { ent.begin = v[0]; ent.end = v[1]; }
+                    } else if (!p.skip()) {
+                        return herr("%s: bad value", path);
+                    }
+                } while (p.lit(','));
+                if (!p.lit('}')) return herr("%s: unterminated entry", path);
+            }
+            if (ent.end < ent.begin || ent.end > dsize) return herr("%s: %s out of range", path, name.c_str());
+            t[name] = ent;
+        } while (p.lit(','));
+        return 0;
+    }
+
+    const StEntry *get(const std::string &k) const {
+        auto it = t.find(k);
+        return it == t.end() ? nullptr : &it->second;
+    }
+
+    // Tensor as f32 (F32 / F16 / BF16 sources), shape-checked.
+    int f32(const std::string &k, std::vector<float> &out, uint64_t expect = 0) const {
+        const StEntry *e = get(k);
+        if (!e) return herr("missing tensor %s", k.c_str());
+        const uint64_t n = e->numel();
+        if (expect && n != expect) return herr("%s: %llu elements, expected %llu", k.c_str(), (unsigned long long)n, (unsigned long long)expect);
+        out.resize(n);
+        const uint8_t *p = data + e->begin;
+        if (e->dtype == "F32") {
+            if (e->end - e->begin != n * 4) return herr("%s: size mismatch", k.c_str());
+            memcpy(out.data(), p, n * 4);
+        } else if (e->dtype == "F16") {
+            if (e->end - e->begin != n * 2) return herr("%s: size mismatch", k.c_str());
+            for (uint64_t i = 0; i < n; i++) {
+                uint16_t b;
+                memcpy(&b, p + 2 * i, 2);
+                _Float16 h;
+                memcpy(&h, &b, 2);
+                out[i] = (float)h;
+            }
+        } else if (e->dtype == "BF16") {
+            if (e->end - e->begin != n * 2) return herr("%s: size mismatch", k.c_str());
+            for (uint64_t i = 0; i < n; i++) {
+                uint16_t b;
+                memcpy(&b, p + 2 * i, 2);
+                const uint32_t w = (uint32_t)b << 16;
+                memcpy(&out[i], &w, 4);
+            }
+        } else {
+            return herr("%s: unsupported dtype %s", k.c_str(), e->dtype.c_str());
+        }
+        return 0;
+    }
+};
+
+// ------------------------------------------------------------ model types
+struct Linear {
+    bool i8 = false;
+    rsv_int8 h{};      // int8
+    uint32_t w16 = NONE; // fp16 [m, k]
+    uint64_t m = 0, k = 0;
+};
+
+struct Layer {
+    uint32_t ln1_w, ln1_b, ln2_w, ln2_b, lnx_w, lnx_b;
+    uint32_t x_r, x_w, x_k, x_v, x_a, x_g, ffn_x_k;
+    uint32_t w0, a0, v0, r_k, k_k, k_a;
+    uint32_t w1, w2, a1, a2, v1, v2, g1, g2;  // fp16 [out, in]
+    Linear rw, kw, vw, ow, fk, fv;
+};
+
+struct GpuState {
+    uint64_t batch = 1;
+    std::vector<uint32_t> tmix_x, rnn, cmix_x;  // per layer
+    uint32_t v_first = NONE;                    // [batch, C]
+};
+
+struct WorkBufs {
+    uint64_t batch = 0;
+    uint32_t x, xr, xw, xk, xv, xa, xg, r, k, v, vmid, wmid, amid, gmid, w, a, g, yn, xb, r2, xnorm, logits, token;
+};
+
+struct SeqBufs {
+    uint64_t cap = 0, segcap = 0;
+    uint32_t tok = NONE, x = NONE, mix[6] = {NONE, NONE, NONE, NONE, NONE, NONE};
+    uint32_t r = NONE, k = NONE, v = NONE, w = NONE, a = NONE, g = NONE, vf = NONE, yn = NONE, yg = NONE, xb = NONE,
+             r2 = NONE;
+    uint32_t vmid = NONE, wmid = NONE, amid = NONE, gmid = NONE;
+    uint32_t row_prev = NONE, seg_start = NONE, seg_len = NONE, seg_slot = NONE, seg_last = NONE, seg_iota = NONE;
+    uint32_t xlast = NONE, xnorm = NONE, logits = NONE;
+};
+
+}  // namespace
+
+struct rsv_state {
+    GpuState s;
+};
+
+struct rsv_bundle {
+    rsv_ctx *ctx = nullptr;
+    rsv_model_info info{};
+    uint32_t emb_ln = NONE, ln_out_w = NONE, ln_out_b = NONE, scale_w = NONE;
+    Linear head;
+    std::vector<Layer> layers;
+    rsv_state *state = nullptr;  // the bundle's own session
+    std::map<uint64_t, WorkBufs> bufs;
+    SeqBufs seq;
+    std::vector<uint32_t> owned;  // every tensor the bundle created
+
+    ~rsv_bundle() {
+        if (ctx) rsv_destroy(ctx);
+    }
+};
+
+namespace {
+
+int new_tensor(rsv_bundle *b, uint64_t len, int dt, uint32_t &id) {
+    CK(rsv_tensor_create(b->ctx, len, dt, &id));
+    return 0;
+}
+
+int upload_vec(rsv_bundle *b, const SafeTensors &st, const std::string &key, uint64_t expect, uint32_t &id) {
+    std::vector<float> v;
+    HK(st.f32(key, v, expect));
+    HK(new_tensor(b, v.size(), RSV_F32, id));
+    CK(rsv_upload(b->ctx, id, v.data(), v.size()));
+    return 0;
+}
+
+// Linear [out=m, in=k]: int8 when `key.int8_idx` exists (gpu_model.rs:3405-3442).
+int load_linear(rsv_bundle *b, const SafeTensors &st, const std::string &key, uint64_t m, uint64_t k, Linear &L) {
+    L.m = m;
+    L.k = k;
+    const StEntry *ie = st.get(key + ".int8_idx");
+    if (ie) {
+        const StEntry *se = st.get(key + ".int8_sz");
+        if (!se) return herr("%s.int8_sz missing", key.c_str());
+        if (k % 128 != 0) return herr("%s: int8 needs k %% 128 == 0", key.c_str());
+        if (ie->end - ie->begin != m * k) return herr("%s.int8_idx: %llu bytes, expected %llu", key.c_str(), (unsigned long long)(ie->end - ie->begin), (unsigned long long)(m * k));
+        if (se->end - se->begin != m * k / 128 * 4) return herr("%s.int8_sz size mismatch", key.c_str());
+        L.i8 = true;
+        HK(new_tensor(b, m * k / 4, RSV_U32, L.h.idx));
+        HK(new_tensor(b, m * k / 128, RSV_U32, L.h.sz));
+        CK(rsv_upload_bytes(b->ctx, L.h.idx, st.data + ie->begin, m * k));
+        CK(rsv_upload_bytes(b->ctx, L.h.sz, st.data + se->begin, m * k / 128 * 4));
+        L.h.m = m;
+        L.h.k = k;
+        return 0;
+    }
+    std::vector<float> w;
+    HK(st.f32(key, w, m * k));
+    HK(new_tensor(b, m * k, RSV_F16, L.w16));
+    CK(rsv_upload(b->ctx, L.w16, w.data(), w.size()));
+    return 0;
+}
+
+// LoRA matrix as fp16 [out, in]; the file may hold either orientation
+// (model.rs:564-581).
+int load_lora(rsv_bundle *b, const SafeTensors &st, const std::string &key, uint64_t in, uint64_t out, uint32_t &id) {
+    const StEntry *e = st.get(key);
+    if (!e) return herr("missing tensor %s", key.c_str());
+    if (e->shape.size() != 2) return herr("%s: expected 2-D", key.c_str());
+    std::vector<float> d;
+    HK(st.f32(key, d, in * out));
+    std::vector<float> o(in * out);
+    if (e->shape[0] == out && e->shape[1] == in) {
+        o = d;
+    } else if (e->shape[0] == in && e->shape[1] == out) {
+        for (uint64_t i = 0; i < in; i++)
+            for (uint64_t j = 0; j < out; j++) o[j * in + i] = d[i * out + j];
+    } else {
+        return herr("%s: shape [%llu,%llu] is neither [%llu,%llu] nor its transpose", key.c_str(),
+                    (unsigned long long)e->shape[0], (unsigned long long)e->shape[1], (unsigned long long)out, (unsigned long long)in);
+    }
+    HK(new_tensor(b, in * out, RSV_F16, id));
+    CK(rsv_upload(b->ctx, id, o.data(), o.size()));
+    return 0;
+}
+
+// model.rs:625-635
+void layer_norm_cpu(const float *x, const float *w, const float *bb, uint64_t n, float *y) {
+    float s = 0.0f;
+    for (uint64_t i = 0; i < n; i++) s += x[i];
+    const float mean = s / (float)n;
+    float v = 0.0f;
+    for (uint64_t i = 0; i < n; i++) { const float d = x[i] - mean; v += d * d; }
+    const float inv = 1.0f / sqrtf(v / (float)n + LN_EPS);
+    for (uint64_t i = 0; i < n; i++) y[i] = (x[i] - mean) * inv * w[i] + bb[i];
+}
+
+int load_model(rsv_bundle *b, const char *path) {
+    SafeTensors st;
+    HK(st.open_file(path));
+    // n_layer from the largest blocks.N index (model.rs:520-532)
+    uint64_t n_layer = 0;
+    for (auto &kv : st.t) {
+        const std::string &k = kv.first;
+        if (k.rfind("blocks.", 0) == 0) {
+            const uint64_t idx = strtoull(k.c_str() + 7, nullptr, 10);
+            if (idx + 1 > n_layer) n_layer = idx + 1;
+        }
+    }
+    const StEntry *emb = st.get("emb.weight");
+    const StEntry *rk = st.get("blocks.0.att.r_k");
+    if (!emb || emb->shape.size() != 2 || !rk || rk->shape.size() != 2) return herr("%s: not an RWKV-7 model", path);
+    rsv_model_info &I = b->info;
+    I.n_layer = n_layer;
+    I.vocab = emb->shape[0];
+    I.n_embd = emb->shape[1];
+    I.n_head = rk->shape[0];
+    I.head_size = rk->shape[1];
+    const uint64_t C = I.n_embd;
+    auto mid_of = [&](const char *k, uint64_t &mid) -> int {
+        const StEntry *e = st.get(k);
+        if (!e || e->shape.size() != 2) return herr("missing %s", k);
+        mid = e->shape[0] == C ? e->shape[1] : e->shape[0];
+        return 0;
+    };
+    HK(mid_of("blocks.0.att.w1", I.w_mid));
+    HK(mid_of("blocks.0.att.a1", I.a_mid));
+    HK(mid_of("blocks.0.att.v1", I.v_mid));
+    HK(mid_of("blocks.0.att.g1", I.g_mid));
+    if (const StEntry *fk = st.get("blocks.0.ffn.key.weight")) I.ffn = fk->shape[0];
+    else if (const StEntry *fk8 = st.get("blocks.0.ffn.key.weight.int8_idx")) I.ffn = fk8->shape[0];
+    else return herr("missing blocks.0.ffn.key.weight");
+    if (I.n_head * I.head_size != C) return herr("n_head*head_size != n_embd");
+    if (I.head_size != 64) return herr("head_size %llu unsupported (64 required)", (unsigned long long)I.head_size);
+
+    // emb_ln = LN0(emb) on the CPU, kept fp32 on the device (the reference
+    // stores it fp16, gpu_model.rs:450-460)
+    {
+        std::vector<float> e, w, bb;
+        HK(st.f32("emb.weight", e));
+        HK(st.f32("blocks.0.ln0.weight", w, C));
+        HK(st.f32("blocks.0.ln0.bias", bb, C));
+        std::vector<float> out(e.size());
+        for (uint64_t r = 0; r < I.vocab; r++) layer_norm_cpu(&e[r * C], w.data(), bb.data(), C, &out[r * C]);
+        HK(new_tensor(b, out.size(), RSV_F32, b->emb_ln));
+        CK(rsv_upload(b->ctx, b->emb_ln, out.data(), out.size()));
+    }
+    HK(upload_vec(b, st, "ln_out.weight", C, b->ln_out_w));
+    HK(upload_vec(b, st, "ln_out.bias", C, b->ln_out_b));
+    HK(load_linear(b, st, "head.weight", I.vocab, C, b->head));
+    I.int8_head = b->head.i8;
+    {
+        const float sw = -1.0f / sqrtf(2.718281828459045f);  // gpu_model.rs:517-518
+        HK(new_tensor(b, 1, RSV_F32, b->scale_w));
+        CK(rsv_upload(b->ctx, b->scale_w, &sw, 1));
+    }
+    b->layers.resize(n_layer);
+    bool all_i8 = true;
+    for (uint64_t i = 0; i < n_layer; i++) {
+        Layer &L = b->layers[i];
+        const std::string p = "blocks." + std::to_string(i) + ".";
+        HK(upload_vec(b, st, p + "ln1.weight", C, L.ln1_w));
+        HK(upload_vec(b, st, p + "ln1.bias", C, L.ln1_b));
+        HK(upload_vec(b, st, p + "ln2.weight", C, L.ln2_w));
+        HK(upload_vec(b, st, p + "ln2.bias", C, L.ln2_b));
+        HK(upload_vec(b, st, p + "att.ln_x.weight", C, L.lnx_w));
+        HK(upload_vec(b, st, p + "att.ln_x.bias", C, L.lnx_b));
+        HK(upload_vec(b, st, p + "att.x_r", C, L.x_r));
+        HK(upload_vec(b, st, p + "att.x_w", C, L.x_w));
+        HK(upload_vec(b, st, p + "att.x_k", C, L.x_k));
+        HK(upload_vec(b, st, p + "att.x_v", C, L.x_v));
+        HK(upload_vec(b, st, p + "att.x_a", C, L.x_a));
+        HK(upload_vec(b, st, p + "att.x_g", C, L.x_g));
+        HK(upload_vec(b, st, p + "ffn.x_k", C, L.ffn_x_k));
+        HK(upload_vec(b, st, p + "att.w0", C, L.w0));
+        HK(upload_vec(b, st, p + "att.a0", C, L.a0));
+        HK(upload_vec(b, st, p + "att.v0", C, L.v0));
+        HK(upload_vec(b, st, p + "att.r_k", C, L.r_k));
+        HK(upload_vec(b, st, p + "att.k_k", C, L.k_k));
+        HK(upload_vec(b, st, p + "att.k_a", C, L.k_a));
+        HK(load_lora(b, st, p + "att.w1", C, I.w_mid, L.w1));
+        HK(load_lora(b, st, p + "att.w2", I.w_mid, C, L.w2));
+        HK(load_lora(b, st, p + "att.a1", C, I.a_mid, L.a1));
+        HK(load_lora(b, st, p + "att.a2", I.a_mid, C, L.a2));
+        HK(load_lora(b, st, p + "att.v1", C, I.v_mid, L.v1));
+        HK(load_lora(b, st, p + "att.v2", I.v_mid, C, L.v2));
+        HK(load_lora(b, st, p + "att.g1", C, I.g_mid, L.g1));
+        HK(load_lora(b, st, p + "att.g2", I.g_mid, C, L.g2));
+        HK(load_linear(b, st, p + "att.receptance.weight", C, C, L.rw));
+        HK(load_linear(b, st, p + "att.key.weight", C, C, L.kw));
+        HK(load_linear(b, st, p + "att.value.weight", C, C, L.vw));
+        HK(load_linear(b, st, p + "att.output.weight", C, C, L.ow));
+        HK(load_linear(b, st, p + "ffn.key.weight", I.ffn, C, L.fk));
+        HK(load_linear(b, st, p + "ffn.value.weight", C, I.ffn, L.fv));
+        all_i8 = all_i8 && L.rw.i8 && L.kw.i8 && L.vw.i8 && L.ow.i8 && L.fk.i8 && L.fv.i8;
+    }
+    I.int8_linears = all_i8;
+    CK(rsv_synchronize(b->ctx));
+    return 0;
+}
+
+// ------------------------------------------------------------ state
+int state_create(rsv_bundle *b, uint64_t batch, GpuState &s) {
+    const rsv_model_info &I = b->info;
+    const uint64_t C = I.n_embd, HNN = I.n_head * I.head_size * I.head_size;
+    s.batch = batch;
+    s.tmix_x.assign(I.n_layer, NONE);
+    s.rnn.assign(I.n_layer, NONE);
+    s.cmix_x.assign(I.n_layer, NONE);
+    for (uint64_t i = 0; i < I.n_layer; i++) {
+        HK(new_tensor(b, C * batch, RSV_F32, s.tmix_x[i]));
+        HK(new_tensor(b, HNN * batch, RSV_F32, s.rnn[i]));
+        HK(new_tensor(b, C * batch, RSV_F32, s.cmix_x[i]));
+    }
+    HK(new_tensor(b, C * batch, RSV_F32, s.v_first));  // tensors start zeroed
+    return 0;
+}
+
+void state_free(rsv_bundle *b, GpuState &s) {
+    for (auto id : s.tmix_x) rsv_tensor_free(b->ctx, id);
+    for (auto id : s.rnn) rsv_tensor_free(b->ctx, id);
+    for (auto id : s.cmix_x) rsv_tensor_free(b->ctx, id);
+    rsv_tensor_free(b->ctx, s.v_first);
+    s.tmix_x.clear();
+    s.rnn.clear();
+    s.cmix_x.clear();
+}
+
+uint64_t state_len1(const rsv_bundle *b) {
+    const rsv_model_info &I = b->info;
+    return I.n_layer * (2 * I.n_embd + I.n_head * I.head_size * I.head_size) + I.n_embd;
+}
+
+// Slot-major serialisation, gpu_model.rs:3972-3990 / 4038-4095.
+int state_back_slots(rsv_bundle *b, GpuState &s, uint64_t slot0, uint64_t nslots, float *out) {
+    const rsv_model_info &I = b->info;
+    const uint64_t C = I.n_embd, HNN = I.n_head * I.head_size * I.head_size, B = s.batch;
+    std::vector<float> tx(C * B), rn(HNN * B), cx(C * B), vf(C * B);
+    const uint64_t per = state_len1(b);
+    for (uint64_t i = 0; i < I.n_layer; i++) {
+        CK(rsv_download(b->ctx, s.tmix_x[i], tx.data(), C * B));
+        CK(rsv_download(b->ctx, s.rnn[i], rn.data(), HNN * B));
+        CK(rsv_download(b->ctx, s.cmix_x[i], cx.data(), C * B));
+        for (uint64_t q = 0; q < nslots; q++) {
+            const uint64_t sl = slot0 + q;
+            float *o = out + q * per + i * (2 * C + HNN);
+            memcpy(o, &tx[sl * C], C * 4);
+            memcpy(o + C, &rn[sl * HNN], HNN * 4);
+            memcpy(o + C + HNN, &cx[sl * C], C * 4);
+        }
+    }
+    CK(rsv_download(b->ctx, s.v_first, vf.data(), C * B));
+    for (uint64_t q = 0; q < nslots; q++) memcpy(out + q * per + I.n_layer * (2 * C + HNN), &vf[(slot0 + q) * C], C * 4);
+    return 0;
+}
+
+int state_load_slots(rsv_bundle *b, GpuState &s, uint64_t slot0, uint64_t nslots, const float *data) {
+    const rsv_model_info &I = b->info;
+    const uint64_t C = I.n_embd, HNN = I.n_head * I.head_size * I.head_size;
+    const uint64_t per = state_len1(b);
+    for (uint64_t q = 0; q < nslots; q++) {
+        const uint64_t sl = slot0 + q;
+        const float *d = data + q * per;
+        for (uint64_t i = 0; i < I.n_layer; i++) {
+            const float *o = d + i * (2 * C + HNN);
+            CK(rsv_upload_part(b->ctx, s.tmix_x[i], sl * C, o, C));
+            CK(rsv_upload_part(b->ctx, s.rnn[i], sl * HNN, o + C, HNN));
+            CK(rsv_upload_part(b->ctx, s.cmix_x[i], sl * C, o + C + HNN, C));
+        }
+        CK(rsv_upload_part(b->ctx, s.v_first, sl * C, d + I.n_layer * (2 * C + HNN), C));
+    }
+    return 0;
+}
+
+int state_reset(rsv_bundle *b, GpuState &s) {
+    const uint64_t per = state_len1(b);
+    std::vector<float> z(per * s.batch, 0.0f);
+    return state_load_slots(b, s, 0, s.batch, z.data());
+}
+
+// ------------------------------------------------------------ decode
+int get_bufs(rsv_bundle *b, uint64_t B, WorkBufs *&out) {
+    auto it = b->bufs.find(B);
+    if (it != b->bufs.end()) { out = &it->second; return 0; }
+    const rsv_model_info &I = b->info;
+    const uint64_t C = I.n_embd;
+    WorkBufs w;
+    w.batch = B;
+    uint32_t *c_ids[] = {&w.x, &w.xr, &w.xw, &w.xk, &w.xv, &w.xa, &w.xg, &w.r, &w.k, &w.v, &w.w, &w.a, &w.g, &w.yn, &w.xb, &w.xnorm};
+    for (auto p : c_ids) HK(new_tensor(b, C * B, RSV_F32, *p));
+    HK(new_tensor(b, I.v_mid * B, RSV_F32, w.vmid));
+    HK(new_tensor(b, I.w_mid * B, RSV_F32, w.wmid));
+    HK(new_tensor(b, I.a_mid * B, RSV_F32, w.amid));
+    HK(new_tensor(b, I.g_mid * B, RSV_F32, w.gmid));
+    HK(new_tensor(b, I.ffn * B, RSV_F32, w.r2));
+    HK(new_tensor(b, I.vocab * B, RSV_F32, w.logits));
+    HK(new_tensor(b, B, RSV_U32, w.token));
+    out = &(b->bufs[B] = w);
+    return 0;
+}
+
+int gemv_lin(rsv_bundle *b, const Linear &L, uint32_t x, uint32_t y, uint64_t B, int op, uint32_t g = NONE) {
+    // op: 0 plain, 1 relu2, 2 add, 3 mul_add
+    rsv_ctx *c = b->ctx;
+    if (L.i8) {
+        switch (op) {
+            case 0: CK(rsv_gemv_int8_plain(c, &L.h, x, y, L.m, L.k, B)); break;
+            case 1: CK(rsv_gemv_int8_relu2(c, &L.h, x, y, L.m, L.k, B)); break;
+            case 2: CK(rsv_gemv_int8_add(c, &L.h, x, y, L.m, L.k, B)); break;
+            default: CK(rsv_gemv_int8_mul_add(c, &L.h, x, g, y, L.m, L.k, B)); break;
+        }
+    } else {
+        switch (op) {
+            case 0: CK(rsv_gemv_f16(c, L.w16, x, y, L.m, L.k, B)); break;
+            case 1: CK(rsv_gemv_f16_relu2(c, L.w16, x, y, L.m, L.k, B)); break;
+            case 2: CK(rsv_gemv_f16_add(c, L.w16, x, y, L.m, L.k, B)); break;
+            default: CK(rsv_gemv_f16_mul_add(c, L.w16, x, g, y, L.m, L.k, B)); break;
+        }
+    }
+    return 0;
+}
+
+// One layer for B slots (gpu_model.rs:2060-2392 / 1373-1566).
+int forward_layer(rsv_bundle *b, uint64_t i, WorkBufs &w, GpuState &s) {
+    rsv_ctx *c = b->ctx;
+    const rsv_model_info &I = b->info;
+    const uint64_t C = I.n_embd, B = w.batch;
+    Layer &L = b->layers[i];
+    CK(rsv_norm_lerp6_batch(c, w.x, s.tmix_x[i], L.ln1_w, L.ln1_b, L.x_r, L.x_w, L.x_k, L.x_v, L.x_a, L.x_g, w.xr,
+                            w.xw, w.xk, w.xv, w.xa, w.xg, C, LN_EPS, B));
+    if (L.rw.i8 && L.kw.i8 && L.vw.i8) {
+        CK(rsv_gemv_int8_rkv_stage1_batch(c, &L.rw.h, &L.kw.h, &L.vw.h, L.v1, L.w1, L.a1, L.g1, w.xr, w.xk, w.xv, w.xw,
+                                          w.xa, w.xg, w.r, w.k, w.v, w.vmid, w.wmid, w.amid, w.gmid, C, I.v_mid,
+                                          I.w_mid, I.a_mid, I.g_mid, B));
+    } else if (!L.rw.i8 && !L.kw.i8 && !L.vw.i8) {
+        CK(rsv_gemv_rkv_stage1_batch(c, L.rw.w16, L.kw.w16, L.vw.w16, L.v1, L.w1, L.a1, L.g1, w.xr, w.xk, w.xv, w.xw,
+                                     w.xa, w.xg, w.r, w.k, w.v, w.vmid, w.wmid, w.amid, w.gmid, C, I.v_mid, I.w_mid,
+                                     I.a_mid, I.g_mid, B));
+    } else {
+        return herr("layer %llu: receptance/key/value must share one format", (unsigned long long)i);
+    }
+    if (i == 0) CK(rsv_copy_device(c, w.v, s.v_first));  // v_first snapshot (gpu_model.rs:2200-2204)
+    CK(rsv_gemv_lowrank_chain4_batch(c, L.w2, L.a2, L.v2, L.g2, w.wmid, w.amid, w.vmid, w.gmid, L.w0, L.a0, L.v0,
+                                     b->scale_w, s.v_first, w.w, w.a, w.v, w.g, C, I.w_mid, I.a_mid, I.v_mid, I.g_mid,
+                                     B));
+    CK(rsv_fuse_ka_dplr_norm_batch(c, s.rnn[i], w.k, L.k_k, w.a, L.k_a, w.r, w.v, w.w, L.lnx_w, L.lnx_b, L.r_k, NONE,
+                                   NONE, w.yn, I.n_head, I.head_size, L2_EPS, GN_EPS, B));
+    HK(gemv_lin(b, L.ow, w.yn, w.x, B, 3, w.g));
+    CK(rsv_cmix_norm_lerp_batch(c, w.x, s.cmix_x[i], L.ln2_w, L.ln2_b, L.ffn_x_k, w.xb, C, LN_EPS, B));
+    HK(gemv_lin(b, L.fk, w.xb, w.r2, B, 1));
+    HK(gemv_lin(b, L.fv, w.r2, w.x, B, 2));
+    return 0;
+}
+
+// gather -> layers -> ln_out -> head (gpu_model.rs:1879-1913 minus the sampler)
+int decode_step(rsv_bundle *b, WorkBufs &w, GpuState &s) {
+    rsv_ctx *c = b->ctx;
+    const rsv_model_info &I = b->info;
+    CK(rsv_gather_rows_device_f16(c, b->emb_ln, w.x, w.token, I.n_embd, w.batch));
+    for (uint64_t i = 0; i < I.n_layer; i++) HK(forward_layer(b, i, w, s));
+    CK(rsv_norm(c, w.x, b->ln_out_w, b->ln_out_b, w.xnorm, I.n_embd, 1, LN_EPS, w.batch));
+    HK(gemv_lin(b, b->head, w.xnorm, w.logits, w.batch, 0));
+    return 0;
+}
+
+// ------------------------------------------------------------ prefill
+int get_seq(rsv_bundle *b, uint64_t T, uint64_t nseg) {
+    SeqBufs &q = b->seq;
+    const rsv_model_info &I = b->info;
+    const uint64_t C = I.n_embd;
+    if (T > q.cap) {
+        uint32_t *f32s[] = {&q.x, &q.r, &q.k, &q.v, &q.w, &q.a, &q.g, &q.vf, &q.yn};
+        uint32_t *f16s[] = {&q.mix[0], &q.mix[1], &q.mix[2], &q.mix[3], &q.mix[4], &q.mix[5], &q.yg, &q.xb};
+        for (auto p : f32s) { if (*p != NONE) rsv_tensor_free(b->ctx, *p); HK(new_tensor(b, T * C, RSV_F32, *p)); }
+        for (auto p : f16s) { if (*p != NONE) rsv_tensor_free(b->ctx, *p); HK(new_tensor(b, T * C, RSV_F16, *p)); }
+        struct { uint32_t *id; uint64_t n; int dt; } more[] = {
+            {&q.r2, T * I.ffn, RSV_F16}, {&q.vmid, T * I.v_mid, RSV_F16}, {&q.wmid, T * I.w_mid, RSV_F16},
+            {&q.amid, T * I.a_mid, RSV_F16}, {&q.gmid, T * I.g_mid, RSV_F16}, {&q.tok, T, RSV_U32},
+            {&q.row_prev, T, RSV_U32}};
+        for (auto &m : more) { if (*m.id != NONE) rsv_tensor_free(b->ctx, *m.id); HK(new_tensor(b, m.n, m.dt, *m.id)); }
+        q.cap = T;
+    }
+    if (nseg > q.segcap) {
+        uint32_t *u32s[] = {&q.seg_start, &q.seg_len, &q.seg_slot, &q.seg_last, &q.seg_iota};
+        for (auto p : u32s) { if (*p != NONE) rsv_tensor_free(b->ctx, *p); HK(new_tensor(b, nseg, RSV_U32, *p)); }
+        uint32_t *f32s[] = {&q.xlast, &q.xnorm};
+        for (auto p : f32s) { if (*p != NONE) rsv_tensor_free(b->ctx, *p); HK(new_tensor(b, nseg * C, RSV_F32, *p)); }
+        if (q.logits != NONE) rsv_tensor_free(b->ctx, q.logits);
+        HK(new_tensor(b, nseg * I.vocab, RSV_F32, q.logits));
+        std::vector<uint32_t> iota(nseg);
+        for (uint64_t i = 0; i < nseg; i++) iota[i] = (uint32_t)i;
+        CK(rsv_upload_u32(b->ctx, q.seg_iota, iota.data(), nseg));
+        q.segcap = nseg;
+    }
+    return 0;
+}
+
+struct Seg {
+    const uint32_t *tok;
+    uint64_t len;
+    uint64_t slot;
+};
+
+int gemm_lin(rsv_bundle *b, const Linear &L, uint32_t a, uint32_t c, uint64_t m, int epi) {
+    CK(rsv_gemm_ex(b->ctx, a, L.i8 ? NONE : L.w16, L.i8 ? &L.h : nullptr, c, m, L.m, L.k, epi, NONE, NONE, NONE));
+    return 0;
+}
+
+// Packed prefill of non-empty segments into state slots; logits (optional)
+// receives nseg*vocab floats (last token of each segment).
+int prefill(rsv_bundle *b, GpuState &s, const std::vector<Seg> &segs, float *logits) {
+    rsv_ctx *c = b->ctx;
+    const rsv_model_info &I = b->info;
+    const uint64_t C = I.n_embd, H = I.n_head, N = I.head_size;
+    uint64_t T = 0;
+    for (auto &g : segs) {
+        if (g.len == 0) return herr("prefill: empty segment");
+        if (g.slot >= s.batch) return herr("prefill: slot %llu >= batch %llu", (unsigned long long)g.slot, (unsigned long long)s.batch);
+        T += g.len;
+    }
+    const uint64_t S = segs.size();
+    if (S == 0) return 0;
+    HK(get_seq(b, T, S));
+    SeqBufs &q = b->seq;
+    std::vector<uint32_t> tok(T), prev(T), st(S), ln(S), sl(S), last(S);
+    uint64_t pos = 0;
+    for (uint64_t g = 0; g < S; g++) {
+        st[g] = (uint32_t)pos;
+        ln[g] = (uint32_t)segs[g].len;
+        sl[g] = (uint32_t)segs[g].slot;
+        for (uint64_t t = 0; t < segs[g].len; t++) {
+            if (segs[g].tok[t] >= I.vocab) return herr("prefill: token %u >= vocab", segs[g].tok[t]);
+            tok[pos + t] = segs[g].tok[t];
+            prev[pos + t] = t == 0 ? (0x80000000u | (uint32_t)segs[g].slot) : (uint32_t)(pos + t - 1);
+        }
+        pos += segs[g].len;
+        last[g] = (uint32_t)(pos - 1);
+    }
+    CK(rsv_upload_u32(c, q.tok, tok.data(), T));
+    CK(rsv_upload_u32(c, q.row_prev, prev.data(), T));
+    CK(rsv_upload_u32(c, q.seg_start, st.data(), S));
+    CK(rsv_upload_u32(c, q.seg_len, ln.data(), S));
+    CK(rsv_upload_u32(c, q.seg_slot, sl.data(), S));
+    CK(rsv_upload_u32(c, q.seg_last, last.data(), S));
+
+    CK(rsv_gather_rows_device_f16(c, b->emb_ln, q.x, q.tok, C, T));
+    for (uint64_t i = 0; i < I.n_layer; i++) {
+        Layer &L = b->layers[i];
+        const uint32_t coef6[6] = {L.x_r, L.x_w, L.x_k, L.x_v, L.x_a, L.x_g};
+        CK(rsv_seq_norm_mix(c, q.x, s.tmix_x[i], L.ln1_w, L.ln1_b, coef6, q.mix, 6, q.row_prev, T, C, LN_EPS));
+        CK(rsv_seq_state_store(c, q.x, s.tmix_x[i], L.ln1_w, L.ln1_b, q.seg_last, q.seg_slot, S, C, LN_EPS));
+        const uint32_t xr = q.mix[0], xw = q.mix[1], xk = q.mix[2], xv = q.mix[3], xa = q.mix[4], xg = q.mix[5];
+        HK(gemm_lin(b, L.rw, xr, q.r, T, 0));
+        HK(gemm_lin(b, L.kw, xk, q.k, T, 0));
+        HK(gemm_lin(b, L.vw, xv, q.v, T, 0));
+        CK(rsv_gemm_ex(c, xv, L.v1, nullptr, q.vmid, T, I.v_mid, C, 0, NONE, NONE, NONE));
+        CK(rsv_gemm_ex(c, xw, L.w1, nullptr, q.wmid, T, I.w_mid, C, 4, NONE, NONE, NONE));
+        CK(rsv_gemm_ex(c, xa, L.a1, nullptr, q.amid, T, I.a_mid, C, 0, NONE, NONE, NONE));
+        CK(rsv_gemm_ex(c, xg, L.g1, nullptr, q.gmid, T, I.g_mid, C, 8, NONE, NONE, NONE));
+        if (i == 0) {
+            CK(rsv_copy_device(c, q.v, q.vf));
+            CK(rsv_copy_rows(c, q.v, s.v_first, q.seg_last, q.seg_slot, S, C));
+        }
+        CK(rsv_gemm_ex(c, q.wmid, L.w2, nullptr, q.w, T, C, I.w_mid, 5, L.w0, NONE, b->scale_w));
+        CK(rsv_gemm_ex(c, q.amid, L.a2, nullptr, q.a, T, C, I.a_mid, 6, L.a0, NONE, NONE));
+        CK(rsv_gemm_ex(c, q.vmid, L.v2, nullptr, q.v, T, C, I.v_mid, 7, L.v0, q.vf, NONE));
+        CK(rsv_gemm_ex(c, q.gmid, L.g2, nullptr, q.g, T, C, I.g_mid, 0, NONE, NONE, NONE));
+        CK(rsv_wkv7_seq_ragged(c, s.rnn[i], q.r, q.w, q.k, q.v, q.a, L.k_k, L.k_a, L.r_k, L.lnx_w, L.lnx_b, q.yn,
+                               q.seg_start, q.seg_len, q.seg_slot, S, H, N, GN_EPS));
+        CK(rsv_mul_to_f16(c, q.yn, q.g, q.yg, T * C));
+        HK(gemm_lin(b, L.ow, q.yg, q.x, T, 2));
+        const uint32_t coef1[1] = {L.ffn_x_k};
+        CK(rsv_seq_norm_mix(c, q.x, s.cmix_x[i], L.ln2_w, L.ln2_b, coef1, &q.xb, 1, q.row_prev, T, C, LN_EPS));
+        CK(rsv_seq_state_store(c, q.x, s.cmix_x[i], L.ln2_w, L.ln2_b, q.seg_last, q.seg_slot, S, C, LN_EPS));
+        HK(gemm_lin(b, L.fk, q.xb, q.r2, T, 3));
+        HK(gemm_lin(b, L.fv, q.r2, q.x, T, 2));
+    }
+    if (logits) {
+        CK(rsv_copy_rows(c, q.x, q.xlast, q.seg_last, q.seg_iota, S, C));
+        CK(rsv_norm(c, q.xlast, b->ln_out_w, b->ln_out_b, q.xnorm, C, 1, LN_EPS, S));
+        HK(gemv_lin(b, b->head, q.xnorm, q.logits, S, 0));
+        CK(rsv_download(c, q.logits, logits, S * I.vocab));
+    } else {
+        CK(rsv_synchronize(c));
+    }
+    return 0;
+}
+
+constexpr uint64_t kMaxChunk = 4096;
+
+// Single-session prefill in chunks of at most kMaxChunk tokens.
+int seq_single(rsv_bundle *b, GpuState &s, uint64_t slot, const uint32_t *tokens, uint64_t n, float *logits) {
+    if (n == 0) return herr("infer_seq: empty token list");
+    for (uint64_t off = 0; off < n; off += kMaxChunk) {
+        const uint64_t len = n - off < kMaxChunk ? n - off : kMaxChunk;
+        std::vector<Seg> segs{{tokens + off, len, slot}};
+        HK(prefill(b, s, segs, off + len == n ? logits : nullptr));
+    }
+    return 0;
+}
+
+// ------------------------------------------------------------ self-loops
+int selfloop(rsv_bundle *b, GpuState &s, const uint32_t *seeds, uint64_t n, const rsv_sampler_params *sp,
+             uint32_t *out, float *ms) {
+    rsv_ctx *c = b->ctx;
+    const rsv_model_info &I = b->info;
+    const uint64_t B = s.batch;
+    if (n == 0) return 0;
+    WorkBufs *w;
+    HK(get_bufs(b, B, w));
+    uint32_t seq = NONE, cnt = NONE, temp = NONE, counter = NONE, sampler = NONE;
+    auto cleanup = [&]() {
+        for (uint32_t id : {seq, cnt, temp, counter, sampler})
+            if (id != NONE) rsv_tensor_free(c, id);
+    };
+    int rc = 0;
+    do {
+        if ((rc = new_tensor(b, n * B, RSV_U32, seq))) break;
+        if ((rc = new_tensor(b, B, RSV_U32, cnt))) break;
+        if (sp) {
+            if ((rc = new_tensor(b, I.vocab * B, RSV_F32, temp))) break;
+            if ((rc = new_tensor(b, I.vocab * B, RSV_U32, counter))) break;
+            if ((rc = new_tensor(b, 8 * B, RSV_F32, sampler))) break;
+        }
+        if (rsv_store_tokens(c, w->token, seeds, B)) { rc = herr("store_tokens: %s", rsv_last_error()); break; }
+        if (rsv_synchronize(c)) { rc = herr("%s", rsv_last_error()); break; }
+        if (rsv_graph_begin(c)) { rc = herr("graph_begin: %s", rsv_last_error()); break; }
+        int cap = decode_step(b, *w, s);
+        if (!cap) {
+            if (sp) cap = rsv_sample_into_host_seeded_batch(c, w->logits, w->token, I.vocab, temp, NONE, counter,
+                                                           sampler, seq, B);
+            else cap = rsv_argmax_batch(c, w->logits, w->token, I.vocab, B);
+            if (cap) herr("sampler: %s", rsv_last_error());
+        }
+        if (!cap && rsv_record_tokens(c, w->token, seq, cnt, n, B)) cap = herr("record: %s", rsv_last_error());
+        const int end_rc = rsv_graph_end(c);
+        if (cap) { rc = cap; break; }
+        if (end_rc) { rc = herr("graph_end: %s", rsv_last_error()); break; }
+        hipEvent_t e0 = nullptr, e1 = nullptr;
+        void *stream = nullptr;
+        rsv_stream(c, &stream);
+        if (ms) {
+            hipEventCreate(&e0);
+            hipEventCreate(&e1);
+            hipEventRecord(e0, (hipStream_t)stream);
+        }
+        std::vector<uint32_t> seeds_r(B);
+        for (uint64_t r = 0; r < n && !rc; r++) {
+            if (sp) {
+                // per-round seed = seed + round, hist_len = round (gpu_model.rs:799-812, 1712-1731)
+                for (uint64_t q = 0; q < B; q++) seeds_r[q] = seeds[q] + (uint32_t)r;
+                if (rsv_store_sampler_async_batch(c, sampler, r, sp->temperature, sp->top_k, sp->top_p, seeds_r.data(),
+                                                  B, sp->repetition_penalty, sp->frequency_penalty,
+                                                  sp->presence_penalty, (uint32_t)r))
+                    rc = herr("store_sampler: %s", rsv_last_error());
+            }
+            if (!rc && rsv_graph_replay(c)) rc = herr("graph_replay: %s", rsv_last_error());
+        }
+        if (ms) {
+            hipEventRecord(e1, (hipStream_t)stream);
+            hipEventSynchronize(e1);
+            hipEventElapsedTime(ms, e0, e1);
+            hipEventDestroy(e0);
+            hipEventDestroy(e1);
+        }
+        if (rc) break;
+        if (rsv_download_u32(c, seq, out, n * B)) { rc = herr("download: %s", rsv_last_error()); break; }
+    } while (0);
+    cleanup();
+    return rc;
+}
+
+}  // namespace
+
+// ================================================================ C-ABI
+extern "C" {
+
+const char *rsv_host_last_error(void) { return g_herr.c_str(); }
+
+int rsv_model_build(const char *path, int device, rsv_bundle **out) {
+    if (!path || !out) return herr("rsv_model_build: null argument");
+    auto b = std::make_unique<rsv_bundle>();
+    if (rsv_create(device, &b->ctx)) return herr("rsv_create: %s", rsv_last_error());
+    HK(load_model(b.get(), path));
+    b->state = new rsv_state();
+    if (state_create(b.get(), 1, b->state->s)) { delete b->state; b->state = nullptr; return -1; }
+    *out = b.release();
+    return 0;
+}
+
+int rsv_bundle_free(rsv_bundle *b) {
+    if (!b) return 0;
+    delete b->state;
+    delete b;
+    return 0;
+}
+
+int rsv_bundle_info(rsv_bundle *b, rsv_model_info *info) {
+    if (!b || !info) return herr("null argument");
+    *info = b->info;
+    return 0;
+}
+
+void *rsv_bundle_ctx(rsv_bundle *b) { return b ? (void *)b->ctx : nullptr; }
+
+static int tokens_ok(rsv_bundle *b, const uint32_t *t, uint64_t n) {
+    if (!b) return herr("null bundle");
+    if (n == 0) return herr("empty token list");
+    if (!t) return herr("null tokens");
+    for (uint64_t i = 0; i < n; i++)
+        if (t[i] >= b->info.vocab) return herr("token %u at %llu >= vocab %llu", t[i], (unsigned long long)i, (unsigned long long)b->info.vocab);
+    return 0;
+}
+
+// forward_with_state (gpu_model.rs:668): token-by-token decode path.
+static int run_tokens(rsv_bundle *b, GpuState &s, const uint32_t *tokens, uint64_t n) {
+    WorkBufs *w;
+    HK(get_bufs(b, 1, w));
+    for (uint64_t t = 0; t < n; t++) {
+        CK(rsv_store_token(b->ctx, w->token, tokens[t]));
+        HK(decode_step(b, *w, s));
+    }
+    return 0;
+}
+
+int rsv_infer_tokens(rsv_bundle *b, const uint32_t *tokens, uint64_t n, float *logits) {
+    HK(tokens_ok(b, tokens, n));
+    HK(run_tokens(b, b->state->s, tokens, n));
+    CK(rsv_download(b->ctx, b->bufs[1].logits, logits, b->info.vocab));
+    return 0;
+}
+
+int rsv_infer_seq(rsv_bundle *b, const uint32_t *tokens, uint64_t n, float *logits) {
+    HK(tokens_ok(b, tokens, n));
+    return seq_single(b, b->state->s, 0, tokens, n, logits);
+}
+
+int rsv_infer_chunked(rsv_bundle *b, const uint32_t *tokens, uint64_t n, uint64_t chunk, float *logits) {
+    HK(tokens_ok(b, tokens, n));
+    if (chunk == 0) chunk = 1;
+    for (uint64_t off = 0; off < n; off += chunk) {
+        const uint64_t len = n - off < chunk ? n - off : chunk;
+        HK(seq_single(b, b->state->s, 0, tokens + off, len, off + len == n ? logits : nullptr));
+    }
+    return 0;
+}
+
+int rsv_infer_full(rsv_bundle *b, const uint32_t *tokens, uint64_t n, float *logits) {
+    HK(tokens_ok(b, tokens, n));
+    for (uint64_t t = 0; t < n; t++) HK(seq_single(b, b->state->s, 0, tokens + t, 1, logits + t * b->info.vocab));
+    return 0;
+}
+
+int rsv_infer_argmax(rsv_bundle *b, const uint32_t *tokens, uint64_t n, uint32_t *token) {
+    HK(tokens_ok(b, tokens, n));
+    HK(run_tokens(b, b->state->s, tokens, n));
+    WorkBufs &w = b->bufs[1];
+    CK(rsv_argmax(b->ctx, w.logits, w.token, b->info.vocab));
+    CK(rsv_download_u32(b->ctx, w.token, token, 1));
+    return 0;
+}
+
+int rsv_infer_argmax_selfloop(rsv_bundle *b, uint32_t seed, uint64_t n, uint32_t *out) {
+    if (!b) return herr("null bundle");
+    if (seed >= b->info.vocab) return herr("seed token %u >= vocab", seed);
+    return selfloop(b, b->state->s, &seed, n, nullptr, out, nullptr);
+}
+
+int rsv_infer_sample(rsv_bundle *b, const uint32_t *tokens, uint64_t n, const rsv_sampler_params *sp,
+                     const uint32_t *history, uint64_t hist_len, uint32_t *token) {
+    HK(tokens_ok(b, tokens, n));
+    if (!sp) return herr("null sampler params");
+    HK(run_tokens(b, b->state->s, tokens, n));
+    WorkBufs &w = b->bufs[1];
+    CK(rsv_sample(b->ctx, w.logits, w.token, b->info.vocab, sp->temperature, sp->top_k, sp->top_p, sp->seed,
+                  sp->repetition_penalty, sp->frequency_penalty, sp->presence_penalty, history, hist_len));
+    CK(rsv_download_u32(b->ctx, w.token, token, 1));
+    return 0;
+}
+
+int rsv_infer_sample_selfloop(rsv_bundle *b, uint32_t seed, uint64_t n, const rsv_sampler_params *sp,
+                              uint32_t *out) {
+    if (!b || !sp) return herr("null argument");
+    if (seed >= b->info.vocab) return herr("seed token %u >= vocab", seed);
+    return selfloop(b, b->state->s, &seed, n, sp, out, nullptr);
+}
+
+int rsv_state_len(rsv_bundle *b, uint64_t *len) {
+    if (!b || !len) return herr("null argument");
+    *len = state_len1(b);
+    return 0;
+}
+
+int rsv_state_back(rsv_bundle *b, float *out) {
+    if (!b || !out) return herr("null argument");
+    return state_back_slots(b, b->state->s, 0, 1, out);
+}
+
+int rsv_state_load(rsv_bundle *b, const float *data, uint64_t len) {
+    if (!b || !data) return herr("null argument");
+    if (len != state_len1(b))
+        return herr("State::load length mismatch: got %llu, expected %llu", (unsigned long long)len, (unsigned long long)state_len1(b));
+    return state_load_slots(b, b->state->s, 0, 1, data);
+}
+
+int rsv_reset(rsv_bundle *b) {
+    if (!b) return herr("null bundle");
+    return state_reset(b, b->state->s);
+}
+
+int rsv_create_batch_state(rsv_bundle *b, uint64_t batch, rsv_state **out) {
+    if (!b || !out) return herr("null argument");
+    if (batch == 0) return herr("batch must be >= 1");
+    auto s = std::make_unique<rsv_state>();
+    if (state_create(b, batch, s->s)) { state_free(b, s->s); return -1; }
+    *out = s.release();
+    return 0;
+}
+
+int rsv_state_free(rsv_bundle *b, rsv_state *s) {
+    if (!b || !s) return 0;
+    state_free(b, s->s);
+    delete s;
+    return 0;
+}
+
+int rsv_state_batch(rsv_state *s, uint64_t *batch) {
+    if (!s || !batch) return herr("null argument");
+    *batch = s->s.batch;
+    return 0;
+}
+
+int rsv_batch_state_back(rsv_bundle *b, rsv_state *s, float *out) {
+    if (!b || !s || !out) return herr("null argument");
+    return state_back_slots(b, s->s, 0, s->s.batch, out);
+}
+
+int rsv_batch_state_load(rsv_bundle *b, rsv_state *s, const float *data, uint64_t len) {
+    if (!b || !s || !data) return herr("null argument");
+    if (len != state_len1(b) * s->s.batch)
+        return herr("State::load length mismatch: got %llu, expected %llu", (unsigned long long)len, (unsigned long long)(state_len1(b) * s->s.batch));
+    return state_load_slots(b, s->s, 0, s->s.batch, data);
+}
+
+int rsv_state_slot_back(rsv_bundle *b, rsv_state *s, uint64_t slot, float *out) {
+    if (!b || !s || !out) return herr("null argument");
+    if (slot >= s->s.batch) return herr("slot_back: slot %llu >= batch %llu", (unsigned long long)slot, (unsigned long long)s->s.batch);
+    return state_back_slots(b, s->s, slot, 1, out);
+}
+
+int rsv_state_slot_load(rsv_bundle *b, rsv_state *s, uint64_t slot, const float *data, uint64_t len) {
+    if (!b || !s || !data) return herr("null argument");
+    if (slot >= s->s.batch) return herr("slot_load: slot %llu >= batch %llu", (unsigned long long)slot, (unsigned long long)s->s.batch);
+    if (len != state_len1(b))
+        return herr("State::slot_load length mismatch: got %llu, expected %llu", (unsigned long long)len, (unsigned long long)state_len1(b));
+    return state_load_slots(b, s->s, slot, 1, data);
+}
+
+int rsv_batch_state_reset(rsv_bundle *b, rsv_state *s) {
+    if (!b || !s) return herr("null argument");
+    return state_reset(b, s->s);
+}
+
+int rsv_forward_seq_batch(rsv_bundle *b, rsv_state *s, const uint32_t *tokens, const uint64_t *lens, uint32_t *seeds,
+                          float *logits) {
+    if (!b || !s || !tokens || !lens) return herr("null argument");
+    const uint64_t B = s->s.batch;
+    std::vector<Seg> segs;
+    uint64_t off = 0, T = 0;
+    for (uint64_t q = 0; q < B; q++) {
+        if (lens[q] == 0) return herr("forward_seq_batch: prompt %llu is empty", (unsigned long long)q);
+        HK(tokens_ok(b, tokens + off, lens[q]));
+        segs.push_back({tokens + off, lens[q], q});
+        if (seeds) seeds[q] = tokens[off + lens[q] - 1];
+        off += lens[q];
+        T += lens[q];
+    }
+    // split into packed chunks of at most kMaxChunk tokens; long prompts are
+    // cut into consecutive pieces that keep their slot order
+    std::vector<Seg> pending;
+    uint64_t used = 0;
+    std::vector<float> lg;
+    auto flush = [&]() -> int {
+        if (pending.empty()) return 0;
+        std::vector<float> tmp;
+        if (logits) tmp.resize(pending.size() * b->info.vocab);
+        HK(prefill(b, s->s, pending, logits ? tmp.data() : nullptr));
+        if (logits)
+            for (size_t i = 0; i < pending.size(); i++)
+                memcpy(logits + pending[i].slot * b->info.vocab, &tmp[i * b->info.vocab], b->info.vocab * 4);
+        pending.clear();
+        used = 0;
+        return 0;
+    };
+    for (auto &g : segs) {
+        uint64_t done = 0;
+        while (done < g.len) {
+            if (used == kMaxChunk) HK(flush());
+            // a slot may appear only once per packed chunk
+            for (auto &p : pending)
+                if (p.slot == g.slot) { HK(flush()); break; }
+            const uint64_t take = std::min<uint64_t>(g.len - done, kMaxChunk - used);
+            pending.push_back({g.tok + done, take, g.slot});
+            used += take;
+            done += take;
+        }
+    }
+    HK(flush());
+    return 0;
+}
+
+int rsv_forward_tokens_batch(rsv_bundle *b, rsv_state *s, const uint32_t *tokens, float *logits) {
+    if (!b || !s || !tokens) return herr("null argument");
+    const uint64_t B = s->s.batch;
+    HK(tokens_ok(b, tokens, B));
+    WorkBufs *w;
+    HK(get_bufs(b, B, w));
+    CK(rsv_store_tokens(b->ctx, w->token, tokens, B));
+    HK(decode_step(b, *w, s->s));
+    if (logits) CK(rsv_download(b->ctx, w->logits, logits, B * b->info.vocab));
+    else CK(rsv_synchronize(b->ctx));
+    return 0;
+}
+
+int rsv_argmax_selfloop_batch(rsv_bundle *b, rsv_state *s, const uint32_t *seeds, uint64_t n, uint32_t *out) {
+    if (!b || !s || !seeds || !out) return herr("null argument");
+    HK(tokens_ok(b, seeds, s->s.batch));
+    return selfloop(b, s->s, seeds, n, nullptr, out, nullptr);
+}
+
+int rsv_argmax_selfloop_batch_timed(rsv_bundle *b, rsv_state *s, const uint32_t *seeds, uint64_t n, uint32_t *out,
+                                    float *ms) {
+    if (!b || !s || !seeds || !out || !ms) return herr("null argument");
+    HK(tokens_ok(b, seeds, s->s.batch));
+    return selfloop(b, s->s, seeds, n, nullptr, out, ms);
+}
+
+int rsv_sample_selfloop_batch(rsv_bundle *b, rsv_state *s, const uint32_t *seeds, uint64_t n,
+                              const rsv_sampler_params *sp, uint32_t *out) {
+    if (!b || !s || !seeds || !out || !sp) return herr("null argument");
+    HK(tokens_ok(b, seeds, s->s.batch));
+    return selfloop(b, s->s, seeds, n, sp, out, nullptr);
+}
+
+}  // extern "C"

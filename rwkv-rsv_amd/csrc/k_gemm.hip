@@ -1,0 +1,184 @@
+// Prefill GEMM on CDNA matrix cores: C[m,n] = epi(A[m,k] . B[n,k]^T).
+//
+// A (token activations) is fp16 row-major; B (weights, [out,in]) is fp16 or
+// the reference int8 format, dequantised to fp16 in the tile loader
+// (w = s*q + z in fp32, rounded to fp16 -- the same rounding as the
+// reference's dequant-to-fp16 prefill scheme, backend_cuda.rs:4195-4227).
+// Accumulation is fp32 (v_mfma_f32_32x32x8_f16).
+//
+// Tile: 128x128 per 256-thread block, BK = 32; each wave owns a 64x64
+// quadrant as 2x2 MFMA 32x32 blocks.  The next K-slab is prefetched into
+// registers while the current one is multiplied out of LDS.
+#include "rsv_common.h"
+
+namespace rsv {
+
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef float float16_t __attribute__((ext_vector_type(16)));
+typedef unsigned int u32x4g __attribute__((ext_vector_type(4)));
+
+constexpr int BM = 128, BN = 128, BK = 32, LDK = BK + 8;
+
+__device__ __forceinline__ float sigm_g(float v) { return 1.0f / (1.0f + expf(-v)); }
+__device__ __forceinline__ float h2f_g(uint32_t b) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(b & 0xFFFFu));
+}
+
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+    const uint16_t lo = __builtin_bit_cast(uint16_t, (_Float16)a);
+    const uint16_t hi = __builtin_bit_cast(uint16_t, (_Float16)b);
+    return (uint32_t)lo | ((uint32_t)hi << 16);
+}
+
+template <bool B_I8>
+__global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
+    __shared__ __attribute__((aligned(16))) _Float16 As[BM * LDK];
+    __shared__ __attribute__((aligned(16))) _Float16 Bs[BN * LDK];
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+    const int lr = tid >> 1, lc = (tid & 1) * 16;  // loader: row, first k of 16
+
+    float16_t acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) acc[i][j][e] = 0.0f;
+
+    u32x4g ra[2], rb[2];
+    uint32_t rsz = 0;
+    const int arow = m0 + lr, brow = n0 + lr;
+    const bool aok = arow < g.m, bok = brow < g.n;
+    const int KG = g.k / 128;
+
+    auto load = [&](int k0) {
+        if (aok) {
+            const u32x4g *p = (const u32x4g *)(g.a + (size_t)arow * g.lda + k0 + lc);
+            ra[0] = p[0];
+            ra[1] = p[1];
+        } else {
+            ra[0] = ra[1] = (u32x4g){0u, 0u, 0u, 0u};
+        }
+        if (B_I8) {
+            if (bok) {
+                rb[0] = *(const u32x4g *)((const uint8_t *)g.b + (size_t)brow * g.k + k0 + lc);
+                rsz = g.sz[(size_t)brow * KG + (k0 + lc) / 128];
+            } else {
+                rb[0] = (u32x4g){0u, 0u, 0u, 0u};
+                rsz = 0;
+            }
+        } else {
+            if (bok) {
+                const u32x4g *p = (const u32x4g *)((const _Float16 *)g.b + (size_t)brow * g.k + k0 + lc);
+                rb[0] = p[0];
+                rb[1] = p[1];
+            } else {
+                rb[0] = rb[1] = (u32x4g){0u, 0u, 0u, 0u};
+            }
+        }
+    };
+
+    load(0);
+    for (int k0 = 0; k0 < g.k; k0 += BK) {
+        __syncthreads();
+        u32x4g *ad = (u32x4g *)(As + lr * LDK + lc);
+        ad[0] = ra[0];
+        ad[1] = ra[1];
+        u32x4g *bd = (u32x4g *)(Bs + lr * LDK + lc);
+        if (B_I8) {
+            const float s = h2f_g(rsz), z = h2f_g(rsz >> 16);
+            uint32_t o[8];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const uint32_t w = rb[0][q];
+                const float w0 = __fadd_rn(__fmul_rn(s, (float)(w & 0xFFu)), z);
+                const float w1 = __fadd_rn(__fmul_rn(s, (float)((w >> 8) & 0xFFu)), z);
+                const float w2 = __fadd_rn(__fmul_rn(s, (float)((w >> 16) & 0xFFu)), z);
+                const float w3 = __fadd_rn(__fmul_rn(s, (float)(w >> 24)), z);
+                o[2 * q] = pack2(w0, w1);
+                o[2 * q + 1] = pack2(w2, w3);
+            }
+            bd[0] = (u32x4g){o[0], o[1], o[2], o[3]};
+            bd[1] = (u32x4g){o[4], o[5], o[6], o[7]};
+        } else {
+            bd[0] = rb[0];
+            bd[1] = rb[1];
+        }
+        __syncthreads();
+        if (k0 + BK < g.k) load(k0 + BK);
+#pragma unroll
+        for (int kk = 0; kk < BK; kk += 8) {
+            half4_t af[2], bf[2];
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+                af[i] = *(const half4_t *)(As + (wm + i * 32 + (lane & 31)) * LDK + kk + (lane >> 5) * 4);
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+                bf[j] = *(const half4_t *)(Bs + (wn + j * 32 + (lane & 31)) * LDK + kk + (lane >> 5) * 4);
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int j = 0; j < 2; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x8f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+    }
+
+    // epilogue: acc[i][j][e] -> row = 8*(e/4) + 4*(lane/32) + e%4, col = lane%32
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int col = n0 + wn + j * 32 + (lane & 31);
+            if (col >= g.n) continue;
+            const float bias = g.bias ? g.bias[col] : 0.0f;
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                const int row = m0 + wm + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+                if (row >= g.m) continue;
+                const size_t o = (size_t)row * g.ldc + col;
+                float v = acc[i][j][e];
+                switch (g.epi) {
+                    case GE_BIAS: v += bias; break;
+                    case GE_ADD: v += g.aux[o]; break;
+                    case GE_RELU2: v = v > 0.0f ? v * v : 0.0f; break;
+                    case GE_TANH: v = tanhf(v); break;
+                    case GE_WDECAY: v = expf(sigm_g(v + bias) * g.scale[0]); break;
+                    case GE_SIGBIAS: v = sigm_g(v + bias); break;
+                    case GE_VLERP: {
+                        const float cur = ((const float *)g.c)[o];
+                        v = cur + sigm_g(v + bias) * (g.aux[o] - cur);
+                    } break;
+                    case GE_SIGMOID: v = sigm_g(v); break;
+                    default: break;
+                }
+                if (g.c_f16)
+                    ((_Float16 *)g.c)[o] = (_Float16)v;
+                else
+                    ((float *)g.c)[o] = v;
+            }
+        }
+}
+
+int launch_gemm(rsv_ctx *ctx, const GemmArgs &g) {
+    if (g.m <= 0 || g.n <= 0 || g.k <= 0) return RSV_FAIL("gemm: bad shape m=%d n=%d k=%d", g.m, g.n, g.k);
+    if (g.k % BK != 0) return RSV_FAIL("gemm: k=%d must be a multiple of %d", g.k, BK);
+    if (g.b_i8 && (g.k % 128 != 0 || !g.sz)) return RSV_FAIL("gemm: int8 weights need k %% 128 == 0 and scales");
+    if (g.lda < g.k || g.lda % 8 != 0) return RSV_FAIL("gemm: lda=%d must be >= k and a multiple of 8", g.lda);
+    if (g.ldc < g.n) return RSV_FAIL("gemm: ldc=%d < n=%d", g.ldc, g.n);
+    if ((g.epi == GE_ADD || g.epi == GE_VLERP) && !g.aux) return RSV_FAIL("gemm: epilogue needs aux");
+    if ((g.epi == GE_BIAS || g.epi == GE_WDECAY || g.epi == GE_SIGBIAS || g.epi == GE_VLERP) && !g.bias)
+        return RSV_FAIL("gemm: epilogue needs bias");
+    if (g.epi == GE_WDECAY && !g.scale) return RSV_FAIL("gemm: decay epilogue needs scale");
+    if (g.c_f16 && (g.epi == GE_ADD || g.epi == GE_VLERP)) return RSV_FAIL("gemm: in-place epilogues need fp32 C");
+    dim3 grid((g.n + BN - 1) / BN, (g.m + BM - 1) / BM);
+    if (g.b_i8)
+        hipLaunchKernelGGL(k_gemm<true>, grid, dim3(256), 0, ctx->stream, g);
+    else
+        hipLaunchKernelGGL(k_gemm<false>, grid, dim3(256), 0, ctx->stream, g);
+    RSV_HIP(hipGetLastError());
+    return 0;
+}
+
+}  // namespace rsv

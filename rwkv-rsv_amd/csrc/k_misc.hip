@@ -1,0 +1,564 @@
+// Elementwise, normalisation, gather, argmax and token-record kernels of the
+// decode and prefill paths.  All per-session buffers are [batch, ...].
+#include "rsv_common.h"
+
+namespace rsv {
+
+__device__ __forceinline__ float sigmoid_m(float v) { return 1.0f / (1.0f + expf(-v)); }
+
+// Block-wide sum for 256-thread blocks (4 waves).
+__device__ __forceinline__ float block_sum256(float v, float *red) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    const int w = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[w] = v;
+    __syncthreads();
+    return red[0] + red[1] + red[2] + red[3];
+}
+
+// ------------------------------------------------ LayerNorm + token shift
+// model.rs:402-411 / 487-490: ln = LN(x); out_j = ln + coef_j*(prev - ln);
+// state = ln.  grid (batch), block 256; c <= 256*kMaxPer.
+constexpr int kMaxPer = 16;
+struct Ptr6 { const float *p[6]; };
+struct Out6 { float *p[6]; };
+
+__global__ __launch_bounds__(256) void k_norm_lerp(const float *__restrict__ x, float *__restrict__ state,
+                                                   const float *__restrict__ gamma, const float *__restrict__ beta,
+                                                   Ptr6 coef, Out6 out, int nout, int C, float eps) {
+    __shared__ float red[4];
+    const int b = blockIdx.x, tid = threadIdx.x;
+    const float *xb = x + (size_t)b * C;
+    float xv[kMaxPer];
+    float s = 0.0f;
+#pragma unroll
+    for (int m = 0; m < kMaxPer; m++) {
+        const int i = tid + 256 * m;
+        xv[m] = i < C ? xb[i] : 0.0f;
+        s += xv[m];
+    }
+    const float mean = block_sum256(s, red) / (float)C;
+    float q = 0.0f;
+#pragma unroll
+    for (int m = 0; m < kMaxPer; m++) {
+        const int i = tid + 256 * m;
+        const float d = xv[m] - mean;
+        q += i < C ? d * d : 0.0f;
+    }
+    const float var = block_sum256(q, red) / (float)C + eps;
+    const float inv_std = 1.0f / sqrtf(var);
+#pragma unroll
+    for (int m = 0; m < kMaxPer; m++) {
+        const int i = tid + 256 * m;
+        if (i >= C) break;
+        const float ln = (xv[m] - mean) * inv_std * gamma[i] + beta[i];
+        const size_t o = (size_t)b * C + i;
+        const float prev = state[o];
+        const float dlt = prev - ln;
+        for (int j = 0; j < nout; j++) out.p[j][o] = ln + coef.p[j][i] * dlt;
+        state[o] = ln;
+    }
+}
+
+int launch_norm_lerp(rsv_ctx *ctx, const float *x, float *state, const float *gamma, const float *beta,
+                     const float *const *coef, float *const *out, int nout, int c, float eps, int batch) {
+    if (c <= 0 || c > 256 * kMaxPer) return RSV_FAIL("norm_lerp: c=%d outside 1..%d", c, 256 * kMaxPer);
+    if (nout < 1 || nout > 6) return RSV_FAIL("norm_lerp: nout=%d", nout);
+    Ptr6 cp{};
+    Out6 op{};
+    for (int j = 0; j < nout; j++) { cp.p[j] = coef[j]; op.p[j] = out[j]; }
+    hipLaunchKernelGGL(k_norm_lerp, dim3(batch), dim3(256), 0, ctx->stream, x, state, gamma, beta, cp, op, nout,
+                       c, eps);
+    RSV_HIP(hipGetLastError());
+    return 0;
+}
+
+// ---------------------------------------------- LayerNorm / GroupNorm rows
+// backend.rs:171 semantics: rows*h groups of c elements; gamma/beta indexed
+// by (group % h)*c + i.  Two-pass statistics (model.rs:625-635).
+__global__ __launch_bounds__(256) void k_norm(const float *__restrict__ x, const float *__restrict__ gamma,
+                                              const float *__restrict__ beta, float *__restrict__ y, int c,
+                                              int h, float eps) {
+    __shared__ float red[4];
+    const int g = blockIdx.x, hh = g % h, tid = threadIdx.x;
+    const float *xg = x + (size_t)g * c;
+    float s = 0.0f;
+    for (int i = tid; i < c; i += 256) s += xg[i];
+    const float mean = block_sum256(s, red) / (float)c;
+    float q = 0.0f;
+    for (int i = tid; i < c; i += 256) { const float d = xg[i] - mean; q += d * d; }
+    const float var = block_sum256(q, red) / (float)c + eps;
+    const float inv_std = 1.0f / sqrtf(var);
+    for (int i = tid; i < c; i += 256)
+        y[(size_t)g * c + i] = (xg[i] - mean) * inv_std * gamma[hh * c + i] + beta[hh * c + i];
+}
+
+int launch_norm(rsv_ctx *ctx, const float *x, const float *gamma, const float *beta, float *y, int c,
+                int h, float eps, int rows) {
+    if (c <= 0 || h <= 0 || rows <= 0) return RSV_FAIL("norm: bad c=%d h=%d rows=%d", c, h, rows);
+    hipLaunchKernelGGL(k_norm, dim3(rows * h), dim3(256), 0, ctx->stream, x, gamma, beta, y, c, h, eps);
+    RSV_HIP(hipGetLastError());
+    return 0;
+}
+
+// ------------------------------------------------------------- gather rows
+// Token ids at or beyond the table size produce a zero row instead of an
+// out-of-bounds read.
+__global__ void k_gather_rows(const void *__restrict__ src, int src_f16, uint64_t rows, float *__restrict__ dst,
+                              const uint32_t *__restrict__ tok, int c) {
+    const int b = blockIdx.y;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= c) return;
+    const size_t row = tok[b];
+    if (row >= rows) { dst[(size_t)b * c + i] = 0.0f; return; }
+    float v;
+    if (src_f16)
+        v = (float)((const _Float16 *)src)[row * c + i];
+    else
+        v = ((const float *)src)[row * c + i];
+    dst[(size_t)b * c + i] = v;
+}
+
+int launch_gather_rows(rsv_ctx *ctx, const void *src, int src_f16, uint64_t src_rows, float *dst,
+                       const uint32_t *tok, int c, int batch) {
+    if (batch <= 0) return 0;
+    hipLaunchKernelGGL(k_gather_rows, dim3((c + 255) / 256, batch), dim3(256), 0, ctx->stream, src, src_f16,
+                       src_rows, dst, tok, c);
+    RSV_HIP(hipGetLastError());
+    return 0;
+}
+
+// ------------------------------------------------------------------ argmax
+// Ties go to the smaller index (backend_cuda.rs:3640-3680); the scan starts
+// from -1e30 at index 0 like the reference.  grid (batch), block 1024.
+__global__ __launch_bounds__(1024) void k_argmax(const float *__restrict__ logits, uint32_t *__restrict__ tok,
+                                                 int n) {
+    __shared__ float sv[16];
+    __shared__ int si[16];
+    const int b = blockIdx.x, tid = threadIdx.x;
+    const float *lg = logits + (size_t)b * n;
+    float bv = -1e30f;
+    int bi = 0;
+    for (int i = tid; i < n; i += 1024) {
+        const float v = lg[i];
+        if (v > bv) { bv = v; bi = i; }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(bv, o, 64);
+        const int oi = __shfl_xor(bi, o, 64);
+        if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+    }
+    if ((tid & 63) == 0) { sv[tid >> 6] = bv; si[tid >> 6] = bi; }
+    __syncthreads();
+    if (tid == 0) {
+        float v = sv[0];
+        int ix = si[0];
+        for (int w = 1; w < 16; w++)
+            if (sv[w] > v || (sv[w] == v && si[w] < ix)) { v = sv[w]; ix = si[w]; }
+        tok[b] = (uint32_t)ix;
+    }
+}
+
+int launch_argmax(rsv_ctx *ctx, const float *logits, uint32_t *tok, int n, int batch) {
+    if (n <= 0 || batch <= 0) return RSV_FAIL("argmax: bad n=%d batch=%d", n, batch);
+    hipLaunchKernelGGL(k_argmax, dim3(batch), dim3(1024), 0, ctx->stream, logits, tok, n);
+    RSV_HIP(hipGetLastError());
+    return 0;
+}
+
+// ------------------------------------------------------------ token record
+// out_seq[b*stride + cnt[b]++] = in_tok[b] (backend.rs:621, 981).  The slot
+// is bounded by stride so a replay past the buffer end cannot write outside.
+__global__ void k_record_tokens(const uint32_t *__restrict__ in_tok, uint32_t *__restrict__ out_seq,
+                                uint32_t *__restrict__ cnt, int stride, int batch) {
+    const int b = blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= batch) return;
+    const uint32_t i = cnt[b];
+    if (i < (uint32_t)stride) out_seq[(size_t)b * stride + i] = in_tok[b];
+    cnt[b] = i + 1u;
+}
+
+int launch_record_tokens(rsv_ctx *ctx, const uint32_t *in_tok, uint32_t *out_seq, uint32_t *cnt, int stride,
+                         int batch) {
+    hipLaunchKernelGGL(k_record_tokens, dim3((batch + 255) / 256), dim3(256), 0, ctx->stream, in_tok, out_seq,
+                       cnt, stride, batch);
+    RSV_HIP(hipGetLastError());
+    return 0;
+}
+
+// --------------------------------------------------- stream-ordered stores
+constexpr int kMaxVals = 64;
+struct Vals { uint32_t v[kMaxVals]; };
+
+__global__ void k_set_u32(uint32_t *dst, Vals vals, int n) {
+    const int i = threadIdx.x;
+    if (i < n) dst[i] = vals.v[i];
+}
+
+int launch_set_u32(rsv_ctx *ctx, uint32_t *dst, const uint32_t *vals, int n) {
+    for (int off = 0; off < n; off += kMaxVals) {
+        const int cnt = n - off < kMaxVals ? n - off : kMaxVals;
+        Vals v{};
+        for (int i = 0; i < cnt; i++) v.v[i] = vals[off + i];
+        hipLaunchKernelGGL(k_set_u32, dim3(1), dim3(64), 0, ctx->stream, dst + off, v, cnt);
+        RSV_HIP(hipGetLastError());
+    }
+    return 0;
+}
+
+// Sampler row layout (backend_cuda.rs:3700-3718): [T, top_k bits, top_p,
+// seed bits, rep, freq, pres, hist_len bits], one row of 8 per slot.
+struct SamplerRow { float t; uint32_t k; float p; float rep, freq, pres; uint32_t hist; };
+__global__ void k_store_sampler(float *dst, SamplerRow row, Vals seeds, int n) {
+    const int b = threadIdx.x;
+    if (b >= n) return;
+    float *d = dst + (size_t)b * 8;
+    d[0] = row.t;
+    d[1] = __uint_as_float(row.k);
+    d[2] = row.p;
+    d[3] = __uint_as_float(seeds.v[b]);
+    d[4] = row.rep;
+    d[5] = row.freq;
+    d[6] = row.pres;
+    d[7] = __uint_as_float(row.hist);
+}
+
+int launch_store_sampler(rsv_ctx *ctx, float *dst, float temperature, uint32_t top_k, float top_p,
+                         const uint32_t *seeds, int batch, float rep, float freq, float pres,
+                         uint32_t hist_len) {
+    SamplerRow row{temperature, top_k, top_p, rep, freq, pres, hist_len};
+    for (int off = 0; off < batch; off += kMaxVals) {
+        const int cnt = batch - off < kMaxVals ? batch - off : kMaxVals;
+        Vals v{};
+        for (int i = 0; i < cnt; i++) v.v[i] = seeds[off + i];
+        hipLaunchKernelGGL(k_store_sampler, dim3(1), dim3(64), 0, ctx->stream, dst + (size_t)off * 8, row, v, cnt);
+        RSV_HIP(hipGetLastError());
+    }
+    return 0;
+}
+
+int launch_copy(rsv_ctx *ctx, void *dst, const void *src, size_t bytes) {
+    if (bytes == 0) return 0;
+    RSV_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, ctx->stream));
+    return 0;
+}
+
+// -------------------------------------------------------------- elementwise
+// op 0: y = sigmoid(a); 1: y = sigmoid(y); 2: y = exp(a * b[row]); 3: y = a*b
+__global__ void k_elementwise(int op, const float *__restrict__ a, const float *__restrict__ b, float *y, int c,
+                              int batch) {
+    const size_t total = (size_t)c * batch;
+    for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (size_t)gridDim.x * blockDim.x) {
+        switch (op) {
+            case 0: y[e] = sigmoid_m(a[e]); break;
+            case 1: y[e] = sigmoid_m(y[e]); break;
+            case 2: y[e] = expf(a[e] * b[e / c]); break;
+            default: y[e] = a[e] * b[e]; break;
+        }
+    }
+}
+
+int launch_elementwise(rsv_ctx *ctx, int op, const float *a, const float *b, float *y, int c, int batch) {
+    const size_t total = (size_t)c * batch;
+    if (total == 0) return 0;
+    size_t blocks = (total + 255) / 256;
+    if (blocks > 16384) blocks = 16384;
+    hipLaunchKernelGGL(k_elementwise, dim3((unsigned)blocks), dim3(256), 0, ctx->stream, op, a, b, y, c, batch);
+    RSV_HIP(hipGetLastError());
+    return 0;
+}
+
+// f32 -> f16 rows; rows in [t, m_pad) are zeroed (backend.rs:728).
+__global__ void k_to_f16(const float *__restrict__ x, _Float16 *__restrict__ y, int c, int t, int m_pad, int sx,
+                         int sy) {
+    const int row = blockIdx.y;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < c; i += gridDim.x * blockDim.x)
+        y[(size_t)row * sy + i] = row < t ? (_Float16)x[(size_t)row * sx + i] : (_Float16)0.0f;
+}
+
+int launch_to_f16(rsv_ctx *ctx, const float *x, _Float16 *y, int c, int t, int m_pad, int x_stride,
+                  int y_stride) {
+    if (m_pad < t) return RSV_FAIL("to_f16: m_pad %d < t %d", m_pad, t);
+    if (m_pad == 0) return 0;
+    hipLaunchKernelGGL(k_to_f16, dim3((c + 255) / 256, m_pad), dim3(256), 0, ctx->stream, x, y, c, t, m_pad,
+                       x_stride, y_stride);
+    RSV_HIP(hipGetLastError());
+    return 0;
+}
+
+// v = v + gate*(v_first - v), v_first is one [c] row shared by all t rows.
+__global__ void k_v_first_lerp(float *v, const float *__restrict__ gate, const float *__restrict__ vf, int c,
+                               int t, int stride) {
+    const int row = blockIdx.y;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < c; i += gridDim.x * blockDim.x) {
+        const size_t o = (size_t)row * stride + i;
+        const float cur = v[o];
+        v[o] = cur + gate[o] * (vf[i] - cur);
+    }
+}
+
+int launch_v_first_lerp(rsv_ctx *ctx, float *v, const float *gate, const float *vf, int c, int t, int stride) {
+    if (t <= 0) return 0;
+    hipLaunchKernelGGL(k_v_first_lerp, dim3((c + 255) / 256, t), dim3(256), 0, ctx->stream, v, gate, vf, c, t,
+                       stride);
+    RSV_HIP(hipGetLastError());
+    return 0;
+}
+
+// fuse_ka (backend.rs:765): k_mod, kk_l2, b per token row.  grid (h, batch), block 64.
+__global__ __launch_bounds__(64) void k_fuse_ka(const float *__restrict__ k, const float *__restrict__ kk,
+                                                const float *__restrict__ a, const float *__restrict__ ka,
+                                                float *kmod, float *kkl2, float *bo, int H) {
+    const int h = blockIdx.x, b = blockIdx.y, i = threadIdx.x;
+    const size_t o = (size_t)b * H * 64 + h * 64 + i;
+    const float ki = k[o], ai = a[o];
+    const float kkv = ki * kk[h * 64 + i];
+    float ss = kkv * kkv;
+#pragma unroll
+    for (int s = 32; s > 0; s >>= 1) ss += __shfl_xor(ss, s, 64);
+    float nrm = sqrtf(ss);
+    nrm = nrm < 1e-12f ? 1e-12f : nrm;
+    const float kh = kkv * (1.0f / nrm);
+    kmod[o] = ki + ka[h * 64 + i] * (ki * ai - ki);
+    kkl2[o] = kh;
+    bo[o] = kh * (-ai);
+}
+
+int launch_fuse_ka(rsv_ctx *ctx, const float *k, const float *kk, const float *a, const float *ka,
+                   float *kmod, float *kkl2, float *b, int h, int n, int batch) {
+    if (n != 64) return RSV_FAIL("fuse_ka: head_size must be 64");
+    hipLaunchKernelGGL(k_fuse_ka, dim3(h, batch), dim3(64), 0, ctx->stream, k, kk, a, ka, kmod, kkl2, b, h);
+    RSV_HIP(hipGetLastError());
+    return 0;
+}
+
+// y += sum_j(r*k_mod*r_k) * v per head (backend.rs:780).
+__global__ __launch_bounds__(64) void k_sum_rk_rk(const float *__restrict__ r, const float *__restrict__ km,
+                                                  const float *__restrict__ rk, const float *__restrict__ v,
+                                                  float *y, int H) {
+    const int h = blockIdx.x, b = blockIdx.y, i = threadIdx.x;
+    const size_t o = (size_t)b * H * 64 + h * 64 + i;
+    float s = r[o] * km[o] * rk[h * 64 + i];
+#pragma unroll
+    for (int q = 32; q > 0; q >>= 1) s += __shfl_xor(s, q, 64);
+    y[o] += s * v[o];
+}
+
+int launch_sum_rk_rk(rsv_ctx *ctx, const float *r, const float *kmod, const float *rk, const float *v,
+                     float *y, int h, int n, int batch) {
+    if (n != 64) return RSV_FAIL("sum_rk_rk: head_size must be 64");
+    hipLaunchKernelGGL(k_sum_rk_rk, dim3(h, batch), dim3(64), 0, ctx->stream, r, kmod, rk, v, y, h);
+    RSV_HIP(hipGetLastError());
+    return 0;
+}
+
+// seq_shift (backend.rs:793, 824): y[t] = x[t] + tm*(x[t-1] - x[t]); the
+// previous row of t=0 is the slot's state.  Buffers [batch, t, stride].
+__global__ void k_seq_shift(const float *__restrict__ x, const float *__restrict__ st, const float *__restrict__ tm,
+                            float *__restrict__ y, int c, int t, int sx, int sy) {
+    const int row = blockIdx.y, b = blockIdx.z;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < c; i += gridDim.x * blockDim.x) {
+        const float cur = x[((size_t)b * t + row) * sx + i];
+        const float prev = row == 0 ? st[(size_t)b * c + i] : x[((size_t)b * t + row - 1) * sx + i];
+        y[((size_t)b * t + row) * sy + i] = cur + tm[i] * (prev - cur);
+    }
+}
+
+int launch_seq_shift(rsv_ctx *ctx, const float *x, const float *state, const float *tm, float *y, int c,
+                     int t, int sx, int sy, int batch) {
+    if (t <= 0 || batch <= 0) return 0;
+    hipLaunchKernelGGL(k_seq_shift, dim3((c + 255) / 256, t, batch), dim3(256), 0, ctx->stream, x, state, tm, y,
+                       c, t, sx, sy);
+    RSV_HIP(hipGetLastError());
+    return 0;
+}
+
+// state[b] = x[b, lens[b]-1] (backend.rs:839)
+__global__ void k_copy_token_batch(const float *__restrict__ x, float *__restrict__ st,
+                                   const uint32_t *__restrict__ lens, int c, int t) {
+    const int b = blockIdx.y;
+    uint32_t l = lens[b];
+    if (l == 0) return;
+    if (l > (uint32_t)t) l = t;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < c; i += gridDim.x * blockDim.x)
+        st[(size_t)b * c + i] = x[((size_t)b * t + l - 1) * c + i];
+}
+
+int launch_copy_token_batch(rsv_ctx *ctx, const float *x, float *state, const uint32_t *lens, int c, int t,
+                            int batch) {
+    if (batch <= 0) return 0;
+    hipLaunchKernelGGL(k_copy_token_batch, dim3((c + 255) / 256, batch), dim3(256), 0, ctx->stream, x, state,
+                       lens, c, t);
+    RSV_HIP(hipGetLastError());
+    return 0;
+}
+
+// mean over the first lens[b] rows of x[b] (backend.rs:873)
+__global__ void k_segmean(const float *__restrict__ x, float *__restrict__ out, const uint32_t *__restrict__ lens,
+                          int c, int t) {
+    const int b = blockIdx.y;
+    uint32_t l = lens[b];
+    if (l > (uint32_t)t) l = t;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < c; i += gridDim.x * blockDim.x) {
+        float s = 0.0f;
+        for (uint32_t r = 0; r < l; r++) s += x[((size_t)b * t + r) * c + i];
+        out[(size_t)b * c + i] = l ? s / (float)l : 0.0f;
+    }
+}
+
+int launch_segmean(rsv_ctx *ctx, const float *x, float *out, const uint32_t *lens, int c, int t_pad,
+                   int batch) {
+    if (batch <= 0) return 0;
+    hipLaunchKernelGGL(k_segmean, dim3((c + 255) / 256, batch), dim3(256), 0, ctx->stream, x, out, lens, c, t_pad);
+    RSV_HIP(hipGetLastError());
+    return 0;
+}
+
+}  // namespace rsv
+
+namespace rsv {
+
+// ------------------------------------------------ packed prefill token mix
+// One block per token row.  LN of the row and of its predecessor (or the
+// slot's token-shift state for the first row of a segment); outputs fp16
+// GEMM operands.  The state itself is written by k_seq_state_store in a
+// separate launch so no block reads a state row another block rewrites.
+__device__ __forceinline__ void row_ln(const float *xr, const float *gamma, const float *beta, int C, float eps,
+                                       float *red, float (&out)[kMaxPer]) {
+    float xv[kMaxPer];
+    float s = 0.0f;
+#pragma unroll
+    for (int m = 0; m < kMaxPer; m++) {
+        const int i = threadIdx.x + 256 * m;
+        xv[m] = i < C ? xr[i] : 0.0f;
+        s += xv[m];
+    }
+    const float mean = block_sum256(s, red) / (float)C;
+    float q = 0.0f;
+#pragma unroll
+    for (int m = 0; m < kMaxPer; m++) {
+        const int i = threadIdx.x + 256 * m;
+        const float d = xv[m] - mean;
+        q += i < C ? d * d : 0.0f;
+    }
+    const float var = block_sum256(q, red) / (float)C + eps;
+    const float inv_std = 1.0f / sqrtf(var);
+#pragma unroll
+    for (int m = 0; m < kMaxPer; m++) {
+        const int i = threadIdx.x + 256 * m;
+        out[m] = i < C ? (xv[m] - mean) * inv_std * gamma[i] + beta[i] : 0.0f;
+    }
+}
+
+struct HOut6 { _Float16 *p[6]; };
+
+__global__ __launch_bounds__(256) void k_seq_norm_mix(const float *__restrict__ x, const float *__restrict__ state,
+                                                      const float *__restrict__ gamma, const float *__restrict__ beta,
+                                                      Ptr6 coef, HOut6 out, int nout,
+                                                      const uint32_t *__restrict__ row_prev, int C, uint64_t slots,
+                                                      float eps) {
+    __shared__ float red[4];
+    const int t = blockIdx.x;
+    float ln[kMaxPer], pv[kMaxPer];
+    row_ln(x + (size_t)t * C, gamma, beta, C, eps, red, ln);
+    const uint32_t p = row_prev[t];
+    if (p & 0x80000000u) {
+        const uint32_t slot = p & 0x7FFFFFFFu;
+#pragma unroll
+        for (int m = 0; m < kMaxPer; m++) {
+            const int i = threadIdx.x + 256 * m;
+            pv[m] = (i < C && slot < slots) ? state[(size_t)slot * C + i] : 0.0f;
+        }
+    } else {
+        row_ln(x + (size_t)p * C, gamma, beta, C, eps, red, pv);
+    }
+#pragma unroll
+    for (int m = 0; m < kMaxPer; m++) {
+        const int i = threadIdx.x + 256 * m;
+        if (i >= C) break;
+        const float d = pv[m] - ln[m];
+        for (int j = 0; j < nout; j++) out.p[j][(size_t)t * C + i] = (_Float16)(ln[m] + coef.p[j][i] * d);
+    }
+}
+
+int launch_seq_norm_mix(rsv_ctx *ctx, const float *x, const float *state, const float *gamma, const float *beta,
+                        const float *const *coef, _Float16 *const *out, int nout, const uint32_t *row_prev, int t,
+                        int c, uint64_t slots, float eps) {
+    if (c <= 0 || c > 256 * kMaxPer) return RSV_FAIL("seq_norm_mix: c=%d outside 1..%d", c, 256 * kMaxPer);
+    if (nout < 1 || nout > 6) return RSV_FAIL("seq_norm_mix: nout=%d", nout);
+    if (t <= 0) return 0;
+    Ptr6 cp{};
+    HOut6 op{};
+    for (int j = 0; j < nout; j++) { cp.p[j] = coef[j]; op.p[j] = out[j]; }
+    hipLaunchKernelGGL(k_seq_norm_mix, dim3(t), dim3(256), 0, ctx->stream, x, state, gamma, beta, cp, op, nout,
+                       row_prev, c, slots, eps);
+    RSV_HIP(hipGetLastError());
+    return 0;
+}
+
+__global__ __launch_bounds__(256) void k_seq_state_store(const float *__restrict__ x, float *__restrict__ state,
+                                                         const float *__restrict__ gamma,
+                                                         const float *__restrict__ beta,
+                                                         const uint32_t *__restrict__ seg_last,
+                                                         const uint32_t *__restrict__ seg_slot, int C, uint64_t rows,
+                                                         uint64_t slots, float eps) {
+    __shared__ float red[4];
+    const int g = blockIdx.x;
+    const uint32_t row = seg_last[g], slot = seg_slot[g];
+    if (row >= rows || slot >= slots) return;  // uniform per block
+    float ln[kMaxPer];
+    row_ln(x + (size_t)row * C, gamma, beta, C, eps, red, ln);
+#pragma unroll
+    for (int m = 0; m < kMaxPer; m++) {
+        const int i = threadIdx.x + 256 * m;
+        if (i < C) state[(size_t)slot * C + i] = ln[m];
+    }
+}
+
+int launch_seq_state_store(rsv_ctx *ctx, const float *x, float *state, const float *gamma, const float *beta,
+                           const uint32_t *seg_last, const uint32_t *seg_slot, int nseg, int c, uint64_t rows,
+                           uint64_t slots, float eps) {
+    if (c <= 0 || c > 256 * kMaxPer) return RSV_FAIL("seq_state_store: c=%d", c);
+    if (nseg <= 0) return 0;
+    hipLaunchKernelGGL(k_seq_state_store, dim3(nseg), dim3(256), 0, ctx->stream, x, state, gamma, beta, seg_last,
+                       seg_slot, c, rows, slots, eps);
+    RSV_HIP(hipGetLastError());
+    return 0;
+}
+
+__global__ void k_copy_rows(const float *__restrict__ src, float *__restrict__ dst, const uint32_t *__restrict__ sr,
+                            const uint32_t *__restrict__ dr, int c, uint64_t src_n, uint64_t dst_n) {
+    const int r = blockIdx.y;
+    const uint32_t s = sr[r], d = dr[r];
+    if (s >= src_n || d >= dst_n) return;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < c; i += gridDim.x * blockDim.x)
+        dst[(size_t)d * c + i] = src[(size_t)s * c + i];
+}
+
+int launch_copy_rows(rsv_ctx *ctx, const float *src, float *dst, const uint32_t *src_rows, const uint32_t *dst_rows,
+                     int n, int c, uint64_t src_n, uint64_t dst_n) {
+    if (n <= 0) return 0;
+    hipLaunchKernelGGL(k_copy_rows, dim3((c + 255) / 256, n), dim3(256), 0, ctx->stream, src, dst, src_rows,
+                       dst_rows, c, src_n, dst_n);
+    RSV_HIP(hipGetLastError());
+    return 0;
+}
+
+__global__ void k_mul_to_f16(const float *__restrict__ a, const float *__restrict__ b, _Float16 *__restrict__ y,
+                             uint64_t n) {
+    for (uint64_t e = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n; e += (uint64_t)gridDim.x * blockDim.x)
+        y[e] = (_Float16)(a[e] * b[e]);
+}
+
+int launch_mul_to_f16(rsv_ctx *ctx, const float *a, const float *b, _Float16 *y, uint64_t n) {
+    if (n == 0) return 0;
+    uint64_t blocks = (n + 255) / 256;
+    if (blocks > 16384) blocks = 16384;
+    hipLaunchKernelGGL(k_mul_to_f16, dim3((unsigned)blocks), dim3(256), 0, ctx->stream, a, b, y, n);
+    RSV_HIP(hipGetLastError());
+    return 0;
+}
+
+}  // namespace rsv

@@ -1,0 +1,179 @@
+// Internal header of librsv_hip.so: context, tensor table, error plumbing and
+// the launcher prototypes each kernel file provides.  Not part of the C-ABI.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <cstdarg>
+#include <cstdio>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "../../include/rsv_hip.h"
+
+namespace rsv {
+
+// ---------------------------------------------------------------- errors
+void set_error(const char *fmt, ...);
+#define RSV_FAIL(...) (::rsv::set_error(__VA_ARGS__), -1)
+#define RSV_HIP(call)                                                                       \
+    do {                                                                                    \
+        hipError_t e_ = (call);                                                             \
+        if (e_ != hipSuccess) return RSV_FAIL("%s failed: %s", #call, hipGetErrorString(e_)); \
+    } while (0)
+
+// ---------------------------------------------------------------- tensors
+struct Tensor {
+    void *ptr = nullptr;
+    uint64_t len = 0;  // elements
+    int dtype = RSV_F32;
+    bool live = false;
+    bool foreign = false;  // imported from another context: never freed here
+};
+
+inline size_t dtype_size(int dt) { return dt == RSV_F16 ? 2 : 4; }
+
+// Kernel-side view of a GEMV job (one weight matrix times a batch of inputs
+// with a fused prologue on x and a fused epilogue on y).
+enum GemvFmt { FMT_I8 = 0, FMT_F16 = 1 };
+enum GemvPro { PRO_NONE = 0, PRO_MUL = 1, PRO_SIGMOID = 2 };
+enum GemvEpi {
+    EPI_STORE = 0,    // y = acc
+    EPI_RELU2 = 1,    // y = relu(acc)^2
+    EPI_ADD = 2,      // y += acc
+    EPI_TANH = 3,     // y = tanh(acc)
+    EPI_WDECAY = 4,   // y = exp(scale * sigmoid(acc + p0))
+    EPI_SIGBIAS = 5,  // y = sigmoid(acc + p0)
+    EPI_VLERP = 6,    // y = y + sigmoid(acc + p0) * (p1 - y)
+};
+
+struct GemvJob {
+    const void *w;
+    const uint32_t *sz;
+    const float *x;
+    const float *xmul;
+    float *y;
+    const float *p0;
+    const float *p1;
+    const float *scale;  // device scalar (EPI_WDECAY)
+    int M, K;
+    int fmt, epi, pro;
+    int ldx, ldy;  // batch strides in elements
+    int nblk;      // blocks along M (filled by the launcher)
+};
+constexpr int kMaxJobs = 8;
+struct GemvJobs {
+    GemvJob j[kMaxJobs];
+    int n;
+    int blk_start[kMaxJobs + 1];
+};
+
+}  // namespace rsv
+
+struct rsv_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::vector<rsv::Tensor> tensors;  // TensorId = index
+    std::vector<uint32_t> free_ids;
+    bool capturing = false;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t graph_exec = nullptr;
+    // prefill graphs keyed by token count (backend.rs:95-109)
+    std::map<uint64_t, hipGraphExec_t> prefill_graphs;
+    uint64_t prefill_t = 0;
+    bool prefill_capturing = false;
+    // device scratch for `sample(...)` (history upload + work rows)
+    uint32_t *hist_dev = nullptr;
+    uint64_t hist_cap = 0;
+    float *sample_work = nullptr;
+    uint64_t sample_work_cap = 0;
+    int sm_count = 0;
+};
+
+namespace rsv {
+rsv::Tensor *get_tensor(rsv_ctx *ctx, uint32_t id);
+
+// ------------------------------------------------------------ launchers
+// Every launcher validates shapes on the host before enqueuing and returns 0
+// or a failure status (text through set_error).
+int launch_gemv_jobs(rsv_ctx *ctx, GemvJobs &jobs, int batch);
+int launch_dequant_int8(rsv_ctx *ctx, const uint32_t *idx, const uint32_t *sz, uint64_t m, uint64_t k,
+                        void *out, int out_f16);
+
+int launch_norm_lerp(rsv_ctx *ctx, const float *x, float *state, const float *gamma, const float *beta,
+                     const float *const *coef, float *const *out, int nout, int c, float eps, int batch);
+int launch_norm(rsv_ctx *ctx, const float *x, const float *gamma, const float *beta, float *y, int c,
+                int h, float eps, int rows);
+int launch_wkv7_decode(rsv_ctx *ctx, float *s, const float *k, const float *kk, const float *a,
+                       const float *ka, const float *r, const float *v, const float *w,
+                       const float *gamma, const float *beta, const float *rk, float *kmod, float *y,
+                       float *yn, int h, int n, float eps, float gn_eps, int batch);
+int launch_gather_rows(rsv_ctx *ctx, const void *src, int src_f16, uint64_t src_rows, float *dst,
+                       const uint32_t *tok, int c, int batch);
+int launch_argmax(rsv_ctx *ctx, const float *logits, uint32_t *tok, int n, int batch);
+int launch_record_tokens(rsv_ctx *ctx, const uint32_t *in_tok, uint32_t *out_seq, uint32_t *cnt,
+                         int stride, int batch);
+int launch_set_u32(rsv_ctx *ctx, uint32_t *dst, const uint32_t *vals, int n);
+int launch_store_sampler(rsv_ctx *ctx, float *dst, float temperature, uint32_t top_k, float top_p,
+                         const uint32_t *seeds, int batch, float rep, float freq, float pres,
+                         uint32_t hist_len);
+int launch_sample(rsv_ctx *ctx, const float *logits, uint32_t *token, int n, float *temp,
+                  uint32_t *counter, const float *sampler, const uint32_t *hist, int hist_stride,
+                  int batch);
+int launch_copy(rsv_ctx *ctx, void *dst, const void *src, size_t bytes);
+int launch_elementwise(rsv_ctx *ctx, int op, const float *a, const float *b, float *y, int c, int batch);
+int launch_to_f16(rsv_ctx *ctx, const float *x, _Float16 *y, int c, int t, int m_pad, int x_stride,
+                  int y_stride);
+int launch_v_first_lerp(rsv_ctx *ctx, float *v, const float *gate, const float *vf, int c, int t,
+                        int stride);
+int launch_fuse_ka(rsv_ctx *ctx, const float *k, const float *kk, const float *a, const float *ka,
+                   float *kmod, float *kkl2, float *b, int h, int n, int batch);
+int launch_sum_rk_rk(rsv_ctx *ctx, const float *r, const float *kmod, const float *rk, const float *v,
+                     float *y, int h, int n, int batch);
+int launch_seq_shift(rsv_ctx *ctx, const float *x, const float *state, const float *tm, float *y,
+                     int c, int t, int sx, int sy, int batch);
+int launch_copy_token_batch(rsv_ctx *ctx, const float *x, float *state, const uint32_t *lens, int c,
+                            int t, int batch);
+int launch_dplr_seq(rsv_ctx *ctx, float *s, const float *r, const float *w, const float *k,
+                    const float *v, const float *a, const float *b, float *y, const uint32_t *lens,
+                    int h, int n, int t, int c, int batch);
+int launch_segmean(rsv_ctx *ctx, const float *x, float *out, const uint32_t *lens, int c, int t_pad,
+                   int batch);
+int launch_wkv7_seq_ragged(rsv_ctx *ctx, float *s, const float *r, const float *w, const float *k,
+                           const float *v, const float *a, const float *kk, const float *ka,
+                           const float *rk, const float *gamma, const float *beta, float *yn,
+                           const uint32_t *seg_start, const uint32_t *seg_len,
+                           const uint32_t *seg_slot, int nseg, int h, int n, float gn_eps, uint64_t rows,
+                           uint64_t slots);
+// Prefill GEMM: C[m,n] = epi(A[m,k] B[n,k]^T), A fp16, B fp16 or int8
+// (dequantised in the tile loader), C fp32 or fp16.
+enum GemmEpi {
+    GE_STORE = 0, GE_BIAS = 1, GE_ADD = 2, GE_RELU2 = 3, GE_TANH = 4,
+    GE_WDECAY = 5,   // exp(scale*sigmoid(acc + bias[n]))
+    GE_SIGBIAS = 6,  // sigmoid(acc + bias[n])
+    GE_VLERP = 7,    // c + sigmoid(acc + bias[n]) * (aux - c)   (c read in place)
+    GE_SIGMOID = 8,  // sigmoid(acc)
+};
+struct GemmArgs {
+    const _Float16 *a;
+    const void *b;         // fp16 [n,k] or int8 idx
+    const uint32_t *sz;    // int8 scale/zero (null for fp16)
+    void *c;               // fp32 or fp16 [m,n]
+    const float *bias;     // [n]
+    const float *aux;      // [m,n] fp32
+    const float *scale;    // device scalar
+    int m, n, k;
+    int lda, ldc;
+    int epi, b_i8, c_f16;
+};
+int launch_gemm(rsv_ctx *ctx, const GemmArgs &g);
+int launch_seq_norm_mix(rsv_ctx *ctx, const float *x, const float *state, const float *gamma, const float *beta,
+                        const float *const *coef, _Float16 *const *out, int nout, const uint32_t *row_prev, int t,
+                        int c, uint64_t slots, float eps);
+int launch_seq_state_store(rsv_ctx *ctx, const float *x, float *state, const float *gamma, const float *beta,
+                           const uint32_t *seg_last, const uint32_t *seg_slot, int nseg, int c, uint64_t rows,
+                           uint64_t slots, float eps);
+int launch_copy_rows(rsv_ctx *ctx, const float *src, float *dst, const uint32_t *src_rows, const uint32_t *dst_rows,
+                     int n, int c, uint64_t src_n, uint64_t dst_n);
+int launch_mul_to_f16(rsv_ctx *ctx, const float *a, const float *b, _Float16 *y, uint64_t n);
+}  // namespace rsv

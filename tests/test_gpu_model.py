@@ -1,0 +1,243 @@
+"""Whole-model parity of the HIP path (librsv_host.so over librsv_hip.so)
+against the CPU fp32 oracle, plus the Bundle/State API contract.
+
+Accuracy bar: logits RMSE <= 1e-2 x logit std; teacher-forced top-1
+agreement >= 99% (fp16 / fp32 files) or >= 98% (int8); argmax indices and
+state serialisation bit-exact where the arithmetic is (round trips)."""
+import numpy as np
+import pytest
+
+import oracle as orc
+from conftest import SMALL, rel_rmse
+
+pytestmark = pytest.mark.gpu
+
+RMSE_BOUND = 1e-2
+
+
+def _rsv():
+    import rsv
+    return rsv
+
+
+@pytest.fixture(scope="module")
+def bundles(small_f32, small_f16, small_i8, small_i8_group):
+    rsv = _rsv()
+    out = {}
+    for name, path in (("f32", small_f32), ("f16", small_f16), ("i8", small_i8), ("i8g", small_i8_group)):
+        out[name] = (rsv.ModelBuilder(path).build(), orc.Model(path))
+    yield out
+    for b, _ in out.values():
+        b.close()
+
+
+def _prompt(n, seed):
+    import synth
+    return synth.prompt(SMALL, n, seed=seed)
+
+
+@pytest.mark.parametrize("kind", ["f32", "f16", "i8", "i8g"])
+def test_infer_tokens_matches_oracle(bundles, kind):
+    b, m = bundles[kind]
+    b.reset()
+    st = m.init_state()
+    for t in _prompt(24, 1):
+        got = b.infer_tokens([t])
+        want = m.forward([t], st)
+        assert rel_rmse(got, want) <= RMSE_BOUND
+    # state after the same tokens
+    assert rel_rmse(b.state_back(), st) <= RMSE_BOUND
+
+
+@pytest.mark.parametrize("kind", ["f32", "i8"])
+def test_infer_seq_matches_oracle_and_decode(bundles, kind):
+    b, m = bundles[kind]
+    p = _prompt(77, 2)
+    b.reset()
+    lg_seq = b.infer_seq(p)
+    st_seq = b.state_back()
+    st = m.init_state()
+    want = m.forward(p, st)
+    assert rel_rmse(lg_seq, want) <= RMSE_BOUND
+    assert rel_rmse(st_seq, st) <= RMSE_BOUND
+    b.reset()
+    lg_tok = b.infer_tokens(p)
+    assert rel_rmse(lg_tok, lg_seq) <= RMSE_BOUND
+    # chunked prefill carries state across chunks
+    b.reset()
+    lg_ch = b.infer_chunked(p, 10)
+    assert rel_rmse(lg_ch, lg_seq) <= 1e-4
+
+
+@pytest.mark.parametrize("kind,bar", [("f32", 0.99), ("f16", 0.99), ("i8", 0.98)])
+def test_argmax_selfloop_teacher_forced(bundles, kind, bar):
+    b, m = bundles[kind]
+    p = _prompt(16, 3)
+    b.reset()
+    b.infer_seq(p[:-1])
+    n = 48
+    toks = b.infer_argmax_selfloop(int(p[-1]), n)
+    st = m.init_state()
+    m.forward(p[:-1], st)
+    agree = 0
+    prev = int(p[-1])
+    for i in range(n):
+        lg = m.forward([prev], st)
+        agree += orc.argmax(lg) == toks[i]
+        prev = int(toks[i])  # teacher forcing along the GPU's path
+    assert agree / n >= bar, f"top-1 agreement {agree}/{n}"
+
+
+def test_argmax_selfloop_equals_per_token_argmax(bundles):
+    """ARGMAX_VERIFY / SELFLOOP_VERIFY (main.rs:1056-1088): the graph-replayed
+    self-loop equals per-token infer_argmax on the same device path."""
+    b, _ = bundles["i8"]
+    b.reset()
+    loop = b.infer_argmax_selfloop(17, 20)
+    b.reset()
+    tok = 17
+    for i in range(20):
+        tok = b.infer_argmax([tok])
+        assert tok == loop[i], i
+
+
+def test_state_roundtrip_bit_exact(bundles):
+    """examples/state_persist.rs:38-69: back -> load -> back is lossless and
+    generation continues identically."""
+    b, _ = bundles["f16"]
+    b.reset()
+    b.infer_seq(_prompt(30, 4))
+    s1 = b.state_back()
+    cont1 = b.infer_tokens([5, 6, 7])
+    b.reset()
+    assert np.all(b.state_back() == 0)
+    b.state_load(s1)
+    s2 = b.state_back()
+    assert np.array_equal(s1.view(np.uint32), s2.view(np.uint32))
+    cont2 = b.infer_tokens([5, 6, 7])
+    assert np.array_equal(cont1.view(np.uint32), cont2.view(np.uint32))
+    rsv = _rsv()
+    with pytest.raises(rsv.RsvError, match="length mismatch"):
+        b.state_load(s1[:-1])
+
+
+def test_batch_prefill_and_decode_match_single(bundles):
+    """forward_seq_batch over ragged prompts == per-session infer_seq; batch
+    argmax self-loop == per-session self-loops; slot back/load."""
+    b, _ = bundles["i8"]
+    lens = [5, 17, 1, 33]
+    prompts = [_prompt(l, 10 + i) for i, l in enumerate(lens)]
+    S = b.create_batch_state(len(lens))
+    seeds, lg = b.forward_seq_batch(S, prompts, want_logits=True)
+    assert list(seeds) == [int(p[-1]) for p in prompts]
+    singles = []
+    for i, p in enumerate(prompts):
+        b.reset()
+        lg1 = b.infer_seq(p)
+        singles.append(b.state_back())
+        assert rel_rmse(lg[i], lg1) <= 1e-5
+        assert rel_rmse(S.slot_back(i), singles[-1]) <= 1e-5
+    n = 12
+    out = b.argmax_selfloop_batch(S, seeds, n)
+    for i, p in enumerate(prompts):
+        b.reset()
+        b.state_load(singles[i])
+        one = b.infer_argmax_selfloop(int(seeds[i]), n)
+        assert np.array_equal(out[i], one), i
+    # slot round trip and bounds
+    data = S.slot_back(2)
+    S.slot_load(0, data)
+    assert np.array_equal(S.slot_back(0).view(np.uint32), data.view(np.uint32))
+    rsv = _rsv()
+    with pytest.raises(rsv.RsvError, match="slot"):
+        S.slot_back(9)
+    S.free()
+
+
+def test_forward_tokens_batch_matches_single(bundles):
+    b, m = bundles["f32"]
+    S = b.create_batch_state(3)
+    toks = np.array([[1, 2, 3], [500, 7, 1023], [9, 9, 9]], np.uint32)
+    for t in range(3):
+        lg = b.forward_tokens_batch(S, toks[:, t])
+    for i in range(3):
+        st = m.init_state()
+        want = m.forward(toks[i], st)
+        assert rel_rmse(lg[i], want) <= RMSE_BOUND
+        assert rel_rmse(S.slot_back(i), st) <= RMSE_BOUND
+    S.free()
+
+
+def test_sample_selfloop_teacher_forced(bundles):
+    """Sampling self-loop: per round seed = seed_token + round, history = the
+    tokens generated so far (gpu_model.rs:799-812); each draw agrees with the
+    oracle sampler on the oracle's logits along the GPU path."""
+    rsv = _rsv()
+    b, m = bundles["f32"]
+    sp = rsv.SamplerParams(temperature=1.0, top_k=0, top_p=0.9, repetition_penalty=1.1, frequency_penalty=0.1)
+    p = _prompt(8, 5)
+    b.reset()
+    b.infer_seq(p[:-1])
+    n = 24
+    seed = int(p[-1])
+    toks = b.infer_sample_selfloop(seed, n, sp)
+    st = m.init_state()
+    m.forward(p[:-1], st)
+    prev = seed
+    agree = 0
+    for r in range(n):
+        lg = m.forward([prev], st)
+        want = orc.sample(lg, sp.temperature, sp.top_k, sp.top_p, seed + r, sp.repetition_penalty,
+                          sp.frequency_penalty, sp.presence_penalty, toks[:r].tolist())
+        agree += want == toks[r]
+        prev = int(toks[r])
+    assert agree >= n - 1, f"{agree}/{n}"
+
+
+def test_sample_selfloop_batch_low_temperature_is_argmax(bundles):
+    rsv = _rsv()
+    b, _ = bundles["i8"]
+    S = b.create_batch_state(2)
+    seeds = b.forward_seq_batch(S, [_prompt(4, 20), _prompt(9, 21)])
+    snap = S.back()
+    got = b.sample_selfloop_batch(S, seeds, 10, rsv.SamplerParams(temperature=1e-4, top_k=50))
+    S.load(snap)
+    ref = b.argmax_selfloop_batch(S, seeds, 10)
+    assert np.array_equal(got, ref)
+    S.free()
+
+
+def test_api_errors(bundles):
+    rsv = _rsv()
+    b, _ = bundles["f32"]
+    with pytest.raises(rsv.RsvError, match="vocab"):
+        b.infer_tokens([SMALL["vocab"] + 5])
+    with pytest.raises(rsv.RsvError, match="empty"):
+        b.infer_seq([])
+    with pytest.raises(rsv.RsvError):
+        rsv.ModelBuilder("/nonexistent/model.st").build()
+
+
+def test_config1_golden(tiny_cfg1):
+    """Config 1: tiny model seed 0, 64-token prompt + 32 greedy tokens; the GPU
+    tokens must equal the committed golden tokens (teacher-forced >= 99%) and
+    the final logits meet the RMSE bound."""
+    import json
+    import os
+    rsv = _rsv()
+    gdir = os.path.join(os.path.dirname(__file__), "golden")
+    meta = json.load(open(os.path.join(gdir, "config1.json")))
+    prompt = np.array(meta["prompt"], np.uint32)
+    gold = np.array(meta["greedy"], np.uint32)
+    b = rsv.ModelBuilder(tiny_cfg1).build()
+    b.infer_seq(prompt[:-1])
+    toks = b.infer_argmax_selfloop(int(prompt[-1]), 32)
+    agree = int((toks == gold).sum())
+    first_div = int(np.argmax(toks != gold)) if agree < 32 else 32
+    assert first_div >= 31 or agree >= 31, f"golden mismatch at {first_div}: {toks} vs {gold}"
+    # last-prompt-token logits against the committed fixture
+    b.reset()
+    lg = b.infer_seq(prompt)
+    ref = np.load(os.path.join(gdir, "config1_prompt_logits.npy")).astype(np.float32)
+    assert rel_rmse(lg, ref) <= RMSE_BOUND
+    b.close()

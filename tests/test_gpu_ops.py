@@ -1,0 +1,489 @@
+"""Op-level parity of librsv_hip.so against the CPU oracle / float64
+statements, called through the C-ABI (rsv.Backend)."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+NONE = 0xFFFFFFFF
+
+
+@pytest.fixture(scope="module")
+def be():
+    import rsv
+    b = rsv.Backend(0)
+    yield b
+    b.close()
+
+
+def _rsv():
+    import rsv
+    return rsv
+
+
+def rel_err(got, want):
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    return float(np.max(np.abs(got - want)) / max(np.max(np.abs(want)), 1e-30))
+
+
+# ------------------------------------------------------------- dequant
+def test_dequant_bit_exact(be):
+    rsv = _rsv()
+    rng = np.random.default_rng(0)
+    m, k = 64, 1024
+    idx = rng.integers(0, 256, (m, k), dtype=np.uint8)
+    # arbitrary bit patterns (incl. subnormal / inf / nan halves) like backend_cuda.rs:10141-10148
+    sz = rng.integers(0, 2 ** 32, (m, k // 128), dtype=np.uint64).astype(np.uint32)
+    sz[0, 0] = (np.uint32(0x3C00) << 16) | np.uint32(0x3800)  # scale 0.5, zero 1.0
+    h = be.int8(idx, sz)
+    out = be.tensor(n=m * k)
+    be.call("rsv_dequant_int8_f32", ctypes.byref(h), out)
+    got = be.get(out, m * k).reshape(m, k)
+    want = orc.dequant_int8(idx, sz, m, k)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+    o16 = be.tensor(n=m * k, dtype=rsv.F16)
+    be.call("rsv_dequant_int8_to_f16", ctypes.byref(h), o16, m, k)
+    g16 = be.get(o16, m * k).reshape(m, k)
+    w16 = want.astype(np.float16).astype(np.float32)
+    nan16 = np.isnan(w16)
+    assert np.array_equal(g16[~nan16].view(np.uint32), w16[~nan16].view(np.uint32))
+
+
+# ------------------------------------------------------------- GEMV
+def _int8_weight(rng, m, k):
+    import synth
+    w = rng.standard_normal((m, k)).astype(np.float32) * 0.02
+    idx, sz = synth.quantize_rows(w)
+    return idx, sz, orc.dequant_int8(idx, sz, m, k)
+
+
+@pytest.mark.parametrize("m,k", [(2560, 2560), (10240, 2560), (2560, 10240), (65536, 2560)])
+@pytest.mark.parametrize("batch", [1, 8])
+def test_gemv_int8_config2_shapes(be, m, k, batch):
+    rng = np.random.default_rng(m + k + batch)
+    idx, sz, W = _int8_weight(rng, m, k)
+    h = be.int8(idx, sz)
+    x = rng.standard_normal((batch, k)).astype(np.float16).astype(np.float32)
+    xt = be.tensor(x)
+    yt = be.tensor(n=batch * m)
+    be.call("rsv_gemv_int8_plain", ctypes.byref(h), xt, yt, m, k, batch)
+    got = be.get(yt, batch * m).reshape(batch, m)
+    want = x.astype(np.float64) @ W.astype(np.float64).T
+    assert rel_err(got, want) < 2e-5
+
+
+@pytest.mark.parametrize("batch", [1, 2, 3, 5, 17, 64])
+def test_gemv_epilogues_and_batch_tails(be, batch):
+    rsv = _rsv()
+    rng = np.random.default_rng(100 + batch)
+    m, k = 384, 1280
+    idx, sz, W = _int8_weight(rng, m, k)
+    h = be.int8(idx, sz)
+    W16 = (rng.standard_normal((m, k)) * 0.02).astype(np.float16)
+    w16 = be.tensor(W16.astype(np.float32), dtype=rsv.F16)
+    x = rng.standard_normal((batch, k)).astype(np.float32)
+    g = rng.standard_normal((batch, k)).astype(np.float32)
+    y0 = rng.standard_normal((batch, m)).astype(np.float32)
+    xt, gt = be.tensor(x), be.tensor(g)
+    Wd = W.astype(np.float64)
+    Wh = W16.astype(np.float64)
+    cases = [
+        ("rsv_gemv_int8_relu2", (ctypes.byref(h), xt), lambda: np.maximum(x @ Wd.T, 0) ** 2, None),
+        ("rsv_gemv_int8_add", (ctypes.byref(h), xt), lambda: y0 + x @ Wd.T, y0),
+        ("rsv_gemv_int8_mul_add", (ctypes.byref(h), xt, gt), lambda: y0 + (x * g) @ Wd.T, y0),
+        ("rsv_gemv_f16", (w16, xt), lambda: x @ Wh.T, None),
+        ("rsv_gemv_f16_relu2", (w16, xt), lambda: np.maximum(x @ Wh.T, 0) ** 2, None),
+        ("rsv_gemv_f16_add", (w16, xt), lambda: y0 + x @ Wh.T, y0),
+        ("rsv_gemv_f16_mul_add", (w16, xt, gt), lambda: y0 + (x * g) @ Wh.T, y0),
+    ]
+    for name, args, ref, init in cases:
+        yt = be.tensor(init if init is not None else np.zeros((batch, m), np.float32))
+        be.call(name, *args, yt, m, k, batch)
+        got = be.get(yt, batch * m).reshape(batch, m)
+        assert rel_err(got, ref()) < 5e-5, name
+
+
+def test_gemv_rejects_bad_shapes(be):
+    rsv = _rsv()
+    rng = np.random.default_rng(1)
+    idx, sz, _ = _int8_weight(rng, 128, 256)
+    h = be.int8(idx, sz)
+    xt, yt = be.tensor(n=256), be.tensor(n=128)
+    with pytest.raises(rsv.RsvError, match="int8 handle"):
+        be.call("rsv_gemv_int8_plain", ctypes.byref(h), xt, yt, 128, 512, 1)
+    with pytest.raises(rsv.RsvError, match="needs"):
+        be.call("rsv_gemv_int8_plain", ctypes.byref(h), xt, yt, 128, 256, 2)
+    with pytest.raises(rsv.RsvError, match="unknown tensor"):
+        be.call("rsv_gemv_int8_plain", ctypes.byref(h), 99999, yt, 128, 256, 1)
+
+
+def _lora(rng, out, inn):
+    return (rng.standard_normal((out, inn)) * 0.02).astype(np.float16)
+
+
+@pytest.mark.parametrize("batch", [1, 4, 7])
+def test_stage1_and_chain4(be, batch):
+    rsv = _rsv()
+    rng = np.random.default_rng(7 + batch)
+    C, vm, wm, am, gm = 512, 32, 64, 64, 128
+    Ws = [_int8_weight(rng, C, C) for _ in range(3)]
+    hs = [be.int8(i, s) for i, s, _ in Ws]
+    L1 = {n: _lora(rng, mid, C) for n, mid in (("v", vm), ("w", wm), ("a", am), ("g", gm))}
+    L2 = {n: _lora(rng, C, mid) for n, mid in (("v", vm), ("w", wm), ("a", am), ("g", gm))}
+    t1 = {n: be.tensor(a.astype(np.float32), dtype=rsv.F16) for n, a in L1.items()}
+    t2 = {n: be.tensor(a.astype(np.float32), dtype=rsv.F16) for n, a in L2.items()}
+    xs = {n: rng.standard_normal((batch, C)).astype(np.float32) for n in "rkvwag"}
+    xt = {n: be.tensor(a) for n, a in xs.items()}
+    out = {n: be.tensor(n=batch * C) for n in "rkv"}
+    mids = {n: be.tensor(n=batch * L1[n].shape[0]) for n in "vwag"}
+    be.call("rsv_gemv_int8_rkv_stage1_batch", ctypes.byref(hs[0]), ctypes.byref(hs[1]), ctypes.byref(hs[2]),
+            t1["v"], t1["w"], t1["a"], t1["g"], xt["r"], xt["k"], xt["v"], xt["w"], xt["a"], xt["g"],
+            out["r"], out["k"], out["v"], mids["v"], mids["w"], mids["a"], mids["g"], C, vm, wm, am, gm, batch)
+    X = {n: a.astype(np.float64) for n, a in xs.items()}
+    for j, n in enumerate("rkv"):
+        assert rel_err(be.get(out[n], batch * C).reshape(batch, C), X[n] @ Ws[j][2].astype(np.float64).T) < 5e-5
+    M = {}
+    for n in "vwag":
+        src = X["v"] if n == "v" else X[n]
+        want = src @ L1[n].astype(np.float64).T
+        if n == "w":
+            want = np.tanh(want)
+        got = be.get(mids[n], batch * L1[n].shape[0]).reshape(batch, -1)
+        assert rel_err(got, want) < 5e-5, n
+        M[n] = got.astype(np.float64)
+    # stage 2
+    w0, a0, v0 = (rng.standard_normal(C).astype(np.float32) * 0.1 for _ in range(3))
+    vfirst = rng.standard_normal((batch, C)).astype(np.float32)
+    v_in = be.get(out["v"], batch * C).reshape(batch, C)
+    sc = np.float32(-1.0 / np.sqrt(np.e))
+    ids = dict(w0=be.tensor(w0), a0=be.tensor(a0), v0=be.tensor(v0), sc=be.tensor(np.array([sc])),
+               vf=be.tensor(vfirst), w=be.tensor(n=batch * C), a=be.tensor(n=batch * C), g=be.tensor(n=batch * C))
+    be.call("rsv_gemv_lowrank_chain4_batch", t2["w"], t2["a"], t2["v"], t2["g"], mids["w"], mids["a"], mids["v"],
+            mids["g"], ids["w0"], ids["a0"], ids["v0"], ids["sc"], ids["vf"], ids["w"], ids["a"], out["v"], ids["g"],
+            C, wm, am, vm, gm, batch)
+    sig = lambda t: 1 / (1 + np.exp(-t))
+    P = lambda n: L2[n].astype(np.float64).T
+    want_w = np.exp(sc * sig(M["w"] @ P("w") + w0))
+    want_a = sig(M["a"] @ P("a") + a0)
+    gate = sig(M["v"] @ P("v") + v0)
+    want_v = v_in + gate * (vfirst - v_in)
+    want_g = sig(M["g"]) @ P("g")
+    for n, want in (("w", want_w), ("a", want_a), ("g", want_g)):
+        assert rel_err(be.get(ids[n], batch * C).reshape(batch, C), want) < 5e-5, n
+    assert rel_err(be.get(out["v"], batch * C).reshape(batch, C), want_v) < 5e-5
+
+
+# ------------------------------------------------------------- norms
+@pytest.mark.parametrize("batch", [1, 3])
+def test_norm_lerp6_cmix_and_norm(be, batch):
+    rng = np.random.default_rng(20 + batch)
+    C = 2560
+    x = rng.standard_normal((batch, C)).astype(np.float32) * 2 + 0.5
+    st = rng.standard_normal((batch, C)).astype(np.float32)
+    gam, bet = rng.standard_normal(C).astype(np.float32), rng.standard_normal(C).astype(np.float32)
+    coefs = [rng.random(C).astype(np.float32) for _ in range(6)]
+    xt, stt, gt, bt = be.tensor(x), be.tensor(st), be.tensor(gam), be.tensor(bet)
+    ct = [be.tensor(c) for c in coefs]
+    ot = [be.tensor(n=batch * C) for _ in range(6)]
+    be.call("rsv_norm_lerp6_batch", xt, stt, gt, bt, *ct, *ot, C, 1e-5, batch)
+    for b in range(batch):
+        ln = orc.layer_norm(x[b], gam, bet)
+        for j in range(6):
+            want = ln + coefs[j] * (st[b] - ln)
+            assert rel_err(be.get(ot[j], batch * C).reshape(batch, C)[b], want) < 1e-5
+        assert rel_err(be.get(stt, batch * C).reshape(batch, C)[b], ln) < 1e-5
+    st2 = be.tensor(st)
+    xb = be.tensor(n=batch * C)
+    be.call("rsv_cmix_norm_lerp_batch", xt, st2, gt, bt, ct[0], xb, C, 1e-5, batch)
+    for b in range(batch):
+        ln = orc.layer_norm(x[b], gam, bet)
+        assert rel_err(be.get(xb, batch * C).reshape(batch, C)[b], ln + coefs[0] * (st[b] - ln)) < 1e-5
+    # GroupNorm through rsv_norm: 40 groups of 64
+    y = be.tensor(n=batch * C)
+    be.call("rsv_norm", xt, gt, bt, y, 64, 40, 64e-5, batch)
+    got = be.get(y, batch * C).reshape(batch, C)
+    for b in range(batch):
+        assert rel_err(got[b], orc.group_norm(x[b], gam, bet, 40, 64)) < 1e-5
+
+
+# ------------------------------------------------------------- WKV7
+def _wkv_inputs(rng, batch, H):
+    """Config 3 inputs: r, v ~ N(0,1) fp16; k ~ N(0,1) L2-normalised per head;
+    w = exp(-0.6065*sigmoid(x)); a = sigmoid(N(0,1)); S0 ~ N(0, 0.1^2)."""
+    C = H * 64
+    f16 = lambda a: a.astype(np.float16).astype(np.float32)
+    r = f16(rng.standard_normal((batch, C)))
+    v = f16(rng.standard_normal((batch, C)))
+    k = rng.standard_normal((batch, H, 64))
+    k = (k / np.linalg.norm(k, axis=2, keepdims=True)).reshape(batch, C).astype(np.float32)
+    w = np.exp(-0.6065 * (1 / (1 + np.exp(-rng.standard_normal((batch, C)))))).astype(np.float32)
+    a = (1 / (1 + np.exp(-rng.standard_normal((batch, C))))).astype(np.float32)
+    S = (rng.standard_normal((batch, H, 64, 64)) * 0.1).astype(np.float32)
+    kk = np.ones(C, np.float32)
+    ka = (rng.random(C) * 0.5).astype(np.float32)
+    rk = (rng.standard_normal(C) * 0.1).astype(np.float32)
+    gam = (1 + rng.standard_normal(C) * 0.1).astype(np.float32)
+    bet = (rng.standard_normal(C) * 0.1).astype(np.float32)
+    return r, v, k, w, a, S, kk, ka, rk, gam, bet
+
+
+def _wkv_oracle(S, k, kk, a, ka, r, v, w, gam, bet, rk, H):
+    """One token of model.rs:445-473 with the oracle's primitives."""
+    kkv = k * kk
+    kmod = k + ka * (k * a - k)
+    kh = orc.l2_norm_groups(kkv, H, 64)
+    bvec = kh * (-a)
+    S2 = orc.dplr_update(S.reshape(-1), kmod, v, w, kh, bvec, H, 64)
+    y = orc.dplr_matvec(S2, r, H, 64)
+    yn = orc.group_norm(y, gam, bet, H, 64) + orc.sum_rk_rk(r, kmod, rk, v, H, 64)
+    return S2, yn, kmod
+
+
+@pytest.mark.parametrize("batch", [1, 32])
+def test_wkv7_decode_config3(be, batch):
+    H = 40
+    C = H * 64
+    rng = np.random.default_rng(300 + batch)
+    r, v, k, w, a, S, kk, ka, rk, gam, bet = _wkv_inputs(rng, batch, H)
+    ids = [be.tensor(t) for t in (S, k, kk, a, ka, r, v, w, gam, bet, rk)]
+    km, yn = be.tensor(n=batch * C), be.tensor(n=batch * C)
+    be.call("rsv_fuse_ka_dplr_norm_batch", *ids, km, NONE, yn, H, 64, 1e-12, 64e-5, batch)
+    gS = be.get(ids[0], S.size).reshape(batch, -1)
+    gy = be.get(yn, batch * C).reshape(batch, C)
+    for b in range(batch):
+        S2, want, kmod = _wkv_oracle(S[b], k[b], kk, a[b], ka, r[b], v[b], w[b], gam, bet, rk, H)
+        assert rel_err(gS[b], S2) < 1e-5
+        assert rel_err(gy[b], want) < 1e-4
+        assert rel_err(be.get(km, batch * C).reshape(batch, C)[b], kmod) < 1e-6
+
+
+def test_dplr_seq_reference_closed_form(be):
+    """backend_cuda.rs:9996-10082 inputs; rel < 1e-4 on y and S."""
+    h, n, t = 2, 64, 6
+    c = h * n
+    i = np.arange(t * c, dtype=np.float32)
+    sd = np.cos(np.arange(h * n * n, dtype=np.float32) * np.float32(0.1))
+    vec = [np.sin(i * np.float32(0.2)), i * np.float32(0.3) + np.float32(0.5), np.cos(i * np.float32(0.4)),
+           np.sin(i * np.float32(0.5)), i * np.float32(0.6) + np.float32(1.0), np.cos(i * np.float32(0.7))]
+    rd, wd, kd, vd, ad, bd = vec
+    ids = [be.tensor(sd)] + [be.tensor(x) for x in vec]
+    y = be.tensor(n=t * c)
+    be.call("rsv_dplr_seq", ids[0], ids[1], ids[2], ids[3], ids[4], ids[5], ids[6], y, h, n, t, c)
+    S = sd.copy()
+    ys = []
+    for tt in range(t):
+        sl = slice(tt * c, (tt + 1) * c)
+        S = orc.dplr_update(S, kd[sl], vd[sl], wd[sl], ad[sl], bd[sl], h, n)
+        ys.append(orc.dplr_matvec(S, rd[sl], h, n))
+    assert rel_err(be.get(y, t * c), np.concatenate(ys)) < 1e-4
+    assert rel_err(be.get(ids[0], sd.size), S) < 1e-4
+
+
+def test_wkv7_seq_ragged_matches_decode_loop(be):
+    rsv = _rsv()
+    H = 40
+    C = H * 64
+    rng = np.random.default_rng(5)
+    lens = [300, 212]  # T = 512 over two segments
+    T = sum(lens)
+    r, v, k, w, a, _, kk, ka, rk, gam, bet = _wkv_inputs(rng, T, H)
+    S = (rng.standard_normal((2, H, 64, 64)) * 0.1).astype(np.float32)
+    ids = [be.tensor(t) for t in (S, r, w, k, v, a, kk, ka, rk, gam, bet)]
+    yn = be.tensor(n=T * C)
+    st = be.tensor(np.array([0, lens[0]]), dtype=rsv.U32)
+    ln = be.tensor(np.array(lens), dtype=rsv.U32)
+    sl = be.tensor(np.array([1, 0]), dtype=rsv.U32)  # segment 0 -> slot 1
+    be.call("rsv_wkv7_seq_ragged", ids[0], ids[1], ids[2], ids[3], ids[4], ids[5], ids[6], ids[7], ids[8], ids[9],
+            ids[10], yn, st, ln, sl, 2, H, 64, 64e-5)
+    got_y = be.get(yn, T * C).reshape(T, C)
+    got_S = be.get(ids[0], S.size).reshape(2, -1)
+    pos = 0
+    for g, slot in enumerate([1, 0]):
+        Sx = S[slot].reshape(-1).copy()
+        for t in range(pos, pos + lens[g]):
+            Sx, want, _ = _wkv_oracle(Sx, k[t], kk, a[t], ka, r[t], v[t], w[t], gam, bet, rk, H)
+            assert rel_err(got_y[t], want) < 2e-4, t
+        assert rel_err(got_S[slot], Sx) < 2e-4
+        pos += lens[g]
+
+
+# ------------------------------------------------------------- argmax / tokens
+def test_argmax_reference_cases(be):
+    rsv = _rsv()
+    x = np.sin(np.arange(65536, dtype=np.float32) * np.float32(0.1)).astype(np.float32)
+    lt, tok = be.tensor(x), be.tensor(n=1, dtype=rsv.U32)
+    be.call("rsv_argmax", lt, tok, 65536)
+    assert be.get(tok, 1, rsv.U32)[0] == orc.argmax(x)
+    y = np.zeros(1024, np.float32)
+    y[0] = y[999] = 5.0
+    lt2 = be.tensor(y)
+    be.call("rsv_argmax", lt2, tok, 1024)
+    assert be.get(tok, 1, rsv.U32)[0] == 0
+    rng = np.random.default_rng(3)
+    z = rng.standard_normal((64, 65536)).astype(np.float32)
+    z[5, [10, 20000]] = 50.0  # tie inside a batch row
+    lt3, tok3 = be.tensor(z), be.tensor(n=64, dtype=rsv.U32)
+    be.call("rsv_argmax_batch", lt3, tok3, 65536, 64)
+    assert np.array_equal(be.get(tok3, 64, rsv.U32), [orc.argmax(row) for row in z])
+
+
+def test_record_and_store_tokens(be):
+    """backend_cuda.rs:9401-9435: [7,3,5,1] accumulate in order; batch slots count independently."""
+    rsv = _rsv()
+    tok, seq, cnt = be.tensor(n=1, dtype=rsv.U32), be.tensor(n=8, dtype=rsv.U32), be.tensor(n=1, dtype=rsv.U32)
+    for t in [7, 3, 5, 1]:
+        be.call("rsv_store_token", tok, t)
+        be.call("rsv_record_token", tok, seq, cnt)
+    assert list(be.get(seq, 4, rsv.U32)) == [7, 3, 5, 1]
+    assert be.get(cnt, 1, rsv.U32)[0] == 4
+    toks = be.tensor(n=3, dtype=rsv.U32)
+    seqb, cntb = be.tensor(n=3 * 4, dtype=rsv.U32), be.tensor(n=3, dtype=rsv.U32)
+    for r in range(5):  # one past the row length: bounded write
+        vals = (np.arange(3, dtype=np.uint32) + 10 * r)
+        be.call("rsv_store_tokens", toks, vals.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)), 3)
+        be.call("rsv_record_tokens", toks, seqb, cntb, 4, 3)
+    got = be.get(seqb, 12, rsv.U32).reshape(3, 4)
+    assert np.array_equal(got, np.array([[b + 10 * r for r in range(4)] for b in range(3)]))
+    assert list(be.get(cntb, 3, rsv.U32)) == [5, 5, 5]
+
+
+def test_gather_rows(be):
+    rsv = _rsv()
+    rng = np.random.default_rng(4)
+    tab = rng.standard_normal((100, 256)).astype(np.float32)
+    for dt in (rsv.F32, rsv.F16):
+        src = be.tensor(tab, dtype=dt)
+        tk = be.tensor(np.array([3, 99, 0, 150]), dtype=rsv.U32)  # 150: out of range -> zero row
+        dst = be.tensor(n=4 * 256)
+        be.call("rsv_gather_rows_device_f16", src, dst, tk, 256, 4)
+        got = be.get(dst, 4 * 256).reshape(4, 256)
+        ref = tab if dt == rsv.F32 else tab.astype(np.float16).astype(np.float32)
+        assert np.array_equal(got[:3], ref[[3, 99, 0]])
+        assert np.all(got[3] == 0)
+
+
+# ------------------------------------------------------------- sampler
+def _sample_gpu(be, logits, temperature, top_k, top_p, seed, rep=1.0, freq=0.0, pres=0.0, hist=()):
+    rsv = _rsv()
+    lt, tok = be.tensor(logits), be.tensor(n=1, dtype=rsv.U32)
+    h = np.ascontiguousarray(np.asarray(hist, np.uint32)) if len(hist) else np.zeros(1, np.uint32)
+    be.call("rsv_sample", lt, tok, logits.size, temperature, top_k, top_p, seed, rep, freq, pres,
+            h.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)), len(hist))
+    return int(be.get(tok, 1, rsv.U32)[0])
+
+
+def test_sample_reference_cases(be):
+    n = 4096
+    lg = np.zeros(n, np.float32)
+    lg[5] = 100.0
+    for seed in [1, 42, 0xDEADBEEF]:
+        assert _sample_gpu(be, lg, 1.0, 0, 1.0, seed) == 5
+    lg2 = np.ones(n, np.float32)
+    lg2[7] = 2.0
+    assert _sample_gpu(be, lg2, 0.5, 1, 1.0, 7) == 7
+    lg3 = np.full(n, -100.0, np.float32)
+    lg3[0] = lg3[1] = 5.0
+    assert _sample_gpu(be, lg3, 1.0, 0, 1.0, 99, freq=1.0, hist=[0] * 6) == 1
+
+
+@pytest.mark.parametrize("params", [
+    dict(temperature=1.0, top_k=0, top_p=1.0),
+    dict(temperature=0.8, top_k=50, top_p=0.9),
+    dict(temperature=1.0, top_k=0, top_p=0.9),
+    dict(temperature=1.3, top_k=20, top_p=1.0),
+    dict(temperature=1.0, top_k=100, top_p=0.5),
+    dict(temperature=0.7, top_k=0, top_p=0.3, rep=1.3, freq=0.2, pres=0.5),
+])
+def test_sample_matches_oracle(be, params):
+    rng = np.random.default_rng(11)
+    mism = 0
+    trials = 60
+    for s in range(trials):
+        lg = (rng.standard_normal(65536) * 2.0).astype(np.float32)
+        hist = rng.integers(0, 65536, 40).tolist() if "rep" in params else []
+        p = dict(params)
+        rep, freq, pres = p.pop("rep", 1.0), p.pop("freq", 0.0), p.pop("pres", 0.0)
+        want = orc.sample(lg, p["temperature"], p["top_k"], p["top_p"], 1000 + s, rep, freq, pres, hist)
+        got = _sample_gpu(be, lg, p["temperature"], p["top_k"], p["top_p"], 1000 + s, rep, freq, pres, hist)
+        mism += want != got
+    # float sums are reduced in a different order on the GPU: a draw can only
+    # flip when u lands within rounding of a CDF boundary
+    assert mism <= 1, f"{mism}/{trials} draws differ"
+
+
+def test_sample_batch_low_temperature_is_argmax(be):
+    """backend_cuda.rs:7919-8011 (xorshift32 logits, T=1e-4, top_k=50)."""
+    rsv = _rsv()
+    seed = 0xFEED1234
+    vals = []
+    for _ in range(4 * 1024):
+        seed ^= (seed << 13) & 0xFFFFFFFF
+        seed ^= seed >> 17
+        seed ^= (seed << 5) & 0xFFFFFFFF
+        vals.append((np.float32(seed) / np.float32(4294967295.0)) * np.float32(2.0) - np.float32(1.0))
+    lg = np.array(vals, np.float32).reshape(4, 1024) * np.float32(10.0)
+    n, batch = 1024, 4
+    lt, tok = be.tensor(lg), be.tensor(n=batch, dtype=rsv.U32)
+    temp, cnt = be.tensor(n=batch * n), be.tensor(n=batch * n, dtype=rsv.U32)
+    samp, hist = be.tensor(n=batch * 8), be.tensor(n=batch, dtype=rsv.U32)
+    seeds = np.array([42 + b for b in range(batch)], np.uint32)
+    be.call("rsv_store_sampler_async_batch", samp, 0, 0.0001, 50, 1.0,
+            seeds.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)), batch, 1.0, 0.0, 0.0, 0)
+    be.call("rsv_sample_into_host_seeded_batch", lt, tok, n, temp, NONE, cnt, samp, hist, batch)
+    assert list(be.get(tok, batch, rsv.U32)) == [int(np.argmax(r)) for r in lg]
+
+
+# ------------------------------------------------------------- GEMM
+@pytest.mark.parametrize("m,n,k", [(1, 96, 2560), (37, 2560, 96), (128, 256, 512), (300, 2560, 2560)])
+def test_gemm_f16_and_int8(be, m, n, k):
+    rsv = _rsv()
+    rng = np.random.default_rng(m * 7 + n + k)
+    A = rng.standard_normal((m, k)).astype(np.float16)
+    At = be.tensor(A.astype(np.float32), dtype=rsv.F16)
+    W16 = (rng.standard_normal((n, k)) * 0.02).astype(np.float16)
+    Wt = be.tensor(W16.astype(np.float32), dtype=rsv.F16)
+    A64 = A.astype(np.float64)
+    C = be.tensor(n=m * n)
+    be.call("rsv_gemm", At, Wt, C, m, n, k)
+    assert rel_err(be.get(C, m * n).reshape(m, n), A64 @ W16.astype(np.float64).T) < 1e-5
+    if k % 128 == 0:
+        idx, sz, W = _int8_weight(rng, n, k)
+        h = be.int8(idx, sz)
+        Wq = W.astype(np.float16).astype(np.float64)  # dequantised then rounded to fp16 in the loader
+        C8 = be.tensor(n=m * n)
+        be.call("rsv_gemm_int8", At, ctypes.byref(h), C8, m, 0)
+        assert rel_err(be.get(C8, m * n).reshape(m, n), A64 @ Wq.T) < 1e-5
+
+
+def test_gemm_epilogues(be):
+    rsv = _rsv()
+    rng = np.random.default_rng(8)
+    m, n, k = 70, 192, 256
+    A = rng.standard_normal((m, k)).astype(np.float16)
+    W = (rng.standard_normal((n, k)) * 0.05).astype(np.float16)
+    At, Wt = be.tensor(A.astype(np.float32), dtype=rsv.F16), be.tensor(W.astype(np.float32), dtype=rsv.F16)
+    acc = A.astype(np.float64) @ W.astype(np.float64).T
+    bias = rng.standard_normal(n).astype(np.float32)
+    aux = rng.standard_normal((m, n)).astype(np.float32)
+    c0 = rng.standard_normal((m, n)).astype(np.float32)
+    sc = np.float32(-0.6065)
+    bt, xt, st = be.tensor(bias), be.tensor(aux), be.tensor(np.array([sc]))
+    sig = lambda t: 1 / (1 + np.exp(-t))
+    cases = [(0, None, lambda: acc), (1, None, lambda: acc + bias), (2, c0, lambda: c0 + acc),
+             (3, None, lambda: np.maximum(acc, 0) ** 2), (4, None, lambda: np.tanh(acc)),
+             (5, None, lambda: np.exp(sc * sig(acc + bias))), (6, None, lambda: sig(acc + bias)),
+             (7, c0, lambda: c0 + sig(acc + bias) * (aux - c0)), (8, None, lambda: sig(acc))]
+    for epi, init, ref in cases:
+        C = be.tensor(init if init is not None else np.zeros((m, n), np.float32))
+        be.call("rsv_gemm_ex", At, Wt, None, C, m, n, k, epi, bt, xt if epi == 7 else NONE, st)
+        assert rel_err(be.get(C, m * n).reshape(m, n), ref()) < 2e-5, epi
+    C16 = be.tensor(n=m * n, dtype=rsv.F16)
+    be.call("rsv_gemm_ex", At, Wt, None, C16, m, n, k, 4, NONE, NONE, NONE)
+    assert rel_err(be.get(C16, m * n).reshape(m, n), np.tanh(acc)) < 2e-3
