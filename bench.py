@@ -67,7 +67,11 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-tokens", type=int, default=4)
     ap.add_argument("--cache", default=os.environ.get("RSV_BENCH_CACHE", "/tmp"))
+    ap.add_argument("--no-graph", action="store_true",
+                    help="enqueue self-loop steps eagerly instead of replaying a HIP graph (profiling)")
     args = ap.parse_args()
+    if args.no_graph:
+        os.environ["RSV_NO_GRAPH"] = "1"
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}).",
               file=sys.stderr)

@@ -289,6 +289,68 @@ int rsv_mul_to_f16(rsv_ctx *ctx, uint32_t a, uint32_t b, uint32_t y, uint64_t n)
 int rsv_gemm_ex(rsv_ctx *ctx, uint32_t a, uint32_t w16, const rsv_int8 *w8, uint32_t c, uint64_t m,
                 uint64_t n, uint64_t k, int epilogue, uint32_t bias, uint32_t aux, uint32_t scale);
 
+/* General fused GEMV launch (decode).  One launch runs up to 8 weight
+ * matrices ("jobs"); each job is y[batch, m] (epilogue)= x'[batch, k] W^T where
+ * x' is x after the prologue:
+ *   prologue 0: x;  1: x * xmul;  2: sigmoid(x);
+ *   3: LN-mix: ln = LN(x)*gamma + beta (eps 1e-5, over k), x' = ln + coef*(prev - ln);
+ *      lnout (optional, [batch, k]) receives ln.
+ *   epilogue 0: store; 1: relu^2; 2: y += acc; 3: tanh; 4: exp(scale*sigmoid(acc+p0));
+ *      5: sigmoid(acc+p0); 6: y + sigmoid(acc+p0)*(p1 - y); 7: store to y and p1.
+ * W is F16 (w16) or int8 (w8).  After the launch, side_dst[b, :side_n] =
+ * side_src[b, :side_n] for every batch row (ids 0xFFFFFFFF: no copy).
+ * These compose the reference's norm_lerp6 + gemv_*_rkv_stage1,
+ * gemv_lowrank_chain4 and cmix_norm_lerp + gemv_*_relu2 pairs
+ * (backend.rs:185-415) into single launches. */
+typedef struct rsv_gemv_job {
+    uint32_t w16;
+    const rsv_int8 *w8;
+    uint64_t m, k;
+    uint32_t x, y;
+    int prologue, epilogue;
+    uint32_t xmul, p0, p1, scale;
+    uint32_t gamma, beta, prev, coef, lnout;
+} rsv_gemv_job;
+int rsv_gemv_multi(rsv_ctx *ctx, const rsv_gemv_job *jobs, uint64_t njobs, uint32_t side_src,
+                   uint32_t side_dst, uint64_t side_n, uint64_t batch);
+
+/* ---- batched decode on matrix cores (sessions B >= 16).  These compose
+ * the same per-layer math as the *_batch trait ops (backend.rs:461-648) with
+ * fp16 activation operands so the weight products run on MFMA.
+ *
+ * rsv_gemm_skinny: each job computes y[b, n] (epilogue)= sum_k x[b, k] W[n, k]
+ * with x an F16 tensor [batch, k]; W F16 (w16) or int8 (w8); y F32 or F16
+ * [batch, n]; y2 (optional F32) receives a copy; epilogue codes as
+ * rsv_gemm_ex (0 store .. 8 sigmoid). */
+typedef struct rsv_mm_job {
+    uint32_t w16;
+    const rsv_int8 *w8;
+    uint64_t n, k;
+    uint32_t x, y, y2;
+    int epilogue;
+    uint32_t bias, aux, scale;
+    int tiled; /* weights (w16, or w8->idx) are the copy made by rsv_tile_weights */
+} rsv_mm_job;
+/* MFMA-tiled copy of a weight matrix for rsv_gemm_skinny: 32x32 tiles
+ * (1 KiB int8 / 2 KiB fp16), lane-ordered, [row tile][k chunk].  src is an
+ * int8 idx tensor (esz 1) or an F16 tensor (esz 2) of n x k; *out receives
+ * a new tensor (rows padded to a multiple of 32).  The int8 scale/zero
+ * tensor is shared with the original. */
+int rsv_tile_weights(rsv_ctx *ctx, uint32_t src, uint64_t n, uint64_t k, int esz, uint32_t *out);
+int rsv_gemm_skinny(rsv_ctx *ctx, const rsv_mm_job *jobs, uint64_t njobs, uint64_t batch);
+/* LN rows of x [batch, c] + nout (1 or 6) token-shift mixes as F16 outputs;
+ * coef ids may be 0xFFFFFFFF (plain LN); state (optional) is the token-shift
+ * row, read then overwritten with the LN row. */
+int rsv_ln_mix_f16(rsv_ctx *ctx, uint32_t x, uint32_t state, uint32_t gamma, uint32_t beta,
+                   const uint32_t *coef, const uint32_t *out_f16, uint64_t nout, uint64_t c, float eps,
+                   uint64_t batch);
+/* fuse_ka_dplr_norm_batch that also (or only) writes f16(y_norm * g) into
+ * yg_f16 (the att.output operand); y_norm may be 0xFFFFFFFF. */
+int rsv_wkv7_decode_ex(rsv_ctx *ctx, uint32_t s, uint32_t k, uint32_t k_k, uint32_t a, uint32_t k_a,
+                       uint32_t r, uint32_t v, uint32_t w, uint32_t ln_x_w, uint32_t ln_x_b, uint32_t r_k,
+                       uint32_t y_norm, uint32_t g, uint32_t yg_f16, uint64_t h, uint64_t n, float eps,
+                       float gn_eps, uint64_t batch);
+
 /* ---- profiling hooks (backend.rs:67-70); kernel timing is done with rocprofv3 */
 int rsv_clear_kernel_prof(rsv_ctx *ctx);
 int rsv_dump_kernel_prof(rsv_ctx *ctx);

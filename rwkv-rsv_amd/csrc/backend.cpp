@@ -113,6 +113,13 @@ int rsv_create(int device, rsv_ctx **out) {
     }
     hipDeviceProp_t prop;
     if (hipGetDeviceProperties(&prop, device) == hipSuccess) ctx->sm_count = prop.multiProcessorCount;
+    // 32 Mi floats (128 MiB) of split-K partial tiles
+    ctx->skinny_ws_cap = (size_t)32 << 20;
+    if (hipMalloc(&ctx->skinny_ws, ctx->skinny_ws_cap * 4) != hipSuccess) {
+        hipStreamDestroy(ctx->stream);
+        delete ctx;
+        return RSV_FAIL("rsv_create: workspace allocation failed");
+    }
     *out = ctx;
     return 0;
 }
@@ -128,6 +135,7 @@ int rsv_destroy(rsv_ctx *ctx) {
         if (t.live && !t.foreign && t.ptr) hipFree(t.ptr);
     if (ctx->hist_dev) hipFree(ctx->hist_dev);
     if (ctx->sample_work) hipFree(ctx->sample_work);
+    if (ctx->skinny_ws) hipFree(ctx->skinny_ws);
     hipStreamDestroy(ctx->stream);
     delete ctx;
     return 0;
@@ -1150,3 +1158,161 @@ int rsv_gemm_ex(rsv_ctx *ctx, uint32_t a, uint32_t w16, const rsv_int8 *w8, uint
 }
 
 }  // extern "C"
+
+extern "C" int rsv_gemv_multi(rsv_ctx *ctx, const rsv_gemv_job *jobs, uint64_t njobs, uint32_t side_src,
+                              uint32_t side_dst, uint64_t side_n, uint64_t batch) {
+    CHECK_CTX();
+    if (!jobs || njobs == 0 || njobs > (uint64_t)kMaxJobs) return RSV_FAIL("gemv_multi: 1..%d jobs", kMaxJobs);
+    GemvJobs J{};
+    J.n = (int)njobs;
+    for (uint64_t i = 0; i < njobs; i++) {
+        const rsv_gemv_job &q = jobs[i];
+        GemvJob &g = J.j[i];
+        if (q.w8 ? job_i8(ctx, g, q.w8, q.m, q.k, "gemv_multi") : job_f16(ctx, g, q.w16, q.m, q.k, "gemv_multi"))
+            return -1;
+        if (job_xy(ctx, g, q.x, q.y, batch, "gemv_multi")) return -1;
+        if (q.prologue < PRO_NONE || q.prologue > PRO_LNMIX) return RSV_FAIL("gemv_multi: bad prologue %d", q.prologue);
+        if (q.epilogue < EPI_STORE || q.epilogue > EPI_STORE2) return RSV_FAIL("gemv_multi: bad epilogue %d", q.epilogue);
+        g.pro = q.prologue;
+        g.epi = q.epilogue;
+        void *p = nullptr;
+        if (q.xmul != 0xFFFFFFFFu) { if (opnd(ctx, q.xmul, RSV_F32, q.k * batch, &p, "gemv_multi xmul")) return -1; g.xmul = (const float *)p; }
+        if (q.p0 != 0xFFFFFFFFu) { if (opnd(ctx, q.p0, RSV_F32, q.m, &p, "gemv_multi p0")) return -1; g.p0 = (const float *)p; }
+        if (q.p1 != 0xFFFFFFFFu) { if (opnd(ctx, q.p1, RSV_F32, q.m * batch, &p, "gemv_multi p1")) return -1; g.p1 = (const float *)p; }
+        if (q.scale != 0xFFFFFFFFu) { if (opnd(ctx, q.scale, RSV_F32, 1, &p, "gemv_multi scale")) return -1; g.scale = (const float *)p; }
+        if (q.gamma != 0xFFFFFFFFu) { if (opnd(ctx, q.gamma, RSV_F32, q.k, &p, "gemv_multi gamma")) return -1; g.gamma = (const float *)p; }
+        if (q.beta != 0xFFFFFFFFu) { if (opnd(ctx, q.beta, RSV_F32, q.k, &p, "gemv_multi beta")) return -1; g.beta = (const float *)p; }
+        if (q.prev != 0xFFFFFFFFu) { if (opnd(ctx, q.prev, RSV_F32, q.k * batch, &p, "gemv_multi prev")) return -1; g.prev = (const float *)p; }
+        if (q.coef != 0xFFFFFFFFu) { if (opnd(ctx, q.coef, RSV_F32, q.k, &p, "gemv_multi coef")) return -1; g.coef = (const float *)p; }
+        if (q.lnout != 0xFFFFFFFFu) { if (opnd(ctx, q.lnout, RSV_F32, q.k * batch, &p, "gemv_multi lnout")) return -1; g.lnout = (float *)p; }
+    }
+    if (side_src != 0xFFFFFFFFu || side_dst != 0xFFFFFFFFu) {
+        void *a = nullptr, *b = nullptr;
+        if (opnd(ctx, side_src, RSV_F32, side_n * batch, &a, "gemv_multi side_src") ||
+            opnd(ctx, side_dst, RSV_F32, side_n * batch, &b, "gemv_multi side_dst"))
+            return -1;
+        J.side.src = (const float *)a;
+        J.side.dst = (float *)b;
+        J.side.n = (int)side_n;
+    }
+    return launch_gemv_jobs(ctx, J, (int)batch);
+}
+
+extern "C" int rsv_gemm_skinny(rsv_ctx *ctx, const rsv_mm_job *jobs, uint64_t njobs, uint64_t batch) {
+    CHECK_CTX();
+    if (!jobs || njobs == 0 || njobs > (uint64_t)kMaxJobs) return RSV_FAIL("gemm_skinny: 1..%d jobs", kMaxJobs);
+    SkinnyJobs S{};
+    S.n = (int)njobs;
+    for (uint64_t i = 0; i < njobs; i++) {
+        const rsv_mm_job &q = jobs[i];
+        SkinnyJob &J = S.j[i];
+        if (q.w8) {
+            const uint32_t *idx, *sz;
+            if (int8_operands(ctx, q.w8, q.n, q.k, &idx, &sz, "gemm_skinny")) return -1;
+            J.w = idx;
+            J.sz = sz;
+            J.fmt = FMT_I8;
+        } else {
+            void *p = nullptr;
+            if (opnd(ctx, q.w16, RSV_F16, q.n * q.k, &p, "gemm_skinny w16")) return -1;
+            J.w = p;
+            J.fmt = FMT_F16;
+        }
+        void *px = nullptr;
+        if (opnd(ctx, q.x, RSV_F16, q.k * batch, &px, "gemm_skinny x")) return -1;
+        J.x = (const _Float16 *)px;
+        J.ldx = (int)q.k;
+        Tensor *ty = get_tensor(ctx, q.y);
+        if (!ty || ty->dtype == RSV_U32 || ty->len < q.n * batch) return RSV_FAIL("gemm_skinny: bad y tensor %u", q.y);
+        J.y = ty->ptr;
+        J.y_f16 = ty->dtype == RSV_F16;
+        J.ldy = (int)q.n;
+        void *p = nullptr;
+        if (q.y2 != 0xFFFFFFFFu) { if (opnd(ctx, q.y2, RSV_F32, q.n * batch, &p, "gemm_skinny y2")) return -1; J.y2 = (float *)p; }
+        if (q.bias != 0xFFFFFFFFu) { if (opnd(ctx, q.bias, RSV_F32, q.n, &p, "gemm_skinny bias")) return -1; J.bias = (const float *)p; }
+        if (q.aux != 0xFFFFFFFFu) { if (opnd(ctx, q.aux, RSV_F32, q.n * batch, &p, "gemm_skinny aux")) return -1; J.aux = (const float *)p; }
+        if (q.scale != 0xFFFFFFFFu) { if (opnd(ctx, q.scale, RSV_F32, 1, &p, "gemm_skinny scale")) return -1; J.scale = (const float *)p; }
+        if (q.epilogue < GE_STORE || q.epilogue > GE_SIGMOID) return RSV_FAIL("gemm_skinny: bad epilogue %d", q.epilogue);
+        J.epi = q.epilogue;
+        J.tiled = q.tiled ? 1 : 0;
+        if (J.tiled) {  // the tiled copy holds ceil(n/32)*32 rows
+            Tensor *tw = get_tensor(ctx, q.w8 ? q.w8->idx : q.w16);
+            const uint64_t need = (q.n + 31) / 32 * 32 * q.k * (q.w8 ? 1 : 2);
+            if (!tw || tw->len * dtype_size(tw->dtype) < need) return RSV_FAIL("gemm_skinny: tiled weight too small");
+        }
+        J.N = (int)q.n;
+        J.K = (int)q.k;
+    }
+    return launch_skinny(ctx, S, (int)batch);
+}
+
+extern "C" int rsv_ln_mix_f16(rsv_ctx *ctx, uint32_t x, uint32_t state, uint32_t gamma, uint32_t beta,
+                              const uint32_t *coef, const uint32_t *out_f16, uint64_t nout, uint64_t c, float eps,
+                              uint64_t batch) {
+    CHECK_CTX();
+    if ((nout != 1 && nout != 6) || !out_f16) return RSV_FAIL("ln_mix_f16: nout must be 1 or 6");
+    OPND(px, x, RSV_F32, c * batch, "ln_mix_f16 x");
+    OPND(pg, gamma, RSV_F32, c, "ln_mix_f16 gamma");
+    OPND(pb, beta, RSV_F32, c, "ln_mix_f16 beta");
+    float *pst = nullptr;
+    if (state != 0xFFFFFFFFu) { OPND(ps, state, RSV_F32, c * batch, "ln_mix_f16 state"); pst = F32P(ps); }
+    const float *cp[6] = {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
+    _Float16 *op[6];
+    for (uint64_t j = 0; j < nout; j++) {
+        void *p = nullptr;
+        if (coef && coef[j] != 0xFFFFFFFFu) {
+            if (!pst) return RSV_FAIL("ln_mix_f16: a token-shift mix needs the state row");
+            if (opnd(ctx, coef[j], RSV_F32, c, &p, "ln_mix_f16 coef")) return -1;
+            cp[j] = (const float *)p;
+        }
+        if (opnd(ctx, out_f16[j], RSV_F16, c * batch, &p, "ln_mix_f16 out")) return -1;
+        op[j] = (_Float16 *)p;
+    }
+    return launch_ln_mix_f16(ctx, F32P(px), pst, F32P(pg), F32P(pb), cp, op, (int)nout, (int)c, eps, (int)batch);
+}
+
+extern "C" int rsv_wkv7_decode_ex(rsv_ctx *ctx, uint32_t s, uint32_t k, uint32_t k_k, uint32_t a, uint32_t k_a,
+                                  uint32_t r, uint32_t v, uint32_t w, uint32_t ln_x_w, uint32_t ln_x_b, uint32_t r_k,
+                                  uint32_t y_norm, uint32_t g, uint32_t yg_f16, uint64_t h, uint64_t n, float eps,
+                                  float gn_eps, uint64_t batch) {
+    CHECK_CTX();
+    const uint64_t c = h * n;
+    OPND(ss, s, RSV_F32, batch * h * n * n, "wkv state");
+    OPND(kk, k, RSV_F32, c * batch, "wkv k");
+    OPND(kc, k_k, RSV_F32, c, "wkv k_k");
+    OPND(aa, a, RSV_F32, c * batch, "wkv a");
+    OPND(kac, k_a, RSV_F32, c, "wkv k_a");
+    OPND(rr, r, RSV_F32, c * batch, "wkv r");
+    OPND(vv, v, RSV_F32, c * batch, "wkv v");
+    OPND(ww, w, RSV_F32, c * batch, "wkv w");
+    OPND(gw, ln_x_w, RSV_F32, c, "wkv ln_x_w");
+    OPND(gb, ln_x_b, RSV_F32, c, "wkv ln_x_b");
+    OPND(rkc, r_k, RSV_F32, c, "wkv r_k");
+    float *yn = nullptr, *gm = nullptr;
+    _Float16 *yg = nullptr;
+    if (y_norm != 0xFFFFFFFFu) { OPND(p, y_norm, RSV_F32, c * batch, "wkv y_norm"); yn = F32P(p); }
+    if (g != 0xFFFFFFFFu) { OPND(p, g, RSV_F32, c * batch, "wkv g"); gm = F32P(p); }
+    if (yg_f16 != 0xFFFFFFFFu) { OPND(p, yg_f16, RSV_F16, c * batch, "wkv yg"); yg = (_Float16 *)p_v; }
+    return launch_wkv7_decode(ctx, F32P(ss), F32P(kk), F32P(kc), F32P(aa), F32P(kac), F32P(rr), F32P(vv), F32P(ww),
+                              F32P(gw), F32P(gb), F32P(rkc), nullptr, nullptr, yn, (int)h, (int)n, eps, gn_eps,
+                              (int)batch, gm, yg);
+}
+
+extern "C" int rsv_tile_weights(rsv_ctx *ctx, uint32_t src, uint64_t n, uint64_t k, int esz, uint32_t *out) {
+    CHECK_CTX();
+    if (!out || (esz != 1 && esz != 2)) return RSV_FAIL("tile_weights: bad arguments");
+    if (k % 32 != 0) return RSV_FAIL("tile_weights: k=%llu must be a multiple of 32", (unsigned long long)k);
+    void *ps = nullptr;
+    if (opnd(ctx, src, esz == 1 ? RSV_U32 : RSV_F16, esz == 1 ? n * k / 4 : n * k, &ps, "tile_weights src")) return -1;
+    const uint64_t rows = (n + 31) / 32 * 32;
+    uint32_t id;
+    if (esz == 1) {
+        if (rsv_tensor_create(ctx, rows * k / 4, RSV_U32, &id)) return -1;
+    } else {
+        if (rsv_tensor_create(ctx, rows * k, RSV_F16, &id)) return -1;
+    }
+    Tensor *t = get_tensor(ctx, id);
+    if (launch_tile_weights(ctx, ps, t->ptr, (int)n, (int)k, esz)) return -1;
+    *out = id;
+    return 0;
+}

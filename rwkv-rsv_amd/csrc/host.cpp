@@ -237,6 +237,10 @@ struct Linear {
     rsv_int8 h{};      // int8
     uint32_t w16 = NONE; // fp16 [m, k]
     uint64_t m = 0, k = 0;
+    // MFMA-tiled copy for the batched path (made on first use)
+    bool tiled = false;
+    rsv_int8 ht{};
+    uint32_t t16 = NONE;
 };
 
 struct Layer {
@@ -245,6 +249,7 @@ struct Layer {
     uint32_t w0, a0, v0, r_k, k_k, k_a;
     uint32_t w1, w2, a1, a2, v1, v2, g1, g2;  // fp16 [out, in]
     Linear rw, kw, vw, ow, fk, fv;
+    Linear lw1, lw2, la1, la2, lv1, lv2, lg1, lg2;  // LoRA views (fp16) for the batched path
 };
 
 struct GpuState {
@@ -256,7 +261,13 @@ struct GpuState {
 struct WorkBufs {
     uint64_t batch = 0;
     uint32_t x, xr, xw, xk, xv, xa, xg, r, k, v, vmid, wmid, amid, gmid, w, a, g, yn, xb, r2, xnorm, logits, token;
+    uint32_t ln1, ln2;  // LayerNorm rows kept for the token-shift state
+    // fp16 operands of the matrix-core path (batch >= kMmBatch)
+    bool mm = false;
+    uint32_t mix16[6], vmid16, wmid16, amid16, gmid16, yg16, xb16, r216, xn16;
 };
+
+constexpr uint64_t kMmBatch = 16;  // sessions from which decode GEMMs run on MFMA
 
 struct SeqBufs {
     uint64_t cap = 0, segcap = 0;
@@ -550,6 +561,8 @@ int state_reset(rsv_bundle *b, GpuState &s) {
 }
 
 // ------------------------------------------------------------ decode
+int tile_model(rsv_bundle *b);
+
 int get_bufs(rsv_bundle *b, uint64_t B, WorkBufs *&out) {
     auto it = b->bufs.find(B);
     if (it != b->bufs.end()) { out = &it->second; return 0; }
@@ -557,7 +570,7 @@ int get_bufs(rsv_bundle *b, uint64_t B, WorkBufs *&out) {
     const uint64_t C = I.n_embd;
     WorkBufs w;
     w.batch = B;
-    uint32_t *c_ids[] = {&w.x, &w.xr, &w.xw, &w.xk, &w.xv, &w.xa, &w.xg, &w.r, &w.k, &w.v, &w.w, &w.a, &w.g, &w.yn, &w.xb, &w.xnorm};
+    uint32_t *c_ids[] = {&w.x, &w.xr, &w.xw, &w.xk, &w.xv, &w.xa, &w.xg, &w.r, &w.k, &w.v, &w.w, &w.a, &w.g, &w.yn, &w.xb, &w.xnorm, &w.ln1, &w.ln2};
     for (auto p : c_ids) HK(new_tensor(b, C * B, RSV_F32, *p));
     HK(new_tensor(b, I.v_mid * B, RSV_F32, w.vmid));
     HK(new_tensor(b, I.w_mid * B, RSV_F32, w.wmid));
@@ -566,6 +579,19 @@ int get_bufs(rsv_bundle *b, uint64_t B, WorkBufs *&out) {
     HK(new_tensor(b, I.ffn * B, RSV_F32, w.r2));
     HK(new_tensor(b, I.vocab * B, RSV_F32, w.logits));
     HK(new_tensor(b, B, RSV_U32, w.token));
+    w.mm = B >= kMmBatch;
+    if (w.mm) {
+        HK(tile_model(b));
+        for (auto &m : w.mix16) HK(new_tensor(b, C * B, RSV_F16, m));
+        HK(new_tensor(b, I.v_mid * B, RSV_F16, w.vmid16));
+        HK(new_tensor(b, I.w_mid * B, RSV_F16, w.wmid16));
+        HK(new_tensor(b, I.a_mid * B, RSV_F16, w.amid16));
+        HK(new_tensor(b, I.g_mid * B, RSV_F16, w.gmid16));
+        HK(new_tensor(b, C * B, RSV_F16, w.yg16));
+        HK(new_tensor(b, C * B, RSV_F16, w.xb16));
+        HK(new_tensor(b, I.ffn * B, RSV_F16, w.r216));
+        HK(new_tensor(b, C * B, RSV_F16, w.xn16));
+    }
     out = &(b->bufs[B] = w);
     return 0;
 }
@@ -591,8 +617,101 @@ int gemv_lin(rsv_bundle *b, const Linear &L, uint32_t x, uint32_t y, uint64_t B,
     return 0;
 }
 
-// One layer for B slots (gpu_model.rs:2060-2392 / 1373-1566).
-int forward_layer(rsv_bundle *b, uint64_t i, WorkBufs &w, GpuState &s) {
+rsv_gemv_job lin_job(const Linear &L, uint32_t x, uint32_t y, int pro, int epi) {
+    rsv_gemv_job j;
+    memset(&j, 0xFF, sizeof j);
+    j.w16 = L.i8 ? NONE : L.w16;
+    j.w8 = L.i8 ? &L.h : nullptr;
+    j.m = L.m;
+    j.k = L.k;
+    j.x = x;
+    j.y = y;
+    j.prologue = pro;
+    j.epilogue = epi;
+    return j;
+}
+
+rsv_gemv_job lora_job(uint32_t w, uint64_t m, uint64_t k, uint32_t x, uint32_t y, int pro, int epi) {
+    Linear L;
+    L.w16 = w;
+    L.m = m;
+    L.k = k;
+    return lin_job(L, x, y, pro, epi);
+}
+
+void ln_mix(rsv_gemv_job &j, uint32_t gamma, uint32_t beta, uint32_t prev, uint32_t coef, uint32_t lnout) {
+    j.gamma = gamma;
+    j.beta = beta;
+    j.prev = prev;
+    j.coef = coef;
+    j.lnout = lnout;
+}
+
+// One layer for B slots with the op sequence of gpu_model.rs:2060-2392 /
+// 1373-1566, fused into six launches:
+//   1. LN1 + token shift + r/k/v (int8) + LoRA-down projections  (state LN row -> ln1)
+//   2. LoRA-up chain (w, a, v-first lerp, g)                      (ln1 -> tmix state)
+//   3. WKV7 state update + GroupNorm + bonus
+//   4. att.output: x += (y_norm * g) W^T
+//   5. LN2 + token shift + ffn.key relu^2                          (state LN row -> ln2)
+//   6. ffn.value: x += r2 W^T                                      (ln2 -> cmix state)
+// The state writes are deferred by one launch so that no block of a launch
+// reads a token-shift row another block of the same launch rewrites.
+int forward_layer_fused(rsv_bundle *b, uint64_t i, WorkBufs &w, GpuState &s) {
+    rsv_ctx *c = b->ctx;
+    const rsv_model_info &I = b->info;
+    const uint64_t C = I.n_embd, B = w.batch;
+    Layer &L = b->layers[i];
+    enum { P_NONE = 0, P_MUL = 1, P_SIG = 2, P_LN = 3 };
+    enum { E_STORE = 0, E_RELU2 = 1, E_ADD = 2, E_TANH = 3, E_WDECAY = 4, E_SIGB = 5, E_VLERP = 6, E_STORE2 = 7 };
+    if (L.rw.i8 != L.kw.i8 || L.rw.i8 != L.vw.i8)
+        return herr("layer %llu: receptance/key/value must share one format", (unsigned long long)i);
+    rsv_gemv_job j1[7] = {
+        lin_job(L.rw, w.x, w.r, P_LN, E_STORE),
+        lin_job(L.kw, w.x, w.k, P_LN, E_STORE),
+        lin_job(L.vw, w.x, w.v, P_LN, i == 0 ? E_STORE2 : E_STORE),
+        lora_job(L.v1, I.v_mid, C, w.x, w.vmid, P_LN, E_STORE),
+        lora_job(L.w1, I.w_mid, C, w.x, w.wmid, P_LN, E_TANH),
+        lora_job(L.a1, I.a_mid, C, w.x, w.amid, P_LN, E_STORE),
+        lora_job(L.g1, I.g_mid, C, w.x, w.gmid, P_LN, E_STORE),
+    };
+    const uint32_t coef1[7] = {L.x_r, L.x_k, L.x_v, L.x_v, L.x_w, L.x_a, L.x_g};
+    for (int q = 0; q < 7; q++) ln_mix(j1[q], L.ln1_w, L.ln1_b, s.tmix_x[i], coef1[q], q == 0 ? w.ln1 : NONE);
+    if (i == 0) j1[2].p1 = s.v_first;  // v_first snapshot (gpu_model.rs:2200-2204)
+    CK(rsv_gemv_multi(c, j1, 7, NONE, NONE, 0, B));
+
+    rsv_gemv_job j2[4] = {
+        lora_job(L.w2, C, I.w_mid, w.wmid, w.w, P_NONE, E_WDECAY),
+        lora_job(L.a2, C, I.a_mid, w.amid, w.a, P_NONE, E_SIGB),
+        lora_job(L.v2, C, I.v_mid, w.vmid, w.v, P_NONE, E_VLERP),
+        lora_job(L.g2, C, I.g_mid, w.gmid, w.g, P_SIG, E_STORE),
+    };
+    j2[0].p0 = L.w0;
+    j2[0].scale = b->scale_w;
+    j2[1].p0 = L.a0;
+    j2[2].p0 = L.v0;
+    j2[2].p1 = s.v_first;
+    CK(rsv_gemv_multi(c, j2, 4, w.ln1, s.tmix_x[i], C, B));
+
+    CK(rsv_fuse_ka_dplr_norm_batch(c, s.rnn[i], w.k, L.k_k, w.a, L.k_a, w.r, w.v, w.w, L.lnx_w, L.lnx_b, L.r_k, NONE,
+                                   NONE, w.yn, I.n_head, I.head_size, L2_EPS, GN_EPS, B));
+
+    rsv_gemv_job j4 = lin_job(L.ow, w.yn, w.x, P_MUL, E_ADD);
+    j4.xmul = w.g;
+    CK(rsv_gemv_multi(c, &j4, 1, NONE, NONE, 0, B));
+
+    rsv_gemv_job j5 = lin_job(L.fk, w.x, w.r2, P_LN, E_RELU2);
+    ln_mix(j5, L.ln2_w, L.ln2_b, s.cmix_x[i], L.ffn_x_k, w.ln2);
+    CK(rsv_gemv_multi(c, &j5, 1, NONE, NONE, 0, B));
+
+    rsv_gemv_job j6 = lin_job(L.fv, w.r2, w.x, P_NONE, E_ADD);
+    CK(rsv_gemv_multi(c, &j6, 1, w.ln2, s.cmix_x[i], C, B));
+    return 0;
+}
+
+// The same layer through the reference's trait-op sequence, one op per
+// ComputeBackend method (kept for A/B checks; RSV_DECODE_TRAIT_OPS=1).
+int forward_layer_ops(rsv_bundle *b, uint64_t i, WorkBufs &w, GpuState &s) {
     rsv_ctx *c = b->ctx;
     const rsv_model_info &I = b->info;
     const uint64_t C = I.n_embd, B = w.batch;
@@ -623,12 +742,118 @@ int forward_layer(rsv_bundle *b, uint64_t i, WorkBufs &w, GpuState &s) {
     return 0;
 }
 
+rsv_mm_job mm_job(const Linear &L, uint32_t x, uint32_t y, int epi) {
+    rsv_mm_job j;
+    memset(&j, 0xFF, sizeof j);
+    j.tiled = L.tiled ? 1 : 0;
+    j.w16 = L.i8 ? NONE : (L.tiled ? L.t16 : L.w16);
+    j.w8 = L.i8 ? (L.tiled ? &L.ht : &L.h) : nullptr;
+    j.n = L.m;
+    j.k = L.k;
+    j.x = x;
+    j.y = y;
+    j.epilogue = epi;
+    return j;
+}
+
+int tile_linear(rsv_bundle *b, Linear &L) {
+    if (L.tiled) return 0;
+    if (L.i8) {
+        L.ht = L.h;
+        CK(rsv_tile_weights(b->ctx, L.h.idx, L.m, L.k, 1, &L.ht.idx));
+    } else {
+        CK(rsv_tile_weights(b->ctx, L.w16, L.m, L.k, 2, &L.t16));
+    }
+    L.tiled = true;
+    return 0;
+}
+
+// MFMA-tiled weight copies for the batched decode path (extra device memory
+// of the size of the weights; HBM is not the constraint on this GPU).
+int tile_model(rsv_bundle *b) {
+    const rsv_model_info &I = b->info;
+    const uint64_t C = I.n_embd;
+    for (auto &L : b->layers) {
+        auto lora = [&](Linear &V, uint32_t w, uint64_t m, uint64_t k) { V.w16 = w; V.m = m; V.k = k; return tile_linear(b, V); };
+        HK(lora(L.lw1, L.w1, I.w_mid, C));
+        HK(lora(L.lw2, L.w2, C, I.w_mid));
+        HK(lora(L.la1, L.a1, I.a_mid, C));
+        HK(lora(L.la2, L.a2, C, I.a_mid));
+        HK(lora(L.lv1, L.v1, I.v_mid, C));
+        HK(lora(L.lv2, L.v2, C, I.v_mid));
+        HK(lora(L.lg1, L.g1, I.g_mid, C));
+        HK(lora(L.lg2, L.g2, C, I.g_mid));
+        for (Linear *p : {&L.rw, &L.kw, &L.vw, &L.ow, &L.fk, &L.fv}) HK(tile_linear(b, *p));
+    }
+    HK(tile_linear(b, b->head));
+    CK(rsv_synchronize(b->ctx));
+    return 0;
+}
+
+// Batched layer (B >= kMmBatch): the same math with fp16 activation
+// operands so every weight product runs on matrix cores, each weight byte
+// streamed once per step for all sessions.
+int forward_layer_mm(rsv_bundle *b, uint64_t i, WorkBufs &w, GpuState &s) {
+    rsv_ctx *c = b->ctx;
+    const rsv_model_info &I = b->info;
+    const uint64_t C = I.n_embd, B = w.batch;
+    Layer &L = b->layers[i];
+    enum { G_STORE = 0, G_BIAS = 1, G_ADD = 2, G_RELU2 = 3, G_TANH = 4, G_WDECAY = 5, G_SIGB = 6, G_VLERP = 7, G_SIG = 8 };
+    const uint32_t coef6[6] = {L.x_r, L.x_w, L.x_k, L.x_v, L.x_a, L.x_g};
+    CK(rsv_ln_mix_f16(c, w.x, s.tmix_x[i], L.ln1_w, L.ln1_b, coef6, w.mix16, 6, C, LN_EPS, B));
+    const uint32_t xr = w.mix16[0], xw = w.mix16[1], xk = w.mix16[2], xv = w.mix16[3], xa = w.mix16[4], xg = w.mix16[5];
+    rsv_mm_job j1[7] = {
+        mm_job(L.rw, xr, w.r, G_STORE), mm_job(L.kw, xk, w.k, G_STORE), mm_job(L.vw, xv, w.v, G_STORE),
+        mm_job(L.lv1, xv, w.vmid16, G_STORE), mm_job(L.lw1, xw, w.wmid16, G_TANH),
+        mm_job(L.la1, xa, w.amid16, G_STORE), mm_job(L.lg1, xg, w.gmid16, G_SIG),
+    };
+    if (i == 0) j1[2].y2 = s.v_first;  // v_first snapshot (gpu_model.rs:2200-2204)
+    CK(rsv_gemm_skinny(c, j1, 7, B));
+    rsv_mm_job j2[4] = {
+        mm_job(L.lw2, w.wmid16, w.w, G_WDECAY), mm_job(L.la2, w.amid16, w.a, G_SIGB),
+        mm_job(L.lv2, w.vmid16, w.v, G_VLERP), mm_job(L.lg2, w.gmid16, w.g, G_STORE),
+    };
+    j2[0].bias = L.w0;
+    j2[0].scale = b->scale_w;
+    j2[1].bias = L.a0;
+    j2[2].bias = L.v0;
+    j2[2].aux = s.v_first;
+    CK(rsv_gemm_skinny(c, j2, 4, B));
+    CK(rsv_wkv7_decode_ex(c, s.rnn[i], w.k, L.k_k, w.a, L.k_a, w.r, w.v, w.w, L.lnx_w, L.lnx_b, L.r_k, NONE, w.g,
+                          w.yg16, I.n_head, I.head_size, L2_EPS, GN_EPS, B));
+    rsv_mm_job j4 = mm_job(L.ow, w.yg16, w.x, G_ADD);
+    CK(rsv_gemm_skinny(c, &j4, 1, B));
+    CK(rsv_ln_mix_f16(c, w.x, s.cmix_x[i], L.ln2_w, L.ln2_b, &L.ffn_x_k, &w.xb16, 1, C, LN_EPS, B));
+    rsv_mm_job j5 = mm_job(L.fk, w.xb16, w.r216, G_RELU2);
+    CK(rsv_gemm_skinny(c, &j5, 1, B));
+    rsv_mm_job j6 = mm_job(L.fv, w.r216, w.x, G_ADD);
+    CK(rsv_gemm_skinny(c, &j6, 1, B));
+    return 0;
+}
+
+bool use_trait_ops() {
+    const char *e = getenv("RSV_DECODE_TRAIT_OPS");
+    return e && e[0] && e[0] != '0';
+}
+
+int forward_layer(rsv_bundle *b, uint64_t i, WorkBufs &w, GpuState &s) {
+    if (use_trait_ops()) return forward_layer_ops(b, i, w, s);
+    if (w.mm) return forward_layer_mm(b, i, w, s);
+    return forward_layer_fused(b, i, w, s);
+}
+
 // gather -> layers -> ln_out -> head (gpu_model.rs:1879-1913 minus the sampler)
 int decode_step(rsv_bundle *b, WorkBufs &w, GpuState &s) {
     rsv_ctx *c = b->ctx;
     const rsv_model_info &I = b->info;
     CK(rsv_gather_rows_device_f16(c, b->emb_ln, w.x, w.token, I.n_embd, w.batch));
     for (uint64_t i = 0; i < I.n_layer; i++) HK(forward_layer(b, i, w, s));
+    if (w.mm && !use_trait_ops()) {
+        CK(rsv_ln_mix_f16(c, w.x, NONE, b->ln_out_w, b->ln_out_b, nullptr, &w.xn16, 1, I.n_embd, LN_EPS, w.batch));
+        rsv_mm_job jh = mm_job(b->head, w.xn16, w.logits, 0);
+        CK(rsv_gemm_skinny(c, &jh, 1, w.batch));
+        return 0;
+    }
     CK(rsv_norm(c, w.x, b->ln_out_w, b->ln_out_b, w.xnorm, I.n_embd, 1, LN_EPS, w.batch));
     HK(gemv_lin(b, b->head, w.xnorm, w.logits, w.batch, 0));
     return 0;
@@ -795,18 +1020,29 @@ int selfloop(rsv_bundle *b, GpuState &s, const uint32_t *seeds, uint64_t n, cons
         }
         if (rsv_store_tokens(c, w->token, seeds, B)) { rc = herr("store_tokens: %s", rsv_last_error()); break; }
         if (rsv_synchronize(c)) { rc = herr("%s", rsv_last_error()); break; }
-        if (rsv_graph_begin(c)) { rc = herr("graph_begin: %s", rsv_last_error()); break; }
-        int cap = decode_step(b, *w, s);
-        if (!cap) {
-            if (sp) cap = rsv_sample_into_host_seeded_batch(c, w->logits, w->token, I.vocab, temp, NONE, counter,
-                                                           sampler, seq, B);
-            else cap = rsv_argmax_batch(c, w->logits, w->token, I.vocab, B);
-            if (cap) herr("sampler: %s", rsv_last_error());
+        // One step = gather -> layers -> head -> sampler -> record.  It is
+        // captured once as a HIP graph and replayed n times; RSV_NO_GRAPH=1
+        // enqueues the same kernels eagerly every round instead (the
+        // reference's SKIP_GRAPH debugging path, gpu_model.rs:1698-1721).
+        const bool eager = getenv("RSV_NO_GRAPH") && getenv("RSV_NO_GRAPH")[0] && getenv("RSV_NO_GRAPH")[0] != '0';
+        auto step = [&]() -> int {
+            int e = decode_step(b, *w, s);
+            if (!e) {
+                if (sp) e = rsv_sample_into_host_seeded_batch(c, w->logits, w->token, I.vocab, temp, NONE, counter,
+                                                             sampler, seq, B);
+                else e = rsv_argmax_batch(c, w->logits, w->token, I.vocab, B);
+                if (e) herr("sampler: %s", rsv_last_error());
+            }
+            if (!e && rsv_record_tokens(c, w->token, seq, cnt, n, B)) e = herr("record: %s", rsv_last_error());
+            return e;
+        };
+        if (!eager) {
+            if (rsv_graph_begin(c)) { rc = herr("graph_begin: %s", rsv_last_error()); break; }
+            const int cap = step();
+            const int end_rc = rsv_graph_end(c);
+            if (cap) { rc = cap; break; }
+            if (end_rc) { rc = herr("graph_end: %s", rsv_last_error()); break; }
         }
-        if (!cap && rsv_record_tokens(c, w->token, seq, cnt, n, B)) cap = herr("record: %s", rsv_last_error());
-        const int end_rc = rsv_graph_end(c);
-        if (cap) { rc = cap; break; }
-        if (end_rc) { rc = herr("graph_end: %s", rsv_last_error()); break; }
         hipEvent_t e0 = nullptr, e1 = nullptr;
         void *stream = nullptr;
         rsv_stream(c, &stream);
@@ -825,7 +1061,10 @@ int selfloop(rsv_bundle *b, GpuState &s, const uint32_t *seeds, uint64_t n, cons
                                                   sp->presence_penalty, (uint32_t)r))
                     rc = herr("store_sampler: %s", rsv_last_error());
             }
-            if (!rc && rsv_graph_replay(c)) rc = herr("graph_replay: %s", rsv_last_error());
+            if (!rc) {
+                if (eager) rc = step();
+                else if (rsv_graph_replay(c)) rc = herr("graph_replay: %s", rsv_last_error());
+            }
         }
         if (ms) {
             hipEventRecord(e1, (hipStream_t)stream);

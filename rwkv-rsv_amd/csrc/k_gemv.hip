@@ -23,43 +23,80 @@ __device__ __forceinline__ float h2f(uint32_t b) {
 }
 __device__ __forceinline__ float sigmoid_f(float v) { return 1.0f / (1.0f + expf(-v)); }
 
-template <int FMT, int LPR, int BT, int RU>
-__device__ __forceinline__ void gemv_body(const GemvJob &J, int rb, int batch, float4 *xs, float *dxs) {
-    constexpr int CW = FMT == FMT_I8 ? 16 : 8;  // weights per 16-byte chunk
-    constexpr int P = CW / 4;                   // float4 parts of x per chunk
-    constexpr int SLOTS = 64 / LPR;
-    constexpr int U = 4;
-    const int K = J.K, M = J.M, NC = K / CW;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int slot = lane / LPR, li = lane % LPR;
-    const int rows_per_block = 4 * SLOTS * RU;
-    const int rbase = rb * rows_per_block + (wave * SLOTS + slot) * RU;
-    const int b0 = blockIdx.y * BT;
-    const int nb = min(BT, batch - b0);
-    const u32x4 *W = (const u32x4 *)J.w;
-    const int KG = K / 128;
+__device__ __forceinline__ float block_sum_256(float v, float *red) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return red[0] + red[1] + red[2] + red[3];
+}
 
-    // Stage x (with the prologue applied) into LDS, chunk-major.
+// Stages the (prologue-transformed) x rows of the block's batch tile into
+// LDS, chunk-major: float4 part p of chunk c of row b sits at
+// xs[(b*P + p)*NC + c], so lanes reading consecutive chunks read
+// consecutive 16-byte LDS words.  For int8 weights the per-chunk sum of x
+// (the zero-point term) goes to dxs[b*NC + c].
+template <int FMT, int BT>
+__device__ __forceinline__ void stage_x(const GemvJob &J, int rb, int b0, int nb, float4 *xs, float *dxs,
+                                        float *red) {
+    constexpr int CW = FMT == FMT_I8 ? 16 : 8;
+    constexpr int P = CW / 4;
+    const int K = J.K, NC = K / CW, tid = threadIdx.x;
+    float mean[BT], inv[BT];
+    if (J.pro == PRO_LNMIX) {
+        // LayerNorm statistics of each batch row, two-pass (model.rs:625-635)
+#pragma unroll
+        for (int b = 0; b < BT; b++) {
+            mean[b] = 0.0f;
+            inv[b] = 0.0f;
+            if (b >= nb) continue;
+            const float *xr = J.x + (size_t)(b0 + b) * J.ldx;
+            float s = 0.0f;
+            for (int i = tid; i < K; i += 256) s += xr[i];
+            const float mu = block_sum_256(s, red) / (float)K;
+            float q = 0.0f;
+            for (int i = tid; i < K; i += 256) { const float d = xr[i] - mu; q += d * d; }
+            const float var = block_sum_256(q, red) / (float)K + 1.0e-5f;
+            mean[b] = mu;
+            inv[b] = 1.0f / sqrtf(var);
+        }
+    }
     for (int e = tid; e < BT * NC; e += 256) {
         const int b = e / NC, c = e - (e / NC) * NC;
         float v[CW];
         if (b < nb) {
-            const float4 *xp = (const float4 *)(J.x + (size_t)(b0 + b) * J.ldx + (size_t)c * CW);
+            const size_t ro = (size_t)(b0 + b) * J.ldx + (size_t)c * CW;
+            const float4 *xp = (const float4 *)(J.x + ro);
 #pragma unroll
             for (int p = 0; p < P; p++) {
-                float4 t = xp[p];
+                const float4 t = xp[p];
                 v[4 * p] = t.x; v[4 * p + 1] = t.y; v[4 * p + 2] = t.z; v[4 * p + 3] = t.w;
             }
             if (J.pro == PRO_MUL) {
-                const float4 *gp = (const float4 *)(J.xmul + (size_t)(b0 + b) * J.ldx + (size_t)c * CW);
+                const float4 *gp = (const float4 *)(J.xmul + ro);
 #pragma unroll
                 for (int p = 0; p < P; p++) {
-                    float4 t = gp[p];
+                    const float4 t = gp[p];
                     v[4 * p] *= t.x; v[4 * p + 1] *= t.y; v[4 * p + 2] *= t.z; v[4 * p + 3] *= t.w;
                 }
             } else if (J.pro == PRO_SIGMOID) {
 #pragma unroll
                 for (int i = 0; i < CW; i++) v[i] = sigmoid_f(v[i]);
+            } else if (J.pro == PRO_LNMIX) {
+                const float *gm = J.gamma + (size_t)c * CW, *bt = J.beta + (size_t)c * CW;
+                const float *pv = J.prev + ro, *cf = J.coef + (size_t)c * CW;
+                float mu = 0.0f, is = 0.0f;
+#pragma unroll
+                for (int q = 0; q < BT; q++)
+                    if (q == b) { mu = mean[q]; is = inv[q]; }
+                const bool wr = J.lnout && rb == 0;
+#pragma unroll
+                for (int i = 0; i < CW; i++) {
+                    const float ln = (v[i] - mu) * is * gm[i] + bt[i];
+                    if (wr) J.lnout[ro + i] = ln;
+                    v[i] = ln + cf[i] * (pv[i] - ln);
+                }
             }
         } else {
 #pragma unroll
@@ -75,26 +112,37 @@ __device__ __forceinline__ void gemv_body(const GemvJob &J, int rb, int batch, f
             dxs[b * NC + c] = s;
         }
     }
-    __syncthreads();
+}
 
-    float acc[RU][BT];
-#pragma unroll
-    for (int r = 0; r < RU; r++)
-#pragma unroll
-        for (int b = 0; b < BT; b++) acc[r][b] = 0.0f;
-
+// LPR lanes per row, BT batch rows per block, RU rows per lane slot, U
+// 16-byte chunks per lane per load round; DB double-buffers load rounds
+// (long rows), otherwise every round is loaded before it is used.
+template <int FMT, int LPR, int BT, int RU, int U, bool DB>
+__device__ __forceinline__ void gemv_body(const GemvJob &J, int rb, int batch, float4 *xs, float *dxs, float *red) {
+    constexpr int CW = FMT == FMT_I8 ? 16 : 8;  // weights per 16-byte chunk
+    constexpr int P = CW / 4;                   // float4 parts of x per chunk
+    constexpr int SLOTS = 64 / LPR;
+    const int K = J.K, M = J.M, NC = K / CW;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int slot = lane / LPR, li = lane % LPR;
+    const int rows_per_block = 4 * SLOTS * RU;
+    const int rbase = rb * rows_per_block + (wave * SLOTS + slot) * RU;
+    const int b0 = blockIdx.y * BT;
+    const int nb = min(BT, batch - b0);
+    const u32x4 *W = (const u32x4 *)J.w;
+    const int KG = K / 128;
     const int NJ = (NC + LPR - 1) / LPR;
-    for (int j0 = 0; j0 < NJ; j0 += U) {
-        u32x4 wv[RU][U];
-        uint32_t szv[RU][U];
+
+    u32x4 wa[RU][U], wb[DB ? RU : 1][DB ? U : 1];
+    uint32_t sa[RU][U], sb[DB ? RU : 1][DB ? U : 1];
+    auto load = [&](u32x4 (&wv)[RU][U], uint32_t (&szv)[RU][U], int j0) {
 #pragma unroll
         for (int r = 0; r < RU; r++) {
             const int row = rbase + r;
 #pragma unroll
             for (int u = 0; u < U; u++) {
                 const int c = li + (j0 + u) * LPR;
-                const bool ok = (c < NC) && (row < M);
-                if (ok) {
+                if (c < NC && row < M) {
                     wv[r][u] = __builtin_nontemporal_load(W + (size_t)row * NC + c);
                     if (FMT == FMT_I8) szv[r][u] = J.sz[(size_t)row * KG + (c >> 3)];
                 } else {
@@ -103,6 +151,15 @@ __device__ __forceinline__ void gemv_body(const GemvJob &J, int rb, int batch, f
                 }
             }
         }
+    };
+
+    float acc[RU][BT];
+#pragma unroll
+    for (int r = 0; r < RU; r++)
+#pragma unroll
+        for (int b = 0; b < BT; b++) acc[r][b] = 0.0f;
+
+    auto compute = [&](const u32x4 (&wv)[RU][U], const uint32_t (&szv)[RU][U], int j0) {
 #pragma unroll
         for (int u = 0; u < U; u++) {
             int c = li + (j0 + u) * LPR;
@@ -112,7 +169,7 @@ __device__ __forceinline__ void gemv_body(const GemvJob &J, int rb, int batch, f
                 float xv[CW];
 #pragma unroll
                 for (int p = 0; p < P; p++) {
-                    float4 t = xs[(b * P + p) * NC + c];
+                    const float4 t = xs[(b * P + p) * NC + c];
                     xv[4 * p] = t.x; xv[4 * p + 1] = t.y; xv[4 * p + 2] = t.z; xv[4 * p + 3] = t.w;
                 }
                 if (FMT == FMT_I8) {
@@ -145,6 +202,24 @@ __device__ __forceinline__ void gemv_body(const GemvJob &J, int rb, int batch, f
                     }
                 }
             }
+        }
+    };
+
+    // Weight loads go out before x is staged: they do not depend on it.
+    load(wa, sa, 0);
+    stage_x<FMT, BT>(J, rb, b0, nb, xs, dxs, red);
+    __syncthreads();
+    if constexpr (DB) {
+        for (int j0 = 0; j0 < NJ; j0 += 2 * U) {
+            if (j0 + U < NJ) load(wb, sb, j0 + U);
+            compute(wa, sa, j0);
+            if (j0 + 2 * U < NJ) load(wa, sa, j0 + 2 * U);
+            if (j0 + U < NJ) compute(wb, sb, j0 + U);
+        }
+    } else {
+        for (int j0 = 0; j0 < NJ; j0 += U) {
+            if (j0) load(wa, sa, j0);
+            compute(wa, sa, j0);
         }
     }
 
@@ -182,6 +257,10 @@ __device__ __forceinline__ void gemv_body(const GemvJob &J, int rb, int batch, f
                         const float vf = J.p1[(size_t)(b0 + b) * J.ldy + row];
                         *yp = cur + g * (vf - cur);
                     } break;
+                    case EPI_STORE2:
+                        *yp = v;
+                        ((float *)J.p1)[(size_t)(b0 + b) * J.ldy + row] = v;
+                        break;
                     default: break;
                 }
             }
@@ -189,25 +268,30 @@ __device__ __forceinline__ void gemv_body(const GemvJob &J, int rb, int batch, f
     }
 }
 
-template <int LPR, int BT, int RU>
+template <int LPR, int BT, int RU, int U, bool DB>
 __global__ __launch_bounds__(256) void k_gemv(GemvJobs jobs, int batch) {
     extern __shared__ float4 smem4[];
+    __shared__ float red[4];
     const int bid = blockIdx.x;
+    if (bid == 0 && jobs.side.src) {
+        const int b0 = blockIdx.y * BT, nb = min(BT, batch - b0);
+        for (int b = 0; b < nb; b++)
+            for (int i = threadIdx.x; i < jobs.side.n; i += 256)
+                jobs.side.dst[(size_t)(b0 + b) * jobs.side.n + i] = jobs.side.src[(size_t)(b0 + b) * jobs.side.n + i];
+    }
     int ji = 0;
     while (ji + 1 < jobs.n && bid >= jobs.blk_start[ji + 1]) ji++;
     const GemvJob &J = jobs.j[ji];
     const int rb = bid - jobs.blk_start[ji];
-    const int cw = J.fmt == FMT_I8 ? 16 : 8;
     float4 *xs = smem4;
     float *dxs = (float *)(smem4 + (size_t)BT * J.K / 4);
-    (void)cw;
     if (J.fmt == FMT_I8)
-        gemv_body<FMT_I8, LPR, BT, RU>(J, rb, batch, xs, dxs);
+        gemv_body<FMT_I8, LPR, BT, RU, U, DB>(J, rb, batch, xs, dxs, red);
     else
-        gemv_body<FMT_F16, LPR, BT, RU>(J, rb, batch, xs, dxs);
+        gemv_body<FMT_F16, LPR, BT, RU, U, DB>(J, rb, batch, xs, dxs, red);
 }
 
-template <int LPR, int BT, int RU>
+template <int LPR, int BT, int RU, int U, bool DB>
 static int launch_t(rsv_ctx *ctx, GemvJobs &jobs, int batch) {
     const int rows_per_block = 4 * (64 / LPR) * RU;
     size_t smem = 0;
@@ -223,7 +307,7 @@ static int launch_t(rsv_ctx *ctx, GemvJobs &jobs, int batch) {
     }
     jobs.blk_start[jobs.n] = total;
     dim3 grid(total, (batch + BT - 1) / BT);
-    hipLaunchKernelGGL((k_gemv<LPR, BT, RU>), grid, dim3(256), smem, ctx->stream, jobs, batch);
+    hipLaunchKernelGGL((k_gemv<LPR, BT, RU, U, DB>), grid, dim3(256), smem, ctx->stream, jobs, batch);
     RSV_HIP(hipGetLastError());
     return 0;
 }
@@ -231,7 +315,7 @@ static int launch_t(rsv_ctx *ctx, GemvJobs &jobs, int batch) {
 int launch_gemv_jobs(rsv_ctx *ctx, GemvJobs &jobs, int batch) {
     if (jobs.n <= 0 || jobs.n > kMaxJobs) return RSV_FAIL("gemv: bad job count %d", jobs.n);
     if (batch <= 0) return RSV_FAIL("gemv: batch must be >= 1 (got %d)", batch);
-    int kmax = 0, ncmin = 1 << 30;
+    int kmax = 0, ncmin = 1 << 30, ncmax = 0;
     for (int i = 0; i < jobs.n; i++) {
         const GemvJob &J = jobs.j[i];
         if (!J.w || !J.x || !J.y) return RSV_FAIL("gemv job %d: null operand", i);
@@ -242,28 +326,39 @@ int launch_gemv_jobs(rsv_ctx *ctx, GemvJobs &jobs, int batch) {
         if (J.ldx % 4 != 0) return RSV_FAIL("gemv job %d: x batch stride must be a multiple of 4", i);
         if ((J.epi == EPI_WDECAY || J.epi == EPI_SIGBIAS || J.epi == EPI_VLERP) && !J.p0)
             return RSV_FAIL("gemv job %d: epilogue needs a bias", i);
-        if (J.epi == EPI_VLERP && !J.p1) return RSV_FAIL("gemv job %d: v-lerp needs v_first", i);
+        if ((J.epi == EPI_VLERP || J.epi == EPI_STORE2) && !J.p1) return RSV_FAIL("gemv job %d: needs v_first", i);
         if (J.epi == EPI_WDECAY && !J.scale) return RSV_FAIL("gemv job %d: decay needs scale", i);
         if (J.pro == PRO_MUL && !J.xmul) return RSV_FAIL("gemv job %d: mul prologue needs g", i);
+        if (J.pro == PRO_LNMIX && (!J.gamma || !J.beta || !J.prev || !J.coef))
+            return RSV_FAIL("gemv job %d: LN-mix prologue needs gamma/beta/prev/coef", i);
         if (J.K > kmax) kmax = J.K;
         const int nc = J.K / (J.fmt == FMT_I8 ? 16 : 8);
         if (nc < ncmin) ncmin = nc;
+        if (nc > ncmax) ncmax = nc;
     }
+    if (jobs.side.src && (!jobs.side.dst || jobs.side.n <= 0)) return RSV_FAIL("gemv: bad side copy");
     // Lanes per row: a full wave when rows are long, a quarter wave for the
-    // short LoRA-up rows (k = rank).
+    // short LoRA-up rows (k = rank).  Long rows (ffn.value) keep fewer rows
+    // per wave so more waves are resident.
     const bool wide = ncmin >= 128;
+    const bool long_rows = ncmax > 6 * 64;
     auto fits = [&](int bt) { return (size_t)bt * kmax * 4 * 17 / 16 <= 64 * 1024; };
     int bt = batch >= 4 ? 4 : (batch >= 2 ? 2 : 1);
     while (bt > 1 && !fits(bt)) bt >>= 1;
     if (!fits(bt)) return RSV_FAIL("gemv: k=%d too large for the LDS x stage", kmax);
     if (wide) {
-        if (bt == 4) return launch_t<64, 4, 2>(ctx, jobs, batch);
-        if (bt == 2) return launch_t<64, 2, 4>(ctx, jobs, batch);
-        return launch_t<64, 1, 4>(ctx, jobs, batch);
+        if (long_rows) {
+            if (bt == 4) return launch_t<64, 4, 1, 4, true>(ctx, jobs, batch);
+            if (bt == 2) return launch_t<64, 2, 1, 4, true>(ctx, jobs, batch);
+            return launch_t<64, 1, 1, 4, true>(ctx, jobs, batch);
+        }
+        if (bt == 4) return launch_t<64, 4, 1, 6, false>(ctx, jobs, batch);
+        if (bt == 2) return launch_t<64, 2, 2, 6, false>(ctx, jobs, batch);
+        return launch_t<64, 1, 2, 6, false>(ctx, jobs, batch);
     }
-    if (bt == 4) return launch_t<16, 4, 2>(ctx, jobs, batch);
-    if (bt == 2) return launch_t<16, 2, 2>(ctx, jobs, batch);
-    return launch_t<16, 1, 2>(ctx, jobs, batch);
+    if (bt == 4) return launch_t<16, 4, 2, 2, false>(ctx, jobs, batch);
+    if (bt == 2) return launch_t<16, 2, 2, 2, false>(ctx, jobs, batch);
+    return launch_t<16, 1, 2, 2, false>(ctx, jobs, batch);
 }
 
 // ---------------------------------------------------------------- dequant

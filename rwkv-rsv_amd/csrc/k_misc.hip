@@ -20,56 +20,80 @@ __device__ __forceinline__ float block_sum256(float v, float *red) {
 // ------------------------------------------------ LayerNorm + token shift
 // model.rs:402-411 / 487-490: ln = LN(x); out_j = ln + coef_j*(prev - ln);
 // state = ln.  grid (batch), block 256; c <= 256*kMaxPer.
-constexpr int kMaxPer = 16;
+constexpr int kMaxPer = 16;  // prefill rows: c <= 4096
 struct Ptr6 { const float *p[6]; };
 struct Out6 { float *p[6]; };
 
-__global__ __launch_bounds__(256) void k_norm_lerp(const float *__restrict__ x, float *__restrict__ state,
-                                                   const float *__restrict__ gamma, const float *__restrict__ beta,
-                                                   Ptr6 coef, Out6 out, int nout, int C, float eps) {
-    __shared__ float red[4];
+template <int NOUT>
+__global__ __launch_bounds__(1024) void k_norm_lerp(const float *__restrict__ x, float *__restrict__ state,
+                                                    const float *__restrict__ gamma, const float *__restrict__ beta,
+                                                    Ptr6 coef, Out6 out, int C, float eps) {
+    // every load is issued before the statistics are reduced
+    __shared__ float red[16];
     const int b = blockIdx.x, tid = threadIdx.x;
-    const float *xb = x + (size_t)b * C;
-    float xv[kMaxPer];
+    constexpr int PER = 4;  // C <= 4096
+    float xv[PER], gv[PER], bv[PER], pv[PER], cv[NOUT][PER];
+#pragma unroll
+    for (int m = 0; m < PER; m++) {
+        const int i = tid + 1024 * m;
+        const bool ok = i < C;
+        xv[m] = ok ? x[(size_t)b * C + i] : 0.0f;
+        gv[m] = ok ? gamma[i] : 0.0f;
+        bv[m] = ok ? beta[i] : 0.0f;
+        pv[m] = ok ? state[(size_t)b * C + i] : 0.0f;
+#pragma unroll
+        for (int j = 0; j < NOUT; j++) cv[j][m] = ok ? coef.p[j][i] : 0.0f;
+    }
     float s = 0.0f;
 #pragma unroll
-    for (int m = 0; m < kMaxPer; m++) {
-        const int i = tid + 256 * m;
-        xv[m] = i < C ? xb[i] : 0.0f;
-        s += xv[m];
-    }
-    const float mean = block_sum256(s, red) / (float)C;
+    for (int m = 0; m < PER; m++) s += xv[m];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+    if ((tid & 63) == 0) red[tid >> 6] = s;
+    __syncthreads();
+    float tot = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 16; w++) tot += red[w];
+    const float mean = tot / (float)C;
     float q = 0.0f;
 #pragma unroll
-    for (int m = 0; m < kMaxPer; m++) {
-        const int i = tid + 256 * m;
+    for (int m = 0; m < PER; m++) {
         const float d = xv[m] - mean;
-        q += i < C ? d * d : 0.0f;
+        q += (tid + 1024 * m < C) ? d * d : 0.0f;
     }
-    const float var = block_sum256(q, red) / (float)C + eps;
-    const float inv_std = 1.0f / sqrtf(var);
 #pragma unroll
-    for (int m = 0; m < kMaxPer; m++) {
-        const int i = tid + 256 * m;
-        if (i >= C) break;
-        const float ln = (xv[m] - mean) * inv_std * gamma[i] + beta[i];
+    for (int o = 32; o > 0; o >>= 1) q += __shfl_xor(q, o, 64);
+    __syncthreads();
+    if ((tid & 63) == 0) red[tid >> 6] = q;
+    __syncthreads();
+    float qt = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 16; w++) qt += red[w];
+    const float inv_std = 1.0f / sqrtf(qt / (float)C + eps);
+#pragma unroll
+    for (int m = 0; m < PER; m++) {
+        const int i = tid + 1024 * m;
+        if (i >= C) continue;
+        const float ln = (xv[m] - mean) * inv_std * gv[m] + bv[m];
         const size_t o = (size_t)b * C + i;
-        const float prev = state[o];
-        const float dlt = prev - ln;
-        for (int j = 0; j < nout; j++) out.p[j][o] = ln + coef.p[j][i] * dlt;
+        const float dlt = pv[m] - ln;
+#pragma unroll
+        for (int j = 0; j < NOUT; j++) out.p[j][o] = ln + cv[j][m] * dlt;
         state[o] = ln;
     }
 }
 
 int launch_norm_lerp(rsv_ctx *ctx, const float *x, float *state, const float *gamma, const float *beta,
                      const float *const *coef, float *const *out, int nout, int c, float eps, int batch) {
-    if (c <= 0 || c > 256 * kMaxPer) return RSV_FAIL("norm_lerp: c=%d outside 1..%d", c, 256 * kMaxPer);
-    if (nout < 1 || nout > 6) return RSV_FAIL("norm_lerp: nout=%d", nout);
+    if (c <= 0 || c > 4096) return RSV_FAIL("norm_lerp: c=%d outside 1..4096", c);
     Ptr6 cp{};
     Out6 op{};
     for (int j = 0; j < nout; j++) { cp.p[j] = coef[j]; op.p[j] = out[j]; }
-    hipLaunchKernelGGL(k_norm_lerp, dim3(batch), dim3(256), 0, ctx->stream, x, state, gamma, beta, cp, op, nout,
-                       c, eps);
+    switch (nout) {
+        case 1: hipLaunchKernelGGL(k_norm_lerp<1>, dim3(batch), dim3(1024), 0, ctx->stream, x, state, gamma, beta, cp, op, c, eps); break;
+        case 6: hipLaunchKernelGGL(k_norm_lerp<6>, dim3(batch), dim3(1024), 0, ctx->stream, x, state, gamma, beta, cp, op, c, eps); break;
+        default: return RSV_FAIL("norm_lerp: nout must be 1 or 6 (got %d)", nout);
+    }
     RSV_HIP(hipGetLastError());
     return 0;
 }
@@ -557,6 +581,90 @@ int launch_mul_to_f16(rsv_ctx *ctx, const float *a, const float *b, _Float16 *y,
     uint64_t blocks = (n + 255) / 256;
     if (blocks > 16384) blocks = 16384;
     hipLaunchKernelGGL(k_mul_to_f16, dim3((unsigned)blocks), dim3(256), 0, ctx->stream, a, b, y, n);
+    RSV_HIP(hipGetLastError());
+    return 0;
+}
+
+}  // namespace rsv
+
+namespace rsv {
+
+// LayerNorm of each batch row + up to six token-shift mixes written as fp16
+// GEMM operands (batched decode on matrix cores).  With coef[j] == null the
+// output is the plain LN row.  state (optional) is read as the previous
+// token's LN row and overwritten with this row.  Every load is issued before
+// the statistics are reduced.  grid (batch), block 1024; c <= 4096.
+template <int NOUT>
+__global__ __launch_bounds__(1024) void k_ln_mix_f16(const float *__restrict__ x, float *__restrict__ state,
+                                                     const float *__restrict__ gamma,
+                                                     const float *__restrict__ beta, Ptr6 coef, HOut6 out, int C,
+                                                     float eps) {
+    __shared__ float red[16];
+    const int b = blockIdx.x, tid = threadIdx.x;
+    constexpr int PER = 4;
+    float xv[PER], gv[PER], bv[PER], pv[PER], cv[NOUT][PER];
+#pragma unroll
+    for (int m = 0; m < PER; m++) {
+        const int i = tid + 1024 * m;
+        const bool ok = i < C;
+        xv[m] = ok ? x[(size_t)b * C + i] : 0.0f;
+        gv[m] = ok ? gamma[i] : 0.0f;
+        bv[m] = ok ? beta[i] : 0.0f;
+        pv[m] = (ok && state) ? state[(size_t)b * C + i] : 0.0f;
+#pragma unroll
+        for (int j = 0; j < NOUT; j++) cv[j][m] = (ok && coef.p[j]) ? coef.p[j][i] : 0.0f;
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int m = 0; m < PER; m++) s += xv[m];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+    if ((tid & 63) == 0) red[tid >> 6] = s;
+    __syncthreads();
+    float tot = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 16; w++) tot += red[w];
+    const float mean = tot / (float)C;
+    float q = 0.0f;
+#pragma unroll
+    for (int m = 0; m < PER; m++) {
+        const float d = xv[m] - mean;
+        q += (tid + 1024 * m < C) ? d * d : 0.0f;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) q += __shfl_xor(q, o, 64);
+    __syncthreads();
+    if ((tid & 63) == 0) red[tid >> 6] = q;
+    __syncthreads();
+    float qt = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 16; w++) qt += red[w];
+    const float inv = 1.0f / sqrtf(qt / (float)C + eps);
+#pragma unroll
+    for (int m = 0; m < PER; m++) {
+        const int i = tid + 1024 * m;
+        if (i >= C) continue;
+        const float ln = (xv[m] - mean) * inv * gv[m] + bv[m];
+        const size_t o = (size_t)b * C + i;
+#pragma unroll
+        for (int j = 0; j < NOUT; j++)
+            out.p[j][o] = (_Float16)(coef.p[j] ? ln + cv[j][m] * (pv[m] - ln) : ln);
+        if (state) state[o] = ln;
+    }
+}
+
+int launch_ln_mix_f16(rsv_ctx *ctx, const float *x, float *state, const float *gamma, const float *beta,
+                      const float *const *coef, _Float16 *const *out, int nout, int c, float eps, int batch) {
+    if (c <= 0 || c > 4096) return RSV_FAIL("ln_mix_f16: c=%d outside 1..4096", c);
+    if (batch <= 0) return 0;
+    Ptr6 cp{};
+    HOut6 op{};
+    for (int j = 0; j < nout; j++) { cp.p[j] = coef ? coef[j] : nullptr; op.p[j] = out[j]; }
+    switch (nout) {
+        case 1: hipLaunchKernelGGL(k_ln_mix_f16<1>, dim3(batch), dim3(1024), 0, ctx->stream, x, state, gamma, beta, cp, op, c, eps); break;
+        case 6: hipLaunchKernelGGL(k_ln_mix_f16<6>, dim3(batch), dim3(1024), 0, ctx->stream, x, state, gamma, beta, cp, op, c, eps); break;
+        default: return RSV_FAIL("ln_mix_f16: nout must be 1 or 6 (got %d)", nout);
+    }
     RSV_HIP(hipGetLastError());
     return 0;
 }

@@ -1,0 +1,599 @@
+// Batched decode GEMM on matrix cores ("skinny" M = sessions <= 64):
+//   y[b, n] (epilogue)= sum_k x[b, k] W[n, k]
+// W is the reference int8 format (dequantised in registers, fp32 s*q+z
+// rounded to fp16) or fp16; x is fp16 [batch, k].
+//
+// Block = 4 waves, tile = 32 weight rows x (32*MT) sessions.  The K
+// dimension is split across the 4 waves (chunk c of 32 columns goes to wave
+// c % 4) and the partial tiles are summed in LDS in a fixed order, so the
+// result is deterministic.  Each wave keeps PF chunks of loads in flight.
+//
+// v_mfma_f32_32x32x8_f16 operand layout: lane l holds A[i = l%32][4g..4g+3]
+// and B[4g..4g+3][j = l%32] with g = l/32.  A lane loads 16 consecutive
+// k-values (k0 + 16g .. +15) of its weight row and of its session's x row;
+// MFMA step s (0..3) consumes values 4s..4s+3 of both.  A and B use the same
+// k permutation, so the products pair up exactly.
+#include <cstdlib>
+
+#include "rsv_common.h"
+
+namespace rsv {
+
+typedef _Float16 sk_half4 __attribute__((ext_vector_type(4)));
+typedef float sk_f16x __attribute__((ext_vector_type(16)));
+typedef unsigned int sk_u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float sk_h2f(uint32_t b) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(b & 0xFFFFu));
+}
+__device__ __forceinline__ float sk_sig(float v) { return 1.0f / (1.0f + expf(-v)); }
+
+__device__ __forceinline__ uint32_t sk_pack(float a, float b) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)a) |
+           ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)b) << 16);
+}
+
+// One 32-column k-chunk of a wave's operands: two 32-row weight tiles and
+// MT session tiles of x.
+template <int MT>
+struct SkChunk {
+    sk_u32x4 w[2][2];  // [row tile]: int8 uses [rt][0] (16 bytes); fp16 uses both (16 halves)
+    uint32_t sz[2];
+    sk_u32x4 x[MT][2];  // [session tile][16 halves]
+};
+
+template <int MT>
+__device__ __forceinline__ void sk_load(const SkinnyJob &J, int n0, int k0, int g, int lane, int MB, bool i8,
+                                        SkChunk<MT> &ch) {
+    const int kk = k0 + 16 * g;
+#pragma unroll
+    for (int rt = 0; rt < 2; rt++) {
+        const int row = n0 + rt * 32 + (lane & 31);
+        if (row < J.N) {
+            if (i8) {
+                ch.w[rt][0] = __builtin_nontemporal_load((const sk_u32x4 *)((const uint8_t *)J.w + (size_t)row * J.K + kk));
+                ch.sz[rt] = J.sz[(size_t)row * (J.K / 128) + kk / 128];
+            } else {
+                const sk_u32x4 *p = (const sk_u32x4 *)((const _Float16 *)J.w + (size_t)row * J.K + kk);
+                ch.w[rt][0] = __builtin_nontemporal_load(p);
+                ch.w[rt][1] = __builtin_nontemporal_load(p + 1);
+            }
+        } else {
+            ch.w[rt][0] = ch.w[rt][1] = (sk_u32x4){0u, 0u, 0u, 0u};
+            ch.sz[rt] = 0u;
+        }
+    }
+#pragma unroll
+    for (int ct = 0; ct < MT; ct++) {
+        const int b = ct * 32 + (lane & 31);
+        if (b < MB) {
+            const sk_u32x4 *p = (const sk_u32x4 *)(J.x + (size_t)b * J.ldx + kk);
+            ch.x[ct][0] = p[0];
+            ch.x[ct][1] = p[1];
+        } else {
+            ch.x[ct][0] = ch.x[ct][1] = (sk_u32x4){0u, 0u, 0u, 0u};
+        }
+    }
+}
+
+template <int MT>
+__device__ __forceinline__ void sk_mma(const SkChunk<MT> &ch, bool i8, sk_f16x (&acc)[2][MT]) {
+#pragma unroll
+    for (int rt = 0; rt < 2; rt++) {
+        uint32_t wh[8];  // 16 halves
+        if (i8) {
+            const float s = sk_h2f(ch.sz[rt]), z = sk_h2f(ch.sz[rt] >> 16);
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const uint32_t w = ch.w[rt][0][q];
+                wh[2 * q] = sk_pack(fmaf(s, (float)(w & 0xFFu), z), fmaf(s, (float)((w >> 8) & 0xFFu), z));
+                wh[2 * q + 1] = sk_pack(fmaf(s, (float)((w >> 16) & 0xFFu), z), fmaf(s, (float)(w >> 24), z));
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                wh[q] = ch.w[rt][0][q];
+                wh[4 + q] = ch.w[rt][1][q];
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            const sk_half4 a = __builtin_bit_cast(sk_half4, (unsigned long long)wh[2 * s] |
+                                                                ((unsigned long long)wh[2 * s + 1] << 32));
+#pragma unroll
+            for (int ct = 0; ct < MT; ct++) {
+                const uint32_t lo = ch.x[ct][s >> 1][(s & 1) * 2], hi = ch.x[ct][s >> 1][(s & 1) * 2 + 1];
+                const sk_half4 bv =
+                    __builtin_bit_cast(sk_half4, (unsigned long long)lo | ((unsigned long long)hi << 32));
+                acc[rt][ct] = __builtin_amdgcn_mfma_f32_32x32x8f16(a, bv, acc[rt][ct], 0, 0, 0);
+            }
+        }
+    }
+}
+
+__device__ __forceinline__ float sk_epilogue(const SkinnyJob &J, float v, int n, size_t yo) {
+    const float bias = J.bias ? J.bias[n] : 0.0f;
+    switch (J.epi) {
+        case GE_BIAS: v += bias; break;
+        case GE_ADD: v += ((const float *)J.y)[yo]; break;
+        case GE_RELU2: v = v > 0.0f ? v * v : 0.0f; break;
+        case GE_TANH: v = tanhf(v); break;
+        case GE_WDECAY: v = expf(sk_sig(v + bias) * J.scale[0]); break;
+        case GE_SIGBIAS: v = sk_sig(v + bias); break;
+        case GE_VLERP: {
+            const float cur = ((const float *)J.y)[yo];
+            v = cur + sk_sig(v + bias) * (J.aux[yo] - cur);
+        } break;
+        case GE_SIGMOID: v = sk_sig(v); break;
+        default: break;
+    }
+    return v;
+}
+
+// grid: for each job, (rows/64) row groups x J.split k-slices.  Block = 4
+// waves on one row group; wave w takes k-chunks w, w+4, ... of the slice.
+// The 4 wave tiles are summed in LDS in wave order.  With split == 1 the
+// block applies the epilogue; otherwise it stores its tile to the workspace
+// and k_skinny_reduce (the next launch) sums the slices in slice order, so
+// no cross-block synchronisation is needed inside a launch.
+template <int MT>
+__global__ __launch_bounds__(256) void k_skinny(SkinnyJobs jobs, int MB, float *__restrict__ ws) {
+    constexpr int PF = 4;  // chunks in flight per wave
+    constexpr int TB = MT * 32;
+    __shared__ float tile[64][TB + 1];
+    const int bid = blockIdx.x;
+    int ji = 0;
+    while (ji + 1 < jobs.n && bid >= jobs.blk_start[ji + 1]) ji++;
+    const SkinnyJob &J = jobs.j[ji];
+    const int local = bid - jobs.blk_start[ji];
+    const int rg = local / J.split, sl = local - (local / J.split) * J.split;
+    const int n0 = rg * 64;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 5;
+    const bool i8 = J.fmt == FMT_I8;
+    const int nchunks = J.K / 32;
+    const int per = (nchunks + J.split - 1) / J.split;
+    const int c_lo = sl * per, c_hi = min(nchunks, c_lo + per);
+
+    sk_f16x acc[2][MT];
+#pragma unroll
+    for (int rt = 0; rt < 2; rt++)
+#pragma unroll
+        for (int ct = 0; ct < MT; ct++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) acc[rt][ct][e] = 0.0f;
+
+    SkChunk<MT> ring[PF];
+#pragma unroll
+    for (int p = 0; p < PF; p++) {
+        const int c = c_lo + wave + 4 * p;
+        if (c < c_hi) sk_load<MT>(J, n0, c * 32, g, lane, MB, i8, ring[p]);
+    }
+    for (int it = 0; c_lo + wave + 4 * it < c_hi; it += PF) {
+#pragma unroll
+        for (int p = 0; p < PF; p++) {
+            const int c = c_lo + wave + 4 * (it + p);
+            if (c < c_hi) {
+                sk_mma<MT>(ring[p], i8, acc);
+                const int cn = c + 4 * PF;
+                if (cn < c_hi) sk_load<MT>(J, n0, cn * 32, g, lane, MB, i8, ring[p]);
+            }
+        }
+    }
+
+    // wave tiles -> LDS in wave order; acc[rt][ct][e] is (row rt*32 + 8*(e/4) + 4g + e%4, col ct*32 + lane%32)
+    for (int w = 0; w < 4; w++) {
+        if (wave == w) {
+#pragma unroll
+            for (int rt = 0; rt < 2; rt++)
+#pragma unroll
+                for (int ct = 0; ct < MT; ct++)
+#pragma unroll
+                    for (int e = 0; e < 16; e++) {
+                        float &d = tile[rt * 32 + 8 * (e >> 2) + 4 * g + (e & 3)][ct * 32 + (lane & 31)];
+                        d = w == 0 ? acc[rt][ct][e] : d + acc[rt][ct][e];
+                    }
+        }
+        __syncthreads();
+    }
+    if (J.split > 1) {
+        // slice tile, row-group-major then slice: [rg][sl][64 rows][TB sessions]
+        float *wsp = ws + ((size_t)J.ws_slot + (size_t)rg * J.split + sl) * 64 * TB;
+        for (int o = tid; o < 64 * TB; o += 256) wsp[o] = tile[o & 63][o >> 6];
+        return;
+    }
+    for (int o = tid; o < 64 * TB; o += 256) {
+        const int r = o & 63, b = o >> 6;  // consecutive threads: consecutive weight rows n
+        const int n = n0 + r;
+        if (n >= J.N || b >= MB) continue;
+        const size_t yo = (size_t)b * J.ldy + n;
+        const float v = sk_epilogue(J, tile[r][b], n, yo);
+        if (J.y_f16)
+            ((_Float16 *)J.y)[yo] = (_Float16)v;
+        else
+            ((float *)J.y)[yo] = v;
+        if (J.y2) J.y2[yo] = v;
+    }
+}
+
+// Sums the k-slices of every split job in slice order and applies the
+// epilogue.  grid: one block per (job, row group); jobs with split == 1
+// were finished by k_skinny and have no blocks here.
+template <int MT>
+__global__ __launch_bounds__(256) void k_skinny_reduce(SkinnyJobs jobs, int MB, const float *__restrict__ ws) {
+    constexpr int TB = MT * 32;
+    const int bid = blockIdx.x;
+    int ji = 0;
+    while (ji + 1 < jobs.n && bid >= jobs.red_start[ji + 1]) ji++;
+    const SkinnyJob &J = jobs.j[ji];
+    constexpr int PB = 64 * TB / 256;  // blocks per row group: one output per thread
+    const int rg = (bid - jobs.red_start[ji]) / PB, part = (bid - jobs.red_start[ji]) % PB;
+    const float *base = ws + ((size_t)J.ws_slot + (size_t)rg * J.split) * 64 * TB;
+    {
+        const int o = part * 256 + threadIdx.x;
+        const int r = o & 63, b = o >> 6;
+        const int n = rg * 64 + r;
+        if (n >= J.N || b >= MB) return;
+        float v = base[o];
+        for (int q = 1; q < J.split; q++) v += base[(size_t)q * 64 * TB + o];
+        const size_t yo = (size_t)b * J.ldy + n;
+        v = sk_epilogue(J, v, n, yo);
+        if (J.y_f16)
+            ((_Float16 *)J.y)[yo] = (_Float16)v;
+        else
+            ((float *)J.y)[yo] = v;
+        if (J.y2) J.y2[yo] = v;
+    }
+}
+
+// ------------------------------------------------------------------ v4
+// Same contract with the weights in the MFMA-tiled copy made by
+// launch_tile_weights: a 32-row x 32-column tile is 1 KiB (int8) / 2 KiB
+// (fp16) contiguous, lane l's 16 (32) bytes = row l%32, columns
+// 16*(l/32) .. +15, tiles ordered [row tile][k chunk].  A wave's weight load
+// is one fully contiguous 1 KiB burst per chunk.
+//
+// Block = 4 waves = 4 row tiles (128 rows) on one k-slice; the x slab of a
+// 4-chunk group (batch x 128 columns, fp16) is staged once per block in LDS
+// (double buffered) and shared by the 4 waves.
+template <int MT, bool I8>
+__global__ __launch_bounds__(256) void k_skinny4(SkinnyJobs jobs, int MB, float *__restrict__ ws) {
+    constexpr int TB = MT * 32;
+    constexpr int G = 4;              // chunks per group
+    constexpr int D = I8 ? 3 : 2;     // weight groups in flight per wave
+    constexpr int WV = I8 ? 1 : 2;    // 16-byte loads per lane per chunk
+    constexpr int XS = G * 32 + 8;    // LDS row stride (halves) of the x slab
+    // the x slab double buffer and the output tile are never live together
+    __shared__ __attribute__((aligned(16))) unsigned char smem[2 * TB * XS * 2 > 128 * (TB + 1) * 4
+                                                                  ? 2 * TB * XS * 2 : 128 * (TB + 1) * 4];
+    _Float16 (*xs)[TB][XS] = reinterpret_cast<_Float16 (*)[TB][XS]>(smem);
+    float (*tile)[TB + 1] = reinterpret_cast<float (*)[TB + 1]>(smem);
+    const int bid = blockIdx.x;
+    int ji = 0;
+    while (ji + 1 < jobs.n && bid >= jobs.blk_start[ji + 1]) ji++;
+    const SkinnyJob &J = jobs.j[ji];
+    const int local = bid - jobs.blk_start[ji];
+    const int rg = local / J.split, sl = local - (local / J.split) * J.split;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 5;
+    const int nchunks = J.K / 32;
+    const int ngroups = (nchunks + G - 1) / G;
+    const int per = (ngroups + J.split - 1) / J.split;
+    const int g_lo = sl * per, g_hi = min(ngroups, g_lo + per);
+    const int rt_glob = rg * 4 + wave;  // this wave's row tile
+    const int row = rt_glob * 32 + (lane & 31);
+    constexpr int tbytes = I8 ? 1024 : 2048;
+    const uint8_t *wt = (const uint8_t *)J.w + ((size_t)rt_glob * nchunks) * tbytes + lane * (I8 ? 16 : 32);
+    const bool row_ok = row < J.N;
+    const uint32_t *szrow = I8 ? J.sz + (size_t)(row_ok ? row : 0) * (J.K / 128) : nullptr;
+
+    sk_f16x acc[MT];
+#pragma unroll
+    for (int ct = 0; ct < MT; ct++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) acc[ct][e] = 0.0f;
+
+    sk_u32x4 wr[D][G][WV];
+    uint32_t sr[D][G];
+    sk_u32x4 xr[4];  // x staging: thread t -> session t/4, 32 halves at (t%4)*32
+    const int xb = tid >> 2, xk = (tid & 3) * 32;
+
+    auto load_w = [&](int grp, sk_u32x4 (&w)[G][WV], uint32_t (&sz)[G]) {
+#pragma unroll
+        for (int q = 0; q < G; q++) {
+            const int c = grp * G + q;
+            if (grp < g_hi && c < nchunks && row_ok) {
+                const sk_u32x4 *p = (const sk_u32x4 *)(wt + (size_t)c * tbytes);
+#pragma unroll
+                for (int v = 0; v < WV; v++) w[q][v] = __builtin_nontemporal_load(p + v);
+                if (I8) sz[q] = szrow[(c * 32) / 128];
+            } else {
+#pragma unroll
+                for (int v = 0; v < WV; v++) w[q][v] = (sk_u32x4){0u, 0u, 0u, 0u};
+                sz[q] = 0u;
+            }
+        }
+    };
+    auto load_x = [&](int grp) {
+        const int k0 = grp * G * 32 + xk;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            if (xb < MB && k0 + 8 * q < J.K)
+                xr[q] = *(const sk_u32x4 *)(J.x + (size_t)xb * J.ldx + k0 + 8 * q);
+            else
+                xr[q] = (sk_u32x4){0u, 0u, 0u, 0u};
+        }
+    };
+    auto store_x = [&](int buf) {
+        if (xb < TB) {
+#pragma unroll
+            for (int q = 0; q < 4; q++) *(sk_u32x4 *)&xs[buf][xb][xk + 8 * q] = xr[q];
+        }
+    };
+    auto compute = [&](const sk_u32x4 (&w)[G][WV], const uint32_t (&sz)[G], int buf) {
+#pragma unroll
+        for (int q = 0; q < G; q++) {
+            uint32_t wh[8];
+            if (I8) {
+                const float s = sk_h2f(sz[q]), z = sk_h2f(sz[q] >> 16);
+#pragma unroll
+                for (int h = 0; h < 4; h++) {
+                    const uint32_t u = w[q][0][h];
+                    wh[2 * h] = sk_pack(fmaf(s, (float)(u & 0xFFu), z), fmaf(s, (float)((u >> 8) & 0xFFu), z));
+                    wh[2 * h + 1] = sk_pack(fmaf(s, (float)((u >> 16) & 0xFFu), z), fmaf(s, (float)(u >> 24), z));
+                }
+            } else {
+#pragma unroll
+                for (int h = 0; h < 4; h++) {
+                    wh[h] = w[q][0][h];
+                    wh[4 + h] = w[q][WV - 1][h];
+                }
+            }
+#pragma unroll
+            for (int ct = 0; ct < MT; ct++) {
+                const _Float16 *xp = &xs[buf][ct * 32 + (lane & 31)][q * 32 + 16 * g];
+                const sk_u32x4 x0 = *(const sk_u32x4 *)xp, x1 = *(const sk_u32x4 *)(xp + 8);
+#pragma unroll
+                for (int s2 = 0; s2 < 4; s2++) {
+                    const sk_half4 a = __builtin_bit_cast(sk_half4, (unsigned long long)wh[2 * s2] |
+                                                                        ((unsigned long long)wh[2 * s2 + 1] << 32));
+                    const sk_u32x4 &xx = s2 < 2 ? x0 : x1;
+                    const uint32_t lo = xx[(s2 & 1) * 2], hi = xx[(s2 & 1) * 2 + 1];
+                    const sk_half4 bv =
+                        __builtin_bit_cast(sk_half4, (unsigned long long)lo | ((unsigned long long)hi << 32));
+                    acc[ct] = __builtin_amdgcn_mfma_f32_32x32x8f16(a, bv, acc[ct], 0, 0, 0);
+                }
+            }
+        }
+    };
+
+#pragma unroll
+    for (int d = 0; d < D; d++) load_w(g_lo + d, wr[d], sr[d]);
+    if (g_lo < g_hi) {
+        load_x(g_lo);
+        store_x(0);
+    }
+    __syncthreads();
+    for (int base = g_lo; base < g_hi; base += D) {
+#pragma unroll
+        for (int d = 0; d < D; d++) {
+            const int grp = base + d;
+            if (grp < g_hi) {  // uniform across the block
+                const int buf = (grp - g_lo) & 1;
+                const bool more = grp + 1 < g_hi;
+                if (more) load_x(grp + 1);
+                compute(wr[d], sr[d], buf);
+                load_w(grp + D, wr[d], sr[d]);
+                if (more) store_x(buf ^ 1);
+                __syncthreads();
+            }
+        }
+    }
+
+    // wave w owns tile rows 32w .. 32w+31: acc[ct][e] -> (row 32w + 8*(e/4) + 4g + e%4, col ct*32 + lane%32)
+#pragma unroll
+    for (int ct = 0; ct < MT; ct++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) tile[wave * 32 + 8 * (e >> 2) + 4 * g + (e & 3)][ct * 32 + (lane & 31)] = acc[ct][e];
+    __syncthreads();
+    const int n0 = rg * 128;
+    if (J.split > 1) {
+        float *wsp = ws + ((size_t)J.ws_slot + (size_t)rg * J.split + sl) * 128 * TB;
+        for (int o = tid; o < 128 * TB; o += 256) wsp[o] = tile[o & 127][o >> 7];
+        return;
+    }
+    for (int o = tid; o < 128 * TB; o += 256) {
+        const int r = o & 127, b = o >> 7;
+        const int n = n0 + r;
+        if (n >= J.N || b >= MB) continue;
+        const size_t yo = (size_t)b * J.ldy + n;
+        const float v = sk_epilogue(J, tile[r][b], n, yo);
+        if (J.y_f16)
+            ((_Float16 *)J.y)[yo] = (_Float16)v;
+        else
+            ((float *)J.y)[yo] = v;
+        if (J.y2) J.y2[yo] = v;
+    }
+}
+
+template <int MT>
+__global__ __launch_bounds__(256) void k_skinny4_reduce(SkinnyJobs jobs, int MB, const float *__restrict__ ws) {
+    constexpr int TB = MT * 32;
+    const int bid = blockIdx.x;
+    int ji = 0;
+    while (ji + 1 < jobs.n && bid >= jobs.red_start[ji + 1]) ji++;
+    const SkinnyJob &J = jobs.j[ji];
+    constexpr int PB = 128 * TB / 256;  // blocks per row group: one output per thread
+    const int rg = (bid - jobs.red_start[ji]) / PB, part = (bid - jobs.red_start[ji]) % PB;
+    const float *base = ws + ((size_t)J.ws_slot + (size_t)rg * J.split) * 128 * TB;
+    {
+        const int o = part * 256 + threadIdx.x;
+        const int r = o & 127, b = o >> 7;
+        const int n = rg * 128 + r;
+        if (n >= J.N || b >= MB) return;
+        float v = base[o];
+        for (int q = 1; q < J.split; q++) v += base[(size_t)q * 128 * TB + o];
+        const size_t yo = (size_t)b * J.ldy + n;
+        v = sk_epilogue(J, v, n, yo);
+        if (J.y_f16)
+            ((_Float16 *)J.y)[yo] = (_Float16)v;
+        else
+            ((float *)J.y)[yo] = v;
+        if (J.y2) J.y2[yo] = v;
+    }
+}
+
+// Tiled copy of a weight matrix [n, k] (int8 bytes or fp16) for k_skinny4;
+// rows beyond n (up to the next multiple of 32) are zero.  One thread per
+// 16-byte lane slice.
+__global__ void k_tile_weights(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst, int n, int k, int esz) {
+    const int nchunks = k / 32;
+    const int lane_bytes = 16 * esz;
+    const size_t total = (size_t)((n + 31) / 32) * nchunks * 64;
+    for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (size_t)gridDim.x * blockDim.x) {
+        const int lane = (int)(e % 64);
+        const size_t t = e / 64;
+        const int c = (int)(t % nchunks), rt = (int)(t / nchunks);
+        const int row = rt * 32 + (lane & 31);
+        const int col = c * 32 + 16 * (lane >> 5);
+        uint8_t *d = dst + e * lane_bytes;
+        if (row < n) {
+            const uint8_t *s = src + ((size_t)row * k + col) * esz;
+            for (int i = 0; i < lane_bytes; i++) d[i] = s[i];
+        } else {
+            for (int i = 0; i < lane_bytes; i++) d[i] = 0;
+        }
+    }
+}
+
+int launch_tile_weights(rsv_ctx *ctx, const void *src, void *dst, int n, int k, int esz) {
+    if (k % 32 != 0) return RSV_FAIL("tile_weights: k=%d must be a multiple of 32", k);
+    const size_t total = (size_t)((n + 31) / 32) * (k / 32) * 64;
+    size_t blocks = (total + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL(k_tile_weights, dim3((unsigned)blocks), dim3(256), 0, ctx->stream, (const uint8_t *)src,
+                       (uint8_t *)dst, n, k, esz);
+    RSV_HIP(hipGetLastError());
+    return 0;
+}
+
+static int launch_slab(rsv_ctx *ctx, SkinnyJobs &jobs, int MB);
+
+// Batches above 64 run as consecutive 64-row slabs; tiled jobs of the two
+// weight formats run as separate launches (per-format register budgets).
+int launch_skinny(rsv_ctx *ctx, SkinnyJobs &jobs, int MB) {
+    if (MB <= 0) return RSV_FAIL("skinny gemm: batch %d", MB);
+    if (jobs.n > 0 && jobs.j[0].tiled) {
+        SkinnyJobs parts[2]{};
+        for (int i = 0; i < jobs.n; i++) {
+            SkinnyJobs &p = parts[jobs.j[i].fmt == FMT_I8 ? 0 : 1];
+            p.j[p.n++] = jobs.j[i];
+        }
+        if (parts[0].n && parts[1].n) {
+            for (auto &p : parts)
+                if (launch_skinny(ctx, p, MB)) return -1;
+            return 0;
+        }
+    }
+    for (int s0 = 0; s0 < MB; s0 += 64) {
+        SkinnyJobs sl = jobs;
+        for (int i = 0; i < sl.n; i++) {
+            SkinnyJob &J = sl.j[i];
+            J.x += (size_t)s0 * J.ldx;
+            J.y = J.y_f16 ? (void *)((_Float16 *)J.y + (size_t)s0 * J.ldy) : (void *)((float *)J.y + (size_t)s0 * J.ldy);
+            if (J.y2) J.y2 += (size_t)s0 * J.ldy;
+            if (J.aux) J.aux += (size_t)s0 * J.ldy;
+        }
+        if (launch_slab(ctx, sl, MB - s0 < 64 ? MB - s0 : 64)) return -1;
+    }
+    return 0;
+}
+
+static int launch_slab(rsv_ctx *ctx, SkinnyJobs &jobs, int MB) {
+    if (MB <= 0 || MB > 64) return RSV_FAIL("skinny gemm: batch %d outside 1..64", MB);
+    if (jobs.n <= 0 || jobs.n > kMaxJobs) return RSV_FAIL("skinny gemm: bad job count %d", jobs.n);
+    static const int max_split = [] {
+        const char *e = getenv("RSV_SKINNY_MAX_SPLIT");
+        return e ? atoi(e) : 16;
+    }();
+    const int TB = MB <= 32 ? 32 : 64;
+    int total = 0, red_total = 0;
+    size_t ws_need = 0;
+    for (int i = 0; i < jobs.n; i++) {
+        SkinnyJob &J = jobs.j[i];
+        if (!J.w || !J.x || !J.y) return RSV_FAIL("skinny job %d: null operand", i);
+        if (J.N <= 0 || J.K <= 0 || J.K % 32 != 0) return RSV_FAIL("skinny job %d: k=%d must be a multiple of 32", i, J.K);
+        if (J.fmt == FMT_I8 && (J.K % 128 != 0 || !J.sz)) return RSV_FAIL("skinny job %d: int8 needs k %% 128 == 0", i);
+        if (J.ldx % 8 != 0 || J.ldx < J.K) return RSV_FAIL("skinny job %d: bad ldx %d", i, J.ldx);
+        if ((J.epi == GE_BIAS || J.epi == GE_WDECAY || J.epi == GE_SIGBIAS || J.epi == GE_VLERP) && !J.bias)
+            return RSV_FAIL("skinny job %d: epilogue needs bias", i);
+        if (J.epi == GE_VLERP && !J.aux) return RSV_FAIL("skinny job %d: v-lerp needs aux", i);
+        if (J.epi == GE_WDECAY && !J.scale) return RSV_FAIL("skinny job %d: decay needs scale", i);
+        if (J.y_f16 && (J.epi == GE_ADD || J.epi == GE_VLERP)) return RSV_FAIL("skinny job %d: in-place needs fp32 y", i);
+        if (J.tiled != jobs.j[0].tiled) return RSV_FAIL("skinny gemm: jobs mix tiled and row-major weights");
+        const int rows_per_block = J.tiled ? 128 : 64;
+        const int rgs = (J.N + rows_per_block - 1) / rows_per_block;
+        const int nchunks = J.K / 32;
+        int split = 1;
+        if (J.tiled) {
+            // k-slices of whole 4-chunk groups: aim for ~2 blocks per CU with
+            // at least 2 groups per slice
+            const int ngroups = (nchunks + 3) / 4;
+            while (split < max_split && ngroups >= (split + 1) * 2 && rgs * (split + 1) <= 512) split++;
+        } else {
+            // each wave streams at most ~8 chunks (256 columns)
+            while (split < max_split && nchunks > split * 4 * 8 && rgs * split * 2 <= 1024) split++;
+        }
+        J.split = split;
+        J.ws_slot = (int)(ws_need / ((J.tiled ? 128 : 64) * TB));
+        J.nblk = rgs * split;
+        jobs.blk_start[i] = total;
+        total += J.nblk;
+        jobs.red_start[i] = red_total;
+        if (split > 1) {
+            ws_need += (size_t)rgs * split * rows_per_block * TB;
+            red_total += rgs * (rows_per_block * TB / 256);
+        }
+    }
+    jobs.blk_start[jobs.n] = total;
+    jobs.red_start[jobs.n] = red_total;
+    if (ws_need > ctx->skinny_ws_cap) return RSV_FAIL("skinny gemm: workspace too small (%zu floats)", ws_need);
+    const bool tiled = jobs.j[0].tiled;
+    if (tiled) {
+        const bool i8 = jobs.j[0].fmt == FMT_I8;
+        for (int i = 1; i < jobs.n; i++)
+            if ((jobs.j[i].fmt == FMT_I8) != i8) return RSV_FAIL("skinny gemm: mixed formats in one tiled launch");
+        if (MB <= 32) {
+            if (i8) hipLaunchKernelGGL((k_skinny4<1, true>), dim3(total), dim3(256), 0, ctx->stream, jobs, MB, ctx->skinny_ws);
+            else hipLaunchKernelGGL((k_skinny4<1, false>), dim3(total), dim3(256), 0, ctx->stream, jobs, MB, ctx->skinny_ws);
+        } else {
+            if (i8) hipLaunchKernelGGL((k_skinny4<2, true>), dim3(total), dim3(256), 0, ctx->stream, jobs, MB, ctx->skinny_ws);
+            else hipLaunchKernelGGL((k_skinny4<2, false>), dim3(total), dim3(256), 0, ctx->stream, jobs, MB, ctx->skinny_ws);
+        }
+    } else {
+        if (MB <= 32)
+            hipLaunchKernelGGL(k_skinny<1>, dim3(total), dim3(256), 0, ctx->stream, jobs, MB, ctx->skinny_ws);
+        else
+            hipLaunchKernelGGL(k_skinny<2>, dim3(total), dim3(256), 0, ctx->stream, jobs, MB, ctx->skinny_ws);
+    }
+    RSV_HIP(hipGetLastError());
+    if (red_total) {
+        if (tiled) {
+            if (MB <= 32)
+                hipLaunchKernelGGL(k_skinny4_reduce<1>, dim3(red_total), dim3(256), 0, ctx->stream, jobs, MB,
+                                   ctx->skinny_ws);
+            else
+                hipLaunchKernelGGL(k_skinny4_reduce<2>, dim3(red_total), dim3(256), 0, ctx->stream, jobs, MB,
+                                   ctx->skinny_ws);
+        } else {
+            if (MB <= 32)
+                hipLaunchKernelGGL(k_skinny_reduce<1>, dim3(red_total), dim3(256), 0, ctx->stream, jobs, MB,
+                                   ctx->skinny_ws);
+            else
+                hipLaunchKernelGGL(k_skinny_reduce<2>, dim3(red_total), dim3(256), 0, ctx->stream, jobs, MB,
+                                   ctx->skinny_ws);
+        }
+        RSV_HIP(hipGetLastError());
+    }
+    return 0;
+}
+
+}  // namespace rsv

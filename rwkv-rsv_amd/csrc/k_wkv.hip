@@ -80,7 +80,8 @@ __global__ __launch_bounds__(64) void k_wkv7_decode(float *__restrict__ S, const
                                                     const float *__restrict__ beta,
                                                     const float *__restrict__ rk, float *__restrict__ kmod_out,
                                                     float *__restrict__ y_out, float *__restrict__ yn_out,
-                                                    int H, float eps, float gn_eps) {
+                                                    int H, float eps, float gn_eps,
+                                                    const float *__restrict__ gmul, _Float16 *__restrict__ yg16) {
     __shared__ float tile[64 * 65];
     __shared__ HeadVecs hv;
     const int h = blockIdx.x, b = blockIdx.y, i = threadIdx.x;
@@ -117,7 +118,8 @@ __global__ __launch_bounds__(64) void k_wkv7_decode(float *__restrict__ S, const
     for (int j = 0; j < 64; j++) tile[i * 65 + j] = s[j];
     const float yn = head_norm(y, gamma[h * 64 + i], beta[h * 64 + i], ri * kmod * rk[h * 64 + i], vi_own, gn_eps);
     if (y_out) y_out[vo + i] = y;
-    yn_out[vo + i] = yn;
+    if (yn_out) yn_out[vo + i] = yn;
+    if (yg16) yg16[vo + i] = (_Float16)(yn * gmul[vo + i]);  // att.output operand (y_norm * g)
     __syncthreads();
 #pragma unroll
     for (int m = 0; m < 16; m++) {
@@ -130,11 +132,14 @@ __global__ __launch_bounds__(64) void k_wkv7_decode(float *__restrict__ S, const
 int launch_wkv7_decode(rsv_ctx *ctx, float *s, const float *k, const float *kk, const float *a,
                        const float *ka, const float *r, const float *v, const float *w,
                        const float *gamma, const float *beta, const float *rk, float *kmod, float *y,
-                       float *yn, int h, int n, float eps, float gn_eps, int batch) {
+                       float *yn, int h, int n, float eps, float gn_eps, int batch, const float *gmul,
+                       _Float16 *yg16) {
     if (n != 64) return RSV_FAIL("wkv7: head_size must be 64 (got %d)", n);
     if (h <= 0 || batch <= 0) return RSV_FAIL("wkv7: bad h=%d batch=%d", h, batch);
+    if ((yg16 != nullptr) != (gmul != nullptr)) return RSV_FAIL("wkv7: y*g output needs g");
+    if (!yn && !yg16) return RSV_FAIL("wkv7: no output");
     hipLaunchKernelGGL(k_wkv7_decode, dim3(h, batch), dim3(64), 0, ctx->stream, s, k, kk, a, ka, r, v, w,
-                       gamma, beta, rk, kmod, y, yn, h, eps, gn_eps);
+                       gamma, beta, rk, kmod, y, yn, h, eps, gn_eps, gmul, yg16);
     RSV_HIP(hipGetLastError());
     return 0;
 }

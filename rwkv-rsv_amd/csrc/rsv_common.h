@@ -36,7 +36,12 @@ inline size_t dtype_size(int dt) { return dt == RSV_F16 ? 2 : 4; }
 // Kernel-side view of a GEMV job (one weight matrix times a batch of inputs
 // with a fused prologue on x and a fused epilogue on y).
 enum GemvFmt { FMT_I8 = 0, FMT_F16 = 1 };
-enum GemvPro { PRO_NONE = 0, PRO_MUL = 1, PRO_SIGMOID = 2 };
+enum GemvPro {
+    PRO_NONE = 0,
+    PRO_MUL = 1,      // x * xmul
+    PRO_SIGMOID = 2,  // sigmoid(x)
+    PRO_LNMIX = 3,    // ln = LN(x)*gamma+beta; ln + coef*(prev - ln)   (LN over the K columns)
+};
 enum GemvEpi {
     EPI_STORE = 0,    // y = acc
     EPI_RELU2 = 1,    // y = relu(acc)^2
@@ -45,6 +50,7 @@ enum GemvEpi {
     EPI_WDECAY = 4,   // y = exp(scale * sigmoid(acc + p0))
     EPI_SIGBIAS = 5,  // y = sigmoid(acc + p0)
     EPI_VLERP = 6,    // y = y + sigmoid(acc + p0) * (p1 - y)
+    EPI_STORE2 = 7,   // y = acc and p1 = acc (v_first snapshot)
 };
 
 struct GemvJob {
@@ -56,16 +62,29 @@ struct GemvJob {
     const float *p0;
     const float *p1;
     const float *scale;  // device scalar (EPI_WDECAY)
+    // PRO_LNMIX operands: gamma/beta [K], prev [batch, K] (token-shift state),
+    // coef [K]; lnout [batch, K] receives the plain LN rows when non-null
+    const float *gamma, *beta, *prev, *coef;
+    float *lnout;
     int M, K;
     int fmt, epi, pro;
     int ldx, ldy;  // batch strides in elements
     int nblk;      // blocks along M (filled by the launcher)
 };
 constexpr int kMaxJobs = 8;
+// A side copy done by the first block column of a launch: dst[b, :n] =
+// src[b, :n] for the launch's batch rows (moves a token-shift LN row from a
+// scratch buffer into the state once no block of the launch reads it).
+struct SideCopy {
+    const float *src;
+    float *dst;
+    int n;
+};
 struct GemvJobs {
     GemvJob j[kMaxJobs];
     int n;
     int blk_start[kMaxJobs + 1];
+    SideCopy side;
 };
 
 }  // namespace rsv
@@ -88,6 +107,10 @@ struct rsv_ctx {
     float *sample_work = nullptr;
     uint64_t sample_work_cap = 0;
     int sm_count = 0;
+    // split-K workspace of the batched-decode GEMM (fixed size, allocated
+    // with the context so that graph capture never allocates)
+    float *skinny_ws = nullptr;
+    size_t skinny_ws_cap = 0;
 };
 
 namespace rsv {
@@ -107,7 +130,8 @@ int launch_norm(rsv_ctx *ctx, const float *x, const float *gamma, const float *b
 int launch_wkv7_decode(rsv_ctx *ctx, float *s, const float *k, const float *kk, const float *a,
                        const float *ka, const float *r, const float *v, const float *w,
                        const float *gamma, const float *beta, const float *rk, float *kmod, float *y,
-                       float *yn, int h, int n, float eps, float gn_eps, int batch);
+                       float *yn, int h, int n, float eps, float gn_eps, int batch,
+                       const float *gmul = nullptr, _Float16 *yg16 = nullptr);
 int launch_gather_rows(rsv_ctx *ctx, const void *src, int src_f16, uint64_t src_rows, float *dst,
                        const uint32_t *tok, int c, int batch);
 int launch_argmax(rsv_ctx *ctx, const float *logits, uint32_t *tok, int n, int batch);
@@ -167,6 +191,32 @@ struct GemmArgs {
     int epi, b_i8, c_f16;
 };
 int launch_gemm(rsv_ctx *ctx, const GemmArgs &g);
+// Batched-decode GEMM on matrix cores (see k_skinny.hip); epilogue codes are GemmEpi.
+struct SkinnyJob {
+    const void *w;
+    const uint32_t *sz;
+    int fmt;
+    const _Float16 *x;  // [batch, K] fp16, row stride ldx
+    int ldx;
+    void *y;            // [batch, N] fp32 or fp16, row stride ldy
+    int ldy, y_f16;
+    float *y2;          // optional fp32 copy of the result
+    const float *bias, *aux, *scale;
+    int N, K, epi, nblk;
+    int split, ws_off, ws_slot;  // k-slices per row group; (unused); first workspace tile
+    int tiled;                   // weights are the MFMA-tiled copy
+};
+struct SkinnyJobs {
+    SkinnyJob j[kMaxJobs];
+    int n;
+    int blk_start[kMaxJobs + 1];
+    int red_start[kMaxJobs + 1];  // blocks of the slice-reduction launch
+};
+int launch_skinny(rsv_ctx *ctx, SkinnyJobs &jobs, int MB);
+int launch_tile_weights(rsv_ctx *ctx, const void *src, void *dst, int n, int k, int esz);
+// LayerNorm rows + up to 6 token-shift mixes, fp16 outputs (state optional).
+int launch_ln_mix_f16(rsv_ctx *ctx, const float *x, float *state, const float *gamma, const float *beta,
+                      const float *const *coef, _Float16 *const *out, int nout, int c, float eps, int batch);
 int launch_seq_norm_mix(rsv_ctx *ctx, const float *x, const float *state, const float *gamma, const float *beta,
                         const float *const *coef, _Float16 *const *out, int nout, const uint32_t *row_prev, int t,
                         int c, uint64_t slots, float eps);

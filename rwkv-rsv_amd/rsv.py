@@ -43,6 +43,24 @@ class Int8Handle(ctypes.Structure):
     _fields_ = [("idx", ctypes.c_uint32), ("sz", ctypes.c_uint32), ("m", ctypes.c_uint64), ("k", ctypes.c_uint64)]
 
 
+class GemvJob(ctypes.Structure):
+    """rsv_gemv_job (include/rsv_hip.h)."""
+    _fields_ = [("w16", ctypes.c_uint32), ("w8", ctypes.POINTER(Int8Handle)), ("m", ctypes.c_uint64),
+                ("k", ctypes.c_uint64), ("x", ctypes.c_uint32), ("y", ctypes.c_uint32), ("prologue", ctypes.c_int),
+                ("epilogue", ctypes.c_int), ("xmul", ctypes.c_uint32), ("p0", ctypes.c_uint32),
+                ("p1", ctypes.c_uint32), ("scale", ctypes.c_uint32), ("gamma", ctypes.c_uint32),
+                ("beta", ctypes.c_uint32), ("prev", ctypes.c_uint32), ("coef", ctypes.c_uint32),
+                ("lnout", ctypes.c_uint32)]
+
+
+class MmJob(ctypes.Structure):
+    """rsv_mm_job (include/rsv_hip.h)."""
+    _fields_ = [("w16", ctypes.c_uint32), ("w8", ctypes.POINTER(Int8Handle)), ("n", ctypes.c_uint64),
+                ("k", ctypes.c_uint64), ("x", ctypes.c_uint32), ("y", ctypes.c_uint32), ("y2", ctypes.c_uint32),
+                ("epilogue", ctypes.c_int), ("bias", ctypes.c_uint32), ("aux", ctypes.c_uint32),
+                ("scale", ctypes.c_uint32), ("tiled", ctypes.c_int)]
+
+
 def _ctype(decl):
     d = decl.replace("const", "").strip()
     ptr = d.count("*")
@@ -57,7 +75,7 @@ def _ctype(decl):
         return ctypes.c_char_p
     if base == "rsv_int8":
         return ctypes.POINTER(Int8Handle)
-    if base in ("rsv_model_info", "rsv_sampler_params"):
+    if base in ("rsv_model_info", "rsv_sampler_params", "rsv_gemv_job", "rsv_mm_job"):
         return ctypes.c_void_p
     return ctypes.POINTER(scalars[base])
 

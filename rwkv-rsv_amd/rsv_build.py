@@ -17,7 +17,8 @@ ARCH = "gfx950"
 COMMON = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-I", INC, "-I", CSRC,
           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-Wno-unused-result", "-Wno-unused-value"]
 
-BACKEND_SRCS = ["backend.cpp", "k_gemv.hip", "k_wkv.hip", "k_misc.hip", "k_sample.hip", "k_gemm.hip"]
+BACKEND_SRCS = ["backend.cpp", "k_gemv.hip", "k_wkv.hip", "k_misc.hip", "k_sample.hip", "k_gemm.hip",
+                "k_skinny.hip"]
 HOST_SRCS = ["host.cpp"]
 
 

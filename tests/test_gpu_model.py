@@ -241,3 +241,57 @@ def test_config1_golden(tiny_cfg1):
     ref = np.load(os.path.join(gdir, "config1_prompt_logits.npy")).astype(np.float32)
     assert rel_rmse(lg, ref) <= RMSE_BOUND
     b.close()
+
+
+@pytest.mark.parametrize("kind", ["f32", "i8"])
+def test_fused_decode_matches_trait_op_sequence(bundles, kind, monkeypatch):
+    """The six-launch fused layer equals the reference's one-op-per-method
+    sequence (norm_lerp6, stage1, chain4, fuse_ka_dplr_norm, ...)."""
+    b, _ = bundles[kind]
+    p = _prompt(10, 30)
+    b.reset()
+    fused = [b.infer_tokens([t]) for t in p]
+    s_fused = b.state_back()
+    monkeypatch.setenv("RSV_DECODE_TRAIT_OPS", "1")
+    b.reset()
+    ops = [b.infer_tokens([t]) for t in p]
+    s_ops = b.state_back()
+    monkeypatch.delenv("RSV_DECODE_TRAIT_OPS")
+    for a, c in zip(fused, ops):
+        assert rel_rmse(a, c) <= 1e-5
+    assert rel_rmse(s_fused, s_ops) <= 1e-5
+
+
+@pytest.mark.parametrize("kind,bar", [("f32", 0.98), ("i8", 0.98)])
+def test_batch_matrix_core_decode(bundles, kind, bar):
+    """B >= 16 runs the decode GEMMs on MFMA with fp16 activations: logits and
+    states meet the RMSE bound against the oracle, and the batched argmax
+    self-loop agrees teacher-forced with the oracle."""
+    b, m = bundles[kind]
+    B = 20
+    S = b.create_batch_state(B)
+    prompts = [_prompt(3 + (i % 5), 40 + i) for i in range(B)]
+    seeds = b.forward_seq_batch(S, prompts)
+    snap = S.back()
+    toks = np.array([(7 * i + 3) % SMALL["vocab"] for i in range(B)], np.uint32)
+    lg = b.forward_tokens_batch(S, toks)
+    for i in range(0, B, 7):
+        st = m.init_state()
+        m.forward(prompts[i], st)
+        want = m.forward([int(toks[i])], st)
+        assert rel_rmse(lg[i], want) <= RMSE_BOUND
+        assert rel_rmse(S.slot_back(i), st) <= RMSE_BOUND
+    S.load(snap)
+    n = 12
+    out = b.argmax_selfloop_batch(S, seeds, n)
+    agree = total = 0
+    for i in range(B):
+        st = m.init_state()
+        m.forward(prompts[i][:-1], st)
+        prev = int(seeds[i])
+        for t in range(n):
+            agree += orc.argmax(m.forward([prev], st)) == out[i, t]
+            total += 1
+            prev = int(out[i, t])
+    assert agree / total >= bar
+    S.free()

@@ -487,3 +487,120 @@ def test_gemm_epilogues(be):
     C16 = be.tensor(n=m * n, dtype=rsv.F16)
     be.call("rsv_gemm_ex", At, Wt, None, C16, m, n, k, 4, NONE, NONE, NONE)
     assert rel_err(be.get(C16, m * n).reshape(m, n), np.tanh(acc)) < 2e-3
+
+
+@pytest.mark.parametrize("batch", [1, 3, 8])
+def test_gemv_multi_lnmix_and_side_copy(be, batch):
+    """LN-mix prologue (LN + token-shift lerp), lnout, STORE2 and the side
+    copy of rsv_gemv_multi against the oracle's layer_norm/lerp/matvec."""
+    rsv = _rsv()
+    rng = np.random.default_rng(50 + batch)
+    C, M = 1024, 384
+    idx, sz, W = _int8_weight(rng, M, C)
+    h = be.int8(idx, sz)
+    x = (rng.standard_normal((batch, C)) * 2 + 0.3).astype(np.float32)
+    prev = rng.standard_normal((batch, C)).astype(np.float32)
+    gam, bet = rng.standard_normal(C).astype(np.float32), rng.standard_normal(C).astype(np.float32)
+    coef = rng.random(C).astype(np.float32)
+    ids = dict(x=be.tensor(x), prev=be.tensor(prev), g=be.tensor(gam), b=be.tensor(bet), c=be.tensor(coef),
+               ln=be.tensor(n=batch * C), y=be.tensor(n=batch * M), y2=be.tensor(n=batch * M),
+               dst=be.tensor(n=batch * C))
+    j = rsv.GemvJob()
+    ctypes.memset(ctypes.byref(j), 0xFF, ctypes.sizeof(j))
+    j.w8 = ctypes.pointer(h)
+    j.m, j.k, j.x, j.y = M, C, ids["x"], ids["y"]
+    j.prologue, j.epilogue = 3, 7
+    j.p1 = ids["y2"]
+    j.gamma, j.beta, j.prev, j.coef, j.lnout = ids["g"], ids["b"], ids["prev"], ids["c"], ids["ln"]
+    be.call("rsv_gemv_multi", ctypes.byref(j), 1, NONE, NONE, 0, batch)
+    got = be.get(ids["y"], batch * M).reshape(batch, M)
+    for q in range(batch):
+        ln = orc.layer_norm(x[q], gam, bet)
+        mix = ln + coef * (prev[q] - ln)
+        assert rel_err(got[q], mix.astype(np.float64) @ W.astype(np.float64).T) < 5e-5
+        assert rel_err(be.get(ids["ln"], batch * C).reshape(batch, C)[q], ln) < 1e-5
+    assert np.array_equal(be.get(ids["y2"], batch * M), be.get(ids["y"], batch * M))
+    # the side copy moves the previous launch's LN rows (the state write is
+    # deferred by one launch)
+    j.lnout = NONE
+    be.call("rsv_gemv_multi", ctypes.byref(j), 1, ids["ln"], ids["dst"], C, batch)
+    assert np.array_equal(be.get(ids["dst"], batch * C), be.get(ids["ln"], batch * C))
+
+
+@pytest.mark.parametrize("batch", [16, 33, 64, 100])
+def test_gemm_skinny(be, batch):
+    """Batched-decode MFMA GEMM (fp16 x, int8/fp16 W) against float64 with
+    the loader's fp16 rounding of the dequantised weights."""
+    rsv = _rsv()
+    rng = np.random.default_rng(60 + batch)
+    n, k = 320, 1280
+    idx, sz, W = _int8_weight(rng, n, k)
+    h = be.int8(idx, sz)
+    W16 = (rng.standard_normal((n, k)) * 0.02).astype(np.float16)
+    x = rng.standard_normal((batch, k)).astype(np.float16)
+    xt = be.tensor(x.astype(np.float32), dtype=rsv.F16)
+    w16 = be.tensor(W16.astype(np.float32), dtype=rsv.F16)
+    bias = rng.standard_normal(n).astype(np.float32)
+    aux = rng.standard_normal((batch, n)).astype(np.float32)
+    y0 = rng.standard_normal((batch, n)).astype(np.float32)
+    bt, at, st = be.tensor(bias), be.tensor(aux), be.tensor(np.array([-0.6], np.float32))
+    X = x.astype(np.float64)
+    Wq = W.astype(np.float16).astype(np.float64)
+    sig = lambda t: 1 / (1 + np.exp(-t))
+    for wname, w8, w16id, Wm in (("i8", ctypes.pointer(h), NONE, Wq), ("f16", None, w16, W16.astype(np.float64))):
+        acc = X @ Wm.T
+        for epi, init, ref in [(0, None, acc), (1, None, acc + bias), (2, y0, y0 + acc),
+                               (3, None, np.maximum(acc, 0) ** 2), (4, None, np.tanh(acc)),
+                               (5, None, np.exp(-0.6 * sig(acc + bias))), (6, None, sig(acc + bias)),
+                               (7, y0, y0 + sig(acc + bias) * (aux - y0)), (8, None, sig(acc))]:
+            y = be.tensor(init if init is not None else np.zeros((batch, n), np.float32))
+            y2 = be.tensor(n=batch * n)
+            j = rsv.MmJob(w16id, w8, n, k, xt, y, y2, epi, bt, at, st)
+            be.call("rsv_gemm_skinny", ctypes.byref(j), 1, batch)
+            got = be.get(y, batch * n).reshape(batch, n)
+            assert rel_err(got, ref) < 2e-5, (wname, epi)
+            assert np.array_equal(be.get(y2, batch * n), got.reshape(-1))
+        y16 = be.tensor(n=batch * n, dtype=rsv.F16)
+        j = rsv.MmJob(w16id, w8, n, k, xt, y16, NONE, 4, NONE, NONE, NONE)
+        be.call("rsv_gemm_skinny", ctypes.byref(j), 1, batch)
+        assert rel_err(be.get(y16, batch * n).reshape(batch, n), np.tanh(acc)) < 2e-3
+
+
+def test_ln_mix_f16_and_wkv_yg(be):
+    rsv = _rsv()
+    rng = np.random.default_rng(70)
+    B, C = 5, 2560
+    x = (rng.standard_normal((B, C)) * 2).astype(np.float32)
+    st = rng.standard_normal((B, C)).astype(np.float32)
+    gam, bet = rng.standard_normal(C).astype(np.float32), rng.standard_normal(C).astype(np.float32)
+    coefs = [rng.random(C).astype(np.float32) for _ in range(6)]
+    xt, stt, gt, btt = be.tensor(x), be.tensor(st), be.tensor(gam), be.tensor(bet)
+    cids = np.array([be.tensor(c) for c in coefs], np.uint32)
+    oids = np.array([be.tensor(n=B * C, dtype=rsv.F16) for _ in range(6)], np.uint32)
+    P = lambda a: a.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32))
+    be.call("rsv_ln_mix_f16", xt, stt, gt, btt, P(cids), P(oids), 6, C, 1e-5, B)
+    for q in range(B):
+        ln = orc.layer_norm(x[q], gam, bet)
+        for j in range(6):
+            want = (ln + coefs[j] * (st[q] - ln)).astype(np.float16).astype(np.float32)
+            got = be.get(int(oids[j]), B * C).reshape(B, C)[q]
+            assert np.max(np.abs(got - want)) <= 2e-3 * np.max(np.abs(want)), j
+        assert rel_err(be.get(stt, B * C).reshape(B, C)[q], ln) < 1e-5
+    # plain LN (no state, no coefficients)
+    one = np.array([int(oids[0])], np.uint32)
+    none = np.array([NONE], np.uint32)
+    be.call("rsv_ln_mix_f16", xt, NONE, gt, btt, P(none), P(one), 1, C, 1e-5, B)
+    got = be.get(int(oids[0]), B * C).reshape(B, C)
+    for q in range(B):
+        assert rel_err(got[q], orc.layer_norm(x[q], gam, bet)) < 2e-3
+    # WKV with the y*g fp16 output
+    H = 40
+    r, v, k, w, a, S, kk, ka, rk, g2, b2 = _wkv_inputs(rng, B, H)
+    g = rng.standard_normal((B, H * 64)).astype(np.float32)
+    ids = [be.tensor(t) for t in (S, k, kk, a, ka, r, v, w, g2, b2, rk)]
+    gt2, yg = be.tensor(g), be.tensor(n=B * H * 64, dtype=rsv.F16)
+    be.call("rsv_wkv7_decode_ex", *ids, NONE, gt2, yg, H, 64, 1e-12, 64e-5, B)
+    got = be.get(yg, B * H * 64).reshape(B, -1)
+    for q in range(B):
+        _, want, _ = _wkv_oracle(S[q], k[q], kk, a[q], ka, r[q], v[q], w[q], g2, b2, rk, H)
+        assert rel_err(got[q], want * g[q]) < 2e-3
