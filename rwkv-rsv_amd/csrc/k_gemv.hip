@@ -13,6 +13,8 @@
 // For a 16-element chunk inside one 128-group the contribution is
 // s*sum(x*q) + z*sum(x); sum(x) per chunk is precomputed while staging.
 #include "rsv_common.h"
+#include <cstdlib>
+#include <algorithm>
 
 namespace rsv {
 
@@ -22,6 +24,30 @@ __device__ __forceinline__ float h2f(uint32_t b) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)(b & 0xFFFFu));
 }
 __device__ __forceinline__ float sigmoid_f(float v) { return 1.0f / (1.0f + expf(-v)); }
+
+// Epilogue of one output element y[b, row] (codes of GemvEpi).
+__device__ __forceinline__ void apply_epi(const GemvJob &J, int row, int b, float v) {
+    float *yp = J.y + (size_t)b * J.ldy + row;
+    switch (J.epi) {
+        case EPI_STORE: *yp = v; break;
+        case EPI_RELU2: { const float t = v > 0.0f ? v : 0.0f; *yp = t * t; } break;
+        case EPI_ADD: *yp = *yp + v; break;
+        case EPI_TANH: *yp = tanhf(v); break;
+        case EPI_WDECAY: *yp = expf(sigmoid_f(v + J.p0[row]) * J.scale[0]); break;
+        case EPI_SIGBIAS: *yp = sigmoid_f(v + J.p0[row]); break;
+        case EPI_VLERP: {
+            const float g = sigmoid_f(v + J.p0[row]);
+            const float cur = *yp;
+            const float vf = J.p1[(size_t)b * J.ldy + row];
+            *yp = cur + g * (vf - cur);
+        } break;
+        case EPI_STORE2:
+            *yp = v;
+            ((float *)J.p1)[(size_t)b * J.ldy + row] = v;
+            break;
+        default: break;
+    }
+}
 
 __device__ __forceinline__ float block_sum_256(float v, float *red) {
 #pragma unroll
@@ -37,12 +63,93 @@ __device__ __forceinline__ float block_sum_256(float v, float *red) {
 // xs[(b*P + p)*NC + c], so lanes reading consecutive chunks read
 // consecutive 16-byte LDS words.  For int8 weights the per-chunk sum of x
 // (the zero-point term) goes to dxs[b*NC + c].
+// LN-mix staging for rows of at most kLnPT*256 elements: every load of the
+// block (x, prev, gamma, beta, coef) is issued up front in coalesced
+// element order, the two-pass statistics are taken from registers, and the
+// mixed row is scattered into the chunk-major LDS layout.  One memory
+// latency per batch row instead of one per loop iteration.
+constexpr int kLnPT = 16;
+template <int FMT, int BT>
+__device__ __forceinline__ void stage_x_lnmix(const GemvJob &J, int rb, int b0, int nb, float4 *xs, float *dxs,
+                                              float *red) {
+    constexpr int CW = FMT == FMT_I8 ? 16 : 8;
+    constexpr int P = CW / 4;
+    const int K = J.K, NC = K / CW, tid = threadIdx.x;
+    float *xsf = (float *)xs;
+    float gm[kLnPT], bt[kLnPT], cf[kLnPT];
+#pragma unroll
+    for (int j = 0; j < kLnPT; j++) {
+        const int e = tid + 256 * j;
+        const bool in = e < K;
+        gm[j] = in ? J.gamma[e] : 0.0f;
+        bt[j] = in ? J.beta[e] : 0.0f;
+        cf[j] = in ? J.coef[e] : 0.0f;
+    }
+    const bool wr = J.lnout && rb == 0;
+#pragma unroll
+    for (int b = 0; b < BT; b++) {
+        float xv[kLnPT], pv[kLnPT];
+        const bool live = b < nb;
+        const size_t ro = (size_t)(b0 + (live ? b : 0)) * J.ldx;
+#pragma unroll
+        for (int j = 0; j < kLnPT; j++) {
+            const int e = tid + 256 * j;
+            const bool in = live && e < K;
+            xv[j] = in ? J.x[ro + e] : 0.0f;
+            pv[j] = in ? J.prev[ro + e] : 0.0f;
+        }
+        // model.rs:625-635: mean, then the mean of squared deviations
+        float s = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kLnPT; j++) s += xv[j];
+        const float mu = block_sum_256(s, red) / (float)K;
+        float q = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kLnPT; j++) {
+            const int e = tid + 256 * j;
+            const float d = xv[j] - mu;
+            q += e < K ? d * d : 0.0f;
+        }
+        const float inv = 1.0f / sqrtf(block_sum_256(q, red) / (float)K + 1.0e-5f);
+#pragma unroll
+        for (int j = 0; j < kLnPT; j++) {
+            const int e = tid + 256 * j;
+            if (e >= K) continue;
+            float v = 0.0f;
+            if (live) {
+                const float ln = (xv[j] - mu) * inv * gm[j] + bt[j];
+                if (wr) J.lnout[ro + e] = ln;
+                v = ln + cf[j] * (pv[j] - ln);
+            }
+            const int c = e / CW, r = e - c * CW;
+            xsf[((b * P + (r >> 2)) * NC + c) * 4 + (r & 3)] = v;
+        }
+    }
+    if (FMT == FMT_I8) {
+        __syncthreads();
+        for (int e = tid; e < BT * NC; e += 256) {
+            const int b = e / NC, c = e - b * NC;
+            float s = 0.0f;
+#pragma unroll
+            for (int p = 0; p < P; p++) {
+                const float4 t = xs[(b * P + p) * NC + c];
+                s += t.x; s += t.y; s += t.z; s += t.w;
+            }
+            dxs[b * NC + c] = s;
+        }
+    }
+}
+
 template <int FMT, int BT>
 __device__ __forceinline__ void stage_x(const GemvJob &J, int rb, int b0, int nb, float4 *xs, float *dxs,
                                         float *red) {
     constexpr int CW = FMT == FMT_I8 ? 16 : 8;
     constexpr int P = CW / 4;
     const int K = J.K, NC = K / CW, tid = threadIdx.x;
+    if (J.pro == PRO_LNMIX && K <= 256 * kLnPT) {
+        stage_x_lnmix<FMT, BT>(J, rb, b0, nb, xs, dxs, red);
+        return;
+    }
     float mean[BT], inv[BT];
     if (J.pro == PRO_LNMIX) {
         // LayerNorm statistics of each batch row, two-pass (model.rs:625-635)
@@ -242,27 +349,7 @@ __device__ __forceinline__ void gemv_body(const GemvJob &J, int rb, int batch, f
 #pragma unroll
             for (int b = 0; b < BT; b++) {
                 if (b >= nb) continue;
-                const float v = acc[r][b];
-                float *yp = J.y + (size_t)(b0 + b) * J.ldy + row;
-                switch (J.epi) {
-                    case EPI_STORE: *yp = v; break;
-                    case EPI_RELU2: { const float t = v > 0.0f ? v : 0.0f; *yp = t * t; } break;
-                    case EPI_ADD: *yp = *yp + v; break;
-                    case EPI_TANH: *yp = tanhf(v); break;
-                    case EPI_WDECAY: *yp = expf(sigmoid_f(v + J.p0[row]) * J.scale[0]); break;
-                    case EPI_SIGBIAS: *yp = sigmoid_f(v + J.p0[row]); break;
-                    case EPI_VLERP: {
-                        const float g = sigmoid_f(v + J.p0[row]);
-                        const float cur = *yp;
-                        const float vf = J.p1[(size_t)(b0 + b) * J.ldy + row];
-                        *yp = cur + g * (vf - cur);
-                    } break;
-                    case EPI_STORE2:
-                        *yp = v;
-                        ((float *)J.p1)[(size_t)(b0 + b) * J.ldy + row] = v;
-                        break;
-                    default: break;
-                }
+                apply_epi(J, row, b0 + b, acc[r][b]);
             }
         }
     }
@@ -312,6 +399,364 @@ static int launch_t(rsv_ctx *ctx, GemvJobs &jobs, int batch) {
     return 0;
 }
 
+// ---------------------------------------------------------------- B = 1
+// Decode GEMV for one session, built for memory-level parallelism.
+// A job's rows are cut into tiles of (4/KS)*RU rows; each block of the
+// launch owns the tiles rb, rb + nblk, ... of one job.  Per block:
+//   1. its share of the prologue inputs (x and, per prologue, the LN
+//      gamma/beta/mix coefficient/token-shift row or the gate) is loaded,
+//      4 elements per thread per round, coalesced;
+//   2. the first tile's weights, scale/zero words and epilogue operands are
+//      loaded with clamped addresses and no branches, so none is sunk;
+//   3. the prologue runs once per block (LN statistics by block reduction)
+//      and the transformed x goes through LDS into registers: lane li of a
+//      wave always reads chunks li + 64*j of its K-slice (8-byte chunks, so
+//      each weight load instruction covers 512 contiguous bytes), the same
+//      x chunks for every row;
+//   4. tiles are then software-pipelined: the next tile's loads go out
+//      before the current tile's dot products.
+// A row is split over KS waves (KS = 1, 2 or 4) whose partial sums meet in
+// LDS in a fixed order, so results do not depend on timing.
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+// Q: prologue rounds (K <= 1024*Q).  The LN-mix and gate prologues need four
+// more vectors per round, so they are compiled only into the short-row
+// variant (Q <= 3); long rows take the plain and sigmoid prologues.
+constexpr int kRegQShort = 3, kRegQLong = 10;
+
+template <int FMT, int CPL, int RU>
+struct RegTile {
+    typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+    u32x2_t w[RU][CPL];
+    uint32_t sz[RU][CPL];
+    float e0[RU], e1[RU], e2[RU];  // y (read-modify-write epilogues), p0[row], p1[row]
+};
+
+template <int FMT, int CPL, int RU>
+__device__ __forceinline__ void reg_load(const GemvJob &J, int tile, int ks, int rg, int li,
+                                         RegTile<FMT, CPL, RU> &T) {
+    constexpr int CW = FMT == FMT_I8 ? 8 : 4;
+    constexpr int SL = 64 * CPL;
+    const int K = J.K, M = J.M, NC = K / CW, KG = K / 128;
+    const int rbase = (tile * (4 / J.ks) + rg) * RU;
+    const u32x2 *W = (const u32x2 *)J.w;
+    const bool need_y = J.epi == EPI_ADD || J.epi == EPI_VLERP;
+#pragma unroll
+    for (int r = 0; r < RU; r++) {
+        const int row = min(rbase + r, M - 1);
+#pragma unroll
+        for (int j = 0; j < CPL; j++) {
+            const int c = min(ks * SL + li + j * 64, NC - 1);
+            T.w[r][j] = __builtin_nontemporal_load(W + (size_t)row * NC + c);
+            if (FMT == FMT_I8) T.sz[r][j] = __builtin_nontemporal_load(J.sz + (size_t)row * KG + (c >> 4));
+        }
+        T.e0[r] = need_y ? J.y[row] : 0.0f;
+        T.e1[r] = J.p0 ? J.p0[row] : 0.0f;
+        T.e2[r] = J.epi == EPI_VLERP ? J.p1[row] : 0.0f;
+    }
+}
+
+template <int FMT, int CPL, int RU>
+__device__ __forceinline__ void reg_dot(const GemvJob &J, int tile, int it, int ks, int rg, int wave, int li,
+                                        const float (&xv)[CPL][FMT == FMT_I8 ? 8 : 4], const float (&dx)[CPL],
+                                        const RegTile<FMT, CPL, RU> &T, float scale, float *part) {
+    const int M = J.M, KS = J.ks;
+    const int rbase = (tile * (4 / KS) + rg) * RU;
+    float acc[RU];
+#pragma unroll
+    for (int r = 0; r < RU; r++) acc[r] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < CPL; j++) {
+#ifdef RSV_X_NODOT
+#pragma unroll
+        for (int r = 0; r < RU; r++) acc[r] += __uint_as_float((T.w[r][j].x ^ T.w[r][j].y ^ T.sz[r][j]) & 0x0FFFFFFFu);
+        continue;
+#endif
+        if (FMT == FMT_I8) {
+            // w = s*q + z over one 8-weight chunk of a 128-group (model.rs:234-252):
+            // contribution s*sum(x*q) + z*sum(x)
+#pragma unroll
+            for (int r = 0; r < RU; r++) {
+                float d = 0.0f;
+#pragma unroll
+                for (int q = 0; q < 2; q++) {
+                    const uint32_t wq = T.w[r][j][q];
+                    d = fmaf(xv[j][4 * q + 0], (float)(wq & 0xFFu), d);
+                    d = fmaf(xv[j][4 * q + 1], (float)((wq >> 8) & 0xFFu), d);
+                    d = fmaf(xv[j][4 * q + 2], (float)((wq >> 16) & 0xFFu), d);
+                    d = fmaf(xv[j][4 * q + 3], (float)(wq >> 24), d);
+                }
+                const uint32_t sw = T.sz[r][j];
+                acc[r] = fmaf(h2f(sw), d, fmaf(h2f(sw >> 16), dx[j], acc[r]));
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < RU; r++) {
+                float d = acc[r];
+#pragma unroll
+                for (int q = 0; q < 2; q++) {
+                    const uint32_t wq = T.w[r][j][q];
+                    d = fmaf(xv[j][2 * q + 0], h2f(wq), d);
+                    d = fmaf(xv[j][2 * q + 1], h2f(wq >> 16), d);
+                }
+                acc[r] = d;
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < RU; r++) {
+        float v = acc[r];
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+        acc[r] = v;
+    }
+    if (KS > 1) {
+        // slice partials meet in LDS (double-buffered by tile parity); slice
+        // 0 adds them in slice order
+        float *pp = part + (it & 1) * 4 * RU;
+        if (li == 0)
+#pragma unroll
+            for (int r = 0; r < RU; r++) pp[wave * RU + r] = acc[r];
+        __syncthreads();
+        if (ks != 0) return;
+#pragma unroll
+        for (int r = 0; r < RU; r++) {
+            float v = pp[wave * RU + r];
+            for (int q = 1; q < KS; q++) v += pp[(wave + q) * RU + r];
+            acc[r] = v;
+        }
+    }
+    if (li != 0) return;
+#pragma unroll
+    for (int r = 0; r < RU; r++) {
+        const int row = rbase + r;
+        if (row >= M) continue;
+        const float v = acc[r];
+        float *yp = J.y + row;
+        switch (J.epi) {
+            case EPI_STORE: *yp = v; break;
+            case EPI_RELU2: { const float t = v > 0.0f ? v : 0.0f; *yp = t * t; } break;
+            case EPI_ADD: *yp = T.e0[r] + v; break;
+            case EPI_TANH: *yp = tanhf(v); break;
+            case EPI_WDECAY: *yp = expf(sigmoid_f(v + T.e1[r]) * scale); break;
+            case EPI_SIGBIAS: *yp = sigmoid_f(v + T.e1[r]); break;
+            case EPI_VLERP: {
+                const float g = sigmoid_f(v + T.e1[r]);
+                *yp = T.e0[r] + g * (T.e2[r] - T.e0[r]);
+            } break;
+            case EPI_STORE2:
+                *yp = v;
+                ((float *)J.p1)[row] = v;
+                break;
+            default: break;
+        }
+    }
+}
+
+template <int FMT, int CPL, int RU, int Q>
+__device__ __forceinline__ void gemv_reg_body(const GemvJob &J, int rb, float *red, float4 *xs) {
+    constexpr bool kMix = Q <= kRegQShort;
+    constexpr int CW = FMT == FMT_I8 ? 8 : 4;  // weights per 8-byte chunk
+    constexpr int P = CW / 4;                  // float4 parts of x per chunk
+    constexpr int SL = 64 * CPL;
+    const int K = J.K, M = J.M, NC = K / CW, KS = J.ks, K4 = K / 4;
+    const int tid = threadIdx.x, wave = tid >> 6, li = tid & 63;
+    const int ks = wave % KS, rg = wave / KS;
+    const int ntile = (M + (4 / KS) * RU - 1) / ((4 / KS) * RU);
+    const int nblk = J.nblk;
+
+    // 1. prologue inputs
+    const float4 *X4 = (const float4 *)J.x;
+    constexpr int QM = kMix ? Q : 1;
+    float4 xa[Q], pa[QM], ga[QM], ba[QM], ca[QM];
+#pragma unroll
+    for (int i = 0; i < Q; i++) {
+        const int q = tid + 256 * i;
+        const bool in = q < K4;
+        xa[i] = in ? X4[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+        if (!kMix) continue;
+        if (J.pro == PRO_MUL) pa[i] = in ? ((const float4 *)J.xmul)[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+        if (J.pro == PRO_LNMIX) {
+            pa[i] = in ? ((const float4 *)J.prev)[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+            ga[i] = in ? ((const float4 *)J.gamma)[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+            ba[i] = in ? ((const float4 *)J.beta)[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+            ca[i] = in ? ((const float4 *)J.coef)[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    }
+    const float scale = J.epi == EPI_WDECAY ? J.scale[0] : 0.0f;
+
+    // 2. first tile
+    RegTile<FMT, CPL, RU> A, B;
+    int t = rb;
+    reg_load<FMT, CPL, RU>(J, t, ks, rg, li, A);
+
+    // 3. prologue, once per block, into LDS (float4 part p of chunk c at p*NC + c)
+#ifdef RSV_X_NOPRO
+    if (false) {
+#else
+    if (kMix && J.pro == PRO_LNMIX) {
+#endif
+        float s = 0.0f;
+#pragma unroll
+        for (int i = 0; i < Q; i++) s += (xa[i].x + xa[i].y) + (xa[i].z + xa[i].w);
+        const float mu = block_sum_256(s, red) / (float)K;
+        float v2 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < Q; i++) {
+            if (tid + 256 * i >= K4) continue;
+            const float d0 = xa[i].x - mu, d1 = xa[i].y - mu, d2 = xa[i].z - mu, d3 = xa[i].w - mu;
+            v2 += (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
+        }
+        const float inv = 1.0f / sqrtf(block_sum_256(v2, red) / (float)K + 1.0e-5f);
+        const bool wr = J.lnout && rb == 0;
+#pragma unroll
+        for (int i = 0; i < Q; i++) {
+            const int q = tid + 256 * i;
+            if (q >= K4) continue;
+            const int m = kMix ? i : 0;
+            float4 ln;
+            ln.x = (xa[i].x - mu) * inv * ga[m].x + ba[m].x;
+            ln.y = (xa[i].y - mu) * inv * ga[m].y + ba[m].y;
+            ln.z = (xa[i].z - mu) * inv * ga[m].z + ba[m].z;
+            ln.w = (xa[i].w - mu) * inv * ga[m].w + ba[m].w;
+            if (wr) ((float4 *)J.lnout)[q] = ln;
+            xa[i].x = ln.x + ca[m].x * (pa[m].x - ln.x);
+            xa[i].y = ln.y + ca[m].y * (pa[m].y - ln.y);
+            xa[i].z = ln.z + ca[m].z * (pa[m].z - ln.z);
+            xa[i].w = ln.w + ca[m].w * (pa[m].w - ln.w);
+        }
+    } else if (kMix && J.pro == PRO_MUL) {
+#pragma unroll
+        for (int i = 0; i < Q; i++) {
+            const int m = kMix ? i : 0;
+            xa[i].x *= pa[m].x; xa[i].y *= pa[m].y; xa[i].z *= pa[m].z; xa[i].w *= pa[m].w;
+        }
+    } else if (J.pro == PRO_SIGMOID) {
+#pragma unroll
+        for (int i = 0; i < Q; i++) {
+            xa[i].x = sigmoid_f(xa[i].x); xa[i].y = sigmoid_f(xa[i].y);
+            xa[i].z = sigmoid_f(xa[i].z); xa[i].w = sigmoid_f(xa[i].w);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < Q; i++) {
+        const int q = tid + 256 * i;
+        if (q >= K4) continue;
+        const int c = (4 * q) / CW, pp = ((4 * q) % CW) >> 2;
+        xs[pp * NC + c] = xa[i];
+    }
+    __syncthreads();
+    float xv[CPL][CW], dx[CPL];
+#pragma unroll
+    for (int j = 0; j < CPL; j++) {
+        const int cr = ks * SL + li + j * 64;
+        const bool cin = cr < NC;
+        const int c = cin ? cr : NC - 1;
+#pragma unroll
+        for (int p = 0; p < P; p++) {
+            const float4 v = xs[p * NC + c];
+            xv[j][4 * p] = cin ? v.x : 0.0f; xv[j][4 * p + 1] = cin ? v.y : 0.0f;
+            xv[j][4 * p + 2] = cin ? v.z : 0.0f; xv[j][4 * p + 3] = cin ? v.w : 0.0f;
+        }
+        float sx = 0.0f;
+#pragma unroll
+        for (int i = 0; i < CW; i++) sx += xv[j][i];
+        dx[j] = sx;
+    }
+
+    // 4. software-pipelined tiles (the prefetch past the last tile re-reads
+    // the current one instead of branching, so no load waits on a join)
+    float *part = red + 8;
+    for (int it = 0;; it += 2) {
+        int tn = t + nblk;
+        reg_load<FMT, CPL, RU>(J, tn < ntile ? tn : t, ks, rg, li, B);
+        reg_dot<FMT, CPL, RU>(J, t, it, ks, rg, wave, li, xv, dx, A, scale, part);
+        t = tn;
+        if (t >= ntile) break;
+        tn = t + nblk;
+        reg_load<FMT, CPL, RU>(J, tn < ntile ? tn : t, ks, rg, li, A);
+        reg_dot<FMT, CPL, RU>(J, t, it + 1, ks, rg, wave, li, xv, dx, B, scale, part);
+        t = tn;
+        if (t >= ntile) break;
+    }
+}
+
+template <int CPL, int RU, int Q>
+__global__ __launch_bounds__(256) void k_gemv_reg(GemvJobs jobs) {
+    extern __shared__ float4 xs4[];
+    __shared__ float red[8 + 8 * RU];
+    const int bid = blockIdx.x;
+    if (bid == 0 && jobs.side.src)
+        for (int i = threadIdx.x; i < jobs.side.n; i += 256) jobs.side.dst[i] = jobs.side.src[i];
+    int ji = 0;
+    while (ji + 1 < jobs.n && bid >= jobs.blk_start[ji + 1]) ji++;
+    const GemvJob &J = jobs.j[ji];
+    const int rb = bid - jobs.blk_start[ji];
+    if (J.fmt == FMT_I8)
+        gemv_reg_body<FMT_I8, CPL, RU, Q>(J, rb, red, xs4);
+    else
+        gemv_reg_body<FMT_F16, CPL, RU, Q>(J, rb, red, xs4);
+}
+
+constexpr int kRegCPL = 5;
+
+// k-slices per row for the register kernel, or 0 when the job does not fit
+// it (rows too short to fill the lanes, or more than 4 slices).
+static int reg_slices(const GemvJob &J) {
+    const int nc = J.K / (J.fmt == FMT_I8 ? 8 : 4);
+    const int sl = 64 * kRegCPL;
+    const int ks = (nc + sl - 1) / sl;
+    if (ks == 3 || ks > 4 || J.K % 4 != 0) return 0;
+    if (J.K > 1024 * kRegQLong) return 0;
+    if ((J.pro == PRO_LNMIX || J.pro == PRO_MUL) && J.K > 1024 * kRegQShort) return 0;
+    if (nc * 4 < ks * sl * 3) return 0;  // under 75% of the lanes busy
+    return ks;
+}
+
+// Blocks per job: the launch targets `target` blocks in all, shared by the
+// jobs in proportion to their tiles, every block of a job getting the same
+// number of tiles (up to the last).
+template <int RU>
+static int launch_reg(rsv_ctx *ctx, GemvJobs &jobs, int target) {
+    int tiles_all = 0;
+    for (int i = 0; i < jobs.n; i++) {
+        const int rpt = (4 / jobs.j[i].ks) * RU;
+        tiles_all += (jobs.j[i].M + rpt - 1) / rpt;
+    }
+    int total = 0, kmax = 0;
+    for (int i = 0; i < jobs.n; i++) {
+        GemvJob &J = jobs.j[i];
+        const int rpt = (4 / J.ks) * RU;
+        const int tiles = (J.M + rpt - 1) / rpt;
+        const int want = std::max(1, (int)((int64_t)tiles * target / std::max(1, tiles_all)));
+        const int tpb = (tiles + want - 1) / want;
+        J.nblk = (tiles + tpb - 1) / tpb;
+        jobs.blk_start[i] = total;
+        total += J.nblk;
+        kmax = std::max(kmax, J.K);
+    }
+    jobs.blk_start[jobs.n] = total;
+    if (kmax <= 1024 * kRegQShort)
+        hipLaunchKernelGGL((k_gemv_reg<kRegCPL, RU, kRegQShort>), dim3(total), dim3(256), (size_t)kmax * 4, ctx->stream, jobs);
+    else
+        hipLaunchKernelGGL((k_gemv_reg<kRegCPL, RU, kRegQLong>), dim3(total), dim3(256), (size_t)kmax * 4, ctx->stream, jobs);
+    RSV_HIP(hipGetLastError());
+    return 0;
+}
+
+static int env_int(const char *name, int dflt) {
+    const char *e = getenv(name);
+    return (e && e[0]) ? atoi(e) : dflt;
+}
+
+static bool reg_disabled() {
+    static int v = -1;
+    if (v < 0) {
+        const char *e = getenv("RSV_GEMV_REG");
+        v = (e && e[0] == '0') ? 1 : 0;
+    }
+    return v == 1;
+}
+
 int launch_gemv_jobs(rsv_ctx *ctx, GemvJobs &jobs, int batch) {
     if (jobs.n <= 0 || jobs.n > kMaxJobs) return RSV_FAIL("gemv: bad job count %d", jobs.n);
     if (batch <= 0) return RSV_FAIL("gemv: batch must be >= 1 (got %d)", batch);
@@ -337,6 +782,21 @@ int launch_gemv_jobs(rsv_ctx *ctx, GemvJobs &jobs, int batch) {
         if (nc > ncmax) ncmax = nc;
     }
     if (jobs.side.src && (!jobs.side.dst || jobs.side.n <= 0)) return RSV_FAIL("gemv: bad side copy");
+    if (batch == 1 && !reg_disabled()) {
+        bool ok = true;
+        for (int i = 0; i < jobs.n && ok; i++) {
+            GemvJob &J = jobs.j[i];
+            J.ks = reg_slices(J);
+            ok = J.ks > 0;
+        }
+        if (ok) {
+            const int cus = ctx->sm_count > 0 ? ctx->sm_count : 256;
+            static const int ru = env_int("RSV_GEMV_RU", 2);
+            static const int bpc = env_int("RSV_GEMV_BPC", 2);
+            if (ru == 4) return launch_reg<4>(ctx, jobs, bpc * cus);
+            return launch_reg<2>(ctx, jobs, bpc * cus);
+        }
+    }
     // Lanes per row: a full wave when rows are long, a quarter wave for the
     // short LoRA-up rows (k = rank).  Long rows (ffn.value) keep fewer rows
     // per wave so more waves are resident.

@@ -70,6 +70,7 @@ struct GemvJob {
     int fmt, epi, pro;
     int ldx, ldy;  // batch strides in elements
     int nblk;      // blocks along M (filled by the launcher)
+    int ks;        // k-slices per row (register-resident B=1 kernel; filled by the launcher)
 };
 constexpr int kMaxJobs = 8;
 // A side copy done by the first block column of a launch: dst[b, :n] =
