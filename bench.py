@@ -107,8 +107,8 @@ def kernel_leg(reps=200):
     us = e0.elapsed_time(e1) * 1000.0 / reps
     be.close()
     nbytes = ffn_key_bytes(C, F)
-    return dict(kernel="k_gemv<64,1,2,6,false> (ffn.key: LN-mix prologue, int8 10240x2560, relu^2)",
-                avg_us=us, bytes=nbytes, gbs=nbytes / us / 1e3)
+    return dict(kernel="k_gemv_reg<5,2,3> (B=1 ffn.key: LN2 + token-shift mix prologue, int8 10240x2560, relu^2)",
+                avg_us=us, bytes=nbytes, gbs=nbytes / us / 1e3, launches=reps)
 
 
 def main():
@@ -121,6 +121,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-tokens", type=int, default=4)
     ap.add_argument("--cache", default=os.environ.get("RSV_BENCH_CACHE", "/tmp"))
+    ap.add_argument("--kernel-only", action="store_true",
+                    help="run only the dominant-kernel leg (for rocprofv3 summaries of that kernel)")
     ap.add_argument("--no-graph", action="store_true",
                     help="enqueue self-loop steps eagerly instead of replaying a HIP graph (profiling)")
     args = ap.parse_args()
@@ -130,6 +132,12 @@ def main():
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}).",
               file=sys.stderr)
         sys.exit(2)
+
+    if args.kernel_only:
+        kl = kernel_leg()
+        log(f"kernel: {kl['kernel']}: {kl['avg_us']:.2f} us/launch over {kl['launches']} launches, {kl['gbs']:.0f} GB/s")
+        print(json.dumps({"kernel_leg": kl}))
+        return
 
     import rsv
     import synth

@@ -329,13 +329,14 @@ typedef struct rsv_mm_job {
     uint32_t x, y, y2;
     int epilogue;
     uint32_t bias, aux, scale;
-    int tiled; /* weights (w16, or w8->idx) are the copy made by rsv_tile_weights */
+    int tiled; /* weights (w16, or w8->idx and w8->sz) are the copies made by rsv_tile_weights */
 } rsv_mm_job;
 /* MFMA-tiled copy of a weight matrix for rsv_gemm_skinny: 32x32 tiles
  * (1 KiB int8 / 2 KiB fp16), lane-ordered, [row tile][k chunk].  src is an
  * int8 idx tensor (esz 1) or an F16 tensor (esz 2) of n x k; *out receives
- * a new tensor (rows padded to a multiple of 32).  The int8 scale/zero
- * tensor is shared with the original. */
+ * a new tensor (rows padded to a multiple of 32).  esz 4 tiles an int8
+ * scale/zero tensor [n, k/128] as [row tile][group][32 rows]; a tiled int8
+ * job takes both tiled tensors in its rsv_int8 handle. */
 int rsv_tile_weights(rsv_ctx *ctx, uint32_t src, uint64_t n, uint64_t k, int esz, uint32_t *out);
 int rsv_gemm_skinny(rsv_ctx *ctx, const rsv_mm_job *jobs, uint64_t njobs, uint64_t batch);
 /* LN rows of x [batch, c] + nout (1 or 6) token-shift mixes as F16 outputs;

@@ -120,6 +120,12 @@ int rsv_create(int device, rsv_ctx **out) {
         delete ctx;
         return RSV_FAIL("rsv_create: workspace allocation failed");
     }
+    if (hipMalloc(&ctx->mix_buf, (size_t)kMaxJobs * kMixMaxK * 4) != hipSuccess) {
+        hipFree(ctx->skinny_ws);
+        hipStreamDestroy(ctx->stream);
+        delete ctx;
+        return RSV_FAIL("rsv_create: LN-mix buffer allocation failed");
+    }
     *out = ctx;
     return 0;
 }
@@ -136,6 +142,7 @@ int rsv_destroy(rsv_ctx *ctx) {
     if (ctx->hist_dev) hipFree(ctx->hist_dev);
     if (ctx->sample_work) hipFree(ctx->sample_work);
     if (ctx->skinny_ws) hipFree(ctx->skinny_ws);
+    if (ctx->mix_buf) hipFree(ctx->mix_buf);
     hipStreamDestroy(ctx->stream);
     delete ctx;
     return 0;
@@ -1239,6 +1246,11 @@ extern "C" int rsv_gemm_skinny(rsv_ctx *ctx, const rsv_mm_job *jobs, uint64_t nj
             Tensor *tw = get_tensor(ctx, q.w8 ? q.w8->idx : q.w16);
             const uint64_t need = (q.n + 31) / 32 * 32 * q.k * (q.w8 ? 1 : 2);
             if (!tw || tw->len * dtype_size(tw->dtype) < need) return RSV_FAIL("gemm_skinny: tiled weight too small");
+            if (q.w8) {
+                Tensor *ts = get_tensor(ctx, q.w8->sz);
+                if (!ts || ts->len < (q.n + 31) / 32 * 32 * (q.k / 128))
+                    return RSV_FAIL("gemm_skinny: tiled scale/zero tensor too small (tile it with esz 4)");
+            }
         }
         J.N = (int)q.n;
         J.K = (int)q.k;
@@ -1300,13 +1312,17 @@ extern "C" int rsv_wkv7_decode_ex(rsv_ctx *ctx, uint32_t s, uint32_t k, uint32_t
 
 extern "C" int rsv_tile_weights(rsv_ctx *ctx, uint32_t src, uint64_t n, uint64_t k, int esz, uint32_t *out) {
     CHECK_CTX();
-    if (!out || (esz != 1 && esz != 2)) return RSV_FAIL("tile_weights: bad arguments");
+    if (!out || (esz != 1 && esz != 2 && esz != 4)) return RSV_FAIL("tile_weights: bad arguments");
     if (k % 32 != 0) return RSV_FAIL("tile_weights: k=%llu must be a multiple of 32", (unsigned long long)k);
+    if (esz == 4 && k % 128 != 0) return RSV_FAIL("tile_weights: k=%llu must be a multiple of 128", (unsigned long long)k);
     void *ps = nullptr;
-    if (opnd(ctx, src, esz == 1 ? RSV_U32 : RSV_F16, esz == 1 ? n * k / 4 : n * k, &ps, "tile_weights src")) return -1;
+    const uint64_t src_len = esz == 1 ? n * k / 4 : esz == 2 ? n * k : n * (k / 128);
+    if (opnd(ctx, src, esz == 2 ? RSV_F16 : RSV_U32, src_len, &ps, "tile_weights src")) return -1;
     const uint64_t rows = (n + 31) / 32 * 32;
     uint32_t id;
-    if (esz == 1) {
+    if (esz == 4) {
+        if (rsv_tensor_create(ctx, rows * (k / 128), RSV_U32, &id)) return -1;
+    } else if (esz == 1) {
         if (rsv_tensor_create(ctx, rows * k / 4, RSV_U32, &id)) return -1;
     } else {
         if (rsv_tensor_create(ctx, rows * k, RSV_F16, &id)) return -1;

@@ -761,6 +761,7 @@ int tile_linear(rsv_bundle *b, Linear &L) {
     if (L.i8) {
         L.ht = L.h;
         CK(rsv_tile_weights(b->ctx, L.h.idx, L.m, L.k, 1, &L.ht.idx));
+        CK(rsv_tile_weights(b->ctx, L.h.sz, L.m, L.k, 4, &L.ht.sz));
     } else {
         CK(rsv_tile_weights(b->ctx, L.w16, L.m, L.k, 2, &L.t16));
     }

@@ -743,19 +743,244 @@ static int launch_reg(rsv_ctx *ctx, GemvJobs &jobs, int target) {
     return 0;
 }
 
+// ---------------------------------------------------------------- B = 1, one-shot
+// LN + token-shift mixes of one row x [K] for a B=1 launch, computed once
+// (model.rs:625-635, 654-660): out_m = ln + coef_m * (prev - ln) with
+// ln = LN(x)*gamma + beta; lnout (optional) receives ln.  Every block takes
+// the row statistics itself (two-pass, from registers) and writes its slice
+// of 1024 elements.
+struct MixArgs {
+    const float *x, *gamma, *beta, *prev;
+    const float *coef[kMaxJobs];
+    float *out[kMaxJobs];
+    float *lnout;
+    int nmix, K;
+};
+constexpr int kMixQ = kMixMaxK / 1024;
+
+__global__ __launch_bounds__(256) void k_lnmix_pre(MixArgs a) {
+    __shared__ float red[4];
+    const int tid = threadIdx.x, K4 = a.K / 4;
+    const float4 *X4 = (const float4 *)a.x;
+    float s = 0.0f;
+    for (int q = tid; q < K4; q += 256) { const float4 v = X4[q]; s += (v.x + v.y) + (v.z + v.w); }
+    const float mu = block_sum_256(s, red) / (float)a.K;
+    float v2 = 0.0f;
+    for (int q = tid; q < K4; q += 256) {
+        const float4 v = X4[q];
+        const float d0 = v.x - mu, d1 = v.y - mu, d2 = v.z - mu, d3 = v.w - mu;
+        v2 += (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
+    }
+    const float inv = 1.0f / sqrtf(block_sum_256(v2, red) / (float)a.K + 1.0e-5f);
+    const int q = blockIdx.x * 256 + tid;
+    if (q >= K4) return;
+    const float4 v = X4[q], g = ((const float4 *)a.gamma)[q], b = ((const float4 *)a.beta)[q];
+    const float4 p = ((const float4 *)a.prev)[q];
+    float4 ln;
+    ln.x = (v.x - mu) * inv * g.x + b.x;
+    ln.y = (v.y - mu) * inv * g.y + b.y;
+    ln.z = (v.z - mu) * inv * g.z + b.z;
+    ln.w = (v.w - mu) * inv * g.w + b.w;
+    if (a.lnout) ((float4 *)a.lnout)[q] = ln;
+    for (int m = 0; m < a.nmix; m++) {
+        const float4 c = ((const float4 *)a.coef[m])[q];
+        float4 o;
+        o.x = ln.x + c.x * (p.x - ln.x);
+        o.y = ln.y + c.y * (p.y - ln.y);
+        o.z = ln.z + c.z * (p.z - ln.z);
+        o.w = ln.w + c.w * (p.w - ln.w);
+        ((float4 *)a.out[m])[q] = o;
+    }
+}
+
+// One-shot GEMV for one session: a block owns 4*(64/LPR) consecutive rows of
+// one job (LPR = 32 lanes per row for rows of at most 160 16-byte chunks,
+// else 64); lane li of a row reads chunks li + LPR*j, so each load
+// instruction covers LPR*16 contiguous bytes.  Every weight and scale/zero
+// load of the block goes out first (clamped addresses, no branches), then x
+// (after the prologue: gate multiply or sigmoid) is staged chunk-major in
+// LDS, and the dot products read it from there.  Small register footprint
+// and short blocks keep many blocks resident per CU, which is what hides the
+// memory latency here.
+template <int FMT, int LPR, int CPL, int Q>
+__device__ __forceinline__ void gemv_os_body(const GemvJob &J, int rb, float4 *xs) {
+    constexpr int CW = FMT == FMT_I8 ? 16 : 8;
+    constexpr int P = CW / 4;
+    constexpr int SLOTS = 64 / LPR;
+    const int K = J.K, M = J.M, NC = K / CW, KG = K / 128, K4 = K / 4;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int slot = lane / LPR, li = lane % LPR;
+    const int row0 = (rb * 4 + wave) * SLOTS + slot;
+    const int row = min(row0, M - 1);
+    const u32x4 *W = (const u32x4 *)J.w;
+    u32x4 wv[CPL];
+    uint32_t szv[CPL];
+#pragma unroll
+    for (int j = 0; j < CPL; j++) {
+        const int c = min(li + LPR * j, NC - 1);
+        wv[j] = __builtin_nontemporal_load(W + (size_t)row * NC + c);
+        if (FMT == FMT_I8) szv[j] = J.sz[(size_t)row * KG + (c >> 3)];
+    }
+    // x (with the gate multiply or sigmoid) into LDS: float4 part p of chunk c at p*NC + c
+    {
+        const float4 *X4 = (const float4 *)J.x;
+        float4 xa[Q];
+#pragma unroll
+        for (int i = 0; i < Q; i++) {
+            const int q = tid + 256 * i;
+            xa[i] = q < K4 ? X4[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        if (J.pro == PRO_MUL) {
+#pragma unroll
+            for (int i = 0; i < Q; i++) {
+                const int q = tid + 256 * i;
+                const float4 g = q < K4 ? ((const float4 *)J.xmul)[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+                xa[i].x *= g.x; xa[i].y *= g.y; xa[i].z *= g.z; xa[i].w *= g.w;
+            }
+        } else if (J.pro == PRO_SIGMOID) {
+#pragma unroll
+            for (int i = 0; i < Q; i++) {
+                xa[i].x = sigmoid_f(xa[i].x); xa[i].y = sigmoid_f(xa[i].y);
+                xa[i].z = sigmoid_f(xa[i].z); xa[i].w = sigmoid_f(xa[i].w);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < Q; i++) {
+            const int q = tid + 256 * i;
+            if (q < K4) xs[((4 * q) % CW >> 2) * NC + (4 * q) / CW] = xa[i];
+        }
+    }
+    __syncthreads();
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < CPL; j++) {
+        const int cr = li + LPR * j;
+        const bool live = cr < NC;
+        const int c = live ? cr : NC - 1;
+        float xv[CW];
+#pragma unroll
+        for (int p = 0; p < P; p++) {
+            const float4 t = xs[p * NC + c];
+            xv[4 * p] = t.x; xv[4 * p + 1] = t.y; xv[4 * p + 2] = t.z; xv[4 * p + 3] = t.w;
+        }
+        if (FMT == FMT_I8) {
+            // w = s*q + z over one 16-weight chunk of a 128-group (model.rs:234-252)
+            float dx = 0.0f, d = 0.0f;
+#pragma unroll
+            for (int i = 0; i < CW; i++) dx += xv[i];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const uint32_t wq = wv[j][q];
+                d = fmaf(xv[4 * q + 0], (float)(wq & 0xFFu), d);
+                d = fmaf(xv[4 * q + 1], (float)((wq >> 8) & 0xFFu), d);
+                d = fmaf(xv[4 * q + 2], (float)((wq >> 16) & 0xFFu), d);
+                d = fmaf(xv[4 * q + 3], (float)(wq >> 24), d);
+            }
+            const uint32_t sw = live ? szv[j] : 0u;
+            acc = fmaf(h2f(sw), d, fmaf(h2f(sw >> 16), dx, acc));
+        } else {
+            float d = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const uint32_t wq = wv[j][q];
+                d = fmaf(xv[2 * q + 0], h2f(wq), d);
+                d = fmaf(xv[2 * q + 1], h2f(wq >> 16), d);
+            }
+            acc += live ? d : 0.0f;
+        }
+    }
+#pragma unroll
+    for (int o = LPR / 2; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+    if (li == 0 && row0 < M) apply_epi(J, row0, 0, acc);
+}
+
+template <int CPL, int Q>
+__global__ __launch_bounds__(256) void k_gemv_os(GemvJobs jobs) {
+    extern __shared__ float4 xs4[];
+    const int bid = blockIdx.x;
+    if (bid == 0 && jobs.side.src)
+        for (int i = threadIdx.x; i < jobs.side.n; i += 256) jobs.side.dst[i] = jobs.side.src[i];
+    int ji = 0;
+    while (ji + 1 < jobs.n && bid >= jobs.blk_start[ji + 1]) ji++;
+    const GemvJob &J = jobs.j[ji];
+    const int rb = bid - jobs.blk_start[ji];
+    if (J.fmt == FMT_I8) {
+        if (J.lpr == 32) gemv_os_body<FMT_I8, 32, CPL, Q>(J, rb, xs4);
+        else gemv_os_body<FMT_I8, 64, CPL, Q>(J, rb, xs4);
+    } else {
+        if (J.lpr == 32) gemv_os_body<FMT_F16, 32, CPL, Q>(J, rb, xs4);
+        else gemv_os_body<FMT_F16, 64, CPL, Q>(J, rb, xs4);
+    }
+}
+
+// B=1 launch on the one-shot kernel: LN-mix prologues become one pre-pass
+// launch writing each distinct mixed vector once.  Returns 1 when the jobs
+// do not fit this path (the caller then uses the general kernel).
+static int launch_os(rsv_ctx *ctx, GemvJobs &jobs) {
+    int cpl_max = 0, kmax = 0;
+    for (int i = 0; i < jobs.n; i++) {
+        GemvJob &J = jobs.j[i];
+        const int nc = J.K / (J.fmt == FMT_I8 ? 16 : 8);
+        J.lpr = nc <= 32 * 5 ? 32 : 64;
+        const int cpl = (nc + J.lpr - 1) / J.lpr;
+        if (cpl > 10 || J.K > 10240 || J.K % 4 != 0 || nc < J.lpr / 2) return 1;
+        cpl_max = std::max(cpl_max, cpl);
+        kmax = std::max(kmax, J.K);
+    }
+    // LN-mix pre-pass: every LN-mix job of the launch must share x, LN and
+    // token-shift row (true of the decode layer); mixes are de-duplicated by
+    // coefficient vector
+    MixArgs ma{};
+    for (int i = 0; i < jobs.n; i++) {
+        GemvJob &J = jobs.j[i];
+        if (J.pro != PRO_LNMIX) continue;
+        if (J.K > kMixMaxK) return 1;
+        if (ma.nmix == 0) {
+            ma.x = J.x; ma.gamma = J.gamma; ma.beta = J.beta; ma.prev = J.prev; ma.K = J.K;
+        } else if (ma.x != J.x || ma.gamma != J.gamma || ma.beta != J.beta || ma.prev != J.prev || ma.K != J.K) {
+            return 1;
+        }
+        if (J.lnout) {
+            if (ma.lnout && ma.lnout != J.lnout) return 1;
+            ma.lnout = J.lnout;
+        }
+        int m = 0;
+        while (m < ma.nmix && ma.coef[m] != J.coef) m++;
+        if (m == ma.nmix) {
+            ma.coef[m] = J.coef;
+            ma.out[m] = ctx->mix_buf + (size_t)m * kMixMaxK;
+            ma.nmix++;
+        }
+        J.x = ma.out[m];
+        J.pro = PRO_NONE;
+    }
+    if (ma.nmix) {
+        hipLaunchKernelGGL(k_lnmix_pre, dim3((ma.K / 4 + 255) / 256), dim3(256), 0, ctx->stream, ma);
+        RSV_HIP(hipGetLastError());
+    }
+    int total = 0;
+    for (int i = 0; i < jobs.n; i++) {
+        GemvJob &J = jobs.j[i];
+        const int rpb = 4 * (64 / J.lpr);
+        J.nblk = (J.M + rpb - 1) / rpb;
+        jobs.blk_start[i] = total;
+        total += J.nblk;
+    }
+    jobs.blk_start[jobs.n] = total;
+    const size_t lds = (size_t)kmax * 4;
+    if (cpl_max <= 5 && kmax <= 3072)
+        hipLaunchKernelGGL((k_gemv_os<5, 3>), dim3(total), dim3(256), lds, ctx->stream, jobs);
+    else
+        hipLaunchKernelGGL((k_gemv_os<10, 10>), dim3(total), dim3(256), lds, ctx->stream, jobs);
+    RSV_HIP(hipGetLastError());
+    return 0;
+}
+
 static int env_int(const char *name, int dflt) {
     const char *e = getenv(name);
     return (e && e[0]) ? atoi(e) : dflt;
 }
 
-static bool reg_disabled() {
-    static int v = -1;
-    if (v < 0) {
-        const char *e = getenv("RSV_GEMV_REG");
-        v = (e && e[0] == '0') ? 1 : 0;
-    }
-    return v == 1;
-}
 
 int launch_gemv_jobs(rsv_ctx *ctx, GemvJobs &jobs, int batch) {
     if (jobs.n <= 0 || jobs.n > kMaxJobs) return RSV_FAIL("gemv: bad job count %d", jobs.n);
@@ -782,7 +1007,16 @@ int launch_gemv_jobs(rsv_ctx *ctx, GemvJobs &jobs, int batch) {
         if (nc > ncmax) ncmax = nc;
     }
     if (jobs.side.src && (!jobs.side.dst || jobs.side.n <= 0)) return RSV_FAIL("gemv: bad side copy");
-    if (batch == 1 && !reg_disabled()) {
+    // B=1: launches with an LN-mix prologue take the register-resident kernel
+    // (the prologue runs inside it), the others the one-shot kernel
+    static const int b1_kernel = env_int("RSV_GEMV_B1", 3);  // 3 by prologue, 2 one-shot, 1 register, 0 general
+    bool lnmix = false;
+    for (int i = 0; i < jobs.n; i++) lnmix |= jobs.j[i].pro == PRO_LNMIX;
+    if (batch == 1 && (b1_kernel == 2 || (b1_kernel == 3 && !lnmix))) {
+        const int rc = launch_os(ctx, jobs);
+        if (rc <= 0) return rc;
+    }
+    if (batch == 1 && b1_kernel >= 1) {
         bool ok = true;
         for (int i = 0; i < jobs.n && ok; i++) {
             GemvJob &J = jobs.j[i];

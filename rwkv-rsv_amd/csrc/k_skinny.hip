@@ -13,6 +13,7 @@
 // k-values (k0 + 16g .. +15) of its weight row and of its session's x row;
 // MFMA step s (0..3) consumes values 4s..4s+3 of both.  A and B use the same
 // k permutation, so the products pair up exactly.
+#include <algorithm>
 #include <cstdlib>
 
 #include "rsv_common.h"
@@ -283,7 +284,8 @@ __global__ __launch_bounds__(256) void k_skinny4(SkinnyJobs jobs, int MB, float 
     constexpr int tbytes = I8 ? 1024 : 2048;
     const uint8_t *wt = (const uint8_t *)J.w + ((size_t)rt_glob * nchunks) * tbytes + lane * (I8 ? 16 : 32);
     const bool row_ok = row < J.N;
-    const uint32_t *szrow = I8 ? J.sz + (size_t)(row_ok ? row : 0) * (J.K / 128) : nullptr;
+    // tiled scale/zero: [row tile][group][32 rows]
+    const uint32_t *szrow = I8 ? J.sz + (size_t)rt_glob * (J.K / 128) * 32 + (lane & 31) : nullptr;
 
     sk_f16x acc[MT];
 #pragma unroll
@@ -304,7 +306,7 @@ __global__ __launch_bounds__(256) void k_skinny4(SkinnyJobs jobs, int MB, float 
                 const sk_u32x4 *p = (const sk_u32x4 *)(wt + (size_t)c * tbytes);
 #pragma unroll
                 for (int v = 0; v < WV; v++) w[q][v] = __builtin_nontemporal_load(p + v);
-                if (I8) sz[q] = szrow[(c * 32) / 128];
+                if (I8) sz[q] = szrow[(size_t)(c >> 2) * 32];
             } else {
 #pragma unroll
                 for (int v = 0; v < WV; v++) w[q][v] = (sk_u32x4){0u, 0u, 0u, 0u};
@@ -397,6 +399,192 @@ __global__ __launch_bounds__(256) void k_skinny4(SkinnyJobs jobs, int MB, float 
     const int n0 = rg * 128;
     if (J.split > 1) {
         float *wsp = ws + ((size_t)J.ws_slot + (size_t)rg * J.split + sl) * 128 * TB;
+#ifdef RSV_X_NOEPI
+        if (tid == 0) wsp[0] = tile[0][0];
+        return;
+#endif
+        for (int o = tid; o < 128 * TB; o += 256) wsp[o] = tile[o & 127][o >> 7];
+        return;
+    }
+    for (int o = tid; o < 128 * TB; o += 256) {
+        const int r = o & 127, b = o >> 7;
+        const int n = n0 + r;
+        if (n >= J.N || b >= MB) continue;
+        const size_t yo = (size_t)b * J.ldy + n;
+        const float v = sk_epilogue(J, tile[r][b], n, yo);
+        if (J.y_f16)
+            ((_Float16 *)J.y)[yo] = (_Float16)v;
+        else
+            ((float *)J.y)[yo] = v;
+        if (J.y2) J.y2[yo] = v;
+    }
+}
+
+// ------------------------------------------------------------------ v5
+// Batched decode GEMM, weights in the MFMA-tiled copy (see v4).  Block = 4
+// waves = 4 row tiles (128 rows) on one k-slice of J.kslice chunks:
+//   1. the block's whole x slab (batch x slice columns, fp16) is staged in
+//      LDS once, with one barrier, so the weight stream never waits on x;
+//   2. each wave streams its row tile's chunks through a PD-deep register
+//      ring (no barriers; the prefetch past the slice end re-reads the last
+//      chunk instead of branching, so no load waits on a join);
+//   3. v_mfma_f32_32x32x16_f16: lane (i = l%32, g = l/32) supplies columns
+//      16g + 8s .. +7 of step s for both operands, so A and B pair up;
+//   4. split k-slices write partial tiles that k_skinny4_reduce (a second
+//      launch over many blocks) adds in slice order, so the result does not
+//      depend on timing.
+typedef _Float16 sk_half8 __attribute__((ext_vector_type(8)));
+
+template <int MT, bool I8>
+__global__ __launch_bounds__(256) void k_skinny5(SkinnyJobs jobs, int MB, float *__restrict__ ws) {
+    constexpr int TB = MT * 32;
+#ifndef SK_PD
+#define SK_PD 8
+#endif
+    constexpr int PD = I8 ? SK_PD : 6;    // chunks in flight per wave
+    constexpr int WV = I8 ? 1 : 2;    // 16-byte loads per lane per chunk
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem5[];
+    const int bid = blockIdx.x;
+    int ji = 0;
+    while (ji + 1 < jobs.n && bid >= jobs.blk_start[ji + 1]) ji++;
+    const SkinnyJob &J = jobs.j[ji];
+    const int local = bid - jobs.blk_start[ji];
+    const int rg = local / J.split, sl = local - (local / J.split) * J.split;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 5;
+    const int nchunks = J.K / 32;
+    const int c_lo = sl * J.kslice, c_hi = min(nchunks, c_lo + J.kslice);
+    const int nloc = c_hi - c_lo;
+    const int XS = J.kslice * 32 + 8;  // LDS row stride (halves) of the x slab
+    _Float16 *xs = reinterpret_cast<_Float16 *>(smem5);
+    float (*tile)[TB + 1] = reinterpret_cast<float (*)[TB + 1]>(smem5);
+    const int rt_glob = rg * 4 + wave;
+    const int row = rt_glob * 32 + (lane & 31);
+    constexpr int tbytes = I8 ? 1024 : 2048;
+    const uint8_t *wt = (const uint8_t *)J.w + ((size_t)rt_glob * nchunks) * tbytes + lane * (I8 ? 16 : 32);
+    const bool row_ok = row < J.N;
+    // tiled scale/zero: [row tile][group][32 rows], one 128-byte line per group
+    const uint32_t *szrow = I8 ? J.sz + (size_t)min(rt_glob, (J.N - 1) / 32) * (J.K / 128) * 32 + (lane & 31) : nullptr;
+
+    // 2a. first PD chunks of weights go out before the x slab
+    sk_u32x4 wr[PD][WV];
+    uint32_t sr[PD];
+    // rows past N read row 0 of the tile and chunks past the slice re-read
+    // its last chunk; both are masked to zero in compute(), so no load sits
+    // behind a branch
+    const uint8_t *wt_ok = row_ok ? wt : (const uint8_t *)J.w + (size_t)lane * (I8 ? 16 : 32);
+    auto load_w = [&](int p, int c) {
+        c = min(c, c_hi - 1);
+        const sk_u32x4 *q = (const sk_u32x4 *)(wt_ok + (size_t)c * tbytes);
+#ifdef SK_NONT
+#pragma unroll
+        for (int v = 0; v < WV; v++) wr[p][v] = q[v];
+#else
+#pragma unroll
+        for (int v = 0; v < WV; v++) wr[p][v] = __builtin_nontemporal_load(q + v);
+#endif
+        if (I8) sr[p] = szrow[(size_t)(c >> 2) * 32];
+    };
+#pragma unroll
+    for (int p = 0; p < PD; p++) load_w(p, c_lo + p);
+
+    // 1. x slab: TB rows x nloc*32 halves in 16-byte pieces, every load of
+    // the thread issued before the first LDS store (kslice <= 16 chunks)
+    {
+        constexpr int NP = TB * 16 * 4 / 256;  // pieces per thread at the largest slice
+        const int pieces_row = nloc * 4;
+        const int total = TB * pieces_row;
+        sk_u32x4 xv[NP];
+#pragma unroll
+        for (int i = 0; i < NP; i++) {
+            const int e = tid + 256 * i;
+            const int b = e / pieces_row, pc = e - b * pieces_row;
+#ifdef RSV_X_NOSLAB
+            xv[i] = (sk_u32x4){(unsigned)e, 0u, 0u, 0u};
+            continue;
+#endif
+            xv[i] = (e < total && b < MB) ? *(const sk_u32x4 *)(J.x + (size_t)b * J.ldx + c_lo * 32 + pc * 8)
+                                          : (sk_u32x4){0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int i = 0; i < NP; i++) {
+            const int e = tid + 256 * i;
+            const int b = e / pieces_row, pc = e - b * pieces_row;
+            if (e < total) *(sk_u32x4 *)&xs[(size_t)b * XS + pc * 8] = xv[i];
+        }
+    }
+    __syncthreads();
+
+    sk_f16x acc[MT];
+#pragma unroll
+    for (int ct = 0; ct < MT; ct++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) acc[ct][e] = 0.0f;
+
+    auto compute = [&](int p, int cl) {  // cl: chunk index within the slice
+        const bool live = row_ok && cl < nloc;
+        cl = min(cl, nloc - 1);
+        uint32_t wh[8];
+#ifdef RSV_X_NODQ
+        if (I8) {
+            for (int h = 0; h < 4; h++) { wh[2 * h] = wr[p][0][h] ^ sr[p]; wh[2 * h + 1] = wr[p][0][h]; }
+        } else
+#endif
+        if (I8) {
+            const float s = live ? sk_h2f(sr[p]) : 0.0f, z = live ? sk_h2f(sr[p] >> 16) : 0.0f;
+#pragma unroll
+            for (int h = 0; h < 4; h++) {
+                const uint32_t u = wr[p][0][h];
+                wh[2 * h] = sk_pack(fmaf(s, (float)(u & 0xFFu), z), fmaf(s, (float)((u >> 8) & 0xFFu), z));
+                wh[2 * h + 1] = sk_pack(fmaf(s, (float)((u >> 16) & 0xFFu), z), fmaf(s, (float)(u >> 24), z));
+            }
+        } else {
+#pragma unroll
+            for (int h = 0; h < 4; h++) {
+                wh[h] = live ? wr[p][0][h] : 0u;
+                wh[4 + h] = live ? wr[p][WV - 1][h] : 0u;
+            }
+        }
+#pragma unroll
+        for (int st = 0; st < 2; st++) {
+            const sk_half8 a = __builtin_bit_cast(sk_half8, (sk_u32x4){wh[4 * st], wh[4 * st + 1], wh[4 * st + 2], wh[4 * st + 3]});
+#pragma unroll
+            for (int ct = 0; ct < MT; ct++) {
+                const sk_u32x4 xv = *(const sk_u32x4 *)&xs[(size_t)(ct * 32 + (lane & 31)) * XS + cl * 32 + 16 * g + 8 * st];
+#ifdef RSV_X_NOMMA
+                acc[ct][0] += __uint_as_float((wh[4 * st] ^ xv[0]) & 0x0FFFFFFFu);
+#else
+                acc[ct] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, __builtin_bit_cast(sk_half8, xv), acc[ct], 0, 0, 0);
+#endif
+            }
+        }
+    };
+
+    // branch-free body: the trip count is rounded up to PD and the extra
+    // chunks contribute zero
+    for (int base = 0; base < nloc; base += PD) {
+#pragma unroll
+        for (int p = 0; p < PD; p++) {
+            compute(p, base + p);
+            load_w(p, c_lo + base + p + PD);
+        }
+    }
+    __syncthreads();  // x slab dead: the LDS becomes the output tile
+
+    // wave w owns tile rows 32w .. 32w+31: acc[ct][e] -> (row 32w + 8*(e/4) + 4g + e%4, col ct*32 + lane%32)
+#pragma unroll
+    for (int ct = 0; ct < MT; ct++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) tile[wave * 32 + 8 * (e >> 2) + 4 * g + (e & 3)][ct * 32 + (lane & 31)] = acc[ct][e];
+    __syncthreads();
+    const int n0 = rg * 128;
+    if (J.split > 1) {
+        // slice tile, row-group-major then slice: [rg][sl][128 rows][TB sessions];
+        // k_skinny4_reduce (the next launch) sums the slices in slice order
+        float *wsp = ws + ((size_t)J.ws_slot + (size_t)rg * J.split + sl) * 128 * TB;
+#ifdef RSV_X_NOEPI
+        if (tid == 0) wsp[0] = tile[0][0];
+        return;
+#endif
         for (int o = tid; o < 128 * TB; o += 256) wsp[o] = tile[o & 127][o >> 7];
         return;
     }
@@ -429,8 +617,17 @@ __global__ __launch_bounds__(256) void k_skinny4_reduce(SkinnyJobs jobs, int MB,
         const int r = o & 127, b = o >> 7;
         const int n = rg * 128 + r;
         if (n >= J.N || b >= MB) return;
-        float v = base[o];
-        for (int q = 1; q < J.split; q++) v += base[(size_t)q * 128 * TB + o];
+        // partials are loaded 8 at a time (all in flight together) and added
+        // in slice order
+        float v = 0.0f;
+        for (int q0 = 0; q0 < J.split; q0 += 8) {
+            float part[8];
+#pragma unroll
+            for (int q = 0; q < 8; q++) part[q] = q0 + q < J.split ? base[(size_t)(q0 + q) * 128 * TB + o] : 0.0f;
+#pragma unroll
+            for (int q = 0; q < 8; q++)
+                if (q0 + q < J.split) v = q0 + q == 0 ? part[q] : v + part[q];
+        }
         const size_t yo = (size_t)b * J.ldy + n;
         v = sk_epilogue(J, v, n, yo);
         if (J.y_f16)
@@ -464,7 +661,31 @@ __global__ void k_tile_weights(const uint8_t *__restrict__ src, uint8_t *__restr
     }
 }
 
+// Tiled copy of an int8 scale/zero array [n, k/128] for k_skinny4/5:
+// [row tile][group][32 rows], so the 32 rows of a tile read one 128-byte
+// line per group.  Rows beyond n are zero.
+__global__ void k_tile_sz(const uint32_t *__restrict__ src, uint32_t *__restrict__ dst, int n, int groups) {
+    const size_t total = (size_t)((n + 31) / 32) * groups * 32;
+    for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (size_t)gridDim.x * blockDim.x) {
+        const int r = (int)(e % 32);
+        const size_t t = e / 32;
+        const int gq = (int)(t % groups), rt = (int)(t / groups);
+        const int row = rt * 32 + r;
+        dst[e] = row < n ? src[(size_t)row * groups + gq] : 0u;
+    }
+}
+
 int launch_tile_weights(rsv_ctx *ctx, const void *src, void *dst, int n, int k, int esz) {
+    if (esz == 4) {
+        if (k % 128 != 0) return RSV_FAIL("tile_weights: k=%d must be a multiple of 128 for scale/zero", k);
+        const size_t total = (size_t)((n + 31) / 32) * (k / 128) * 32;
+        size_t blocks = (total + 255) / 256;
+        if (blocks > 65536) blocks = 65536;
+        hipLaunchKernelGGL(k_tile_sz, dim3((unsigned)blocks), dim3(256), 0, ctx->stream, (const uint32_t *)src,
+                           (uint32_t *)dst, n, k / 128);
+        RSV_HIP(hipGetLastError());
+        return 0;
+    }
     if (k % 32 != 0) return RSV_FAIL("tile_weights: k=%d must be a multiple of 32", k);
     const size_t total = (size_t)((n + 31) / 32) * (k / 32) * 64;
     size_t blocks = (total + 255) / 256;
@@ -507,9 +728,95 @@ int launch_skinny(rsv_ctx *ctx, SkinnyJobs &jobs, int MB) {
     return 0;
 }
 
+// v5 launch of tiled jobs.  Each job's k-slice count is set so that the
+// launch has about two blocks per CU, with slices of 8..16 chunks when the
+// row count allows (16 chunks = the LDS x slab limit, 8 = enough chunks per
+// wave to amortise the slab and the partial-tile traffic).
+#ifndef SK_KMAX
+#define SK_KMAX 16
+#endif
+static int launch_v5(rsv_ctx *ctx, SkinnyJobs &jobs, int MB) {
+    const int TB = MB <= 32 ? 32 : 64;
+    const int cus = ctx->sm_count > 0 ? ctx->sm_count : 256;
+    const int target = 2 * cus;
+    int64_t W = 0;
+    for (int i = 0; i < jobs.n; i++) {
+        const SkinnyJob &J = jobs.j[i];
+        W += (int64_t)((J.N + 127) / 128) * (J.K / 32);
+    }
+    int total = 0, red_total = 0;
+    size_t ws_need = 0, lds = 0;
+    for (int i = 0; i < jobs.n; i++) {
+        SkinnyJob &J = jobs.j[i];
+        const int rgs = (J.N + 127) / 128;
+        const int nch = J.K / 32;
+        int split = (int)(((int64_t)target * nch + W - 1) / W);
+        split = std::min(split, std::max(1, nch / 8));
+        split = std::max(split, (nch + SK_KMAX - 1) / SK_KMAX);
+        int kslice = (nch + split - 1) / split;
+        if (kslice > 8) kslice = std::min(SK_KMAX, (kslice + 7) / 8 * 8);  // whole prefetch rounds
+        split = (nch + kslice - 1) / kslice;
+        J.split = split;
+        J.kslice = kslice;
+        J.ws_slot = (int)(ws_need / (128 * (size_t)TB));
+        J.nblk = rgs * split;
+        jobs.blk_start[i] = total;
+        total += J.nblk;
+        jobs.red_start[i] = red_total;
+        if (split > 1) {
+            ws_need += (size_t)rgs * split * 128 * TB;
+            red_total += rgs * (128 * TB / 256);
+        }
+        lds = std::max(lds, std::max((size_t)TB * (kslice * 32 + 8) * 2, (size_t)128 * (TB + 1) * 4));
+    }
+    jobs.blk_start[jobs.n] = total;
+    jobs.red_start[jobs.n] = red_total;
+    if (ws_need > ctx->skinny_ws_cap) return RSV_FAIL("skinny gemm: workspace too small (%zu floats)", ws_need);
+    const bool i8 = jobs.j[0].fmt == FMT_I8;
+    for (int i = 1; i < jobs.n; i++)
+        if ((jobs.j[i].fmt == FMT_I8) != i8) return RSV_FAIL("skinny gemm: mixed formats in one tiled launch");
+    if (MB <= 32) {
+        if (i8) hipLaunchKernelGGL((k_skinny5<1, true>), dim3(total), dim3(256), lds, ctx->stream, jobs, MB, ctx->skinny_ws);
+        else hipLaunchKernelGGL((k_skinny5<1, false>), dim3(total), dim3(256), lds, ctx->stream, jobs, MB, ctx->skinny_ws);
+    } else {
+        if (i8) hipLaunchKernelGGL((k_skinny5<2, true>), dim3(total), dim3(256), lds, ctx->stream, jobs, MB, ctx->skinny_ws);
+        else hipLaunchKernelGGL((k_skinny5<2, false>), dim3(total), dim3(256), lds, ctx->stream, jobs, MB, ctx->skinny_ws);
+    }
+    RSV_HIP(hipGetLastError());
+    if (red_total) {
+        if (MB <= 32)
+            hipLaunchKernelGGL(k_skinny4_reduce<1>, dim3(red_total), dim3(256), 0, ctx->stream, jobs, MB, ctx->skinny_ws);
+        else
+            hipLaunchKernelGGL(k_skinny4_reduce<2>, dim3(red_total), dim3(256), 0, ctx->stream, jobs, MB, ctx->skinny_ws);
+        RSV_HIP(hipGetLastError());
+    }
+    return 0;
+}
+
 static int launch_slab(rsv_ctx *ctx, SkinnyJobs &jobs, int MB) {
     if (MB <= 0 || MB > 64) return RSV_FAIL("skinny gemm: batch %d outside 1..64", MB);
     if (jobs.n <= 0 || jobs.n > kMaxJobs) return RSV_FAIL("skinny gemm: bad job count %d", jobs.n);
+    static const int use_v5 = [] {
+        const char *e = getenv("RSV_SKINNY_V5");
+        return e ? atoi(e) : 1;
+    }();
+    if (use_v5 && jobs.j[0].tiled) {
+        // jobs with at least two row groups per CU need no k-split: they stay
+        // on the v4 path, whose x window is not bounded by the LDS slab
+        bool big = false;
+        const int cus = ctx->sm_count > 0 ? ctx->sm_count : 256;
+        for (int i = 0; i < jobs.n; i++) big |= (jobs.j[i].N + 127) / 128 >= 2 * cus;
+        bool ok = true;
+        for (int i = 0; i < jobs.n; i++) {
+            const SkinnyJob &J = jobs.j[i];
+            ok &= J.tiled && J.w && J.x && J.y && J.N > 0 && J.K > 0 && J.K % 32 == 0 && J.ldx % 8 == 0 &&
+                  J.ldx >= J.K && (J.fmt != FMT_I8 || (J.K % 128 == 0 && J.sz)) &&
+                  !((J.epi == GE_BIAS || J.epi == GE_WDECAY || J.epi == GE_SIGBIAS || J.epi == GE_VLERP) && !J.bias) &&
+                  !(J.epi == GE_VLERP && !J.aux) && !(J.epi == GE_WDECAY && !J.scale) &&
+                  !(J.y_f16 && (J.epi == GE_ADD || J.epi == GE_VLERP));
+        }
+        if (!big && ok) return launch_v5(ctx, jobs, MB);
+    }
     static const int max_split = [] {
         const char *e = getenv("RSV_SKINNY_MAX_SPLIT");
         return e ? atoi(e) : 16;

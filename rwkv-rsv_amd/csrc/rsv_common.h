@@ -71,8 +71,10 @@ struct GemvJob {
     int ldx, ldy;  // batch strides in elements
     int nblk;      // blocks along M (filled by the launcher)
     int ks;        // k-slices per row (register-resident B=1 kernel; filled by the launcher)
+    int lpr;       // lanes per row (one-shot B=1 kernel; filled by the launcher)
 };
 constexpr int kMaxJobs = 8;
+constexpr int kMixMaxK = 16384;  // longest row the B=1 LN-mix pre-pass serves
 // A side copy done by the first block column of a launch: dst[b, :n] =
 // src[b, :n] for the launch's batch rows (moves a token-shift LN row from a
 // scratch buffer into the state once no block of the launch reads it).
@@ -112,6 +114,8 @@ struct rsv_ctx {
     // with the context so that graph capture never allocates)
     float *skinny_ws = nullptr;
     size_t skinny_ws_cap = 0;
+    // LN-mix vectors of a B=1 GEMV launch (kMaxJobs x kMixMaxK floats)
+    float *mix_buf = nullptr;
 };
 
 namespace rsv {
@@ -204,7 +208,8 @@ struct SkinnyJob {
     float *y2;          // optional fp32 copy of the result
     const float *bias, *aux, *scale;
     int N, K, epi, nblk;
-    int split, ws_off, ws_slot;  // k-slices per row group; (unused); first workspace tile
+    int split, ws_slot;  // k-slices per row group; first workspace tile
+    int kslice;                    // k-chunks (of 32) per slice
     int tiled;                   // weights are the MFMA-tiled copy
 };
 struct SkinnyJobs {

@@ -547,7 +547,18 @@ def test_gemm_skinny(be, batch):
     X = x.astype(np.float64)
     Wq = W.astype(np.float16).astype(np.float64)
     sig = lambda t: 1 / (1 + np.exp(-t))
-    for wname, w8, w16id, Wm in (("i8", ctypes.pointer(h), NONE, Wq), ("f16", None, w16, W16.astype(np.float64))):
+    # MFMA-tiled copies (weights and, for int8, the scale/zero words)
+    ht = rsv.Int8Handle(h.idx, h.sz, h.m, h.k)
+    out = ctypes.c_uint32()
+    be.call("rsv_tile_weights", h.idx, n, k, 1, ctypes.byref(out))
+    ht.idx = out.value
+    be.call("rsv_tile_weights", h.sz, n, k, 4, ctypes.byref(out))
+    ht.sz = out.value
+    be.call("rsv_tile_weights", w16, n, k, 2, ctypes.byref(out))
+    w16t = out.value
+    cases = (("i8", ctypes.pointer(h), NONE, Wq, 0), ("f16", None, w16, W16.astype(np.float64), 0),
+             ("i8-tiled", ctypes.pointer(ht), NONE, Wq, 1), ("f16-tiled", None, w16t, W16.astype(np.float64), 1))
+    for wname, w8, w16id, Wm, tiled in cases:
         acc = X @ Wm.T
         for epi, init, ref in [(0, None, acc), (1, None, acc + bias), (2, y0, y0 + acc),
                                (3, None, np.maximum(acc, 0) ** 2), (4, None, np.tanh(acc)),
@@ -555,13 +566,13 @@ def test_gemm_skinny(be, batch):
                                (7, y0, y0 + sig(acc + bias) * (aux - y0)), (8, None, sig(acc))]:
             y = be.tensor(init if init is not None else np.zeros((batch, n), np.float32))
             y2 = be.tensor(n=batch * n)
-            j = rsv.MmJob(w16id, w8, n, k, xt, y, y2, epi, bt, at, st)
+            j = rsv.MmJob(w16id, w8, n, k, xt, y, y2, epi, bt, at, st, tiled)
             be.call("rsv_gemm_skinny", ctypes.byref(j), 1, batch)
             got = be.get(y, batch * n).reshape(batch, n)
             assert rel_err(got, ref) < 2e-5, (wname, epi)
             assert np.array_equal(be.get(y2, batch * n), got.reshape(-1))
         y16 = be.tensor(n=batch * n, dtype=rsv.F16)
-        j = rsv.MmJob(w16id, w8, n, k, xt, y16, NONE, 4, NONE, NONE, NONE)
+        j = rsv.MmJob(w16id, w8, n, k, xt, y16, NONE, 4, NONE, NONE, NONE, tiled)
         be.call("rsv_gemm_skinny", ctypes.byref(j), 1, batch)
         assert rel_err(be.get(y16, batch * n).reshape(batch, n), np.tanh(acc)) < 2e-3
 
