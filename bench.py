@@ -26,6 +26,10 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path[:0] = [os.path.join(ROOT, "rwkv-rsv_amd"), os.path.join(ROOT, "oracle")]
 
 HBM_PEAK_GBS = 8000.0
+# HBM bytes per launch of the dominant kernel, from the two rocprofv3 --pmc
+# passes (FETCH_SIZE, WRITE_SIZE) of `bench.py --kernel-only`, scaled by the
+# same counters of a plain 64 MiB copy; profiles/ffn_key_gemv_b1.md
+FFN_KEY_TRAFFIC = 29001184
 NONE = 0xFFFFFFFF
 
 
@@ -98,17 +102,32 @@ def kernel_leg(reps=200):
     for _ in range(10):
         be.call("rsv_gemv_multi", ctypes.byref(j), 1, NONE, NONE, 0, 1)
     be.sync()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
+    # the launches are captured into one HIP graph so that host enqueue time
+    # does not leak into the measurement; the graph is replayed once untimed
+    be.call("rsv_graph_begin")
     for _ in range(reps):
         be.call("rsv_gemv_multi", ctypes.byref(j), 1, NONE, NONE, 0, 1)
+    be.call("rsv_graph_end")
+    be.call("rsv_graph_replay")
+    be.sync()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    be.call("rsv_graph_replay")
     e1.record(stream)
     e1.synchronize()
     us = e0.elapsed_time(e1) * 1000.0 / reps
     be.close()
+    # a plain device copy of known size: the reference point that scales the
+    # rocprofv3 FETCH_SIZE / WRITE_SIZE counters of this run to bytes
+    src = torch.empty(16 << 20, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(4):
+        dst.copy_(src)
+    torch.cuda.synchronize()
     nbytes = ffn_key_bytes(C, F)
     return dict(kernel="k_gemv_reg<5,2,3> (B=1 ffn.key: LN2 + token-shift mix prologue, int8 10240x2560, relu^2)",
-                avg_us=us, bytes=nbytes, gbs=nbytes / us / 1e3, launches=reps)
+                avg_us=us, bytes=nbytes, gbs=nbytes / us / 1e3, launches=reps,
+                timing="HIP events around one replay of a graph of the launches, on the backend stream")
 
 
 def main():
@@ -247,7 +266,7 @@ def main():
                    "n_layer": 32, "d_model": 2560, "heads": 40, "ffn": 10240, "vocab": 65536,
                    "batch": 1, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(kl["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(kl["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(kl["gbs"] / HBM_PEAK_GBS, 4), "traffic": FFN_KEY_TRAFFIC,
                      "kernel": kl["kernel"], "avg_us": round(kl["avg_us"], 3), "bytes_per_launch": kl["bytes"],
                      "step_achieved_gbs": round(bytes1 / (ms / args.steps / 1000) / 1e9, 1),
                      "step_frac": round(bytes1 / (ms / args.steps / 1000) / 1e9 / HBM_PEAK_GBS, 4)},
