@@ -138,6 +138,9 @@ def main():
     ap.add_argument("--steps-b64", type=int, default=200)
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-serve", action="store_true")
+    ap.add_argument("--serve-decode", type=int, default=256,
+                    help="tokens sampled per session in the configs[4] ragged-serving leg")
     ap.add_argument("--cpu-tokens", type=int, default=4)
     ap.add_argument("--cache", default=os.environ.get("RSV_BENCH_CACHE", "/tmp"))
     ap.add_argument("--kernel-only", action="store_true",
@@ -224,6 +227,36 @@ def main():
         log(f"prefill: {lens.sum()} tokens in {dt:.3f}s -> {prefill['tok_s']:.0f} tok/s")
         SP.free()
 
+    # ---------------- ragged continuous batching
+    serve = None
+    if not args.no_serve:
+        rng = np.random.Generator(np.random.PCG64(2))
+        lens = rng.integers(16, 2049, size=64)
+        pr = [synth.prompt(cfg, int(n), seed=1000 + i) for i, n in enumerate(lens)]
+        SV = bundle.create_batch_state(64)
+        sp = rsv.SamplerParams(temperature=1.0, top_k=0, top_p=0.9)
+        seeds = np.arange(64, dtype=np.uint32) * 7919 + 2
+        bundle.serve_ragged(SV, [p[:16] for p in pr], 2, sp, seeds, budget=4096)  # warm-up
+        SV.reset()
+        t0 = time.perf_counter()
+        toks, steps = bundle.serve_ragged(SV, pr, args.serve_decode, sp, seeds, budget=4096)
+        wall = time.perf_counter() - t0
+        sms = np.array([st["ms"] for st in steps])
+        pre = np.array([st["prefill_tokens"] for st in steps])
+        dec = np.array([st["decode_tokens"] for st in steps])
+        only_dec = pre == 0
+        serve = dict(sessions=64, prompt_tokens=int(lens.sum()), decode_per_session=args.serve_decode,
+                     steps=len(steps), wall_s=round(wall, 3),
+                     prefill_tok_s=round(float(pre.sum() / (sms[pre > 0].sum() / 1e3)), 1),
+                     decode_tok_s=round(float(dec[only_dec].sum() / (sms[only_dec].sum() / 1e3)), 1)
+                     if only_dec.any() else None,
+                     total_tok_s=round(float((pre.sum() + dec.sum() + 64) / wall), 1),
+                     p50_step_ms=round(float(np.percentile(sms, 50)), 3),
+                     p99_step_ms=round(float(np.percentile(sms, 99)), 3),
+                     sampler="GPU top-p 0.9, T=1.0, seed of token k of session q = seeds[q] + k")
+        log(f"serve: {serve}")
+        SV.free()
+
     # ---------------- dominant kernel (roofline)
     kl = kernel_leg()
     log(f"kernel: {kl['kernel']}: {kl['avg_us']:.2f} us/launch, {kl['gbs']:.0f} GB/s")
@@ -274,7 +307,7 @@ def main():
         "extra": {"b1_wall_tok_s": round(b1_wall_tps, 2),
                   "b64_tok_s": round(b64_tps, 1), "b64_ms_per_step": round(ms64 / args.steps_b64, 4),
                   "b64_hbm_frac": round(bytes64 / (ms64 / args.steps_b64 / 1000) / 1e9 / HBM_PEAK_GBS, 4),
-                  "prefill": prefill},
+                  "prefill": prefill, "serve_ragged": serve},
     }
     print(json.dumps(out))
     bundle.close()

@@ -87,6 +87,23 @@ int rsv_argmax_selfloop_batch(rsv_bundle *b, rsv_state *s, const uint32_t *seeds
 int rsv_sample_selfloop_batch(rsv_bundle *b, rsv_state *s, const uint32_t *seeds, uint64_t n,
                               const rsv_sampler_params *sp, uint32_t *out);
 
+/* Ragged continuous batching (the north star's scheduler; no counterpart
+ * in the reference, which pads batch prefill, gpu_model.rs:914-997).  Slot q
+ * of s serves prompt q (tokens packed, lens[batch]) and then samples
+ * decode_len tokens into out[q*decode_len ...].  Each step is one packed
+ * dispatch: a decode token for every generating slot, then prompt chunks
+ * (slots in order, split across steps when needed), budget tokens in all
+ * (budget >= batch, <= 4096).  The GPU sampler (sp) draws token k of slot q
+ * with seed seeds[q] + k.  steps (optional, max_steps entries) receives one
+ * record per step; *nsteps the step count. */
+typedef struct rsv_serve_step {
+    uint64_t prefill_tokens, decode_tokens, sampled;
+    double ms; /* host wall time of the step: dispatch, sampling, token download */
+} rsv_serve_step;
+int rsv_serve_ragged(rsv_bundle *b, rsv_state *s, const uint32_t *tokens, const uint64_t *lens, uint64_t decode_len,
+                     const rsv_sampler_params *sp, const uint32_t *seeds, uint64_t budget, uint32_t *out,
+                     rsv_serve_step *steps, uint64_t max_steps, uint64_t *nsteps);
+
 /* Timed variants for benchmarks: run the self-loop with the graph already
  * captured, synchronising before and after, and report device-side elapsed
  * milliseconds through *ms (hipEvent timing on the context stream). */

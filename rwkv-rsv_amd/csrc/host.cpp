@@ -25,6 +25,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -268,6 +269,7 @@ struct WorkBufs {
 };
 
 constexpr uint64_t kMmBatch = 16;  // sessions from which decode GEMMs run on MFMA
+constexpr uint64_t kSmallPrefill = 128;  // packed prefill rows that still take the decode MFMA kernel
 
 struct SeqBufs {
     uint64_t cap = 0, segcap = 0;
@@ -295,6 +297,7 @@ struct rsv_bundle {
     std::map<uint64_t, WorkBufs> bufs;
     SeqBufs seq;
     std::vector<uint32_t> owned;  // every tensor the bundle created
+    bool tiled = false;           // MFMA-tiled weight copies made (tile_model)
 
     ~rsv_bundle() {
         if (ctx) rsv_destroy(ctx);
@@ -772,6 +775,7 @@ int tile_linear(rsv_bundle *b, Linear &L) {
 // MFMA-tiled weight copies for the batched decode path (extra device memory
 // of the size of the weights; HBM is not the constraint on this GPU).
 int tile_model(rsv_bundle *b) {
+    if (b->tiled) return 0;
     const rsv_model_info &I = b->info;
     const uint64_t C = I.n_embd;
     for (auto &L : b->layers) {
@@ -788,6 +792,7 @@ int tile_model(rsv_bundle *b) {
     }
     HK(tile_linear(b, b->head));
     CK(rsv_synchronize(b->ctx));
+    b->tiled = true;
     return 0;
 }
 
@@ -904,8 +909,9 @@ int gemm_lin(rsv_bundle *b, const Linear &L, uint32_t a, uint32_t c, uint64_t m,
 }
 
 // Packed prefill of non-empty segments into state slots; logits (optional)
-// receives nseg*vocab floats (last token of each segment).
-int prefill(rsv_bundle *b, GpuState &s, const std::vector<Seg> &segs, float *logits) {
+// receives nseg*vocab floats (last token of each segment).  With head set
+// and no host buffer the logits stay on the device in b->seq.logits.
+int prefill(rsv_bundle *b, GpuState &s, const std::vector<Seg> &segs, float *logits, bool head = false) {
     rsv_ctx *c = b->ctx;
     const rsv_model_info &I = b->info;
     const uint64_t C = I.n_embd, H = I.n_head, N = I.head_size;
@@ -917,6 +923,12 @@ int prefill(rsv_bundle *b, GpuState &s, const std::vector<Seg> &segs, float *log
     }
     const uint64_t S = segs.size();
     if (S == 0) return 0;
+    // Short packed batches (decode tokens of ragged serving, small prompt
+    // chunks) run their weight products on the batched-decode matrix-core
+    // kernel, which streams each weight once per 64 rows; longer ones on the
+    // prefill GEMM.
+    const bool small = T <= kSmallPrefill;
+    if (small) HK(tile_model(b));
     HK(get_seq(b, T, S));
     SeqBufs &q = b->seq;
     std::vector<uint32_t> tok(T), prev(T), st(S), ln(S), sl(S), last(S);
@@ -947,36 +959,68 @@ int prefill(rsv_bundle *b, GpuState &s, const std::vector<Seg> &segs, float *log
         CK(rsv_seq_norm_mix(c, q.x, s.tmix_x[i], L.ln1_w, L.ln1_b, coef6, q.mix, 6, q.row_prev, T, C, LN_EPS));
         CK(rsv_seq_state_store(c, q.x, s.tmix_x[i], L.ln1_w, L.ln1_b, q.seg_last, q.seg_slot, S, C, LN_EPS));
         const uint32_t xr = q.mix[0], xw = q.mix[1], xk = q.mix[2], xv = q.mix[3], xa = q.mix[4], xg = q.mix[5];
-        HK(gemm_lin(b, L.rw, xr, q.r, T, 0));
-        HK(gemm_lin(b, L.kw, xk, q.k, T, 0));
-        HK(gemm_lin(b, L.vw, xv, q.v, T, 0));
-        CK(rsv_gemm_ex(c, xv, L.v1, nullptr, q.vmid, T, I.v_mid, C, 0, NONE, NONE, NONE));
-        CK(rsv_gemm_ex(c, xw, L.w1, nullptr, q.wmid, T, I.w_mid, C, 4, NONE, NONE, NONE));
-        CK(rsv_gemm_ex(c, xa, L.a1, nullptr, q.amid, T, I.a_mid, C, 0, NONE, NONE, NONE));
-        CK(rsv_gemm_ex(c, xg, L.g1, nullptr, q.gmid, T, I.g_mid, C, 8, NONE, NONE, NONE));
+        if (small) {
+            rsv_mm_job j1[7] = {
+                mm_job(L.rw, xr, q.r, 0), mm_job(L.kw, xk, q.k, 0), mm_job(L.vw, xv, q.v, 0),
+                mm_job(L.lv1, xv, q.vmid, 0), mm_job(L.lw1, xw, q.wmid, 4),
+                mm_job(L.la1, xa, q.amid, 0), mm_job(L.lg1, xg, q.gmid, 8),
+            };
+            CK(rsv_gemm_skinny(c, j1, 7, T));
+        } else {
+            HK(gemm_lin(b, L.rw, xr, q.r, T, 0));
+            HK(gemm_lin(b, L.kw, xk, q.k, T, 0));
+            HK(gemm_lin(b, L.vw, xv, q.v, T, 0));
+            CK(rsv_gemm_ex(c, xv, L.v1, nullptr, q.vmid, T, I.v_mid, C, 0, NONE, NONE, NONE));
+            CK(rsv_gemm_ex(c, xw, L.w1, nullptr, q.wmid, T, I.w_mid, C, 4, NONE, NONE, NONE));
+            CK(rsv_gemm_ex(c, xa, L.a1, nullptr, q.amid, T, I.a_mid, C, 0, NONE, NONE, NONE));
+            CK(rsv_gemm_ex(c, xg, L.g1, nullptr, q.gmid, T, I.g_mid, C, 8, NONE, NONE, NONE));
+        }
         if (i == 0) {
             CK(rsv_copy_device(c, q.v, q.vf));
             CK(rsv_copy_rows(c, q.v, s.v_first, q.seg_last, q.seg_slot, S, C));
         }
-        CK(rsv_gemm_ex(c, q.wmid, L.w2, nullptr, q.w, T, C, I.w_mid, 5, L.w0, NONE, b->scale_w));
-        CK(rsv_gemm_ex(c, q.amid, L.a2, nullptr, q.a, T, C, I.a_mid, 6, L.a0, NONE, NONE));
-        CK(rsv_gemm_ex(c, q.vmid, L.v2, nullptr, q.v, T, C, I.v_mid, 7, L.v0, q.vf, NONE));
-        CK(rsv_gemm_ex(c, q.gmid, L.g2, nullptr, q.g, T, C, I.g_mid, 0, NONE, NONE, NONE));
+        if (small) {
+            rsv_mm_job j2[4] = {mm_job(L.lw2, q.wmid, q.w, 5), mm_job(L.la2, q.amid, q.a, 6),
+                                mm_job(L.lv2, q.vmid, q.v, 7), mm_job(L.lg2, q.gmid, q.g, 0)};
+            j2[0].bias = L.w0;
+            j2[0].scale = b->scale_w;
+            j2[1].bias = L.a0;
+            j2[2].bias = L.v0;
+            j2[2].aux = q.vf;
+            CK(rsv_gemm_skinny(c, j2, 4, T));
+        } else {
+            CK(rsv_gemm_ex(c, q.wmid, L.w2, nullptr, q.w, T, C, I.w_mid, 5, L.w0, NONE, b->scale_w));
+            CK(rsv_gemm_ex(c, q.amid, L.a2, nullptr, q.a, T, C, I.a_mid, 6, L.a0, NONE, NONE));
+            CK(rsv_gemm_ex(c, q.vmid, L.v2, nullptr, q.v, T, C, I.v_mid, 7, L.v0, q.vf, NONE));
+            CK(rsv_gemm_ex(c, q.gmid, L.g2, nullptr, q.g, T, C, I.g_mid, 0, NONE, NONE, NONE));
+        }
         CK(rsv_wkv7_seq_ragged(c, s.rnn[i], q.r, q.w, q.k, q.v, q.a, L.k_k, L.k_a, L.r_k, L.lnx_w, L.lnx_b, q.yn,
                                q.seg_start, q.seg_len, q.seg_slot, S, H, N, GN_EPS));
         CK(rsv_mul_to_f16(c, q.yn, q.g, q.yg, T * C));
-        HK(gemm_lin(b, L.ow, q.yg, q.x, T, 2));
+        if (small) {
+            rsv_mm_job j4 = mm_job(L.ow, q.yg, q.x, 2);
+            CK(rsv_gemm_skinny(c, &j4, 1, T));
+        } else {
+            HK(gemm_lin(b, L.ow, q.yg, q.x, T, 2));
+        }
         const uint32_t coef1[1] = {L.ffn_x_k};
         CK(rsv_seq_norm_mix(c, q.x, s.cmix_x[i], L.ln2_w, L.ln2_b, coef1, &q.xb, 1, q.row_prev, T, C, LN_EPS));
         CK(rsv_seq_state_store(c, q.x, s.cmix_x[i], L.ln2_w, L.ln2_b, q.seg_last, q.seg_slot, S, C, LN_EPS));
-        HK(gemm_lin(b, L.fk, q.xb, q.r2, T, 3));
-        HK(gemm_lin(b, L.fv, q.r2, q.x, T, 2));
+        if (small) {
+            rsv_mm_job j5 = mm_job(L.fk, q.xb, q.r2, 3);
+            CK(rsv_gemm_skinny(c, &j5, 1, T));
+            rsv_mm_job j6 = mm_job(L.fv, q.r2, q.x, 2);
+            CK(rsv_gemm_skinny(c, &j6, 1, T));
+        } else {
+            HK(gemm_lin(b, L.fk, q.xb, q.r2, T, 3));
+            HK(gemm_lin(b, L.fv, q.r2, q.x, T, 2));
+        }
     }
-    if (logits) {
+    if (logits || head) {
         CK(rsv_copy_rows(c, q.x, q.xlast, q.seg_last, q.seg_iota, S, C));
         CK(rsv_norm(c, q.xlast, b->ln_out_w, b->ln_out_b, q.xnorm, C, 1, LN_EPS, S));
         HK(gemv_lin(b, b->head, q.xnorm, q.logits, S, 0));
-        CK(rsv_download(c, q.logits, logits, S * I.vocab));
+        if (logits) CK(rsv_download(c, q.logits, logits, S * I.vocab));
     } else {
         CK(rsv_synchronize(c));
     }
@@ -994,6 +1038,125 @@ int seq_single(rsv_bundle *b, GpuState &s, uint64_t slot, const uint32_t *tokens
         HK(prefill(b, s, segs, off + len == n ? logits : nullptr));
     }
     return 0;
+}
+
+// ------------------------------------------------------------ ragged serving
+// Continuous batching over the B slots of a State (the scheduler of the
+// north star; the reference has only padded batch prefill,
+// gpu_model.rs:914-997, and a batch decode self-loop, 1639-1781).  A step is
+// one packed dispatch through the layers: one decode token for every slot
+// that is generating, then chunks of the prompts still being prefilled (slots
+// in order, a prompt split over steps when it does not fit), `budget` tokens
+// in all.  A decode token is a segment of length 1, so prefill and decode
+// share every launch.  After the dispatch the GPU sampler draws the next
+// token of every slot whose prompt or previous token ended in the step; the
+// k-th token of slot q is drawn with seed seeds[q] + k.
+struct ServeSlot {
+    const uint32_t *prompt = nullptr;
+    uint64_t plen = 0, done = 0;  // prompt tokens consumed
+    uint64_t gen = 0;             // tokens sampled
+    uint32_t last = 0;            // last sampled token (next decode input)
+};
+
+int serve_ragged(rsv_bundle *b, GpuState &s, const uint32_t *tokens, const uint64_t *lens, uint64_t decode_len,
+                 const rsv_sampler_params *sp, const uint32_t *seeds, uint64_t budget, uint32_t *out,
+                 rsv_serve_step *steps, uint64_t max_steps, uint64_t *nsteps) {
+    rsv_ctx *c = b->ctx;
+    const rsv_model_info &I = b->info;
+    const uint64_t B = s.batch, V = I.vocab;
+    if (budget == 0 || budget > kMaxChunk) return herr("serve_ragged: budget must be 1..%llu", (unsigned long long)kMaxChunk);
+    if (decode_len == 0) return herr("serve_ragged: decode_len must be >= 1");
+    if (budget < B) return herr("serve_ragged: budget %llu below the slot count %llu", (unsigned long long)budget, (unsigned long long)B);
+    std::vector<ServeSlot> sl(B);
+    uint64_t off = 0;
+    for (uint64_t q = 0; q < B; q++) {
+        if (lens[q] == 0) return herr("serve_ragged: prompt %llu is empty", (unsigned long long)q);
+        sl[q].prompt = tokens + off;
+        sl[q].plen = lens[q];
+        off += lens[q];
+    }
+    for (uint64_t i = 0; i < off; i++)
+        if (tokens[i] >= V) return herr("serve_ragged: token %u >= vocab %llu", tokens[i], (unsigned long long)V);
+    uint32_t temp = NONE, counter = NONE, sampler = NONE, hist = NONE, tok = NONE;
+    auto cleanup = [&]() {
+        for (uint32_t id : {temp, counter, sampler, hist, tok})
+            if (id != NONE) rsv_tensor_free(c, id);
+    };
+    int rc = 0;
+    uint64_t nst = 0;
+    do {
+        // sampler work rows for up to B segments
+        if ((rc = new_tensor(b, V * B, RSV_F32, temp))) break;
+        if ((rc = new_tensor(b, V * B, RSV_U32, counter))) break;
+        if ((rc = new_tensor(b, 8 * B, RSV_F32, sampler))) break;
+        if ((rc = new_tensor(b, B, RSV_U32, hist))) break;
+        if ((rc = new_tensor(b, B, RSV_U32, tok))) break;
+        std::vector<uint32_t> drawn(B), seed_row(B);
+        while (true) {
+            std::vector<Seg> segs;
+            std::vector<uint64_t> seg_slot;
+            std::vector<bool> samples;
+            std::vector<uint32_t> one(B);
+            uint64_t used = 0, npre = 0, ndec = 0;
+            for (uint64_t q = 0; q < B; q++) {  // decode tokens first
+                ServeSlot &z = sl[q];
+                if (z.done == z.plen && z.gen > 0 && z.gen < decode_len) {
+                    one[q] = z.last;
+                    segs.push_back({&one[q], 1, q});
+                    seg_slot.push_back(q);
+                    samples.push_back(true);
+                    used++;
+                    ndec++;
+                }
+            }
+            for (uint64_t q = 0; q < B && used < budget; q++) {  // then prompt chunks
+                ServeSlot &z = sl[q];
+                if (z.done >= z.plen) continue;
+                const uint64_t take = std::min(z.plen - z.done, budget - used);
+                segs.push_back({z.prompt + z.done, take, q});
+                seg_slot.push_back(q);
+                samples.push_back(z.done + take == z.plen);
+                z.done += take;
+                used += take;
+                npre += take;
+            }
+            if (segs.empty()) break;
+            if (nst >= max_steps) { rc = herr("serve_ragged: more than %llu steps", (unsigned long long)max_steps); break; }
+            const auto t0 = std::chrono::steady_clock::now();
+            if ((rc = prefill(b, s, segs, nullptr, true))) break;
+            const uint64_t S = segs.size();
+            for (uint64_t g = 0; g < S; g++) seed_row[g] = seeds[seg_slot[g]] + (uint32_t)sl[seg_slot[g]].gen;
+            if (rsv_store_sampler_async_batch(c, sampler, 0, sp->temperature, sp->top_k, sp->top_p, seed_row.data(), S,
+                                              sp->repetition_penalty, sp->frequency_penalty, sp->presence_penalty, 0) ||
+                rsv_sample_into_host_seeded_batch(c, b->seq.logits, tok, V, temp, NONE, counter, sampler, hist, S) ||
+                rsv_download_u32(c, tok, drawn.data(), S)) {
+                rc = herr("serve_ragged sampler: %s", rsv_last_error());
+                break;
+            }
+            const auto t1 = std::chrono::steady_clock::now();
+            for (uint64_t g = 0; g < S; g++) {
+                if (!samples[g]) continue;
+                ServeSlot &z = sl[seg_slot[g]];
+                out[seg_slot[g] * decode_len + z.gen] = drawn[g];
+                z.last = drawn[g];
+                z.gen++;
+            }
+            if (steps) {
+                steps[nst].prefill_tokens = npre;
+                steps[nst].decode_tokens = ndec;
+                steps[nst].sampled = 0;
+                for (uint64_t g = 0; g < S; g++) steps[nst].sampled += samples[g] ? 1 : 0;
+                steps[nst].ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
+            }
+            nst++;
+            bool busy = false;
+            for (auto &z : sl) busy |= z.done < z.plen || z.gen < decode_len;
+            if (!busy) break;
+        }
+    } while (0);
+    if (nsteps) *nsteps = nst;
+    cleanup();
+    return rc;
 }
 
 // ------------------------------------------------------------ self-loops
@@ -1344,6 +1507,13 @@ int rsv_argmax_selfloop_batch_timed(rsv_bundle *b, rsv_state *s, const uint32_t 
     if (!b || !s || !seeds || !out || !ms) return herr("null argument");
     HK(tokens_ok(b, seeds, s->s.batch));
     return selfloop(b, s->s, seeds, n, nullptr, out, ms);
+}
+
+int rsv_serve_ragged(rsv_bundle *b, rsv_state *s, const uint32_t *tokens, const uint64_t *lens, uint64_t decode_len,
+                     const rsv_sampler_params *sp, const uint32_t *seeds, uint64_t budget, uint32_t *out,
+                     rsv_serve_step *steps, uint64_t max_steps, uint64_t *nsteps) {
+    if (!b || !s || !tokens || !lens || !sp || !seeds || !out) return herr("null argument");
+    return serve_ragged(b, s->s, tokens, lens, decode_len, sp, seeds, budget, out, steps, max_steps, nsteps);
 }
 
 int rsv_sample_selfloop_batch(rsv_bundle *b, rsv_state *s, const uint32_t *seeds, uint64_t n,

@@ -466,11 +466,6 @@ __device__ __forceinline__ void reg_dot(const GemvJob &J, int tile, int it, int 
     for (int r = 0; r < RU; r++) acc[r] = 0.0f;
 #pragma unroll
     for (int j = 0; j < CPL; j++) {
-#ifdef RSV_X_NODOT
-#pragma unroll
-        for (int r = 0; r < RU; r++) acc[r] += __uint_as_float((T.w[r][j].x ^ T.w[r][j].y ^ T.sz[r][j]) & 0x0FFFFFFFu);
-        continue;
-#endif
         if (FMT == FMT_I8) {
             // w = s*q + z over one 8-weight chunk of a 128-group (model.rs:234-252):
             // contribution s*sum(x*q) + z*sum(x)
@@ -590,11 +585,7 @@ __device__ __forceinline__ void gemv_reg_body(const GemvJob &J, int rb, float *r
     reg_load<FMT, CPL, RU>(J, t, ks, rg, li, A);
 
     // 3. prologue, once per block, into LDS (float4 part p of chunk c at p*NC + c)
-#ifdef RSV_X_NOPRO
-    if (false) {
-#else
     if (kMix && J.pro == PRO_LNMIX) {
-#endif
         float s = 0.0f;
 #pragma unroll
         for (int i = 0; i < Q; i++) s += (xa[i].x + xa[i].y) + (xa[i].z + xa[i].w);

@@ -131,6 +131,93 @@ __device__ __forceinline__ float sk_epilogue(const SkinnyJob &J, float v, int n,
     return v;
 }
 
+// Epilogue operands of one job held in registers: the job struct lives in
+// kernel-argument memory, and the compiler would re-read its fields after
+// every store through a generic pointer if the loops used them directly.
+struct SkEpi {
+    void *y;
+    float *y2;
+    const float *bias, *aux;
+    float scale;
+    int ldy, y_f16, epi, N;
+};
+__device__ __forceinline__ SkEpi sk_epi_of(const SkinnyJob &J) {
+    SkEpi e;
+    e.y = J.y; e.y2 = J.y2; e.bias = J.bias; e.aux = J.aux;
+    e.scale = J.epi == GE_WDECAY ? J.scale[0] : 0.0f;
+    e.ldy = J.ldy; e.y_f16 = J.y_f16; e.epi = J.epi; e.N = J.N;
+    return e;
+}
+// y[b, n] (epilogue)= v
+__device__ __forceinline__ void sk_store(const SkEpi &E, float v, int n, int b) {
+    const size_t yo = (size_t)b * E.ldy + n;
+    const float bias = E.bias ? E.bias[n] : 0.0f;
+    switch (E.epi) {
+        case GE_BIAS: v += bias; break;
+        case GE_ADD: v += ((const float *)E.y)[yo]; break;
+        case GE_RELU2: v = v > 0.0f ? v * v : 0.0f; break;
+        case GE_TANH: v = tanhf(v); break;
+        case GE_WDECAY: v = expf(sk_sig(v + bias) * E.scale); break;
+        case GE_SIGBIAS: v = sk_sig(v + bias); break;
+        case GE_VLERP: {
+            const float cur = ((const float *)E.y)[yo];
+            v = cur + sk_sig(v + bias) * (E.aux[yo] - cur);
+        } break;
+        case GE_SIGMOID: v = sk_sig(v); break;
+        default: break;
+    }
+    if (E.y_f16)
+        ((_Float16 *)E.y)[yo] = (_Float16)v;
+    else
+        ((float *)E.y)[yo] = v;
+    if (E.y2) E.y2[yo] = v;
+}
+
+// Epilogue of a 128-row x TB-session tile held in LDS (tile[row][session]).
+// Thread t always handles row t % 128 (coalesced stores along n), so the
+// bias is read once; the read-modify-write operands of 8 sessions are
+// loaded together before any of them is used.
+template <int TB>
+__device__ __forceinline__ void sk_store_tile(const SkEpi &E, const float (*tile)[TB + 1], int n0, int MB) {
+    const int r = threadIdx.x & 127, n = n0 + r;
+    if (n >= E.N) return;
+    const float bias = E.bias ? E.bias[n] : 0.0f;
+    const bool need_y = E.epi == GE_ADD || E.epi == GE_VLERP;
+    for (int b0 = threadIdx.x >> 7; b0 < MB; b0 += 16) {
+        float yc[8], ax[8];
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+            const int b = b0 + 2 * q;
+            const size_t yo = (size_t)b * E.ldy + n;
+            yc[q] = (need_y && b < MB) ? ((const float *)E.y)[yo] : 0.0f;
+            ax[q] = (E.epi == GE_VLERP && b < MB) ? E.aux[yo] : 0.0f;
+        }
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+            const int b = b0 + 2 * q;
+            if (b >= MB) break;
+            const size_t yo = (size_t)b * E.ldy + n;
+            float v = tile[r][b];
+            switch (E.epi) {
+                case GE_BIAS: v += bias; break;
+                case GE_ADD: v += yc[q]; break;
+                case GE_RELU2: v = v > 0.0f ? v * v : 0.0f; break;
+                case GE_TANH: v = tanhf(v); break;
+                case GE_WDECAY: v = expf(sk_sig(v + bias) * E.scale); break;
+                case GE_SIGBIAS: v = sk_sig(v + bias); break;
+                case GE_VLERP: v = yc[q] + sk_sig(v + bias) * (ax[q] - yc[q]); break;
+                case GE_SIGMOID: v = sk_sig(v); break;
+                default: break;
+            }
+            if (E.y_f16)
+                ((_Float16 *)E.y)[yo] = (_Float16)v;
+            else
+                ((float *)E.y)[yo] = v;
+            if (E.y2) E.y2[yo] = v;
+        }
+    }
+}
+
 // grid: for each job, (rows/64) row groups x J.split k-slices.  Block = 4
 // waves on one row group; wave w takes k-chunks w, w+4, ... of the slice.
 // The 4 wave tiles are summed in LDS in wave order.  With split == 1 the
@@ -398,26 +485,14 @@ __global__ __launch_bounds__(256) void k_skinny4(SkinnyJobs jobs, int MB, float 
     __syncthreads();
     const int n0 = rg * 128;
     if (J.split > 1) {
-        float *wsp = ws + ((size_t)J.ws_slot + (size_t)rg * J.split + sl) * 128 * TB;
-#ifdef RSV_X_NOEPI
-        if (tid == 0) wsp[0] = tile[0][0];
-        return;
-#endif
-        for (int o = tid; o < 128 * TB; o += 256) wsp[o] = tile[o & 127][o >> 7];
+        float4 *wsp = (float4 *)(ws + ((size_t)J.ws_slot + (size_t)rg * J.split + sl) * 128 * TB);
+        for (int o4 = tid; o4 < 32 * TB; o4 += 256) {
+            const int r = (4 * o4) & 127, b = (4 * o4) >> 7;
+            wsp[o4] = make_float4(tile[r][b], tile[r + 1][b], tile[r + 2][b], tile[r + 3][b]);
+        }
         return;
     }
-    for (int o = tid; o < 128 * TB; o += 256) {
-        const int r = o & 127, b = o >> 7;
-        const int n = n0 + r;
-        if (n >= J.N || b >= MB) continue;
-        const size_t yo = (size_t)b * J.ldy + n;
-        const float v = sk_epilogue(J, tile[r][b], n, yo);
-        if (J.y_f16)
-            ((_Float16 *)J.y)[yo] = (_Float16)v;
-        else
-            ((float *)J.y)[yo] = v;
-        if (J.y2) J.y2[yo] = v;
-    }
+    sk_store_tile<TB>(sk_epi_of(J), tile, n0, MB);
 }
 
 // ------------------------------------------------------------------ v5
@@ -438,10 +513,7 @@ typedef _Float16 sk_half8 __attribute__((ext_vector_type(8)));
 template <int MT, bool I8>
 __global__ __launch_bounds__(256) void k_skinny5(SkinnyJobs jobs, int MB, float *__restrict__ ws) {
     constexpr int TB = MT * 32;
-#ifndef SK_PD
-#define SK_PD 8
-#endif
-    constexpr int PD = I8 ? SK_PD : 6;    // chunks in flight per wave
+    constexpr int PD = I8 ? 8 : 6;    // chunks in flight per wave
     constexpr int WV = I8 ? 1 : 2;    // 16-byte loads per lane per chunk
     extern __shared__ __attribute__((aligned(16))) unsigned char smem5[];
     const int bid = blockIdx.x;
@@ -475,13 +547,9 @@ __global__ __launch_bounds__(256) void k_skinny5(SkinnyJobs jobs, int MB, float 
     auto load_w = [&](int p, int c) {
         c = min(c, c_hi - 1);
         const sk_u32x4 *q = (const sk_u32x4 *)(wt_ok + (size_t)c * tbytes);
-#ifdef SK_NONT
+        // plain (not non-temporal) loads measured faster here
 #pragma unroll
         for (int v = 0; v < WV; v++) wr[p][v] = q[v];
-#else
-#pragma unroll
-        for (int v = 0; v < WV; v++) wr[p][v] = __builtin_nontemporal_load(q + v);
-#endif
         if (I8) sr[p] = szrow[(size_t)(c >> 2) * 32];
     };
 #pragma unroll
@@ -498,10 +566,6 @@ __global__ __launch_bounds__(256) void k_skinny5(SkinnyJobs jobs, int MB, float 
         for (int i = 0; i < NP; i++) {
             const int e = tid + 256 * i;
             const int b = e / pieces_row, pc = e - b * pieces_row;
-#ifdef RSV_X_NOSLAB
-            xv[i] = (sk_u32x4){(unsigned)e, 0u, 0u, 0u};
-            continue;
-#endif
             xv[i] = (e < total && b < MB) ? *(const sk_u32x4 *)(J.x + (size_t)b * J.ldx + c_lo * 32 + pc * 8)
                                           : (sk_u32x4){0u, 0u, 0u, 0u};
         }
@@ -524,11 +588,6 @@ __global__ __launch_bounds__(256) void k_skinny5(SkinnyJobs jobs, int MB, float 
         const bool live = row_ok && cl < nloc;
         cl = min(cl, nloc - 1);
         uint32_t wh[8];
-#ifdef RSV_X_NODQ
-        if (I8) {
-            for (int h = 0; h < 4; h++) { wh[2 * h] = wr[p][0][h] ^ sr[p]; wh[2 * h + 1] = wr[p][0][h]; }
-        } else
-#endif
         if (I8) {
             const float s = live ? sk_h2f(sr[p]) : 0.0f, z = live ? sk_h2f(sr[p] >> 16) : 0.0f;
 #pragma unroll
@@ -550,11 +609,7 @@ __global__ __launch_bounds__(256) void k_skinny5(SkinnyJobs jobs, int MB, float 
 #pragma unroll
             for (int ct = 0; ct < MT; ct++) {
                 const sk_u32x4 xv = *(const sk_u32x4 *)&xs[(size_t)(ct * 32 + (lane & 31)) * XS + cl * 32 + 16 * g + 8 * st];
-#ifdef RSV_X_NOMMA
-                acc[ct][0] += __uint_as_float((wh[4 * st] ^ xv[0]) & 0x0FFFFFFFu);
-#else
                 acc[ct] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, __builtin_bit_cast(sk_half8, xv), acc[ct], 0, 0, 0);
-#endif
             }
         }
     };
@@ -580,26 +635,14 @@ __global__ __launch_bounds__(256) void k_skinny5(SkinnyJobs jobs, int MB, float 
     if (J.split > 1) {
         // slice tile, row-group-major then slice: [rg][sl][128 rows][TB sessions];
         // k_skinny4_reduce (the next launch) sums the slices in slice order
-        float *wsp = ws + ((size_t)J.ws_slot + (size_t)rg * J.split + sl) * 128 * TB;
-#ifdef RSV_X_NOEPI
-        if (tid == 0) wsp[0] = tile[0][0];
-        return;
-#endif
-        for (int o = tid; o < 128 * TB; o += 256) wsp[o] = tile[o & 127][o >> 7];
+        float4 *wsp = (float4 *)(ws + ((size_t)J.ws_slot + (size_t)rg * J.split + sl) * 128 * TB);
+        for (int o4 = tid; o4 < 32 * TB; o4 += 256) {
+            const int r = (4 * o4) & 127, b = (4 * o4) >> 7;
+            wsp[o4] = make_float4(tile[r][b], tile[r + 1][b], tile[r + 2][b], tile[r + 3][b]);
+        }
         return;
     }
-    for (int o = tid; o < 128 * TB; o += 256) {
-        const int r = o & 127, b = o >> 7;
-        const int n = n0 + r;
-        if (n >= J.N || b >= MB) continue;
-        const size_t yo = (size_t)b * J.ldy + n;
-        const float v = sk_epilogue(J, tile[r][b], n, yo);
-        if (J.y_f16)
-            ((_Float16 *)J.y)[yo] = (_Float16)v;
-        else
-            ((float *)J.y)[yo] = v;
-        if (J.y2) J.y2[yo] = v;
-    }
+    sk_store_tile<TB>(sk_epi_of(J), tile, n0, MB);
 }
 
 template <int MT>
@@ -628,13 +671,7 @@ __global__ __launch_bounds__(256) void k_skinny4_reduce(SkinnyJobs jobs, int MB,
             for (int q = 0; q < 8; q++)
                 if (q0 + q < J.split) v = q0 + q == 0 ? part[q] : v + part[q];
         }
-        const size_t yo = (size_t)b * J.ldy + n;
-        v = sk_epilogue(J, v, n, yo);
-        if (J.y_f16)
-            ((_Float16 *)J.y)[yo] = (_Float16)v;
-        else
-            ((float *)J.y)[yo] = v;
-        if (J.y2) J.y2[yo] = v;
+        sk_store(sk_epi_of(J), v, n, b);
     }
 }
 
@@ -732,9 +769,7 @@ int launch_skinny(rsv_ctx *ctx, SkinnyJobs &jobs, int MB) {
 // launch has about two blocks per CU, with slices of 8..16 chunks when the
 // row count allows (16 chunks = the LDS x slab limit, 8 = enough chunks per
 // wave to amortise the slab and the partial-tile traffic).
-#ifndef SK_KMAX
-#define SK_KMAX 16
-#endif
+constexpr int SK_KMAX = 16;  // longest k-slice (chunks) of the LDS x slab
 static int launch_v5(rsv_ctx *ctx, SkinnyJobs &jobs, int MB) {
     const int TB = MB <= 32 ? 32 : 64;
     const int cus = ctx->sm_count > 0 ? ctx->sm_count : 256;

@@ -75,7 +75,7 @@ def _ctype(decl):
         return ctypes.c_char_p
     if base == "rsv_int8":
         return ctypes.POINTER(Int8Handle)
-    if base in ("rsv_model_info", "rsv_sampler_params", "rsv_gemv_job", "rsv_mm_job"):
+    if base in ("rsv_model_info", "rsv_sampler_params", "rsv_gemv_job", "rsv_mm_job", "rsv_serve_step"):
         return ctypes.c_void_p
     return ctypes.POINTER(scalars[base])
 
@@ -159,6 +159,12 @@ class ModelInfo(ctypes.Structure):
     @property
     def num_vocab(self):
         return self.vocab
+
+
+class ServeStep(ctypes.Structure):
+    """rsv_serve_step (include/rsv_host.h): one dispatch of serve_ragged."""
+    _fields_ = [("prefill_tokens", ctypes.c_uint64), ("decode_tokens", ctypes.c_uint64),
+                ("sampled", ctypes.c_uint64), ("ms", ctypes.c_double)]
 
 
 class _SP(ctypes.Structure):
@@ -359,6 +365,31 @@ class Bundle:
         _hchk(_host.rsv_sample_selfloop_batch(self._h, state._h, _u32p(s), ctypes.c_uint64(n), ctypes.byref(c),
                                               _u32p(out)))
         return out.reshape(state.batch, n)
+
+
+    def serve_ragged(self, state, prompts, decode_len, sp, seeds, budget=4096, max_steps=None):
+        """Ragged continuous batching over the slots of `state`: slot q
+        prefills prompts[q] and samples `decode_len` tokens; every step is one
+        packed dispatch of decode tokens plus prompt chunks (`budget` tokens).
+        Returns (tokens [batch, decode_len], list of per-step dicts)."""
+        if len(prompts) != state.batch:
+            raise RsvError(f"serve_ragged: {len(prompts)} prompts for {state.batch} slots")
+        lens = np.array([len(p) for p in prompts], np.uint64)
+        flat = _toks(np.concatenate([np.asarray(p, np.uint32) for p in prompts]))
+        sd = _toks(seeds)
+        out = np.zeros(state.batch * decode_len, np.uint32)
+        if max_steps is None:
+            max_steps = int(lens.sum()) + state.batch * decode_len + 16
+        steps = (ServeStep * max_steps)()
+        n = ctypes.c_uint64()
+        c = sp._c()
+        _hchk(_host.rsv_serve_ragged(self._h, state._h, _u32p(flat), _u64p(lens), ctypes.c_uint64(decode_len),
+                                     ctypes.byref(c), _u32p(sd), ctypes.c_uint64(budget), _u32p(out),
+                                     ctypes.cast(steps, ctypes.c_void_p), ctypes.c_uint64(max_steps),
+                                     ctypes.byref(n)))
+        recs = [dict(prefill_tokens=steps[i].prefill_tokens, decode_tokens=steps[i].decode_tokens,
+                     sampled=steps[i].sampled, ms=steps[i].ms) for i in range(n.value)]
+        return out.reshape(state.batch, decode_len), recs
 
 
 class ModelBuilder:
