@@ -734,6 +734,11 @@ static int launch_reg(rsv_ctx *ctx, GemvJobs &jobs, int target) {
     return 0;
 }
 
+static int env_int(const char *name, int dflt) {
+    const char *e = getenv(name);
+    return (e && e[0]) ? atoi(e) : dflt;
+}
+
 // ---------------------------------------------------------------- B = 1, one-shot
 // LN + token-shift mixes of one row x [K] for a B=1 launch, computed once
 // (model.rs:625-635, 654-660): out_m = ln + coef_m * (prev - ln) with
@@ -821,7 +826,42 @@ __device__ __forceinline__ void gemv_os_body(const GemvJob &J, int rb, float4 *x
             const int q = tid + 256 * i;
             xa[i] = q < K4 ? X4[q] : make_float4(0.f, 0.f, 0.f, 0.f);
         }
-        if (J.pro == PRO_MUL) {
+        if (Q <= 3 && J.pro == PRO_LNMIX) {
+            // LN over the row (two-pass, model.rs:625-635) from the x values
+            // already in registers, then the token-shift mix; the LN inputs
+            // are loaded only after the statistics to keep registers free
+            float s = 0.0f;
+#pragma unroll
+            for (int i = 0; i < Q; i++) s += (xa[i].x + xa[i].y) + (xa[i].z + xa[i].w);
+            __shared__ float red_os[4];
+            const float mu = block_sum_256(s, red_os) / (float)K;
+            float v2 = 0.0f;
+#pragma unroll
+            for (int i = 0; i < Q; i++) {
+                if (tid + 256 * i >= K4) continue;
+                const float d0 = xa[i].x - mu, d1 = xa[i].y - mu, d2 = xa[i].z - mu, d3 = xa[i].w - mu;
+                v2 += (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
+            }
+            const float inv = 1.0f / sqrtf(block_sum_256(v2, red_os) / (float)K + 1.0e-5f);
+            const bool wr = J.lnout && rb == 0;
+#pragma unroll
+            for (int i = 0; i < Q; i++) {
+                const int q = tid + 256 * i;
+                if (q >= K4) continue;
+                const float4 g = ((const float4 *)J.gamma)[q], bt = ((const float4 *)J.beta)[q];
+                const float4 cf = ((const float4 *)J.coef)[q], pv = ((const float4 *)J.prev)[q];
+                float4 ln;
+                ln.x = (xa[i].x - mu) * inv * g.x + bt.x;
+                ln.y = (xa[i].y - mu) * inv * g.y + bt.y;
+                ln.z = (xa[i].z - mu) * inv * g.z + bt.z;
+                ln.w = (xa[i].w - mu) * inv * g.w + bt.w;
+                if (wr) ((float4 *)J.lnout)[q] = ln;
+                xa[i].x = ln.x + cf.x * (pv.x - ln.x);
+                xa[i].y = ln.y + cf.y * (pv.y - ln.y);
+                xa[i].z = ln.z + cf.z * (pv.z - ln.z);
+                xa[i].w = ln.w + cf.w * (pv.w - ln.w);
+            }
+        } else if (J.pro == PRO_MUL) {
 #pragma unroll
             for (int i = 0; i < Q; i++) {
                 const int q = tid + 256 * i;
@@ -921,10 +961,15 @@ static int launch_os(rsv_ctx *ctx, GemvJobs &jobs) {
     // LN-mix pre-pass: every LN-mix job of the launch must share x, LN and
     // token-shift row (true of the decode layer); mixes are de-duplicated by
     // coefficient vector
+    static const int in_kernel_mix = env_int("RSV_GEMV_OS_MIX", 1);
     MixArgs ma{};
     for (int i = 0; i < jobs.n; i++) {
         GemvJob &J = jobs.j[i];
         if (J.pro != PRO_LNMIX) continue;
+        if (in_kernel_mix) {
+            if (J.K > 3072) return 1;
+            continue;
+        }
         if (J.K > kMixMaxK) return 1;
         if (ma.nmix == 0) {
             ma.x = J.x; ma.gamma = J.gamma; ma.beta = J.beta; ma.prev = J.prev; ma.K = J.K;
@@ -967,10 +1012,6 @@ static int launch_os(rsv_ctx *ctx, GemvJobs &jobs) {
     return 0;
 }
 
-static int env_int(const char *name, int dflt) {
-    const char *e = getenv(name);
-    return (e && e[0]) ? atoi(e) : dflt;
-}
 
 
 int launch_gemv_jobs(rsv_ctx *ctx, GemvJobs &jobs, int batch) {

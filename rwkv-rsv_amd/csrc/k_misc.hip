@@ -164,9 +164,33 @@ __global__ __launch_bounds__(1024) void k_argmax(const float *__restrict__ logit
     const float *lg = logits + (size_t)b * n;
     float bv = -1e30f;
     int bi = 0;
-    for (int i = tid; i < n; i += 1024) {
-        const float v = lg[i];
-        if (v > bv) { bv = v; bi = i; }
+    if ((n & 3) == 0) {
+        // float4 quads q = tid + 1024*j, 8 loads in flight per round; each
+        // thread still visits its elements in increasing index order, so the
+        // strict compare keeps the smallest index of a tie
+        const float4 *l4 = (const float4 *)lg;
+        const int n4 = n >> 2;
+        for (int q0 = tid; q0 < n4; q0 += 8 * 1024) {
+            float4 v[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const int q = q0 + 1024 * j;
+                v[j] = q < n4 ? l4[q] : make_float4(-1e30f, -1e30f, -1e30f, -1e30f);
+            }
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const int e = 4 * (q0 + 1024 * j);
+                if (v[j].x > bv) { bv = v[j].x; bi = e; }
+                if (v[j].y > bv) { bv = v[j].y; bi = e + 1; }
+                if (v[j].z > bv) { bv = v[j].z; bi = e + 2; }
+                if (v[j].w > bv) { bv = v[j].w; bi = e + 3; }
+            }
+        }
+    } else {
+        for (int i = tid; i < n; i += 1024) {
+            const float v = lg[i];
+            if (v > bv) { bv = v; bi = i; }
+        }
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
