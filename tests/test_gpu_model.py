@@ -247,6 +247,7 @@ def test_config1_golden(tiny_cfg1):
 def test_fused_decode_matches_trait_op_sequence(bundles, kind, monkeypatch):
     """The six-launch fused layer equals the reference's one-op-per-method
     sequence (norm_lerp6, stage1, chain4, fuse_ka_dplr_norm, ...)."""
+    monkeypatch.setenv("RSV_MEGA", "0")  # the six-launch layer, not the persistent step
     b, _ = bundles[kind]
     p = _prompt(10, 30)
     b.reset()
