@@ -186,7 +186,22 @@ int rsv_gemv_int8_add(rsv_ctx *ctx, const rsv_int8 *w, uint32_t x, uint32_t y, u
                       uint64_t n);
 int rsv_gemv_int8_plain(rsv_ctx *ctx, const rsv_int8 *w, uint32_t x, uint32_t y, uint64_t m, uint64_t k,
                         uint64_t n);
-int rsv_supports_sparse_ffn(rsv_ctx *ctx); /* :439, returns 0: the dense int8/fp16 path is used */
+int rsv_supports_sparse_ffn(rsv_ctx *ctx); /* :439, returns 1 */
+/* ffn_value_sparse_add (backend.rs:422-441): x[c] += sum over f with
+ * r2[f] != 0 of r2[f] * V[c, f], reading V from value_tiled, the fp16 tiled
+ * copy [fh/128][c/256][128][256] made by rsv_tile_ffn_value.  value_w16 is
+ * accepted for the trait's signature and not read.  c % 256 == 0,
+ * fh % 128 == 0.  Summation order is fixed (no atomics). */
+int rsv_ffn_value_sparse_add(rsv_ctx *ctx, uint32_t value_w16, uint32_t value_tiled, uint32_t r2, uint32_t x,
+                             uint64_t c, uint64_t fh);
+/* ffn_value_sparse_add_batch (backend.rs:592-602): the same for r2 [batch, fh], x [batch, c]. */
+int rsv_ffn_value_sparse_add_batch(rsv_ctx *ctx, uint32_t value_tiled, uint32_t r2, uint32_t x, uint64_t c,
+                                   uint64_t fh, uint64_t batch);
+/* The tiled fp16 copy of ffn.value V [c, fh] for the two ops above (the
+ * reference builds it on the host at load, gpu_model.rs:3290-3340): from an
+ * int8 handle (dequantised as model.rs:234-252, then rounded to fp16) or an
+ * F16 tensor w16 (w8 null).  *out receives a new F16 tensor of fh*c. */
+int rsv_tile_ffn_value(rsv_ctx *ctx, uint32_t w16, const rsv_int8 *w8, uint64_t c, uint64_t fh, uint32_t *out);
 
 /* ---- int8 dequant to f32 / f16 (model.rs:234-252; backend.rs:756) */
 int rsv_dequant_int8_f32(rsv_ctx *ctx, const rsv_int8 *a, uint32_t out);

@@ -120,7 +120,17 @@ int rsv_create(int device, rsv_ctx **out) {
         delete ctx;
         return RSV_FAIL("rsv_create: workspace allocation failed");
     }
+    ctx->sparse_cnt_cap = 1 << 16;
+    if (hipMalloc(&ctx->sparse_cnt, ctx->sparse_cnt_cap * 4) != hipSuccess ||
+        hipMemset(ctx->sparse_cnt, 0, ctx->sparse_cnt_cap * 4) != hipSuccess) {
+        if (ctx->sparse_cnt) hipFree(ctx->sparse_cnt);
+        hipFree(ctx->skinny_ws);
+        hipStreamDestroy(ctx->stream);
+        delete ctx;
+        return RSV_FAIL("rsv_create: counter allocation failed");
+    }
     if (hipMalloc(&ctx->mix_buf, (size_t)kMaxJobs * kMixMaxK * 4) != hipSuccess) {
+        hipFree(ctx->sparse_cnt);
         hipFree(ctx->skinny_ws);
         hipStreamDestroy(ctx->stream);
         delete ctx;
@@ -143,6 +153,7 @@ int rsv_destroy(rsv_ctx *ctx) {
     if (ctx->sample_work) hipFree(ctx->sample_work);
     if (ctx->skinny_ws) hipFree(ctx->skinny_ws);
     if (ctx->mix_buf) hipFree(ctx->mix_buf);
+    if (ctx->sparse_cnt) hipFree(ctx->sparse_cnt);
     mega_free(ctx);
     hipStreamDestroy(ctx->stream);
     delete ctx;
@@ -744,7 +755,49 @@ int rsv_gemv_int8_add(rsv_ctx *ctx, const rsv_int8 *w, uint32_t x, uint32_t y, u
 int rsv_gemv_int8_plain(rsv_ctx *ctx, const rsv_int8 *w, uint32_t x, uint32_t y, uint64_t m, uint64_t k, uint64_t n) {
     return gemv_single(ctx, true, 0, w, x, 0xFFFFFFFFu, y, m, k, n, EPI_STORE, "gemv_int8_plain");
 }
-int rsv_supports_sparse_ffn(rsv_ctx *ctx) { (void)ctx; return 0; }
+int rsv_supports_sparse_ffn(rsv_ctx *ctx) { (void)ctx; return 1; }
+
+int rsv_ffn_value_sparse_add_batch(rsv_ctx *ctx, uint32_t value_tiled, uint32_t r2, uint32_t x, uint64_t c,
+                                   uint64_t fh, uint64_t batch) {
+    CHECK_CTX();
+    if (c == 0 || fh == 0 || batch == 0 || c > (1u << 20) || fh > (1u << 22) || batch > 65535)
+        return RSV_FAIL("ffn_value_sparse_add: bad shape c=%llu fh=%llu batch=%llu", (unsigned long long)c,
+                        (unsigned long long)fh, (unsigned long long)batch);
+    OPND(vt, value_tiled, RSV_F16, c * fh, "ffn_value_sparse_add value_tiled");
+    OPND(rr, r2, RSV_F32, fh * batch, "ffn_value_sparse_add r2");
+    OPND(xx, x, RSV_F32, c * batch, "ffn_value_sparse_add x");
+    return launch_ffn_sparse(ctx, F32P(rr), (const _Float16 *)vt_v, F32P(xx), (int)c, (int)fh, (int)batch);
+}
+
+int rsv_ffn_value_sparse_add(rsv_ctx *ctx, uint32_t value_w16, uint32_t value_tiled, uint32_t r2, uint32_t x,
+                             uint64_t c, uint64_t fh) {
+    (void)value_w16;
+    return rsv_ffn_value_sparse_add_batch(ctx, value_tiled, r2, x, c, fh, 1);
+}
+
+int rsv_tile_ffn_value(rsv_ctx *ctx, uint32_t w16, const rsv_int8 *w8, uint64_t c, uint64_t fh, uint32_t *out) {
+    CHECK_CTX();
+    if (!out) return RSV_FAIL("tile_ffn_value: null out");
+    if (c % 256 || fh % 128 || c == 0 || fh == 0) return RSV_FAIL("tile_ffn_value: c=%llu fh=%llu", (unsigned long long)c, (unsigned long long)fh);
+    const uint32_t *idx = nullptr, *sz = nullptr;
+    const _Float16 *h = nullptr;
+    if (w8) {
+        if (int8_operands(ctx, w8, c, fh, &idx, &sz, "tile_ffn_value")) return -1;
+    } else {
+        void *p = nullptr;
+        if (opnd(ctx, w16, RSV_F16, c * fh, &p, "tile_ffn_value w16")) return -1;
+        h = (const _Float16 *)p;
+    }
+    uint32_t id;
+    if (rsv_tensor_create(ctx, c * fh, RSV_F16, &id)) return -1;
+    Tensor *t = get_tensor(ctx, id);
+    if (launch_tile_ffn_value(ctx, (const uint8_t *)idx, sz, h, (_Float16 *)t->ptr, (int)c, (int)fh)) {
+        rsv_tensor_free(ctx, id);
+        return -1;
+    }
+    *out = id;
+    return 0;
+}
 
 static int stage1(rsv_ctx *ctx, bool i8, uint32_t rw16, uint32_t kw16, uint32_t vw16, const rsv_int8 *rw8,
                   const rsv_int8 *kw8, const rsv_int8 *vw8, uint32_t v1, uint32_t w1, uint32_t a1, uint32_t g1,

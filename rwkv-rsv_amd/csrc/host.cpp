@@ -251,6 +251,7 @@ struct Layer {
     uint32_t w1, w2, a1, a2, v1, v2, g1, g2;  // fp16 [out, in]
     Linear rw, kw, vw, ow, fk, fv;
     Linear lw1, lw2, la1, la2, lv1, lv2, lg1, lg2;  // LoRA views (fp16) for the batched path
+    uint32_t fv_tiled = NONE;  // sparse ffn.value copy, fp16 [F/128][C/256][128][256] (RSV_FFN_SPARSE=1)
 };
 
 struct GpuState {
@@ -385,6 +386,11 @@ void layer_norm_cpu(const float *x, const float *w, const float *bb, uint64_t n,
     for (uint64_t i = 0; i < n; i++) y[i] = (x[i] - mean) * inv * w[i] + bb[i];
 }
 
+bool ffn_sparse_requested() {
+    const char *e = getenv("RSV_FFN_SPARSE");
+    return e && e[0] == '1';
+}
+
 int load_model(rsv_bundle *b, const char *path) {
     SafeTensors st;
     HK(st.open_file(path));
@@ -485,6 +491,15 @@ int load_model(rsv_bundle *b, const char *path) {
         all_i8 = all_i8 && L.rw.i8 && L.kw.i8 && L.vw.i8 && L.ow.i8 && L.fk.i8 && L.fv.i8;
     }
     I.int8_linears = all_i8;
+    // sparse ffn.value (gpu_model.rs:2353-2371, 3290-3340): the tiled fp16 copy is made at load when
+    // RSV_FFN_SPARSE=1 and the shapes allow it; the B<16 decode layer then reads only the rows of
+    // ffn.value whose relu^2 input is non-zero
+    if (ffn_sparse_requested() && C % 256 == 0 && I.ffn % 128 == 0) {
+        for (auto &L : b->layers) {
+            CK(rsv_tile_ffn_value(b->ctx, L.fv.w16, L.fv.i8 ? &L.fv.h : nullptr, C, I.ffn, &L.fv_tiled));
+            b->owned.push_back(L.fv_tiled);
+        }
+    }
     CK(rsv_synchronize(b->ctx));
     return 0;
 }
@@ -713,6 +728,12 @@ int forward_layer_fused(rsv_bundle *b, uint64_t i, WorkBufs &w, GpuState &s) {
     ln_mix(j5, L.ln2_w, L.ln2_b, s.cmix_x[i], L.ffn_x_k, w.ln2);
     CK(rsv_gemv_multi(c, &j5, 1, NONE, NONE, 0, B));
 
+    if (L.fv_tiled != NONE && ffn_sparse_requested()) {
+        // x += r2 V over the non-zero r2 rows only, then the token-shift row into the state
+        CK(rsv_ffn_value_sparse_add_batch(c, L.fv_tiled, w.r2, w.x, C, I.ffn, B));
+        CK(rsv_copy_device(c, w.ln2, s.cmix_x[i]));
+        return 0;
+    }
     rsv_gemv_job j6 = lin_job(L.fv, w.r2, w.x, P_NONE, E_ADD);
     CK(rsv_gemv_multi(c, &j6, 1, w.ln2, s.cmix_x[i], C, B));
     return 0;

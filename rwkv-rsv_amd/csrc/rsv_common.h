@@ -118,6 +118,9 @@ struct rsv_ctx {
     float *mix_buf = nullptr;
     // persistent single-session decode step (k_mega.hip), built on demand
     void *mega = nullptr;  // k_mega.hip plan (device tables + scratch)
+    // arrival counters of the sparse ffn.value reduction (zeroed at create; each launch leaves them zero)
+    unsigned *sparse_cnt = nullptr;
+    size_t sparse_cnt_cap = 0;
 };
 
 namespace rsv {
@@ -234,6 +237,10 @@ int launch_seq_state_store(rsv_ctx *ctx, const float *x, float *state, const flo
 int launch_copy_rows(rsv_ctx *ctx, const float *src, float *dst, const uint32_t *src_rows, const uint32_t *dst_rows,
                      int n, int c, uint64_t src_n, uint64_t dst_n);
 int launch_mul_to_f16(rsv_ctx *ctx, const float *a, const float *b, _Float16 *y, uint64_t n);
+// Sparse ffn.value (k_sparse.hip): tiled fp16 copy and x += r2 V over non-zero r2.
+int launch_tile_ffn_value(rsv_ctx *ctx, const uint8_t *idx, const uint32_t *sz, const _Float16 *w16, _Float16 *out,
+                          int c, int fh);
+int launch_ffn_sparse(rsv_ctx *ctx, const float *r2, const _Float16 *vt, float *x, int c, int fh, int batch);
 
 // Persistent single-session decode step (k_mega.hip): device pointers of one
 // layer and of the model around the layers.

@@ -348,3 +348,30 @@ def test_serve_ragged_errors(bundles):
     with pytest.raises(rsv.RsvError):
         b.serve_ragged(S, [_prompt(4, 1), _prompt(4, 2)], 2, sp, [1, 2], budget=8)
     S.free()
+
+
+def test_sparse_ffn_value_decode(small_i8, monkeypatch):
+    """RSV_FFN_SPARSE=1 (gpu_model.rs:2353-2371): the decode layer reads only the
+    ffn.value rows whose relu^2 input is non-zero, from the tiled fp16 copy.
+    Logits stay within the oracle bound and close to the dense int8 path (the
+    copy rounds the dequantised weights to fp16)."""
+    import rsv
+    monkeypatch.setenv("RSV_FFN_SPARSE", "1")
+    bs = rsv.ModelBuilder(small_i8).build()
+    monkeypatch.delenv("RSV_FFN_SPARSE")
+    bd = rsv.ModelBuilder(small_i8).build()
+    m = orc.Model(small_i8)
+    try:
+        p = _prompt(16, 41)
+        monkeypatch.setenv("RSV_FFN_SPARSE", "1")
+        got = [bs.infer_tokens([t]) for t in p]
+        monkeypatch.delenv("RSV_FFN_SPARSE")
+        dense = [bd.infer_tokens([t]) for t in p]
+        st = m.init_state()
+        want = m.forward(list(p), st)
+        assert rel_rmse(got[-1], want) <= RMSE_BOUND
+        for g, d in zip(got, dense):
+            assert rel_rmse(g, d) <= 2e-3
+    finally:
+        bs.close()
+        bd.close()

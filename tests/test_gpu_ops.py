@@ -615,3 +615,49 @@ def test_ln_mix_f16_and_wkv_yg(be):
     for q in range(B):
         _, want, _ = _wkv_oracle(S[q], k[q], kk, a[q], ka, r[q], v[q], w[q], g2, b2, rk, H)
         assert rel_err(got[q], want * g[q]) < 2e-3
+
+
+# ------------------------------------------------------------- sparse ffn.value
+def _tile_ref(v16, c, fh):
+    """The reference's tiled layout (gpu_model.rs:3290-3340): element (f, c) at
+    [f/128][c/256][f%128][c%256] of V^T, V = v16 [c, fh]."""
+    t = v16.T.reshape(fh // 128, 128, c // 256, 256).transpose(0, 2, 1, 3)
+    return np.ascontiguousarray(t).reshape(-1)
+
+
+@pytest.mark.parametrize("c,fh,batch", [(256, 512, 1), (2560, 10240, 1), (512, 1024, 5)])
+def test_ffn_value_sparse_add(be, c, fh, batch):
+    """ffn_value_sparse_add(_batch) (backend.rs:422-441, 592-602): the tiled fp16
+    copy equals the reference layout of fp16(dequant(V)) bit for bit, and
+    x + r2 V over the non-zero r2 rows matches a float64 product of the same
+    fp16 weights."""
+    rsv = _rsv()
+    rng = np.random.default_rng(7)
+    idx, sz, w = _int8_weight(rng, c, fh)
+    h = be.int8(idx, sz)
+    vt = ctypes.c_uint32(0)
+    be.call("rsv_tile_ffn_value", NONE, ctypes.byref(h), c, fh, ctypes.byref(vt))
+    v16 = w.astype(np.float16)
+    got_t = be.get(vt.value, c * fh)
+    assert np.array_equal(got_t.astype(np.float16).view(np.uint16), _tile_ref(v16, c, fh).view(np.uint16))
+    # relu^2-like input: about half the rows exactly zero, plus whole zero f-blocks
+    r2 = np.maximum(rng.standard_normal((batch, fh)).astype(np.float32), 0.0) ** 2
+    r2[:, : min(128, fh)] = 0.0
+    x0 = rng.standard_normal((batch, c)).astype(np.float32)
+    rt = be.tensor(r2.reshape(-1))
+    xt = be.tensor(x0.reshape(-1))
+    if batch == 1:
+        be.call("rsv_ffn_value_sparse_add", NONE, vt.value, rt, xt, c, fh)
+    else:
+        be.call("rsv_ffn_value_sparse_add_batch", vt.value, rt, xt, c, fh, batch)
+    got = be.get(xt, batch * c).reshape(batch, c)
+    want = x0.astype(np.float64) + r2.astype(np.float64) @ v16.astype(np.float64).T
+    assert rel_err(got, want) <= 1e-5
+    # deterministic: a second call on the same inputs adds the same amount
+    xt2 = be.tensor(x0.reshape(-1))
+    if batch == 1:
+        be.call("rsv_ffn_value_sparse_add", NONE, vt.value, rt, xt2, c, fh)
+    else:
+        be.call("rsv_ffn_value_sparse_add_batch", vt.value, rt, xt2, c, fh, batch)
+    assert np.array_equal(be.get(xt2, batch * c).reshape(batch, c), got)
+    assert rsv.hip_lib().rsv_supports_sparse_ffn(be.ctx) == 1
