@@ -645,6 +645,89 @@ __global__ __launch_bounds__(256) void k_skinny5(SkinnyJobs jobs, int MB, float 
     sk_store_tile<TB>(sk_epi_of(J), tile, n0, MB);
 }
 
+// Small-K batched GEMM (K <= 32*NCH, e.g. the LoRA-up chain, K = 64..256):
+// a block is 4 waves on 128 rows of one job, the whole K in one pass.  Every
+// weight chunk and every x operand of the wave is loaded at once (x straight
+// from global into the MFMA B registers, no LDS slab, no k-split), then the
+// MFMAs run and the tile goes through the same LDS epilogue as k_skinny5.
+template <int MT, bool I8, int NCH>
+__global__ __launch_bounds__(256) void k_skinny_sk(SkinnyJobs jobs, int MB) {
+    constexpr int TB = MT * 32;
+    constexpr int WV = I8 ? 1 : 2;
+    __shared__ float tile[128][TB + 1];
+    const int bid = blockIdx.x;
+    int ji = 0;
+    while (ji + 1 < jobs.n && bid >= jobs.blk_start[ji + 1]) ji++;
+    const SkinnyJob &J = jobs.j[ji];
+    const int rg = bid - jobs.blk_start[ji];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 5;
+    const int nchunks = J.K / 32;
+    const int rt_glob = rg * 4 + wave;
+    const int row = rt_glob * 32 + (lane & 31);
+    const bool row_ok = row < J.N;
+    constexpr int tbytes = I8 ? 1024 : 2048;
+    // rows past N read the job's first tile (masked to zero below)
+    const uint8_t *wt = (const uint8_t *)J.w + (row_ok ? (size_t)rt_glob * nchunks * tbytes : 0) + lane * (I8 ? 16 : 32);
+    const uint32_t *szrow = I8 ? J.sz + (size_t)min(rt_glob, (J.N - 1) / 32) * (J.K / 128) * 32 + (lane & 31) : nullptr;
+    sk_u32x4 wr[NCH][WV];
+    uint32_t sr[NCH];
+    sk_u32x4 xv[NCH][MT][2];
+#pragma unroll
+    for (int c = 0; c < NCH; c++) {
+        const int cc = min(c, nchunks - 1);
+#pragma unroll
+        for (int v = 0; v < WV; v++) wr[c][v] = ((const sk_u32x4 *)(wt + (size_t)cc * tbytes))[v];
+        if (I8) sr[c] = szrow[(size_t)(cc >> 2) * 32];
+#pragma unroll
+        for (int ct = 0; ct < MT; ct++) {
+            const int b = min(ct * 32 + (lane & 31), MB - 1);  // sessions past MB are computed, never stored
+            const sk_u32x4 *xp = (const sk_u32x4 *)(J.x + (size_t)b * J.ldx + cc * 32 + 16 * g);
+            xv[c][ct][0] = xp[0];
+            xv[c][ct][1] = xp[1];
+        }
+    }
+    sk_f16x acc[MT];
+#pragma unroll
+    for (int ct = 0; ct < MT; ct++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) acc[ct][e] = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NCH; c++) {
+        if (c >= nchunks) break;  // uniform: one job per block
+        const bool live = row_ok;
+        uint32_t wh[8];
+        if (I8) {
+            const float sc = live ? sk_h2f(sr[c]) : 0.0f, z = live ? sk_h2f(sr[c] >> 16) : 0.0f;
+#pragma unroll
+            for (int h = 0; h < 4; h++) {
+                const uint32_t u = wr[c][0][h];
+                wh[2 * h] = sk_pack(fmaf(sc, (float)(u & 0xFFu), z), fmaf(sc, (float)((u >> 8) & 0xFFu), z));
+                wh[2 * h + 1] = sk_pack(fmaf(sc, (float)((u >> 16) & 0xFFu), z), fmaf(sc, (float)(u >> 24), z));
+            }
+        } else {
+#pragma unroll
+            for (int h = 0; h < 4; h++) {
+                wh[h] = live ? wr[c][0][h] : 0u;
+                wh[4 + h] = live ? wr[c][WV - 1][h] : 0u;
+            }
+        }
+#pragma unroll
+        for (int st = 0; st < 2; st++) {
+            const sk_half8 a = __builtin_bit_cast(sk_half8, (sk_u32x4){wh[4 * st], wh[4 * st + 1], wh[4 * st + 2], wh[4 * st + 3]});
+#pragma unroll
+            for (int ct = 0; ct < MT; ct++)
+                acc[ct] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, __builtin_bit_cast(sk_half8, xv[c][ct][st]), acc[ct], 0, 0, 0);
+        }
+    }
+    // wave w owns tile rows 32w .. 32w+31: acc[ct][e] -> (row 32w + 8*(e/4) + 4g + e%4, col ct*32 + lane%32)
+#pragma unroll
+    for (int ct = 0; ct < MT; ct++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) tile[wave * 32 + 8 * (e >> 2) + 4 * g + (e & 3)][ct * 32 + (lane & 31)] = acc[ct][e];
+    __syncthreads();
+    sk_store_tile<TB>(sk_epi_of(J), tile, rg * 128, MB);
+}
+
 template <int MT>
 __global__ __launch_bounds__(256) void k_skinny4_reduce(SkinnyJobs jobs, int MB, const float *__restrict__ ws) {
     constexpr int TB = MT * 32;
@@ -773,7 +856,11 @@ constexpr int SK_KMAX = 16;  // longest k-slice (chunks) of the LDS x slab
 static int launch_v5(rsv_ctx *ctx, SkinnyJobs &jobs, int MB) {
     const int TB = MB <= 32 ? 32 : 64;
     const int cus = ctx->sm_count > 0 ? ctx->sm_count : 256;
-    const int target = 2 * cus;
+    static const int per_cu = [] {
+        const char *e = getenv("RSV_SKINNY_BLOCKS_PER_CU");
+        return e && atoi(e) > 0 ? atoi(e) : 2;
+    }();
+    const int target = per_cu * cus;
     int64_t W = 0;
     for (int i = 0; i < jobs.n; i++) {
         const SkinnyJob &J = jobs.j[i];
@@ -828,6 +915,33 @@ static int launch_v5(rsv_ctx *ctx, SkinnyJobs &jobs, int MB) {
     return 0;
 }
 
+// Jobs of K <= 32*SK_SMALL_NCH in one pass each (k_skinny_sk): one block per
+// 128 rows, no k-split and no reduce launch.
+constexpr int SK_SMALL_NCH = 8;
+static int launch_small(rsv_ctx *ctx, SkinnyJobs &jobs, int MB) {
+    int total = 0;
+    for (int i = 0; i < jobs.n; i++) {
+        SkinnyJob &J = jobs.j[i];
+        J.split = 1;
+        J.nblk = (J.N + 127) / 128;
+        jobs.blk_start[i] = total;
+        total += J.nblk;
+    }
+    jobs.blk_start[jobs.n] = total;
+    const bool i8 = jobs.j[0].fmt == FMT_I8;
+    for (int i = 1; i < jobs.n; i++)
+        if ((jobs.j[i].fmt == FMT_I8) != i8) return RSV_FAIL("skinny gemm: mixed formats in one tiled launch");
+    if (MB <= 32) {
+        if (i8) hipLaunchKernelGGL((k_skinny_sk<1, true, SK_SMALL_NCH>), dim3(total), dim3(256), 0, ctx->stream, jobs, MB);
+        else hipLaunchKernelGGL((k_skinny_sk<1, false, SK_SMALL_NCH>), dim3(total), dim3(256), 0, ctx->stream, jobs, MB);
+    } else {
+        if (i8) hipLaunchKernelGGL((k_skinny_sk<2, true, SK_SMALL_NCH>), dim3(total), dim3(256), 0, ctx->stream, jobs, MB);
+        else hipLaunchKernelGGL((k_skinny_sk<2, false, SK_SMALL_NCH>), dim3(total), dim3(256), 0, ctx->stream, jobs, MB);
+    }
+    RSV_HIP(hipGetLastError());
+    return 0;
+}
+
 static int launch_slab(rsv_ctx *ctx, SkinnyJobs &jobs, int MB) {
     if (MB <= 0 || MB > 64) return RSV_FAIL("skinny gemm: batch %d outside 1..64", MB);
     if (jobs.n <= 0 || jobs.n > kMaxJobs) return RSV_FAIL("skinny gemm: bad job count %d", jobs.n);
@@ -850,6 +964,9 @@ static int launch_slab(rsv_ctx *ctx, SkinnyJobs &jobs, int MB) {
                   !(J.epi == GE_VLERP && !J.aux) && !(J.epi == GE_WDECAY && !J.scale) &&
                   !(J.y_f16 && (J.epi == GE_ADD || J.epi == GE_VLERP));
         }
+        bool small = ok;
+        for (int i = 0; i < jobs.n; i++) small &= jobs.j[i].K <= 32 * SK_SMALL_NCH;
+        if (small) return launch_small(ctx, jobs, MB);
         if (!big && ok) return launch_v5(ctx, jobs, MB);
     }
     static const int max_split = [] {

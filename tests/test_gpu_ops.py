@@ -527,14 +527,16 @@ def test_gemv_multi_lnmix_and_side_copy(be, batch):
     assert np.array_equal(be.get(ids["dst"], batch * C), be.get(ids["ln"], batch * C))
 
 
-@pytest.mark.parametrize("batch", [16, 33, 64, 100])
-def test_gemm_skinny(be, batch):
+@pytest.mark.parametrize("batch,k", [(16, 1280), (33, 1280), (64, 1280), (100, 1280), (64, 256), (33, 96), (16, 128)])
+def test_gemm_skinny(be, batch, k):
     """Batched-decode MFMA GEMM (fp16 x, int8/fp16 W) against float64 with
-    the loader's fp16 rounding of the dequantised weights."""
+    the loader's fp16 rounding of the dequantised weights.  k <= 256 takes the
+    one-pass small-K kernel (the LoRA-up chain), larger k the split-K one."""
     rsv = _rsv()
-    rng = np.random.default_rng(60 + batch)
-    n, k = 320, 1280
-    idx, sz, W = _int8_weight(rng, n, k)
+    rng = np.random.default_rng(60 + batch + k)
+    n = 320
+    ki = k if k % 128 == 0 else 128  # int8 needs whole 128-groups
+    idx, sz, W = _int8_weight(rng, n, ki)
     h = be.int8(idx, sz)
     W16 = (rng.standard_normal((n, k)) * 0.02).astype(np.float16)
     x = rng.standard_normal((batch, k)).astype(np.float16)
@@ -550,15 +552,17 @@ def test_gemm_skinny(be, batch):
     # MFMA-tiled copies (weights and, for int8, the scale/zero words)
     ht = rsv.Int8Handle(h.idx, h.sz, h.m, h.k)
     out = ctypes.c_uint32()
-    be.call("rsv_tile_weights", h.idx, n, k, 1, ctypes.byref(out))
+    be.call("rsv_tile_weights", h.idx, n, ki, 1, ctypes.byref(out))
     ht.idx = out.value
-    be.call("rsv_tile_weights", h.sz, n, k, 4, ctypes.byref(out))
+    be.call("rsv_tile_weights", h.sz, n, ki, 4, ctypes.byref(out))
     ht.sz = out.value
     be.call("rsv_tile_weights", w16, n, k, 2, ctypes.byref(out))
     w16t = out.value
     cases = (("i8", ctypes.pointer(h), NONE, Wq, 0), ("f16", None, w16, W16.astype(np.float64), 0),
              ("i8-tiled", ctypes.pointer(ht), NONE, Wq, 1), ("f16-tiled", None, w16t, W16.astype(np.float64), 1))
     for wname, w8, w16id, Wm, tiled in cases:
+        if wname.startswith("i8") and ki != k:
+            continue
         acc = X @ Wm.T
         for epi, init, ref in [(0, None, acc), (1, None, acc + bias), (2, y0, y0 + acc),
                                (3, None, np.maximum(acc, 0) ** 2), (4, None, np.tanh(acc)),
