@@ -367,6 +367,31 @@ int rsv_wkv7_decode_ex(rsv_ctx *ctx, uint32_t s, uint32_t k, uint32_t k_k, uint3
                        uint32_t y_norm, uint32_t g, uint32_t yg_f16, uint64_t h, uint64_t n, float eps,
                        float gn_eps, uint64_t batch);
 
+/* ---- fused LoRA-up chain + WKV7 step for small batches (no reference
+ * counterpart; it composes gemv_lowrank_chain4, backend.rs:309-333, and
+ * fuse_ka_dplr_norm, backend.rs:223-243, into one launch per layer).
+ * From the stage-1 outputs r, k, v [batch, C] and the LoRA-up inputs
+ * w_mid (tanh applied), a_mid, v_mid, g_mid (raw; the sigmoid of g is
+ * applied here), F32 [batch, rank]: w = exp(scale_w*sigmoid(w_mid.W2^T + w0)),
+ * a = sigmoid(a_mid.A2^T + a0), v += sigmoid(v_mid.V2^T + v0)*(v_first - v),
+ * g = sigmoid(g_mid).G2^T; then the WKV7 step on state [batch, H, 64, 64]
+ * (updated in place) and yg = (GroupNorm(y) + bonus) * g, the att.output
+ * operand.  side_src [batch, C] is copied to side_dst when both are given
+ * (ids 0xFFFFFFFF: none).  Ranks must be multiples of 32, summing to at
+ * most 1024. */
+typedef struct rsv_wkv_lora {
+    uint32_t state, r, k, v, v_first;
+    uint32_t w_mid, a_mid, v_mid, g_mid; /* F32 [batch, rank] */
+    uint32_t w2, a2, v2, g2;             /* F16 [C, rank] */
+    uint32_t w0, a0, v0, scale_w;
+    uint32_t k_k, k_a, r_k, ln_x_w, ln_x_b;
+    uint32_t yg;                         /* F32 [batch, C] */
+    uint32_t side_src, side_dst;
+    uint64_t n_head, w_rank, a_rank, v_rank, g_rank;
+    float eps, gn_eps;
+} rsv_wkv_lora;
+int rsv_wkv7_lora_decode(rsv_ctx *ctx, const rsv_wkv_lora *op, uint64_t batch);
+
 /* ---- persistent single-session decode step (no reference counterpart:
  * the reference decodes one token as a sequence of trait ops,
  * gpu_model.rs:1879-1913 + 2060-2392).  One launch runs the embedding row,

@@ -341,6 +341,59 @@ int rsv_import_tensors(rsv_ctx *ctx, rsv_ctx *src) {
 int rsv_begin_batch(rsv_ctx *ctx) { CHECK_CTX(); return 0; }
 int rsv_end_batch(rsv_ctx *ctx) { CHECK_CTX(); return 0; }
 int rsv_supports_graph_capture(rsv_ctx *ctx) { (void)ctx; return 1; }
+// ---------------------------------------------- fused LoRA-up + WKV7 step
+int rsv_wkv7_lora_decode(rsv_ctx *ctx, const rsv_wkv_lora *op, uint64_t batch) {
+    CHECK_CTX();
+    if (!op) return RSV_FAIL("wkv7_lora_decode: null op");
+    const uint64_t H = op->n_head, C = H * 64, B = batch;
+    if (H == 0 || H > 4096 || B == 0 || B > 65535) return RSV_FAIL("wkv7_lora_decode: bad n_head %llu / batch %llu", (unsigned long long)H, (unsigned long long)B);
+    const uint64_t rk[4] = {op->w_rank, op->a_rank, op->v_rank, op->g_rank};
+    WkvLoraArgs a{};
+    a.H = (int)H;
+    for (int m = 0; m < 4; m++) {
+        if (rk[m] == 0 || rk[m] > 1024) return RSV_FAIL("wkv7_lora_decode: rank %llu", (unsigned long long)rk[m]);
+        a.mid_n[m] = (int)rk[m];
+    }
+    a.eps = op->eps;
+    a.gn_eps = op->gn_eps;
+    void *p = nullptr;
+#define WL_F32(field, id, n, what)                                   \
+    if (opnd(ctx, (id), RSV_F32, (n), &p, (what))) return -1;        \
+    field = (decltype(field))p;
+    WL_F32(a.S, op->state, B * H * 4096, "wkv7_lora state");
+    WL_F32(a.r, op->r, B * C, "wkv7_lora r");
+    WL_F32(a.k, op->k, B * C, "wkv7_lora k");
+    WL_F32(a.v, op->v, B * C, "wkv7_lora v");
+    WL_F32(a.vf, op->v_first, B * C, "wkv7_lora v_first");
+    WL_F32(a.mid[0], op->w_mid, B * rk[0], "wkv7_lora w_mid");
+    WL_F32(a.mid[1], op->a_mid, B * rk[1], "wkv7_lora a_mid");
+    WL_F32(a.mid[2], op->v_mid, B * rk[2], "wkv7_lora v_mid");
+    WL_F32(a.mid[3], op->g_mid, B * rk[3], "wkv7_lora g_mid");
+    WL_F32(a.w0, op->w0, C, "wkv7_lora w0");
+    WL_F32(a.a0, op->a0, C, "wkv7_lora a0");
+    WL_F32(a.v0, op->v0, C, "wkv7_lora v0");
+    WL_F32(a.scale, op->scale_w, 1, "wkv7_lora scale_w");
+    WL_F32(a.kk, op->k_k, C, "wkv7_lora k_k");
+    WL_F32(a.ka, op->k_a, C, "wkv7_lora k_a");
+    WL_F32(a.rk, op->r_k, C, "wkv7_lora r_k");
+    WL_F32(a.gamma, op->ln_x_w, C, "wkv7_lora ln_x_w");
+    WL_F32(a.beta, op->ln_x_b, C, "wkv7_lora ln_x_b");
+    WL_F32(a.yg, op->yg, B * C, "wkv7_lora yg");
+#undef WL_F32
+    const uint32_t up[4] = {op->w2, op->a2, op->v2, op->g2};
+    for (int m = 0; m < 4; m++) {
+        if (opnd(ctx, up[m], RSV_F16, C * rk[m], &p, "wkv7_lora up")) return -1;
+        a.up[m] = (const _Float16 *)p;
+    }
+    if (op->side_src != 0xFFFFFFFFu && op->side_dst != 0xFFFFFFFFu) {
+        if (opnd(ctx, op->side_src, RSV_F32, B * C, &p, "wkv7_lora side_src")) return -1;
+        a.side_src = (const float *)p;
+        if (opnd(ctx, op->side_dst, RSV_F32, B * C, &p, "wkv7_lora side_dst")) return -1;
+        a.side_dst = (float *)p;
+    }
+    return launch_wkv7_lora(ctx, a, (int)B);
+}
+
 // ---------------------------------------------- persistent decode step
 static int f32v(rsv_ctx *ctx, uint32_t id, uint64_t n, const float **p, const char *what) {
     void *v = nullptr;

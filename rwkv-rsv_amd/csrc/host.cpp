@@ -671,8 +671,21 @@ void ln_mix(rsv_gemv_job &j, uint32_t gamma, uint32_t beta, uint32_t prev, uint3
     j.lnout = lnout;
 }
 
+bool wkv_lora_ok(const rsv_model_info &I) {
+    const char *e = getenv("RSV_WKV_LORA");
+    if (e && e[0] == '0') return false;
+    const uint64_t r[4] = {I.w_mid, I.a_mid, I.v_mid, I.g_mid};
+    uint64_t sum = 0;
+    for (uint64_t v : r) {
+        if (v == 0 || v % 32) return false;
+        sum += v;
+    }
+    return sum <= 1024 && I.head_size == 64;
+}
+
 // One layer for B slots with the op sequence of gpu_model.rs:2060-2392 /
-// 1373-1566, fused into six launches:
+// 1373-1566, fused into six launches (five when the LoRA-up chain and the
+// WKV7 step share one launch, rsv_wkv7_lora_decode):
 //   1. LN1 + token shift + r/k/v (int8) + LoRA-down projections  (state LN row -> ln1)
 //   2. LoRA-up chain (w, a, v-first lerp, g)                      (ln1 -> tmix state)
 //   3. WKV7 state update + GroupNorm + bonus
@@ -704,25 +717,48 @@ int forward_layer_fused(rsv_bundle *b, uint64_t i, WorkBufs &w, GpuState &s) {
     if (i == 0) j1[2].p1 = s.v_first;  // v_first snapshot (gpu_model.rs:2200-2204)
     CK(rsv_gemv_multi(c, j1, 7, NONE, NONE, 0, B));
 
-    rsv_gemv_job j2[4] = {
-        lora_job(L.w2, C, I.w_mid, w.wmid, w.w, P_NONE, E_WDECAY),
-        lora_job(L.a2, C, I.a_mid, w.amid, w.a, P_NONE, E_SIGB),
-        lora_job(L.v2, C, I.v_mid, w.vmid, w.v, P_NONE, E_VLERP),
-        lora_job(L.g2, C, I.g_mid, w.gmid, w.g, P_SIG, E_STORE),
-    };
-    j2[0].p0 = L.w0;
-    j2[0].scale = b->scale_w;
-    j2[1].p0 = L.a0;
-    j2[2].p0 = L.v0;
-    j2[2].p1 = s.v_first;
-    CK(rsv_gemv_multi(c, j2, 4, w.ln1, s.tmix_x[i], C, B));
+    // LoRA-up chain + WKV7 + GroupNorm in one launch (ranks multiples of 32),
+    // its output y_norm*g going straight into att.output; RSV_WKV_LORA=0 keeps
+    // the two launches below
+    if (wkv_lora_ok(I)) {
+        rsv_wkv_lora op;
+        op.state = s.rnn[i];
+        op.r = w.r; op.k = w.k; op.v = w.v; op.v_first = s.v_first;
+        op.w_mid = w.wmid; op.a_mid = w.amid; op.v_mid = w.vmid; op.g_mid = w.gmid;
+        op.w2 = L.w2; op.a2 = L.a2; op.v2 = L.v2; op.g2 = L.g2;
+        op.w0 = L.w0; op.a0 = L.a0; op.v0 = L.v0; op.scale_w = b->scale_w;
+        op.k_k = L.k_k; op.k_a = L.k_a; op.r_k = L.r_k; op.ln_x_w = L.lnx_w; op.ln_x_b = L.lnx_b;
+        op.yg = w.yn;
+        op.side_src = w.ln1;
+        op.side_dst = s.tmix_x[i];
+        op.n_head = I.n_head;
+        op.w_rank = I.w_mid; op.a_rank = I.a_mid; op.v_rank = I.v_mid; op.g_rank = I.g_mid;
+        op.eps = L2_EPS;
+        op.gn_eps = GN_EPS;
+        CK(rsv_wkv7_lora_decode(c, &op, B));
+        rsv_gemv_job j4 = lin_job(L.ow, w.yn, w.x, P_NONE, E_ADD);
+        CK(rsv_gemv_multi(c, &j4, 1, NONE, NONE, 0, B));
+    } else {
+        rsv_gemv_job j2[4] = {
+            lora_job(L.w2, C, I.w_mid, w.wmid, w.w, P_NONE, E_WDECAY),
+            lora_job(L.a2, C, I.a_mid, w.amid, w.a, P_NONE, E_SIGB),
+            lora_job(L.v2, C, I.v_mid, w.vmid, w.v, P_NONE, E_VLERP),
+            lora_job(L.g2, C, I.g_mid, w.gmid, w.g, P_SIG, E_STORE),
+        };
+        j2[0].p0 = L.w0;
+        j2[0].scale = b->scale_w;
+        j2[1].p0 = L.a0;
+        j2[2].p0 = L.v0;
+        j2[2].p1 = s.v_first;
+        CK(rsv_gemv_multi(c, j2, 4, w.ln1, s.tmix_x[i], C, B));
 
-    CK(rsv_fuse_ka_dplr_norm_batch(c, s.rnn[i], w.k, L.k_k, w.a, L.k_a, w.r, w.v, w.w, L.lnx_w, L.lnx_b, L.r_k, NONE,
-                                   NONE, w.yn, I.n_head, I.head_size, L2_EPS, GN_EPS, B));
+        CK(rsv_fuse_ka_dplr_norm_batch(c, s.rnn[i], w.k, L.k_k, w.a, L.k_a, w.r, w.v, w.w, L.lnx_w, L.lnx_b, L.r_k, NONE,
+                                       NONE, w.yn, I.n_head, I.head_size, L2_EPS, GN_EPS, B));
 
-    rsv_gemv_job j4 = lin_job(L.ow, w.yn, w.x, P_MUL, E_ADD);
-    j4.xmul = w.g;
-    CK(rsv_gemv_multi(c, &j4, 1, NONE, NONE, 0, B));
+        rsv_gemv_job j4 = lin_job(L.ow, w.yn, w.x, P_MUL, E_ADD);
+        j4.xmul = w.g;
+        CK(rsv_gemv_multi(c, &j4, 1, NONE, NONE, 0, B));
+    }
 
     rsv_gemv_job j5 = lin_job(L.fk, w.x, w.r2, P_LN, E_RELU2);
     ln_mix(j5, L.ln2_w, L.ln2_b, s.cmix_x[i], L.ffn_x_k, w.ln2);

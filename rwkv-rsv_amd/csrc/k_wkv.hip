@@ -144,6 +144,145 @@ int launch_wkv7_decode(rsv_ctx *ctx, float *s, const float *k, const float *kk, 
     return 0;
 }
 
+// ------------------------------------------- fused LoRA-up + decode step
+// The LoRA-up chain of one head (gpu_model.rs:2206-2262: w decay, a gate,
+// v-first lerp, g) and the WKV7 step of that head in one block, for small
+// batches: grid (H, B), 256 threads.  Thread (j = tid/4, q = tid%4) owns
+// channel 64h+j: it takes quarter q of each LoRA-up dot (the inputs staged in
+// LDS, the weights read straight from global, 16 bytes at a time) and
+// columns 16q..16q+15 of state row j.  Quad sums run on DPP.  The output is
+// y_norm * g, the att.output operand.  Blocks with h == 0 also copy
+// side_src -> side_dst for their session (the token-shift state row).
+template <int CTRL>
+__device__ __forceinline__ float quad_dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float quad_sum(float v) {
+    v += quad_dpp<0xB1>(v);  // quad_perm 1,0,3,2
+    v += quad_dpp<0x4E>(v);  // quad_perm 2,3,0,1
+    return v;
+}
+__device__ __forceinline__ float block_sum(float v, float *red) {
+    v = wave_sum(v);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return (red[0] + red[1]) + (red[2] + red[3]);
+}
+__device__ __forceinline__ float sig_f(float v) { return 1.0f / (1.0f + expf(-v)); }
+__device__ __forceinline__ float h2f_w(uint32_t b) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(b & 0xFFFFu)); }
+
+__global__ __launch_bounds__(256) void k_wkv7_lora(WkvLoraArgs A) {
+    __shared__ float mids[1024];
+    __shared__ float hv[5 * 64];
+    __shared__ float red[4];
+    const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+    const int j = tid >> 2, q = tid & 3, H = A.H, C = H * 64, c = h * 64 + j;
+    const size_t vo = (size_t)b * C + c;
+    const int m0 = A.mid_n[0], m1 = A.mid_n[1], m2 = A.mid_n[2], m3 = A.mid_n[3];
+    const int L4 = m0 + m1 + m2 + m3;
+    // every global load of the block first: LoRA-up inputs, per-channel vectors, the state row part
+    for (int e = tid; e < L4; e += 256) {
+        const int m = e < m0 ? 0 : e < m0 + m1 ? 1 : e < m0 + m1 + m2 ? 2 : 3;
+        const int off = m == 0 ? 0 : m == 1 ? m0 : m == 2 ? m0 + m1 : m0 + m1 + m2;
+        const float v = A.mid[m][(size_t)b * A.mid_n[m] + (e - off)];
+        mids[e] = m == 3 ? sig_f(v) : v;  // the g input goes through a sigmoid
+    }
+    const float kc = A.k[vo], rc = A.r[vo], vc = A.v[vo], vfc = A.vf[vo];
+    const float w0 = A.w0[c], a0 = A.a0[c], v0 = A.v0[c], kkc = A.kk[c], kac = A.ka[c], rkc = A.rk[c];
+    const float gam = A.gamma[c], bet = A.beta[c], sw = A.scale[0];
+    float4 *srow = (float4 *)(A.S + (((size_t)b * H + h) * 64 + j) * 64 + 16 * q);
+    float4 st4[4];
+#pragma unroll
+    for (int m = 0; m < 4; m++) st4[m] = srow[m];
+    if (h == 0 && A.side_dst)
+        for (int e = tid; e < C; e += 256) A.side_dst[(size_t)b * C + e] = A.side_src[(size_t)b * C + e];
+    __syncthreads();
+    // LoRA-up dots: quarter q of row c of each up matrix [C, mid]
+    float acc[4];
+    int mo = 0;
+#pragma unroll
+    for (int m = 0; m < 4; m++) {
+        const int mid = A.mid_n[m], seg = mid >> 2;
+        const uint4 *wp = (const uint4 *)(A.up[m] + (size_t)c * mid + q * seg);
+        const float *xm = mids + mo + q * seg;
+        float sm = 0.0f;
+        for (int e = 0; e < seg; e += 8) {
+            const uint4 w = wp[e >> 3];
+            const float4 x0 = *(const float4 *)(xm + e), x1 = *(const float4 *)(xm + e + 4);
+            sm = fmaf(x0.x, h2f_w(w.x), sm);
+            sm = fmaf(x0.y, h2f_w(w.x >> 16), sm);
+            sm = fmaf(x0.z, h2f_w(w.y), sm);
+            sm = fmaf(x0.w, h2f_w(w.y >> 16), sm);
+            sm = fmaf(x1.x, h2f_w(w.z), sm);
+            sm = fmaf(x1.y, h2f_w(w.z >> 16), sm);
+            sm = fmaf(x1.z, h2f_w(w.w), sm);
+            sm = fmaf(x1.w, h2f_w(w.w >> 16), sm);
+        }
+        acc[m] = quad_sum(sm);
+        mo += mid;
+    }
+    const float wd = expf(sig_f(acc[0] + w0) * sw);
+    const float aa = sig_f(acc[1] + a0);
+    const float vv = vc + sig_f(acc[2] + v0) * (vfc - vc);
+    const float gg = acc[3];
+    // WKV7 head vectors (model.rs:445-473, 716-826)
+    const float kk = kc * kkc;
+    float nrm = sqrtf(block_sum(q == 0 ? kk * kk : 0.0f, red));
+    nrm = nrm < A.eps ? A.eps : nrm;
+    const float inv = 1.0f / nrm;
+    const float kh = kk * inv;
+    const float kmod = kc + kac * (kc * aa - kc);
+    if (q == 0) {
+        hv[j] = kh;
+        hv[64 + j] = kh * (-aa);
+        hv[128 + j] = wd;
+        hv[192 + j] = kmod;
+        hv[256 + j] = rc;
+    }
+    const float bonus = block_sum(q == 0 ? rc * kmod * rkc : 0.0f, red);
+    // row j, columns 16q..16q+15: S = S diag(w) + (S k_hat) b^T + v k_mod^T; y = S r
+    float sr[16];
+#pragma unroll
+    for (int m = 0; m < 4; m++) {
+        sr[4 * m] = st4[m].x; sr[4 * m + 1] = st4[m].y; sr[4 * m + 2] = st4[m].z; sr[4 * m + 3] = st4[m].w;
+    }
+    float sa = 0.0f;
+#pragma unroll
+    for (int jj = 0; jj < 16; jj++) sa = fmaf(sr[jj], hv[16 * q + jj], sa);
+    sa = quad_sum(sa);
+    float y = 0.0f;
+#pragma unroll
+    for (int jj = 0; jj < 16; jj++) {
+        const int cc = 16 * q + jj;
+        const float ns = sr[jj] * hv[128 + cc] + sa * hv[64 + cc] + vv * hv[192 + cc];
+        sr[jj] = ns;
+        y = fmaf(ns, hv[256 + cc], y);
+    }
+    y = quad_sum(y);
+#pragma unroll
+    for (int m = 0; m < 4; m++) srow[m] = make_float4(sr[4 * m], sr[4 * m + 1], sr[4 * m + 2], sr[4 * m + 3]);
+    // GroupNorm over the head (two-pass, eps inside the sqrt) + bonus, times g
+    const float mean = block_sum(q == 0 ? y : 0.0f, red) * (1.0f / 64.0f);
+    const float d = y - mean;
+    const float var = block_sum(q == 0 ? d * d : 0.0f, red) * (1.0f / 64.0f) + A.gn_eps;
+    const float yn = d * (1.0f / sqrtf(var)) * gam + bet + bonus * vv;
+    if (q == 0) A.yg[vo] = yn * gg;
+}
+
+int launch_wkv7_lora(rsv_ctx *ctx, const WkvLoraArgs &a, int batch) {
+    if (a.H <= 0 || batch <= 0 || batch > 65535) return RSV_FAIL("wkv7_lora: bad h=%d batch=%d", a.H, batch);
+    int L4 = 0;
+    for (int m = 0; m < 4; m++) {
+        if (a.mid_n[m] <= 0 || a.mid_n[m] % 32) return RSV_FAIL("wkv7_lora: LoRA rank %d not a multiple of 32", a.mid_n[m]);
+        L4 += a.mid_n[m];
+    }
+    if (L4 > 1024) return RSV_FAIL("wkv7_lora: LoRA ranks sum to %d (max 1024)", L4);
+    hipLaunchKernelGGL(k_wkv7_lora, dim3(a.H, batch), dim3(256), 0, ctx->stream, a);
+    RSV_HIP(hipGetLastError());
+    return 0;
+}
+
 // ------------------------------------------------------ ragged prefill scan
 // grid (H, nseg), block 64.  Segment g covers packed token rows
 // [seg_start[g], seg_start[g]+seg_len[g]) and state slot seg_slot[g]; the

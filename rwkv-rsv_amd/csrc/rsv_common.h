@@ -237,6 +237,22 @@ int launch_seq_state_store(rsv_ctx *ctx, const float *x, float *state, const flo
 int launch_copy_rows(rsv_ctx *ctx, const float *src, float *dst, const uint32_t *src_rows, const uint32_t *dst_rows,
                      int n, int c, uint64_t src_n, uint64_t dst_n);
 int launch_mul_to_f16(rsv_ctx *ctx, const float *a, const float *b, _Float16 *y, uint64_t n);
+// Fused LoRA-up chain + WKV7 decode step of small batches (k_wkv.hip).
+struct WkvLoraArgs {
+    float *S;                        // [B, H, 64, 64]
+    const float *r, *k, *v, *vf;     // [B, C] (vf: v_first)
+    const float *mid[4];             // LoRA-up inputs w (tanh applied), a, v, g (raw): [B, mid]
+    const _Float16 *up[4];           // LoRA-up weights [C, mid]
+    const float *w0, *a0, *v0;       // [C]
+    const float *scale;              // device scalar (decay scale)
+    const float *kk, *ka, *rk, *gamma, *beta;  // [C]
+    float *yg;                       // [B, C] out: (GroupNorm(y) + bonus) * g
+    const float *side_src;           // [B, C] copied to side_dst (optional)
+    float *side_dst;
+    int H, mid_n[4];
+    float eps, gn_eps;
+};
+int launch_wkv7_lora(rsv_ctx *ctx, const WkvLoraArgs &a, int batch);
 // Sparse ffn.value (k_sparse.hip): tiled fp16 copy and x += r2 V over non-zero r2.
 int launch_tile_ffn_value(rsv_ctx *ctx, const uint8_t *idx, const uint32_t *sz, const _Float16 *w16, _Float16 *out,
                           int c, int fh);

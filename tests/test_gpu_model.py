@@ -375,3 +375,24 @@ def test_sparse_ffn_value_decode(small_i8, monkeypatch):
     finally:
         bs.close()
         bd.close()
+
+
+@pytest.mark.parametrize("kind", ["f32", "f16", "i8", "i8g"])
+def test_fused_lora_wkv_matches_two_launches(bundles, kind, monkeypatch):
+    """rsv_wkv7_lora_decode (LoRA-up chain + WKV7 + GroupNorm in one launch)
+    equals the two-launch form (gemv_lowrank_chain4 then fuse_ka_dplr_norm)
+    on logits and state, fp32 throughout."""
+    monkeypatch.setenv("RSV_MEGA", "0")
+    b, _ = bundles[kind]
+    p = _prompt(12, 52)
+    monkeypatch.setenv("RSV_WKV_LORA", "0")
+    b.reset()
+    two = [b.infer_tokens([t]) for t in p]
+    s_two = b.state_back()
+    monkeypatch.setenv("RSV_WKV_LORA", "1")
+    b.reset()
+    one = [b.infer_tokens([t]) for t in p]
+    s_one = b.state_back()
+    for a, c in zip(one, two):
+        assert rel_rmse(a, c) <= 1e-5
+    assert rel_rmse(s_one, s_two) <= 1e-5
