@@ -389,6 +389,7 @@ typedef struct rsv_wkv_lora {
     uint32_t side_src, side_dst;
     uint64_t n_head, w_rank, a_rank, v_rank, g_rank;
     float eps, gn_eps;
+    int f16_io; /* 1: the four *_mid inputs are F16, g_mid already holds sigmoid(g), and yg is F16 */
 } rsv_wkv_lora;
 int rsv_wkv7_lora_decode(rsv_ctx *ctx, const rsv_wkv_lora *op, uint64_t batch);
 

@@ -365,10 +365,12 @@ int rsv_wkv7_lora_decode(rsv_ctx *ctx, const rsv_wkv_lora *op, uint64_t batch) {
     WL_F32(a.k, op->k, B * C, "wkv7_lora k");
     WL_F32(a.v, op->v, B * C, "wkv7_lora v");
     WL_F32(a.vf, op->v_first, B * C, "wkv7_lora v_first");
-    WL_F32(a.mid[0], op->w_mid, B * rk[0], "wkv7_lora w_mid");
-    WL_F32(a.mid[1], op->a_mid, B * rk[1], "wkv7_lora a_mid");
-    WL_F32(a.mid[2], op->v_mid, B * rk[2], "wkv7_lora v_mid");
-    WL_F32(a.mid[3], op->g_mid, B * rk[3], "wkv7_lora g_mid");
+    a.f16_io = op->f16_io ? 1 : 0;
+    const uint32_t mid_ids[4] = {op->w_mid, op->a_mid, op->v_mid, op->g_mid};
+    for (int m = 0; m < 4; m++) {
+        if (opnd(ctx, mid_ids[m], a.f16_io ? RSV_F16 : RSV_F32, B * rk[m], &p, "wkv7_lora mid")) return -1;
+        a.mid[m] = p;
+    }
     WL_F32(a.w0, op->w0, C, "wkv7_lora w0");
     WL_F32(a.a0, op->a0, C, "wkv7_lora a0");
     WL_F32(a.v0, op->v0, C, "wkv7_lora v0");
@@ -378,7 +380,8 @@ int rsv_wkv7_lora_decode(rsv_ctx *ctx, const rsv_wkv_lora *op, uint64_t batch) {
     WL_F32(a.rk, op->r_k, C, "wkv7_lora r_k");
     WL_F32(a.gamma, op->ln_x_w, C, "wkv7_lora ln_x_w");
     WL_F32(a.beta, op->ln_x_b, C, "wkv7_lora ln_x_b");
-    WL_F32(a.yg, op->yg, B * C, "wkv7_lora yg");
+    if (opnd(ctx, op->yg, a.f16_io ? RSV_F16 : RSV_F32, B * C, &p, "wkv7_lora yg")) return -1;
+    a.yg = p;
 #undef WL_F32
     const uint32_t up[4] = {op->w2, op->a2, op->v2, op->g2};
     for (int m = 0; m < 4; m++) {

@@ -671,6 +671,13 @@ void ln_mix(rsv_gemv_job &j, uint32_t gamma, uint32_t beta, uint32_t prev, uint3
     j.lnout = lnout;
 }
 
+// The batched layer uses the fused LoRA-up + WKV7 launch only with
+// RSV_WKV_LORA_MM=1 (measured against the two launches per batch size).
+bool mm_wkv_lora() {
+    const char *e = getenv("RSV_WKV_LORA_MM");
+    return e && e[0] == '1';
+}
+
 bool wkv_lora_ok(const rsv_model_info &I) {
     const char *e = getenv("RSV_WKV_LORA");
     if (e && e[0] == '0') return false;
@@ -735,6 +742,7 @@ int forward_layer_fused(rsv_bundle *b, uint64_t i, WorkBufs &w, GpuState &s) {
         op.w_rank = I.w_mid; op.a_rank = I.a_mid; op.v_rank = I.v_mid; op.g_rank = I.g_mid;
         op.eps = L2_EPS;
         op.gn_eps = GN_EPS;
+        op.f16_io = 0;
         CK(rsv_wkv7_lora_decode(c, &op, B));
         rsv_gemv_job j4 = lin_job(L.ow, w.yn, w.x, P_NONE, E_ADD);
         CK(rsv_gemv_multi(c, &j4, 1, NONE, NONE, 0, B));
@@ -878,6 +886,32 @@ int forward_layer_mm(rsv_bundle *b, uint64_t i, WorkBufs &w, GpuState &s) {
     };
     if (i == 0) j1[2].y2 = s.v_first;  // v_first snapshot (gpu_model.rs:2200-2204)
     CK(rsv_gemm_skinny(c, j1, 7, B));
+    if (wkv_lora_ok(I) && mm_wkv_lora()) {
+        // LoRA-up chain + WKV7 + GroupNorm in one launch, fp16 in and out
+        rsv_wkv_lora op;
+        op.state = s.rnn[i];
+        op.r = w.r; op.k = w.k; op.v = w.v; op.v_first = s.v_first;
+        op.w_mid = w.wmid16; op.a_mid = w.amid16; op.v_mid = w.vmid16; op.g_mid = w.gmid16;
+        op.w2 = L.w2; op.a2 = L.a2; op.v2 = L.v2; op.g2 = L.g2;
+        op.w0 = L.w0; op.a0 = L.a0; op.v0 = L.v0; op.scale_w = b->scale_w;
+        op.k_k = L.k_k; op.k_a = L.k_a; op.r_k = L.r_k; op.ln_x_w = L.lnx_w; op.ln_x_b = L.lnx_b;
+        op.yg = w.yg16;
+        op.side_src = op.side_dst = NONE;
+        op.n_head = I.n_head;
+        op.w_rank = I.w_mid; op.a_rank = I.a_mid; op.v_rank = I.v_mid; op.g_rank = I.g_mid;
+        op.eps = L2_EPS;
+        op.gn_eps = GN_EPS;
+        op.f16_io = 1;
+        CK(rsv_wkv7_lora_decode(c, &op, B));
+        rsv_mm_job j4 = mm_job(L.ow, w.yg16, w.x, G_ADD);
+        CK(rsv_gemm_skinny(c, &j4, 1, B));
+        CK(rsv_ln_mix_f16(c, w.x, s.cmix_x[i], L.ln2_w, L.ln2_b, &L.ffn_x_k, &w.xb16, 1, C, LN_EPS, B));
+        rsv_mm_job j5 = mm_job(L.fk, w.xb16, w.r216, G_RELU2);
+        CK(rsv_gemm_skinny(c, &j5, 1, B));
+        rsv_mm_job j6 = mm_job(L.fv, w.r216, w.x, G_ADD);
+        CK(rsv_gemm_skinny(c, &j6, 1, B));
+        return 0;
+    }
     rsv_mm_job j2[4] = {
         mm_job(L.lw2, w.wmid16, w.w, G_WDECAY), mm_job(L.la2, w.amid16, w.a, G_SIGB),
         mm_job(L.lv2, w.vmid16, w.v, G_VLERP), mm_job(L.lg2, w.gmid16, w.g, G_STORE),

@@ -172,6 +172,7 @@ __device__ __forceinline__ float block_sum(float v, float *red) {
 __device__ __forceinline__ float sig_f(float v) { return 1.0f / (1.0f + expf(-v)); }
 __device__ __forceinline__ float h2f_w(uint32_t b) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(b & 0xFFFFu)); }
 
+template <bool F16IO>
 __global__ __launch_bounds__(256) void k_wkv7_lora(WkvLoraArgs A) {
     __shared__ float mids[1024];
     __shared__ float hv[5 * 64];
@@ -185,8 +186,9 @@ __global__ __launch_bounds__(256) void k_wkv7_lora(WkvLoraArgs A) {
     for (int e = tid; e < L4; e += 256) {
         const int m = e < m0 ? 0 : e < m0 + m1 ? 1 : e < m0 + m1 + m2 ? 2 : 3;
         const int off = m == 0 ? 0 : m == 1 ? m0 : m == 2 ? m0 + m1 : m0 + m1 + m2;
-        const float v = A.mid[m][(size_t)b * A.mid_n[m] + (e - off)];
-        mids[e] = m == 3 ? sig_f(v) : v;  // the g input goes through a sigmoid
+        const size_t mi = (size_t)b * A.mid_n[m] + (e - off);
+        if (F16IO) mids[e] = (float)((const _Float16 *)A.mid[m])[mi];  // g input already through its sigmoid
+        else mids[e] = m == 3 ? sig_f(((const float *)A.mid[m])[mi]) : ((const float *)A.mid[m])[mi];
     }
     const float kc = A.k[vo], rc = A.r[vo], vc = A.v[vo], vfc = A.vf[vo];
     const float w0 = A.w0[c], a0 = A.a0[c], v0 = A.v0[c], kkc = A.kk[c], kac = A.ka[c], rkc = A.rk[c];
@@ -267,7 +269,10 @@ __global__ __launch_bounds__(256) void k_wkv7_lora(WkvLoraArgs A) {
     const float d = y - mean;
     const float var = block_sum(q == 0 ? d * d : 0.0f, red) * (1.0f / 64.0f) + A.gn_eps;
     const float yn = d * (1.0f / sqrtf(var)) * gam + bet + bonus * vv;
-    if (q == 0) A.yg[vo] = yn * gg;
+    if (q == 0) {
+        if (F16IO) ((_Float16 *)A.yg)[vo] = (_Float16)(yn * gg);
+        else ((float *)A.yg)[vo] = yn * gg;
+    }
 }
 
 int launch_wkv7_lora(rsv_ctx *ctx, const WkvLoraArgs &a, int batch) {
@@ -278,7 +283,8 @@ int launch_wkv7_lora(rsv_ctx *ctx, const WkvLoraArgs &a, int batch) {
         L4 += a.mid_n[m];
     }
     if (L4 > 1024) return RSV_FAIL("wkv7_lora: LoRA ranks sum to %d (max 1024)", L4);
-    hipLaunchKernelGGL(k_wkv7_lora, dim3(a.H, batch), dim3(256), 0, ctx->stream, a);
+    if (a.f16_io) hipLaunchKernelGGL(k_wkv7_lora<true>, dim3(a.H, batch), dim3(256), 0, ctx->stream, a);
+    else hipLaunchKernelGGL(k_wkv7_lora<false>, dim3(a.H, batch), dim3(256), 0, ctx->stream, a);
     RSV_HIP(hipGetLastError());
     return 0;
 }

@@ -241,15 +241,17 @@ int launch_mul_to_f16(rsv_ctx *ctx, const float *a, const float *b, _Float16 *y,
 struct WkvLoraArgs {
     float *S;                        // [B, H, 64, 64]
     const float *r, *k, *v, *vf;     // [B, C] (vf: v_first)
-    const float *mid[4];             // LoRA-up inputs w (tanh applied), a, v, g (raw): [B, mid]
+    const void *mid[4];              // LoRA-up inputs w (tanh applied), a, v, g: [B, mid], F32 (g raw) or,
+                                     // with f16_io, F16 (g with its sigmoid applied)
     const _Float16 *up[4];           // LoRA-up weights [C, mid]
     const float *w0, *a0, *v0;       // [C]
     const float *scale;              // device scalar (decay scale)
     const float *kk, *ka, *rk, *gamma, *beta;  // [C]
-    float *yg;                       // [B, C] out: (GroupNorm(y) + bonus) * g
+    void *yg;                        // [B, C] out: (GroupNorm(y) + bonus) * g, F32 or (f16_io) F16
     const float *side_src;           // [B, C] copied to side_dst (optional)
     float *side_dst;
     int H, mid_n[4];
+    int f16_io;
     float eps, gn_eps;
 };
 int launch_wkv7_lora(rsv_ctx *ctx, const WkvLoraArgs &a, int batch);

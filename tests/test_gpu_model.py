@@ -396,3 +396,23 @@ def test_fused_lora_wkv_matches_two_launches(bundles, kind, monkeypatch):
     for a, c in zip(one, two):
         assert rel_rmse(a, c) <= 1e-5
     assert rel_rmse(s_one, s_two) <= 1e-5
+
+
+@pytest.mark.parametrize("kind", ["f16", "i8"])
+def test_batched_fused_lora_wkv(bundles, kind, monkeypatch):
+    """The batched layer's fused LoRA-up + WKV7 launch (RSV_WKV_LORA_MM=1,
+    fp16 operands in and out) equals its two-launch form to fp32 rounding."""
+    b, _ = bundles[kind]
+    B = 20
+    prompts = [_prompt(3 + (i % 5), 60 + i) for i in range(B)]
+    toks = np.array([(11 * i + 5) % SMALL["vocab"] for i in range(B)], np.uint32)
+    out = {}
+    for flag in ("0", "1"):
+        monkeypatch.setenv("RSV_WKV_LORA_MM", flag)
+        S = b.create_batch_state(B)
+        b.forward_seq_batch(S, prompts)
+        lg = b.forward_tokens_batch(S, toks)
+        out[flag] = (lg.copy(), S.back().copy())
+        S.free()
+    assert rel_rmse(out["1"][0], out["0"][0]) <= 1e-4
+    assert rel_rmse(out["1"][1], out["0"][1]) <= 1e-4
