@@ -944,6 +944,252 @@ __global__ __launch_bounds__(256) void k_gemv_os(GemvJobs jobs) {
     }
 }
 
+// One-shot GEMV, second form: NT threads per block (NT/64 waves x 64/LPR
+// rows each).  Every vector load of the block (x and, for the LN-mix
+// prologue, gamma/beta/coef/prev) goes out before the weight loads and
+// returns ahead of them (vector memory returns in order), so the prologue
+// runs while the weights stream.  The per-chunk sums of x (zero-point term
+// of the int8 dot) are taken once per block into LDS instead of once per
+// row.  Wider blocks than k_gemv_os mean fewer copies of x and of the LN
+// vectors per CU, and one LN per 10-20 rows instead of per 4-8.
+template <int NT>
+__device__ __forceinline__ float block_sum_nt(float v, float *red) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float t = red[0];
+#pragma unroll
+    for (int w = 1; w < NT / 64; w++) t += red[w];
+    return t;
+}
+
+// PV: vectors the prologue may need (0 x only, 1 x and the gate, 2 the LN-mix set)
+template <int FMT, int LPR, int CPL, int Q, int NT, int PV>
+__device__ __forceinline__ void gemv_os2_body(const GemvJob &J, int rb, float4 *xs, float *red) {
+    constexpr int CW = FMT == FMT_I8 ? 16 : 8;
+    constexpr int P = CW / 4;
+    constexpr int SLOTS = 64 / LPR, NW = NT / 64;
+    const int K = J.K, M = J.M, NC = K / CW, KG = K / 128, K4 = K / 4;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int slot = lane / LPR, li = lane % LPR;
+    const int row0 = (rb * NW + wave) * SLOTS + slot;
+    const int row = min(row0, M - 1);
+    const bool ln = PV == 2 && J.pro == PRO_LNMIX, mul = PV >= 1 && J.pro == PRO_MUL;
+    // 1. vectors (clamped addresses; lanes past K are zeroed after the loads)
+    const float4 *X4 = (const float4 *)J.x;
+    float4 xa[Q], ga[PV >= 1 ? Q : 1], ba[PV == 2 ? Q : 1], ca[PV == 2 ? Q : 1], pa[PV == 2 ? Q : 1];
+#pragma unroll
+    for (int i = 0; i < Q; i++) {
+        const int q = min(tid + NT * i, K4 - 1);
+        xa[i] = X4[q];
+        if constexpr (PV == 2) {
+            if (ln) {
+                ga[i] = ((const float4 *)J.gamma)[q];
+                ba[i] = ((const float4 *)J.beta)[q];
+                ca[i] = ((const float4 *)J.coef)[q];
+                pa[i] = ((const float4 *)J.prev)[q];
+            }
+        }
+        if constexpr (PV >= 1) {
+            if (mul) ga[i] = ((const float4 *)J.xmul)[q];
+        }
+    }
+    // 2. weights of the block's rows, all in flight
+    const u32x4 *W = (const u32x4 *)J.w;
+    u32x4 wv[CPL];
+    uint32_t szv[CPL];
+#pragma unroll
+    for (int j = 0; j < CPL; j++) {
+        const int c = min(li + LPR * j, NC - 1);
+        wv[j] = __builtin_nontemporal_load(W + (size_t)row * NC + c);
+        if (FMT == FMT_I8) szv[j] = J.sz[(size_t)row * KG + (c >> 3)];
+    }
+    // 3. prologue
+#pragma unroll
+    for (int i = 0; i < Q; i++)
+        if (tid + NT * i >= K4) xa[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if constexpr (PV == 2) {
+      if (ln) {
+        // LN over the row (two-pass, model.rs:625-635), then the token-shift mix
+        float s = 0.0f;
+#pragma unroll
+        for (int i = 0; i < Q; i++) s += (xa[i].x + xa[i].y) + (xa[i].z + xa[i].w);
+        const float mu = block_sum_nt<NT>(s, red) / (float)K;
+        float v2 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < Q; i++) {
+            if (tid + NT * i >= K4) continue;
+            const float d0 = xa[i].x - mu, d1 = xa[i].y - mu, d2 = xa[i].z - mu, d3 = xa[i].w - mu;
+            v2 += (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
+        }
+        const float inv = 1.0f / sqrtf(block_sum_nt<NT>(v2, red) / (float)K + 1.0e-5f);
+        const bool wr = J.lnout && rb == 0;
+#pragma unroll
+        for (int i = 0; i < Q; i++) {
+            const int q = tid + NT * i;
+            if (q >= K4) continue;
+            float4 l;
+            l.x = (xa[i].x - mu) * inv * ga[i].x + ba[i].x;
+            l.y = (xa[i].y - mu) * inv * ga[i].y + ba[i].y;
+            l.z = (xa[i].z - mu) * inv * ga[i].z + ba[i].z;
+            l.w = (xa[i].w - mu) * inv * ga[i].w + ba[i].w;
+            if (wr) ((float4 *)J.lnout)[q] = l;
+            xa[i].x = l.x + ca[i].x * (pa[i].x - l.x);
+            xa[i].y = l.y + ca[i].y * (pa[i].y - l.y);
+            xa[i].z = l.z + ca[i].z * (pa[i].z - l.z);
+            xa[i].w = l.w + ca[i].w * (pa[i].w - l.w);
+        }
+      }
+    }
+    if constexpr (PV >= 1) {
+        if (mul) {
+#pragma unroll
+            for (int i = 0; i < Q; i++) {
+                xa[i].x *= ga[i].x; xa[i].y *= ga[i].y; xa[i].z *= ga[i].z; xa[i].w *= ga[i].w;
+            }
+        }
+    }
+    if (J.pro == PRO_SIGMOID) {
+#pragma unroll
+        for (int i = 0; i < Q; i++) {
+            if (tid + NT * i >= K4) continue;
+            xa[i].x = sigmoid_f(xa[i].x); xa[i].y = sigmoid_f(xa[i].y);
+            xa[i].z = sigmoid_f(xa[i].z); xa[i].w = sigmoid_f(xa[i].w);
+        }
+    }
+    // 4. x chunk-major into LDS (float4 part p of chunk c at p*NC + c); for
+    // int8 the chunk sums of x after it, from the 4 lanes holding the chunk
+    float *dxs = reinterpret_cast<float *>(xs + K4);
+#pragma unroll
+    for (int i = 0; i < Q; i++) {
+        const int q = tid + NT * i;
+        if (q < K4) xs[((4 * q) % CW >> 2) * NC + (4 * q) / CW] = xa[i];
+        if (FMT == FMT_I8) {
+            float cs = (xa[i].x + xa[i].y) + (xa[i].z + xa[i].w);
+            cs += __shfl_xor(cs, 1, 64);
+            cs += __shfl_xor(cs, 2, 64);
+            if (q < K4 && (q & 3) == 0) dxs[q >> 2] = cs;
+        }
+    }
+    __syncthreads();
+    // 5. dot products
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < CPL; j++) {
+        const int cr = li + LPR * j;
+        const bool live = cr < NC;
+        const int c = live ? cr : NC - 1;
+        float xv[CW];
+#pragma unroll
+        for (int p = 0; p < P; p++) {
+            const float4 t = xs[p * NC + c];
+            xv[4 * p] = t.x; xv[4 * p + 1] = t.y; xv[4 * p + 2] = t.z; xv[4 * p + 3] = t.w;
+        }
+        if (FMT == FMT_I8) {
+            // w = s*q + z over one 16-weight chunk of a 128-group (model.rs:234-252)
+            const float dx = dxs[c];
+            float d = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const uint32_t wq = wv[j][q];
+                d = fmaf(xv[4 * q + 0], (float)(wq & 0xFFu), d);
+                d = fmaf(xv[4 * q + 1], (float)((wq >> 8) & 0xFFu), d);
+                d = fmaf(xv[4 * q + 2], (float)((wq >> 16) & 0xFFu), d);
+                d = fmaf(xv[4 * q + 3], (float)(wq >> 24), d);
+            }
+            const uint32_t sw = live ? szv[j] : 0u;
+            acc = fmaf(h2f(sw), d, fmaf(h2f(sw >> 16), dx, acc));
+        } else {
+            float d = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const uint32_t wq = wv[j][q];
+                d = fmaf(xv[2 * q + 0], h2f(wq), d);
+                d = fmaf(xv[2 * q + 1], h2f(wq >> 16), d);
+            }
+            acc += live ? d : 0.0f;
+        }
+    }
+#pragma unroll
+    for (int o = LPR / 2; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+    if (li == 0 && row0 < M) apply_epi(J, row0, 0, acc);
+}
+
+template <int CPL, int Q, int NT, int PV>
+__global__ __launch_bounds__(NT) void k_gemv_os2(GemvJobs jobs) {
+    extern __shared__ float4 xs4[];
+    __shared__ float red[NT / 64];
+    const int bid = blockIdx.x;
+    if (bid == 0 && jobs.side.src)
+        for (int i = threadIdx.x; i < jobs.side.n; i += NT) jobs.side.dst[i] = jobs.side.src[i];
+    int ji = 0;
+    while (ji + 1 < jobs.n && bid >= jobs.blk_start[ji + 1]) ji++;
+    const GemvJob &J = jobs.j[ji];
+    const int rb = bid - jobs.blk_start[ji];
+    if (J.fmt == FMT_I8) {
+        if (J.lpr == 32) gemv_os2_body<FMT_I8, 32, CPL, Q, NT, PV>(J, rb, xs4, red);
+        else gemv_os2_body<FMT_I8, 64, CPL, Q, NT, PV>(J, rb, xs4, red);
+    } else {
+        if (J.lpr == 32) gemv_os2_body<FMT_F16, 32, CPL, Q, NT, PV>(J, rb, xs4, red);
+        else gemv_os2_body<FMT_F16, 64, CPL, Q, NT, PV>(J, rb, xs4, red);
+    }
+}
+
+// B=1 launch on k_gemv_os2 (prologues in the kernel).  640-thread blocks
+// for LN-mix launches and rows longer than 2560, 320 otherwise (measured on
+// the 3B decode shapes).  Returns 1 when the jobs do not fit.
+static int launch_os2(rsv_ctx *ctx, GemvJobs &jobs) {
+    int cpl_max = 0, kmax = 0;
+    bool lnmix = false, gate = false;
+    for (int i = 0; i < jobs.n; i++) {
+        GemvJob &J = jobs.j[i];
+        const int nc = J.K / (J.fmt == FMT_I8 ? 16 : 8);
+        J.lpr = nc <= 32 * 5 ? 32 : 64;
+        const int cpl = (nc + J.lpr - 1) / J.lpr;
+        if (cpl > 10 || J.K % 16 != 0 || nc < J.lpr / 2) return 1;
+        cpl_max = std::max(cpl_max, cpl);
+        kmax = std::max(kmax, J.K);
+        lnmix |= J.pro == PRO_LNMIX;
+        gate |= J.pro == PRO_MUL;
+    }
+    const int nt = (lnmix || kmax > 2560) ? 640 : 320;
+    const int qn = (kmax / 4 + nt - 1) / nt;
+    const int q = qn <= 1 ? 1 : qn <= 2 ? 2 : qn <= 4 ? 4 : 0;
+    if (!q || (lnmix && q > 2)) return 1;
+    int total = 0;
+    for (int i = 0; i < jobs.n; i++) {
+        GemvJob &J = jobs.j[i];
+        const int rpb = (nt / 64) * (64 / J.lpr);
+        J.nblk = (J.M + rpb - 1) / rpb;
+        jobs.blk_start[i] = total;
+        total += J.nblk;
+    }
+    jobs.blk_start[jobs.n] = total;
+    const size_t lds = (size_t)kmax * 4 + (size_t)kmax / 16 * 4;
+#define OS2(C, QQ, N, V) hipLaunchKernelGGL((k_gemv_os2<C, QQ, N, V>), dim3(total), dim3(N), lds, ctx->stream, jobs)
+    const bool c5 = cpl_max <= 5;
+    if (lnmix) {
+        if (q == 1) { if (c5) OS2(5, 1, 640, 2); else OS2(10, 1, 640, 2); }
+        else { if (c5) OS2(5, 2, 640, 2); else OS2(10, 2, 640, 2); }
+    } else if (nt == 320) {  // k <= 2560: at most 5 chunks per lane
+        if (q == 1) { if (gate) OS2(5, 1, 320, 1); else OS2(5, 1, 320, 0); }
+        else { if (gate) OS2(5, 2, 320, 1); else OS2(5, 2, 320, 0); }
+    } else {
+        if (q <= 2) {
+            if (gate) { if (c5) OS2(5, 2, 640, 1); else OS2(10, 2, 640, 1); }
+            else { if (c5) OS2(5, 2, 640, 0); else OS2(10, 2, 640, 0); }
+        } else {
+            if (gate) { if (c5) OS2(5, 4, 640, 1); else OS2(10, 4, 640, 1); }
+            else { if (c5) OS2(5, 4, 640, 0); else OS2(10, 4, 640, 0); }
+        }
+    }
+#undef OS2
+    RSV_HIP(hipGetLastError());
+    return 0;
+}
+
 // B=1 launch on the one-shot kernel: LN-mix prologues become one pre-pass
 // launch writing each distinct mixed vector once.  Returns 1 when the jobs
 // do not fit this path (the caller then uses the general kernel).
@@ -1041,7 +1287,11 @@ int launch_gemv_jobs(rsv_ctx *ctx, GemvJobs &jobs, int batch) {
     if (jobs.side.src && (!jobs.side.dst || jobs.side.n <= 0)) return RSV_FAIL("gemv: bad side copy");
     // B=1: launches with an LN-mix prologue take the register-resident kernel
     // (the prologue runs inside it), the others the one-shot kernel
-    static const int b1_kernel = env_int("RSV_GEMV_B1", 3);  // 3 by prologue, 2 one-shot, 1 register, 0 general
+    static const int b1_kernel = env_int("RSV_GEMV_B1", 4);  // 4 one-shot v2, 3 by prologue, 2 one-shot, 1 register, 0 general
+    if (batch == 1 && b1_kernel == 4) {
+        const int rc = launch_os2(ctx, jobs);
+        if (rc <= 0) return rc;
+    }
     bool lnmix = false;
     for (int i = 0; i < jobs.n; i++) lnmix |= jobs.j[i].pro == PRO_LNMIX;
     if (batch == 1 && (b1_kernel == 2 || (b1_kernel == 3 && !lnmix))) {
