@@ -377,8 +377,7 @@ int rsv_wkv7_decode_ex(rsv_ctx *ctx, uint32_t s, uint32_t k, uint32_t k_k, uint3
  * g = sigmoid(g_mid).G2^T; then the WKV7 step on state [batch, H, 64, 64]
  * (updated in place) and yg = (GroupNorm(y) + bonus) * g, the att.output
  * operand.  side_src [batch, C] is copied to side_dst when both are given
- * (ids 0xFFFFFFFF: none).  Ranks must be multiples of 32, summing to at
- * most 1024. */
+ * (ids 0xFFFFFFFF: none).  Each rank must be a multiple of 32 in 32..256. */
 typedef struct rsv_wkv_lora {
     uint32_t state, r, k, v, v_first;
     uint32_t w_mid, a_mid, v_mid, g_mid; /* F32 [batch, rank] */

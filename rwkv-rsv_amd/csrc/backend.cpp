@@ -351,7 +351,7 @@ int rsv_wkv7_lora_decode(rsv_ctx *ctx, const rsv_wkv_lora *op, uint64_t batch) {
     WkvLoraArgs a{};
     a.H = (int)H;
     for (int m = 0; m < 4; m++) {
-        if (rk[m] == 0 || rk[m] > 1024) return RSV_FAIL("wkv7_lora_decode: rank %llu", (unsigned long long)rk[m]);
+        if (rk[m] == 0 || rk[m] > 256) return RSV_FAIL("wkv7_lora_decode: rank %llu", (unsigned long long)rk[m]);
         a.mid_n[m] = (int)rk[m];
     }
     a.eps = op->eps;

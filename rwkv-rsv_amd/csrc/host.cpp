@@ -684,7 +684,7 @@ bool wkv_lora_ok(const rsv_model_info &I) {
     const uint64_t r[4] = {I.w_mid, I.a_mid, I.v_mid, I.g_mid};
     uint64_t sum = 0;
     for (uint64_t v : r) {
-        if (v == 0 || v % 32) return false;
+        if (v == 0 || v % 32 || v > 256) return false;
         sum += v;
     }
     return sum <= 1024 && I.head_size == 64;

@@ -34,6 +34,16 @@ __device__ __forceinline__ uint32_t sk_pack(float a, float b) {
            ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)b) << 16);
 }
 
+// fp16 pair (s*q0 + z, s*q1 + z): each an fp32 fma, the pair converted to
+// fp16 (round to nearest even) by one v_cvt_pk_f16_f32.  Building the pair
+// as a vector keeps the compiler from packing two halves with a shift and an
+// or, which is what the scalar-half form lowers to.
+typedef _Float16 sk_half2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t sk_deq2(float s, float q0, float q1, float z) {
+    const sk_half2 h = {(_Float16)fmaf(s, q0, z), (_Float16)fmaf(s, q1, z)};
+    return __builtin_bit_cast(uint32_t, h);
+}
+
 // One 32-column k-chunk of a wave's operands: two 32-row weight tiles and
 // MT session tiles of x.
 template <int MT>
@@ -87,8 +97,8 @@ __device__ __forceinline__ void sk_mma(const SkChunk<MT> &ch, bool i8, sk_f16x (
 #pragma unroll
             for (int q = 0; q < 4; q++) {
                 const uint32_t w = ch.w[rt][0][q];
-                wh[2 * q] = sk_pack(fmaf(s, (float)(w & 0xFFu), z), fmaf(s, (float)((w >> 8) & 0xFFu), z));
-                wh[2 * q + 1] = sk_pack(fmaf(s, (float)((w >> 16) & 0xFFu), z), fmaf(s, (float)(w >> 24), z));
+                wh[2 * q] = sk_deq2(s, (float)(w & 0xFFu), (float)((w >> 8) & 0xFFu), z);
+                wh[2 * q + 1] = sk_deq2(s, (float)((w >> 16) & 0xFFu), (float)(w >> 24), z);
             }
         } else {
 #pragma unroll
@@ -426,8 +436,8 @@ __global__ __launch_bounds__(256) void k_skinny4(SkinnyJobs jobs, int MB, float 
 #pragma unroll
                 for (int h = 0; h < 4; h++) {
                     const uint32_t u = w[q][0][h];
-                    wh[2 * h] = sk_pack(fmaf(s, (float)(u & 0xFFu), z), fmaf(s, (float)((u >> 8) & 0xFFu), z));
-                    wh[2 * h + 1] = sk_pack(fmaf(s, (float)((u >> 16) & 0xFFu), z), fmaf(s, (float)(u >> 24), z));
+                    wh[2 * h] = sk_deq2(s, (float)(u & 0xFFu), (float)((u >> 8) & 0xFFu), z);
+                    wh[2 * h + 1] = sk_deq2(s, (float)((u >> 16) & 0xFFu), (float)(u >> 24), z);
                 }
             } else {
 #pragma unroll
@@ -593,8 +603,8 @@ __global__ __launch_bounds__(256) void k_skinny5(SkinnyJobs jobs, int MB, float 
 #pragma unroll
             for (int h = 0; h < 4; h++) {
                 const uint32_t u = wr[p][0][h];
-                wh[2 * h] = sk_pack(fmaf(s, (float)(u & 0xFFu), z), fmaf(s, (float)((u >> 8) & 0xFFu), z));
-                wh[2 * h + 1] = sk_pack(fmaf(s, (float)((u >> 16) & 0xFFu), z), fmaf(s, (float)(u >> 24), z));
+                wh[2 * h] = sk_deq2(s, (float)(u & 0xFFu), (float)((u >> 8) & 0xFFu), z);
+                wh[2 * h + 1] = sk_deq2(s, (float)((u >> 16) & 0xFFu), (float)(u >> 24), z);
             }
         } else {
 #pragma unroll
@@ -701,8 +711,8 @@ __global__ __launch_bounds__(256) void k_skinny_sk(SkinnyJobs jobs, int MB) {
 #pragma unroll
             for (int h = 0; h < 4; h++) {
                 const uint32_t u = wr[c][0][h];
-                wh[2 * h] = sk_pack(fmaf(sc, (float)(u & 0xFFu), z), fmaf(sc, (float)((u >> 8) & 0xFFu), z));
-                wh[2 * h + 1] = sk_pack(fmaf(sc, (float)((u >> 16) & 0xFFu), z), fmaf(sc, (float)(u >> 24), z));
+                wh[2 * h] = sk_deq2(sc, (float)(u & 0xFFu), (float)((u >> 8) & 0xFFu), z);
+                wh[2 * h + 1] = sk_deq2(sc, (float)((u >> 16) & 0xFFu), (float)(u >> 24), z);
             }
         } else {
 #pragma unroll

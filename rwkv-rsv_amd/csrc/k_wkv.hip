@@ -149,7 +149,7 @@ int launch_wkv7_decode(rsv_ctx *ctx, float *s, const float *k, const float *kk, 
 // v-first lerp, g) and the WKV7 step of that head in one block, for small
 // batches: grid (H, B), 256 threads.  Thread (j = tid/4, q = tid%4) owns
 // channel 64h+j: it takes quarter q of each LoRA-up dot (the inputs staged in
-// LDS, the weights read straight from global, 16 bytes at a time) and
+// LDS, the weights loaded into registers at kernel entry, ranks <= 256) and
 // columns 16q..16q+15 of state row j.  Quad sums run on DPP.  The output is
 // y_norm * g, the att.output operand.  Blocks with h == 0 also copy
 // side_src -> side_dst for their session (the token-shift state row).
@@ -182,7 +182,20 @@ __global__ __launch_bounds__(256) void k_wkv7_lora(WkvLoraArgs A) {
     const size_t vo = (size_t)b * C + c;
     const int m0 = A.mid_n[0], m1 = A.mid_n[1], m2 = A.mid_n[2], m3 = A.mid_n[3];
     const int L4 = m0 + m1 + m2 + m3;
-    // every global load of the block first: LoRA-up inputs, per-channel vectors, the state row part
+    // every global load of the block first, the LoRA-up weights ahead of the
+    // rest: quarter q of row c of each up matrix [C, mid], at most 8 16-byte
+    // pieces per matrix (rank <= 256); pieces past a matrix's quarter are not
+    // loaded (uniform branches)
+    constexpr int kUp = 8;
+    uint4 wl[4][kUp];
+#pragma unroll
+    for (int m = 0; m < 4; m++) {
+        const int mid = A.mid_n[m], np = mid >> 5;
+        const uint4 *wp = (const uint4 *)(A.up[m] + (size_t)c * mid + q * (mid >> 2));
+#pragma unroll
+        for (int e = 0; e < kUp; e++)
+            if (e < np) wl[m][e] = wp[e];
+    }
     for (int e = tid; e < L4; e += 256) {
         const int m = e < m0 ? 0 : e < m0 + m1 ? 1 : e < m0 + m1 + m2 ? 2 : 3;
         const int off = m == 0 ? 0 : m == 1 ? m0 : m == 2 ? m0 + m1 : m0 + m1 + m2;
@@ -200,18 +213,19 @@ __global__ __launch_bounds__(256) void k_wkv7_lora(WkvLoraArgs A) {
     if (h == 0 && A.side_dst)
         for (int e = tid; e < C; e += 256) A.side_dst[(size_t)b * C + e] = A.side_src[(size_t)b * C + e];
     __syncthreads();
-    // LoRA-up dots: quarter q of row c of each up matrix [C, mid]
+    // LoRA-up dots, reduced over the quad
     float acc[4];
     int mo = 0;
 #pragma unroll
     for (int m = 0; m < 4; m++) {
-        const int mid = A.mid_n[m], seg = mid >> 2;
-        const uint4 *wp = (const uint4 *)(A.up[m] + (size_t)c * mid + q * seg);
-        const float *xm = mids + mo + q * seg;
+        const int mid = A.mid_n[m], np = mid >> 5;
+        const float *xm = mids + mo + q * (mid >> 2);
         float sm = 0.0f;
-        for (int e = 0; e < seg; e += 8) {
-            const uint4 w = wp[e >> 3];
-            const float4 x0 = *(const float4 *)(xm + e), x1 = *(const float4 *)(xm + e + 4);
+#pragma unroll
+        for (int e = 0; e < kUp; e++) {
+            if (e >= np) break;
+            const uint4 w = wl[m][e];
+            const float4 x0 = *(const float4 *)(xm + 8 * e), x1 = *(const float4 *)(xm + 8 * e + 4);
             sm = fmaf(x0.x, h2f_w(w.x), sm);
             sm = fmaf(x0.y, h2f_w(w.x >> 16), sm);
             sm = fmaf(x0.z, h2f_w(w.y), sm);
@@ -279,7 +293,8 @@ int launch_wkv7_lora(rsv_ctx *ctx, const WkvLoraArgs &a, int batch) {
     if (a.H <= 0 || batch <= 0 || batch > 65535) return RSV_FAIL("wkv7_lora: bad h=%d batch=%d", a.H, batch);
     int L4 = 0;
     for (int m = 0; m < 4; m++) {
-        if (a.mid_n[m] <= 0 || a.mid_n[m] % 32) return RSV_FAIL("wkv7_lora: LoRA rank %d not a multiple of 32", a.mid_n[m]);
+        if (a.mid_n[m] <= 0 || a.mid_n[m] % 32 || a.mid_n[m] > 256)
+            return RSV_FAIL("wkv7_lora: LoRA rank %d must be a multiple of 32 in 32..256", a.mid_n[m]);
         L4 += a.mid_n[m];
     }
     if (L4 > 1024) return RSV_FAIL("wkv7_lora: LoRA ranks sum to %d (max 1024)", L4);
