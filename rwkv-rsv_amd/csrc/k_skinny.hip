@@ -29,6 +29,17 @@ __device__ __forceinline__ float sk_h2f(uint32_t b) {
 }
 __device__ __forceinline__ float sk_sig(float v) { return 1.0f / (1.0f + expf(-v)); }
 
+// Output stores carry the non-temporal hint.  Every output here is read only
+// by a later launch; with plain stores a wave's writes took ~7 us to be
+// acknowledged (measured on a 2.6 MB output), with the hint ~1 us, and the
+// launch cannot end before its stores have.
+__device__ __forceinline__ void sk_st(float *p, float v) { __builtin_nontemporal_store(v, p); }
+__device__ __forceinline__ void sk_st(_Float16 *p, _Float16 v) { __builtin_nontemporal_store(v, p); }
+typedef float sk_f32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void sk_st4(float4 *p, float4 v) {
+    __builtin_nontemporal_store((sk_f32x4){v.x, v.y, v.z, v.w}, reinterpret_cast<sk_f32x4 *>(p));
+}
+
 __device__ __forceinline__ uint32_t sk_pack(float a, float b) {
     return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)a) |
            ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)b) << 16);
@@ -177,22 +188,82 @@ __device__ __forceinline__ void sk_store(const SkEpi &E, float v, int n, int b) 
         default: break;
     }
     if (E.y_f16)
-        ((_Float16 *)E.y)[yo] = (_Float16)v;
+        sk_st((_Float16 *)E.y + yo, (_Float16)v);
     else
-        ((float *)E.y)[yo] = v;
-    if (E.y2) E.y2[yo] = v;
+        sk_st((float *)E.y + yo, v);
+    if (E.y2) sk_st(E.y2 + yo, v);
 }
+
+// y[b, n] (epilogue)= v with the read operands (y for add / v-lerp, aux,
+// bias) already loaded by the caller.
+__device__ __forceinline__ void sk_store_v(const SkEpi &E, float v, float yc, float ax, float bias, int n, int b) {
+    const size_t yo = (size_t)b * E.ldy + n;
+    switch (E.epi) {
+        case GE_BIAS: v += bias; break;
+        case GE_ADD: v += yc; break;
+        case GE_RELU2: v = v > 0.0f ? v * v : 0.0f; break;
+        case GE_TANH: v = tanhf(v); break;
+        case GE_WDECAY: v = expf(sk_sig(v + bias) * E.scale); break;
+        case GE_SIGBIAS: v = sk_sig(v + bias); break;
+        case GE_VLERP: v = yc + sk_sig(v + bias) * (ax - yc); break;
+        case GE_SIGMOID: v = sk_sig(v); break;
+        default: break;
+    }
+    if (E.y_f16)
+        sk_st((_Float16 *)E.y + yo, (_Float16)v);
+    else
+        sk_st((float *)E.y + yo, v);
+    if (E.y2) sk_st(E.y2 + yo, v);
+}
+
+// Epilogue value for a compile-time epilogue kind.  The tile epilogues
+// switch on the kind once and run a loop instantiated for it: a switch inside
+// an unrolled per-element loop put ~10k instructions into one kernel, and
+// its waves then spent most of the epilogue waiting on instruction fetch.
+template <int EPI>
+__device__ __forceinline__ float sk_epi_val(float v, float yc, float ax, float bias, float scale) {
+    if constexpr (EPI == GE_BIAS) return v + bias;
+    else if constexpr (EPI == GE_ADD) return v + yc;
+    else if constexpr (EPI == GE_RELU2) return v > 0.0f ? v * v : 0.0f;
+    else if constexpr (EPI == GE_TANH) return tanhf(v);
+    else if constexpr (EPI == GE_WDECAY) return expf(sk_sig(v + bias) * scale);
+    else if constexpr (EPI == GE_SIGBIAS) return sk_sig(v + bias);
+    else if constexpr (EPI == GE_VLERP) return yc + sk_sig(v + bias) * (ax - yc);
+    else if constexpr (EPI == GE_SIGMOID) return sk_sig(v);
+    else return v;
+}
+__device__ __forceinline__ void sk_put(const SkEpi &E, size_t yo, float v) {
+    if (E.y_f16)
+        sk_st((_Float16 *)E.y + yo, (_Float16)v);
+    else
+        sk_st((float *)E.y + yo, v);
+    if (E.y2) sk_st(E.y2 + yo, v);
+}
+// Runs f.template operator()<EPI>() for the epilogue kind of E.
+#define SK_EPI_DISPATCH(E, CALL)                      \
+    switch ((E).epi) {                                \
+        case GE_BIAS: CALL(GE_BIAS); break;           \
+        case GE_ADD: CALL(GE_ADD); break;             \
+        case GE_RELU2: CALL(GE_RELU2); break;         \
+        case GE_TANH: CALL(GE_TANH); break;           \
+        case GE_WDECAY: CALL(GE_WDECAY); break;       \
+        case GE_SIGBIAS: CALL(GE_SIGBIAS); break;     \
+        case GE_VLERP: CALL(GE_VLERP); break;         \
+        case GE_SIGMOID: CALL(GE_SIGMOID); break;     \
+        default: CALL(GE_STORE); break;               \
+    }
 
 // Epilogue of a 128-row x TB-session tile held in LDS (tile[row][session]).
 // Thread t always handles row t % 128 (coalesced stores along n), so the
 // bias is read once; the read-modify-write operands of 8 sessions are
 // loaded together before any of them is used.
-template <int TB>
-__device__ __forceinline__ void sk_store_tile(const SkEpi &E, const float (*tile)[TB + 1], int n0, int MB) {
+template <int EPI, int TB>
+__device__ __forceinline__ void sk_store_tile_t(const SkEpi &E, const float (*tile)[TB + 1], int n0, int MB) {
     const int r = threadIdx.x & 127, n = n0 + r;
     if (n >= E.N) return;
-    const float bias = E.bias ? E.bias[n] : 0.0f;
-    const bool need_y = E.epi == GE_ADD || E.epi == GE_VLERP;
+    constexpr bool need_y = EPI == GE_ADD || EPI == GE_VLERP;
+    constexpr bool need_b = EPI == GE_BIAS || EPI == GE_WDECAY || EPI == GE_SIGBIAS || EPI == GE_VLERP;
+    const float bias = need_b ? E.bias[n] : 0.0f;
     for (int b0 = threadIdx.x >> 7; b0 < MB; b0 += 16) {
         float yc[8], ax[8];
 #pragma unroll
@@ -200,32 +271,21 @@ __device__ __forceinline__ void sk_store_tile(const SkEpi &E, const float (*tile
             const int b = b0 + 2 * q;
             const size_t yo = (size_t)b * E.ldy + n;
             yc[q] = (need_y && b < MB) ? ((const float *)E.y)[yo] : 0.0f;
-            ax[q] = (E.epi == GE_VLERP && b < MB) ? E.aux[yo] : 0.0f;
+            ax[q] = (EPI == GE_VLERP && b < MB) ? E.aux[yo] : 0.0f;
         }
 #pragma unroll
         for (int q = 0; q < 8; q++) {
             const int b = b0 + 2 * q;
             if (b >= MB) break;
-            const size_t yo = (size_t)b * E.ldy + n;
-            float v = tile[r][b];
-            switch (E.epi) {
-                case GE_BIAS: v += bias; break;
-                case GE_ADD: v += yc[q]; break;
-                case GE_RELU2: v = v > 0.0f ? v * v : 0.0f; break;
-                case GE_TANH: v = tanhf(v); break;
-                case GE_WDECAY: v = expf(sk_sig(v + bias) * E.scale); break;
-                case GE_SIGBIAS: v = sk_sig(v + bias); break;
-                case GE_VLERP: v = yc[q] + sk_sig(v + bias) * (ax[q] - yc[q]); break;
-                case GE_SIGMOID: v = sk_sig(v); break;
-                default: break;
-            }
-            if (E.y_f16)
-                ((_Float16 *)E.y)[yo] = (_Float16)v;
-            else
-                ((float *)E.y)[yo] = v;
-            if (E.y2) E.y2[yo] = v;
+            sk_put(E, (size_t)b * E.ldy + n, sk_epi_val<EPI>(tile[r][b], yc[q], ax[q], bias, E.scale));
         }
     }
+}
+template <int TB>
+__device__ __forceinline__ void sk_store_tile(const SkEpi &E, const float (*tile)[TB + 1], int n0, int MB) {
+#define SK_TILE_CALL(K) sk_store_tile_t<K, TB>(E, tile, n0, MB)
+    SK_EPI_DISPATCH(E, SK_TILE_CALL)
+#undef SK_TILE_CALL
 }
 
 // grid: for each job, (rows/64) row groups x J.split k-slices.  Block = 4
@@ -296,7 +356,7 @@ __global__ __launch_bounds__(256) void k_skinny(SkinnyJobs jobs, int MB, float *
     if (J.split > 1) {
         // slice tile, row-group-major then slice: [rg][sl][64 rows][TB sessions]
         float *wsp = ws + ((size_t)J.ws_slot + (size_t)rg * J.split + sl) * 64 * TB;
-        for (int o = tid; o < 64 * TB; o += 256) wsp[o] = tile[o & 63][o >> 6];
+        for (int o = tid; o < 64 * TB; o += 256) sk_st(wsp + o, tile[o & 63][o >> 6]);
         return;
     }
     for (int o = tid; o < 64 * TB; o += 256) {
@@ -498,7 +558,7 @@ __global__ __launch_bounds__(256) void k_skinny4(SkinnyJobs jobs, int MB, float 
         float4 *wsp = (float4 *)(ws + ((size_t)J.ws_slot + (size_t)rg * J.split + sl) * 128 * TB);
         for (int o4 = tid; o4 < 32 * TB; o4 += 256) {
             const int r = (4 * o4) & 127, b = (4 * o4) >> 7;
-            wsp[o4] = make_float4(tile[r][b], tile[r + 1][b], tile[r + 2][b], tile[r + 3][b]);
+            sk_st4(wsp + o4, make_float4(tile[r][b], tile[r + 1][b], tile[r + 2][b], tile[r + 3][b]));
         }
         return;
     }
@@ -648,7 +708,7 @@ __global__ __launch_bounds__(256) void k_skinny5(SkinnyJobs jobs, int MB, float 
         float4 *wsp = (float4 *)(ws + ((size_t)J.ws_slot + (size_t)rg * J.split + sl) * 128 * TB);
         for (int o4 = tid; o4 < 32 * TB; o4 += 256) {
             const int r = (4 * o4) & 127, b = (4 * o4) >> 7;
-            wsp[o4] = make_float4(tile[r][b], tile[r + 1][b], tile[r + 2][b], tile[r + 3][b]);
+            sk_st4(wsp + o4, make_float4(tile[r][b], tile[r + 1][b], tile[r + 2][b], tile[r + 3][b]));
         }
         return;
     }
@@ -928,6 +988,119 @@ static int launch_v5(rsv_ctx *ctx, SkinnyJobs &jobs, int MB) {
 // Jobs of K <= 32*SK_SMALL_NCH in one pass each (k_skinny_sk): one block per
 // 128 rows, no k-split and no reduce launch.
 constexpr int SK_SMALL_NCH = 8;
+// Epilogue of k_skinny_sk1 for one epilogue kind: every read operand of the
+// thread's sessions is loaded in one round, then the values are stored.
+template <int EPI, int TB>
+__device__ __forceinline__ void sk1_epilogue(const SkEpi &E, const float (*tile)[TB + 1], int n, int lane, int MB) {
+    constexpr int NI = TB / 2;
+    constexpr bool need_y = EPI == GE_ADD || EPI == GE_VLERP;
+    constexpr bool need_b = EPI == GE_BIAS || EPI == GE_WDECAY || EPI == GE_SIGBIAS || EPI == GE_VLERP;
+    const int r = lane & 31, g = lane >> 5;
+    float yc[NI], ax[NI];
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+        const int b = g + 2 * i;
+        const size_t yo = (size_t)b * E.ldy + n;
+        yc[i] = (need_y && b < MB) ? ((const float *)E.y)[yo] : 0.0f;
+        ax[i] = (EPI == GE_VLERP && b < MB) ? E.aux[yo] : 0.0f;
+    }
+    const float bias = need_b ? E.bias[n] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+        const int b = g + 2 * i;
+        if (b >= MB) break;
+        sk_put(E, (size_t)b * E.ldy + n, sk_epi_val<EPI>(tile[r][b], yc[i], ax[i], bias, E.scale));
+    }
+}
+
+// Small-K batched GEMM, one wave per block on one 32-row tile of one job.
+// A small-K job moves little data per row, so the launch is bound by what
+// each CU can pull: one-wave blocks spread the row tiles of all jobs over
+// up to N/32 CUs (k_skinny_sk puts 128 rows, i.e. four copies of x, on one
+// CU).  Only the job's own chunks are loaded (uniform branches), every load
+// of the wave goes out at once, and the epilogue loads all of its
+// read-modify-write operands in one round after the MFMAs.
+template <int MT, bool I8, int NCH>
+__global__ __launch_bounds__(64) void k_skinny_sk1(SkinnyJobs jobs, int MB) {
+    constexpr int TB = MT * 32;
+    constexpr int WV = I8 ? 1 : 2;
+    __shared__ float tile[32][TB + 1];
+    const int bid = blockIdx.x;
+    int ji = 0;
+    while (ji + 1 < jobs.n && bid >= jobs.blk_start[ji + 1]) ji++;
+    const SkinnyJob &J = jobs.j[ji];
+    const int rt = bid - jobs.blk_start[ji];
+    const int lane = threadIdx.x, g = lane >> 5;
+    const int nchunks = J.K / 32;
+    const int row = rt * 32 + (lane & 31);
+    const bool row_ok = row < J.N;
+    constexpr int tbytes = I8 ? 1024 : 2048;
+    const uint8_t *wt = (const uint8_t *)J.w + (row_ok ? (size_t)rt * nchunks * tbytes : 0) + lane * (I8 ? 16 : 32);
+    const uint32_t *szrow = I8 ? J.sz + (size_t)min(rt, (J.N - 1) / 32) * (J.K / 128) * 32 + (lane & 31) : nullptr;
+    sk_u32x4 wr[NCH][WV];
+    uint32_t sr[NCH];
+    sk_u32x4 xv[NCH][MT][2];
+#pragma unroll
+    for (int c = 0; c < NCH; c++) {
+        if (c >= nchunks) break;  // uniform: one job per block
+#pragma unroll
+        for (int v = 0; v < WV; v++) wr[c][v] = ((const sk_u32x4 *)(wt + (size_t)c * tbytes))[v];
+        if (I8) sr[c] = szrow[(size_t)(c >> 2) * 32];
+#pragma unroll
+        for (int ct = 0; ct < MT; ct++) {
+            const int b = min(ct * 32 + (lane & 31), MB - 1);  // sessions past MB are computed, never stored
+            const sk_u32x4 *xp = (const sk_u32x4 *)(J.x + (size_t)b * J.ldx + c * 32 + 16 * g);
+            xv[c][ct][0] = xp[0];
+            xv[c][ct][1] = xp[1];
+        }
+    }
+    sk_f16x acc[MT];
+#pragma unroll
+    for (int ct = 0; ct < MT; ct++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) acc[ct][e] = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NCH; c++) {
+        if (c >= nchunks) break;
+        uint32_t wh[8];
+        if (I8) {
+            const float sc = row_ok ? sk_h2f(sr[c]) : 0.0f, z = row_ok ? sk_h2f(sr[c] >> 16) : 0.0f;
+#pragma unroll
+            for (int h = 0; h < 4; h++) {
+                const uint32_t u = wr[c][0][h];
+                wh[2 * h] = sk_deq2(sc, (float)(u & 0xFFu), (float)((u >> 8) & 0xFFu), z);
+                wh[2 * h + 1] = sk_deq2(sc, (float)((u >> 16) & 0xFFu), (float)(u >> 24), z);
+            }
+        } else {
+#pragma unroll
+            for (int h = 0; h < 4; h++) {
+                wh[h] = row_ok ? wr[c][0][h] : 0u;
+                wh[4 + h] = row_ok ? wr[c][WV - 1][h] : 0u;
+            }
+        }
+#pragma unroll
+        for (int st = 0; st < 2; st++) {
+            const sk_half8 a = __builtin_bit_cast(sk_half8, (sk_u32x4){wh[4 * st], wh[4 * st + 1], wh[4 * st + 2], wh[4 * st + 3]});
+#pragma unroll
+            for (int ct = 0; ct < MT; ct++)
+                acc[ct] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, __builtin_bit_cast(sk_half8, xv[c][ct][st]), acc[ct], 0, 0, 0);
+        }
+    }
+    // acc[ct][e] -> (row 8*(e/4) + 4g + e%4, session ct*32 + lane%32)
+#pragma unroll
+    for (int ct = 0; ct < MT; ct++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) tile[8 * (e >> 2) + 4 * g + (e & 3)][ct * 32 + (lane & 31)] = acc[ct][e];
+    __syncthreads();
+    // thread: row r = lane % 32, sessions lane/32 + 2i (32 consecutive rows per store)
+    const SkEpi E = sk_epi_of(J);
+    const int n = rt * 32 + (lane & 31);
+    if (n >= E.N) return;
+#define SK1_CALL(K) sk1_epilogue<K, TB>(E, tile, n, lane, MB)
+    SK_EPI_DISPATCH(E, SK1_CALL)
+#undef SK1_CALL
+}
+
 static int launch_small(rsv_ctx *ctx, SkinnyJobs &jobs, int MB) {
     int total = 0;
     for (int i = 0; i < jobs.n; i++) {
@@ -941,6 +1114,29 @@ static int launch_small(rsv_ctx *ctx, SkinnyJobs &jobs, int MB) {
     const bool i8 = jobs.j[0].fmt == FMT_I8;
     for (int i = 1; i < jobs.n; i++)
         if ((jobs.j[i].fmt == FMT_I8) != i8) return RSV_FAIL("skinny gemm: mixed formats in one tiled launch");
+    static const int one_wave = [] {
+        const char *e = getenv("RSV_SKINNY_SK1");
+        return e ? atoi(e) : 1;
+    }();
+    if (one_wave) {
+        total = 0;
+        for (int i = 0; i < jobs.n; i++) {
+            SkinnyJob &J = jobs.j[i];
+            J.nblk = (J.N + 31) / 32;
+            jobs.blk_start[i] = total;
+            total += J.nblk;
+        }
+        jobs.blk_start[jobs.n] = total;
+        if (MB <= 32) {
+            if (i8) hipLaunchKernelGGL((k_skinny_sk1<1, true, SK_SMALL_NCH>), dim3(total), dim3(64), 0, ctx->stream, jobs, MB);
+            else hipLaunchKernelGGL((k_skinny_sk1<1, false, SK_SMALL_NCH>), dim3(total), dim3(64), 0, ctx->stream, jobs, MB);
+        } else {
+            if (i8) hipLaunchKernelGGL((k_skinny_sk1<2, true, SK_SMALL_NCH>), dim3(total), dim3(64), 0, ctx->stream, jobs, MB);
+            else hipLaunchKernelGGL((k_skinny_sk1<2, false, SK_SMALL_NCH>), dim3(total), dim3(64), 0, ctx->stream, jobs, MB);
+        }
+        RSV_HIP(hipGetLastError());
+        return 0;
+    }
     if (MB <= 32) {
         if (i8) hipLaunchKernelGGL((k_skinny_sk<1, true, SK_SMALL_NCH>), dim3(total), dim3(256), 0, ctx->stream, jobs, MB);
         else hipLaunchKernelGGL((k_skinny_sk<1, false, SK_SMALL_NCH>), dim3(total), dim3(256), 0, ctx->stream, jobs, MB);
