@@ -571,16 +571,11 @@ __global__ __launch_bounds__(256) void k_skinny4(SkinnyJobs jobs, int MB, float 
 typedef _Float16 sk_half8 __attribute__((ext_vector_type(8)));
 
 template <int MT, bool I8>
-__global__ __launch_bounds__(256) void k_skinny5(SkinnyJobs jobs, int MB, float *__restrict__ ws) {
+__device__ __forceinline__ void skinny5_body(const SkinnyJob &J, int local, int MB, float *__restrict__ ws,
+                                             unsigned char *smem5) {
     constexpr int TB = MT * 32;
     constexpr int PD = I8 ? 8 : 6;    // chunks in flight per wave
     constexpr int WV = I8 ? 1 : 2;    // 16-byte loads per lane per chunk
-    extern __shared__ __attribute__((aligned(16))) unsigned char smem5[];
-    const int bid = blockIdx.x;
-    int ji = 0;
-    while (ji + 1 < jobs.n && bid >= jobs.blk_start[ji + 1]) ji++;
-    const SkinnyJob &J = jobs.j[ji];
-    const int local = bid - jobs.blk_start[ji];
     const int rg = local / J.split, sl = local - (local / J.split) * J.split;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 5;
     const int nchunks = J.K / 32;
@@ -703,6 +698,30 @@ __global__ __launch_bounds__(256) void k_skinny5(SkinnyJobs jobs, int MB, float 
         return;
     }
     sk_store_tile<TB>(sk_epi_of(J), tile, n0, MB);
+}
+
+template <int MT, bool I8>
+__global__ __launch_bounds__(256) void k_skinny5(SkinnyJobs jobs, int MB, float *__restrict__ ws) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem5[];
+    const int bid = blockIdx.x;
+    int ji = 0;
+    while (ji + 1 < jobs.n && bid >= jobs.blk_start[ji + 1]) ji++;
+    skinny5_body<MT, I8>(jobs.j[ji], bid - jobs.blk_start[ji], MB, ws, smem5);
+}
+
+// The same for a job list holding both weight formats (stage-1: int8 r/k/v
+// next to the fp16 LoRA-down matrices): the block takes its job's body, so
+// the two formats share one launch and one slice reduction.
+template <int MT>
+__global__ __launch_bounds__(256) void k_skinny5_mixed(SkinnyJobs jobs, int MB, float *__restrict__ ws) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem5[];
+    const int bid = blockIdx.x;
+    int ji = 0;
+    while (ji + 1 < jobs.n && bid >= jobs.blk_start[ji + 1]) ji++;
+    if (jobs.j[ji].fmt == FMT_I8)
+        skinny5_body<MT, true>(jobs.j[ji], bid - jobs.blk_start[ji], MB, ws, smem5);
+    else
+        skinny5_body<MT, false>(jobs.j[ji], bid - jobs.blk_start[ji], MB, ws, smem5);
 }
 
 // Small-K batched GEMM (K <= 32*NCH, e.g. the LoRA-up chain, K = 64..256):
@@ -880,6 +899,8 @@ static int launch_slab(rsv_ctx *ctx, SkinnyJobs &jobs, int MB);
 
 // Batches above 64 run as consecutive 64-row slabs; tiled jobs of the two
 // weight formats run as separate launches (per-format register budgets).
+constexpr int SK_SMALL_NCH = 8;  // chunks (of 32) of the small-K kernels: K <= 256
+
 int launch_skinny(rsv_ctx *ctx, SkinnyJobs &jobs, int MB) {
     if (MB <= 0) return RSV_FAIL("skinny gemm: batch %d", MB);
     if (jobs.n > 0 && jobs.j[0].tiled) {
@@ -888,7 +909,17 @@ int launch_skinny(rsv_ctx *ctx, SkinnyJobs &jobs, int MB) {
             SkinnyJobs &p = parts[jobs.j[i].fmt == FMT_I8 ? 0 : 1];
             p.j[p.n++] = jobs.j[i];
         }
-        if (parts[0].n && parts[1].n) {
+        // both formats share one k_skinny5_mixed launch when every job takes
+        // that path (no small-K job, none large enough for k_skinny4)
+        static const int mixed_on = [] {
+            const char *e = getenv("RSV_SKINNY_MIXED");
+            return e ? atoi(e) : 1;
+        }();
+        bool one = mixed_on != 0;
+        const int cus = ctx->sm_count > 0 ? ctx->sm_count : 256;
+        for (int i = 0; i < jobs.n; i++)
+            one &= jobs.j[i].K > 32 * SK_SMALL_NCH && (jobs.j[i].N + 127) / 128 < 2 * cus;
+        if (parts[0].n && parts[1].n && !one) {
             for (auto &p : parts)
                 if (launch_skinny(ctx, p, MB)) return -1;
             return 0;
@@ -955,9 +986,12 @@ static int launch_v5(rsv_ctx *ctx, SkinnyJobs &jobs, int MB) {
     jobs.red_start[jobs.n] = red_total;
     if (ws_need > ctx->skinny_ws_cap) return RSV_FAIL("skinny gemm: workspace too small (%zu floats)", ws_need);
     const bool i8 = jobs.j[0].fmt == FMT_I8;
-    for (int i = 1; i < jobs.n; i++)
-        if ((jobs.j[i].fmt == FMT_I8) != i8) return RSV_FAIL("skinny gemm: mixed formats in one tiled launch");
-    if (MB <= 32) {
+    bool mixed = false;
+    for (int i = 1; i < jobs.n; i++) mixed |= (jobs.j[i].fmt == FMT_I8) != i8;
+    if (mixed) {
+        if (MB <= 32) hipLaunchKernelGGL((k_skinny5_mixed<1>), dim3(total), dim3(256), lds, ctx->stream, jobs, MB, ctx->skinny_ws);
+        else hipLaunchKernelGGL((k_skinny5_mixed<2>), dim3(total), dim3(256), lds, ctx->stream, jobs, MB, ctx->skinny_ws);
+    } else if (MB <= 32) {
         if (i8) hipLaunchKernelGGL((k_skinny5<1, true>), dim3(total), dim3(256), lds, ctx->stream, jobs, MB, ctx->skinny_ws);
         else hipLaunchKernelGGL((k_skinny5<1, false>), dim3(total), dim3(256), lds, ctx->stream, jobs, MB, ctx->skinny_ws);
     } else {
@@ -975,9 +1009,6 @@ static int launch_v5(rsv_ctx *ctx, SkinnyJobs &jobs, int MB) {
     return 0;
 }
 
-// Jobs of K <= 32*SK_SMALL_NCH in one pass each (k_skinny_sk): one block per
-// 128 rows, no k-split and no reduce launch.
-constexpr int SK_SMALL_NCH = 8;
 // Epilogue of k_skinny_sk1 for one epilogue kind: every read operand of the
 // thread's sessions is loaded in one round, then the values are stored.
 template <int EPI, int TB>
@@ -1091,6 +1122,9 @@ __global__ __launch_bounds__(64) void k_skinny_sk1(SkinnyJobs jobs, int MB) {
 #undef SK1_CALL
 }
 
+// Jobs of K <= 32*SK_SMALL_NCH in one pass each, no k-split and no reduce
+// launch: k_skinny_sk1 (one wave per 32 rows; default) or k_skinny_sk (one
+// block per 128 rows, RSV_SKINNY_SK1=0).
 static int launch_small(rsv_ctx *ctx, SkinnyJobs &jobs, int MB) {
     int total = 0;
     for (int i = 0; i < jobs.n; i++) {
