@@ -15,10 +15,23 @@
 
 namespace rsv {
 
+// Sum over the 64 lanes of a wave, returned to every lane.  DPP row
+// operations (quad perms, half-row and row mirrors, then row broadcasts 15
+// and 31 into the upper rows) leave the total in lane 63, which readlane
+// broadcasts: a few cycles per step instead of an LDS round trip per
+// butterfly step of __shfl_xor.
+template <int CTRL, int RM = 0xF>
+__device__ __forceinline__ float wdpp(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, RM, 0xF, false));
+}
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
+    v += wdpp<0xB1>(v);        // quad_perm 1,0,3,2
+    v += wdpp<0x4E>(v);        // quad_perm 2,3,0,1
+    v += wdpp<0x141>(v);       // row_half_mirror
+    v += wdpp<0x140>(v);       // row_mirror: each lane holds its 16-lane row sum
+    v += wdpp<0x142, 0xA>(v);  // row_bcast:15 into rows 1 and 3
+    v += wdpp<0x143, 0xC>(v);  // row_bcast:31 into rows 2 and 3
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
 struct HeadVecs {
@@ -330,9 +343,17 @@ __global__ __launch_bounds__(64) void k_wkv7_seq_ragged(
     }
     const float kkc_i = kkc[h * 64 + i], ka_i = ka[h * 64 + i], rk_i = rk[h * 64 + i];
     const float gm_i = gamma[h * 64 + i], bt_i = beta[h * 64 + i];
+    // the next token's vectors are loaded while the current one is computed
+    size_t vn = (size_t)t0 * C + (size_t)h * 64 + i;
+    float nk = 0.f, na = 0.f, nr = 0.f, nv = 0.f, nw = 0.f;
+    if (len > 0) { nk = k[vn]; na = a[vn]; nr = r[vn]; nv = v[vn]; nw = w[vn]; }
     for (uint32_t t = 0; t < len; t++) {
         const size_t vo = (size_t)(t0 + t) * C + (size_t)h * 64;
-        const float ki = k[vo + i], ai = a[vo + i], ri = r[vo + i], vi = v[vo + i], wi = w[vo + i];
+        const float ki = nk, ai = na, ri = nr, vi = nv, wi = nw;
+        if (t + 1 < len) {  // uniform
+            vn += C;
+            nk = k[vn]; na = a[vn]; nr = r[vn]; nv = v[vn]; nw = w[vn];
+        }
         float kmod;
         __syncthreads();  // previous token's readers are done with hv
         head_vectors(hv, i, ki, kkc_i, ai, ka_i, ri, wi, eps, kmod);
