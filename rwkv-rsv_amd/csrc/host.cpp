@@ -1201,6 +1201,28 @@ int prefill(rsv_bundle *b, GpuState &s, const std::vector<Seg> &segs, float *log
 
 constexpr uint64_t kMaxChunk = 4096;
 
+// Water filling: the largest piece length L with sum_i min(rem_i, L) <= cap
+// (every remaining length when they all fit).  Packing one piece of at most
+// L tokens per unfinished prompt keeps a chunk's longest piece, and so its
+// sequential WKV scan, as short as the chunk size allows.
+static uint64_t water_fill(const std::vector<uint64_t> &rem, uint64_t cap) {
+    uint64_t hi = 0, all = 0;
+    for (uint64_t r : rem) {
+        hi = std::max(hi, r);
+        all += r;
+    }
+    if (all <= cap || hi == 0) return hi;
+    uint64_t lo = 0;
+    while (lo < hi) {
+        const uint64_t mid = (lo + hi + 1) / 2;
+        uint64_t sum = 0;
+        for (uint64_t r : rem) sum += std::min(r, mid);
+        if (sum <= cap) lo = mid;
+        else hi = mid - 1;
+    }
+    return lo;
+}
+
 // Single-session prefill in chunks of at most kMaxChunk tokens.
 int seq_single(rsv_bundle *b, GpuState &s, uint64_t slot, const uint32_t *tokens, uint64_t n, float *logits) {
     if (n == 0) return herr("infer_seq: empty token list");
@@ -1281,10 +1303,15 @@ int serve_ragged(rsv_bundle *b, GpuState &s, const uint32_t *tokens, const uint6
                     ndec++;
                 }
             }
-            for (uint64_t q = 0; q < B && used < budget; q++) {  // then prompt chunks
+            // then one prompt piece per prompting slot, water-filled into the
+            // rest of the budget
+            std::vector<uint64_t> rem(B);
+            for (uint64_t q = 0; q < B; q++) rem[q] = sl[q].plen - sl[q].done;
+            const uint64_t L = std::max<uint64_t>(1, water_fill(rem, budget - used));
+            for (uint64_t q = 0; q < B && used < budget; q++) {
                 ServeSlot &z = sl[q];
                 if (z.done >= z.plen) continue;
-                const uint64_t take = std::min(z.plen - z.done, budget - used);
+                const uint64_t take = std::min({z.plen - z.done, budget - used, L});
                 segs.push_back({z.prompt + z.done, take, q});
                 seg_slot.push_back(q);
                 samples.push_back(z.done + take == z.plen);
@@ -1636,11 +1663,14 @@ int rsv_forward_seq_batch(rsv_bundle *b, rsv_state *s, const uint32_t *tokens, c
         off += lens[q];
         T += lens[q];
     }
-    // split into packed chunks of at most kMaxChunk tokens; long prompts are
-    // cut into consecutive pieces that keep their slot order
+    // Packed chunks of at most kMaxChunk tokens, filled breadth-first: every
+    // unfinished prompt contributes its next piece of at most L tokens, with
+    // L the largest length whose pieces still fit one chunk (water filling).
+    // A prompt's pieces go through consecutive chunks in order, its state
+    // carried between them.  The WKV scan of a chunk is sequential over its
+    // longest piece, so many short pieces per chunk keep that scan short;
+    // per-token arithmetic does not depend on the packing.
     std::vector<Seg> pending;
-    uint64_t used = 0;
-    std::vector<float> lg;
     auto flush = [&]() -> int {
         if (pending.empty()) return 0;
         std::vector<float> tmp;
@@ -1650,21 +1680,23 @@ int rsv_forward_seq_batch(rsv_bundle *b, rsv_state *s, const uint32_t *tokens, c
             for (size_t i = 0; i < pending.size(); i++)
                 memcpy(logits + pending[i].slot * b->info.vocab, &tmp[i * b->info.vocab], b->info.vocab * 4);
         pending.clear();
-        used = 0;
         return 0;
     };
-    for (auto &g : segs) {
-        uint64_t done = 0;
-        while (done < g.len) {
-            if (used == kMaxChunk) HK(flush());
-            // a slot may appear only once per packed chunk
-            for (auto &p : pending)
-                if (p.slot == g.slot) { HK(flush()); break; }
-            const uint64_t take = std::min<uint64_t>(g.len - done, kMaxChunk - used);
-            pending.push_back({g.tok + done, take, g.slot});
+    std::vector<uint64_t> done(segs.size(), 0);
+    for (;;) {
+        std::vector<uint64_t> rem(segs.size());
+        for (size_t i = 0; i < segs.size(); i++) rem[i] = segs[i].len - done[i];
+        if (rem.empty() || *std::max_element(rem.begin(), rem.end()) == 0) break;
+        const uint64_t L = std::max<uint64_t>(1, water_fill(rem, kMaxChunk));
+        uint64_t used = 0;
+        for (size_t i = 0; i < segs.size(); i++) {
+            const uint64_t take = std::min({segs[i].len - done[i], L, kMaxChunk - used});
+            if (take == 0) continue;
+            pending.push_back({segs[i].tok + done[i], take, segs[i].slot});
+            done[i] += take;
             used += take;
-            done += take;
         }
+        HK(flush());
     }
     HK(flush());
     return 0;
