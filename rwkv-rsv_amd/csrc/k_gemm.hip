@@ -161,6 +161,175 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
         }
 }
 
+// Second form: the same 128x128 tile, loaders and dequant, with the LDS
+// stage double-buffered (one barrier per k-step: the next slab is written to
+// the other buffer while this one is multiplied out) and the gfx950
+// v_mfma_f32_32x32x16_f16 (16 k per instruction; lane l holds k 8*(l/32) ..
+// +7 of each 16-k half of the 32-k slab, the same mapping for A and B).  The
+// epilogue switches once on its kind (a per-element switch unrolled 64 times
+// made the kernel body several thousand instructions long).
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+
+template <int EPI>
+__device__ __forceinline__ float gemm_epi_val(float v, float bias, float aux, float cur, float scale) {
+    if constexpr (EPI == GE_BIAS) return v + bias;
+    else if constexpr (EPI == GE_ADD) return v + aux;
+    else if constexpr (EPI == GE_RELU2) return v > 0.0f ? v * v : 0.0f;
+    else if constexpr (EPI == GE_TANH) return tanhf(v);
+    else if constexpr (EPI == GE_WDECAY) return expf(sigm_g(v + bias) * scale);
+    else if constexpr (EPI == GE_SIGBIAS) return sigm_g(v + bias);
+    else if constexpr (EPI == GE_VLERP) return cur + sigm_g(v + bias) * (aux - cur);
+    else if constexpr (EPI == GE_SIGMOID) return sigm_g(v);
+    else return v;
+}
+
+template <int EPI>
+__device__ __forceinline__ void gemm2_epilogue(const GemmArgs &g, const float16_t (&acc)[2][2], int m0, int n0, int wm,
+                                               int wn, int lane) {
+    constexpr bool need_b = EPI == GE_BIAS || EPI == GE_WDECAY || EPI == GE_SIGBIAS || EPI == GE_VLERP;
+    constexpr bool need_aux = EPI == GE_ADD || EPI == GE_VLERP;
+    const float scale = EPI == GE_WDECAY ? g.scale[0] : 0.0f;
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int col = n0 + wn + j * 32 + (lane & 31);
+        if (col >= g.n) continue;
+        const float bias = need_b ? g.bias[col] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                const int row = m0 + wm + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+                if (row >= g.m) continue;
+                const size_t o = (size_t)row * g.ldc + col;
+                const float aux = need_aux ? g.aux[o] : 0.0f;
+                const float cur = EPI == GE_VLERP ? ((const float *)g.c)[o] : 0.0f;
+                const float v = gemm_epi_val<EPI>(acc[i][j][e], bias, aux, cur, scale);
+                if (g.c_f16)
+                    ((_Float16 *)g.c)[o] = (_Float16)v;
+                else
+                    ((float *)g.c)[o] = v;
+            }
+        }
+    }
+}
+
+template <bool B_I8>
+__global__ __launch_bounds__(256) void k_gemm2(GemmArgs g) {
+    __shared__ __attribute__((aligned(16))) _Float16 As[2][BM * LDK];
+    __shared__ __attribute__((aligned(16))) _Float16 Bs[2][BN * LDK];
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+    const int lr = tid >> 1, lc = (tid & 1) * 16;  // loader: row, first k of 16
+
+    float16_t acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) acc[i][j][e] = 0.0f;
+
+    u32x4g ra[2], rb[2];
+    uint32_t rsz = 0;
+    const int arow = m0 + lr, brow = n0 + lr;
+    const bool aok = arow < g.m, bok = brow < g.n;
+    const int KG = g.k / 128;
+    auto load = [&](int k0) {
+        if (aok) {
+            const u32x4g *p = (const u32x4g *)(g.a + (size_t)arow * g.lda + k0 + lc);
+            ra[0] = p[0];
+            ra[1] = p[1];
+        } else {
+            ra[0] = ra[1] = (u32x4g){0u, 0u, 0u, 0u};
+        }
+        if (B_I8) {
+            if (bok) {
+                rb[0] = *(const u32x4g *)((const uint8_t *)g.b + (size_t)brow * g.k + k0 + lc);
+                rsz = g.sz[(size_t)brow * KG + (k0 + lc) / 128];
+            } else {
+                rb[0] = (u32x4g){0u, 0u, 0u, 0u};
+                rsz = 0;
+            }
+        } else {
+            if (bok) {
+                const u32x4g *p = (const u32x4g *)((const _Float16 *)g.b + (size_t)brow * g.k + k0 + lc);
+                rb[0] = p[0];
+                rb[1] = p[1];
+            } else {
+                rb[0] = rb[1] = (u32x4g){0u, 0u, 0u, 0u};
+            }
+        }
+    };
+    auto stage = [&](int buf) {
+        u32x4g *ad = (u32x4g *)(As[buf] + lr * LDK + lc);
+        ad[0] = ra[0];
+        ad[1] = ra[1];
+        u32x4g *bd = (u32x4g *)(Bs[buf] + lr * LDK + lc);
+        if (B_I8) {
+            // w = s*q + z with the product and the sum each rounded to fp32
+            // (model.rs:234-252), then rounded to fp16
+            const float s = h2f_g(rsz), z = h2f_g(rsz >> 16);
+            uint32_t o[8];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const uint32_t w = rb[0][q];
+                const float w0 = __fadd_rn(__fmul_rn(s, (float)(w & 0xFFu)), z);
+                const float w1 = __fadd_rn(__fmul_rn(s, (float)((w >> 8) & 0xFFu)), z);
+                const float w2 = __fadd_rn(__fmul_rn(s, (float)((w >> 16) & 0xFFu)), z);
+                const float w3 = __fadd_rn(__fmul_rn(s, (float)(w >> 24)), z);
+                o[2 * q] = pack2(w0, w1);
+                o[2 * q + 1] = pack2(w2, w3);
+            }
+            bd[0] = (u32x4g){o[0], o[1], o[2], o[3]};
+            bd[1] = (u32x4g){o[4], o[5], o[6], o[7]};
+        } else {
+            bd[0] = rb[0];
+            bd[1] = rb[1];
+        }
+    };
+
+    load(0);
+    stage(0);
+    __syncthreads();
+    int cur = 0;
+    for (int k0 = 0; k0 < g.k; k0 += BK) {
+        const bool more = k0 + BK < g.k;
+        if (more) load(k0 + BK);
+#pragma unroll
+        for (int st = 0; st < 2; st++) {
+            half8_t af[2], bf[2];
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+                af[i] = *(const half8_t *)(As[cur] + (wm + i * 32 + (lane & 31)) * LDK + 16 * st + 8 * (lane >> 5));
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+                bf[j] = *(const half8_t *)(Bs[cur] + (wn + j * 32 + (lane & 31)) * LDK + 16 * st + 8 * (lane >> 5));
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int j = 0; j < 2; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+        if (more) stage(cur ^ 1);
+        __syncthreads();
+        cur ^= 1;
+    }
+#define GEMM2_EPI(K) gemm2_epilogue<K>(g, acc, m0, n0, wm, wn, lane)
+    switch (g.epi) {
+        case GE_BIAS: GEMM2_EPI(GE_BIAS); break;
+        case GE_ADD: GEMM2_EPI(GE_ADD); break;
+        case GE_RELU2: GEMM2_EPI(GE_RELU2); break;
+        case GE_TANH: GEMM2_EPI(GE_TANH); break;
+        case GE_WDECAY: GEMM2_EPI(GE_WDECAY); break;
+        case GE_SIGBIAS: GEMM2_EPI(GE_SIGBIAS); break;
+        case GE_VLERP: GEMM2_EPI(GE_VLERP); break;
+        case GE_SIGMOID: GEMM2_EPI(GE_SIGMOID); break;
+        default: GEMM2_EPI(GE_STORE); break;
+    }
+#undef GEMM2_EPI
+}
+
 int launch_gemm(rsv_ctx *ctx, const GemmArgs &g) {
     if (g.m <= 0 || g.n <= 0 || g.k <= 0) return RSV_FAIL("gemm: bad shape m=%d n=%d k=%d", g.m, g.n, g.k);
     if (g.k % BK != 0) return RSV_FAIL("gemm: k=%d must be a multiple of %d", g.k, BK);
@@ -173,6 +342,18 @@ int launch_gemm(rsv_ctx *ctx, const GemmArgs &g) {
     if (g.epi == GE_WDECAY && !g.scale) return RSV_FAIL("gemm: decay epilogue needs scale");
     if (g.c_f16 && (g.epi == GE_ADD || g.epi == GE_VLERP)) return RSV_FAIL("gemm: in-place epilogues need fp32 C");
     dim3 grid((g.n + BN - 1) / BN, (g.m + BM - 1) / BM);
+    static const int v2 = [] {
+        const char *e = getenv("RSV_GEMM_V2");
+        return e ? atoi(e) : 1;
+    }();
+    if (v2) {
+        if (g.b_i8)
+            hipLaunchKernelGGL(k_gemm2<true>, grid, dim3(256), 0, ctx->stream, g);
+        else
+            hipLaunchKernelGGL(k_gemm2<false>, grid, dim3(256), 0, ctx->stream, g);
+        RSV_HIP(hipGetLastError());
+        return 0;
+    }
     if (g.b_i8)
         hipLaunchKernelGGL(k_gemm<true>, grid, dim3(256), 0, ctx->stream, g);
     else
