@@ -183,8 +183,8 @@ __device__ __forceinline__ float gemm_epi_val(float v, float bias, float aux, fl
     else return v;
 }
 
-template <int EPI>
-__device__ __forceinline__ void gemm2_epilogue(const GemmArgs &g, const float16_t (&acc)[2][2], int m0, int n0, int wm,
+template <int EPI, int MI>
+__device__ __forceinline__ void gemm2_epilogue(const GemmArgs &g, const float16_t (&acc)[MI][2], int m0, int n0, int wm,
                                                int wn, int lane) {
     constexpr bool need_b = EPI == GE_BIAS || EPI == GE_WDECAY || EPI == GE_SIGBIAS || EPI == GE_VLERP;
     constexpr bool need_aux = EPI == GE_ADD || EPI == GE_VLERP;
@@ -195,7 +195,7 @@ __device__ __forceinline__ void gemm2_epilogue(const GemmArgs &g, const float16_
         if (col >= g.n) continue;
         const float bias = need_b ? g.bias[col] : 0.0f;
 #pragma unroll
-        for (int i = 0; i < 2; i++) {
+        for (int i = 0; i < MI; i++) {
 #pragma unroll
             for (int e = 0; e < 16; e++) {
                 const int row = m0 + wm + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
@@ -213,35 +213,37 @@ __device__ __forceinline__ void gemm2_epilogue(const GemmArgs &g, const float16_
     }
 }
 
-template <bool B_I8>
+// BM2 rows (128 or 256) x 128 columns per block of 4 waves in a 2x2 layout:
+// each wave owns (BM2/2) x 64 as (BM2/64) x 2 MFMA 32x32 tiles.
+template <bool B_I8, int BM2>
 __global__ __launch_bounds__(256) void k_gemm2(GemmArgs g) {
-    __shared__ __attribute__((aligned(16))) _Float16 As[2][BM * LDK];
+    constexpr int MI = BM2 / 64;
+    constexpr int PA = BM2 * BK / 8 / 256;  // 16-byte A pieces per thread
+    __shared__ __attribute__((aligned(16))) _Float16 As[2][BM2 * LDK];
     __shared__ __attribute__((aligned(16))) _Float16 Bs[2][BN * LDK];
-    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    const int m0 = blockIdx.y * BM2, n0 = blockIdx.x * BN;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
-    const int lr = tid >> 1, lc = (tid & 1) * 16;  // loader: row, first k of 16
+    const int wm = (wave >> 1) * (BM2 / 2), wn = (wave & 1) * 64;
+    const int lr = tid >> 1, lc = (tid & 1) * 16;  // B loader: row, first k of 16
 
-    float16_t acc[2][2];
+    float16_t acc[MI][2];
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < MI; i++)
 #pragma unroll
         for (int j = 0; j < 2; j++)
 #pragma unroll
             for (int e = 0; e < 16; e++) acc[i][j][e] = 0.0f;
 
-    u32x4g ra[2], rb[2];
+    u32x4g ra[PA], rb[2];
     uint32_t rsz = 0;
-    const int arow = m0 + lr, brow = n0 + lr;
-    const bool aok = arow < g.m, bok = brow < g.n;
+    const int brow = n0 + lr;
+    const bool bok = brow < g.n;
     const int KG = g.k / 128;
     auto load = [&](int k0) {
-        if (aok) {
-            const u32x4g *p = (const u32x4g *)(g.a + (size_t)arow * g.lda + k0 + lc);
-            ra[0] = p[0];
-            ra[1] = p[1];
-        } else {
-            ra[0] = ra[1] = (u32x4g){0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int i = 0; i < PA; i++) {
+            const int p = tid + 256 * i, row = m0 + p / (BK / 8), c8 = p % (BK / 8);
+            ra[i] = row < g.m ? *(const u32x4g *)(g.a + (size_t)row * g.lda + k0 + 8 * c8) : (u32x4g){0u, 0u, 0u, 0u};
         }
         if (B_I8) {
             if (bok) {
@@ -262,9 +264,11 @@ __global__ __launch_bounds__(256) void k_gemm2(GemmArgs g) {
         }
     };
     auto stage = [&](int buf) {
-        u32x4g *ad = (u32x4g *)(As[buf] + lr * LDK + lc);
-        ad[0] = ra[0];
-        ad[1] = ra[1];
+#pragma unroll
+        for (int i = 0; i < PA; i++) {
+            const int p = tid + 256 * i;
+            *(u32x4g *)(As[buf] + (p / (BK / 8)) * LDK + 8 * (p % (BK / 8))) = ra[i];
+        }
         u32x4g *bd = (u32x4g *)(Bs[buf] + lr * LDK + lc);
         if (B_I8) {
             // w = s*q + z with the product and the sum each rounded to fp32
@@ -298,15 +302,15 @@ __global__ __launch_bounds__(256) void k_gemm2(GemmArgs g) {
         if (more) load(k0 + BK);
 #pragma unroll
         for (int st = 0; st < 2; st++) {
-            half8_t af[2], bf[2];
+            half8_t af[MI], bf[2];
 #pragma unroll
-            for (int i = 0; i < 2; i++)
+            for (int i = 0; i < MI; i++)
                 af[i] = *(const half8_t *)(As[cur] + (wm + i * 32 + (lane & 31)) * LDK + 16 * st + 8 * (lane >> 5));
 #pragma unroll
             for (int j = 0; j < 2; j++)
                 bf[j] = *(const half8_t *)(Bs[cur] + (wn + j * 32 + (lane & 31)) * LDK + 16 * st + 8 * (lane >> 5));
 #pragma unroll
-            for (int i = 0; i < 2; i++)
+            for (int i = 0; i < MI; i++)
 #pragma unroll
                 for (int j = 0; j < 2; j++)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
@@ -315,7 +319,7 @@ __global__ __launch_bounds__(256) void k_gemm2(GemmArgs g) {
         __syncthreads();
         cur ^= 1;
     }
-#define GEMM2_EPI(K) gemm2_epilogue<K>(g, acc, m0, n0, wm, wn, lane)
+#define GEMM2_EPI(K) gemm2_epilogue<K, MI>(g, acc, m0, n0, wm, wn, lane)
     switch (g.epi) {
         case GE_BIAS: GEMM2_EPI(GE_BIAS); break;
         case GE_ADD: GEMM2_EPI(GE_ADD); break;
@@ -347,10 +351,10 @@ int launch_gemm(rsv_ctx *ctx, const GemmArgs &g) {
         return e ? atoi(e) : 1;
     }();
     if (v2) {
-        if (g.b_i8)
-            hipLaunchKernelGGL(k_gemm2<true>, grid, dim3(256), 0, ctx->stream, g);
-        else
-            hipLaunchKernelGGL(k_gemm2<false>, grid, dim3(256), 0, ctx->stream, g);
+        // 128-row tiles: 256-row tiles (one wave per SIMD at 275 registers)
+        // measured 1.5x slower on the prefill GEMMs
+        if (g.b_i8) hipLaunchKernelGGL((k_gemm2<true, 128>), grid, dim3(256), 0, ctx->stream, g);
+        else hipLaunchKernelGGL((k_gemm2<false, 128>), grid, dim3(256), 0, ctx->stream, g);
         RSV_HIP(hipGetLastError());
         return 0;
     }
