@@ -581,6 +581,56 @@ def test_gemm_skinny(be, batch, k):
         assert rel_err(be.get(y16, batch * n).reshape(batch, n), np.tanh(acc)) < 2e-3
 
 
+@pytest.mark.parametrize("batch", [16, 64])
+def test_gemm_skinny_mixed_formats(be, batch):
+    """One job list with int8 and fp16 tiled weights (the batched stage-1
+    shape: int8 r/k/v next to fp16 LoRA-down) runs as one launch; every job
+    matches float64 with the loader's fp16 rounding of the weights, and the
+    shared launch matches one launch per format."""
+    rsv = _rsv()
+    rng = np.random.default_rng(90 + batch)
+    k = 1024
+    sig = lambda t: 1 / (1 + np.exp(-t))
+    x = rng.standard_normal((batch, k)).astype(np.float16)
+    xt = be.tensor(x.astype(np.float32), dtype=rsv.F16)
+    X = x.astype(np.float64)
+    out = ctypes.c_uint32()
+    jobs, refs, keep = [], [], []
+    for q, (fmt, n, epi) in enumerate([("i8", 640, 0), ("f16", 96, 4), ("i8", 320, 0), ("f16", 256, 8)]):
+        if fmt == "i8":
+            idx, sz, W = _int8_weight(rng, n, k)
+            h = be.int8(idx, sz)
+            ht = rsv.Int8Handle(h.idx, h.sz, h.m, h.k)
+            be.call("rsv_tile_weights", h.idx, n, k, 1, ctypes.byref(out))
+            ht.idx = out.value
+            be.call("rsv_tile_weights", h.sz, n, k, 4, ctypes.byref(out))
+            ht.sz = out.value
+            keep.append(ht)
+            w8, w16, Wm = ctypes.pointer(ht), NONE, W.astype(np.float16).astype(np.float64)
+        else:
+            W16 = (rng.standard_normal((n, k)) * 0.02).astype(np.float16)
+            wt = be.tensor(W16.astype(np.float32), dtype=rsv.F16)
+            be.call("rsv_tile_weights", wt, n, k, 2, ctypes.byref(out))
+            w8, w16, Wm = None, out.value, W16.astype(np.float64)
+        acc = X @ Wm.T
+        refs.append({0: acc, 4: np.tanh(acc), 8: sig(acc)}[epi])
+        y = be.tensor(n=batch * n)
+        jobs.append((rsv.MmJob(w16, w8, n, k, xt, y, NONE, epi, NONE, NONE, NONE, 1), y, n))
+    arr = (rsv.MmJob * len(jobs))(*[j for j, _, _ in jobs])
+    be.call("rsv_gemm_skinny", ctypes.cast(arr, ctypes.c_void_p), len(jobs), batch)
+    mixed = []
+    for (j, y, n), ref in zip(jobs, refs):
+        got = be.get(y, batch * n).reshape(batch, n)
+        assert rel_err(got, ref) < 2e-5, n
+        mixed.append(got)
+    for fmt_jobs in ([0, 2], [1, 3]):  # one launch per format
+        sub = (rsv.MmJob * 2)(*[jobs[i][0] for i in fmt_jobs])
+        be.call("rsv_gemm_skinny", ctypes.cast(sub, ctypes.c_void_p), 2, batch)
+        for i in fmt_jobs:
+            _, y, n = jobs[i]
+            assert rel_err(be.get(y, batch * n).reshape(batch, n), mixed[i]) < 1e-6, i
+
+
 def test_ln_mix_f16_and_wkv_yg(be):
     rsv = _rsv()
     rng = np.random.default_rng(70)
