@@ -95,14 +95,18 @@ __global__ __launch_bounds__(64) void k_wkv7_decode(float *__restrict__ S, const
                                                     float *__restrict__ y_out, float *__restrict__ yn_out,
                                                     int H, float eps, float gn_eps,
                                                     const float *__restrict__ gmul, _Float16 *__restrict__ yg16) {
-    __shared__ float tile[64 * 65];
+    // the transpose goes through a 32-row tile twice (8.3 KB instead of
+    // 16.6 KB), so that ten blocks fit a CU and a B=64 launch (2560 blocks)
+    // runs in one round
+    __shared__ float tile[32 * 65];
     __shared__ HeadVecs hv;
     const int h = blockIdx.x, b = blockIdx.y, i = threadIdx.x;
     const size_t C = (size_t)H * 64;
     const size_t vo = (size_t)b * C + (size_t)h * 64;
     float4 *Sg = (float4 *)(S + ((size_t)b * H + h) * 4096);
 
-    // issue the state loads first; they do not depend on the vectors
+    // issue the state loads first; they do not depend on the vectors.  Load m
+    // covers rows 4m .. 4m+3, so loads 0..7 are rows 0..31 and 8..15 rows 32..63.
     float4 st[16];
 #pragma unroll
     for (int m = 0; m < 16; m++) st[m] = Sg[m * 64 + i];
@@ -112,33 +116,44 @@ __global__ __launch_bounds__(64) void k_wkv7_decode(float *__restrict__ S, const
     head_vectors(hv, i, ki, kkc[h * 64 + i], ai, ka[h * 64 + i], ri, wi, eps, kmod);
     if (kmod_out) kmod_out[vo + i] = kmod;
 
-#pragma unroll
-    for (int m = 0; m < 16; m++) {
-        const int e = (m * 64 + i) * 4, row = e >> 6, col = e & 63;
-        tile[row * 65 + col + 0] = st[m].x;
-        tile[row * 65 + col + 1] = st[m].y;
-        tile[row * 65 + col + 2] = st[m].z;
-        tile[row * 65 + col + 3] = st[m].w;
-    }
-    __syncthreads();
     float s[64];
 #pragma unroll
-    for (int j = 0; j < 64; j++) s[j] = tile[i * 65 + j];
-    const float y = row_update(s, hv, vi_own);
-    // GroupNorm and the bonus term need every lane's y; the row write-back
-    // goes through the tile again.
+    for (int half = 0; half < 2; half++) {
 #pragma unroll
-    for (int j = 0; j < 64; j++) tile[i * 65 + j] = s[j];
+        for (int m = 8 * half; m < 8 * half + 8; m++) {
+            const int e = (m * 64 + i) * 4, row = (e >> 6) - 32 * half, col = e & 63;
+            tile[row * 65 + col + 0] = st[m].x;
+            tile[row * 65 + col + 1] = st[m].y;
+            tile[row * 65 + col + 2] = st[m].z;
+            tile[row * 65 + col + 3] = st[m].w;
+        }
+        __syncthreads();
+        if ((i >> 5) == half) {
+#pragma unroll
+            for (int j = 0; j < 64; j++) s[j] = tile[(i & 31) * 65 + j];
+        }
+        __syncthreads();
+    }
+    const float y = row_update(s, hv, vi_own);
     const float yn = head_norm(y, gamma[h * 64 + i], beta[h * 64 + i], ri * kmod * rk[h * 64 + i], vi_own, gn_eps);
     if (y_out) y_out[vo + i] = y;
     if (yn_out) yn_out[vo + i] = yn;
     if (yg16) yg16[vo + i] = (_Float16)(yn * gmul[vo + i]);  // att.output operand (y_norm * g)
-    __syncthreads();
+    // row write-back through the tile again, 32 rows at a time
 #pragma unroll
-    for (int m = 0; m < 16; m++) {
-        const int e = (m * 64 + i) * 4, row = e >> 6, col = e & 63;
-        Sg[m * 64 + i] = make_float4(tile[row * 65 + col], tile[row * 65 + col + 1], tile[row * 65 + col + 2],
-                                     tile[row * 65 + col + 3]);
+    for (int half = 0; half < 2; half++) {
+        if ((i >> 5) == half) {
+#pragma unroll
+            for (int j = 0; j < 64; j++) tile[(i & 31) * 65 + j] = s[j];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int m = 8 * half; m < 8 * half + 8; m++) {
+            const int e = (m * 64 + i) * 4, row = (e >> 6) - 32 * half, col = e & 63;
+            Sg[m * 64 + i] = make_float4(tile[row * 65 + col], tile[row * 65 + col + 1], tile[row * 65 + col + 2],
+                                         tile[row * 65 + col + 3]);
+        }
+        __syncthreads();
     }
 }
 
