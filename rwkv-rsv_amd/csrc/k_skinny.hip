@@ -807,6 +807,30 @@ __global__ __launch_bounds__(256) void k_skinny_sk(SkinnyJobs jobs, int MB) {
     sk_store_tile<TB>(sk_epi_of(J), tile, rg * 128, MB);
 }
 
+// One output of a split job: the slices in slice order, then the epilogue.
+// The epilogue's read operands (y for add / v-lerp, aux, bias) are loaded
+// together with the slices, so the thread waits on one round of loads.
+template <int EPI, int TB>
+__device__ __forceinline__ void sk_reduce_one(const SkinnyJob &J, const float *base, int o, int n, int b) {
+    const SkEpi E = sk_epi_of(J);
+    constexpr bool need_y = EPI == GE_ADD || EPI == GE_VLERP;
+    constexpr bool need_b = EPI == GE_BIAS || EPI == GE_WDECAY || EPI == GE_SIGBIAS || EPI == GE_VLERP;
+    const size_t yo = (size_t)b * E.ldy + n;
+    const float yc = need_y ? ((const float *)E.y)[yo] : 0.0f;
+    const float ax = EPI == GE_VLERP ? E.aux[yo] : 0.0f;
+    const float bias = need_b ? E.bias[n] : 0.0f;
+    float v = 0.0f;
+    for (int q0 = 0; q0 < J.split; q0 += 8) {
+        float part[8];
+#pragma unroll
+        for (int q = 0; q < 8; q++) part[q] = q0 + q < J.split ? base[(size_t)(q0 + q) * 128 * TB + o] : 0.0f;
+#pragma unroll
+        for (int q = 0; q < 8; q++)
+            if (q0 + q < J.split) v = q0 + q == 0 ? part[q] : v + part[q];
+    }
+    sk_put(E, yo, sk_epi_val<EPI>(v, yc, ax, bias, E.scale));
+}
+
 template <int MT>
 __global__ __launch_bounds__(256) void k_skinny4_reduce(SkinnyJobs jobs, int MB, const float *__restrict__ ws) {
     constexpr int TB = MT * 32;
@@ -817,24 +841,13 @@ __global__ __launch_bounds__(256) void k_skinny4_reduce(SkinnyJobs jobs, int MB,
     constexpr int PB = 128 * TB / 256;  // blocks per row group: one output per thread
     const int rg = (bid - jobs.red_start[ji]) / PB, part = (bid - jobs.red_start[ji]) % PB;
     const float *base = ws + ((size_t)J.ws_slot + (size_t)rg * J.split) * 128 * TB;
-    {
-        const int o = part * 256 + threadIdx.x;
-        const int r = o & 127, b = o >> 7;
-        const int n = rg * 128 + r;
-        if (n >= J.N || b >= MB) return;
-        // partials are loaded 8 at a time (all in flight together) and added
-        // in slice order
-        float v = 0.0f;
-        for (int q0 = 0; q0 < J.split; q0 += 8) {
-            float part[8];
-#pragma unroll
-            for (int q = 0; q < 8; q++) part[q] = q0 + q < J.split ? base[(size_t)(q0 + q) * 128 * TB + o] : 0.0f;
-#pragma unroll
-            for (int q = 0; q < 8; q++)
-                if (q0 + q < J.split) v = q0 + q == 0 ? part[q] : v + part[q];
-        }
-        sk_store(sk_epi_of(J), v, n, b);
-    }
+    const int o = part * 256 + threadIdx.x;
+    const int r = o & 127, b = o >> 7;
+    const int n = rg * 128 + r;
+    if (n >= J.N || b >= MB) return;
+#define SK_RED_CALL(K) sk_reduce_one<K, TB>(J, base, o, n, b)
+    SK_EPI_DISPATCH(J, SK_RED_CALL)
+#undef SK_RED_CALL
 }
 
 // Tiled copy of a weight matrix [n, k] (int8 bytes or fp16) for k_skinny4;
