@@ -592,7 +592,7 @@ __device__ __forceinline__ void skinny5_body(const SkinnyJob &J, int local, int 
     // tiled scale/zero: [row tile][group][32 rows], one 128-byte line per group
     const uint32_t *szrow = I8 ? J.sz + (size_t)min(rt_glob, (J.N - 1) / 32) * (J.K / 128) * 32 + (lane & 31) : nullptr;
 
-    // 2a. first PD chunks of weights go out before the x slab
+    // 2a. weight chunk loads (the first PD go out right after the x slab's)
     sk_u32x4 wr[PD][WV];
     uint32_t sr[PD];
     // rows past N read row 0 of the tile and chunks past the slice re-read
@@ -607,23 +607,23 @@ __device__ __forceinline__ void skinny5_body(const SkinnyJob &J, int local, int 
         for (int v = 0; v < WV; v++) wr[p][v] = q[v];
         if (I8) sr[p] = szrow[(size_t)(c >> 2) * 32];
     };
+    // 1. x slab: TB rows x nloc*32 halves in 16-byte pieces.  Its loads go
+    // out first (the main loop waits on the slab), then the first PD weight
+    // chunks, then the slab is stored to LDS (kslice <= 16 chunks)
+    constexpr int NP = TB * 16 * 4 / 256;  // pieces per thread at the largest slice
+    const int pieces_row = nloc * 4;
+    const int total = TB * pieces_row;
+    sk_u32x4 xv[NP];
+#pragma unroll
+    for (int i = 0; i < NP; i++) {
+        const int e = tid + 256 * i;
+        const int b = e / pieces_row, pc = e - b * pieces_row;
+        xv[i] = (e < total && b < MB) ? *(const sk_u32x4 *)(J.x + (size_t)b * J.ldx + c_lo * 32 + pc * 8)
+                                      : (sk_u32x4){0u, 0u, 0u, 0u};
+    }
 #pragma unroll
     for (int p = 0; p < PD; p++) load_w(p, c_lo + p);
-
-    // 1. x slab: TB rows x nloc*32 halves in 16-byte pieces, every load of
-    // the thread issued before the first LDS store (kslice <= 16 chunks)
     {
-        constexpr int NP = TB * 16 * 4 / 256;  // pieces per thread at the largest slice
-        const int pieces_row = nloc * 4;
-        const int total = TB * pieces_row;
-        sk_u32x4 xv[NP];
-#pragma unroll
-        for (int i = 0; i < NP; i++) {
-            const int e = tid + 256 * i;
-            const int b = e / pieces_row, pc = e - b * pieces_row;
-            xv[i] = (e < total && b < MB) ? *(const sk_u32x4 *)(J.x + (size_t)b * J.ldx + c_lo * 32 + pc * 8)
-                                          : (sk_u32x4){0u, 0u, 0u, 0u};
-        }
 #pragma unroll
         for (int i = 0; i < NP; i++) {
             const int e = tid + 256 * i;
