@@ -613,11 +613,13 @@ __device__ __forceinline__ void skinny5_body(const SkinnyJob &J, int local, int 
     constexpr int NP = TB * 16 * 4 / 256;  // pieces per thread at the largest slice
     const int pieces_row = nloc * 4;
     const int total = TB * pieces_row;
+    // e / pieces_row as a multiply-high: exact for e * pieces_row < 2^32
+    const uint32_t rmag = (uint32_t)((0x100000000ull + pieces_row - 1) / pieces_row);
     sk_u32x4 xv[NP];
 #pragma unroll
     for (int i = 0; i < NP; i++) {
         const int e = tid + 256 * i;
-        const int b = e / pieces_row, pc = e - b * pieces_row;
+        const int b = (int)__umulhi((uint32_t)e, rmag), pc = e - b * pieces_row;
         xv[i] = (e < total && b < MB) ? *(const sk_u32x4 *)(J.x + (size_t)b * J.ldx + c_lo * 32 + pc * 8)
                                       : (sk_u32x4){0u, 0u, 0u, 0u};
     }
@@ -627,7 +629,7 @@ __device__ __forceinline__ void skinny5_body(const SkinnyJob &J, int local, int 
 #pragma unroll
         for (int i = 0; i < NP; i++) {
             const int e = tid + 256 * i;
-            const int b = e / pieces_row, pc = e - b * pieces_row;
+            const int b = (int)__umulhi((uint32_t)e, rmag), pc = e - b * pieces_row;
             if (e < total) *(sk_u32x4 *)&xs[(size_t)b * XS + pc * 8] = xv[i];
         }
     }
