@@ -1,6 +1,7 @@
 // Elementwise, normalisation, gather, argmax and token-record kernels of the
 // decode and prefill paths.  All per-session buffers are [batch, ...].
 #include "rsv_common.h"
+#include <algorithm>
 
 namespace rsv {
 
@@ -616,33 +617,40 @@ namespace rsv {
 // LayerNorm of each batch row + up to six token-shift mixes written as fp16
 // GEMM operands (batched decode on matrix cores).  With coef[j] == null the
 // output is the plain LN row.  state (optional) is read as the previous
-// token's LN row and overwritten with this row.  Every load is issued before
-// the statistics are reduced.  grid (batch), block 1024; c <= 4096.
+// token's LN row and overwritten with this row.  c <= 4096.
 template <int NOUT>
 __global__ __launch_bounds__(1024) void k_ln_mix_f16(const float *__restrict__ x, float *__restrict__ state,
                                                      const float *__restrict__ gamma,
                                                      const float *__restrict__ beta, Ptr6 coef, HOut6 out, int C,
                                                      float eps) {
+    // grid (batch, parts): block (b, y) writes elements [y*plen, (y+1)*plen)
+    // of row b (plen <= 1024) and takes the row statistics itself.  Every
+    // load of the block (the whole row of x, and gamma/beta/state/coef of its
+    // share) is issued before the statistics.
     __shared__ float red[16];
     const int b = blockIdx.x, tid = threadIdx.x;
+    const int plen = (C + gridDim.y - 1) / gridDim.y;
+    const int i = blockIdx.y * plen + tid;
+    const bool mine = tid < plen && i < C;
+    const size_t o = (size_t)b * C + i;
     constexpr int PER = 4;
-    float xv[PER], gv[PER], bv[PER], pv[PER], cv[NOUT][PER];
+    float xv[PER];
 #pragma unroll
     for (int m = 0; m < PER; m++) {
-        const int i = tid + 1024 * m;
-        const bool ok = i < C;
-        xv[m] = ok ? x[(size_t)b * C + i] : 0.0f;
-        gv[m] = ok ? gamma[i] : 0.0f;
-        bv[m] = ok ? beta[i] : 0.0f;
-        pv[m] = (ok && state) ? state[(size_t)b * C + i] : 0.0f;
-#pragma unroll
-        for (int j = 0; j < NOUT; j++) cv[j][m] = (ok && coef.p[j]) ? coef.p[j][i] : 0.0f;
+        const int e = tid + 1024 * m;
+        xv[m] = e < C ? x[(size_t)b * C + e] : 0.0f;
     }
+    const float xi = mine ? x[o] : 0.0f;
+    const float gi = mine ? gamma[i] : 0.0f, bi = mine ? beta[i] : 0.0f;
+    const float pi = (mine && state) ? state[o] : 0.0f;
+    float ci[NOUT];
+#pragma unroll
+    for (int j = 0; j < NOUT; j++) ci[j] = (mine && coef.p[j]) ? coef.p[j][i] : 0.0f;
     float s = 0.0f;
 #pragma unroll
     for (int m = 0; m < PER; m++) s += xv[m];
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+    for (int of = 32; of > 0; of >>= 1) s += __shfl_xor(s, of, 64);
     if ((tid & 63) == 0) red[tid >> 6] = s;
     __syncthreads();
     float tot = 0.0f;
@@ -656,7 +664,7 @@ __global__ __launch_bounds__(1024) void k_ln_mix_f16(const float *__restrict__ x
         q += (tid + 1024 * m < C) ? d * d : 0.0f;
     }
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) q += __shfl_xor(q, o, 64);
+    for (int of = 32; of > 0; of >>= 1) q += __shfl_xor(q, of, 64);
     __syncthreads();
     if ((tid & 63) == 0) red[tid >> 6] = q;
     __syncthreads();
@@ -664,17 +672,11 @@ __global__ __launch_bounds__(1024) void k_ln_mix_f16(const float *__restrict__ x
 #pragma unroll
     for (int w = 0; w < 16; w++) qt += red[w];
     const float inv = 1.0f / sqrtf(qt / (float)C + eps);
+    if (!mine) return;
+    const float ln = (xi - mean) * inv * gi + bi;
 #pragma unroll
-    for (int m = 0; m < PER; m++) {
-        const int i = tid + 1024 * m;
-        if (i >= C) continue;
-        const float ln = (xv[m] - mean) * inv * gv[m] + bv[m];
-        const size_t o = (size_t)b * C + i;
-#pragma unroll
-        for (int j = 0; j < NOUT; j++)
-            out.p[j][o] = (_Float16)(coef.p[j] ? ln + cv[j][m] * (pv[m] - ln) : ln);
-        if (state) state[o] = ln;
-    }
+    for (int j = 0; j < NOUT; j++) out.p[j][o] = (_Float16)(coef.p[j] ? ln + ci[j] * (pi - ln) : ln);
+    if (state) state[o] = ln;
 }
 
 int launch_ln_mix_f16(rsv_ctx *ctx, const float *x, float *state, const float *gamma, const float *beta,
@@ -684,9 +686,15 @@ int launch_ln_mix_f16(rsv_ctx *ctx, const float *x, float *state, const float *g
     Ptr6 cp{};
     HOut6 op{};
     for (int j = 0; j < nout; j++) { cp.p[j] = coef ? coef[j] : nullptr; op.p[j] = out[j]; }
+    // a row is split over up to 8 blocks (each takes the row statistics
+    // itself and writes its share) so that the launch covers the CUs
+    const int cus = ctx->sm_count > 0 ? ctx->sm_count : 256;
+    int parts = std::min(8, std::max(1, (cus + batch - 1) / batch));
+    while ((c + parts - 1) / parts > 1024) parts++;
+    const dim3 grid(batch, parts);
     switch (nout) {
-        case 1: hipLaunchKernelGGL(k_ln_mix_f16<1>, dim3(batch), dim3(1024), 0, ctx->stream, x, state, gamma, beta, cp, op, c, eps); break;
-        case 6: hipLaunchKernelGGL(k_ln_mix_f16<6>, dim3(batch), dim3(1024), 0, ctx->stream, x, state, gamma, beta, cp, op, c, eps); break;
+        case 1: hipLaunchKernelGGL(k_ln_mix_f16<1>, grid, dim3(1024), 0, ctx->stream, x, state, gamma, beta, cp, op, c, eps); break;
+        case 6: hipLaunchKernelGGL(k_ln_mix_f16<6>, grid, dim3(1024), 0, ctx->stream, x, state, gamma, beta, cp, op, c, eps); break;
         default: return RSV_FAIL("ln_mix_f16: nout must be 1 or 6 (got %d)", nout);
     }
     RSV_HIP(hipGetLastError());
