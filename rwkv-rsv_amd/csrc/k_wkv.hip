@@ -112,6 +112,10 @@ __global__ __launch_bounds__(64) void k_wkv7_decode(float *__restrict__ S, const
     for (int m = 0; m < 16; m++) st[m] = Sg[m * 64 + i];
 
     const float ki = k[vo + i], ai = a[vo + i], ri = r[vo + i], vi_own = v[vo + i], wi = w[vo + i];
+    // the GroupNorm operands too: loads after the barriers below would be a
+    // second round trip at the end of the block
+    const float gam = gamma[h * 64 + i], bet = beta[h * 64 + i], rki = rk[h * 64 + i];
+    const float gmi = yg16 ? gmul[vo + i] : 0.0f;
     float kmod;
     head_vectors(hv, i, ki, kkc[h * 64 + i], ai, ka[h * 64 + i], ri, wi, eps, kmod);
     if (kmod_out) kmod_out[vo + i] = kmod;
@@ -135,10 +139,10 @@ __global__ __launch_bounds__(64) void k_wkv7_decode(float *__restrict__ S, const
         __syncthreads();
     }
     const float y = row_update(s, hv, vi_own);
-    const float yn = head_norm(y, gamma[h * 64 + i], beta[h * 64 + i], ri * kmod * rk[h * 64 + i], vi_own, gn_eps);
+    const float yn = head_norm(y, gam, bet, ri * kmod * rki, vi_own, gn_eps);
     if (y_out) y_out[vo + i] = y;
     if (yn_out) yn_out[vo + i] = yn;
-    if (yg16) yg16[vo + i] = (_Float16)(yn * gmul[vo + i]);  // att.output operand (y_norm * g)
+    if (yg16) yg16[vo + i] = (_Float16)(yn * gmi);  // att.output operand (y_norm * g)
     // row write-back through the tile again, 32 rows at a time
 #pragma unroll
     for (int half = 0; half < 2; half++) {
