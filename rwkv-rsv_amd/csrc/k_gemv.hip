@@ -49,6 +49,57 @@ __device__ __forceinline__ void apply_epi(const GemvJob &J, int row, int b, floa
     }
 }
 
+// Sum over each aligned group of G lanes (32 or 64) on DPP row operations;
+// the result is valid in the last lane of each group (lane 31 / 63 of the
+// wave for G = 32, lane 63 for G = 64).
+template <int CTRL, int RM = 0xF>
+__device__ __forceinline__ float gdpp(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, RM, 0xF, false));
+}
+template <int G>
+__device__ __forceinline__ float group_sum_last(float v) {
+    v += gdpp<0xB1>(v);        // quad_perm 1,0,3,2
+    v += gdpp<0x4E>(v);        // quad_perm 2,3,0,1
+    v += gdpp<0x141>(v);       // row_half_mirror
+    v += gdpp<0x140>(v);       // row_mirror: 16-lane row sums
+    v += gdpp<0x142, 0xA>(v);  // row_bcast:15 into rows 1 and 3: 32-lane sums in rows 1, 3
+    if (G == 64) v += gdpp<0x143, 0xC>(v);  // row_bcast:31 into rows 2 and 3: total in row 3
+    return v;
+}
+
+// Read operands of a row's epilogue, loaded at kernel entry by the lane that
+// stores the row (a load after the block's barriers would be one more round
+// trip at the end of the launch).
+struct EpiPre {
+    float y, p0, p1;
+};
+__device__ __forceinline__ EpiPre epi_prefetch(const GemvJob &J, int row, bool live) {
+    EpiPre e{0.0f, 0.0f, 0.0f};
+    if (!live) return e;
+    if (J.epi == EPI_ADD || J.epi == EPI_VLERP) e.y = J.y[row];
+    if (J.epi == EPI_WDECAY || J.epi == EPI_SIGBIAS || J.epi == EPI_VLERP) e.p0 = J.p0[row];
+    if (J.epi == EPI_VLERP) e.p1 = J.p1[row];
+    return e;
+}
+// apply_epi for batch row 0 with the operands of epi_prefetch.
+__device__ __forceinline__ void apply_epi_pre(const GemvJob &J, int row, float v, const EpiPre &e) {
+    float *yp = J.y + row;
+    switch (J.epi) {
+        case EPI_STORE: *yp = v; break;
+        case EPI_RELU2: { const float t = v > 0.0f ? v : 0.0f; *yp = t * t; } break;
+        case EPI_ADD: *yp = e.y + v; break;
+        case EPI_TANH: *yp = tanhf(v); break;
+        case EPI_WDECAY: *yp = expf(sigmoid_f(v + e.p0) * J.scale[0]); break;
+        case EPI_SIGBIAS: *yp = sigmoid_f(v + e.p0); break;
+        case EPI_VLERP: *yp = e.y + sigmoid_f(v + e.p0) * (e.p1 - e.y); break;
+        case EPI_STORE2:
+            *yp = v;
+            ((float *)J.p1)[row] = v;
+            break;
+        default: break;
+    }
+}
+
 __device__ __forceinline__ float block_sum_256(float v, float *red) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
@@ -954,10 +1005,9 @@ __global__ __launch_bounds__(256) void k_gemv_os(GemvJobs jobs) {
 // vectors per CU, and one LN per 10-20 rows instead of per 4-8.
 template <int NT>
 __device__ __forceinline__ float block_sum_nt(float v, float *red) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    v = group_sum_last<64>(v);
     __syncthreads();
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    if ((threadIdx.x & 63) == 63) red[threadIdx.x >> 6] = v;
     __syncthreads();
     float t = red[0];
 #pragma unroll
@@ -1006,6 +1056,7 @@ __device__ __forceinline__ void gemv_os2_body(const GemvJob &J, int rb, float4 *
         wv[j] = __builtin_nontemporal_load(W + (size_t)row * NC + c);
         if (FMT == FMT_I8) szv[j] = J.sz[(size_t)row * KG + (c >> 3)];
     }
+    const EpiPre ep = epi_prefetch(J, row0, li == LPR - 1 && row0 < M);
     // 3. prologue
 #pragma unroll
     for (int i = 0; i < Q; i++)
@@ -1068,8 +1119,8 @@ __device__ __forceinline__ void gemv_os2_body(const GemvJob &J, int rb, float4 *
         if (q < K4) xs[((4 * q) % CW >> 2) * NC + (4 * q) / CW] = xa[i];
         if (FMT == FMT_I8) {
             float cs = (xa[i].x + xa[i].y) + (xa[i].z + xa[i].w);
-            cs += __shfl_xor(cs, 1, 64);
-            cs += __shfl_xor(cs, 2, 64);
+            cs += gdpp<0xB1>(cs);  // quad_perm 1,0,3,2
+            cs += gdpp<0x4E>(cs);  // quad_perm 2,3,0,1: the chunk's sum in its 4 lanes
             if (q < K4 && (q & 3) == 0) dxs[q >> 2] = cs;
         }
     }
@@ -1112,9 +1163,8 @@ __device__ __forceinline__ void gemv_os2_body(const GemvJob &J, int rb, float4 *
             acc += live ? d : 0.0f;
         }
     }
-#pragma unroll
-    for (int o = LPR / 2; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
-    if (li == 0 && row0 < M) apply_epi(J, row0, 0, acc);
+    acc = group_sum_last<LPR>(acc);
+    if (li == LPR - 1 && row0 < M) apply_epi_pre(J, row0, acc, ep);
 }
 
 template <int CPL, int Q, int NT, int PV>
