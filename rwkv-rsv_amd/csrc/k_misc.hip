@@ -1,6 +1,7 @@
 // Elementwise, normalisation, gather, argmax and token-record kernels of the
 // decode and prefill paths.  All per-session buffers are [batch, ...].
 #include "rsv_common.h"
+#include "k_dpp.h"
 #include <algorithm>
 
 namespace rsv {
@@ -9,11 +10,10 @@ __device__ __forceinline__ float sigmoid_m(float v) { return 1.0f / (1.0f + expf
 
 // Block-wide sum for 256-thread blocks (4 waves).
 __device__ __forceinline__ float block_sum256(float v, float *red) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    v = wave_sum_last(v);
     const int w = threadIdx.x >> 6;
     __syncthreads();
-    if ((threadIdx.x & 63) == 0) red[w] = v;
+    if ((threadIdx.x & 63) == 63) red[w] = v;
     __syncthreads();
     return red[0] + red[1] + red[2] + red[3];
 }
@@ -48,9 +48,8 @@ __global__ __launch_bounds__(1024) void k_norm_lerp(const float *__restrict__ x,
     float s = 0.0f;
 #pragma unroll
     for (int m = 0; m < PER; m++) s += xv[m];
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
-    if ((tid & 63) == 0) red[tid >> 6] = s;
+    s = wave_sum_last(s);
+    if ((tid & 63) == 63) red[tid >> 6] = s;
     __syncthreads();
     float tot = 0.0f;
 #pragma unroll
@@ -62,10 +61,9 @@ __global__ __launch_bounds__(1024) void k_norm_lerp(const float *__restrict__ x,
         const float d = xv[m] - mean;
         q += (tid + 1024 * m < C) ? d * d : 0.0f;
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) q += __shfl_xor(q, o, 64);
+    q = wave_sum_last(q);
     __syncthreads();
-    if ((tid & 63) == 0) red[tid >> 6] = q;
+    if ((tid & 63) == 63) red[tid >> 6] = q;
     __syncthreads();
     float qt = 0.0f;
 #pragma unroll
@@ -193,13 +191,8 @@ __global__ __launch_bounds__(1024) void k_argmax(const float *__restrict__ logit
             if (v > bv) { bv = v; bi = i; }
         }
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const float ov = __shfl_xor(bv, o, 64);
-        const int oi = __shfl_xor(bi, o, 64);
-        if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-    }
-    if ((tid & 63) == 0) { sv[tid >> 6] = bv; si[tid >> 6] = bi; }
+    wave_argmax_last(bv, bi);
+    if ((tid & 63) == 63) { sv[tid >> 6] = bv; si[tid >> 6] = bi; }
     __syncthreads();
     if (tid == 0) {
         float v = sv[0];
@@ -365,8 +358,7 @@ __global__ __launch_bounds__(64) void k_fuse_ka(const float *__restrict__ k, con
     const float ki = k[o], ai = a[o];
     const float kkv = ki * kk[h * 64 + i];
     float ss = kkv * kkv;
-#pragma unroll
-    for (int s = 32; s > 0; s >>= 1) ss += __shfl_xor(ss, s, 64);
+    ss = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wave_sum_last(ss)), 63));
     float nrm = sqrtf(ss);
     nrm = nrm < 1e-12f ? 1e-12f : nrm;
     const float kh = kkv * (1.0f / nrm);
@@ -390,8 +382,7 @@ __global__ __launch_bounds__(64) void k_sum_rk_rk(const float *__restrict__ r, c
     const int h = blockIdx.x, b = blockIdx.y, i = threadIdx.x;
     const size_t o = (size_t)b * H * 64 + h * 64 + i;
     float s = r[o] * km[o] * rk[h * 64 + i];
-#pragma unroll
-    for (int q = 32; q > 0; q >>= 1) s += __shfl_xor(s, q, 64);
+    s = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wave_sum_last(s)), 63));
     y[o] += s * v[o];
 }
 
@@ -649,9 +640,8 @@ __global__ __launch_bounds__(1024) void k_ln_mix_f16(const float *__restrict__ x
     float s = 0.0f;
 #pragma unroll
     for (int m = 0; m < PER; m++) s += xv[m];
-#pragma unroll
-    for (int of = 32; of > 0; of >>= 1) s += __shfl_xor(s, of, 64);
-    if ((tid & 63) == 0) red[tid >> 6] = s;
+    s = wave_sum_last(s);
+    if ((tid & 63) == 63) red[tid >> 6] = s;
     __syncthreads();
     float tot = 0.0f;
 #pragma unroll
@@ -663,10 +653,9 @@ __global__ __launch_bounds__(1024) void k_ln_mix_f16(const float *__restrict__ x
         const float d = xv[m] - mean;
         q += (tid + 1024 * m < C) ? d * d : 0.0f;
     }
-#pragma unroll
-    for (int of = 32; of > 0; of >>= 1) q += __shfl_xor(q, of, 64);
+    q = wave_sum_last(q);
     __syncthreads();
-    if ((tid & 63) == 0) red[tid >> 6] = q;
+    if ((tid & 63) == 63) red[tid >> 6] = q;
     __syncthreads();
     float qt = 0.0f;
 #pragma unroll

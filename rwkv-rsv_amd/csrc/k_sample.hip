@@ -16,6 +16,7 @@
 // in LDS by (value desc, index asc) -- the same sequence the iterative
 // extraction produces.
 #include "rsv_common.h"
+#include "k_dpp.h"
 
 namespace rsv {
 
@@ -52,10 +53,9 @@ struct SampShared {
 };
 
 __device__ float block_max(float v, SampShared &sh) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    v = wave_max_last(v);
     __syncthreads();
-    if ((threadIdx.x & 63) == 0) sh.red[threadIdx.x >> 6] = v;
+    if ((threadIdx.x & 63) == 63) sh.red[threadIdx.x >> 6] = v;
     __syncthreads();
     float m = sh.red[0];
     for (int w = 1; w < 16; w++) m = fmaxf(m, sh.red[w]);
@@ -63,10 +63,9 @@ __device__ float block_max(float v, SampShared &sh) {
 }
 
 __device__ float block_sum(float v, SampShared &sh) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    v = wave_sum_last(v);
     __syncthreads();
-    if ((threadIdx.x & 63) == 0) sh.red[threadIdx.x >> 6] = v;
+    if ((threadIdx.x & 63) == 63) sh.red[threadIdx.x >> 6] = v;
     __syncthreads();
     float s = 0.0f;
     for (int w = 0; w < 16; w++) s += sh.red[w];
