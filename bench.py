@@ -29,7 +29,7 @@ HBM_PEAK_GBS = 8000.0
 # HBM bytes per launch of the dominant kernel, from the two rocprofv3 --pmc
 # passes (FETCH_SIZE, WRITE_SIZE) of `bench.py --kernel-only`, scaled by the
 # same counters of a plain 64 MiB copy; profiles/ffn_key_gemv_b1.md
-FFN_KEY_TRAFFIC = 27680637
+FFN_KEY_TRAFFIC = 27671041
 NONE = 0xFFFFFFFF
 
 
