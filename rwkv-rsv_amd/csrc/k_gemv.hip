@@ -49,9 +49,9 @@ __device__ __forceinline__ void apply_epi(const GemvJob &J, int row, int b, floa
     }
 }
 
-// Sum over each aligned group of G lanes (32 or 64) on DPP row operations;
-// the result is valid in the last lane of each group (lane 31 / 63 of the
-// wave for G = 32, lane 63 for G = 64).
+// Sum over each aligned group of G lanes (16, 32 or 64) on DPP row
+// operations; the result is valid in the last lane of each group (every lane
+// for G = 16, lanes 31 and 63 for G = 32, lane 63 for G = 64).
 template <int CTRL, int RM = 0xF>
 __device__ __forceinline__ float gdpp(float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, RM, 0xF, false));
@@ -62,7 +62,7 @@ __device__ __forceinline__ float group_sum_last(float v) {
     v += gdpp<0x4E>(v);        // quad_perm 2,3,0,1
     v += gdpp<0x141>(v);       // row_half_mirror
     v += gdpp<0x140>(v);       // row_mirror: 16-lane row sums
-    v += gdpp<0x142, 0xA>(v);  // row_bcast:15 into rows 1 and 3: 32-lane sums in rows 1, 3
+    if (G >= 32) v += gdpp<0x142, 0xA>(v);  // row_bcast:15 into rows 1 and 3: 32-lane sums in rows 1, 3
     if (G == 64) v += gdpp<0x143, 0xC>(v);  // row_bcast:31 into rows 2 and 3: total in row 3
     return v;
 }
@@ -101,10 +101,9 @@ __device__ __forceinline__ void apply_epi_pre(const GemvJob &J, int row, float v
 }
 
 __device__ __forceinline__ float block_sum_256(float v, float *red) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    v = group_sum_last<64>(v);
     __syncthreads();
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    if ((threadIdx.x & 63) == 63) red[threadIdx.x >> 6] = v;
     __syncthreads();
     return red[0] + red[1] + red[2] + red[3];
 }
@@ -386,13 +385,10 @@ __device__ __forceinline__ void gemv_body(const GemvJob &J, int rb, int batch, f
     for (int r = 0; r < RU; r++)
 #pragma unroll
         for (int b = 0; b < BT; b++) {
-            float v = acc[r][b];
-#pragma unroll
-            for (int o = LPR / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-            acc[r][b] = v;
+            acc[r][b] = group_sum_last<LPR>(acc[r][b]);
         }
 
-    if (li == 0) {
+    if (li == LPR - 1) {
 #pragma unroll
         for (int r = 0; r < RU; r++) {
             const int row = rbase + r;
@@ -550,16 +546,13 @@ __device__ __forceinline__ void reg_dot(const GemvJob &J, int tile, int it, int 
     }
 #pragma unroll
     for (int r = 0; r < RU; r++) {
-        float v = acc[r];
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-        acc[r] = v;
+        acc[r] = group_sum_last<64>(acc[r]);
     }
     if (KS > 1) {
         // slice partials meet in LDS (double-buffered by tile parity); slice
         // 0 adds them in slice order
         float *pp = part + (it & 1) * 4 * RU;
-        if (li == 0)
+        if (li == 63)
 #pragma unroll
             for (int r = 0; r < RU; r++) pp[wave * RU + r] = acc[r];
         __syncthreads();
@@ -571,7 +564,7 @@ __device__ __forceinline__ void reg_dot(const GemvJob &J, int tile, int it, int 
             acc[r] = v;
         }
     }
-    if (li != 0) return;
+    if (li != 63) return;
 #pragma unroll
     for (int r = 0; r < RU; r++) {
         const int row = rbase + r;
@@ -971,9 +964,8 @@ __device__ __forceinline__ void gemv_os_body(const GemvJob &J, int rb, float4 *x
             acc += live ? d : 0.0f;
         }
     }
-#pragma unroll
-    for (int o = LPR / 2; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
-    if (li == 0 && row0 < M) apply_epi(J, row0, 0, acc);
+    acc = group_sum_last<LPR>(acc);
+    if (li == LPR - 1 && row0 < M) apply_epi(J, row0, 0, acc);
 }
 
 template <int CPL, int Q>
