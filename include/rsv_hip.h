@@ -354,6 +354,16 @@ typedef struct rsv_mm_job {
  * job takes both tiled tensors in its rsv_int8 handle. */
 int rsv_tile_weights(rsv_ctx *ctx, uint32_t src, uint64_t n, uint64_t k, int esz, uint32_t *out);
 int rsv_gemm_skinny(rsv_ctx *ctx, const rsv_mm_job *jobs, uint64_t njobs, uint64_t batch);
+
+/* ---- several prefill GEMMs in one launch (no reference counterpart: the
+ * reference issues one cuBLAS GEMM per weight, backend.rs:691-725).  Job i
+ * computes y_i[t, n] (epilogue)= sum_k x_i[t, k] W_i[n, k] for t < m, as
+ * rsv_gemm_ex does, with the fields of rsv_mm_job: x F16 [m, k]; W
+ * row-major F16 (w16) or int8 (w8), tiled = 0; y F32 or F16 [m, n]; y2
+ * unused (0xFFFFFFFF); epilogue, bias, aux, scale as rsv_gemm_ex.  Jobs may
+ * mix weight formats; each job's results equal its own rsv_gemm_ex launch
+ * bit for bit.  At most 8 jobs. */
+int rsv_gemm_multi(rsv_ctx *ctx, const rsv_mm_job *jobs, uint64_t njobs, uint64_t m);
 /* LN rows of x [batch, c] + nout (1 or 6) token-shift mixes as F16 outputs;
  * coef ids may be 0xFFFFFFFF (plain LN); state (optional) is the token-shift
  * row, read then overwritten with the LN row. */

@@ -1482,6 +1482,46 @@ extern "C" int rsv_gemm_skinny(rsv_ctx *ctx, const rsv_mm_job *jobs, uint64_t nj
     return launch_skinny(ctx, S, (int)batch);
 }
 
+extern "C" int rsv_gemm_multi(rsv_ctx *ctx, const rsv_mm_job *jobs, uint64_t njobs, uint64_t m) {
+    CHECK_CTX();
+    if (!jobs || njobs == 0 || njobs > (uint64_t)kMaxJobs) return RSV_FAIL("gemm_multi: 1..%d jobs", kMaxJobs);
+    if (m == 0 || m > 0x7FFFFFFF) return RSV_FAIL("gemm_multi: bad m %llu", (unsigned long long)m);
+    GemmJobs G{};
+    G.n = (int)njobs;
+    for (uint64_t i = 0; i < njobs; i++) {
+        const rsv_mm_job &q = jobs[i];
+        GemmArgs &g = G.j[i];
+        if (q.tiled) return RSV_FAIL("gemm_multi job %llu: takes row-major weights (tiled = 0)", (unsigned long long)i);
+        if (q.y2 != 0xFFFFFFFFu) return RSV_FAIL("gemm_multi job %llu: y2 is not supported", (unsigned long long)i);
+        if (q.epilogue < GE_STORE || q.epilogue > GE_SIGMOID) return RSV_FAIL("gemm_multi: bad epilogue %d", q.epilogue);
+        void *p = nullptr;
+        if (opnd(ctx, q.x, RSV_F16, m * q.k, &p, "gemm_multi x")) return -1;
+        g.a = (const _Float16 *)p;
+        if (q.w8) {
+            const uint32_t *idx, *sz;
+            if (int8_operands(ctx, q.w8, q.n, q.k, &idx, &sz, "gemm_multi w8")) return -1;
+            g.b = idx;
+            g.sz = sz;
+            g.b_i8 = 1;
+        } else {
+            if (opnd(ctx, q.w16, RSV_F16, q.n * q.k, &p, "gemm_multi w16")) return -1;
+            g.b = p;
+        }
+        Tensor *tc = get_tensor(ctx, q.y);
+        if (!tc || tc->dtype == RSV_U32 || tc->len < m * q.n) return RSV_FAIL("gemm_multi: bad y tensor %u", q.y);
+        g.c = tc->ptr;
+        g.c_f16 = tc->dtype == RSV_F16;
+        if (q.epilogue == GE_ADD) g.aux = (const float *)tc->ptr;
+        if (q.bias != 0xFFFFFFFFu) { if (opnd(ctx, q.bias, RSV_F32, q.n, &p, "gemm_multi bias")) return -1; g.bias = (const float *)p; }
+        if (q.aux != 0xFFFFFFFFu) { if (opnd(ctx, q.aux, RSV_F32, m * q.n, &p, "gemm_multi aux")) return -1; g.aux = (const float *)p; }
+        if (q.scale != 0xFFFFFFFFu) { if (opnd(ctx, q.scale, RSV_F32, 1, &p, "gemm_multi scale")) return -1; g.scale = (const float *)p; }
+        g.m = (int)m; g.n = (int)q.n; g.k = (int)q.k;
+        g.lda = (int)q.k; g.ldc = (int)q.n;
+        g.epi = q.epilogue;
+    }
+    return launch_gemm_multi(ctx, G);
+}
+
 extern "C" int rsv_ln_mix_f16(rsv_ctx *ctx, uint32_t x, uint32_t state, uint32_t gamma, uint32_t beta,
                               const uint32_t *coef, const uint32_t *out_f16, uint64_t nout, uint64_t c, float eps,
                               uint64_t batch) {

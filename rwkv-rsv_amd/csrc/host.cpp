@@ -830,6 +830,21 @@ rsv_mm_job mm_job(const Linear &L, uint32_t x, uint32_t y, int epi) {
     return j;
 }
 
+// A prefill GEMM job on the row-major weights (rsv_gemm_multi).
+rsv_mm_job gemm_job(const Linear &L, uint32_t x, uint32_t y, int epi) {
+    rsv_mm_job j;
+    memset(&j, 0xFF, sizeof j);
+    j.tiled = 0;
+    j.w16 = L.i8 ? NONE : L.w16;
+    j.w8 = L.i8 ? &L.h : nullptr;
+    j.n = L.m;
+    j.k = L.k;
+    j.x = x;
+    j.y = y;
+    j.epilogue = epi;
+    return j;
+}
+
 int tile_linear(rsv_bundle *b, Linear &L) {
     if (L.tiled) return 0;
     if (L.i8) {
@@ -1139,13 +1154,13 @@ int prefill(rsv_bundle *b, GpuState &s, const std::vector<Seg> &segs, float *log
             };
             CK(rsv_gemm_skinny(c, j1, 7, T));
         } else {
-            HK(gemm_lin(b, L.rw, xr, q.r, T, 0));
-            HK(gemm_lin(b, L.kw, xk, q.k, T, 0));
-            HK(gemm_lin(b, L.vw, xv, q.v, T, 0));
-            CK(rsv_gemm_ex(c, xv, L.v1, nullptr, q.vmid, T, I.v_mid, C, 0, NONE, NONE, NONE));
-            CK(rsv_gemm_ex(c, xw, L.w1, nullptr, q.wmid, T, I.w_mid, C, 4, NONE, NONE, NONE));
-            CK(rsv_gemm_ex(c, xa, L.a1, nullptr, q.amid, T, I.a_mid, C, 0, NONE, NONE, NONE));
-            CK(rsv_gemm_ex(c, xg, L.g1, nullptr, q.gmid, T, I.g_mid, C, 8, NONE, NONE, NONE));
+            // r/k/v and the four LoRA-down products in one launch
+            rsv_mm_job j1[7] = {
+                gemm_job(L.rw, xr, q.r, 0), gemm_job(L.kw, xk, q.k, 0), gemm_job(L.vw, xv, q.v, 0),
+                gemm_job(L.lv1, xv, q.vmid, 0), gemm_job(L.lw1, xw, q.wmid, 4),
+                gemm_job(L.la1, xa, q.amid, 0), gemm_job(L.lg1, xg, q.gmid, 8),
+            };
+            CK(rsv_gemm_multi(c, j1, 7, T));
         }
         if (i == 0) {
             CK(rsv_copy_device(c, q.v, q.vf));
@@ -1161,10 +1176,15 @@ int prefill(rsv_bundle *b, GpuState &s, const std::vector<Seg> &segs, float *log
             j2[2].aux = q.vf;
             CK(rsv_gemm_skinny(c, j2, 4, T));
         } else {
-            CK(rsv_gemm_ex(c, q.wmid, L.w2, nullptr, q.w, T, C, I.w_mid, 5, L.w0, NONE, b->scale_w));
-            CK(rsv_gemm_ex(c, q.amid, L.a2, nullptr, q.a, T, C, I.a_mid, 6, L.a0, NONE, NONE));
-            CK(rsv_gemm_ex(c, q.vmid, L.v2, nullptr, q.v, T, C, I.v_mid, 7, L.v0, q.vf, NONE));
-            CK(rsv_gemm_ex(c, q.gmid, L.g2, nullptr, q.g, T, C, I.g_mid, 0, NONE, NONE, NONE));
+            // the LoRA-up chain in one launch
+            rsv_mm_job j2[4] = {gemm_job(L.lw2, q.wmid, q.w, 5), gemm_job(L.la2, q.amid, q.a, 6),
+                                gemm_job(L.lv2, q.vmid, q.v, 7), gemm_job(L.lg2, q.gmid, q.g, 0)};
+            j2[0].bias = L.w0;
+            j2[0].scale = b->scale_w;
+            j2[1].bias = L.a0;
+            j2[2].bias = L.v0;
+            j2[2].aux = q.vf;
+            CK(rsv_gemm_multi(c, j2, 4, T));
         }
         CK(rsv_wkv7_seq_ragged(c, s.rnn[i], q.r, q.w, q.k, q.v, q.a, L.k_k, L.k_a, L.r_k, L.lnx_w, L.lnx_b, q.yn,
                                q.seg_start, q.seg_len, q.seg_slot, S, H, N, GN_EPS));

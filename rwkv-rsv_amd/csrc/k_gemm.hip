@@ -216,12 +216,10 @@ __device__ __forceinline__ void gemm2_epilogue(const GemmArgs &g, const float16_
 // BM2 rows (128 or 256) x 128 columns per block of 4 waves in a 2x2 layout:
 // each wave owns (BM2/2) x 64 as (BM2/64) x 2 MFMA 32x32 tiles.
 template <bool B_I8, int BM2>
-__global__ __launch_bounds__(256) void k_gemm2(GemmArgs g) {
+__device__ __forceinline__ void gemm2_body(const GemmArgs &g, int m0, int n0, _Float16 (*As)[BM2 * LDK],
+                                           _Float16 (*Bs)[BN * LDK]) {
     constexpr int MI = BM2 / 64;
     constexpr int PA = BM2 * BK / 8 / 256;  // 16-byte A pieces per thread
-    __shared__ __attribute__((aligned(16))) _Float16 As[2][BM2 * LDK];
-    __shared__ __attribute__((aligned(16))) _Float16 Bs[2][BN * LDK];
-    const int m0 = blockIdx.y * BM2, n0 = blockIdx.x * BN;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int wm = (wave >> 1) * (BM2 / 2), wn = (wave & 1) * 64;
     const int lr = tid >> 1, lc = (tid & 1) * 16;  // B loader: row, first k of 16
@@ -332,6 +330,60 @@ __global__ __launch_bounds__(256) void k_gemm2(GemmArgs g) {
         default: GEMM2_EPI(GE_STORE); break;
     }
 #undef GEMM2_EPI
+}
+
+template <bool B_I8, int BM2>
+__global__ __launch_bounds__(256) void k_gemm2(GemmArgs g) {
+    __shared__ __attribute__((aligned(16))) _Float16 As[2][BM2 * LDK];
+    __shared__ __attribute__((aligned(16))) _Float16 Bs[2][BN * LDK];
+    gemm2_body<B_I8, BM2>(g, blockIdx.y * BM2, blockIdx.x * BN, As, Bs);
+}
+
+// A job list in one launch: the block finds its job and tile (row-major over
+// the job's n-tiles) and runs that job's body, int8 or fp16.
+template <int BM2>
+__global__ __launch_bounds__(256) void k_gemm2_multi(GemmJobs jobs) {
+    __shared__ __attribute__((aligned(16))) _Float16 As[2][BM2 * LDK];
+    __shared__ __attribute__((aligned(16))) _Float16 Bs[2][BN * LDK];
+    const int bid = blockIdx.x;
+    int ji = 0;
+    while (ji + 1 < jobs.n && bid >= jobs.blk_start[ji + 1]) ji++;
+    const GemmArgs &g = jobs.j[ji];
+    const int local = bid - jobs.blk_start[ji], nt = (g.n + BN - 1) / BN;
+    const int m0 = (local / nt) * BM2, n0 = (local % nt) * BN;
+    if (g.b_i8)
+        gemm2_body<true, BM2>(g, m0, n0, As, Bs);
+    else
+        gemm2_body<false, BM2>(g, m0, n0, As, Bs);
+}
+
+static int gemm_check(const GemmArgs &g) {
+    if (g.m <= 0 || g.n <= 0 || g.k <= 0) return RSV_FAIL("gemm: bad shape m=%d n=%d k=%d", g.m, g.n, g.k);
+    if (g.k % BK != 0) return RSV_FAIL("gemm: k=%d must be a multiple of %d", g.k, BK);
+    if (g.b_i8 && (g.k % 128 != 0 || !g.sz)) return RSV_FAIL("gemm: int8 weights need k %% 128 == 0 and scales");
+    if (g.lda < g.k || g.lda % 8 != 0) return RSV_FAIL("gemm: lda=%d must be >= k and a multiple of 8", g.lda);
+    if (g.ldc < g.n) return RSV_FAIL("gemm: ldc=%d < n=%d", g.ldc, g.n);
+    if ((g.epi == GE_ADD || g.epi == GE_VLERP) && !g.aux) return RSV_FAIL("gemm: epilogue needs aux");
+    if ((g.epi == GE_BIAS || g.epi == GE_WDECAY || g.epi == GE_SIGBIAS || g.epi == GE_VLERP) && !g.bias)
+        return RSV_FAIL("gemm: epilogue needs bias");
+    if (g.epi == GE_WDECAY && !g.scale) return RSV_FAIL("gemm: decay epilogue needs scale");
+    if (g.c_f16 && (g.epi == GE_ADD || g.epi == GE_VLERP)) return RSV_FAIL("gemm: in-place epilogues need fp32 C");
+    return 0;
+}
+
+int launch_gemm_multi(rsv_ctx *ctx, GemmJobs &jobs) {
+    if (jobs.n <= 0 || jobs.n > kMaxJobs) return RSV_FAIL("gemm_multi: 1..%d jobs", kMaxJobs);
+    int total = 0;
+    for (int i = 0; i < jobs.n; i++) {
+        const GemmArgs &g = jobs.j[i];
+        if (gemm_check(g)) return -1;
+        jobs.blk_start[i] = total;
+        total += ((g.n + BN - 1) / BN) * ((g.m + BM - 1) / BM);
+    }
+    jobs.blk_start[jobs.n] = total;
+    hipLaunchKernelGGL((k_gemm2_multi<128>), dim3(total), dim3(256), 0, ctx->stream, jobs);
+    RSV_HIP(hipGetLastError());
+    return 0;
 }
 
 int launch_gemm(rsv_ctx *ctx, const GemmArgs &g) {

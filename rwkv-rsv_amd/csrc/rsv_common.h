@@ -201,6 +201,14 @@ struct GemmArgs {
     int epi, b_i8, c_f16;
 };
 int launch_gemm(rsv_ctx *ctx, const GemmArgs &g);
+// Several prefill GEMMs with the same m in one launch (k_gemm2 tiles; jobs
+// may mix int8 and fp16 weights).
+struct GemmJobs {
+    GemmArgs j[kMaxJobs];
+    int n;
+    int blk_start[kMaxJobs + 1];
+};
+int launch_gemm_multi(rsv_ctx *ctx, GemmJobs &jobs);
 // Batched-decode GEMM on matrix cores (see k_skinny.hip); epilogue codes are GemmEpi.
 struct SkinnyJob {
     const void *w;

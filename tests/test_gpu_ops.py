@@ -462,6 +462,40 @@ def test_gemm_f16_and_int8(be, m, n, k):
         assert rel_err(be.get(C8, m * n).reshape(m, n), A64 @ Wq.T) < 1e-5
 
 
+@pytest.mark.parametrize("m", [200, 1030])
+def test_gemm_multi_equals_single_launches(be, m):
+    """rsv_gemm_multi runs a job list (int8 and fp16 weights, different
+    inputs, outputs and epilogues) in one launch; each job's output equals
+    its own rsv_gemm_ex launch bit for bit."""
+    rsv = _rsv()
+    rng = np.random.default_rng(m)
+    k1, k2 = 512, 96
+    A1 = be.tensor(rng.standard_normal((m, k1)).astype(np.float32), dtype=rsv.F16)
+    A2 = be.tensor(rng.standard_normal((m, k2)).astype(np.float32), dtype=rsv.F16)
+    idx, sz, _ = _int8_weight(rng, 384, k1)
+    h = be.int8(idx, sz)
+    W1 = be.tensor((rng.standard_normal((96, k1)) * 0.02).astype(np.float32), dtype=rsv.F16)
+    W2 = be.tensor((rng.standard_normal((640, k2)) * 0.02).astype(np.float32), dtype=rsv.F16)
+    bias = be.tensor(rng.standard_normal(640).astype(np.float32))
+    aux = be.tensor(rng.standard_normal((m, 640)).astype(np.float32))
+    y0 = rng.standard_normal((m, 640)).astype(np.float32)
+    # (w8, w16, n, k, x, epilogue, bias, aux)
+    specs = [(ctypes.pointer(h), NONE, 384, k1, A1, 0, NONE, NONE), (None, W1, 96, k1, A1, 4, NONE, NONE),
+             (None, W2, 640, k2, A2, 7, bias, aux), (None, W2, 640, k2, A2, 8, NONE, NONE)]
+    outs_multi, outs_single, jobs = [], [], []
+    for w8, w16, n, k, x, epi, bt, at in specs:
+        init = y0[:, :n].copy() if epi == 7 else np.zeros((m, n), np.float32)
+        ym, ys = be.tensor(init), be.tensor(init)
+        outs_multi.append((ym, n))
+        outs_single.append((ys, n))
+        jobs.append(rsv.MmJob(w16, w8, n, k, x, ym, NONE, epi, bt, at, NONE, 0))
+        be.call("rsv_gemm_ex", x, w16, w8, ys, m, n, k, epi, bt, at, NONE)
+    arr = (rsv.MmJob * len(jobs))(*jobs)
+    be.call("rsv_gemm_multi", ctypes.cast(arr, ctypes.c_void_p), len(jobs), m)
+    for (ym, n), (ys, _) in zip(outs_multi, outs_single):
+        assert np.array_equal(be.get(ym, m * n), be.get(ys, m * n)), n
+
+
 def test_gemm_epilogues(be):
     rsv = _rsv()
     rng = np.random.default_rng(8)
