@@ -194,13 +194,6 @@ __device__ __forceinline__ float quad_sum(float v) {
     v += quad_dpp<0x4E>(v);  // quad_perm 2,3,0,1
     return v;
 }
-__device__ __forceinline__ float block_sum(float v, float *red) {
-    v = wave_sum(v);
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    return (red[0] + red[1]) + (red[2] + red[3]);
-}
 __device__ __forceinline__ float sig_f(float v) { return 1.0f / (1.0f + expf(-v)); }
 __device__ __forceinline__ float h2f_w(uint32_t b) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(b & 0xFFFFu)); }
 
@@ -208,7 +201,7 @@ template <bool F16IO>
 __global__ __launch_bounds__(256) void k_wkv7_lora(WkvLoraArgs A) {
     __shared__ float mids[1024];
     __shared__ float hv[5 * 64];
-    __shared__ float red[4];
+    __shared__ float red[16];
     const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
     const int j = tid >> 2, q = tid & 3, H = A.H, C = H * 64, c = h * 64 + j;
     const size_t vo = (size_t)b * C + c;
@@ -274,46 +267,67 @@ __global__ __launch_bounds__(256) void k_wkv7_lora(WkvLoraArgs A) {
     const float aa = sig_f(acc[1] + a0);
     const float vv = vc + sig_f(acc[2] + v0) * (vfc - vc);
     const float gg = acc[3];
-    // WKV7 head vectors (model.rs:445-473, 716-826)
+    // WKV7 head vectors (model.rs:445-473, 716-826).  The raw kk and a of
+    // each column go to LDS next to the wave partials of |kk|^2 and of the
+    // bonus sum, so one barrier serves both reductions; k_hat = kk/|kk| and
+    // b = -k_hat*a are formed per column after it, with the same roundings.
     const float kk = kc * kkc;
-    float nrm = sqrtf(block_sum(q == 0 ? kk * kk : 0.0f, red));
-    nrm = nrm < A.eps ? A.eps : nrm;
-    const float inv = 1.0f / nrm;
-    const float kh = kk * inv;
     const float kmod = kc + kac * (kc * aa - kc);
+    const float p_nrm = wave_sum(q == 0 ? kk * kk : 0.0f);
+    const float p_bon = wave_sum(q == 0 ? rc * kmod * rkc : 0.0f);
     if (q == 0) {
-        hv[j] = kh;
-        hv[64 + j] = kh * (-aa);
+        hv[j] = kk;
+        hv[64 + j] = aa;
         hv[128 + j] = wd;
         hv[192 + j] = kmod;
         hv[256 + j] = rc;
     }
-    const float bonus = block_sum(q == 0 ? rc * kmod * rkc : 0.0f, red);
+    if ((tid & 63) == 0) {
+        red[tid >> 6] = p_nrm;
+        red[4 + (tid >> 6)] = p_bon;
+    }
+    __syncthreads();
+    float nrm = sqrtf((red[0] + red[1]) + (red[2] + red[3]));
+    nrm = nrm < A.eps ? A.eps : nrm;
+    const float inv = 1.0f / nrm;
+    const float bonus = (red[4] + red[5]) + (red[6] + red[7]);
     // row j, columns 16q..16q+15: S = S diag(w) + (S k_hat) b^T + v k_mod^T; y = S r
     float sr[16];
 #pragma unroll
     for (int m = 0; m < 4; m++) {
         sr[4 * m] = st4[m].x; sr[4 * m + 1] = st4[m].y; sr[4 * m + 2] = st4[m].z; sr[4 * m + 3] = st4[m].w;
     }
+    float kh[16];
     float sa = 0.0f;
 #pragma unroll
-    for (int jj = 0; jj < 16; jj++) sa = fmaf(sr[jj], hv[16 * q + jj], sa);
+    for (int jj = 0; jj < 16; jj++) {
+        kh[jj] = hv[16 * q + jj] * inv;
+        sa = fmaf(sr[jj], kh[jj], sa);
+    }
     sa = quad_sum(sa);
     float y = 0.0f;
 #pragma unroll
     for (int jj = 0; jj < 16; jj++) {
         const int cc = 16 * q + jj;
-        const float ns = sr[jj] * hv[128 + cc] + sa * hv[64 + cc] + vv * hv[192 + cc];
+        const float bb = kh[jj] * (-hv[64 + cc]);
+        const float ns = sr[jj] * hv[128 + cc] + sa * bb + vv * hv[192 + cc];
         sr[jj] = ns;
         y = fmaf(ns, hv[256 + cc], y);
     }
     y = quad_sum(y);
 #pragma unroll
     for (int m = 0; m < 4; m++) srow[m] = make_float4(sr[4 * m], sr[4 * m + 1], sr[4 * m + 2], sr[4 * m + 3]);
-    // GroupNorm over the head (two-pass, eps inside the sqrt) + bonus, times g
-    const float mean = block_sum(q == 0 ? y : 0.0f, red) * (1.0f / 64.0f);
+    // GroupNorm over the head (two-pass, eps inside the sqrt) + bonus, times
+    // g; each pass one barrier on its own slots
+    const float p_mean = wave_sum(q == 0 ? y : 0.0f);
+    if ((tid & 63) == 0) red[8 + (tid >> 6)] = p_mean;
+    __syncthreads();
+    const float mean = ((red[8] + red[9]) + (red[10] + red[11])) * (1.0f / 64.0f);
     const float d = y - mean;
-    const float var = block_sum(q == 0 ? d * d : 0.0f, red) * (1.0f / 64.0f) + A.gn_eps;
+    const float p_var = wave_sum(q == 0 ? d * d : 0.0f);
+    if ((tid & 63) == 0) red[12 + (tid >> 6)] = p_var;
+    __syncthreads();
+    const float var = ((red[12] + red[13]) + (red[14] + red[15])) * (1.0f / 64.0f) + A.gn_eps;
     const float yn = d * (1.0f / sqrtf(var)) * gam + bet + bonus * vv;
     if (q == 0) {
         if (F16IO) ((_Float16 *)A.yg)[vo] = (_Float16)(yn * gg);
