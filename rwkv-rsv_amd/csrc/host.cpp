@@ -671,11 +671,12 @@ void ln_mix(rsv_gemv_job &j, uint32_t gamma, uint32_t beta, uint32_t prev, uint3
     j.lnout = lnout;
 }
 
-// The batched layer uses the fused LoRA-up + WKV7 launch only with
-// RSV_WKV_LORA_MM=1 (measured against the two launches per batch size).
+// The batched layer runs the LoRA-up chain and the WKV7 step as one launch
+// (k_wkv7_lora_mb: the head's LoRA-up rows read once per 4 sessions) when
+// the LoRA ranks sum to at most 512; RSV_WKV_LORA_MM=0 keeps the two launches (skinny GEMM + k_wkv7_decode).
 bool mm_wkv_lora() {
     const char *e = getenv("RSV_WKV_LORA_MM");
-    return e && e[0] == '1';
+    return !(e && e[0] == '0');
 }
 
 bool wkv_lora_ok(const rsv_model_info &I) {
@@ -901,7 +902,7 @@ int forward_layer_mm(rsv_bundle *b, uint64_t i, WorkBufs &w, GpuState &s) {
     };
     if (i == 0) j1[2].y2 = s.v_first;  // v_first snapshot (gpu_model.rs:2200-2204)
     CK(rsv_gemm_skinny(c, j1, 7, B));
-    if (wkv_lora_ok(I) && mm_wkv_lora()) {
+    if (wkv_lora_ok(I) && mm_wkv_lora() && I.w_mid + I.a_mid + I.v_mid + I.g_mid <= 512) {
         // LoRA-up chain + WKV7 + GroupNorm in one launch, fp16 in and out
         rsv_wkv_lora op;
         op.state = s.rnn[i];

@@ -12,6 +12,7 @@
 // The L2 norm uses the true per-head sum of squares (the CPU path), not the
 // doubled sum of the reference's 2-threads-per-row GPU kernels.
 #include "rsv_common.h"
+#include <cstdlib>
 
 namespace rsv {
 
@@ -335,6 +336,182 @@ __global__ __launch_bounds__(256) void k_wkv7_lora(WkvLoraArgs A) {
     }
 }
 
+// ------------------------------- fused LoRA-up + decode step, batched
+// grid (H, ceil(B/SB)), 256 threads; fp16 LoRA inputs and fp16 output (the
+// operands of the batched path).  The head's 64 rows of each LoRA-up matrix
+// are read once per block for its SB sessions instead of once per session:
+//   1. wave w takes rows 16w..16w+15 of every up matrix on
+//      v_mfma_f32_16x16x16_f16 (A = weight rows, B = the sessions' LoRA
+//      inputs staged in LDS, fp32 accumulation).  A 16-byte piece of lane
+//      (i = l%16, g = l/16) covers k = 32e + 8g .. +7 of both operands and
+//      feeds two MFMAs, so A and B pair up on the same k;
+//   2. the dots pass through LDS to the WKV7 step, where wave w runs sessions
+//      w, w+4, ... with the lane-per-row layout of k_wkv7_decode (its state
+//      transpose tile and head vectors private to the wave, so the step needs
+//      no block barrier); the next session's state and vectors are loaded
+//      while the current one is computed.
+typedef _Float16 wk_h4 __attribute__((ext_vector_type(4)));
+typedef float wk_f4 __attribute__((ext_vector_type(4)));
+
+template <int SB>
+__global__ __launch_bounds__(256, SB == 4 ? 3 : 2) void k_wkv7_lora_mb(WkvLoraArgs A, int batch) {
+    constexpr int XS = 512 + 8;  // LDS row stride (halves) of one session's inputs (ranks sum <= 512)
+    __shared__ __attribute__((aligned(16))) _Float16 xs[SB * XS];
+    __shared__ float dots[4][64][SB + 1];
+    __shared__ float tile[4][32 * 65];
+    __shared__ HeadVecs hvs[4];
+    const int h = blockIdx.x, b0 = blockIdx.y * SB, tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int li = lane & 15, g = lane >> 4;
+    const int H = A.H, C = H * 64;
+    int moff[5];
+    moff[0] = 0;
+#pragma unroll
+    for (int m = 0; m < 4; m++) moff[m + 1] = moff[m] + A.mid_n[m];
+    const int L4 = moff[4];
+
+    // 1a. weight pieces of the wave's rows (the largest stream) first.  The
+    // four matrices' 32-wide k pieces are numbered p = 0 .. L4/32 - 1 in
+    // matrix order (piece p covers columns 32p.. of the concatenated
+    // inputs); the launcher admits L4 <= 512, so all of them fit the wave's
+    // registers at once
+    constexpr int kRing = 16;
+    const int P = L4 >> 5;
+    uint4 wl[kRing];
+#pragma unroll
+    for (int e = 0; e < kRing; e++) {
+        if (e < P) {
+            const int k = 32 * e, m = (k >= moff[1]) + (k >= moff[2]) + (k >= moff[3]);
+            // selects, not an indexed kernel-argument array (which would go through scratch)
+            const _Float16 *up = m == 0 ? A.up[0] : m == 1 ? A.up[1] : m == 2 ? A.up[2] : A.up[3];
+            const int mid = m == 0 ? A.mid_n[0] : m == 1 ? A.mid_n[1] : m == 2 ? A.mid_n[2] : A.mid_n[3];
+            const int off = m == 0 ? 0 : m == 1 ? moff[1] : m == 2 ? moff[2] : moff[3];
+            wl[e] = *((const uint4 *)(up + (size_t)(h * 64 + wave * 16 + li) * mid + (k - off)) + g);
+        }
+    }
+    // 1b. the block's LoRA inputs, session-major, 16-byte pieces
+    const int ppr = L4 >> 3;  // pieces per session
+    for (int e = tid; e < SB * ppr; e += 256) {
+        const int sl = e / ppr, k = (e - sl * ppr) * 8, b = b0 + sl;
+        const int m = (k >= moff[1]) + (k >= moff[2]) + (k >= moff[3]);
+        const _Float16 *src = (const _Float16 *)(m == 0 ? A.mid[0] : m == 1 ? A.mid[1] : m == 2 ? A.mid[2] : A.mid[3]);
+        const int mid = m == 0 ? A.mid_n[0] : m == 1 ? A.mid_n[1] : m == 2 ? A.mid_n[2] : A.mid_n[3];
+        const int off = m == 0 ? 0 : m == 1 ? moff[1] : m == 2 ? moff[2] : moff[3];
+        uint4 v = make_uint4(0u, 0u, 0u, 0u);
+        if (b < batch) v = *(const uint4 *)(src + (size_t)b * mid + (k - off));
+        *(uint4 *)&xs[sl * XS + k] = v;
+    }
+    // 1c. the first session's state rows and vectors of this wave
+    const int c = h * 64 + lane;
+    const float w0 = A.w0[c], a0 = A.a0[c], v0 = A.v0[c], kkc = A.kk[c], kac = A.ka[c], rkc = A.rk[c];
+    const float gam = A.gamma[c], bet = A.beta[c], sw = A.scale[0];
+    float4 st[16];
+    float nk = 0.0f, nr = 0.0f, nv = 0.0f, nvf = 0.0f;
+    // (a session index past the batch reads session b0, which always exists;
+    // its values are never used)
+#define WKV_MB_LOAD_SESSION(SL)                                                            \
+    {                                                                                      \
+        const int bq = b0 + (SL) < batch ? b0 + (SL) : b0;                                 \
+        const float4 *Sg = (const float4 *)(A.S + ((size_t)bq * H + h) * 4096);            \
+        _Pragma("unroll") for (int m = 0; m < 16; m++) st[m] = Sg[m * 64 + lane];          \
+        const size_t vq = (size_t)bq * C + c;                                              \
+        nk = A.k[vq]; nr = A.r[vq]; nv = A.v[vq]; nvf = A.vf[vq];                          \
+    }
+    WKV_MB_LOAD_SESSION(wave)
+    __syncthreads();
+
+    // 1d. LoRA-up dots: rows 16*wave + 4g + q (q = 0..3) for session li; one
+    // accumulator, flushed to LDS where the matrix changes (uniform branch)
+    {
+        wk_f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        int mcur = 0;
+        auto flush = [&](int m) {
+            if (li < SB) {
+#pragma unroll
+                for (int q = 0; q < 4; q++) dots[m][wave * 16 + 4 * g + q][li] = acc[q];
+            }
+        };
+#pragma unroll
+        for (int e = 0; e < kRing; e++) {
+            const int k = 32 * e, m = (k >= moff[1]) + (k >= moff[2]) + (k >= moff[3]);
+            if (e >= P) continue;
+            if (m != mcur) {
+                flush(mcur);
+                acc = (wk_f4){0.0f, 0.0f, 0.0f, 0.0f};
+                mcur = m;
+            }
+            const uint4 w = wl[e];
+            const uint4 x = li < SB ? *(const uint4 *)(xs + li * XS + k + 8 * g) : make_uint4(0u, 0u, 0u, 0u);
+            acc = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(wk_h4, make_uint2(w.x, w.y)),
+                                                        __builtin_bit_cast(wk_h4, make_uint2(x.x, x.y)), acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(wk_h4, make_uint2(w.z, w.w)),
+                                                        __builtin_bit_cast(wk_h4, make_uint2(x.z, x.w)), acc, 0, 0, 0);
+        }
+        flush(mcur);
+    }
+    if (h == 0 && A.side_dst)
+        for (int e = tid; e < SB * C; e += 256) {
+            const int b = b0 + e / C;
+            if (b < batch) A.side_dst[(size_t)b * C + e % C] = A.side_src[(size_t)b * C + e % C];
+        }
+    __syncthreads();
+
+    // 2. WKV7 step of sessions wave, wave + 4, ... (model.rs:445-473, 716-826)
+    float *tl = tile[wave];
+    HeadVecs &hv = hvs[wave];
+    for (int sl = wave; sl < SB && b0 + sl < batch; sl += 4) {
+        const int b = b0 + sl;
+        const float kc = nk, rc = nr, vc = nv, vfc = nvf;
+        float s[64];
+#pragma unroll
+        for (int half = 0; half < 2; half++) {
+#pragma unroll
+            for (int m = 8 * half; m < 8 * half + 8; m++) {
+                const int e = (m * 64 + lane) * 4, row = (e >> 6) - 32 * half, col = e & 63;
+                tl[row * 65 + col + 0] = st[m].x;
+                tl[row * 65 + col + 1] = st[m].y;
+                tl[row * 65 + col + 2] = st[m].z;
+                tl[row * 65 + col + 3] = st[m].w;
+            }
+            __builtin_amdgcn_wave_barrier();
+            if ((lane >> 5) == half) {
+#pragma unroll
+                for (int j = 0; j < 64; j++) s[j] = tl[(lane & 31) * 65 + j];
+            }
+            __builtin_amdgcn_wave_barrier();
+        }
+        if (sl + 4 < SB) WKV_MB_LOAD_SESSION(sl + 4)  // in flight during this session's step
+        const float wd = expf(sig_f(dots[0][lane][sl] + w0) * sw);
+        const float aa = sig_f(dots[1][lane][sl] + a0);
+        const float vv = vc + sig_f(dots[2][lane][sl] + v0) * (vfc - vc);
+        const float gg = dots[3][lane][sl];
+        float kmod;
+        head_vectors(hv, lane, kc, kkc, aa, kac, rc, wd, A.eps, kmod);
+        __builtin_amdgcn_wave_barrier();
+        const float y = row_update(s, hv, vv);
+        const float yn = head_norm(y, gam, bet, rc * kmod * rkc, vv, A.gn_eps);
+        ((_Float16 *)A.yg)[(size_t)b * C + c] = (_Float16)(yn * gg);
+        float4 *Sg = (float4 *)(A.S + ((size_t)b * H + h) * 4096);
+#pragma unroll
+        for (int half = 0; half < 2; half++) {
+            __builtin_amdgcn_wave_barrier();
+            if ((lane >> 5) == half) {
+#pragma unroll
+                for (int j = 0; j < 64; j++) tl[(lane & 31) * 65 + j] = s[j];
+            }
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int m = 8 * half; m < 8 * half + 8; m++) {
+                const int e = (m * 64 + lane) * 4, row = (e >> 6) - 32 * half, col = e & 63;
+                Sg[m * 64 + lane] = make_float4(tl[row * 65 + col], tl[row * 65 + col + 1], tl[row * 65 + col + 2],
+                                                tl[row * 65 + col + 3]);
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+#undef WKV_MB_LOAD_SESSION
+}
+
 int launch_wkv7_lora(rsv_ctx *ctx, const WkvLoraArgs &a, int batch) {
     if (a.H <= 0 || batch <= 0 || batch > 65535) return RSV_FAIL("wkv7_lora: bad h=%d batch=%d", a.H, batch);
     int L4 = 0;
@@ -344,7 +521,17 @@ int launch_wkv7_lora(rsv_ctx *ctx, const WkvLoraArgs &a, int batch) {
         L4 += a.mid_n[m];
     }
     if (L4 > 1024) return RSV_FAIL("wkv7_lora: LoRA ranks sum to %d (max 1024)", L4);
-    if (a.f16_io) hipLaunchKernelGGL(k_wkv7_lora<true>, dim3(a.H, batch), dim3(256), 0, ctx->stream, a);
+    // batches of 16 and more with fp16 operands and ranks summing to at most
+    // 512: SB sessions per block (the head's LoRA-up rows read once per
+    // block); RSV_WKV_LORA_SB = 0 keeps one block per (head, session)
+    const char *sbe = getenv("RSV_WKV_LORA_SB");
+    const int sb = sbe ? atoi(sbe) : 4;
+    if (a.f16_io && batch >= 16 && L4 <= 512 && (sb == 4 || sb == 8 || sb == 16)) {
+        const int nb = (batch + sb - 1) / sb;
+        if (sb == 4) hipLaunchKernelGGL(k_wkv7_lora_mb<4>, dim3(a.H, nb), dim3(256), 0, ctx->stream, a, batch);
+        else if (sb == 8) hipLaunchKernelGGL(k_wkv7_lora_mb<8>, dim3(a.H, nb), dim3(256), 0, ctx->stream, a, batch);
+        else hipLaunchKernelGGL(k_wkv7_lora_mb<16>, dim3(a.H, nb), dim3(256), 0, ctx->stream, a, batch);
+    } else if (a.f16_io) hipLaunchKernelGGL(k_wkv7_lora<true>, dim3(a.H, batch), dim3(256), 0, ctx->stream, a);
     else hipLaunchKernelGGL(k_wkv7_lora<false>, dim3(a.H, batch), dim3(256), 0, ctx->stream, a);
     RSV_HIP(hipGetLastError());
     return 0;

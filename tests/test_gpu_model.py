@@ -398,12 +398,15 @@ def test_fused_lora_wkv_matches_two_launches(bundles, kind, monkeypatch):
     assert rel_rmse(s_one, s_two) <= 1e-5
 
 
-@pytest.mark.parametrize("kind", ["f16", "i8"])
-def test_batched_fused_lora_wkv(bundles, kind, monkeypatch):
+@pytest.mark.parametrize("kind,sb,B", [("f16", "8", 20), ("i8", "8", 20), ("i8", "4", 37), ("i8", "16", 37),
+                                       ("i8", "0", 20)])
+def test_batched_fused_lora_wkv(bundles, kind, sb, B, monkeypatch):
     """The batched layer's fused LoRA-up + WKV7 launch (RSV_WKV_LORA_MM=1,
-    fp16 operands in and out) equals its two-launch form to fp32 rounding."""
+    fp16 operands in and out) equals its two-launch form to fp32 rounding:
+    the SB-sessions-per-block kernel (SB = 4, 8, 16, batches that leave the
+    last block partly empty) and the one-block-per-session kernel (SB = 0)."""
+    monkeypatch.setenv("RSV_WKV_LORA_SB", sb)
     b, _ = bundles[kind]
-    B = 20
     prompts = [_prompt(3 + (i % 5), 60 + i) for i in range(B)]
     toks = np.array([(11 * i + 5) % SMALL["vocab"] for i in range(B)], np.uint32)
     out = {}
