@@ -183,14 +183,14 @@ __device__ __forceinline__ float gemm_epi_val(float v, float bias, float aux, fl
     else return v;
 }
 
-template <int EPI, int MI>
-__device__ __forceinline__ void gemm2_epilogue(const GemmArgs &g, const float16_t (&acc)[MI][2], int m0, int n0, int wm,
+template <int EPI, int MI, int NJ = 2>
+__device__ __forceinline__ void gemm2_epilogue(const GemmArgs &g, const float16_t (&acc)[MI][NJ], int m0, int n0, int wm,
                                                int wn, int lane) {
     constexpr bool need_b = EPI == GE_BIAS || EPI == GE_WDECAY || EPI == GE_SIGBIAS || EPI == GE_VLERP;
     constexpr bool need_aux = EPI == GE_ADD || EPI == GE_VLERP;
     const float scale = EPI == GE_WDECAY ? g.scale[0] : 0.0f;
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
+    for (int j = 0; j < NJ; j++) {
         const int col = n0 + wn + j * 32 + (lane & 31);
         if (col >= g.n) continue;
         const float bias = need_b ? g.bias[col] : 0.0f;
@@ -357,6 +357,161 @@ __global__ __launch_bounds__(256) void k_gemm2_multi(GemmJobs jobs) {
         gemm2_body<false, BM2>(g, m0, n0, As, Bs);
 }
 
+// Third form: the 128x128 tile of k_gemm2 with BKT (64 or 128) k per stage
+// and one LDS buffer.  The next stage's loads are issued before the current
+// stage is multiplied out, as in k_gemm2, but each stage carries 2x or 4x
+// the bytes, so a block keeps 24 or 48 KB in flight instead of 12 KB (the
+// stage-to-stage wait is a memory latency, several times a 32-k stage's
+// MFMA work).  Two barriers per stage: all waves are done reading the
+// buffer before it is overwritten.
+template <bool B_I8, int BKT, int NJ>
+__device__ __forceinline__ void gemm3_body(const GemmArgs &g, int m0, int n0, _Float16 *As, _Float16 *Bs) {
+    constexpr int MI = 2, LD = BKT + 8, BNJ = 64 * NJ;  // block columns
+    constexpr int PA = 128 * BKT / 8 / 256;   // 16-byte A pieces per thread
+    constexpr int KH = BKT * BNJ / 256;       // k per thread of the B loader (256 / BNJ threads per row)
+    constexpr int PB = B_I8 ? KH / 16 : KH / 8;  // its 16-byte pieces
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 32 * NJ;
+    const int lr = tid / (256 / BNJ), lc = (tid % (256 / BNJ)) * KH;
+
+    float16_t acc[MI][NJ];
+#pragma unroll
+    for (int i = 0; i < MI; i++)
+#pragma unroll
+        for (int j = 0; j < NJ; j++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) acc[i][j][e] = 0.0f;
+
+    u32x4g ra[PA], rb[PB];
+    uint32_t rsz = 0;
+    const int brow = n0 + lr;
+    const bool bok = brow < g.n;
+    const int KG = g.k / 128;
+    auto load = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < PA; i++) {
+            const int p = tid + 256 * i, row = m0 + p / (BKT / 8), c8 = p % (BKT / 8);
+            ra[i] = row < g.m ? *(const u32x4g *)(g.a + (size_t)row * g.lda + k0 + 8 * c8) : (u32x4g){0u, 0u, 0u, 0u};
+        }
+        if (bok) {
+            const u32x4g *bp = B_I8 ? (const u32x4g *)((const uint8_t *)g.b + (size_t)brow * g.k + k0 + lc)
+                                    : (const u32x4g *)((const _Float16 *)g.b + (size_t)brow * g.k + k0 + lc);
+#pragma unroll
+            for (int e = 0; e < PB; e++) rb[e] = bp[e];
+            // KH <= 64 consecutive k from a multiple of KH: one 128-group
+            if (B_I8) rsz = g.sz[(size_t)brow * KG + (k0 + lc) / 128];
+        } else {
+#pragma unroll
+            for (int e = 0; e < PB; e++) rb[e] = (u32x4g){0u, 0u, 0u, 0u};
+            rsz = 0;
+        }
+    };
+    auto stage = [&]() {
+#pragma unroll
+        for (int i = 0; i < PA; i++) {
+            const int p = tid + 256 * i;
+            *(u32x4g *)(As + (p / (BKT / 8)) * LD + 8 * (p % (BKT / 8))) = ra[i];
+        }
+        u32x4g *bd = (u32x4g *)(Bs + lr * LD + lc);
+        if (B_I8) {
+            // w = s*q + z with the product and the sum each rounded to fp32
+            // (model.rs:234-252), then rounded to fp16
+            const float s = h2f_g(rsz), z = h2f_g(rsz >> 16);
+#pragma unroll
+            for (int e = 0; e < PB; e++) {
+                uint32_t o[8];
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const uint32_t w = rb[e][q];
+                    const float w0 = __fadd_rn(__fmul_rn(s, (float)(w & 0xFFu)), z);
+                    const float w1 = __fadd_rn(__fmul_rn(s, (float)((w >> 8) & 0xFFu)), z);
+                    const float w2 = __fadd_rn(__fmul_rn(s, (float)((w >> 16) & 0xFFu)), z);
+                    const float w3 = __fadd_rn(__fmul_rn(s, (float)(w >> 24)), z);
+                    o[2 * q] = pack2(w0, w1);
+                    o[2 * q + 1] = pack2(w2, w3);
+                }
+                bd[2 * e] = (u32x4g){o[0], o[1], o[2], o[3]};
+                bd[2 * e + 1] = (u32x4g){o[4], o[5], o[6], o[7]};
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < PB; e++) bd[e] = rb[e];
+        }
+    };
+
+    load(0);
+    stage();
+    __syncthreads();
+    for (int k0 = 0; k0 < g.k; k0 += BKT) {
+        const bool more = k0 + BKT < g.k;
+        if (more) load(k0 + BKT);
+#pragma unroll
+        for (int st = 0; st < BKT / 16; st++) {
+            half8_t af[MI], bf[NJ];
+#pragma unroll
+            for (int i = 0; i < MI; i++)
+                af[i] = *(const half8_t *)(As + (wm + i * 32 + (lane & 31)) * LD + 16 * st + 8 * (lane >> 5));
+#pragma unroll
+            for (int j = 0; j < NJ; j++)
+                bf[j] = *(const half8_t *)(Bs + (wn + j * 32 + (lane & 31)) * LD + 16 * st + 8 * (lane >> 5));
+#pragma unroll
+            for (int i = 0; i < MI; i++)
+#pragma unroll
+                for (int j = 0; j < NJ; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+        if (more) {
+            __syncthreads();
+            stage();
+            __syncthreads();
+        }
+    }
+#define GEMM3_EPI(K) gemm2_epilogue<K, MI, NJ>(g, acc, m0, n0, wm, wn, lane)
+    switch (g.epi) {
+        case GE_BIAS: GEMM3_EPI(GE_BIAS); break;
+        case GE_ADD: GEMM3_EPI(GE_ADD); break;
+        case GE_RELU2: GEMM3_EPI(GE_RELU2); break;
+        case GE_TANH: GEMM3_EPI(GE_TANH); break;
+        case GE_WDECAY: GEMM3_EPI(GE_WDECAY); break;
+        case GE_SIGBIAS: GEMM3_EPI(GE_SIGBIAS); break;
+        case GE_VLERP: GEMM3_EPI(GE_VLERP); break;
+        case GE_SIGMOID: GEMM3_EPI(GE_SIGMOID); break;
+        default: GEMM3_EPI(GE_STORE); break;
+    }
+#undef GEMM3_EPI
+}
+
+template <bool B_I8, int BKT>
+__global__ __launch_bounds__(256, BKT == 64 ? 3 : 2) void k_gemm3(GemmArgs g) {
+    __shared__ __attribute__((aligned(16))) _Float16 As[128 * (BKT + 8)];
+    __shared__ __attribute__((aligned(16))) _Float16 Bs[BN * (BKT + 8)];
+    gemm3_body<B_I8, BKT, 2>(g, blockIdx.y * 128, blockIdx.x * BN, As, Bs);
+}
+
+template <int BKT>
+__global__ __launch_bounds__(256, BKT == 64 ? 3 : 2) void k_gemm3_multi(GemmJobs jobs) {
+    __shared__ __attribute__((aligned(16))) _Float16 As[128 * (BKT + 8)];
+    __shared__ __attribute__((aligned(16))) _Float16 Bs[BN * (BKT + 8)];
+    const int bid = blockIdx.x;
+    int ji = 0;
+    while (ji + 1 < jobs.n && bid >= jobs.blk_start[ji + 1]) ji++;
+    const GemmArgs &g = jobs.j[ji];
+    const int local = bid - jobs.blk_start[ji], nt = (g.n + BN - 1) / BN;
+    const int m0 = (local / nt) * 128, n0 = (local % nt) * BN;
+    if (g.b_i8)
+        gemm3_body<true, BKT, 2>(g, m0, n0, As, Bs);
+    else
+        gemm3_body<false, BKT, 2>(g, m0, n0, As, Bs);
+}
+
+// k per stage of the prefill GEMMs: RSV_GEMM_BK = 32 (k_gemm2, double-
+// buffered), 64 or 128 (k_gemm3); a job whose k is not a multiple takes 32.
+static int gemm_bk() {
+    const char *e = getenv("RSV_GEMM_BK");
+    const int v = e ? atoi(e) : 64;
+    return v == 128 || v == 64 ? v : 32;
+}
+
 static int gemm_check(const GemmArgs &g) {
     if (g.m <= 0 || g.n <= 0 || g.k <= 0) return RSV_FAIL("gemm: bad shape m=%d n=%d k=%d", g.m, g.n, g.k);
     if (g.k % BK != 0) return RSV_FAIL("gemm: k=%d must be a multiple of %d", g.k, BK);
@@ -381,7 +536,12 @@ int launch_gemm_multi(rsv_ctx *ctx, GemmJobs &jobs) {
         total += ((g.n + BN - 1) / BN) * ((g.m + BM - 1) / BM);
     }
     jobs.blk_start[jobs.n] = total;
-    hipLaunchKernelGGL((k_gemm2_multi<128>), dim3(total), dim3(256), 0, ctx->stream, jobs);
+    int bk = gemm_bk();
+    for (int i = 0; i < jobs.n; i++)
+        while (bk > 32 && jobs.j[i].k % bk) bk /= 2;
+    if (bk == 128) hipLaunchKernelGGL((k_gemm3_multi<128>), dim3(total), dim3(256), 0, ctx->stream, jobs);
+    else if (bk == 64) hipLaunchKernelGGL((k_gemm3_multi<64>), dim3(total), dim3(256), 0, ctx->stream, jobs);
+    else hipLaunchKernelGGL((k_gemm2_multi<128>), dim3(total), dim3(256), 0, ctx->stream, jobs);
     RSV_HIP(hipGetLastError());
     return 0;
 }
@@ -405,7 +565,15 @@ int launch_gemm(rsv_ctx *ctx, const GemmArgs &g) {
     if (v2) {
         // 128-row tiles: 256-row tiles (one wave per SIMD at 275 registers)
         // measured 1.5x slower on the prefill GEMMs
-        if (g.b_i8) hipLaunchKernelGGL((k_gemm2<true, 128>), grid, dim3(256), 0, ctx->stream, g);
+        int bk = gemm_bk();
+        while (bk > 32 && g.k % bk) bk /= 2;
+        if (bk == 128) {
+            if (g.b_i8) hipLaunchKernelGGL((k_gemm3<true, 128>), grid, dim3(256), 0, ctx->stream, g);
+            else hipLaunchKernelGGL((k_gemm3<false, 128>), grid, dim3(256), 0, ctx->stream, g);
+        } else if (bk == 64) {
+            if (g.b_i8) hipLaunchKernelGGL((k_gemm3<true, 64>), grid, dim3(256), 0, ctx->stream, g);
+            else hipLaunchKernelGGL((k_gemm3<false, 64>), grid, dim3(256), 0, ctx->stream, g);
+        } else if (g.b_i8) hipLaunchKernelGGL((k_gemm2<true, 128>), grid, dim3(256), 0, ctx->stream, g);
         else hipLaunchKernelGGL((k_gemm2<false, 128>), grid, dim3(256), 0, ctx->stream, g);
         RSV_HIP(hipGetLastError());
         return 0;
