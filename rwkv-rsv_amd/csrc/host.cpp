@@ -242,6 +242,8 @@ struct Linear {
     bool tiled = false;
     rsv_int8 ht{};
     uint32_t t16 = NONE;
+    // fp16 copy of an int8 matrix for the prefill GEMM (made on first use)
+    uint32_t p16 = NONE;
 };
 
 struct Layer {
@@ -299,6 +301,7 @@ struct rsv_bundle {
     SeqBufs seq;
     std::vector<uint32_t> owned;  // every tensor the bundle created
     bool tiled = false;           // MFMA-tiled weight copies made (tile_model)
+    bool p16 = false;             // fp16 prefill copies of the int8 linears made (prefill_weights)
     // persistent single-session decode step: the state it is bound to, and
     // whether building it failed for good (shape or format unsupported)
     const GpuState *mega_for = nullptr;
@@ -832,12 +835,22 @@ rsv_mm_job mm_job(const Linear &L, uint32_t x, uint32_t y, int epi) {
 }
 
 // A prefill GEMM job on the row-major weights (rsv_gemm_multi).
+// fp16 prefill copies of the int8 matrices are made and used unless
+// RSV_PREFILL_F16=0 (read at each use, so a process can compare both)
+bool use_p16() {
+    const char *e = getenv("RSV_PREFILL_F16");
+    return !(e && e[0] == '0');
+}
+
+// Row-major GEMM job of a linear; an int8 matrix with an fp16 prefill copy
+// runs on the copy (the same fp16 values the int8 loader would make).
 rsv_mm_job gemm_job(const Linear &L, uint32_t x, uint32_t y, int epi) {
     rsv_mm_job j;
     memset(&j, 0xFF, sizeof j);
     j.tiled = 0;
-    j.w16 = L.i8 ? NONE : L.w16;
-    j.w8 = L.i8 ? &L.h : nullptr;
+    const bool i8 = L.i8 && (L.p16 == NONE || !use_p16());
+    j.w16 = i8 ? NONE : L.i8 ? L.p16 : L.w16;
+    j.w8 = i8 ? &L.h : nullptr;
     j.n = L.m;
     j.k = L.k;
     j.x = x;
@@ -1092,7 +1105,28 @@ struct Seg {
 };
 
 int gemm_lin(rsv_bundle *b, const Linear &L, uint32_t a, uint32_t c, uint64_t m, int epi) {
-    CK(rsv_gemm_ex(b->ctx, a, L.i8 ? NONE : L.w16, L.i8 ? &L.h : nullptr, c, m, L.m, L.k, epi, NONE, NONE, NONE));
+    const bool i8 = L.i8 && (L.p16 == NONE || !use_p16());
+    CK(rsv_gemm_ex(b->ctx, a, i8 ? NONE : L.i8 ? L.p16 : L.w16, i8 ? &L.h : nullptr, c, m, L.m, L.k, epi, NONE, NONE,
+                   NONE));
+    return 0;
+}
+
+// fp16 copies of the int8 layer matrices for the prefill GEMM, dequantised
+// with the roundings of the GEMM's own int8 loader (model.rs:234-252: the
+// product and the sum each rounded to fp32, then to fp16), so prefill gives
+// the same bits with or without them.  The copies take twice the int8 bytes
+// (5.2 GB for the 3B shape); RSV_PREFILL_F16=0 keeps the int8 loader.
+int prefill_weights(rsv_bundle *b) {
+    if (b->p16 || !use_p16()) return 0;
+    b->p16 = true;
+    for (auto &L : b->layers)
+        for (Linear *p : {&L.rw, &L.kw, &L.vw, &L.ow, &L.fk, &L.fv}) {
+            if (!p->i8 || p->p16 != NONE) continue;
+            uint32_t id;
+            CK(rsv_tensor_create(b->ctx, p->m * p->k, RSV_F16, &id));
+            CK(rsv_dequant_int8_to_f16(b->ctx, &p->h, id, p->m, p->k));
+            p->p16 = id;
+        }
     return 0;
 }
 
@@ -1116,7 +1150,10 @@ int prefill(rsv_bundle *b, GpuState &s, const std::vector<Seg> &segs, float *log
     // kernel, which streams each weight once per 64 rows; longer ones on the
     // prefill GEMM.
     const bool small = T <= kSmallPrefill;
-    if (small) HK(tile_model(b));
+    // the LoRA matrices' descriptors (and the batched path's tiled copies,
+    // which decode needs next) come from tile_model on both paths
+    HK(tile_model(b));
+    if (!small) HK(prefill_weights(b));
     HK(get_seq(b, T, S));
     SeqBufs &q = b->seq;
     std::vector<uint32_t> tok(T), prev(T), st(S), ln(S), sl(S), last(S);

@@ -504,6 +504,153 @@ __global__ __launch_bounds__(256, BKT == 64 ? 3 : 2) void k_gemm3_multi(GemmJobs
         gemm3_body<false, BKT, 2>(g, m0, n0, As, Bs);
 }
 
+// Fourth form, fp16 weights only (the prefill's dequantised copies of the
+// int8 matrices and the fp16 LoRA matrices): the A and B stages go from
+// global memory straight into LDS (buffer_load_dwordx4 ... lds), so no
+// VGPRs stage them and NS - 1 stages of 32 k are in flight while one is
+// multiplied out.
+//   - LDS: each stage has its own A and B arrays (separate objects, so the
+//     compiler's wait before a fragment read covers that stage's copies
+//     only).  A row of a stage is 4 chunks of 8 halves; chunk c of row r
+//     sits in 16-byte slot 4r + (c ^ ((r >> 2) & 3)), which makes the
+//     fragment reads (32 rows, one chunk) conflict-free per 16 lanes.  One
+//     copy instruction fills 64 consecutive slots, so lane i of copy j
+//     fetches the chunk that belongs in slot 64j + i.
+//   - Rows past m (A) or n (B) lie past the buffer's size and read as zero.
+//   - Each wave waits for its own copies of the stage, then one barrier
+//     makes every wave's copies visible and frees the stage read before it;
+//     stages past the end copy from an offset outside the buffer (zeros), so
+//     the wait count is the same every stage.
+//   - The MFMA sequence (k ascending, 16 per instruction, the same lane to
+//     k mapping) is that of k_gemm2, so the results are bit-identical to it.
+typedef __attribute__((address_space(3))) void *g4_lds_t;
+constexpr int G4_PER = 4;  // copy instructions per wave per stage (A 2, B 2)
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t g4_rsrc(const void *p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, 0x00020000);
+}
+
+template <int NS>
+__device__ __forceinline__ void gemm4_body(const GemmArgs &g, int m0, int n0, _Float16 *const (&As)[NS],
+                                           _Float16 *const (&Bs)[NS]) {
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+    const __amdgpu_buffer_rsrc_t ra = g4_rsrc(g.a, (uint32_t)((size_t)g.m * g.lda * 2));
+    const __amdgpu_buffer_rsrc_t rb = g4_rsrc(g.b, (uint32_t)((size_t)g.n * g.k * 2));
+    // the two slots of each copy instruction of this wave: row and source chunk
+    int a_off[2], b_off[2];
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+        const int sl = 64 * (2 * wave + t) + lane, row = sl >> 2, c = (sl & 3) ^ ((row >> 2) & 3);
+        a_off[t] = ((m0 + row) * g.lda + 8 * c) * 2;
+        b_off[t] = ((n0 + row) * g.k + 8 * c) * 2;
+    }
+    const int nst = g.k / 32;
+    auto issue = [&](int st, _Float16 *Ad, _Float16 *Bd) {
+        const bool live = st < nst;
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            const int ka = live ? a_off[t] + 64 * st : 0x7FFFFFF0;
+            const int kb = live ? b_off[t] + 64 * st : 0x7FFFFFF0;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (g4_lds_t)(Ad + (2 * wave + t) * 512), 16, ka, 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (g4_lds_t)(Bd + (2 * wave + t) * 512), 16, kb, 0, 0, 0);
+        }
+    };
+
+    float16_t acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) acc[i][j][e] = 0.0f;
+    auto compute = [&](const _Float16 *A_, const _Float16 *B_) {
+#pragma unroll
+        for (int st = 0; st < 2; st++) {
+            const int c = 2 * st + (lane >> 5);
+            half8_t af[2], bf[2];
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                const int r = wm + i * 32 + (lane & 31);
+                af[i] = *(const half8_t *)(A_ + 8 * (4 * r + (c ^ ((r >> 2) & 3))));
+            }
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const int r = wn + j * 32 + (lane & 31);
+                bf[j] = *(const half8_t *)(B_ + 8 * (4 * r + (c ^ ((r >> 2) & 3))));
+            }
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int j = 0; j < 2; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+    };
+
+#pragma unroll
+    for (int u = 0; u < NS - 1; u++) issue(u, As[u], Bs[u]);
+    for (int s0 = 0; s0 < nst; s0 += NS) {
+#pragma unroll
+        for (int u = 0; u < NS; u++) {
+            if (s0 + u >= nst) break;
+            // this wave's copies of stage s0 + u are done when at most the
+            // NS - 2 later stages' copies are outstanding
+            __builtin_amdgcn_s_waitcnt(((G4_PER * (NS - 2)) & 0xF) | (((G4_PER * (NS - 2)) >> 4) << 14) | (0x7 << 4) |
+                                       (0xF << 8));
+            __builtin_amdgcn_s_barrier();
+            issue(s0 + u + NS - 1, As[(u + NS - 1) % NS], Bs[(u + NS - 1) % NS]);
+            compute(As[u], Bs[u]);
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // no copy may land in LDS after the block
+#define GEMM4_EPI(K) gemm2_epilogue<K, 2>(g, acc, m0, n0, wm, wn, lane)
+    switch (g.epi) {
+        case GE_BIAS: GEMM4_EPI(GE_BIAS); break;
+        case GE_ADD: GEMM4_EPI(GE_ADD); break;
+        case GE_RELU2: GEMM4_EPI(GE_RELU2); break;
+        case GE_TANH: GEMM4_EPI(GE_TANH); break;
+        case GE_WDECAY: GEMM4_EPI(GE_WDECAY); break;
+        case GE_SIGBIAS: GEMM4_EPI(GE_SIGBIAS); break;
+        case GE_VLERP: GEMM4_EPI(GE_VLERP); break;
+        case GE_SIGMOID: GEMM4_EPI(GE_SIGMOID); break;
+        default: GEMM4_EPI(GE_STORE); break;
+    }
+#undef GEMM4_EPI
+}
+
+constexpr int G4_NS = 3;  // LDS stages (48 KB per block: three blocks per CU)
+
+#define G4_LDS                                                                                  \
+    __shared__ __attribute__((aligned(16))) _Float16 A0[128 * 32], A1[128 * 32], A2[128 * 32];  \
+    __shared__ __attribute__((aligned(16))) _Float16 B0[128 * 32], B1[128 * 32], B2[128 * 32];  \
+    _Float16 *const As[G4_NS] = {A0, A1, A2};                                                   \
+    _Float16 *const Bs[G4_NS] = {B0, B1, B2};
+
+__global__ __launch_bounds__(256) void k_gemm4(GemmArgs g) {
+    G4_LDS
+    gemm4_body<G4_NS>(g, blockIdx.y * 128, blockIdx.x * BN, As, Bs);
+}
+
+__global__ __launch_bounds__(256) void k_gemm4_multi(GemmJobs jobs) {
+    G4_LDS
+    const int bid = blockIdx.x;
+    int ji = 0;
+    while (ji + 1 < jobs.n && bid >= jobs.blk_start[ji + 1]) ji++;
+    const GemmArgs &g = jobs.j[ji];
+    const int local = bid - jobs.blk_start[ji], nt = (g.n + BN - 1) / BN;
+    gemm4_body<G4_NS>(g, (local / nt) * 128, (local % nt) * BN, As, Bs);
+}
+#undef G4_LDS
+
+// k_gemm4 takes a job, with RSV_GEMM_DMA=1, when its weights are fp16, k is
+// a multiple of 32 and both operands fit a 32-bit buffer range (measured
+// slower than k_gemm3 on the prefill shapes, so off by default)
+static bool gemm4_ok(const GemmArgs &g) {
+    const char *e = getenv("RSV_GEMM_DMA");
+    if (!(e && e[0] == '1')) return false;
+    return !g.b_i8 && g.k % 32 == 0 && (size_t)g.m * g.lda * 2 < 0x7FFFFFF0ull && (size_t)g.n * g.k * 2 < 0x7FFFFFF0ull;
+}
+
 // k per stage of the prefill GEMMs: RSV_GEMM_BK = 32 (k_gemm2, double-
 // buffered), 64 or 128 (k_gemm3); a job whose k is not a multiple takes 32.
 static int gemm_bk() {
@@ -536,6 +683,13 @@ int launch_gemm_multi(rsv_ctx *ctx, GemmJobs &jobs) {
         total += ((g.n + BN - 1) / BN) * ((g.m + BM - 1) / BM);
     }
     jobs.blk_start[jobs.n] = total;
+    bool dma = true;
+    for (int i = 0; i < jobs.n; i++) dma &= gemm4_ok(jobs.j[i]);
+    if (dma) {
+        hipLaunchKernelGGL(k_gemm4_multi, dim3(total), dim3(256), 0, ctx->stream, jobs);
+        RSV_HIP(hipGetLastError());
+        return 0;
+    }
     int bk = gemm_bk();
     for (int i = 0; i < jobs.n; i++)
         while (bk > 32 && jobs.j[i].k % bk) bk /= 2;
@@ -565,6 +719,11 @@ int launch_gemm(rsv_ctx *ctx, const GemmArgs &g) {
     if (v2) {
         // 128-row tiles: 256-row tiles (one wave per SIMD at 275 registers)
         // measured 1.5x slower on the prefill GEMMs
+        if (gemm4_ok(g)) {
+            hipLaunchKernelGGL(k_gemm4, grid, dim3(256), 0, ctx->stream, g);
+            RSV_HIP(hipGetLastError());
+            return 0;
+        }
         int bk = gemm_bk();
         while (bk > 32 && g.k % bk) bk /= 2;
         if (bk == 128) {

@@ -419,3 +419,22 @@ def test_batched_fused_lora_wkv(bundles, kind, sb, B, monkeypatch):
         S.free()
     assert rel_rmse(out["1"][0], out["0"][0]) <= 1e-4
     assert rel_rmse(out["1"][1], out["0"][1]) <= 1e-4
+
+
+@pytest.mark.parametrize("kind", ["i8", "i8g"])
+def test_prefill_f16_weight_copies_bit_identical(bundles, kind, monkeypatch):
+    """Prefill of more than 128 packed rows runs its int8 layer matrices on
+    fp16 copies made with the int8 loader's roundings (and the DMA-staged
+    GEMM); logits and state equal those of the int8 loader bit for bit."""
+    monkeypatch.setenv("RSV_MEGA", "0")
+    b, _ = bundles[kind]
+    prompts = [_prompt(90 + 17 * i, 300 + i) for i in range(3)]
+    out = {}
+    for flag in ("0", "1"):
+        monkeypatch.setenv("RSV_PREFILL_F16", flag)
+        S = b.create_batch_state(3)
+        _, lg = b.forward_seq_batch(S, prompts, want_logits=True)
+        out[flag] = (lg.copy(), S.back().copy())
+        S.free()
+    assert np.array_equal(out["1"][0], out["0"][0])
+    assert np.array_equal(out["1"][1], out["0"][1])

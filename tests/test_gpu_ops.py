@@ -501,9 +501,10 @@ def test_gemm_multi_equals_single_launches(be, m, k2, bk, monkeypatch):
 @pytest.mark.parametrize("m,n,k", [(300, 2560, 2560), (1030, 384, 640), (257, 200, 10240)])
 def test_gemm_stage_depths_bit_identical(be, m, n, k, monkeypatch):
     """The prefill GEMM with 32 (k_gemm2), 64 and 128 (k_gemm3) k per LDS
-    stage issues the same MFMA sequence per output tile (16 k each, k
-    ascending), so the three give the same bits, int8 and fp16 weights, with
-    a fused epilogue; 64 also agrees with float64 to fp32 rounding."""
+    stage, and the DMA-staged k_gemm4 (fp16 weights), issue the same MFMA
+    sequence per output tile (16 k each, k ascending), so all give the same
+    bits, int8 and fp16 weights, with a fused epilogue; 64 also agrees with
+    float64 to fp32 rounding."""
     rsv = _rsv()
     rng = np.random.default_rng(m + n + k)
     A = rng.standard_normal((m, k)).astype(np.float16)
@@ -514,8 +515,9 @@ def test_gemm_stage_depths_bit_identical(be, m, n, k, monkeypatch):
     h = be.int8(idx, sz)
     bias = be.tensor(rng.standard_normal(n).astype(np.float32))
     got = {}
-    for bk in ("32", "64", "128"):
-        monkeypatch.setenv("RSV_GEMM_BK", bk)
+    for bk in ("32", "64", "128", "dma"):
+        monkeypatch.setenv("RSV_GEMM_BK", "32" if bk == "dma" else bk)
+        monkeypatch.setenv("RSV_GEMM_DMA", "1" if bk == "dma" else "0")
         C16, C8 = be.tensor(n=m * n), be.tensor(n=m * n)
         be.call("rsv_gemm_ex", At, Wt, None, C16, m, n, k, 1, bias, NONE, NONE)
         be.call("rsv_gemm_ex", At, NONE, ctypes.pointer(h), C8, m, n, k, 3, NONE, NONE, NONE)
@@ -523,6 +525,9 @@ def test_gemm_stage_depths_bit_identical(be, m, n, k, monkeypatch):
     for bk in ("64", "128"):
         assert np.array_equal(got[bk][0], got["32"][0]), bk
         assert np.array_equal(got[bk][1], got["32"][1]), bk
+    # the DMA-staged kernel takes fp16 weights only (int8 stays on k_gemm2)
+    assert np.array_equal(got["dma"][0], got["32"][0])
+    assert np.array_equal(got["dma"][1], got["32"][1])
     A64 = A.astype(np.float64)
     ref16 = A64 @ W16.astype(np.float64).T + be.get(bias, n).astype(np.float64)
     assert rel_err(got["64"][0].reshape(m, n), ref16) < 1e-5
