@@ -524,36 +524,38 @@ __global__ __launch_bounds__(256, BKT == 64 ? 3 : 2) void k_gemm3_multi(GemmJobs
 //   - The MFMA sequence (k ascending, 16 per instruction, the same lane to
 //     k mapping) is that of k_gemm2, so the results are bit-identical to it.
 typedef __attribute__((address_space(3))) void *g4_lds_t;
-constexpr int G4_PER = 4;  // copy instructions per wave per stage (A 2, B 2)
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t g4_rsrc(const void *p, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, 0x00020000);
 }
 
-template <int NS>
+// NS stages of BKT (32 or 64) k; a stage row is CPR = BKT/8 chunks, chunk c
+// of row r in slot CPR*r + (c ^ ((r >> SH) & (CPR - 1))), SH = 4 - log2(CPR)
+template <int NS, int BKT>
 __device__ __forceinline__ void gemm4_body(const GemmArgs &g, int m0, int n0, _Float16 *const (&As)[NS],
                                            _Float16 *const (&Bs)[NS]) {
+    constexpr int CPR = BKT / 8, SH = CPR == 4 ? 2 : 1, PW = CPR / 2;  // copies per wave per operand
+    constexpr int PER = 2 * PW;
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
     const __amdgpu_buffer_rsrc_t ra = g4_rsrc(g.a, (uint32_t)((size_t)g.m * g.lda * 2));
     const __amdgpu_buffer_rsrc_t rb = g4_rsrc(g.b, (uint32_t)((size_t)g.n * g.k * 2));
-    // the two slots of each copy instruction of this wave: row and source chunk
-    int a_off[2], b_off[2];
+    int a_off[PW], b_off[PW];
 #pragma unroll
-    for (int t = 0; t < 2; t++) {
-        const int sl = 64 * (2 * wave + t) + lane, row = sl >> 2, c = (sl & 3) ^ ((row >> 2) & 3);
+    for (int t = 0; t < PW; t++) {
+        const int sl = 64 * (PW * wave + t) + lane, row = sl / CPR, c = (sl % CPR) ^ ((row >> SH) & (CPR - 1));
         a_off[t] = ((m0 + row) * g.lda + 8 * c) * 2;
         b_off[t] = ((n0 + row) * g.k + 8 * c) * 2;
     }
-    const int nst = g.k / 32;
+    const int nst = g.k / BKT;
     auto issue = [&](int st, _Float16 *Ad, _Float16 *Bd) {
         const bool live = st < nst;
 #pragma unroll
-        for (int t = 0; t < 2; t++) {
-            const int ka = live ? a_off[t] + 64 * st : 0x7FFFFFF0;
-            const int kb = live ? b_off[t] + 64 * st : 0x7FFFFFF0;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (g4_lds_t)(Ad + (2 * wave + t) * 512), 16, ka, 0, 0, 0);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (g4_lds_t)(Bd + (2 * wave + t) * 512), 16, kb, 0, 0, 0);
+        for (int t = 0; t < PW; t++) {
+            const int ka = live ? a_off[t] + 2 * BKT * st : 0x7FFFFFF0;
+            const int kb = live ? b_off[t] + 2 * BKT * st : 0x7FFFFFF0;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (g4_lds_t)(Ad + (PW * wave + t) * 512), 16, ka, 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (g4_lds_t)(Bd + (PW * wave + t) * 512), 16, kb, 0, 0, 0);
         }
     };
 
@@ -566,18 +568,18 @@ __device__ __forceinline__ void gemm4_body(const GemmArgs &g, int m0, int n0, _F
             for (int e = 0; e < 16; e++) acc[i][j][e] = 0.0f;
     auto compute = [&](const _Float16 *A_, const _Float16 *B_) {
 #pragma unroll
-        for (int st = 0; st < 2; st++) {
+        for (int st = 0; st < BKT / 16; st++) {
             const int c = 2 * st + (lane >> 5);
             half8_t af[2], bf[2];
 #pragma unroll
             for (int i = 0; i < 2; i++) {
                 const int r = wm + i * 32 + (lane & 31);
-                af[i] = *(const half8_t *)(A_ + 8 * (4 * r + (c ^ ((r >> 2) & 3))));
+                af[i] = *(const half8_t *)(A_ + 8 * (CPR * r + (c ^ ((r >> SH) & (CPR - 1)))));
             }
 #pragma unroll
             for (int j = 0; j < 2; j++) {
                 const int r = wn + j * 32 + (lane & 31);
-                bf[j] = *(const half8_t *)(B_ + 8 * (4 * r + (c ^ ((r >> 2) & 3))));
+                bf[j] = *(const half8_t *)(B_ + 8 * (CPR * r + (c ^ ((r >> SH) & (CPR - 1)))));
             }
 #pragma unroll
             for (int i = 0; i < 2; i++)
@@ -595,7 +597,7 @@ __device__ __forceinline__ void gemm4_body(const GemmArgs &g, int m0, int n0, _F
             if (s0 + u >= nst) break;
             // this wave's copies of stage s0 + u are done when at most the
             // NS - 2 later stages' copies are outstanding
-            __builtin_amdgcn_s_waitcnt(((G4_PER * (NS - 2)) & 0xF) | (((G4_PER * (NS - 2)) >> 4) << 14) | (0x7 << 4) |
+            __builtin_amdgcn_s_waitcnt(((PER * (NS - 2)) & 0xF) | (((PER * (NS - 2)) >> 4) << 14) | (0x7 << 4) |
                                        (0xF << 8));
             __builtin_amdgcn_s_barrier();
             issue(s0 + u + NS - 1, As[(u + NS - 1) % NS], Bs[(u + NS - 1) % NS]);
@@ -618,37 +620,46 @@ __device__ __forceinline__ void gemm4_body(const GemmArgs &g, int m0, int n0, _F
 #undef GEMM4_EPI
 }
 
-constexpr int G4_NS = 3;  // LDS stages (48 KB per block: three blocks per CU)
+// one LDS array per stage and operand (unreferenced ones are dropped)
+#define G4_LDS(NS, BKT)                                                                            \
+    __shared__ __attribute__((aligned(16))) _Float16 A0[128 * BKT], A1[128 * BKT], A2[128 * BKT],  \
+        A3[128 * BKT];                                                                             \
+    __shared__ __attribute__((aligned(16))) _Float16 B0[128 * BKT], B1[128 * BKT], B2[128 * BKT],  \
+        B3[128 * BKT];                                                                             \
+    _Float16 *const As4[4] = {A0, A1, A2, A3};                                                     \
+    _Float16 *const Bs4[4] = {B0, B1, B2, B3};                                                     \
+    _Float16 *const(&As)[NS] = *reinterpret_cast<_Float16 *const(*)[NS]>(&As4);                    \
+    _Float16 *const(&Bs)[NS] = *reinterpret_cast<_Float16 *const(*)[NS]>(&Bs4);
 
-#define G4_LDS                                                                                  \
-    __shared__ __attribute__((aligned(16))) _Float16 A0[128 * 32], A1[128 * 32], A2[128 * 32];  \
-    __shared__ __attribute__((aligned(16))) _Float16 B0[128 * 32], B1[128 * 32], B2[128 * 32];  \
-    _Float16 *const As[G4_NS] = {A0, A1, A2};                                                   \
-    _Float16 *const Bs[G4_NS] = {B0, B1, B2};
-
-__global__ __launch_bounds__(256) void k_gemm4(GemmArgs g) {
-    G4_LDS
-    gemm4_body<G4_NS>(g, blockIdx.y * 128, blockIdx.x * BN, As, Bs);
+template <int NS, int BKT>
+__global__ __launch_bounds__(256, NS * BKT <= 96 ? 3 : 2) void k_gemm4(GemmArgs g) {
+    G4_LDS(NS, BKT)
+    gemm4_body<NS, BKT>(g, blockIdx.y * 128, blockIdx.x * BN, As, Bs);
 }
 
-__global__ __launch_bounds__(256) void k_gemm4_multi(GemmJobs jobs) {
-    G4_LDS
+template <int NS, int BKT>
+__global__ __launch_bounds__(256, NS * BKT <= 96 ? 3 : 2) void k_gemm4_multi(GemmJobs jobs) {
+    G4_LDS(NS, BKT)
     const int bid = blockIdx.x;
     int ji = 0;
     while (ji + 1 < jobs.n && bid >= jobs.blk_start[ji + 1]) ji++;
     const GemmArgs &g = jobs.j[ji];
     const int local = bid - jobs.blk_start[ji], nt = (g.n + BN - 1) / BN;
-    gemm4_body<G4_NS>(g, (local / nt) * 128, (local % nt) * BN, As, Bs);
+    gemm4_body<NS, BKT>(g, (local / nt) * 128, (local % nt) * BN, As, Bs);
 }
 #undef G4_LDS
 
 // k_gemm4 takes a job, with RSV_GEMM_DMA=1, when its weights are fp16, k is
 // a multiple of 32 and both operands fit a 32-bit buffer range (measured
 // slower than k_gemm3 on the prefill shapes, so off by default)
-static bool gemm4_ok(const GemmArgs &g) {
+static int gemm4_mode() {
     const char *e = getenv("RSV_GEMM_DMA");
-    if (!(e && e[0] == '1')) return false;
-    return !g.b_i8 && g.k % 32 == 0 && (size_t)g.m * g.lda * 2 < 0x7FFFFFF0ull && (size_t)g.n * g.k * 2 < 0x7FFFFFF0ull;
+    return e ? atoi(e) : 0;
+}
+static bool gemm4_ok(const GemmArgs &g) {
+    const int md = gemm4_mode();
+    if (md < 1 || md > 4) return false;
+    return !g.b_i8 && g.k % (md >= 3 ? 64 : 32) == 0 && (size_t)g.m * g.lda * 2 < 0x7FFFFFF0ull && (size_t)g.n * g.k * 2 < 0x7FFFFFF0ull;
 }
 
 // k per stage of the prefill GEMMs: RSV_GEMM_BK = 32 (k_gemm2, double-
@@ -686,7 +697,12 @@ int launch_gemm_multi(rsv_ctx *ctx, GemmJobs &jobs) {
     bool dma = true;
     for (int i = 0; i < jobs.n; i++) dma &= gemm4_ok(jobs.j[i]);
     if (dma) {
-        hipLaunchKernelGGL(k_gemm4_multi, dim3(total), dim3(256), 0, ctx->stream, jobs);
+        switch (gemm4_mode()) {
+            case 2: hipLaunchKernelGGL((k_gemm4_multi<4, 32>), dim3(total), dim3(256), 0, ctx->stream, jobs); break;
+            case 3: hipLaunchKernelGGL((k_gemm4_multi<2, 64>), dim3(total), dim3(256), 0, ctx->stream, jobs); break;
+            case 4: hipLaunchKernelGGL((k_gemm4_multi<3, 64>), dim3(total), dim3(256), 0, ctx->stream, jobs); break;
+            default: hipLaunchKernelGGL((k_gemm4_multi<3, 32>), dim3(total), dim3(256), 0, ctx->stream, jobs); break;
+        }
         RSV_HIP(hipGetLastError());
         return 0;
     }
@@ -720,7 +736,12 @@ int launch_gemm(rsv_ctx *ctx, const GemmArgs &g) {
         // 128-row tiles: 256-row tiles (one wave per SIMD at 275 registers)
         // measured 1.5x slower on the prefill GEMMs
         if (gemm4_ok(g)) {
-            hipLaunchKernelGGL(k_gemm4, grid, dim3(256), 0, ctx->stream, g);
+            switch (gemm4_mode()) {
+                case 2: hipLaunchKernelGGL((k_gemm4<4, 32>), grid, dim3(256), 0, ctx->stream, g); break;
+                case 3: hipLaunchKernelGGL((k_gemm4<2, 64>), grid, dim3(256), 0, ctx->stream, g); break;
+                case 4: hipLaunchKernelGGL((k_gemm4<3, 64>), grid, dim3(256), 0, ctx->stream, g); break;
+                default: hipLaunchKernelGGL((k_gemm4<3, 32>), grid, dim3(256), 0, ctx->stream, g); break;
+            }
             RSV_HIP(hipGetLastError());
             return 0;
         }

@@ -515,9 +515,9 @@ def test_gemm_stage_depths_bit_identical(be, m, n, k, monkeypatch):
     h = be.int8(idx, sz)
     bias = be.tensor(rng.standard_normal(n).astype(np.float32))
     got = {}
-    for bk in ("32", "64", "128", "dma"):
-        monkeypatch.setenv("RSV_GEMM_BK", "32" if bk == "dma" else bk)
-        monkeypatch.setenv("RSV_GEMM_DMA", "1" if bk == "dma" else "0")
+    for bk in ("32", "64", "128", "dma1", "dma2", "dma3", "dma4"):
+        monkeypatch.setenv("RSV_GEMM_BK", "32" if bk.startswith("dma") else bk)
+        monkeypatch.setenv("RSV_GEMM_DMA", bk[3:] if bk.startswith("dma") else "0")
         C16, C8 = be.tensor(n=m * n), be.tensor(n=m * n)
         be.call("rsv_gemm_ex", At, Wt, None, C16, m, n, k, 1, bias, NONE, NONE)
         be.call("rsv_gemm_ex", At, NONE, ctypes.pointer(h), C8, m, n, k, 3, NONE, NONE, NONE)
@@ -525,9 +525,11 @@ def test_gemm_stage_depths_bit_identical(be, m, n, k, monkeypatch):
     for bk in ("64", "128"):
         assert np.array_equal(got[bk][0], got["32"][0]), bk
         assert np.array_equal(got[bk][1], got["32"][1]), bk
-    # the DMA-staged kernel takes fp16 weights only (int8 stays on k_gemm2)
-    assert np.array_equal(got["dma"][0], got["32"][0])
-    assert np.array_equal(got["dma"][1], got["32"][1])
+    # the DMA-staged kernel (stages x k: 3x32, 4x32, 2x64, 3x64) takes fp16
+    # weights only (int8 stays on k_gemm2)
+    for bk in ("dma1", "dma2", "dma3", "dma4"):
+        assert np.array_equal(got[bk][0], got["32"][0]), bk
+        assert np.array_equal(got[bk][1], got["32"][1]), bk
     A64 = A.astype(np.float64)
     ref16 = A64 @ W16.astype(np.float64).T + be.get(bias, n).astype(np.float64)
     assert rel_err(got["64"][0].reshape(m, n), ref16) < 1e-5
