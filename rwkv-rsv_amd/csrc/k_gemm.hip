@@ -188,12 +188,26 @@ __device__ __forceinline__ void gemm2_epilogue(const GemmArgs &g, const float16_
                                                int wn, int lane) {
     constexpr bool need_b = EPI == GE_BIAS || EPI == GE_WDECAY || EPI == GE_SIGBIAS || EPI == GE_VLERP;
     constexpr bool need_aux = EPI == GE_ADD || EPI == GE_VLERP;
+    constexpr bool need_cur = EPI == GE_VLERP;
     const float scale = EPI == GE_WDECAY ? g.scale[0] : 0.0f;
 #pragma unroll
     for (int j = 0; j < NJ; j++) {
         const int col = n0 + wn + j * 32 + (lane & 31);
         if (col >= g.n) continue;
         const float bias = need_b ? g.bias[col] : 0.0f;
+        // every read operand of the column first: the output may be one of
+        // them (x += ..., v in place), so a load placed after a store would
+        // wait for that store (loads and stores share one counter here)
+        float aux[MI][16], cur[MI][16];
+#pragma unroll
+        for (int i = 0; i < MI; i++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                const int row = m0 + wm + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+                const size_t o = (size_t)row * g.ldc + col;
+                aux[i][e] = need_aux && row < g.m ? g.aux[o] : 0.0f;
+                cur[i][e] = need_cur && row < g.m ? ((const float *)g.c)[o] : 0.0f;
+            }
 #pragma unroll
         for (int i = 0; i < MI; i++) {
 #pragma unroll
@@ -201,9 +215,7 @@ __device__ __forceinline__ void gemm2_epilogue(const GemmArgs &g, const float16_
                 const int row = m0 + wm + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
                 if (row >= g.m) continue;
                 const size_t o = (size_t)row * g.ldc + col;
-                const float aux = need_aux ? g.aux[o] : 0.0f;
-                const float cur = EPI == GE_VLERP ? ((const float *)g.c)[o] : 0.0f;
-                const float v = gemm_epi_val<EPI>(acc[i][j][e], bias, aux, cur, scale);
+                const float v = gemm_epi_val<EPI>(acc[i][j][e], bias, aux[i][e], cur[i][e], scale);
                 if (g.c_f16)
                     ((_Float16 *)g.c)[o] = (_Float16)v;
                 else
