@@ -740,7 +740,7 @@ int launch_gemm(rsv_ctx *ctx, const GemmArgs &g) {
     if (g.epi == GE_WDECAY && !g.scale) return RSV_FAIL("gemm: decay epilogue needs scale");
     if (g.c_f16 && (g.epi == GE_ADD || g.epi == GE_VLERP)) return RSV_FAIL("gemm: in-place epilogues need fp32 C");
     dim3 grid((g.n + BN - 1) / BN, (g.m + BM - 1) / BM);
-    static const int v2 = [] {
+    const int v2 = [] {  // read at each launch, so one process can compare settings
         const char *e = getenv("RSV_GEMM_V2");
         return e ? atoi(e) : 1;
     }();

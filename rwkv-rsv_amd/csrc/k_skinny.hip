@@ -926,7 +926,7 @@ int launch_skinny(rsv_ctx *ctx, SkinnyJobs &jobs, int MB) {
         }
         // both formats share one k_skinny5_mixed launch when every job takes
         // that path (no small-K job, none large enough for k_skinny4)
-        static const int mixed_on = [] {
+        const int mixed_on = [] {  // read at each launch, so one process can compare settings
             const char *e = getenv("RSV_SKINNY_MIXED");
             return e ? atoi(e) : 1;
         }();
@@ -962,7 +962,7 @@ constexpr int SK_KMAX = 16;  // longest k-slice (chunks) of the LDS x slab
 static int launch_v5(rsv_ctx *ctx, SkinnyJobs &jobs, int MB) {
     const int TB = MB <= 32 ? 32 : 64;
     const int cus = ctx->sm_count > 0 ? ctx->sm_count : 256;
-    static const int per_cu = [] {
+    const int per_cu = [] {  // read at each launch, so one process can compare settings
         const char *e = getenv("RSV_SKINNY_BLOCKS_PER_CU");
         return e && atoi(e) > 0 ? atoi(e) : 2;
     }();
@@ -1153,7 +1153,7 @@ static int launch_small(rsv_ctx *ctx, SkinnyJobs &jobs, int MB) {
     const bool i8 = jobs.j[0].fmt == FMT_I8;
     for (int i = 1; i < jobs.n; i++)
         if ((jobs.j[i].fmt == FMT_I8) != i8) return RSV_FAIL("skinny gemm: mixed formats in one tiled launch");
-    static const int one_wave = [] {
+    const int one_wave = [] {  // read at each launch, so one process can compare settings
         const char *e = getenv("RSV_SKINNY_SK1");
         return e ? atoi(e) : 1;
     }();
@@ -1190,7 +1190,7 @@ static int launch_small(rsv_ctx *ctx, SkinnyJobs &jobs, int MB) {
 static int launch_slab(rsv_ctx *ctx, SkinnyJobs &jobs, int MB) {
     if (MB <= 0 || MB > 64) return RSV_FAIL("skinny gemm: batch %d outside 1..64", MB);
     if (jobs.n <= 0 || jobs.n > kMaxJobs) return RSV_FAIL("skinny gemm: bad job count %d", jobs.n);
-    static const int use_v5 = [] {
+    const int use_v5 = [] {  // read at each launch, so one process can compare settings
         const char *e = getenv("RSV_SKINNY_V5");
         return e ? atoi(e) : 1;
     }();
@@ -1214,7 +1214,7 @@ static int launch_slab(rsv_ctx *ctx, SkinnyJobs &jobs, int MB) {
         if (small) return launch_small(ctx, jobs, MB);
         if (!big && ok) return launch_v5(ctx, jobs, MB);
     }
-    static const int max_split = [] {
+    const int max_split = [] {  // read at each launch, so one process can compare settings
         const char *e = getenv("RSV_SKINNY_MAX_SPLIT");
         return e ? atoi(e) : 16;
     }();

@@ -438,3 +438,30 @@ def test_prefill_f16_weight_copies_bit_identical(bundles, kind, monkeypatch):
         S.free()
     assert np.array_equal(out["1"][0], out["0"][0])
     assert np.array_equal(out["1"][1], out["0"][1])
+
+
+@pytest.mark.parametrize("env", ["RSV_SKINNY_V5=0", "RSV_SKINNY_SK1=0", "RSV_SKINNY_MIXED=0", "RSV_SKINNY_MAX_SPLIT=4",
+                                 "RSV_SKINNY_BLOCKS_PER_CU=1", "RSV_GEMM_V2=0", "RSV_WKV_LORA_MM=0"])
+def test_batched_alternative_kernels_agree(bundles, env, monkeypatch):
+    """Each selectable alternative of the batched paths (older skinny GEMM
+    forms, split limits, the first prefill GEMM, the two-launch LoRA-up +
+    WKV7) gives the default's logits and state to fp32 rounding, on a
+    prefill of more than 128 packed rows and batched decode steps."""
+    monkeypatch.setenv("RSV_MEGA", "0")
+    b, _ = bundles["i8"]
+    B = 20
+    prompts = [_prompt(4 + 9 * (i % 4), 500 + i) for i in range(B)]
+    toks = np.array([(7 * i + 3) % SMALL["vocab"] for i in range(B)], np.uint32)
+    out = {}
+    for flag in ("default", env):
+        if flag != "default":
+            name, val = flag.split("=")
+            monkeypatch.setenv(name, val)
+        S = b.create_batch_state(B)
+        _, lp = b.forward_seq_batch(S, prompts, want_logits=True)
+        lg = b.forward_tokens_batch(S, toks)
+        lg2 = b.forward_tokens_batch(S, toks[::-1].copy())
+        out[flag] = (lp.copy(), lg.copy(), lg2.copy(), S.back().copy())
+        S.free()
+    for got, want in zip(out[env], out["default"]):
+        assert rel_rmse(got, want) <= 1e-4
