@@ -195,27 +195,26 @@ __device__ __forceinline__ void gemm2_epilogue(const GemmArgs &g, const float16_
         const int col = n0 + wn + j * 32 + (lane & 31);
         if (col >= g.n) continue;
         const float bias = need_b ? g.bias[col] : 0.0f;
-        // every read operand of the column first: the output may be one of
-        // them (x += ..., v in place), so a load placed after a store would
-        // wait for that store (loads and stores share one counter here)
-        float aux[MI][16], cur[MI][16];
 #pragma unroll
-        for (int i = 0; i < MI; i++)
+        for (int i = 0; i < MI; i++) {
+            // every read operand of the 32 x 32 tile first: the output may be
+            // one of them (x += ..., v in place), so a load placed after a
+            // store would wait for that store (loads and stores share one
+            // counter here)
+            float aux[16], cur[16];
 #pragma unroll
             for (int e = 0; e < 16; e++) {
                 const int row = m0 + wm + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
                 const size_t o = (size_t)row * g.ldc + col;
-                aux[i][e] = need_aux && row < g.m ? g.aux[o] : 0.0f;
-                cur[i][e] = need_cur && row < g.m ? ((const float *)g.c)[o] : 0.0f;
+                aux[e] = need_aux && row < g.m ? g.aux[o] : 0.0f;
+                cur[e] = need_cur && row < g.m ? ((const float *)g.c)[o] : 0.0f;
             }
-#pragma unroll
-        for (int i = 0; i < MI; i++) {
 #pragma unroll
             for (int e = 0; e < 16; e++) {
                 const int row = m0 + wm + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
                 if (row >= g.m) continue;
                 const size_t o = (size_t)row * g.ldc + col;
-                const float v = gemm_epi_val<EPI>(acc[i][j][e], bias, aux[i][e], cur[i][e], scale);
+                const float v = gemm_epi_val<EPI>(acc[i][j][e], bias, aux[e], cur[e], scale);
                 if (g.c_f16)
                     ((_Float16 *)g.c)[o] = (_Float16)v;
                 else
@@ -376,14 +375,14 @@ __global__ __launch_bounds__(256) void k_gemm2_multi(GemmJobs jobs) {
 // stage-to-stage wait is a memory latency, several times a 32-k stage's
 // MFMA work).  Two barriers per stage: all waves are done reading the
 // buffer before it is overwritten.
-template <bool B_I8, int BKT, int NJ>
+template <bool B_I8, int BKT, int NJ, int BMR = 128>
 __device__ __forceinline__ void gemm3_body(const GemmArgs &g, int m0, int n0, _Float16 *As, _Float16 *Bs) {
-    constexpr int MI = 2, LD = BKT + 8, BNJ = 64 * NJ;  // block columns
-    constexpr int PA = 128 * BKT / 8 / 256;   // 16-byte A pieces per thread
+    constexpr int MI = BMR / 64, LD = BKT + 8, BNJ = 64 * NJ;  // block rows BMR, columns BNJ
+    constexpr int PA = BMR * BKT / 8 / 256;   // 16-byte A pieces per thread
     constexpr int KH = BKT * BNJ / 256;       // k per thread of the B loader (256 / BNJ threads per row)
     constexpr int PB = B_I8 ? KH / 16 : KH / 8;  // its 16-byte pieces
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 32 * NJ;
+    const int wm = (wave >> 1) * (BMR / 2), wn = (wave & 1) * 32 * NJ;
     const int lr = tid / (256 / BNJ), lc = (tid % (256 / BNJ)) * KH;
 
     float16_t acc[MI][NJ];
@@ -493,11 +492,11 @@ __device__ __forceinline__ void gemm3_body(const GemmArgs &g, int m0, int n0, _F
 #undef GEMM3_EPI
 }
 
-template <bool B_I8, int BKT>
-__global__ __launch_bounds__(256, BKT == 64 ? 3 : 2) void k_gemm3(GemmArgs g) {
-    __shared__ __attribute__((aligned(16))) _Float16 As[128 * (BKT + 8)];
+template <bool B_I8, int BKT, int BMR = 128>
+__global__ __launch_bounds__(256, BKT == 64 && BMR == 128 ? 3 : 2) void k_gemm3(GemmArgs g) {
+    __shared__ __attribute__((aligned(16))) _Float16 As[BMR * (BKT + 8)];
     __shared__ __attribute__((aligned(16))) _Float16 Bs[BN * (BKT + 8)];
-    gemm3_body<B_I8, BKT, 2>(g, blockIdx.y * 128, blockIdx.x * BN, As, Bs);
+    gemm3_body<B_I8, BKT, 2, BMR>(g, blockIdx.y * BMR, blockIdx.x * BN, As, Bs);
 }
 
 template <int BKT>
@@ -763,7 +762,14 @@ int launch_gemm(rsv_ctx *ctx, const GemmArgs &g) {
             if (g.b_i8) hipLaunchKernelGGL((k_gemm3<true, 128>), grid, dim3(256), 0, ctx->stream, g);
             else hipLaunchKernelGGL((k_gemm3<false, 128>), grid, dim3(256), 0, ctx->stream, g);
         } else if (bk == 64) {
-            if (g.b_i8) hipLaunchKernelGGL((k_gemm3<true, 64>), grid, dim3(256), 0, ctx->stream, g);
+            // 256-row blocks (128 x 64 per wave: 0.75 LDS fragment reads per
+            // MFMA instead of 1) with RSV_GEMM_BM=256
+            const char *bme = getenv("RSV_GEMM_BM");
+            if (bme && atoi(bme) == 256) {
+                const dim3 g2((g.n + BN - 1) / BN, (g.m + 255) / 256);
+                if (g.b_i8) hipLaunchKernelGGL((k_gemm3<true, 64, 256>), g2, dim3(256), 0, ctx->stream, g);
+                else hipLaunchKernelGGL((k_gemm3<false, 64, 256>), g2, dim3(256), 0, ctx->stream, g);
+            } else if (g.b_i8) hipLaunchKernelGGL((k_gemm3<true, 64>), grid, dim3(256), 0, ctx->stream, g);
             else hipLaunchKernelGGL((k_gemm3<false, 64>), grid, dim3(256), 0, ctx->stream, g);
         } else if (g.b_i8) hipLaunchKernelGGL((k_gemm2<true, 128>), grid, dim3(256), 0, ctx->stream, g);
         else hipLaunchKernelGGL((k_gemm2<false, 128>), grid, dim3(256), 0, ctx->stream, g);

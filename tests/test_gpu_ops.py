@@ -515,14 +515,15 @@ def test_gemm_stage_depths_bit_identical(be, m, n, k, monkeypatch):
     h = be.int8(idx, sz)
     bias = be.tensor(rng.standard_normal(n).astype(np.float32))
     got = {}
-    for bk in ("32", "64", "128", "dma1", "dma2", "dma3", "dma4"):
-        monkeypatch.setenv("RSV_GEMM_BK", "32" if bk.startswith("dma") else bk)
+    for bk in ("32", "64", "128", "dma1", "dma2", "dma3", "dma4", "bm256"):
+        monkeypatch.setenv("RSV_GEMM_BK", "32" if bk.startswith("dma") else "64" if bk == "bm256" else bk)
         monkeypatch.setenv("RSV_GEMM_DMA", bk[3:] if bk.startswith("dma") else "0")
+        monkeypatch.setenv("RSV_GEMM_BM", "256" if bk == "bm256" else "128")
         C16, C8 = be.tensor(n=m * n), be.tensor(n=m * n)
         be.call("rsv_gemm_ex", At, Wt, None, C16, m, n, k, 1, bias, NONE, NONE)
         be.call("rsv_gemm_ex", At, NONE, ctypes.pointer(h), C8, m, n, k, 3, NONE, NONE, NONE)
         got[bk] = (be.get(C16, m * n), be.get(C8, m * n))
-    for bk in ("64", "128"):
+    for bk in ("64", "128", "bm256"):
         assert np.array_equal(got[bk][0], got["32"][0]), bk
         assert np.array_equal(got[bk][1], got["32"][1]), bk
     # the DMA-staged kernel (stages x k: 3x32, 4x32, 2x64, 3x64) takes fp16
