@@ -377,7 +377,7 @@ int rsv_wkv7_decode_ex(rsv_ctx *ctx, uint32_t s, uint32_t k, uint32_t k_k, uint3
                        uint32_t y_norm, uint32_t g, uint32_t yg_f16, uint64_t h, uint64_t n, float eps,
                        float gn_eps, uint64_t batch);
 
-/* ---- fused LoRA-up chain + WKV7 step for small batches (no reference
+/* ---- fused LoRA-up chain + WKV7 step (no reference
  * counterpart; it composes gemv_lowrank_chain4, backend.rs:309-333, and
  * fuse_ka_dplr_norm, backend.rs:223-243, into one launch per layer).
  * From the stage-1 outputs r, k, v [batch, C] and the LoRA-up inputs
@@ -387,7 +387,11 @@ int rsv_wkv7_decode_ex(rsv_ctx *ctx, uint32_t s, uint32_t k, uint32_t k_k, uint3
  * g = sigmoid(g_mid).G2^T; then the WKV7 step on state [batch, H, 64, 64]
  * (updated in place) and yg = (GroupNorm(y) + bonus) * g, the att.output
  * operand.  side_src [batch, C] is copied to side_dst when both are given
- * (ids 0xFFFFFFFF: none).  Each rank must be a multiple of 32 in 32..256. */
+ * (ids 0xFFFFFFFF: none).  Each rank must be a multiple of 32 in 32..256.
+ * With f16_io, batches of 16 and more, and ranks summing to at most 512,
+ * the launch takes 4 sessions per block (the head's LoRA-up rows read once
+ * per block, the dots on matrix cores); otherwise one block per (head,
+ * session).  Results agree to fp32 rounding. */
 typedef struct rsv_wkv_lora {
     uint32_t state, r, k, v, v_first;
     uint32_t w_mid, a_mid, v_mid, g_mid; /* F32 [batch, rank] */
