@@ -147,7 +147,8 @@ def main():
     ap.add_argument("--no-serve", action="store_true")
     ap.add_argument("--serve-decode", type=int, default=256,
                     help="tokens sampled per session in the configs[4] ragged-serving leg")
-    ap.add_argument("--cpu-tokens", type=int, default=4)
+    ap.add_argument("--cpu-tokens", type=int, default=24,
+                    help="decode tokens of the CPU-baseline sample (about 14 s of one core; at most 28)")
     ap.add_argument("--cache", default=os.environ.get("RSV_BENCH_CACHE", "/tmp"))
     ap.add_argument("--kernel-only", action="store_true",
                     help="run only the dominant-kernel leg (for rocprofv3 summaries of that kernel)")
@@ -277,6 +278,8 @@ def main():
         st = m.init_state()
         m.forward(prompt[:4], st)
         tt = time.perf_counter()
+        if args.cpu_tokens > len(prompt) - 4:
+            sys.exit(f"--cpu-tokens {args.cpu_tokens}: the sample prompt has {len(prompt) - 4} tokens after its prefix")
         for i in range(args.cpu_tokens):
             m.forward([int(prompt[4 + i])], st)
         cdt = time.perf_counter() - tt
