@@ -63,12 +63,19 @@ def lib():
         L.orc_sample.argtypes = [f32p, ctypes.c_int64, ctypes.c_float, ctypes.c_uint32, ctypes.c_float,
                                  ctypes.c_uint32, ctypes.c_float, ctypes.c_float, ctypes.c_float, u32p,
                                  ctypes.c_uint32, f32p]
+        L.orc_set_threads.argtypes = [ctypes.c_int]
         L.orc_nfields.restype = ctypes.c_int
         L.orc_state_len.restype = ctypes.c_int64
         L.orc_forward.argtypes = [ctypes.c_void_p, u32p, ctypes.c_int64, f32p, f32p]
         assert L.orc_nfields() == len(FIELDS)
         _lib = L
     return _lib
+
+
+def set_threads(n):
+    """Splits the oracle's matvec columns over n threads (bit-identical to one
+    thread; a checker speed-up for the 3B tests).  The CPU baseline uses 1."""
+    lib().orc_set_threads(int(n))
 
 
 def fp(a):

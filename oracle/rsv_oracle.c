@@ -26,6 +26,7 @@
  *   orc_u01              MurmurHash3 fmix32 closed form (published finaliser)
  */
 #include <math.h>
+#include <pthread.h>
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
@@ -136,13 +137,48 @@ static void lerp(const float *x, const float *y, const float *w, int64_t n, floa
 static float sigmoidf_(float v) { return 1.0f / (1.0f + expf(-v)); } /* model.rs:662-664 */
 
 /* model.rs:700-713: y = x @ W, W [inp, out] row-major, i-outer with zero skip */
-void orc_matvec(const float *x, const float *w, int64_t inp, int64_t out, float *y) {
-    for (int64_t j = 0; j < out; j++) y[j] = 0.0f;
+static void matvec_cols(const float *x, const float *w, int64_t inp, int64_t out, int64_t j0, int64_t j1,
+                        float *y) {
+    for (int64_t j = j0; j < j1; j++) y[j] = 0.0f;
     for (int64_t i = 0; i < inp; i++) {
         float xi = x[i];
         if (xi == 0.0f) continue;
         const float *row = w + i * out;
-        for (int64_t j = 0; j < out; j++) y[j] += xi * row[j];
+        for (int64_t j = j0; j < j1; j++) y[j] += xi * row[j];
+    }
+}
+
+/* Checker-side speed-up only: with orc_set_threads(n > 1) the output columns
+ * are split over n threads.  Each y[j] is still accumulated over i in the
+ * same order with the same zero skip, so results are bit-identical to the
+ * single-threaded loop (tests/test_oracle.py checks this).  The CPU baseline
+ * keeps the default of 1 thread, the reference's own threading. */
+static int orc_threads = 1;
+void orc_set_threads(int n) { orc_threads = n < 1 ? 1 : (n > 64 ? 64 : n); }
+
+struct mv_part { const float *x, *w; int64_t inp, out, j0, j1; float *y; };
+static void *mv_run(void *p) {
+    struct mv_part *a = (struct mv_part *)p;
+    matvec_cols(a->x, a->w, a->inp, a->out, a->j0, a->j1, a->y);
+    return NULL;
+}
+
+void orc_matvec(const float *x, const float *w, int64_t inp, int64_t out, float *y) {
+    int nt = orc_threads;
+    if (nt <= 1 || out < 1024) { matvec_cols(x, w, inp, out, 0, out, y); return; }
+    pthread_t th[64];
+    struct mv_part parts[64];
+    int64_t per = ((out + nt - 1) / nt + 15) & ~(int64_t)15;
+    int n = 0;
+    for (int64_t j0 = 0; j0 < out; j0 += per, n++) {
+        parts[n] = (struct mv_part){x, w, inp, out, j0, j0 + per < out ? j0 + per : out, y};
+    }
+    int started[64] = {0};
+    for (int t = 1; t < n; t++) started[t] = pthread_create(&th[t], NULL, mv_run, &parts[t]) == 0;
+    mv_run(&parts[0]);
+    for (int t = 1; t < n; t++) {
+        if (started[t]) pthread_join(th[t], NULL);
+        else mv_run(&parts[t]);
     }
 }
 

@@ -64,3 +64,22 @@ def rel_rmse(a, b):
     a = np.asarray(a, np.float64)
     b = np.asarray(b, np.float64)
     return float(np.sqrt(np.mean((a - b) ** 2)) / max(np.std(b), 1e-30))
+
+
+def _cache_dir():
+    return os.environ.get("RSV_BENCH_CACHE", "/tmp")
+
+
+def three_b_model(kind):
+    """The configs[3] 3B-shape model files (seed 1), cached like bench.py's:
+    "i8" = int8 per-row-scale linears + int8 head (fp32 embedding in the file);
+    "i8_f16" = int8 linears + fp16 embedding and fp16 head (the variant)."""
+    import synth
+    name, kw = {"i8": ("rsv_3b_i8_seed1.st", dict(linear="i8", head="i8")),
+                "i8_f16": ("rsv_3b_i8_f16head_seed1.st", dict(linear="i8", head="f16", emb="f16"))}[kind]
+    path = os.path.join(_cache_dir(), name)
+    if not os.path.exists(path):
+        tmp = path + ".tmp%d" % os.getpid()
+        synth.write_model(tmp, synth.THREE_B, seed=1, **kw)
+        os.replace(tmp, path)
+    return path

@@ -1,0 +1,222 @@
+"""Accuracy at the benchmarked shape: the configs[3] 3B-shape model (32
+layers, d_model 2560, 40 heads x 64, FFN 10240, vocab 65536, LoRA
+96/96/64/256, seed 1) through the HIP path against the CPU fp32 oracle.
+
+These run exactly the kernels the bench times at B=1 and B=64 (the one-shot
+B=1 GEMVs, the fused LoRA-up + WKV7 launches, the batched MFMA GEMMs with
+3B K-slices, the prefill GEMM on 4096-row chunks) and hold them to the
+north_star bounds, the same criteria as the reference's TOP1_REF /
+COMPARE_LOGITS checks (main.rs):
+
+- logits RMSE <= 1e-2 x logit std, at every checked step;
+- teacher-forced top-1 agreement >= 98% for int8 linears + int8 head, and
+  >= 99% for the fp16 embedding/head variant.  Teacher forcing: the oracle
+  is fed the tokens the GPU chose, and its argmax at every step is compared
+  with the GPU's choice.
+
+The oracle splits its matvec columns over threads (bit-identical to one
+thread) so that the 3B checks take seconds per token, not half a second.
+"""
+import os
+import time
+
+import numpy as np
+import pytest
+
+import oracle as orc
+from conftest import rel_rmse, three_b_model
+
+pytestmark = [pytest.mark.gpu, pytest.mark.timeout(900)]
+
+RMSE_BOUND = 1e-2
+BAR = {"i8": 0.98, "i8_f16": 0.99}
+
+
+def log(*a):
+    print("[3b]", *a, flush=True)
+
+
+def _prompt(n, seed):
+    import synth
+    return synth.prompt(synth.THREE_B, n, seed=seed)
+
+
+@pytest.fixture(scope="module", params=["i8", "i8_f16"])
+def model3b(request):
+    import rsv
+    kind = request.param
+    t = time.time()
+    path = three_b_model(kind)
+    log(kind, "model file ready", f"{time.time() - t:.1f}s")
+    b = rsv.ModelBuilder(path).build()
+    orc.set_threads(min(16, os.cpu_count() or 1))
+    t = time.time()
+    m = orc.Model(path)
+    log(kind, "oracle built", f"{time.time() - t:.1f}s")
+    yield kind, b, m
+    b.close()
+    orc.set_threads(1)
+    del m
+
+
+def _teacher_forced(m, st, first, toks):
+    """Feeds `first` then toks[:-1] to the oracle; returns its per-step logits."""
+    out = []
+    prev = int(first)
+    for t in toks:
+        out.append(m.forward([prev], st))
+        prev = int(t)
+    return out
+
+
+def test_3b_b1_prefill_and_selfloop(model3b):
+    """B=1: prompt logits and state after infer_seq, then a 64-token argmax
+    self-loop (the graph-replayed step the bench times) teacher-forced
+    against the oracle, with the GPU's per-token logits along the same path
+    held to the RMSE bound at every step."""
+    kind, b, m = model3b
+    p = _prompt(16, 1)
+    b.reset()
+    lg = b.infer_seq(p[:-1])
+    st = m.init_state()
+    want = m.forward(p[:-1], st)
+    e = rel_rmse(lg, want)
+    es = rel_rmse(b.state_back(), st)
+    log(kind, f"prefill logits rel rmse {e:.2e}, state {es:.2e}")
+    assert e <= RMSE_BOUND and es <= RMSE_BOUND
+    st_pre = st.copy()
+    n = 64
+    toks = b.infer_argmax_selfloop(int(p[-1]), n)
+    t = time.time()
+    olg = _teacher_forced(m, st, p[-1], toks)
+    log(kind, f"oracle {n} tokens in {time.time() - t:.1f}s")
+    agree = sum(int(orc.argmax(o) == toks[i]) for i, o in enumerate(olg))
+    log(kind, f"B=1 teacher-forced top-1 {agree}/{n}")
+    assert agree / n >= BAR[kind], f"top-1 agreement {agree}/{n}"
+    # the per-token path (one decode step per call) along the same tokens:
+    # logits within the bound at every step, argmax equal to the self-loop's
+    b.reset()
+    b.infer_seq(p[:-1])
+    prev = int(p[-1])
+    worst = 0.0
+    for i in range(n):
+        g = b.infer_tokens([prev])
+        worst = max(worst, rel_rmse(g, olg[i]))
+        assert int(np.argmax(g)) == int(toks[i]) or g[int(toks[i])] == g.max(), i
+        prev = int(toks[i])
+    log(kind, f"B=1 worst per-step logits rel rmse {worst:.2e}")
+    assert worst <= RMSE_BOUND
+    assert rel_rmse(b.state_back(), st) <= RMSE_BOUND
+    del st_pre
+
+
+def test_3b_b64_prefill_and_selfloop(model3b):
+    """B=64: 64 sessions prefilled as one packed batch (512 rows: the prefill
+    GEMM path), then a 24-step batched argmax self-loop (the B>=16 MFMA
+    decode the bench times).  Sessions 0, 31 and 63 are checked against the
+    oracle: prompt logits and teacher-forced top-1."""
+    kind, b, m = model3b
+    B, plen, n = 64, 8, 24
+    prompts = [_prompt(plen, 100 + i) for i in range(B)]
+    S = b.create_batch_state(B)
+    try:
+        seeds, lg = b.forward_seq_batch(S, [q[:-1] for q in prompts], want_logits=True)
+        seeds = np.array([int(q[-1]) for q in prompts], np.uint32)
+        out = b.argmax_selfloop_batch(S, seeds, n)
+    finally:
+        S.free()
+    agree = total = 0
+    for s in (0, 31, 63):
+        st = m.init_state()
+        want = m.forward(prompts[s][:-1], st)
+        e = rel_rmse(lg[s], want)
+        log(kind, f"B=64 session {s}: prompt logits rel rmse {e:.2e}")
+        assert e <= RMSE_BOUND, s
+        olg = _teacher_forced(m, st, seeds[s], out[s])
+        a = sum(int(orc.argmax(o) == out[s][i]) for i, o in enumerate(olg))
+        log(kind, f"B=64 session {s}: teacher-forced top-1 {a}/{n}")
+        agree += a
+        total += n
+    assert agree / total >= BAR[kind], f"top-1 agreement {agree}/{total}"
+
+
+def _serve_vs_single(b, m, kind, sp, check):
+    lens = [5, 300, 37, 700, 64, 129]
+    prompts = [_prompt(L, 200 + i) for i, L in enumerate(lens)]
+    seeds = [3, 5, 7, 11, 13, 17]
+    D = 6
+    S = b.create_batch_state(len(lens))
+    try:
+        toks, steps = b.serve_ragged(S, prompts, D, sp, seeds, budget=512)
+    finally:
+        S.free()
+    assert sum(s["prefill_tokens"] for s in steps) == sum(lens)
+    assert sum(s["sampled"] for s in steps) == len(lens) * D
+    assert any(s["prefill_tokens"] and s["decode_tokens"] for s in steps)
+    res = []
+    for q, p in enumerate(prompts):
+        b.reset()
+        lg = b.infer_seq(p)
+        if q == 0:
+            st = m.init_state()
+            e = rel_rmse(lg, m.forward(p, st))
+            log(kind, f"serve: session 0 prompt logits rel rmse {e:.2e}")
+            assert e <= RMSE_BOUND
+        prev = None
+        for k in range(D):
+            if k:
+                lg = b.infer_seq([prev])
+            res.append(check(q, k, lg, int(toks[q, k]), seeds[q] + k))
+            prev = int(toks[q, k])
+    return res
+
+
+def test_3b_serve_ragged_greedy_matches_per_session(model3b):
+    """configs[4] at the 3B shape, scaled down: six sessions with prompts of
+    5..700 tokens served by the ragged scheduler with a 512-token budget
+    (prompts split across steps and sharing steps with decode tokens),
+    drawn by the GPU sampler with top_k = 1.  Every token equals the argmax
+    of the logits of that session run alone (prompt as one prefill, then one
+    token at a time): the schedule, the packing and the slot bookkeeping
+    change no session's tokens.  Session 0's prompt logits are also checked
+    against the oracle."""
+    import rsv
+    kind, b, m = model3b
+    sp = rsv.SamplerParams(temperature=1.0, top_k=1, top_p=1.0)
+
+    def check(q, k, lg, got, seed):
+        return got == int(np.argmax(lg)) or lg[got] == lg.max()
+
+    res = _serve_vs_single(b, m, kind, sp, check)
+    log(kind, f"serve greedy: packed vs per-session {sum(res)}/{len(res)}")
+    assert all(res), res
+
+
+def test_3b_serve_ragged_top_p_matches_per_session(model3b):
+    """The same schedule with the configs[4] sampler (T = 1, top_p = 0.9,
+    seeded).  With near-flat random-init logits the 0.9 nucleus always hits
+    the 512-candidate cap, and the draw scans the candidates in token order:
+    a logit difference at fp16-rounding level between the packed run and
+    the single-session run can move the draw to the next candidate in token
+    order, never further.  So every packed draw must be the oracle sampler's
+    draw on the single-session logits, or its neighbour in the token-ordered
+    top-512 set; and at least 3/4 of the draws must be exact."""
+    import rsv
+    kind, b, m = model3b
+    sp = rsv.SamplerParams(temperature=1.0, top_k=0, top_p=0.9)
+
+    def check(q, k, lg, got, seed):
+        want = orc.sample(lg, sp.temperature, sp.top_k, sp.top_p, seed)
+        if want == got:
+            return 2
+        cand = np.sort(np.argsort(-lg.astype(np.float64), kind="stable")[:512])
+        pos = {int(t): i for i, t in enumerate(cand)}
+        ok = got in pos and want in pos and abs(pos[got] - pos[want]) <= 1
+        log(kind, f"serve top-p q={q} k={k}: packed {got}, single-session {want}, neighbours {ok}")
+        return 1 if ok else 0
+
+    res = _serve_vs_single(b, m, kind, sp, check)
+    exact = sum(r == 2 for r in res)
+    log(kind, f"serve top-p: exact {exact}/{len(res)}, neighbour {sum(r == 1 for r in res)}")
+    assert all(r > 0 for r in res)
+    assert exact >= 0.75 * len(res)

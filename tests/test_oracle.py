@@ -117,6 +117,23 @@ def test_matvec_zero_skip_and_orientation():
     assert np.allclose(orc.matvec(x, W), x.astype(np.float64) @ W.astype(np.float64), rtol=1e-4, atol=1e-4)
 
 
+def test_matvec_threads_bit_identical():
+    """The checker's threaded matvec (column split) gives the same bits as one
+    thread, including the zero skip and a column count that is not a
+    multiple of the split."""
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal(257).astype(np.float32)
+    x[::5] = 0.0
+    W = rng.standard_normal((257, 5003)).astype(np.float32)
+    one = orc.matvec(x, W)
+    try:
+        for n in (2, 3, 16):
+            orc.set_threads(n)
+            assert np.array_equal(orc.matvec(x, W).view(np.uint32), one.view(np.uint32)), n
+    finally:
+        orc.set_threads(1)
+
+
 def test_l2_norm_groups():
     rng = np.random.default_rng(4)
     x = rng.standard_normal(128).astype(np.float32)
