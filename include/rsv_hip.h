@@ -406,46 +406,6 @@ typedef struct rsv_wkv_lora {
 } rsv_wkv_lora;
 int rsv_wkv7_lora_decode(rsv_ctx *ctx, const rsv_wkv_lora *op, uint64_t batch);
 
-/* ---- persistent single-session decode step (no reference counterpart:
- * the reference decodes one token as a sequence of trait ops,
- * gpu_model.rs:1879-1913 + 2060-2392).  One launch runs the embedding row,
- * every layer, ln_out, the head and the argmax of one session, with one
- * workgroup per CU and grid barriers between the phases of a layer.
- * Requires int8 receptance/key/value/output/ffn weights, fp16 LoRA,
- * head_size 64, n_embd a multiple of 256 up to 4096, LoRA ranks multiples of
- * 32; rsv_decode_mega_build fails with a message otherwise.
- *
- * rsv_decode_mega_build binds the weights and one session's state tensors
- * (tmix_x/cmix_x [C] and rnn [H*64*64] per layer, v_first [C]).
- * rsv_decode_mega: token_in (U32 [1]) -> every layer (state updated in
- * place) -> token_out (U32 [1], argmax, smallest index among equal maxima);
- * logits (F32 [vocab]) may be 0xFFFFFFFF.  Enqueue only (graph-capturable).
- * rsv_decode_mega_status synchronises and reports whether a launch gave up
- * at a grid barrier (its results are then invalid). */
-typedef struct rsv_mega_layer {
-    uint32_t ln1_w, ln1_b, ln2_w, ln2_b, lnx_w, lnx_b;
-    uint32_t x_r, x_w, x_k, x_v, x_a, x_g, ffn_x_k;
-    uint32_t w0, a0, v0, r_k, k_k, k_a;
-    uint32_t w1, a1, v1, g1; /* F16 [mid, C] */
-    uint32_t w2, a2, v2, g2; /* F16 [C, mid] */
-    rsv_int8 receptance, key, value, output, ffn_key, ffn_value;
-    uint32_t tmix_x, cmix_x, rnn; /* this layer's state of the session */
-} rsv_mega_layer;
-typedef struct rsv_mega_model {
-    uint64_t n_layer, n_embd, n_head, ffn, vocab;
-    uint64_t w_mid, a_mid, v_mid, g_mid;
-    uint32_t emb; /* F32 [vocab, C]: LN0 of the embedding */
-    uint32_t ln_out_w, ln_out_b;
-    uint32_t head_w16; /* F16 [vocab, C], or 0xFFFFFFFF for the int8 head */
-    rsv_int8 head;
-    uint32_t scale_w; /* F32 [1]: the decay scale -exp(-0.5) */
-    uint32_t v_first;
-    float ln_eps, l2_eps, gn_eps;
-} rsv_mega_model;
-int rsv_decode_mega_build(rsv_ctx *ctx, const rsv_mega_model *model, const rsv_mega_layer *layers);
-int rsv_decode_mega(rsv_ctx *ctx, uint32_t token_in, uint32_t token_out, uint32_t logits);
-int rsv_decode_mega_status(rsv_ctx *ctx, int *aborted);
-
 /* ---- profiling hooks (backend.rs:67-70); kernel timing is done with rocprofv3 */
 int rsv_clear_kernel_prof(rsv_ctx *ctx);
 int rsv_dump_kernel_prof(rsv_ctx *ctx);

@@ -7,6 +7,7 @@
 #include <cmath>
 #include <cstring>
 #include <mutex>
+#include <string>
 #include <vector>
 
 #include "rsv_common.h"
@@ -129,13 +130,6 @@ int rsv_create(int device, rsv_ctx **out) {
         delete ctx;
         return RSV_FAIL("rsv_create: counter allocation failed");
     }
-    if (hipMalloc(&ctx->mix_buf, (size_t)kMaxJobs * kMixMaxK * 4) != hipSuccess) {
-        hipFree(ctx->sparse_cnt);
-        hipFree(ctx->skinny_ws);
-        hipStreamDestroy(ctx->stream);
-        delete ctx;
-        return RSV_FAIL("rsv_create: LN-mix buffer allocation failed");
-    }
     *out = ctx;
     return 0;
 }
@@ -152,9 +146,7 @@ int rsv_destroy(rsv_ctx *ctx) {
     if (ctx->hist_dev) hipFree(ctx->hist_dev);
     if (ctx->sample_work) hipFree(ctx->sample_work);
     if (ctx->skinny_ws) hipFree(ctx->skinny_ws);
-    if (ctx->mix_buf) hipFree(ctx->mix_buf);
     if (ctx->sparse_cnt) hipFree(ctx->sparse_cnt);
-    mega_free(ctx);
     hipStreamDestroy(ctx->stream);
     delete ctx;
     return 0;
@@ -395,120 +387,6 @@ int rsv_wkv7_lora_decode(rsv_ctx *ctx, const rsv_wkv_lora *op, uint64_t batch) {
         a.side_dst = (float *)p;
     }
     return launch_wkv7_lora(ctx, a, (int)B);
-}
-
-// ---------------------------------------------- persistent decode step
-static int f32v(rsv_ctx *ctx, uint32_t id, uint64_t n, const float **p, const char *what) {
-    void *v = nullptr;
-    if (opnd(ctx, id, RSV_F32, n, &v, what)) return -1;
-    *p = (const float *)v;
-    return 0;
-}
-static int f16v(rsv_ctx *ctx, uint32_t id, uint64_t n, const _Float16 **p, const char *what) {
-    void *v = nullptr;
-    if (opnd(ctx, id, RSV_F16, n, &v, what)) return -1;
-    *p = (const _Float16 *)v;
-    return 0;
-}
-
-int rsv_decode_mega_build(rsv_ctx *ctx, const rsv_mega_model *mm, const rsv_mega_layer *layers) {
-    CHECK_CTX();
-    if (!mm || !layers) return RSV_FAIL("decode_mega_build: null argument");
-    if (ctx->capturing || ctx->prefill_capturing) return RSV_FAIL("decode_mega_build: not allowed during capture");
-    const uint64_t C = mm->n_embd, F = mm->ffn, H = mm->n_head, V = mm->vocab, NL = mm->n_layer;
-    if (NL == 0 || C == 0 || H * 64 != C || F == 0 || V == 0 || C > (1u << 20) || F > (1u << 20) || V > (1u << 30))
-        return RSV_FAIL("decode_mega_build: bad shape (layers %llu, C %llu, H %llu, F %llu, V %llu)",
-                        (unsigned long long)NL, (unsigned long long)C, (unsigned long long)H, (unsigned long long)F,
-                        (unsigned long long)V);
-    const uint64_t mids[4] = {mm->w_mid, mm->a_mid, mm->v_mid, mm->g_mid};
-    MegaModelDev m{};
-    m.n_layer = (int)NL;
-    m.C = (int)C;
-    m.F = (int)F;
-    m.H = (int)H;
-    m.V = (int)V;
-    for (int q = 0; q < 4; q++) {
-        if (mids[q] == 0 || mids[q] > 4096) return RSV_FAIL("decode_mega_build: LoRA rank %llu", (unsigned long long)mids[q]);
-        m.mid[q] = (int)mids[q];
-    }
-    if (f32v(ctx, mm->emb, V * C, &m.emb, "mega emb") || f32v(ctx, mm->ln_out_w, C, &m.lno_w, "mega ln_out.w") ||
-        f32v(ctx, mm->ln_out_b, C, &m.lno_b, "mega ln_out.b") || f32v(ctx, mm->scale_w, 1, &m.scale_w, "mega scale_w"))
-        return -1;
-    {
-        const float *vf;
-        if (f32v(ctx, mm->v_first, C, &vf, "mega v_first")) return -1;
-        m.v_first = (float *)vf;
-    }
-    if (mm->head_w16 != 0xFFFFFFFFu) {
-        const _Float16 *h16;
-        if (f16v(ctx, mm->head_w16, V * C, &h16, "mega head")) return -1;
-        m.head = h16;
-        m.head_sz = nullptr;
-        m.head_i8 = 0;
-    } else {
-        const uint32_t *ix, *sz;
-        if (int8_operands(ctx, &mm->head, V, C, &ix, &sz, "mega head")) return -1;
-        m.head = ix;
-        m.head_sz = sz;
-        m.head_i8 = 1;
-    }
-    m.ln_eps = mm->ln_eps;
-    m.l2_eps = mm->l2_eps;
-    m.gn_eps = mm->gn_eps;
-    std::vector<MegaLayerDev> L(NL);
-    for (uint64_t i = 0; i < NL; i++) {
-        const rsv_mega_layer &s = layers[i];
-        MegaLayerDev &d = L[i];
-        const uint32_t vec_ids[19] = {s.ln1_w, s.ln1_b, s.ln2_w, s.ln2_b, s.lnx_w, s.lnx_b, s.x_r, s.x_w, s.x_k, s.x_v,
-                                      s.x_a, s.x_g, s.ffn_x_k, s.w0, s.a0, s.v0, s.r_k, s.k_k, s.k_a};
-        const float **vec_dst[19] = {&d.ln1_w, &d.ln1_b, &d.ln2_w, &d.ln2_b, &d.lnx_w, &d.lnx_b, &d.x_r,
-                                     &d.x_w, &d.x_k, &d.x_v, &d.x_a, &d.x_g, &d.ffn_x_k, &d.w0,
-                                     &d.a0, &d.v0, &d.r_k, &d.k_k, &d.k_a};
-        for (int q = 0; q < 19; q++)
-            if (f32v(ctx, vec_ids[q], C, vec_dst[q], "mega layer vector")) return -1;
-        const uint32_t dn[4] = {s.w1, s.a1, s.v1, s.g1}, up[4] = {s.w2, s.a2, s.v2, s.g2};
-        for (int q = 0; q < 4; q++)
-            if (f16v(ctx, dn[q], mids[q] * C, &d.down[q], "mega LoRA down") ||
-                f16v(ctx, up[q], mids[q] * C, &d.up[q], "mega LoRA up"))
-                return -1;
-        const rsv_int8 *lin[6] = {&s.receptance, &s.key, &s.value, &s.output, &s.ffn_key, &s.ffn_value};
-        const uint64_t lm[6] = {C, C, C, C, F, C}, lk[6] = {C, C, C, C, C, F};
-        for (int q = 0; q < 6; q++) {
-            const uint32_t *ix, *sz;
-            if (int8_operands(ctx, lin[q], lm[q], lk[q], &ix, &sz, "mega linear")) return -1;
-            d.idx[q] = (const uint8_t *)ix;
-            d.sz[q] = sz;
-        }
-        const float *tm, *cm, *rn;
-        if (f32v(ctx, s.tmix_x, C, &tm, "mega tmix_x") || f32v(ctx, s.cmix_x, C, &cm, "mega cmix_x") ||
-            f32v(ctx, s.rnn, H * 4096, &rn, "mega rnn"))
-            return -1;
-        d.tmix = (float *)tm;
-        d.cmix = (float *)cm;
-        d.rnn = (float *)rn;
-    }
-    return mega_build(ctx, m, L);
-}
-
-int rsv_decode_mega(rsv_ctx *ctx, uint32_t token_in, uint32_t token_out, uint32_t logits) {
-    CHECK_CTX();
-    if (!ctx->mega) return RSV_FAIL("decode_mega: rsv_decode_mega_build has not succeeded");
-    OPND(ti, token_in, RSV_U32, 1, "mega token_in");
-    OPND(to, token_out, RSV_U32, 1, "mega token_out");
-    float *lg = nullptr;
-    if (logits != 0xFFFFFFFFu) {
-        const float *p;
-        if (f32v(ctx, logits, (uint64_t)mega_vocab(ctx), &p, "mega logits")) return -1;
-        lg = (float *)p;
-    }
-    return mega_launch(ctx, U32P(ti), U32P(to), lg);
-}
-
-int rsv_decode_mega_status(rsv_ctx *ctx, int *aborted) {
-    CHECK_CTX();
-    if (!aborted) return RSV_FAIL("decode_mega_status: null out");
-    if (no_capture(ctx, "decode_mega_status")) return -1;
-    return mega_status(ctx, aborted);
 }
 
 int rsv_clear_kernel_prof(rsv_ctx *ctx) { (void)ctx; return 0; }
@@ -1003,8 +881,10 @@ int rsv_sample_into_host_seeded_batch(rsv_ctx *ctx, uint32_t logits, uint32_t to
     OPND(tp, temp, RSV_F32, n * batch, "sample temp");
     OPND(ct, counter, RSV_U32, n * batch, "sample counter");
     OPND(sp, sampler, RSV_F32, 8 * batch, "sample sampler");
+    if (batch == 0) return RSV_FAIL("sample: batch must be >= 1");
     Tensor *h = get_tensor(ctx, hist);
     if (!h) return RSV_FAIL("sample: unknown hist tensor %u", hist);
+    // each row's history capacity; the kernel reads no further than this
     const int stride = (int)(h->len / batch);
     return launch_sample(ctx, F32P(l), U32P(t), (int)n, F32P(tp), U32P(ct), F32P(sp), (const uint32_t *)h->ptr,
                          stride, (int)batch);

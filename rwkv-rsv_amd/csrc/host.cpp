@@ -304,9 +304,6 @@ struct rsv_bundle {
     bool p16 = false;             // fp16 prefill copies of the int8 linears made (prefill_weights)
     // persistent single-session decode step: the state it is bound to, and
     // whether building it failed for good (shape or format unsupported)
-    const GpuState *mega_for = nullptr;
-    bool mega_off = false;
-    std::string mega_why;
 
     ~rsv_bundle() {
         if (ctx) rsv_destroy(ctx);
@@ -525,7 +522,6 @@ int state_create(rsv_bundle *b, uint64_t batch, GpuState &s) {
 }
 
 void state_free(rsv_bundle *b, GpuState &s) {
-    if (b->mega_for == &s) b->mega_for = nullptr;
     for (auto id : s.tmix_x) rsv_tensor_free(b->ctx, id);
     for (auto id : s.rnn) rsv_tensor_free(b->ctx, id);
     for (auto id : s.cmix_x) rsv_tensor_free(b->ctx, id);
@@ -974,85 +970,11 @@ int forward_layer(rsv_bundle *b, uint64_t i, WorkBufs &w, GpuState &s) {
     return forward_layer_fused(b, i, w, s);
 }
 
-// Binds the persistent single-session decode step (one launch per token) to
-// state s, building it on first use, when RSV_MEGA=1 (use it where it can
-// serve the model) or RSV_MEGA=2 (an error where it cannot).  use = false
-// otherwise; the six-launch path then runs.  Must run outside graph capture.
-bool mega_enabled() {
-    const char *e = getenv("RSV_MEGA");
-    return e && (e[0] == '1' || e[0] == '2');
-}
-int mega_ready(rsv_bundle *b, GpuState &s, bool &use) {
-    const char *e = getenv("RSV_MEGA");
-    const bool off = !mega_enabled(), required = e && e[0] == '2';
-    use = false;
-    if (off || s.batch != 1 || use_trait_ops()) return 0;
-    if (b->mega_for == &s) {
-        use = true;
-        return 0;
-    }
-    if (b->mega_off) return required ? herr("single-session decode step unavailable: %s", b->mega_why.c_str()) : 0;
-    const rsv_model_info &I = b->info;
-    if (!I.int8_linears) {
-        b->mega_off = true;
-        b->mega_why = "linears are not int8";
-        return required ? herr("single-session decode step unavailable: %s", b->mega_why.c_str()) : 0;
-    }
-    rsv_mega_model m;
-    memset(&m, 0, sizeof m);
-    m.n_layer = I.n_layer;
-    m.n_embd = I.n_embd;
-    m.n_head = I.n_head;
-    m.ffn = I.ffn;
-    m.vocab = I.vocab;
-    m.w_mid = I.w_mid;
-    m.a_mid = I.a_mid;
-    m.v_mid = I.v_mid;
-    m.g_mid = I.g_mid;
-    m.emb = b->emb_ln;
-    m.ln_out_w = b->ln_out_w;
-    m.ln_out_b = b->ln_out_b;
-    m.head_w16 = b->head.i8 ? NONE : b->head.w16;
-    if (b->head.i8) m.head = b->head.h;
-    m.scale_w = b->scale_w;
-    m.v_first = s.v_first;
-    m.ln_eps = LN_EPS;
-    m.l2_eps = L2_EPS;
-    m.gn_eps = GN_EPS;
-    std::vector<rsv_mega_layer> ls(I.n_layer);
-    for (uint64_t i = 0; i < I.n_layer; i++) {
-        const Layer &L = b->layers[i];
-        rsv_mega_layer &d = ls[i];
-        d = rsv_mega_layer{L.ln1_w, L.ln1_b, L.ln2_w, L.ln2_b, L.lnx_w, L.lnx_b, L.x_r, L.x_w, L.x_k, L.x_v, L.x_a,
-                           L.x_g, L.ffn_x_k, L.w0, L.a0, L.v0, L.r_k, L.k_k, L.k_a, L.w1, L.a1, L.v1, L.g1, L.w2,
-                           L.a2, L.v2, L.g2, L.rw.h, L.kw.h, L.vw.h, L.ow.h, L.fk.h, L.fv.h, s.tmix_x[i],
-                           s.cmix_x[i], s.rnn[i]};
-    }
-    if (rsv_decode_mega_build(b->ctx, &m, ls.data())) {
-        // unsupported here: the six-launch path serves this model
-        b->mega_off = true;
-        b->mega_why = rsv_last_error();
-        return required ? herr("single-session decode step unavailable: %s", b->mega_why.c_str()) : 0;
-    }
-    b->mega_for = &s;
-    use = true;
-    return 0;
-}
-
 // gather -> layers -> ln_out -> head (gpu_model.rs:1879-1913 minus the
-// sampler).  A bound single-session step runs all of it in one launch and
-// also leaves the argmax in w.token (*argmax_done).
-int decode_step(rsv_bundle *b, WorkBufs &w, GpuState &s, bool want_logits = true, bool *argmax_done = nullptr) {
+// sampler).
+int decode_step(rsv_bundle *b, WorkBufs &w, GpuState &s) {
     rsv_ctx *c = b->ctx;
     const rsv_model_info &I = b->info;
-    if (argmax_done) *argmax_done = false;
-    if (w.batch == 1 && b->mega_for == &s && !use_trait_ops()) {
-        if (mega_enabled()) {
-            CK(rsv_decode_mega(c, w.token, w.token, want_logits ? w.logits : NONE));
-            if (argmax_done) *argmax_done = true;
-            return 0;
-        }
-    }
     CK(rsv_gather_rows_device_f16(c, b->emb_ln, w.x, w.token, I.n_embd, w.batch));
     for (uint64_t i = 0; i < I.n_layer; i++) HK(forward_layer(b, i, w, s));
     if (w.mm && !use_trait_ops()) {
@@ -1440,8 +1362,6 @@ int selfloop(rsv_bundle *b, GpuState &s, const uint32_t *seeds, uint64_t n, cons
             if ((rc = new_tensor(b, 8 * B, RSV_F32, sampler))) break;
         }
         if (rsv_store_tokens(c, w->token, seeds, B)) { rc = herr("store_tokens: %s", rsv_last_error()); break; }
-        bool mega = false;
-        if ((rc = mega_ready(b, s, mega))) break;
         if (rsv_synchronize(c)) { rc = herr("%s", rsv_last_error()); break; }
         // One step = gather -> layers -> head -> sampler -> record.  It is
         // captured once as a HIP graph and replayed n times; RSV_NO_GRAPH=1
@@ -1449,12 +1369,11 @@ int selfloop(rsv_bundle *b, GpuState &s, const uint32_t *seeds, uint64_t n, cons
         // reference's SKIP_GRAPH debugging path, gpu_model.rs:1698-1721).
         const bool eager = getenv("RSV_NO_GRAPH") && getenv("RSV_NO_GRAPH")[0] && getenv("RSV_NO_GRAPH")[0] != '0';
         auto step = [&]() -> int {
-            bool done = false;
-            int e = decode_step(b, *w, s, sp != nullptr, &done);
+            int e = decode_step(b, *w, s);
             if (!e) {
                 if (sp) e = rsv_sample_into_host_seeded_batch(c, w->logits, w->token, I.vocab, temp, NONE, counter,
                                                              sampler, seq, B);
-                else if (!done) e = rsv_argmax_batch(c, w->logits, w->token, I.vocab, B);
+                else e = rsv_argmax_batch(c, w->logits, w->token, I.vocab, B);
                 if (e) herr("sampler: %s", rsv_last_error());
             }
             if (!e && rsv_record_tokens(c, w->token, seq, cnt, n, B)) e = herr("record: %s", rsv_last_error());
@@ -1498,11 +1417,6 @@ int selfloop(rsv_bundle *b, GpuState &s, const uint32_t *seeds, uint64_t n, cons
             hipEventDestroy(e1);
         }
         if (rc) break;
-        if (mega) {
-            int aborted = 0;
-            if (rsv_decode_mega_status(c, &aborted)) { rc = herr("mega status: %s", rsv_last_error()); break; }
-            if (aborted) { rc = herr("decode step gave up at a grid barrier (a workgroup never arrived)"); break; }
-        }
         if (rsv_download_u32(c, seq, out, n * B)) { rc = herr("download: %s", rsv_last_error()); break; }
     } while (0);
     cleanup();
@@ -1555,16 +1469,9 @@ static int tokens_ok(rsv_bundle *b, const uint32_t *t, uint64_t n) {
 static int run_tokens(rsv_bundle *b, GpuState &s, const uint32_t *tokens, uint64_t n) {
     WorkBufs *w;
     HK(get_bufs(b, 1, w));
-    bool mega = false;
-    HK(mega_ready(b, s, mega));
     for (uint64_t t = 0; t < n; t++) {
         CK(rsv_store_token(b->ctx, w->token, tokens[t]));
         HK(decode_step(b, *w, s));
-    }
-    if (mega) {
-        int aborted = 0;
-        CK(rsv_decode_mega_status(b->ctx, &aborted));
-        if (aborted) return herr("decode step gave up at a grid barrier (a workgroup never arrived)");
     }
     return 0;
 }
@@ -1767,8 +1674,6 @@ int rsv_forward_tokens_batch(rsv_bundle *b, rsv_state *s, const uint32_t *tokens
     WorkBufs *w;
     HK(get_bufs(b, B, w));
     CK(rsv_store_tokens(b->ctx, w->token, tokens, B));
-    bool mega = false;
-    if (B == 1) HK(mega_ready(b, s->s, mega));
     HK(decode_step(b, *w, s->s));
     if (logits) CK(rsv_download(b->ctx, w->logits, logits, B * b->info.vocab));
     else CK(rsv_synchronize(b->ctx));

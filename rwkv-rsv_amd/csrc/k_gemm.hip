@@ -4,7 +4,7 @@
 // the reference int8 format, dequantised to fp16 in the tile loader
 // (w = s*q + z in fp32, rounded to fp16 -- the same rounding as the
 // reference's dequant-to-fp16 prefill scheme, backend_cuda.rs:4195-4227).
-// Accumulation is fp32 (v_mfma_f32_32x32x8_f16).
+// Accumulation is fp32 (v_mfma_f32_32x32x16_f16).
 //
 // Tile: 128x128 per 256-thread block, BK = 32; each wave owns a 64x64
 // quadrant as 2x2 MFMA 32x32 blocks.  The next K-slab is prefetched into
@@ -13,7 +13,6 @@
 
 namespace rsv {
 
-typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef float float16_t __attribute__((ext_vector_type(16)));
 typedef unsigned int u32x4g __attribute__((ext_vector_type(4)));
 
@@ -30,138 +29,7 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
     return (uint32_t)lo | ((uint32_t)hi << 16);
 }
 
-template <bool B_I8>
-__global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
-    __shared__ __attribute__((aligned(16))) _Float16 As[BM * LDK];
-    __shared__ __attribute__((aligned(16))) _Float16 Bs[BN * LDK];
-    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
-    const int lr = tid >> 1, lc = (tid & 1) * 16;  // loader: row, first k of 16
-
-    float16_t acc[2][2];
-#pragma unroll
-    for (int i = 0; i < 2; i++)
-#pragma unroll
-        for (int j = 0; j < 2; j++)
-#pragma unroll
-            for (int e = 0; e < 16; e++) acc[i][j][e] = 0.0f;
-
-    u32x4g ra[2], rb[2];
-    uint32_t rsz = 0;
-    const int arow = m0 + lr, brow = n0 + lr;
-    const bool aok = arow < g.m, bok = brow < g.n;
-    const int KG = g.k / 128;
-
-    auto load = [&](int k0) {
-        if (aok) {
-            const u32x4g *p = (const u32x4g *)(g.a + (size_t)arow * g.lda + k0 + lc);
-            ra[0] = p[0];
-            ra[1] = p[1];
-        } else {
-            ra[0] = ra[1] = (u32x4g){0u, 0u, 0u, 0u};
-        }
-        if (B_I8) {
-            if (bok) {
-                rb[0] = *(const u32x4g *)((const uint8_t *)g.b + (size_t)brow * g.k + k0 + lc);
-                rsz = g.sz[(size_t)brow * KG + (k0 + lc) / 128];
-            } else {
-                rb[0] = (u32x4g){0u, 0u, 0u, 0u};
-                rsz = 0;
-            }
-        } else {
-            if (bok) {
-                const u32x4g *p = (const u32x4g *)((const _Float16 *)g.b + (size_t)brow * g.k + k0 + lc);
-                rb[0] = p[0];
-                rb[1] = p[1];
-            } else {
-                rb[0] = rb[1] = (u32x4g){0u, 0u, 0u, 0u};
-            }
-        }
-    };
-
-    load(0);
-    for (int k0 = 0; k0 < g.k; k0 += BK) {
-        __syncthreads();
-        u32x4g *ad = (u32x4g *)(As + lr * LDK + lc);
-        ad[0] = ra[0];
-        ad[1] = ra[1];
-        u32x4g *bd = (u32x4g *)(Bs + lr * LDK + lc);
-        if (B_I8) {
-            const float s = h2f_g(rsz), z = h2f_g(rsz >> 16);
-            uint32_t o[8];
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const uint32_t w = rb[0][q];
-                const float w0 = __fadd_rn(__fmul_rn(s, (float)(w & 0xFFu)), z);
-                const float w1 = __fadd_rn(__fmul_rn(s, (float)((w >> 8) & 0xFFu)), z);
-                const float w2 = __fadd_rn(__fmul_rn(s, (float)((w >> 16) & 0xFFu)), z);
-                const float w3 = __fadd_rn(__fmul_rn(s, (float)(w >> 24)), z);
-                o[2 * q] = pack2(w0, w1);
-                o[2 * q + 1] = pack2(w2, w3);
-            }
-            bd[0] = (u32x4g){o[0], o[1], o[2], o[3]};
-            bd[1] = (u32x4g){o[4], o[5], o[6], o[7]};
-        } else {
-            bd[0] = rb[0];
-            bd[1] = rb[1];
-        }
-        __syncthreads();
-        if (k0 + BK < g.k) load(k0 + BK);
-#pragma unroll
-        for (int kk = 0; kk < BK; kk += 8) {
-            half4_t af[2], bf[2];
-#pragma unroll
-            for (int i = 0; i < 2; i++)
-                af[i] = *(const half4_t *)(As + (wm + i * 32 + (lane & 31)) * LDK + kk + (lane >> 5) * 4);
-#pragma unroll
-            for (int j = 0; j < 2; j++)
-                bf[j] = *(const half4_t *)(Bs + (wn + j * 32 + (lane & 31)) * LDK + kk + (lane >> 5) * 4);
-#pragma unroll
-            for (int i = 0; i < 2; i++)
-#pragma unroll
-                for (int j = 0; j < 2; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x8f16(af[i], bf[j], acc[i][j], 0, 0, 0);
-        }
-    }
-
-    // epilogue: acc[i][j][e] -> row = 8*(e/4) + 4*(lane/32) + e%4, col = lane%32
-#pragma unroll
-    for (int i = 0; i < 2; i++)
-#pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const int col = n0 + wn + j * 32 + (lane & 31);
-            if (col >= g.n) continue;
-            const float bias = g.bias ? g.bias[col] : 0.0f;
-#pragma unroll
-            for (int e = 0; e < 16; e++) {
-                const int row = m0 + wm + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-                if (row >= g.m) continue;
-                const size_t o = (size_t)row * g.ldc + col;
-                float v = acc[i][j][e];
-                switch (g.epi) {
-                    case GE_BIAS: v += bias; break;
-                    case GE_ADD: v += g.aux[o]; break;
-                    case GE_RELU2: v = v > 0.0f ? v * v : 0.0f; break;
-                    case GE_TANH: v = tanhf(v); break;
-                    case GE_WDECAY: v = expf(sigm_g(v + bias) * g.scale[0]); break;
-                    case GE_SIGBIAS: v = sigm_g(v + bias); break;
-                    case GE_VLERP: {
-                        const float cur = ((const float *)g.c)[o];
-                        v = cur + sigm_g(v + bias) * (g.aux[o] - cur);
-                    } break;
-                    case GE_SIGMOID: v = sigm_g(v); break;
-                    default: break;
-                }
-                if (g.c_f16)
-                    ((_Float16 *)g.c)[o] = (_Float16)v;
-                else
-                    ((float *)g.c)[o] = v;
-            }
-        }
-}
-
-// Second form: the same 128x128 tile, loaders and dequant, with the LDS
+// k_gemm2: a 128x128 tile, int8 or fp16 weight loaders, with the LDS
 // stage double-buffered (one barrier per k-step: the next slab is written to
 // the other buffer while this one is multiplied out) and the gfx950
 // v_mfma_f32_32x32x16_f16 (16 k per instruction; lane l holds k 8*(l/32) ..
@@ -515,172 +383,8 @@ __global__ __launch_bounds__(256, BKT == 64 ? 3 : 2) void k_gemm3_multi(GemmJobs
         gemm3_body<false, BKT, 2>(g, m0, n0, As, Bs);
 }
 
-// Fourth form, fp16 weights only (the prefill's dequantised copies of the
-// int8 matrices and the fp16 LoRA matrices): the A and B stages go from
-// global memory straight into LDS (buffer_load_dwordx4 ... lds), so no
-// VGPRs stage them and NS - 1 stages of 32 k are in flight while one is
-// multiplied out.
-//   - LDS: each stage has its own A and B arrays (separate objects, so the
-//     compiler's wait before a fragment read covers that stage's copies
-//     only).  A row of a stage is 4 chunks of 8 halves; chunk c of row r
-//     sits in 16-byte slot 4r + (c ^ ((r >> 2) & 3)), which makes the
-//     fragment reads (32 rows, one chunk) conflict-free per 16 lanes.  One
-//     copy instruction fills 64 consecutive slots, so lane i of copy j
-//     fetches the chunk that belongs in slot 64j + i.
-//   - Rows past m (A) or n (B) lie past the buffer's size and read as zero.
-//   - Each wave waits for its own copies of the stage, then one barrier
-//     makes every wave's copies visible and frees the stage read before it;
-//     stages past the end copy from an offset outside the buffer (zeros), so
-//     the wait count is the same every stage.
-//   - The MFMA sequence (k ascending, 16 per instruction, the same lane to
-//     k mapping) is that of k_gemm2, so the results are bit-identical to it.
-typedef __attribute__((address_space(3))) void *g4_lds_t;
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t g4_rsrc(const void *p, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, 0x00020000);
-}
-
-// NS stages of BKT (32 or 64) k; a stage row is CPR = BKT/8 chunks, chunk c
-// of row r in slot CPR*r + (c ^ ((r >> SH) & (CPR - 1))), SH = 4 - log2(CPR)
-template <int NS, int BKT>
-__device__ __forceinline__ void gemm4_body(const GemmArgs &g, int m0, int n0, _Float16 *const (&As)[NS],
-                                           _Float16 *const (&Bs)[NS]) {
-    constexpr int CPR = BKT / 8, SH = CPR == 4 ? 2 : 1, PW = CPR / 2;  // copies per wave per operand
-    constexpr int PER = 2 * PW;
-    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
-    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
-    const __amdgpu_buffer_rsrc_t ra = g4_rsrc(g.a, (uint32_t)((size_t)g.m * g.lda * 2));
-    const __amdgpu_buffer_rsrc_t rb = g4_rsrc(g.b, (uint32_t)((size_t)g.n * g.k * 2));
-    int a_off[PW], b_off[PW];
-#pragma unroll
-    for (int t = 0; t < PW; t++) {
-        const int sl = 64 * (PW * wave + t) + lane, row = sl / CPR, c = (sl % CPR) ^ ((row >> SH) & (CPR - 1));
-        a_off[t] = ((m0 + row) * g.lda + 8 * c) * 2;
-        b_off[t] = ((n0 + row) * g.k + 8 * c) * 2;
-    }
-    const int nst = g.k / BKT;
-    auto issue = [&](int st, _Float16 *Ad, _Float16 *Bd) {
-        const bool live = st < nst;
-#pragma unroll
-        for (int t = 0; t < PW; t++) {
-            const int ka = live ? a_off[t] + 2 * BKT * st : 0x7FFFFFF0;
-            const int kb = live ? b_off[t] + 2 * BKT * st : 0x7FFFFFF0;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (g4_lds_t)(Ad + (PW * wave + t) * 512), 16, ka, 0, 0, 0);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (g4_lds_t)(Bd + (PW * wave + t) * 512), 16, kb, 0, 0, 0);
-        }
-    };
-
-    float16_t acc[2][2];
-#pragma unroll
-    for (int i = 0; i < 2; i++)
-#pragma unroll
-        for (int j = 0; j < 2; j++)
-#pragma unroll
-            for (int e = 0; e < 16; e++) acc[i][j][e] = 0.0f;
-    auto compute = [&](const _Float16 *A_, const _Float16 *B_) {
-#pragma unroll
-        for (int st = 0; st < BKT / 16; st++) {
-            const int c = 2 * st + (lane >> 5);
-            half8_t af[2], bf[2];
-#pragma unroll
-            for (int i = 0; i < 2; i++) {
-                const int r = wm + i * 32 + (lane & 31);
-                af[i] = *(const half8_t *)(A_ + 8 * (CPR * r + (c ^ ((r >> SH) & (CPR - 1)))));
-            }
-#pragma unroll
-            for (int j = 0; j < 2; j++) {
-                const int r = wn + j * 32 + (lane & 31);
-                bf[j] = *(const half8_t *)(B_ + 8 * (CPR * r + (c ^ ((r >> SH) & (CPR - 1)))));
-            }
-#pragma unroll
-            for (int i = 0; i < 2; i++)
-#pragma unroll
-                for (int j = 0; j < 2; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
-        }
-    };
-
-#pragma unroll
-    for (int u = 0; u < NS - 1; u++) issue(u, As[u], Bs[u]);
-    for (int s0 = 0; s0 < nst; s0 += NS) {
-#pragma unroll
-        for (int u = 0; u < NS; u++) {
-            if (s0 + u >= nst) break;
-            // this wave's copies of stage s0 + u are done when at most the
-            // NS - 2 later stages' copies are outstanding
-            __builtin_amdgcn_s_waitcnt(((PER * (NS - 2)) & 0xF) | (((PER * (NS - 2)) >> 4) << 14) | (0x7 << 4) |
-                                       (0xF << 8));
-            __builtin_amdgcn_s_barrier();
-            issue(s0 + u + NS - 1, As[(u + NS - 1) % NS], Bs[(u + NS - 1) % NS]);
-            compute(As[u], Bs[u]);
-        }
-    }
-    __builtin_amdgcn_s_waitcnt(0);  // no copy may land in LDS after the block
-#define GEMM4_EPI(K) gemm2_epilogue<K, 2>(g, acc, m0, n0, wm, wn, lane)
-    switch (g.epi) {
-        case GE_BIAS: GEMM4_EPI(GE_BIAS); break;
-        case GE_ADD: GEMM4_EPI(GE_ADD); break;
-        case GE_RELU2: GEMM4_EPI(GE_RELU2); break;
-        case GE_TANH: GEMM4_EPI(GE_TANH); break;
-        case GE_WDECAY: GEMM4_EPI(GE_WDECAY); break;
-        case GE_SIGBIAS: GEMM4_EPI(GE_SIGBIAS); break;
-        case GE_VLERP: GEMM4_EPI(GE_VLERP); break;
-        case GE_SIGMOID: GEMM4_EPI(GE_SIGMOID); break;
-        default: GEMM4_EPI(GE_STORE); break;
-    }
-#undef GEMM4_EPI
-}
-
-// one LDS array per stage and operand (unreferenced ones are dropped)
-#define G4_LDS(NS, BKT)                                                                            \
-    __shared__ __attribute__((aligned(16))) _Float16 A0[128 * BKT], A1[128 * BKT], A2[128 * BKT],  \
-        A3[128 * BKT];                                                                             \
-    __shared__ __attribute__((aligned(16))) _Float16 B0[128 * BKT], B1[128 * BKT], B2[128 * BKT],  \
-        B3[128 * BKT];                                                                             \
-    _Float16 *const As4[4] = {A0, A1, A2, A3};                                                     \
-    _Float16 *const Bs4[4] = {B0, B1, B2, B3};                                                     \
-    _Float16 *const(&As)[NS] = *reinterpret_cast<_Float16 *const(*)[NS]>(&As4);                    \
-    _Float16 *const(&Bs)[NS] = *reinterpret_cast<_Float16 *const(*)[NS]>(&Bs4);
-
-template <int NS, int BKT>
-__global__ __launch_bounds__(256, NS * BKT <= 96 ? 3 : 2) void k_gemm4(GemmArgs g) {
-    G4_LDS(NS, BKT)
-    gemm4_body<NS, BKT>(g, blockIdx.y * 128, blockIdx.x * BN, As, Bs);
-}
-
-template <int NS, int BKT>
-__global__ __launch_bounds__(256, NS * BKT <= 96 ? 3 : 2) void k_gemm4_multi(GemmJobs jobs) {
-    G4_LDS(NS, BKT)
-    const int bid = blockIdx.x;
-    int ji = 0;
-    while (ji + 1 < jobs.n && bid >= jobs.blk_start[ji + 1]) ji++;
-    const GemmArgs &g = jobs.j[ji];
-    const int local = bid - jobs.blk_start[ji], nt = (g.n + BN - 1) / BN;
-    gemm4_body<NS, BKT>(g, (local / nt) * 128, (local % nt) * BN, As, Bs);
-}
-#undef G4_LDS
-
-// k_gemm4 takes a job, with RSV_GEMM_DMA=1, when its weights are fp16, k is
-// a multiple of 32 and both operands fit a 32-bit buffer range (measured
-// slower than k_gemm3 on the prefill shapes, so off by default)
-static int gemm4_mode() {
-    const char *e = getenv("RSV_GEMM_DMA");
-    return e ? atoi(e) : 0;
-}
-static bool gemm4_ok(const GemmArgs &g) {
-    const int md = gemm4_mode();
-    if (md < 1 || md > 4) return false;
-    return !g.b_i8 && g.k % (md >= 3 ? 64 : 32) == 0 && (size_t)g.m * g.lda * 2 < 0x7FFFFFF0ull && (size_t)g.n * g.k * 2 < 0x7FFFFFF0ull;
-}
-
-// k per stage of the prefill GEMMs: RSV_GEMM_BK = 32 (k_gemm2, double-
-// buffered), 64 or 128 (k_gemm3); a job whose k is not a multiple takes 32.
-static int gemm_bk() {
-    const char *e = getenv("RSV_GEMM_BK");
-    const int v = e ? atoi(e) : 64;
-    return v == 128 || v == 64 ? v : 32;
-}
-
+// k per stage: 64 (k_gemm3) where every job's k is a multiple of 64, else 32
+// (k_gemm2, double-buffered: the LoRA-up jobs, k = 96 etc.).
 static int gemm_check(const GemmArgs &g) {
     if (g.m <= 0 || g.n <= 0 || g.k <= 0) return RSV_FAIL("gemm: bad shape m=%d n=%d k=%d", g.m, g.n, g.k);
     if (g.k % BK != 0) return RSV_FAIL("gemm: k=%d must be a multiple of %d", g.k, BK);
@@ -705,81 +409,24 @@ int launch_gemm_multi(rsv_ctx *ctx, GemmJobs &jobs) {
         total += ((g.n + BN - 1) / BN) * ((g.m + BM - 1) / BM);
     }
     jobs.blk_start[jobs.n] = total;
-    bool dma = true;
-    for (int i = 0; i < jobs.n; i++) dma &= gemm4_ok(jobs.j[i]);
-    if (dma) {
-        switch (gemm4_mode()) {
-            case 2: hipLaunchKernelGGL((k_gemm4_multi<4, 32>), dim3(total), dim3(256), 0, ctx->stream, jobs); break;
-            case 3: hipLaunchKernelGGL((k_gemm4_multi<2, 64>), dim3(total), dim3(256), 0, ctx->stream, jobs); break;
-            case 4: hipLaunchKernelGGL((k_gemm4_multi<3, 64>), dim3(total), dim3(256), 0, ctx->stream, jobs); break;
-            default: hipLaunchKernelGGL((k_gemm4_multi<3, 32>), dim3(total), dim3(256), 0, ctx->stream, jobs); break;
-        }
-        RSV_HIP(hipGetLastError());
-        return 0;
-    }
-    int bk = gemm_bk();
-    for (int i = 0; i < jobs.n; i++)
-        while (bk > 32 && jobs.j[i].k % bk) bk /= 2;
-    if (bk == 128) hipLaunchKernelGGL((k_gemm3_multi<128>), dim3(total), dim3(256), 0, ctx->stream, jobs);
-    else if (bk == 64) hipLaunchKernelGGL((k_gemm3_multi<64>), dim3(total), dim3(256), 0, ctx->stream, jobs);
+    bool k64 = true;
+    for (int i = 0; i < jobs.n; i++) k64 &= jobs.j[i].k % 64 == 0;
+    if (k64) hipLaunchKernelGGL((k_gemm3_multi<64>), dim3(total), dim3(256), 0, ctx->stream, jobs);
     else hipLaunchKernelGGL((k_gemm2_multi<128>), dim3(total), dim3(256), 0, ctx->stream, jobs);
     RSV_HIP(hipGetLastError());
     return 0;
 }
 
 int launch_gemm(rsv_ctx *ctx, const GemmArgs &g) {
-    if (g.m <= 0 || g.n <= 0 || g.k <= 0) return RSV_FAIL("gemm: bad shape m=%d n=%d k=%d", g.m, g.n, g.k);
-    if (g.k % BK != 0) return RSV_FAIL("gemm: k=%d must be a multiple of %d", g.k, BK);
-    if (g.b_i8 && (g.k % 128 != 0 || !g.sz)) return RSV_FAIL("gemm: int8 weights need k %% 128 == 0 and scales");
-    if (g.lda < g.k || g.lda % 8 != 0) return RSV_FAIL("gemm: lda=%d must be >= k and a multiple of 8", g.lda);
-    if (g.ldc < g.n) return RSV_FAIL("gemm: ldc=%d < n=%d", g.ldc, g.n);
-    if ((g.epi == GE_ADD || g.epi == GE_VLERP) && !g.aux) return RSV_FAIL("gemm: epilogue needs aux");
-    if ((g.epi == GE_BIAS || g.epi == GE_WDECAY || g.epi == GE_SIGBIAS || g.epi == GE_VLERP) && !g.bias)
-        return RSV_FAIL("gemm: epilogue needs bias");
-    if (g.epi == GE_WDECAY && !g.scale) return RSV_FAIL("gemm: decay epilogue needs scale");
-    if (g.c_f16 && (g.epi == GE_ADD || g.epi == GE_VLERP)) return RSV_FAIL("gemm: in-place epilogues need fp32 C");
-    dim3 grid((g.n + BN - 1) / BN, (g.m + BM - 1) / BM);
-    const int v2 = [] {  // read at each launch, so one process can compare settings
-        const char *e = getenv("RSV_GEMM_V2");
-        return e ? atoi(e) : 1;
-    }();
-    if (v2) {
-        // 128-row tiles: 256-row tiles (one wave per SIMD at 275 registers)
-        // measured 1.5x slower on the prefill GEMMs
-        if (gemm4_ok(g)) {
-            switch (gemm4_mode()) {
-                case 2: hipLaunchKernelGGL((k_gemm4<4, 32>), grid, dim3(256), 0, ctx->stream, g); break;
-                case 3: hipLaunchKernelGGL((k_gemm4<2, 64>), grid, dim3(256), 0, ctx->stream, g); break;
-                case 4: hipLaunchKernelGGL((k_gemm4<3, 64>), grid, dim3(256), 0, ctx->stream, g); break;
-                default: hipLaunchKernelGGL((k_gemm4<3, 32>), grid, dim3(256), 0, ctx->stream, g); break;
-            }
-            RSV_HIP(hipGetLastError());
-            return 0;
-        }
-        int bk = gemm_bk();
-        while (bk > 32 && g.k % bk) bk /= 2;
-        if (bk == 128) {
-            if (g.b_i8) hipLaunchKernelGGL((k_gemm3<true, 128>), grid, dim3(256), 0, ctx->stream, g);
-            else hipLaunchKernelGGL((k_gemm3<false, 128>), grid, dim3(256), 0, ctx->stream, g);
-        } else if (bk == 64) {
-            // 256-row blocks (128 x 64 per wave: 0.75 LDS fragment reads per
-            // MFMA instead of 1) with RSV_GEMM_BM=256
-            const char *bme = getenv("RSV_GEMM_BM");
-            if (bme && atoi(bme) == 256) {
-                const dim3 g2((g.n + BN - 1) / BN, (g.m + 255) / 256);
-                if (g.b_i8) hipLaunchKernelGGL((k_gemm3<true, 64, 256>), g2, dim3(256), 0, ctx->stream, g);
-                else hipLaunchKernelGGL((k_gemm3<false, 64, 256>), g2, dim3(256), 0, ctx->stream, g);
-            } else if (g.b_i8) hipLaunchKernelGGL((k_gemm3<true, 64>), grid, dim3(256), 0, ctx->stream, g);
-            else hipLaunchKernelGGL((k_gemm3<false, 64>), grid, dim3(256), 0, ctx->stream, g);
-        } else if (g.b_i8) hipLaunchKernelGGL((k_gemm2<true, 128>), grid, dim3(256), 0, ctx->stream, g);
-        else hipLaunchKernelGGL((k_gemm2<false, 128>), grid, dim3(256), 0, ctx->stream, g);
-        RSV_HIP(hipGetLastError());
-        return 0;
-    }
-    if (g.b_i8)
-        hipLaunchKernelGGL(k_gemm<true>, grid, dim3(256), 0, ctx->stream, g);
-    else
-        hipLaunchKernelGGL(k_gemm<false>, grid, dim3(256), 0, ctx->stream, g);
+    if (gemm_check(g)) return -1;
+    const dim3 grid((g.n + BN - 1) / BN, (g.m + BM - 1) / BM);
+    // 128-row tiles: 256-row tiles (one wave per SIMD at 275 registers)
+    // measured 1.5x slower on the prefill GEMMs
+    if (g.k % 64 == 0) {
+        if (g.b_i8) hipLaunchKernelGGL((k_gemm3<true, 64>), grid, dim3(256), 0, ctx->stream, g);
+        else hipLaunchKernelGGL((k_gemm3<false, 64>), grid, dim3(256), 0, ctx->stream, g);
+    } else if (g.b_i8) hipLaunchKernelGGL((k_gemm2<true, 128>), grid, dim3(256), 0, ctx->stream, g);
+    else hipLaunchKernelGGL((k_gemm2<false, 128>), grid, dim3(256), 0, ctx->stream, g);
     RSV_HIP(hipGetLastError());
     return 0;
 }

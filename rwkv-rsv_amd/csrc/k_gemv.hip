@@ -447,554 +447,14 @@ static int launch_t(rsv_ctx *ctx, GemvJobs &jobs, int batch) {
 }
 
 // ---------------------------------------------------------------- B = 1
-// Decode GEMV for one session, built for memory-level parallelism.
-// A job's rows are cut into tiles of (4/KS)*RU rows; each block of the
-// launch owns the tiles rb, rb + nblk, ... of one job.  Per block:
-//   1. its share of the prologue inputs (x and, per prologue, the LN
-//      gamma/beta/mix coefficient/token-shift row or the gate) is loaded,
-//      4 elements per thread per round, coalesced;
-//   2. the first tile's weights, scale/zero words and epilogue operands are
-//      loaded with clamped addresses and no branches, so none is sunk;
-//   3. the prologue runs once per block (LN statistics by block reduction)
-//      and the transformed x goes through LDS into registers: lane li of a
-//      wave always reads chunks li + 64*j of its K-slice (8-byte chunks, so
-//      each weight load instruction covers 512 contiguous bytes), the same
-//      x chunks for every row;
-//   4. tiles are then software-pipelined: the next tile's loads go out
-//      before the current tile's dot products.
-// A row is split over KS waves (KS = 1, 2 or 4) whose partial sums meet in
-// LDS in a fixed order, so results do not depend on timing.
-typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
-// Q: prologue rounds (K <= 1024*Q).  The LN-mix and gate prologues need four
-// more vectors per round, so they are compiled only into the short-row
-// variant (Q <= 3); long rows take the plain and sigmoid prologues.
-constexpr int kRegQShort = 3, kRegQLong = 10;
-
-template <int FMT, int CPL, int RU>
-struct RegTile {
-    typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
-    u32x2_t w[RU][CPL];
-    uint32_t sz[RU][CPL];
-    float e0[RU], e1[RU], e2[RU];  // y (read-modify-write epilogues), p0[row], p1[row]
-};
-
-template <int FMT, int CPL, int RU>
-__device__ __forceinline__ void reg_load(const GemvJob &J, int tile, int ks, int rg, int li,
-                                         RegTile<FMT, CPL, RU> &T) {
-    constexpr int CW = FMT == FMT_I8 ? 8 : 4;
-    constexpr int SL = 64 * CPL;
-    const int K = J.K, M = J.M, NC = K / CW, KG = K / 128;
-    const int rbase = (tile * (4 / J.ks) + rg) * RU;
-    const u32x2 *W = (const u32x2 *)J.w;
-    const bool need_y = J.epi == EPI_ADD || J.epi == EPI_VLERP;
-#pragma unroll
-    for (int r = 0; r < RU; r++) {
-        const int row = min(rbase + r, M - 1);
-#pragma unroll
-        for (int j = 0; j < CPL; j++) {
-            const int c = min(ks * SL + li + j * 64, NC - 1);
-            T.w[r][j] = __builtin_nontemporal_load(W + (size_t)row * NC + c);
-            if (FMT == FMT_I8) T.sz[r][j] = __builtin_nontemporal_load(J.sz + (size_t)row * KG + (c >> 4));
-        }
-        T.e0[r] = need_y ? J.y[row] : 0.0f;
-        T.e1[r] = J.p0 ? J.p0[row] : 0.0f;
-        T.e2[r] = J.epi == EPI_VLERP ? J.p1[row] : 0.0f;
-    }
-}
-
-template <int FMT, int CPL, int RU>
-__device__ __forceinline__ void reg_dot(const GemvJob &J, int tile, int it, int ks, int rg, int wave, int li,
-                                        const float (&xv)[CPL][FMT == FMT_I8 ? 8 : 4], const float (&dx)[CPL],
-                                        const RegTile<FMT, CPL, RU> &T, float scale, float *part) {
-    const int M = J.M, KS = J.ks;
-    const int rbase = (tile * (4 / KS) + rg) * RU;
-    float acc[RU];
-#pragma unroll
-    for (int r = 0; r < RU; r++) acc[r] = 0.0f;
-#pragma unroll
-    for (int j = 0; j < CPL; j++) {
-        if (FMT == FMT_I8) {
-            // w = s*q + z over one 8-weight chunk of a 128-group (model.rs:234-252):
-            // contribution s*sum(x*q) + z*sum(x)
-#pragma unroll
-            for (int r = 0; r < RU; r++) {
-                float d = 0.0f;
-#pragma unroll
-                for (int q = 0; q < 2; q++) {
-                    const uint32_t wq = T.w[r][j][q];
-                    d = fmaf(xv[j][4 * q + 0], (float)(wq & 0xFFu), d);
-                    d = fmaf(xv[j][4 * q + 1], (float)((wq >> 8) & 0xFFu), d);
-                    d = fmaf(xv[j][4 * q + 2], (float)((wq >> 16) & 0xFFu), d);
-                    d = fmaf(xv[j][4 * q + 3], (float)(wq >> 24), d);
-                }
-                const uint32_t sw = T.sz[r][j];
-                acc[r] = fmaf(h2f(sw), d, fmaf(h2f(sw >> 16), dx[j], acc[r]));
-            }
-        } else {
-#pragma unroll
-            for (int r = 0; r < RU; r++) {
-                float d = acc[r];
-#pragma unroll
-                for (int q = 0; q < 2; q++) {
-                    const uint32_t wq = T.w[r][j][q];
-                    d = fmaf(xv[j][2 * q + 0], h2f(wq), d);
-                    d = fmaf(xv[j][2 * q + 1], h2f(wq >> 16), d);
-                }
-                acc[r] = d;
-            }
-        }
-    }
-#pragma unroll
-    for (int r = 0; r < RU; r++) {
-        acc[r] = group_sum_last<64>(acc[r]);
-    }
-    if (KS > 1) {
-        // slice partials meet in LDS (double-buffered by tile parity); slice
-        // 0 adds them in slice order
-        float *pp = part + (it & 1) * 4 * RU;
-        if (li == 63)
-#pragma unroll
-            for (int r = 0; r < RU; r++) pp[wave * RU + r] = acc[r];
-        __syncthreads();
-        if (ks != 0) return;
-#pragma unroll
-        for (int r = 0; r < RU; r++) {
-            float v = pp[wave * RU + r];
-            for (int q = 1; q < KS; q++) v += pp[(wave + q) * RU + r];
-            acc[r] = v;
-        }
-    }
-    if (li != 63) return;
-#pragma unroll
-    for (int r = 0; r < RU; r++) {
-        const int row = rbase + r;
-        if (row >= M) continue;
-        const float v = acc[r];
-        float *yp = J.y + row;
-        switch (J.epi) {
-            case EPI_STORE: *yp = v; break;
-            case EPI_RELU2: { const float t = v > 0.0f ? v : 0.0f; *yp = t * t; } break;
-            case EPI_ADD: *yp = T.e0[r] + v; break;
-            case EPI_TANH: *yp = tanhf(v); break;
-            case EPI_WDECAY: *yp = expf(sigmoid_f(v + T.e1[r]) * scale); break;
-            case EPI_SIGBIAS: *yp = sigmoid_f(v + T.e1[r]); break;
-            case EPI_VLERP: {
-                const float g = sigmoid_f(v + T.e1[r]);
-                *yp = T.e0[r] + g * (T.e2[r] - T.e0[r]);
-            } break;
-            case EPI_STORE2:
-                *yp = v;
-                ((float *)J.p1)[row] = v;
-                break;
-            default: break;
-        }
-    }
-}
-
-template <int FMT, int CPL, int RU, int Q>
-__device__ __forceinline__ void gemv_reg_body(const GemvJob &J, int rb, float *red, float4 *xs) {
-    constexpr bool kMix = Q <= kRegQShort;
-    constexpr int CW = FMT == FMT_I8 ? 8 : 4;  // weights per 8-byte chunk
-    constexpr int P = CW / 4;                  // float4 parts of x per chunk
-    constexpr int SL = 64 * CPL;
-    const int K = J.K, M = J.M, NC = K / CW, KS = J.ks, K4 = K / 4;
-    const int tid = threadIdx.x, wave = tid >> 6, li = tid & 63;
-    const int ks = wave % KS, rg = wave / KS;
-    const int ntile = (M + (4 / KS) * RU - 1) / ((4 / KS) * RU);
-    const int nblk = J.nblk;
-
-    // 1. prologue inputs
-    const float4 *X4 = (const float4 *)J.x;
-    constexpr int QM = kMix ? Q : 1;
-    float4 xa[Q], pa[QM], ga[QM], ba[QM], ca[QM];
-#pragma unroll
-    for (int i = 0; i < Q; i++) {
-        const int q = tid + 256 * i;
-        const bool in = q < K4;
-        xa[i] = in ? X4[q] : make_float4(0.f, 0.f, 0.f, 0.f);
-        if (!kMix) continue;
-        if (J.pro == PRO_MUL) pa[i] = in ? ((const float4 *)J.xmul)[q] : make_float4(0.f, 0.f, 0.f, 0.f);
-        if (J.pro == PRO_LNMIX) {
-            pa[i] = in ? ((const float4 *)J.prev)[q] : make_float4(0.f, 0.f, 0.f, 0.f);
-            ga[i] = in ? ((const float4 *)J.gamma)[q] : make_float4(0.f, 0.f, 0.f, 0.f);
-            ba[i] = in ? ((const float4 *)J.beta)[q] : make_float4(0.f, 0.f, 0.f, 0.f);
-            ca[i] = in ? ((const float4 *)J.coef)[q] : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-    }
-    const float scale = J.epi == EPI_WDECAY ? J.scale[0] : 0.0f;
-
-    // 2. first tile
-    RegTile<FMT, CPL, RU> A, B;
-    int t = rb;
-    reg_load<FMT, CPL, RU>(J, t, ks, rg, li, A);
-
-    // 3. prologue, once per block, into LDS (float4 part p of chunk c at p*NC + c)
-    if (kMix && J.pro == PRO_LNMIX) {
-        float s = 0.0f;
-#pragma unroll
-        for (int i = 0; i < Q; i++) s += (xa[i].x + xa[i].y) + (xa[i].z + xa[i].w);
-        const float mu = block_sum_256(s, red) / (float)K;
-        float v2 = 0.0f;
-#pragma unroll
-        for (int i = 0; i < Q; i++) {
-            if (tid + 256 * i >= K4) continue;
-            const float d0 = xa[i].x - mu, d1 = xa[i].y - mu, d2 = xa[i].z - mu, d3 = xa[i].w - mu;
-            v2 += (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
-        }
-        const float inv = 1.0f / sqrtf(block_sum_256(v2, red) / (float)K + 1.0e-5f);
-        const bool wr = J.lnout && rb == 0;
-#pragma unroll
-        for (int i = 0; i < Q; i++) {
-            const int q = tid + 256 * i;
-            if (q >= K4) continue;
-            const int m = kMix ? i : 0;
-            float4 ln;
-            ln.x = (xa[i].x - mu) * inv * ga[m].x + ba[m].x;
-            ln.y = (xa[i].y - mu) * inv * ga[m].y + ba[m].y;
-            ln.z = (xa[i].z - mu) * inv * ga[m].z + ba[m].z;
-            ln.w = (xa[i].w - mu) * inv * ga[m].w + ba[m].w;
-            if (wr) ((float4 *)J.lnout)[q] = ln;
-            xa[i].x = ln.x + ca[m].x * (pa[m].x - ln.x);
-            xa[i].y = ln.y + ca[m].y * (pa[m].y - ln.y);
-            xa[i].z = ln.z + ca[m].z * (pa[m].z - ln.z);
-            xa[i].w = ln.w + ca[m].w * (pa[m].w - ln.w);
-        }
-    } else if (kMix && J.pro == PRO_MUL) {
-#pragma unroll
-        for (int i = 0; i < Q; i++) {
-            const int m = kMix ? i : 0;
-            xa[i].x *= pa[m].x; xa[i].y *= pa[m].y; xa[i].z *= pa[m].z; xa[i].w *= pa[m].w;
-        }
-    } else if (J.pro == PRO_SIGMOID) {
-#pragma unroll
-        for (int i = 0; i < Q; i++) {
-            xa[i].x = sigmoid_f(xa[i].x); xa[i].y = sigmoid_f(xa[i].y);
-            xa[i].z = sigmoid_f(xa[i].z); xa[i].w = sigmoid_f(xa[i].w);
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < Q; i++) {
-        const int q = tid + 256 * i;
-        if (q >= K4) continue;
-        const int c = (4 * q) / CW, pp = ((4 * q) % CW) >> 2;
-        xs[pp * NC + c] = xa[i];
-    }
-    __syncthreads();
-    float xv[CPL][CW], dx[CPL];
-#pragma unroll
-    for (int j = 0; j < CPL; j++) {
-        const int cr = ks * SL + li + j * 64;
-        const bool cin = cr < NC;
-        const int c = cin ? cr : NC - 1;
-#pragma unroll
-        for (int p = 0; p < P; p++) {
-            const float4 v = xs[p * NC + c];
-            xv[j][4 * p] = cin ? v.x : 0.0f; xv[j][4 * p + 1] = cin ? v.y : 0.0f;
-            xv[j][4 * p + 2] = cin ? v.z : 0.0f; xv[j][4 * p + 3] = cin ? v.w : 0.0f;
-        }
-        float sx = 0.0f;
-#pragma unroll
-        for (int i = 0; i < CW; i++) sx += xv[j][i];
-        dx[j] = sx;
-    }
-
-    // 4. software-pipelined tiles (the prefetch past the last tile re-reads
-    // the current one instead of branching, so no load waits on a join)
-    float *part = red + 8;
-    for (int it = 0;; it += 2) {
-        int tn = t + nblk;
-        reg_load<FMT, CPL, RU>(J, tn < ntile ? tn : t, ks, rg, li, B);
-        reg_dot<FMT, CPL, RU>(J, t, it, ks, rg, wave, li, xv, dx, A, scale, part);
-        t = tn;
-        if (t >= ntile) break;
-        tn = t + nblk;
-        reg_load<FMT, CPL, RU>(J, tn < ntile ? tn : t, ks, rg, li, A);
-        reg_dot<FMT, CPL, RU>(J, t, it + 1, ks, rg, wave, li, xv, dx, B, scale, part);
-        t = tn;
-        if (t >= ntile) break;
-    }
-}
-
-template <int CPL, int RU, int Q>
-__global__ __launch_bounds__(256) void k_gemv_reg(GemvJobs jobs) {
-    extern __shared__ float4 xs4[];
-    __shared__ float red[8 + 8 * RU];
-    const int bid = blockIdx.x;
-    if (bid == 0 && jobs.side.src)
-        for (int i = threadIdx.x; i < jobs.side.n; i += 256) jobs.side.dst[i] = jobs.side.src[i];
-    int ji = 0;
-    while (ji + 1 < jobs.n && bid >= jobs.blk_start[ji + 1]) ji++;
-    const GemvJob &J = jobs.j[ji];
-    const int rb = bid - jobs.blk_start[ji];
-    if (J.fmt == FMT_I8)
-        gemv_reg_body<FMT_I8, CPL, RU, Q>(J, rb, red, xs4);
-    else
-        gemv_reg_body<FMT_F16, CPL, RU, Q>(J, rb, red, xs4);
-}
-
-constexpr int kRegCPL = 5;
-
-// k-slices per row for the register kernel, or 0 when the job does not fit
-// it (rows too short to fill the lanes, or more than 4 slices).
-static int reg_slices(const GemvJob &J) {
-    const int nc = J.K / (J.fmt == FMT_I8 ? 8 : 4);
-    const int sl = 64 * kRegCPL;
-    const int ks = (nc + sl - 1) / sl;
-    if (ks == 3 || ks > 4 || J.K % 4 != 0) return 0;
-    if (J.K > 1024 * kRegQLong) return 0;
-    if ((J.pro == PRO_LNMIX || J.pro == PRO_MUL) && J.K > 1024 * kRegQShort) return 0;
-    if (nc * 4 < ks * sl * 3) return 0;  // under 75% of the lanes busy
-    return ks;
-}
-
-// Blocks per job: the launch targets `target` blocks in all, shared by the
-// jobs in proportion to their tiles, every block of a job getting the same
-// number of tiles (up to the last).
-template <int RU>
-static int launch_reg(rsv_ctx *ctx, GemvJobs &jobs, int target) {
-    int tiles_all = 0;
-    for (int i = 0; i < jobs.n; i++) {
-        const int rpt = (4 / jobs.j[i].ks) * RU;
-        tiles_all += (jobs.j[i].M + rpt - 1) / rpt;
-    }
-    int total = 0, kmax = 0;
-    for (int i = 0; i < jobs.n; i++) {
-        GemvJob &J = jobs.j[i];
-        const int rpt = (4 / J.ks) * RU;
-        const int tiles = (J.M + rpt - 1) / rpt;
-        const int want = std::max(1, (int)((int64_t)tiles * target / std::max(1, tiles_all)));
-        const int tpb = (tiles + want - 1) / want;
-        J.nblk = (tiles + tpb - 1) / tpb;
-        jobs.blk_start[i] = total;
-        total += J.nblk;
-        kmax = std::max(kmax, J.K);
-    }
-    jobs.blk_start[jobs.n] = total;
-    if (kmax <= 1024 * kRegQShort)
-        hipLaunchKernelGGL((k_gemv_reg<kRegCPL, RU, kRegQShort>), dim3(total), dim3(256), (size_t)kmax * 4, ctx->stream, jobs);
-    else
-        hipLaunchKernelGGL((k_gemv_reg<kRegCPL, RU, kRegQLong>), dim3(total), dim3(256), (size_t)kmax * 4, ctx->stream, jobs);
-    RSV_HIP(hipGetLastError());
-    return 0;
-}
-
-static int env_int(const char *name, int dflt) {
-    const char *e = getenv(name);
-    return (e && e[0]) ? atoi(e) : dflt;
-}
-
-// ---------------------------------------------------------------- B = 1, one-shot
-// LN + token-shift mixes of one row x [K] for a B=1 launch, computed once
-// (model.rs:625-635, 654-660): out_m = ln + coef_m * (prev - ln) with
-// ln = LN(x)*gamma + beta; lnout (optional) receives ln.  Every block takes
-// the row statistics itself (two-pass, from registers) and writes its slice
-// of 1024 elements.
-struct MixArgs {
-    const float *x, *gamma, *beta, *prev;
-    const float *coef[kMaxJobs];
-    float *out[kMaxJobs];
-    float *lnout;
-    int nmix, K;
-};
-constexpr int kMixQ = kMixMaxK / 1024;
-
-__global__ __launch_bounds__(256) void k_lnmix_pre(MixArgs a) {
-    __shared__ float red[4];
-    const int tid = threadIdx.x, K4 = a.K / 4;
-    const float4 *X4 = (const float4 *)a.x;
-    float s = 0.0f;
-    for (int q = tid; q < K4; q += 256) { const float4 v = X4[q]; s += (v.x + v.y) + (v.z + v.w); }
-    const float mu = block_sum_256(s, red) / (float)a.K;
-    float v2 = 0.0f;
-    for (int q = tid; q < K4; q += 256) {
-        const float4 v = X4[q];
-        const float d0 = v.x - mu, d1 = v.y - mu, d2 = v.z - mu, d3 = v.w - mu;
-        v2 += (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
-    }
-    const float inv = 1.0f / sqrtf(block_sum_256(v2, red) / (float)a.K + 1.0e-5f);
-    const int q = blockIdx.x * 256 + tid;
-    if (q >= K4) return;
-    const float4 v = X4[q], g = ((const float4 *)a.gamma)[q], b = ((const float4 *)a.beta)[q];
-    const float4 p = ((const float4 *)a.prev)[q];
-    float4 ln;
-    ln.x = (v.x - mu) * inv * g.x + b.x;
-    ln.y = (v.y - mu) * inv * g.y + b.y;
-    ln.z = (v.z - mu) * inv * g.z + b.z;
-    ln.w = (v.w - mu) * inv * g.w + b.w;
-    if (a.lnout) ((float4 *)a.lnout)[q] = ln;
-    for (int m = 0; m < a.nmix; m++) {
-        const float4 c = ((const float4 *)a.coef[m])[q];
-        float4 o;
-        o.x = ln.x + c.x * (p.x - ln.x);
-        o.y = ln.y + c.y * (p.y - ln.y);
-        o.z = ln.z + c.z * (p.z - ln.z);
-        o.w = ln.w + c.w * (p.w - ln.w);
-        ((float4 *)a.out[m])[q] = o;
-    }
-}
-
-// One-shot GEMV for one session: a block owns 4*(64/LPR) consecutive rows of
-// one job (LPR = 32 lanes per row for rows of at most 160 16-byte chunks,
-// else 64); lane li of a row reads chunks li + LPR*j, so each load
-// instruction covers LPR*16 contiguous bytes.  Every weight and scale/zero
-// load of the block goes out first (clamped addresses, no branches), then x
-// (after the prologue: gate multiply or sigmoid) is staged chunk-major in
-// LDS, and the dot products read it from there.  Small register footprint
-// and short blocks keep many blocks resident per CU, which is what hides the
-// memory latency here.
-template <int FMT, int LPR, int CPL, int Q>
-__device__ __forceinline__ void gemv_os_body(const GemvJob &J, int rb, float4 *xs) {
-    constexpr int CW = FMT == FMT_I8 ? 16 : 8;
-    constexpr int P = CW / 4;
-    constexpr int SLOTS = 64 / LPR;
-    const int K = J.K, M = J.M, NC = K / CW, KG = K / 128, K4 = K / 4;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int slot = lane / LPR, li = lane % LPR;
-    const int row0 = (rb * 4 + wave) * SLOTS + slot;
-    const int row = min(row0, M - 1);
-    const u32x4 *W = (const u32x4 *)J.w;
-    u32x4 wv[CPL];
-    uint32_t szv[CPL];
-#pragma unroll
-    for (int j = 0; j < CPL; j++) {
-        const int c = min(li + LPR * j, NC - 1);
-        wv[j] = __builtin_nontemporal_load(W + (size_t)row * NC + c);
-        if (FMT == FMT_I8) szv[j] = J.sz[(size_t)row * KG + (c >> 3)];
-    }
-    // x (with the gate multiply or sigmoid) into LDS: float4 part p of chunk c at p*NC + c
-    {
-        const float4 *X4 = (const float4 *)J.x;
-        float4 xa[Q];
-#pragma unroll
-        for (int i = 0; i < Q; i++) {
-            const int q = tid + 256 * i;
-            xa[i] = q < K4 ? X4[q] : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-        if (Q <= 3 && J.pro == PRO_LNMIX) {
-            // LN over the row (two-pass, model.rs:625-635) from the x values
-            // already in registers, then the token-shift mix; the LN inputs
-            // are loaded only after the statistics to keep registers free
-            float s = 0.0f;
-#pragma unroll
-            for (int i = 0; i < Q; i++) s += (xa[i].x + xa[i].y) + (xa[i].z + xa[i].w);
-            __shared__ float red_os[4];
-            const float mu = block_sum_256(s, red_os) / (float)K;
-            float v2 = 0.0f;
-#pragma unroll
-            for (int i = 0; i < Q; i++) {
-                if (tid + 256 * i >= K4) continue;
-                const float d0 = xa[i].x - mu, d1 = xa[i].y - mu, d2 = xa[i].z - mu, d3 = xa[i].w - mu;
-                v2 += (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
-            }
-            const float inv = 1.0f / sqrtf(block_sum_256(v2, red_os) / (float)K + 1.0e-5f);
-            const bool wr = J.lnout && rb == 0;
-#pragma unroll
-            for (int i = 0; i < Q; i++) {
-                const int q = tid + 256 * i;
-                if (q >= K4) continue;
-                const float4 g = ((const float4 *)J.gamma)[q], bt = ((const float4 *)J.beta)[q];
-                const float4 cf = ((const float4 *)J.coef)[q], pv = ((const float4 *)J.prev)[q];
-                float4 ln;
-                ln.x = (xa[i].x - mu) * inv * g.x + bt.x;
-                ln.y = (xa[i].y - mu) * inv * g.y + bt.y;
-                ln.z = (xa[i].z - mu) * inv * g.z + bt.z;
-                ln.w = (xa[i].w - mu) * inv * g.w + bt.w;
-                if (wr) ((float4 *)J.lnout)[q] = ln;
-                xa[i].x = ln.x + cf.x * (pv.x - ln.x);
-                xa[i].y = ln.y + cf.y * (pv.y - ln.y);
-                xa[i].z = ln.z + cf.z * (pv.z - ln.z);
-                xa[i].w = ln.w + cf.w * (pv.w - ln.w);
-            }
-        } else if (J.pro == PRO_MUL) {
-#pragma unroll
-            for (int i = 0; i < Q; i++) {
-                const int q = tid + 256 * i;
-                const float4 g = q < K4 ? ((const float4 *)J.xmul)[q] : make_float4(0.f, 0.f, 0.f, 0.f);
-                xa[i].x *= g.x; xa[i].y *= g.y; xa[i].z *= g.z; xa[i].w *= g.w;
-            }
-        } else if (J.pro == PRO_SIGMOID) {
-#pragma unroll
-            for (int i = 0; i < Q; i++) {
-                xa[i].x = sigmoid_f(xa[i].x); xa[i].y = sigmoid_f(xa[i].y);
-                xa[i].z = sigmoid_f(xa[i].z); xa[i].w = sigmoid_f(xa[i].w);
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < Q; i++) {
-            const int q = tid + 256 * i;
-            if (q < K4) xs[((4 * q) % CW >> 2) * NC + (4 * q) / CW] = xa[i];
-        }
-    }
-    __syncthreads();
-    float acc = 0.0f;
-#pragma unroll
-    for (int j = 0; j < CPL; j++) {
-        const int cr = li + LPR * j;
-        const bool live = cr < NC;
-        const int c = live ? cr : NC - 1;
-        float xv[CW];
-#pragma unroll
-        for (int p = 0; p < P; p++) {
-            const float4 t = xs[p * NC + c];
-            xv[4 * p] = t.x; xv[4 * p + 1] = t.y; xv[4 * p + 2] = t.z; xv[4 * p + 3] = t.w;
-        }
-        if (FMT == FMT_I8) {
-            // w = s*q + z over one 16-weight chunk of a 128-group (model.rs:234-252)
-            float dx = 0.0f, d = 0.0f;
-#pragma unroll
-            for (int i = 0; i < CW; i++) dx += xv[i];
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const uint32_t wq = wv[j][q];
-                d = fmaf(xv[4 * q + 0], (float)(wq & 0xFFu), d);
-                d = fmaf(xv[4 * q + 1], (float)((wq >> 8) & 0xFFu), d);
-                d = fmaf(xv[4 * q + 2], (float)((wq >> 16) & 0xFFu), d);
-                d = fmaf(xv[4 * q + 3], (float)(wq >> 24), d);
-            }
-            const uint32_t sw = live ? szv[j] : 0u;
-            acc = fmaf(h2f(sw), d, fmaf(h2f(sw >> 16), dx, acc));
-        } else {
-            float d = 0.0f;
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const uint32_t wq = wv[j][q];
-                d = fmaf(xv[2 * q + 0], h2f(wq), d);
-                d = fmaf(xv[2 * q + 1], h2f(wq >> 16), d);
-            }
-            acc += live ? d : 0.0f;
-        }
-    }
-    acc = group_sum_last<LPR>(acc);
-    if (li == LPR - 1 && row0 < M) apply_epi(J, row0, 0, acc);
-}
-
-template <int CPL, int Q>
-__global__ __launch_bounds__(256) void k_gemv_os(GemvJobs jobs) {
-    extern __shared__ float4 xs4[];
-    const int bid = blockIdx.x;
-    if (bid == 0 && jobs.side.src)
-        for (int i = threadIdx.x; i < jobs.side.n; i += 256) jobs.side.dst[i] = jobs.side.src[i];
-    int ji = 0;
-    while (ji + 1 < jobs.n && bid >= jobs.blk_start[ji + 1]) ji++;
-    const GemvJob &J = jobs.j[ji];
-    const int rb = bid - jobs.blk_start[ji];
-    if (J.fmt == FMT_I8) {
-        if (J.lpr == 32) gemv_os_body<FMT_I8, 32, CPL, Q>(J, rb, xs4);
-        else gemv_os_body<FMT_I8, 64, CPL, Q>(J, rb, xs4);
-    } else {
-        if (J.lpr == 32) gemv_os_body<FMT_F16, 32, CPL, Q>(J, rb, xs4);
-        else gemv_os_body<FMT_F16, 64, CPL, Q>(J, rb, xs4);
-    }
-}
-
-// One-shot GEMV, second form: NT threads per block (NT/64 waves x 64/LPR
+// One-shot GEMV for one session: NT threads per block (NT/64 waves x 64/LPR
 // rows each).  Every vector load of the block (x and, for the LN-mix
 // prologue, gamma/beta/coef/prev) goes out before the weight loads and
 // returns ahead of them (vector memory returns in order), so the prologue
 // runs while the weights stream.  The per-chunk sums of x (zero-point term
 // of the int8 dot) are taken once per block into LDS instead of once per
-// row.  Wider blocks than k_gemv_os mean fewer copies of x and of the LN
-// vectors per CU, and one LN per 10-20 rows instead of per 4-8.
+// row.  Wide blocks mean fewer copies of x and of the LN vectors per CU,
+// and one LN per 10-20 rows.
 template <int NT>
 __device__ __forceinline__ float block_sum_nt(float v, float *red) {
     v = group_sum_last<64>(v);
@@ -1232,76 +692,6 @@ static int launch_os2(rsv_ctx *ctx, GemvJobs &jobs) {
     return 0;
 }
 
-// B=1 launch on the one-shot kernel: LN-mix prologues become one pre-pass
-// launch writing each distinct mixed vector once.  Returns 1 when the jobs
-// do not fit this path (the caller then uses the general kernel).
-static int launch_os(rsv_ctx *ctx, GemvJobs &jobs) {
-    int cpl_max = 0, kmax = 0;
-    for (int i = 0; i < jobs.n; i++) {
-        GemvJob &J = jobs.j[i];
-        const int nc = J.K / (J.fmt == FMT_I8 ? 16 : 8);
-        J.lpr = nc <= 32 * 5 ? 32 : 64;
-        const int cpl = (nc + J.lpr - 1) / J.lpr;
-        if (cpl > 10 || J.K > 10240 || J.K % 4 != 0 || nc < J.lpr / 2) return 1;
-        cpl_max = std::max(cpl_max, cpl);
-        kmax = std::max(kmax, J.K);
-    }
-    // LN-mix pre-pass: every LN-mix job of the launch must share x, LN and
-    // token-shift row (true of the decode layer); mixes are de-duplicated by
-    // coefficient vector
-    static const int in_kernel_mix = env_int("RSV_GEMV_OS_MIX", 1);
-    MixArgs ma{};
-    for (int i = 0; i < jobs.n; i++) {
-        GemvJob &J = jobs.j[i];
-        if (J.pro != PRO_LNMIX) continue;
-        if (in_kernel_mix) {
-            if (J.K > 3072) return 1;
-            continue;
-        }
-        if (J.K > kMixMaxK) return 1;
-        if (ma.nmix == 0) {
-            ma.x = J.x; ma.gamma = J.gamma; ma.beta = J.beta; ma.prev = J.prev; ma.K = J.K;
-        } else if (ma.x != J.x || ma.gamma != J.gamma || ma.beta != J.beta || ma.prev != J.prev || ma.K != J.K) {
-            return 1;
-        }
-        if (J.lnout) {
-            if (ma.lnout && ma.lnout != J.lnout) return 1;
-            ma.lnout = J.lnout;
-        }
-        int m = 0;
-        while (m < ma.nmix && ma.coef[m] != J.coef) m++;
-        if (m == ma.nmix) {
-            ma.coef[m] = J.coef;
-            ma.out[m] = ctx->mix_buf + (size_t)m * kMixMaxK;
-            ma.nmix++;
-        }
-        J.x = ma.out[m];
-        J.pro = PRO_NONE;
-    }
-    if (ma.nmix) {
-        hipLaunchKernelGGL(k_lnmix_pre, dim3((ma.K / 4 + 255) / 256), dim3(256), 0, ctx->stream, ma);
-        RSV_HIP(hipGetLastError());
-    }
-    int total = 0;
-    for (int i = 0; i < jobs.n; i++) {
-        GemvJob &J = jobs.j[i];
-        const int rpb = 4 * (64 / J.lpr);
-        J.nblk = (J.M + rpb - 1) / rpb;
-        jobs.blk_start[i] = total;
-        total += J.nblk;
-    }
-    jobs.blk_start[jobs.n] = total;
-    const size_t lds = (size_t)kmax * 4;
-    if (cpl_max <= 5 && kmax <= 3072)
-        hipLaunchKernelGGL((k_gemv_os<5, 3>), dim3(total), dim3(256), lds, ctx->stream, jobs);
-    else
-        hipLaunchKernelGGL((k_gemv_os<10, 10>), dim3(total), dim3(256), lds, ctx->stream, jobs);
-    RSV_HIP(hipGetLastError());
-    return 0;
-}
-
-
-
 int launch_gemv_jobs(rsv_ctx *ctx, GemvJobs &jobs, int batch) {
     if (jobs.n <= 0 || jobs.n > kMaxJobs) return RSV_FAIL("gemv: bad job count %d", jobs.n);
     if (batch <= 0) return RSV_FAIL("gemv: batch must be >= 1 (got %d)", batch);
@@ -1327,33 +717,10 @@ int launch_gemv_jobs(rsv_ctx *ctx, GemvJobs &jobs, int batch) {
         if (nc > ncmax) ncmax = nc;
     }
     if (jobs.side.src && (!jobs.side.dst || jobs.side.n <= 0)) return RSV_FAIL("gemv: bad side copy");
-    // B=1: launches with an LN-mix prologue take the register-resident kernel
-    // (the prologue runs inside it), the others the one-shot kernel
-    static const int b1_kernel = env_int("RSV_GEMV_B1", 4);  // 4 one-shot v2, 3 by prologue, 2 one-shot, 1 register, 0 general
-    if (batch == 1 && b1_kernel == 4) {
+    // B=1: the one-shot kernel (prologues inside it) where the jobs fit it
+    if (batch == 1) {
         const int rc = launch_os2(ctx, jobs);
         if (rc <= 0) return rc;
-    }
-    bool lnmix = false;
-    for (int i = 0; i < jobs.n; i++) lnmix |= jobs.j[i].pro == PRO_LNMIX;
-    if (batch == 1 && (b1_kernel == 2 || (b1_kernel == 3 && !lnmix))) {
-        const int rc = launch_os(ctx, jobs);
-        if (rc <= 0) return rc;
-    }
-    if (batch == 1 && b1_kernel >= 1) {
-        bool ok = true;
-        for (int i = 0; i < jobs.n && ok; i++) {
-            GemvJob &J = jobs.j[i];
-            J.ks = reg_slices(J);
-            ok = J.ks > 0;
-        }
-        if (ok) {
-            const int cus = ctx->sm_count > 0 ? ctx->sm_count : 256;
-            static const int ru = env_int("RSV_GEMV_RU", 2);
-            static const int bpc = env_int("RSV_GEMV_BPC", 2);
-            if (ru == 4) return launch_reg<4>(ctx, jobs, bpc * cus);
-            return launch_reg<2>(ctx, jobs, bpc * cus);
-        }
     }
     // Lanes per row: a full wave when rows are long, a quarter wave for the
     // short LoRA-up rows (k = rank).  Long rows (ffn.value) keep fewer rows

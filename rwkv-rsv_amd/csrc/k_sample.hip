@@ -208,7 +208,8 @@ __global__ __launch_bounds__(kSampBS) void k_sample(const float *__restrict__ lo
     const float top_p = sp[2];
     const uint32_t seed = __float_as_uint(sp[3]);
     const float rep = sp[4], freq = sp[5], pres = sp[6];
-    const uint32_t hist_len = __float_as_uint(sp[7]);
+    // the row's history length, never past the row's own history capacity
+    const uint32_t hist_len = min(__float_as_uint(sp[7]), (uint32_t)max(hist_stride, 0));
     const bool do_topk = top_k > 0u && top_k < (uint32_t)n;
     const int K = do_topk ? (int)top_k : 0;
     const bool fast = K > 0 && K <= 50;

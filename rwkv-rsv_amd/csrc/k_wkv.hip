@@ -522,15 +522,11 @@ int launch_wkv7_lora(rsv_ctx *ctx, const WkvLoraArgs &a, int batch) {
     }
     if (L4 > 1024) return RSV_FAIL("wkv7_lora: LoRA ranks sum to %d (max 1024)", L4);
     // batches of 16 and more with fp16 operands and ranks summing to at most
-    // 512: SB sessions per block (the head's LoRA-up rows read once per
-    // block); RSV_WKV_LORA_SB = 0 keeps one block per (head, session)
-    const char *sbe = getenv("RSV_WKV_LORA_SB");
-    const int sb = sbe ? atoi(sbe) : 4;
-    if (a.f16_io && batch >= 16 && L4 <= 512 && (sb == 4 || sb == 8 || sb == 16)) {
-        const int nb = (batch + sb - 1) / sb;
-        if (sb == 4) hipLaunchKernelGGL(k_wkv7_lora_mb<4>, dim3(a.H, nb), dim3(256), 0, ctx->stream, a, batch);
-        else if (sb == 8) hipLaunchKernelGGL(k_wkv7_lora_mb<8>, dim3(a.H, nb), dim3(256), 0, ctx->stream, a, batch);
-        else hipLaunchKernelGGL(k_wkv7_lora_mb<16>, dim3(a.H, nb), dim3(256), 0, ctx->stream, a, batch);
+    // 512: 4 sessions per block (the head's LoRA-up rows read once per block;
+    // 8 or 16 sessions per block measured slower: too few blocks to spread
+    // the per-CU traffic)
+    if (a.f16_io && batch >= 16 && L4 <= 512) {
+        hipLaunchKernelGGL(k_wkv7_lora_mb<4>, dim3(a.H, (batch + 3) / 4), dim3(256), 0, ctx->stream, a, batch);
     } else if (a.f16_io) hipLaunchKernelGGL(k_wkv7_lora<true>, dim3(a.H, batch), dim3(256), 0, ctx->stream, a);
     else hipLaunchKernelGGL(k_wkv7_lora<false>, dim3(a.H, batch), dim3(256), 0, ctx->stream, a);
     RSV_HIP(hipGetLastError());

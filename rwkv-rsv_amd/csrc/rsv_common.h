@@ -74,7 +74,6 @@ struct GemvJob {
     int lpr;       // lanes per row (one-shot B=1 kernel; filled by the launcher)
 };
 constexpr int kMaxJobs = 8;
-constexpr int kMixMaxK = 16384;  // longest row the B=1 LN-mix pre-pass serves
 // A side copy done by the first block column of a launch: dst[b, :n] =
 // src[b, :n] for the launch's batch rows (moves a token-shift LN row from a
 // scratch buffer into the state once no block of the launch reads it).
@@ -114,10 +113,6 @@ struct rsv_ctx {
     // with the context so that graph capture never allocates)
     float *skinny_ws = nullptr;
     size_t skinny_ws_cap = 0;
-    // LN-mix vectors of a B=1 GEMV launch (kMaxJobs x kMixMaxK floats)
-    float *mix_buf = nullptr;
-    // persistent single-session decode step (k_mega.hip), built on demand
-    void *mega = nullptr;  // k_mega.hip plan (device tables + scratch)
     // arrival counters of the sparse ffn.value reduction (zeroed at create; each launch leaves them zero)
     unsigned *sparse_cnt = nullptr;
     size_t sparse_cnt_cap = 0;
@@ -268,33 +263,4 @@ int launch_tile_ffn_value(rsv_ctx *ctx, const uint8_t *idx, const uint32_t *sz, 
                           int c, int fh);
 int launch_ffn_sparse(rsv_ctx *ctx, const float *r2, const _Float16 *vt, float *x, int c, int fh, int batch);
 
-// Persistent single-session decode step (k_mega.hip): device pointers of one
-// layer and of the model around the layers.
-struct MegaLayerDev {
-    const float *ln1_w, *ln1_b, *ln2_w, *ln2_b, *lnx_w, *lnx_b;
-    const float *x_r, *x_w, *x_k, *x_v, *x_a, *x_g, *ffn_x_k;
-    const float *w0, *a0, *v0, *r_k, *k_k, *k_a;
-    const _Float16 *down[4];  // LoRA w1, a1, v1, g1: [mid, C]
-    const _Float16 *up[4];    // LoRA w2, a2, v2, g2: [C, mid]
-    const uint8_t *idx[6];    // int8 receptance, key, value, output, ffn.key, ffn.value
-    const uint32_t *sz[6];
-    float *tmix, *cmix, *rnn; // state rows of this layer (one session)
-};
-struct MegaModelDev {
-    int n_layer, C, F, H, V;
-    int mid[4];  // w, a, v, g LoRA ranks
-    const float *emb;  // LN0(emb) fp32 [V, C]
-    const float *lno_w, *lno_b;
-    const void *head;  // int8 idx or fp16 [V, C]
-    const uint32_t *head_sz;
-    int head_i8;
-    const float *scale_w;
-    float *v_first;
-    float ln_eps, l2_eps, gn_eps;
-};
-int mega_build(rsv_ctx *ctx, const MegaModelDev &m, const std::vector<MegaLayerDev> &layers);
-int mega_launch(rsv_ctx *ctx, const uint32_t *token_in, uint32_t *token_out, float *logits);
-int mega_status(rsv_ctx *ctx, int *aborted);
-int mega_vocab(rsv_ctx *ctx);
-void mega_free(rsv_ctx *ctx);
 }  // namespace rsv

@@ -76,7 +76,7 @@ def _ctype(decl):
     if base == "rsv_int8":
         return ctypes.POINTER(Int8Handle)
     if base in ("rsv_model_info", "rsv_sampler_params", "rsv_gemv_job", "rsv_mm_job", "rsv_serve_step",
-                "rsv_mega_model", "rsv_mega_layer", "rsv_wkv_lora"):
+                "rsv_wkv_lora"):
         return ctypes.c_void_p
     return ctypes.POINTER(scalars[base])
 

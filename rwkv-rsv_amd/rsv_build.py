@@ -18,7 +18,7 @@ COMMON = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-I", INC, "-I
           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-Wno-unused-result", "-Wno-unused-value"]
 
 BACKEND_SRCS = ["backend.cpp", "k_gemv.hip", "k_wkv.hip", "k_misc.hip", "k_sample.hip", "k_gemm.hip",
-                "k_skinny.hip", "k_mega.hip", "k_sparse.hip"]
+                "k_skinny.hip", "k_sparse.hip"]
 HOST_SRCS = ["host.cpp"]
 
 

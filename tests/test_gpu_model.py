@@ -247,7 +247,6 @@ def test_config1_golden(tiny_cfg1):
 def test_fused_decode_matches_trait_op_sequence(bundles, kind, monkeypatch):
     """The six-launch fused layer equals the reference's one-op-per-method
     sequence (norm_lerp6, stage1, chain4, fuse_ka_dplr_norm, ...)."""
-    monkeypatch.setenv("RSV_MEGA", "0")  # the six-launch layer, not the persistent step
     b, _ = bundles[kind]
     p = _prompt(10, 30)
     b.reset()
@@ -382,7 +381,6 @@ def test_fused_lora_wkv_matches_two_launches(bundles, kind, monkeypatch):
     """rsv_wkv7_lora_decode (LoRA-up chain + WKV7 + GroupNorm in one launch)
     equals the two-launch form (gemv_lowrank_chain4 then fuse_ka_dplr_norm)
     on logits and state, fp32 throughout."""
-    monkeypatch.setenv("RSV_MEGA", "0")
     b, _ = bundles[kind]
     p = _prompt(12, 52)
     monkeypatch.setenv("RSV_WKV_LORA", "0")
@@ -398,14 +396,12 @@ def test_fused_lora_wkv_matches_two_launches(bundles, kind, monkeypatch):
     assert rel_rmse(s_one, s_two) <= 1e-5
 
 
-@pytest.mark.parametrize("kind,sb,B", [("f16", "8", 20), ("i8", "8", 20), ("i8", "4", 37), ("i8", "16", 37),
-                                       ("i8", "0", 20)])
-def test_batched_fused_lora_wkv(bundles, kind, sb, B, monkeypatch):
+@pytest.mark.parametrize("kind,B", [("f16", 20), ("i8", 20), ("i8", 37)])
+def test_batched_fused_lora_wkv(bundles, kind, B, monkeypatch):
     """The batched layer's fused LoRA-up + WKV7 launch (RSV_WKV_LORA_MM=1,
-    fp16 operands in and out) equals its two-launch form to fp32 rounding:
-    the SB-sessions-per-block kernel (SB = 4, 8, 16, batches that leave the
-    last block partly empty) and the one-block-per-session kernel (SB = 0)."""
-    monkeypatch.setenv("RSV_WKV_LORA_SB", sb)
+    fp16 operands in and out, 4 sessions per block) equals its two-launch
+    form to fp32 rounding, also on batches that leave the last block partly
+    empty."""
     b, _ = bundles[kind]
     prompts = [_prompt(3 + (i % 5), 60 + i) for i in range(B)]
     toks = np.array([(11 * i + 5) % SMALL["vocab"] for i in range(B)], np.uint32)
@@ -424,9 +420,7 @@ def test_batched_fused_lora_wkv(bundles, kind, sb, B, monkeypatch):
 @pytest.mark.parametrize("kind", ["i8", "i8g"])
 def test_prefill_f16_weight_copies_bit_identical(bundles, kind, monkeypatch):
     """Prefill of more than 128 packed rows runs its int8 layer matrices on
-    fp16 copies made with the int8 loader's roundings (and the DMA-staged
-    GEMM); logits and state equal those of the int8 loader bit for bit."""
-    monkeypatch.setenv("RSV_MEGA", "0")
+    fp16 copies made with the int8 loader's roundings; logits and state equal those of the int8 loader bit for bit."""
     b, _ = bundles[kind]
     prompts = [_prompt(90 + 17 * i, 300 + i) for i in range(3)]
     out = {}
@@ -441,13 +435,12 @@ def test_prefill_f16_weight_copies_bit_identical(bundles, kind, monkeypatch):
 
 
 @pytest.mark.parametrize("env", ["RSV_SKINNY_V5=0", "RSV_SKINNY_SK1=0", "RSV_SKINNY_MIXED=0", "RSV_SKINNY_MAX_SPLIT=4",
-                                 "RSV_SKINNY_BLOCKS_PER_CU=1", "RSV_GEMM_V2=0", "RSV_WKV_LORA_MM=0"])
+                                 "RSV_SKINNY_BLOCKS_PER_CU=1", "RSV_WKV_LORA_MM=0"])
 def test_batched_alternative_kernels_agree(bundles, env, monkeypatch):
     """Each selectable alternative of the batched paths (older skinny GEMM
-    forms, split limits, the first prefill GEMM, the two-launch LoRA-up +
+    forms, split limits, the two-launch LoRA-up +
     WKV7) gives the default's logits and state to fp32 rounding, on a
     prefill of more than 128 packed rows and batched decode steps."""
-    monkeypatch.setenv("RSV_MEGA", "0")
     b, _ = bundles["i8"]
     B = 20
     prompts = [_prompt(4 + 9 * (i % 4), 500 + i) for i in range(B)]
