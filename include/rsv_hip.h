@@ -221,6 +221,18 @@ int rsv_sample_into_host_seeded(rsv_ctx *ctx, uint32_t logits, uint32_t token, u
 int rsv_sample_into_host_seeded_batch(rsv_ctx *ctx, uint32_t logits, uint32_t token, uint64_t n,
                                       uint32_t temp, uint32_t mask, uint32_t counter,
                                       uint32_t sampler, uint32_t hist, uint64_t batch);
+/* rsv_sample without allocation.  No counterpart in the reference: it is
+ * for callers that cannot allocate (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  Same pipeline and result
+ * as rsv_sample; the history is a device U32 tensor `hist` holding hist_len
+ * token ids (ignored when hist_len is 0) instead of a host array.  The work
+ * area (temp, counter, sampler row) is one static device array per GPU of
+ * 2*262144+64 words (2 MiB), held until the process ends: n above 262144 is
+ * rejected.  Calls that overlap on one GPU (several contexts or threads on
+ * the same device) race on that array; calls in one stream do not. */
+int rsv_sample_noalloc(rsv_ctx *ctx, uint32_t logits, uint32_t token, uint64_t n, float temperature,
+                       uint32_t top_k, float top_p, uint32_t seed, float repetition_penalty,
+                       float frequency_penalty, float presence_penalty, uint32_t hist, uint64_t hist_len);
 int rsv_record_token(rsv_ctx *ctx, uint32_t in_tok, uint32_t out_seq, uint32_t cnt);
 int rsv_record_tokens(rsv_ctx *ctx, uint32_t in_tok, uint32_t out_seq, uint32_t cnt, uint64_t stride,
                       uint64_t batch);

@@ -121,6 +121,13 @@ int rsv_create(int device, rsv_ctx **out) {
         delete ctx;
         return RSV_FAIL("rsv_create: workspace allocation failed");
     }
+    if (sample_scratch_init(device)) {
+        const std::string why = rsv_last_error();
+        hipFree(ctx->skinny_ws);
+        hipStreamDestroy(ctx->stream);
+        delete ctx;
+        return RSV_FAIL("rsv_create: %s", why.c_str());
+    }
     ctx->sparse_cnt_cap = 1 << 16;
     if (hipMalloc(&ctx->sparse_cnt, ctx->sparse_cnt_cap * 4) != hipSuccess ||
         hipMemset(ctx->sparse_cnt, 0, ctx->sparse_cnt_cap * 4) != hipSuccess) {
@@ -927,6 +934,34 @@ int rsv_sample(rsv_ctx *ctx, uint32_t logits, uint32_t token, uint64_t n, float 
         return -1;
     return launch_sample(ctx, F32P(l), U32P(t), (int)n, temp, counter, srow, hist_len ? ctx->hist_dev : nullptr,
                          (int)hist_len, 1);
+}
+
+int rsv_sample_noalloc(rsv_ctx *ctx, uint32_t logits, uint32_t token, uint64_t n, float temperature, uint32_t top_k,
+                       float top_p, uint32_t seed, float rep, float freq, float pres, uint32_t hist,
+                       uint64_t hist_len) {
+    CHECK_CTX();
+    if (n == 0 || n > kNoAllocMaxN)
+        return RSV_FAIL("sample_noalloc: n=%llu outside 1..%llu (the static work area's limit)",
+                        (unsigned long long)n, (unsigned long long)kNoAllocMaxN);
+    OPND(l, logits, RSV_F32, n, "sample_noalloc logits");
+    OPND(t, token, RSV_U32, 1, "sample_noalloc token");
+    const uint32_t *hp = nullptr;
+    if (hist_len > 0) {
+        if (hist_len > 0xFFFFFFFFull) return RSV_FAIL("sample_noalloc: hist_len too large");
+        OPND(hh, hist, RSV_U32, hist_len, "sample_noalloc history");
+        hp = U32P(hh);
+    }
+    uint32_t *work = sample_scratch(ctx->device);
+    if (!work) return RSV_FAIL("sample_noalloc: no work area on device %d", ctx->device);
+    // temp [n] f32, counter [n] u32, sampler row [8]: every word the kernel
+    // reads is written first in this call (the row here, temp and counter in
+    // the kernel), so the previous call's contents do not matter
+    float *temp = (float *)work;
+    uint32_t *counter = work + n;
+    float *srow = (float *)(work + 2 * n);
+    if (launch_store_sampler(ctx, srow, temperature, top_k, top_p, &seed, 1, rep, freq, pres, (uint32_t)hist_len))
+        return -1;
+    return launch_sample(ctx, F32P(l), U32P(t), (int)n, temp, counter, srow, hp, (int)hist_len, 1);
 }
 
 int rsv_record_tokens(rsv_ctx *ctx, uint32_t in_tok, uint32_t out_seq, uint32_t cnt, uint64_t stride, uint64_t batch) {

@@ -18,6 +18,8 @@
 #include "rsv_common.h"
 #include "k_dpp.h"
 
+#include <mutex>
+
 namespace rsv {
 
 constexpr int kSampBS = 1024;
@@ -366,6 +368,38 @@ __global__ __launch_bounds__(kSampBS) void k_sample(const float *__restrict__ lo
         }
         token[b] = (uint32_t)chosen;
     }
+}
+
+// ------------------------------------------------ allocation-free sampling
+// Work area of rsv_sample_noalloc: temp [n] f32, counter [n] u32 and one
+// sampler row [8], for n up to kNoAllocMaxN.  One copy per device, held
+// until the process ends.  Host code never passes `scratch` itself to a
+// kernel (on the host the name is not a device address): each device's
+// address comes from hipGetSymbolAddress, taken once per device with that
+// device current, and only that address is used.
+static __device__ __align__(256) uint32_t scratch[kNoAllocWords];
+
+static std::mutex g_scratch_mu;
+static void *g_scratch_ptr[kMaxDevices];
+
+int sample_scratch_init(int device) {
+    if (device < 0 || device >= kMaxDevices) return RSV_FAIL("sample scratch: device %d out of range", device);
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (g_scratch_ptr[device]) return 0;
+    int cur = -1;
+    RSV_HIP(hipGetDevice(&cur));
+    if (cur != device) return RSV_FAIL("sample scratch: device %d is not current (%d is)", device, cur);
+    void *p = nullptr;
+    RSV_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (!p) return RSV_FAIL("sample scratch: no device address");
+    g_scratch_ptr[device] = p;
+    return 0;
+}
+
+uint32_t *sample_scratch(int device) {
+    if (device < 0 || device >= kMaxDevices) return nullptr;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    return (uint32_t *)g_scratch_ptr[device];
 }
 
 int launch_sample(rsv_ctx *ctx, const float *logits, uint32_t *token, int n, float *temp, uint32_t *counter,

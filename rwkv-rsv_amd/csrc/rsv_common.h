@@ -146,6 +146,13 @@ int launch_set_u32(rsv_ctx *ctx, uint32_t *dst, const uint32_t *vals, int n);
 int launch_store_sampler(rsv_ctx *ctx, float *dst, float temperature, uint32_t top_k, float top_p,
                          const uint32_t *seeds, int batch, float rep, float freq, float pres,
                          uint32_t hist_len);
+// allocation-free sampling (k_sample.hip): the static work area's size, its
+// per-device set-up (with the device current) and its device address
+constexpr uint64_t kNoAllocMaxN = 262144;
+constexpr uint64_t kNoAllocWords = 2 * kNoAllocMaxN + 64;
+constexpr int kMaxDevices = 64;
+int sample_scratch_init(int device);
+uint32_t *sample_scratch(int device);
 int launch_sample(rsv_ctx *ctx, const float *logits, uint32_t *token, int n, float *temp,
                   uint32_t *counter, const float *sampler, const uint32_t *hist, int hist_stride,
                   int batch);
