@@ -64,8 +64,16 @@ int rsv_download(rsv_ctx *ctx, uint32_t id, float *out, uint64_t len);          
 int rsv_download_u32(rsv_ctx *ctx, uint32_t id, uint32_t *out, uint64_t len);                /* :60 */
 int rsv_copy_device(rsv_ctx *ctx, uint32_t src, uint32_t dst);                              /* :679 */
 int rsv_copy_device_f16(rsv_ctx *ctx, uint32_t src, uint32_t dst);                          /* :155 */
-/* Share another context's tensors (same device, not freed by this ctx). :141 */
+/* Share another context's tensors (backend.rs:137-142): every live tensor
+ * of `src` appears in `ctx` under the same id and memory.  The destination
+ * must hold no tensors yet.  Allocations are shared, not borrowed: each
+ * stays valid until every context holding it has freed it (or been
+ * destroyed), so either context may go first.  Later tensors of either
+ * context get ids of their own table. */
 int rsv_import_tensors(rsv_ctx *ctx, rsv_ctx *src);
+/* Device ordinal of a context (no reference counterpart: build_shared
+ * creates the second context on the source's device). */
+int rsv_context_device(rsv_ctx *ctx, int *device);
 int rsv_synchronize(rsv_ctx *ctx);
 
 /* ---- batching and graphs (backend.rs:63-109) */

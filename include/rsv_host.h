@@ -45,6 +45,11 @@ const char *rsv_host_last_error(void);
 
 /* ModelBuilder::new(path).build() (gpu_model.rs:3697) on HIP device `device`. */
 int rsv_model_build(const char *path, int device, rsv_bundle **out);
+/* GpuModel::build_shared (gpu_model.rs:594-628): a second bundle on the same
+ * device sharing every weight tensor of `src` (no copy), with its own
+ * backend context (stream), work buffers and state.  Either bundle may be
+ * freed first; shared memory is released when both are. */
+int rsv_bundle_build_shared(rsv_bundle *src, rsv_bundle **out);
 int rsv_bundle_free(rsv_bundle *b);
 int rsv_bundle_info(rsv_bundle *b, rsv_model_info *info);
 

@@ -4,6 +4,7 @@
 // so a shape mismatch is an error status, never an out-of-bounds kernel.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <mutex>
@@ -148,8 +149,7 @@ int rsv_destroy(rsv_ctx *ctx) {
     if (ctx->graph_exec) hipGraphExecDestroy(ctx->graph_exec);
     if (ctx->graph) hipGraphDestroy(ctx->graph);
     for (auto &kv : ctx->prefill_graphs) hipGraphExecDestroy(kv.second);
-    for (auto &t : ctx->tensors)
-        if (t.live && !t.foreign && t.ptr) hipFree(t.ptr);
+    ctx->tensors.clear();  // drops this context's hold on each allocation
     if (ctx->hist_dev) hipFree(ctx->hist_dev);
     if (ctx->sample_work) hipFree(ctx->sample_work);
     if (ctx->skinny_ws) hipFree(ctx->skinny_ws);
@@ -185,6 +185,9 @@ int rsv_tensor_create(rsv_ctx *ctx, uint64_t len, int dtype, uint32_t *id) {
     const size_t bytes = (size_t)(len ? len : 1) * dtype_size(dtype);
     // pad to 64 bytes so 16-byte vector tails never cross the allocation
     RSV_HIP(hipMalloc(&t.ptr, (bytes + 63) & ~(size_t)63));
+    t.mem = std::make_shared<DevMem>();
+    t.mem->ptr = t.ptr;
+    t.mem->device = ctx->device;
     RSV_HIP(hipMemsetAsync(t.ptr, 0, (bytes + 63) & ~(size_t)63, ctx->stream));
     t.live = true;
     if (!ctx->free_ids.empty()) {
@@ -202,10 +205,14 @@ int rsv_tensor_free(rsv_ctx *ctx, uint32_t id) {
     CHECK_CTX();
     Tensor *t = get_tensor(ctx, id);
     if (!t) return 0;  // freeing an unknown id is a no-op, like the reference
-    if (!t->foreign) {
-        hipStreamSynchronize(ctx->stream);
-        hipFree(t->ptr);
-    }
+    if (ctx->capturing || ctx->prefill_capturing) return RSV_FAIL("tensor_free: not allowed during graph capture");
+    // this context's work on the tensor finishes before its hold is dropped;
+    // the memory itself goes when no context holds it any more
+    hipStreamSynchronize(ctx->stream);
+    // captured prefill graphs hold device pointers: one of them may point
+    // at this memory, so every such graph is dropped (recaptured on next use)
+    for (auto &kv : ctx->prefill_graphs) hipGraphExecDestroy(kv.second);
+    ctx->prefill_graphs.clear();
     *t = Tensor();
     ctx->free_ids.push_back(id);
     return 0;
@@ -324,15 +331,38 @@ int rsv_copy_device(rsv_ctx *ctx, uint32_t src, uint32_t dst) {
 
 int rsv_copy_device_f16(rsv_ctx *ctx, uint32_t src, uint32_t dst) { return rsv_copy_device(ctx, src, dst); }
 
+int rsv_context_device(rsv_ctx *ctx, int *device) {
+    if (!ctx || !device) return RSV_FAIL("context_device: null argument");
+    *device = ctx->device;
+    return 0;
+}
+
 int rsv_import_tensors(rsv_ctx *ctx, rsv_ctx *src) {
     CHECK_CTX();
     if (!src) return RSV_FAIL("import_tensors: null source");
     if (src->device != ctx->device) return RSV_FAIL("import_tensors: source is on device %d", src->device);
+    if (src == ctx) return RSV_FAIL("import_tensors: source is the destination");
     for (auto &t : ctx->tensors)
-        if (t.live && !t.foreign) return RSV_FAIL("import_tensors: destination already owns tensors");
-    ctx->tensors = src->tensors;
-    for (auto &t : ctx->tensors) t.foreign = true;
+        if (t.live) return RSV_FAIL("import_tensors: destination already holds tensors");
+    // Every live tensor of the source keeps its id and its memory here (the
+    // allocation is shared: it stays valid until every holder has freed it,
+    // so freeing in either context never leaves the other with a dangling
+    // pointer).  Ids that are dead in the source are free here, and later
+    // tensors of this context take those or ids past the source's table;
+    // ids are per context, so the two tables may diverge from then on.
+    ctx->tensors.clear();
     ctx->free_ids.clear();
+    ctx->tensors.reserve(src->tensors.size());
+    for (size_t i = 0; i < src->tensors.size(); i++) {
+        Tensor t = src->tensors[i];
+        if (t.live) t.foreign = true;
+        else {
+            t = Tensor();
+            ctx->free_ids.push_back((uint32_t)i);
+        }
+        ctx->tensors.push_back(t);
+    }
+    std::reverse(ctx->free_ids.begin(), ctx->free_ids.end());
     return 0;
 }
 
@@ -428,7 +458,12 @@ int rsv_graph_replay(rsv_ctx *ctx) {
 
 int rsv_prefill_graph_valid(rsv_ctx *ctx, uint64_t t, int *valid) {
     CHECK_CTX();
+    if (!valid) return RSV_FAIL("prefill_graph_valid: null out");
     *valid = ctx->prefill_graphs.count(t) ? 1 : 0;
+    // a valid graph becomes the one rsv_prefill_graph_replay runs (the
+    // reference replays the last captured T, which is the wrong graph when
+    // chunk sizes alternate)
+    if (*valid) ctx->prefill_t = t;
     return 0;
 }
 

@@ -25,6 +25,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <chrono>
 #include <cmath>
 #include <cstdarg>
@@ -258,6 +259,7 @@ struct Layer {
 
 struct GpuState {
     uint64_t batch = 1;
+    uint64_t serial = 0;  // distinct per state: part of the prefill graph key (graphs hold its tensors)
     std::vector<uint32_t> tmix_x, rnn, cmix_x;  // per layer
     uint32_t v_first = NONE;                    // [batch, C]
 };
@@ -508,7 +510,9 @@ int load_model(rsv_bundle *b, const char *path) {
 int state_create(rsv_bundle *b, uint64_t batch, GpuState &s) {
     const rsv_model_info &I = b->info;
     const uint64_t C = I.n_embd, HNN = I.n_head * I.head_size * I.head_size;
+    static std::atomic<uint64_t> next_serial{1};
     s.batch = batch;
+    s.serial = next_serial++;
     s.tmix_x.assign(I.n_layer, NONE);
     s.rnn.assign(I.n_layer, NONE);
     s.cmix_x.assign(I.n_layer, NONE);
@@ -1052,6 +1056,13 @@ int prefill_weights(rsv_bundle *b) {
     return 0;
 }
 
+// PREFILL_GRAPH=1: prefill chunks replay a HIP graph captured for their
+// shape (the reference's CUDA prefill graph, gpu_model.rs:2440-2450).
+bool prefill_graph_on() {
+    const char *e = getenv("PREFILL_GRAPH");
+    return e && e[0] == '1' && e[1] == 0;
+}
+
 // Packed prefill of non-empty segments into state slots; logits (optional)
 // receives nseg*vocab floats (last token of each segment).  With head set
 // and no host buffer the logits stay on the device in b->seq.logits.
@@ -1099,83 +1110,109 @@ int prefill(rsv_bundle *b, GpuState &s, const std::vector<Seg> &segs, float *log
     CK(rsv_upload_u32(c, q.seg_slot, sl.data(), S));
     CK(rsv_upload_u32(c, q.seg_last, last.data(), S));
 
-    CK(rsv_gather_rows_device_f16(c, b->emb_ln, q.x, q.tok, C, T));
-    for (uint64_t i = 0; i < I.n_layer; i++) {
-        Layer &L = b->layers[i];
-        const uint32_t coef6[6] = {L.x_r, L.x_w, L.x_k, L.x_v, L.x_a, L.x_g};
-        CK(rsv_seq_norm_mix(c, q.x, s.tmix_x[i], L.ln1_w, L.ln1_b, coef6, q.mix, 6, q.row_prev, T, C, LN_EPS));
-        CK(rsv_seq_state_store(c, q.x, s.tmix_x[i], L.ln1_w, L.ln1_b, q.seg_last, q.seg_slot, S, C, LN_EPS));
-        const uint32_t xr = q.mix[0], xw = q.mix[1], xk = q.mix[2], xv = q.mix[3], xa = q.mix[4], xg = q.mix[5];
-        if (small) {
-            rsv_mm_job j1[7] = {
-                mm_job(L.rw, xr, q.r, 0), mm_job(L.kw, xk, q.k, 0), mm_job(L.vw, xv, q.v, 0),
-                mm_job(L.lv1, xv, q.vmid, 0), mm_job(L.lw1, xw, q.wmid, 4),
-                mm_job(L.la1, xa, q.amid, 0), mm_job(L.lg1, xg, q.gmid, 8),
-            };
-            CK(rsv_gemm_skinny(c, j1, 7, T));
-        } else {
-            // r/k/v and the four LoRA-down products in one launch
-            rsv_mm_job j1[7] = {
-                gemm_job(L.rw, xr, q.r, 0), gemm_job(L.kw, xk, q.k, 0), gemm_job(L.vw, xv, q.v, 0),
-                gemm_job(L.lv1, xv, q.vmid, 0), gemm_job(L.lw1, xw, q.wmid, 4),
-                gemm_job(L.la1, xa, q.amid, 0), gemm_job(L.lg1, xg, q.gmid, 8),
-            };
-            CK(rsv_gemm_multi(c, j1, 7, T));
+    // Everything from the embedding gather to the head is enqueue-only, so
+    // with PREFILL_GRAPH=1 it is captured once per (rows, segments, state,
+    // head) and replayed for later chunks of the same shape
+    // (gpu_model.rs:2440-2507); the uploads above and the logits download
+    // below stay outside the graph.
+    const bool want_head = logits || head;
+    auto enqueue = [&]() -> int {
+        CK(rsv_gather_rows_device_f16(c, b->emb_ln, q.x, q.tok, C, T));
+        for (uint64_t i = 0; i < I.n_layer; i++) {
+            Layer &L = b->layers[i];
+            const uint32_t coef6[6] = {L.x_r, L.x_w, L.x_k, L.x_v, L.x_a, L.x_g};
+            CK(rsv_seq_norm_mix(c, q.x, s.tmix_x[i], L.ln1_w, L.ln1_b, coef6, q.mix, 6, q.row_prev, T, C, LN_EPS));
+            CK(rsv_seq_state_store(c, q.x, s.tmix_x[i], L.ln1_w, L.ln1_b, q.seg_last, q.seg_slot, S, C, LN_EPS));
+            const uint32_t xr = q.mix[0], xw = q.mix[1], xk = q.mix[2], xv = q.mix[3], xa = q.mix[4], xg = q.mix[5];
+            if (small) {
+                rsv_mm_job j1[7] = {
+                    mm_job(L.rw, xr, q.r, 0), mm_job(L.kw, xk, q.k, 0), mm_job(L.vw, xv, q.v, 0),
+                    mm_job(L.lv1, xv, q.vmid, 0), mm_job(L.lw1, xw, q.wmid, 4),
+                    mm_job(L.la1, xa, q.amid, 0), mm_job(L.lg1, xg, q.gmid, 8),
+                };
+                CK(rsv_gemm_skinny(c, j1, 7, T));
+            } else {
+                // r/k/v and the four LoRA-down products in one launch
+                rsv_mm_job j1[7] = {
+                    gemm_job(L.rw, xr, q.r, 0), gemm_job(L.kw, xk, q.k, 0), gemm_job(L.vw, xv, q.v, 0),
+                    gemm_job(L.lv1, xv, q.vmid, 0), gemm_job(L.lw1, xw, q.wmid, 4),
+                    gemm_job(L.la1, xa, q.amid, 0), gemm_job(L.lg1, xg, q.gmid, 8),
+                };
+                CK(rsv_gemm_multi(c, j1, 7, T));
+            }
+            if (i == 0) {
+                CK(rsv_copy_device(c, q.v, q.vf));
+                CK(rsv_copy_rows(c, q.v, s.v_first, q.seg_last, q.seg_slot, S, C));
+            }
+            if (small) {
+                rsv_mm_job j2[4] = {mm_job(L.lw2, q.wmid, q.w, 5), mm_job(L.la2, q.amid, q.a, 6),
+                                    mm_job(L.lv2, q.vmid, q.v, 7), mm_job(L.lg2, q.gmid, q.g, 0)};
+                j2[0].bias = L.w0;
+                j2[0].scale = b->scale_w;
+                j2[1].bias = L.a0;
+                j2[2].bias = L.v0;
+                j2[2].aux = q.vf;
+                CK(rsv_gemm_skinny(c, j2, 4, T));
+            } else {
+                // the LoRA-up chain in one launch
+                rsv_mm_job j2[4] = {gemm_job(L.lw2, q.wmid, q.w, 5), gemm_job(L.la2, q.amid, q.a, 6),
+                                    gemm_job(L.lv2, q.vmid, q.v, 7), gemm_job(L.lg2, q.gmid, q.g, 0)};
+                j2[0].bias = L.w0;
+                j2[0].scale = b->scale_w;
+                j2[1].bias = L.a0;
+                j2[2].bias = L.v0;
+                j2[2].aux = q.vf;
+                CK(rsv_gemm_multi(c, j2, 4, T));
+            }
+            CK(rsv_wkv7_seq_ragged(c, s.rnn[i], q.r, q.w, q.k, q.v, q.a, L.k_k, L.k_a, L.r_k, L.lnx_w, L.lnx_b, q.yn,
+                                   q.seg_start, q.seg_len, q.seg_slot, S, H, N, GN_EPS));
+            CK(rsv_mul_to_f16(c, q.yn, q.g, q.yg, T * C));
+            if (small) {
+                rsv_mm_job j4 = mm_job(L.ow, q.yg, q.x, 2);
+                CK(rsv_gemm_skinny(c, &j4, 1, T));
+            } else {
+                HK(gemm_lin(b, L.ow, q.yg, q.x, T, 2));
+            }
+            const uint32_t coef1[1] = {L.ffn_x_k};
+            CK(rsv_seq_norm_mix(c, q.x, s.cmix_x[i], L.ln2_w, L.ln2_b, coef1, &q.xb, 1, q.row_prev, T, C, LN_EPS));
+            CK(rsv_seq_state_store(c, q.x, s.cmix_x[i], L.ln2_w, L.ln2_b, q.seg_last, q.seg_slot, S, C, LN_EPS));
+            if (small) {
+                rsv_mm_job j5 = mm_job(L.fk, q.xb, q.r2, 3);
+                CK(rsv_gemm_skinny(c, &j5, 1, T));
+                rsv_mm_job j6 = mm_job(L.fv, q.r2, q.x, 2);
+                CK(rsv_gemm_skinny(c, &j6, 1, T));
+            } else {
+                HK(gemm_lin(b, L.fk, q.xb, q.r2, T, 3));
+                HK(gemm_lin(b, L.fv, q.r2, q.x, T, 2));
+            }
         }
-        if (i == 0) {
-            CK(rsv_copy_device(c, q.v, q.vf));
-            CK(rsv_copy_rows(c, q.v, s.v_first, q.seg_last, q.seg_slot, S, C));
+
+        if (want_head) {
+            CK(rsv_copy_rows(c, q.x, q.xlast, q.seg_last, q.seg_iota, S, C));
+            CK(rsv_norm(c, q.xlast, b->ln_out_w, b->ln_out_b, q.xnorm, C, 1, LN_EPS, S));
+            HK(gemv_lin(b, b->head, q.xnorm, q.logits, S, 0));
         }
-        if (small) {
-            rsv_mm_job j2[4] = {mm_job(L.lw2, q.wmid, q.w, 5), mm_job(L.la2, q.amid, q.a, 6),
-                                mm_job(L.lv2, q.vmid, q.v, 7), mm_job(L.lg2, q.gmid, q.g, 0)};
-            j2[0].bias = L.w0;
-            j2[0].scale = b->scale_w;
-            j2[1].bias = L.a0;
-            j2[2].bias = L.v0;
-            j2[2].aux = q.vf;
-            CK(rsv_gemm_skinny(c, j2, 4, T));
-        } else {
-            // the LoRA-up chain in one launch
-            rsv_mm_job j2[4] = {gemm_job(L.lw2, q.wmid, q.w, 5), gemm_job(L.la2, q.amid, q.a, 6),
-                                gemm_job(L.lv2, q.vmid, q.v, 7), gemm_job(L.lg2, q.gmid, q.g, 0)};
-            j2[0].bias = L.w0;
-            j2[0].scale = b->scale_w;
-            j2[1].bias = L.a0;
-            j2[2].bias = L.v0;
-            j2[2].aux = q.vf;
-            CK(rsv_gemm_multi(c, j2, 4, T));
+        return 0;
+    };
+    if (prefill_graph_on()) {
+        const uint64_t key = T | (S << 24) | ((uint64_t)want_head << 47) | ((s.serial & 0xFFFF) << 48);
+        int valid = 0;
+        CK(rsv_prefill_graph_valid(c, key, &valid));
+        if (!valid) {
+            CK(rsv_prefill_graph_begin(c, key));
+            const int rc = enqueue();
+            const int end_rc = rsv_prefill_graph_end(c);
+            if (rc || end_rc) {
+                rsv_clear_cache(c);  // no partial graph stays behind
+                return rc ? rc : herr("prefill graph: %s", rsv_last_error());
+            }
         }
-        CK(rsv_wkv7_seq_ragged(c, s.rnn[i], q.r, q.w, q.k, q.v, q.a, L.k_k, L.k_a, L.r_k, L.lnx_w, L.lnx_b, q.yn,
-                               q.seg_start, q.seg_len, q.seg_slot, S, H, N, GN_EPS));
-        CK(rsv_mul_to_f16(c, q.yn, q.g, q.yg, T * C));
-        if (small) {
-            rsv_mm_job j4 = mm_job(L.ow, q.yg, q.x, 2);
-            CK(rsv_gemm_skinny(c, &j4, 1, T));
-        } else {
-            HK(gemm_lin(b, L.ow, q.yg, q.x, T, 2));
-        }
-        const uint32_t coef1[1] = {L.ffn_x_k};
-        CK(rsv_seq_norm_mix(c, q.x, s.cmix_x[i], L.ln2_w, L.ln2_b, coef1, &q.xb, 1, q.row_prev, T, C, LN_EPS));
-        CK(rsv_seq_state_store(c, q.x, s.cmix_x[i], L.ln2_w, L.ln2_b, q.seg_last, q.seg_slot, S, C, LN_EPS));
-        if (small) {
-            rsv_mm_job j5 = mm_job(L.fk, q.xb, q.r2, 3);
-            CK(rsv_gemm_skinny(c, &j5, 1, T));
-            rsv_mm_job j6 = mm_job(L.fv, q.r2, q.x, 2);
-            CK(rsv_gemm_skinny(c, &j6, 1, T));
-        } else {
-            HK(gemm_lin(b, L.fk, q.xb, q.r2, T, 3));
-            HK(gemm_lin(b, L.fv, q.r2, q.x, T, 2));
-        }
-    }
-    if (logits || head) {
-        CK(rsv_copy_rows(c, q.x, q.xlast, q.seg_last, q.seg_iota, S, C));
-        CK(rsv_norm(c, q.xlast, b->ln_out_w, b->ln_out_b, q.xnorm, C, 1, LN_EPS, S));
-        HK(gemv_lin(b, b->head, q.xnorm, q.logits, S, 0));
-        if (logits) CK(rsv_download(c, q.logits, logits, S * I.vocab));
+        CK(rsv_prefill_graph_replay(c));
     } else {
-        CK(rsv_synchronize(c));
+        HK(enqueue());
     }
+    if (logits) CK(rsv_download(c, q.logits, logits, S * I.vocab));
+    else if (!head) CK(rsv_synchronize(c));
     return 0;
 }
 
@@ -1435,6 +1472,36 @@ int rsv_model_build(const char *path, int device, rsv_bundle **out) {
     auto b = std::make_unique<rsv_bundle>();
     if (rsv_create(device, &b->ctx)) return herr("rsv_create: %s", rsv_last_error());
     HK(load_model(b.get(), path));
+    b->state = new rsv_state();
+    if (state_create(b.get(), 1, b->state->s)) { delete b->state; b->state = nullptr; return -1; }
+    *out = b.release();
+    return 0;
+}
+
+// GpuModel::build_shared (gpu_model.rs:594-628): a second instance on the
+// same device whose context imports every tensor of the source (weights are
+// not copied), with its own stream, work buffers and session state.  The
+// shared allocations live until both instances have freed them, so either
+// may be freed first.  Weight copies made lazily after this call (the
+// MFMA-tiled copies of the batched path, the fp16 prefill copies) are made
+// per instance.
+int rsv_bundle_build_shared(rsv_bundle *src, rsv_bundle **out) {
+    if (!src || !out) return herr("rsv_bundle_build_shared: null argument");
+    int dev = 0;
+    CK(rsv_context_device(src->ctx, &dev));
+    auto b = std::make_unique<rsv_bundle>();
+    if (rsv_create(dev, &b->ctx)) return herr("rsv_create: %s", rsv_last_error());
+    CK(rsv_synchronize(src->ctx));
+    CK(rsv_import_tensors(b->ctx, src->ctx));
+    b->info = src->info;
+    b->emb_ln = src->emb_ln;
+    b->ln_out_w = src->ln_out_w;
+    b->ln_out_b = src->ln_out_b;
+    b->scale_w = src->scale_w;
+    b->head = src->head;
+    b->layers = src->layers;
+    b->tiled = src->tiled;
+    b->p16 = src->p16;
     b->state = new rsv_state();
     if (state_create(b.get(), 1, b->state->s)) { delete b->state; b->state = nullptr; return -1; }
     *out = b.release();

@@ -7,6 +7,7 @@
 #include <cstdio>
 #include <map>
 #include <string>
+#include <memory>
 #include <vector>
 
 #include "../../include/rsv_hip.h"
@@ -23,12 +24,26 @@ void set_error(const char *fmt, ...);
     } while (0)
 
 // ---------------------------------------------------------------- tensors
+// A device allocation shared by every context that holds it (the context
+// that made it and any that imported it): freed when the last holder lets go.
+struct DevMem {
+    void *ptr = nullptr;
+    int device = 0;
+    ~DevMem() {
+        if (ptr) {
+            hipSetDevice(device);
+            hipFree(ptr);
+        }
+    }
+};
+
 struct Tensor {
     void *ptr = nullptr;
     uint64_t len = 0;  // elements
     int dtype = RSV_F32;
     bool live = false;
-    bool foreign = false;  // imported from another context: never freed here
+    bool foreign = false;  // imported from another context (same id and memory as there)
+    std::shared_ptr<DevMem> mem;
 };
 
 inline size_t dtype_size(int dt) { return dt == RSV_F16 ? 2 : 4; }

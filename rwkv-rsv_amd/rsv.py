@@ -242,6 +242,12 @@ class Bundle:
         self.state_len = n.value
         self.vocab = info.vocab
 
+    def build_shared(self):
+        """GpuModel::build_shared: a second bundle sharing this one's weights."""
+        h = ctypes.c_void_p()
+        _hchk(_host.rsv_bundle_build_shared(self._h, ctypes.byref(h)))
+        return Bundle(h)
+
     def close(self):
         if self._h:
             _host.rsv_bundle_free(self._h)

@@ -458,3 +458,71 @@ def test_batched_alternative_kernels_agree(bundles, env, monkeypatch):
         S.free()
     for got, want in zip(out[env], out["default"]):
         assert rel_rmse(got, want) <= 1e-4
+
+
+@pytest.mark.parametrize("kind", ["i8", "f16"])
+def test_prefill_graph_replay_bit_exact(bundles, kind, monkeypatch):
+    """PREFILL_GRAPH=1 (gpu_model.rs:2440-2507): a prefill chunk is captured
+    as a HIP graph per (rows, segments, state, head) and replayed for later
+    chunks of the same shape.  Replays with other tokens, shapes that
+    alternate (small and large packed chunks), and a multi-session packed
+    prefill give the eager path's logits and state bit for bit."""
+    b, _ = bundles[kind]
+    prompts = [_prompt(40, 700), _prompt(40, 701), _prompt(200, 702), _prompt(40, 703)]
+
+    def run_all():
+        out = []
+        for p in prompts:
+            b.reset()
+            lg = b.infer_seq(p)
+            out.append((lg.copy(), b.state_back().copy()))
+        S = b.create_batch_state(3)
+        _, lg = b.forward_seq_batch(S, [prompts[0][:7], prompts[2][:150], prompts[1][:33]], want_logits=True)
+        _, lg2 = b.forward_seq_batch(S, [prompts[3][:7], prompts[1][:150], prompts[0][:33]], want_logits=True)
+        out.append((lg.copy(), lg2.copy(), S.back().copy()))
+        S.free()
+        return out
+
+    monkeypatch.delenv("PREFILL_GRAPH", raising=False)
+    eager = run_all()
+    monkeypatch.setenv("PREFILL_GRAPH", "1")
+    graph = run_all()
+    graph2 = run_all()  # graphs captured by the previous pass, replayed
+    monkeypatch.delenv("PREFILL_GRAPH")
+    for e, g, g2 in zip(eager, graph, graph2):
+        for a, c, d in zip(e, g, g2):
+            assert np.array_equal(a.view(np.uint32), c.view(np.uint32))
+            assert np.array_equal(a.view(np.uint32), d.view(np.uint32))
+
+
+def test_build_shared_weights(small_i8):
+    """GpuModel::build_shared (gpu_model.rs:594-628): instances on shared
+    weights give the source's logits bit for bit, each with its own state;
+    freeing the source leaves the importer valid, and an instance imported
+    from an importer works after its parent is freed."""
+    rsv = _rsv()
+    src = rsv.ModelBuilder(small_i8).build()
+    p = _prompt(33, 900)
+    want = src.infer_seq(p)
+    st_want = src.state_back()
+    a = src.build_shared()
+    got = a.infer_seq(p)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    # the source's own session is untouched by the importer's run
+    assert np.array_equal(src.state_back().view(np.uint32), st_want.view(np.uint32))
+    # batched path on the importer (its own tiled weight copies)
+    S = a.create_batch_state(17)
+    lg_b = a.forward_seq_batch(S, [p] * 17, want_logits=True)[1]
+    S.free()
+    assert rel_rmse(lg_b[5], want) <= 1e-3
+    src.close()
+    a.reset()
+    got2 = a.infer_seq(p)
+    assert np.array_equal(got2.view(np.uint32), want.view(np.uint32))
+    c = a.build_shared()
+    a.close()
+    got3 = c.infer_seq(p)
+    assert np.array_equal(got3.view(np.uint32), want.view(np.uint32))
+    toks = c.infer_argmax_selfloop(int(p[-1]), 4)
+    assert len(toks) == 4
+    c.close()
