@@ -726,89 +726,6 @@ __global__ __launch_bounds__(256) void k_skinny5_mixed(SkinnyJobs jobs, int MB, 
         skinny5_body<MT, false>(jobs.j[ji], bid - jobs.blk_start[ji], MB, ws, smem5);
 }
 
-// Small-K batched GEMM (K <= 32*NCH, e.g. the LoRA-up chain, K = 64..256):
-// a block is 4 waves on 128 rows of one job, the whole K in one pass.  Every
-// weight chunk and every x operand of the wave is loaded at once (x straight
-// from global into the MFMA B registers, no LDS slab, no k-split), then the
-// MFMAs run and the tile goes through the same LDS epilogue as k_skinny5.
-template <int MT, bool I8, int NCH>
-__global__ __launch_bounds__(256) void k_skinny_sk(SkinnyJobs jobs, int MB) {
-    constexpr int TB = MT * 32;
-    constexpr int WV = I8 ? 1 : 2;
-    __shared__ float tile[128][TB + 1];
-    const int bid = blockIdx.x;
-    int ji = 0;
-    while (ji + 1 < jobs.n && bid >= jobs.blk_start[ji + 1]) ji++;
-    const SkinnyJob &J = jobs.j[ji];
-    const int rg = bid - jobs.blk_start[ji];
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 5;
-    const int nchunks = J.K / 32;
-    const int rt_glob = rg * 4 + wave;
-    const int row = rt_glob * 32 + (lane & 31);
-    const bool row_ok = row < J.N;
-    constexpr int tbytes = I8 ? 1024 : 2048;
-    // rows past N read the job's first tile (masked to zero below)
-    const uint8_t *wt = (const uint8_t *)J.w + (row_ok ? (size_t)rt_glob * nchunks * tbytes : 0) + lane * (I8 ? 16 : 32);
-    const uint32_t *szrow = I8 ? J.sz + (size_t)min(rt_glob, (J.N - 1) / 32) * (J.K / 128) * 32 + (lane & 31) : nullptr;
-    sk_u32x4 wr[NCH][WV];
-    uint32_t sr[NCH];
-    sk_u32x4 xv[NCH][MT][2];
-#pragma unroll
-    for (int c = 0; c < NCH; c++) {
-        const int cc = min(c, nchunks - 1);
-#pragma unroll
-        for (int v = 0; v < WV; v++) wr[c][v] = ((const sk_u32x4 *)(wt + (size_t)cc * tbytes))[v];
-        if (I8) sr[c] = szrow[(size_t)(cc >> 2) * 32];
-#pragma unroll
-        for (int ct = 0; ct < MT; ct++) {
-            const int b = min(ct * 32 + (lane & 31), MB - 1);  // sessions past MB are computed, never stored
-            const sk_u32x4 *xp = (const sk_u32x4 *)(J.x + (size_t)b * J.ldx + cc * 32 + 16 * g);
-            xv[c][ct][0] = xp[0];
-            xv[c][ct][1] = xp[1];
-        }
-    }
-    sk_f16x acc[MT];
-#pragma unroll
-    for (int ct = 0; ct < MT; ct++)
-#pragma unroll
-        for (int e = 0; e < 16; e++) acc[ct][e] = 0.0f;
-#pragma unroll
-    for (int c = 0; c < NCH; c++) {
-        if (c >= nchunks) break;  // uniform: one job per block
-        const bool live = row_ok;
-        uint32_t wh[8];
-        if (I8) {
-            const float sc = live ? sk_h2f(sr[c]) : 0.0f, z = live ? sk_h2f(sr[c] >> 16) : 0.0f;
-#pragma unroll
-            for (int h = 0; h < 4; h++) {
-                const uint32_t u = wr[c][0][h];
-                wh[2 * h] = sk_deq2(sc, (float)(u & 0xFFu), (float)((u >> 8) & 0xFFu), z);
-                wh[2 * h + 1] = sk_deq2(sc, (float)((u >> 16) & 0xFFu), (float)(u >> 24), z);
-            }
-        } else {
-#pragma unroll
-            for (int h = 0; h < 4; h++) {
-                wh[h] = live ? wr[c][0][h] : 0u;
-                wh[4 + h] = live ? wr[c][WV - 1][h] : 0u;
-            }
-        }
-#pragma unroll
-        for (int st = 0; st < 2; st++) {
-            const sk_half8 a = __builtin_bit_cast(sk_half8, (sk_u32x4){wh[4 * st], wh[4 * st + 1], wh[4 * st + 2], wh[4 * st + 3]});
-#pragma unroll
-            for (int ct = 0; ct < MT; ct++)
-                acc[ct] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, __builtin_bit_cast(sk_half8, xv[c][ct][st]), acc[ct], 0, 0, 0);
-        }
-    }
-    // wave w owns tile rows 32w .. 32w+31: acc[ct][e] -> (row 32w + 8*(e/4) + 4g + e%4, col ct*32 + lane%32)
-#pragma unroll
-    for (int ct = 0; ct < MT; ct++)
-#pragma unroll
-        for (int e = 0; e < 16; e++) tile[wave * 32 + 8 * (e >> 2) + 4 * g + (e & 3)][ct * 32 + (lane & 31)] = acc[ct][e];
-    __syncthreads();
-    sk_store_tile<TB>(sk_epi_of(J), tile, rg * 128, MB);
-}
-
 // One output of a split job: the slices in slice order, then the epilogue.
 // The epilogue's read operands (y for add / v-lerp, aux, bias) are loaded
 // together with the slices, so the thread waits on one round of loads.
@@ -850,6 +767,250 @@ __global__ __launch_bounds__(256) void k_skinny4_reduce(SkinnyJobs jobs, int MB,
 #define SK_RED_CALL(K) sk_reduce_one<K, TB>(J, base, o, n, b)
     SK_EPI_DISPATCH(J, SK_RED_CALL)
 #undef SK_RED_CALL
+}
+
+// s_waitcnt vmcnt(n) for n known at compile time after unrolling (the
+// switch folds); other counters left alone.
+#define SK_VM(n) case n: __builtin_amdgcn_s_waitcnt((n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8)); break;
+__device__ __forceinline__ void sk_wait_vm(int n) {
+    switch (n < 63 ? n : 63) {
+        SK_VM(0) SK_VM(1) SK_VM(2) SK_VM(3) SK_VM(4) SK_VM(5) SK_VM(6) SK_VM(7) SK_VM(8) SK_VM(9) SK_VM(10) SK_VM(11)
+        SK_VM(12) SK_VM(13) SK_VM(14) SK_VM(15) SK_VM(16) SK_VM(17) SK_VM(18) SK_VM(19) SK_VM(20) SK_VM(21) SK_VM(22)
+        SK_VM(23) SK_VM(24) SK_VM(25) SK_VM(26) SK_VM(27) SK_VM(28) SK_VM(29) SK_VM(30) SK_VM(31) SK_VM(32) SK_VM(33)
+        SK_VM(34) SK_VM(35) SK_VM(36) SK_VM(37) SK_VM(38) SK_VM(39) SK_VM(40) SK_VM(41) SK_VM(42) SK_VM(43) SK_VM(44)
+        SK_VM(45) SK_VM(46) SK_VM(47) SK_VM(48) SK_VM(49) SK_VM(50) SK_VM(51) SK_VM(52) SK_VM(53) SK_VM(54) SK_VM(55)
+        SK_VM(56) SK_VM(57) SK_VM(58) SK_VM(59) SK_VM(60) SK_VM(61) SK_VM(62)
+        default: __builtin_amdgcn_s_waitcnt((15) | (3 << 14) | (0x7 << 4) | (0xF << 8)); break;
+    }
+}
+#undef SK_VM
+
+// Epilogue of one 32-row x TB-session tile: thread t owns row t % 32 and
+// sessions t/32, t/32 + 8, ...; v[q] holds its TB/8 sums.  Every read
+// operand goes out before the first store.
+template <int EPI, int TB>
+__device__ __forceinline__ void sk8_epilogue(const SkEpi &E, const float (&v)[TB / 8], int n, int b0, int MB) {
+    constexpr int NQ = TB / 8;
+    constexpr bool need_y = EPI == GE_ADD || EPI == GE_VLERP;
+    constexpr bool need_b = EPI == GE_BIAS || EPI == GE_WDECAY || EPI == GE_SIGBIAS || EPI == GE_VLERP;
+    float yc[NQ], ax[NQ];
+#pragma unroll
+    for (int q = 0; q < NQ; q++) {
+        const int b = b0 + 8 * q;
+        const size_t yo = (size_t)b * E.ldy + n;
+        yc[q] = (need_y && b < MB) ? ((const float *)E.y)[yo] : 0.0f;
+        ax[q] = (EPI == GE_VLERP && b < MB) ? E.aux[yo] : 0.0f;
+    }
+    const float bias = need_b ? E.bias[n] : 0.0f;
+#pragma unroll
+    for (int q = 0; q < NQ; q++) {
+        const int b = b0 + 8 * q;
+        if (b >= MB) break;
+        sk_put(E, (size_t)b * E.ldy + n, sk_epi_val<EPI>(v[q], yc[q], ax[q], bias, E.scale));
+    }
+}
+
+// ------------------------------------------------------------------ v8
+// Batched decode GEMM, one row tile (32 weight rows) per block over the
+// whole k, the k range split over the block's 4 waves (each wave its own
+// quarter; the four partial tiles are summed in LDS in wave order).  Per
+// wave, two 32-column chunks per step:
+//   - x of a step (TB sessions x 128 bytes, whole cache lines) is copied
+//     global -> LDS by global_load_lds_dwordx4 (no VGPR staging):
+//     instruction i fills 1 KiB, lane l taking session 8i + l/8 and 16-byte
+//     piece (l%8) ^ (session & 7)
+//     (the XOR spreads the MFMA operand reads of 32 sessions over the
+//     banks); two wave-private buffers, the next step's copy in flight while
+//     this step is multiplied out; the operand reads are one asm block per
+//     chunk behind an explicit wait for the step's copy;
+//   - the weights of a step (the row tile's next two 1 KiB / 2 KiB tiles, a
+//     sequential stream per wave) go to registers DW steps ahead: HBM
+//     latency needs many weight bytes in flight;
+//   - v_mfma_f32_32x32x16_f16 with the lane mapping of k_skinny5.
+// The common k (2560 columns: 10 steps per wave) runs fully unrolled with
+// exact wait counts; other k (a multiple of 64) take a two-deep loop.
+template <int MT, bool I8, int FIX>
+__device__ __forceinline__ void skinny8_body(const SkinnyJob &J, int rt, int MB, unsigned char *xb0, unsigned char *xb1) {
+    constexpr int TB = MT * 32;
+    constexpr int XB = TB * 128;     // bytes of one x buffer
+    constexpr int NX = TB / 8;       // 1 KiB copies per step
+    constexpr int WV = I8 ? 1 : 2;
+    constexpr int tbytes = I8 ? 1024 : 2048;
+    constexpr int DW = FIX > 0 ? 4 : 2;  // weight steps in flight
+    constexpr int LW = 2 * WV + (I8 ? 1 : 0);  // weight loads per step
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 5;
+    const int nchunks = J.K / 32;
+    // chunk pairs per wave (k is a multiple of 64)
+    const int q4 = ((nchunks + 3) / 4 + 1) & ~1;
+    const int cw0 = min(nchunks, wave * q4), cw1 = min(nchunks, cw0 + q4);
+    const int nw = (cw1 - cw0) / 2;  // steps of this wave
+    unsigned char *xbw[2] = {xb0 + wave * XB, xb1 + wave * XB};
+    const uint8_t *wt = (const uint8_t *)J.w + (size_t)rt * nchunks * tbytes + lane * (I8 ? 16 : 32);
+    const uint32_t *szrow = I8 ? J.sz + (size_t)rt * (J.K / 128) * 32 + (lane & 31) : nullptr;
+    // copy source of lane l in instruction i, relative to the step's column
+    const _Float16 *xsrc[NX];
+#pragma unroll
+    for (int i = 0; i < NX; i++) {
+        const int b = 8 * i + (lane >> 3);
+        const int piece = (lane & 7) ^ (b & 7);
+        xsrc[i] = J.x + (size_t)min(b, MB - 1) * J.ldx + piece * 8;
+    }
+    sk_u32x4 wr[DW][2][WV];
+    uint32_t sr[DW];
+    auto issue_x = [&](int slot, int s) {
+        const int c = cw0 + 2 * min(s, nw - 1);  // clamped: steps past the end re-read (masked)
+        unsigned char *dst = xbw[slot];
+#pragma unroll
+        for (int i = 0; i < NX; i++)
+            __builtin_amdgcn_global_load_lds(xsrc[i] + c * 32, (__attribute__((address_space(3))) void *)(dst + i * 1024), 16, 0, 0);
+    };
+    auto issue_w = [&](int wslot, int s) {
+        const int c = cw0 + 2 * min(s, nw - 1);
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const sk_u32x4 *q = (const sk_u32x4 *)(wt + (size_t)(c + h) * tbytes);
+#pragma unroll
+            for (int v = 0; v < WV; v++) wr[wslot][h][v] = q[v];
+        }
+        if (I8) sr[wslot] = szrow[(size_t)(c >> 2) * 32];  // c even: both chunks in one 128-group
+    };
+    sk_f16x acc[MT];
+#pragma unroll
+    for (int ct = 0; ct < MT; ct++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) acc[ct][e] = 0.0f;
+    // mask = false where every step is a real one: the tiled copy's padding
+    // rows are zero (scale and zero too), so only the loop's clamped steps
+    // past the end need masking
+    auto compute = [&](int slot, int wslot, int s, bool mask) {
+        const unsigned char *xb = xbw[slot];
+        const bool live = !mask || s < nw;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            uint32_t wh[8];
+            if (I8) {
+                const float sc = live ? sk_h2f(sr[wslot]) : 0.0f, z = live ? sk_h2f(sr[wslot] >> 16) : 0.0f;
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const uint32_t u = wr[wslot][h][0][q];
+                    wh[2 * q] = sk_deq2(sc, (float)(u & 0xFFu), (float)((u >> 8) & 0xFFu), z);
+                    wh[2 * q + 1] = sk_deq2(sc, (float)((u >> 16) & 0xFFu), (float)(u >> 24), z);
+                }
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    wh[q] = live ? wr[wslot][h][0][q] : 0u;
+                    wh[4 + q] = live ? wr[wslot][h][WV - 1][q] : 0u;
+                }
+            }
+            // the chunk's x operands: read in one asm block, so that the
+            // compiler, which cannot see which LDS copy a read depends on,
+            // adds no drain of every copy in flight before them (the explicit
+            // wait before the step covers this step's copy)
+            sk_u32x4 xv[2][MT];
+            const int b_lo = lane & 31;
+            const uint32_t a00 = (uint32_t)(uintptr_t)(xb + b_lo * 128 + (((4 * h + 2 * g) ^ (b_lo & 7)) * 16));
+            const uint32_t a01 = (uint32_t)(uintptr_t)(xb + b_lo * 128 + (((4 * h + 2 * g + 1) ^ (b_lo & 7)) * 16));
+            if constexpr (MT == 1) {
+                asm volatile("ds_read_b128 %0, %2\n\tds_read_b128 %1, %3\n\ts_waitcnt lgkmcnt(0)"
+                             : "=v"(xv[0][0]), "=v"(xv[1][0])
+                             : "v"(a00), "v"(a01)
+                             : "memory");
+            } else {
+                // session tile 1 sits 32 sessions (4096 bytes) further, with
+                // the same XOR pattern (b & 7 unchanged)
+                asm volatile("ds_read_b128 %0, %4\n\tds_read_b128 %1, %5\n\t"
+                             "ds_read_b128 %2, %4 offset:4096\n\tds_read_b128 %3, %5 offset:4096\n\t"
+                             "s_waitcnt lgkmcnt(0)"
+                             : "=v"(xv[0][0]), "=v"(xv[1][0]), "=v"(xv[0][MT - 1]), "=v"(xv[1][MT - 1])
+                             : "v"(a00), "v"(a01)
+                             : "memory");
+            }
+#pragma unroll
+            for (int st = 0; st < 2; st++) {
+                const sk_half8 a = __builtin_bit_cast(sk_half8, (sk_u32x4){wh[4 * st], wh[4 * st + 1], wh[4 * st + 2], wh[4 * st + 3]});
+#pragma unroll
+                for (int ct = 0; ct < MT; ct++)
+                    acc[ct] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, __builtin_bit_cast(sk_half8, xv[st][ct]), acc[ct], 0, 0, 0);
+            }
+        }
+    };
+    if (FIX > 0 && nw == FIX) {
+        issue_x(0, 0);
+#pragma unroll
+        for (int d = 0; d < DW; d++) issue_w(d, d);
+#pragma unroll
+        for (int s = 0; s < FIX; s++) {
+            // order per step: the next step's x copy, this step's products,
+            // then the weights DW steps ahead into the slot just consumed.
+            // Scheduling barriers keep that order: otherwise the scheduler
+            // sinks the weight loads next to their use (register pressure
+            // first) and the ring degenerates to one step
+            __builtin_amdgcn_sched_barrier(0);
+            if (s + 1 < FIX) issue_x((s + 1) & 1, s + 1);
+            // loads younger than x(s): the weights issued after it (at the end
+            // of step s-1, or the whole prologue ring for s = 0) and x(s+1)
+            const int younger = (s == 0 ? DW * LW : (s - 1 + DW < FIX ? LW : 0)) + (s + 1 < FIX ? NX : 0);
+            sk_wait_vm(younger);
+            compute(s & 1, s % DW, s, false);
+            __builtin_amdgcn_sched_barrier(0);
+            if (s + DW < FIX) issue_w(s % DW, s + DW);
+        }
+    } else if (nw > 0) {
+        // the x copies are not register results, so the wait before a step
+        // is explicit: only the next step's loads may still be outstanding
+        constexpr int VM = NX + LW;
+        constexpr int WAIT = (VM & 0xF) | ((VM >> 4) << 14) | (0x7 << 4) | (0xF << 8);
+        issue_x(0, 0);
+        issue_w(0, 0);
+        for (int s0 = 0; s0 < nw; s0 += 2) {
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const int s = s0 + u;
+                issue_x(u ^ 1, s + 1);
+                issue_w(u ^ 1, s + 1);
+                __builtin_amdgcn_s_waitcnt(WAIT);
+                compute(u, u, s, true);
+            }
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();  // x buffers dead: the LDS holds the wave tiles now
+    float (*part)[32][TB + 1] = reinterpret_cast<float (*)[32][TB + 1]>(xb1);
+#pragma unroll
+    for (int ct = 0; ct < MT; ct++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) part[wave][8 * (e >> 2) + 4 * g + (e & 3)][ct * 32 + (lane & 31)] = acc[ct][e];
+    __syncthreads();
+    const int r = tid & 31, b0 = tid >> 5;
+    float v[TB / 8];
+#pragma unroll
+    for (int q = 0; q < TB / 8; q++) {
+        const int b = b0 + 8 * q;
+        v[q] = ((part[0][r][b] + part[1][r][b]) + part[2][r][b]) + part[3][r][b];
+    }
+    const int n = rt * 32 + r;
+    if (n >= J.N) return;
+    const SkEpi E = sk_epi_of(J);
+#define SK8_CALL(K) sk8_epilogue<K, TB>(E, v, n, b0, MB)
+    SK_EPI_DISPATCH(E, SK8_CALL)
+#undef SK8_CALL
+}
+
+template <int MT>
+__global__ __launch_bounds__(256) void k_skinny8(SkinnyJobs jobs, int MB) {
+    // 4 waves x TB sessions x 128 bytes per buffer; the second also holds
+    // the 4 x 32 x (TB+1) wave tiles at the end
+    constexpr int XBYTES = 4 * MT * 32 * 128 > 4 * 32 * (MT * 32 + 1) * 4 ? 4 * MT * 32 * 128 : 4 * 32 * (MT * 32 + 1) * 4;
+    __shared__ __attribute__((aligned(16))) unsigned char xb0[4 * MT * 32 * 128];
+    __shared__ __attribute__((aligned(16))) unsigned char xb1[XBYTES];
+    const int bid = blockIdx.x;
+    int ji = 0;
+    while (ji + 1 < jobs.n && bid >= jobs.blk_start[ji + 1]) ji++;
+    if (jobs.j[ji].fmt == FMT_I8)
+        skinny8_body<MT, true, 10>(jobs.j[ji], bid - jobs.blk_start[ji], MB, xb0, xb1);
+    else
+        skinny8_body<MT, false, 10>(jobs.j[ji], bid - jobs.blk_start[ji], MB, xb0, xb1);
 }
 
 // Tiled copy of a weight matrix [n, k] (int8 bytes or fp16) for k_skinny4;
@@ -912,34 +1073,11 @@ int launch_tile_weights(rsv_ctx *ctx, const void *src, void *dst, int n, int k, 
 
 static int launch_slab(rsv_ctx *ctx, SkinnyJobs &jobs, int MB);
 
-// Batches above 64 run as consecutive 64-row slabs; tiled jobs of the two
-// weight formats run as separate launches (per-format register budgets).
-constexpr int SK_SMALL_NCH = 8;  // chunks (of 32) of the small-K kernels: K <= 256
+// Batches above 64 run as consecutive 64-row slabs.
+constexpr int SK_SMALL_NCH = 8;  // chunks (of 32) of the small-K kernel: K <= 256
 
 int launch_skinny(rsv_ctx *ctx, SkinnyJobs &jobs, int MB) {
     if (MB <= 0) return RSV_FAIL("skinny gemm: batch %d", MB);
-    if (jobs.n > 0 && jobs.j[0].tiled) {
-        SkinnyJobs parts[2]{};
-        for (int i = 0; i < jobs.n; i++) {
-            SkinnyJobs &p = parts[jobs.j[i].fmt == FMT_I8 ? 0 : 1];
-            p.j[p.n++] = jobs.j[i];
-        }
-        // both formats share one k_skinny5_mixed launch when every job takes
-        // that path (no small-K job, none large enough for k_skinny4)
-        const int mixed_on = [] {  // read at each launch, so one process can compare settings
-            const char *e = getenv("RSV_SKINNY_MIXED");
-            return e ? atoi(e) : 1;
-        }();
-        bool one = mixed_on != 0;
-        const int cus = ctx->sm_count > 0 ? ctx->sm_count : 256;
-        for (int i = 0; i < jobs.n; i++)
-            one &= jobs.j[i].K > 32 * SK_SMALL_NCH && (jobs.j[i].N + 127) / 128 < 2 * cus;
-        if (parts[0].n && parts[1].n && !one) {
-            for (auto &p : parts)
-                if (launch_skinny(ctx, p, MB)) return -1;
-            return 0;
-        }
-    }
     for (int s0 = 0; s0 < MB; s0 += 64) {
         SkinnyJobs sl = jobs;
         for (int i = 0; i < sl.n; i++) {
@@ -954,6 +1092,24 @@ int launch_skinny(rsv_ctx *ctx, SkinnyJobs &jobs, int MB) {
     return 0;
 }
 
+// k_skinny8: one block per 32-row tile over the whole k (both weight
+// formats in one launch).
+static int launch_v8(rsv_ctx *ctx, SkinnyJobs &jobs, int MB) {
+    int total = 0;
+    for (int i = 0; i < jobs.n; i++) {
+        SkinnyJob &J = jobs.j[i];
+        J.split = 1;
+        J.nblk = (J.N + 31) / 32;
+        jobs.blk_start[i] = total;
+        total += J.nblk;
+    }
+    jobs.blk_start[jobs.n] = total;
+    if (MB <= 32) hipLaunchKernelGGL((k_skinny8<1>), dim3(total), dim3(256), 0, ctx->stream, jobs, MB);
+    else hipLaunchKernelGGL((k_skinny8<2>), dim3(total), dim3(256), 0, ctx->stream, jobs, MB);
+    RSV_HIP(hipGetLastError());
+    return 0;
+}
+
 // v5 launch of tiled jobs.  Each job's k-slice count is set so that the
 // launch has about two blocks per CU, with slices of 8..16 chunks when the
 // row count allows (16 chunks = the LDS x slab limit, 8 = enough chunks per
@@ -962,11 +1118,7 @@ constexpr int SK_KMAX = 16;  // longest k-slice (chunks) of the LDS x slab
 static int launch_v5(rsv_ctx *ctx, SkinnyJobs &jobs, int MB) {
     const int TB = MB <= 32 ? 32 : 64;
     const int cus = ctx->sm_count > 0 ? ctx->sm_count : 256;
-    const int per_cu = [] {  // read at each launch, so one process can compare settings
-        const char *e = getenv("RSV_SKINNY_BLOCKS_PER_CU");
-        return e && atoi(e) > 0 ? atoi(e) : 2;
-    }();
-    const int target = per_cu * cus;
+    const int target = 2 * cus;
     int64_t W = 0;
     for (int i = 0; i < jobs.n; i++) {
         const SkinnyJob &J = jobs.j[i];
@@ -1024,6 +1176,31 @@ static int launch_v5(rsv_ctx *ctx, SkinnyJobs &jobs, int MB) {
     return 0;
 }
 
+// k_skinny4 for jobs with at least two 128-row groups per CU (the head):
+// one block per row group over the whole k, no split.
+static int launch_v4(rsv_ctx *ctx, SkinnyJobs &jobs, int MB) {
+    const bool i8 = jobs.j[0].fmt == FMT_I8;
+    int total = 0;
+    for (int i = 0; i < jobs.n; i++) {
+        SkinnyJob &J = jobs.j[i];
+        if ((J.fmt == FMT_I8) != i8) return RSV_FAIL("skinny gemm: mixed formats in one large-job launch");
+        J.split = 1;
+        J.nblk = (J.N + 127) / 128;
+        jobs.blk_start[i] = total;
+        total += J.nblk;
+    }
+    jobs.blk_start[jobs.n] = total;
+    if (MB <= 32) {
+        if (i8) hipLaunchKernelGGL((k_skinny4<1, true>), dim3(total), dim3(256), 0, ctx->stream, jobs, MB, ctx->skinny_ws);
+        else hipLaunchKernelGGL((k_skinny4<1, false>), dim3(total), dim3(256), 0, ctx->stream, jobs, MB, ctx->skinny_ws);
+    } else {
+        if (i8) hipLaunchKernelGGL((k_skinny4<2, true>), dim3(total), dim3(256), 0, ctx->stream, jobs, MB, ctx->skinny_ws);
+        else hipLaunchKernelGGL((k_skinny4<2, false>), dim3(total), dim3(256), 0, ctx->stream, jobs, MB, ctx->skinny_ws);
+    }
+    RSV_HIP(hipGetLastError());
+    return 0;
+}
+
 // Epilogue of k_skinny_sk1 for one epilogue kind: every read operand of the
 // thread's sessions is loaded in one round, then the values are stored.
 template <int EPI, int TB>
@@ -1052,7 +1229,7 @@ __device__ __forceinline__ void sk1_epilogue(const SkEpi &E, const float (*tile)
 // Small-K batched GEMM, one wave per block on one 32-row tile of one job.
 // A small-K job moves little data per row, so the launch is bound by what
 // each CU can pull: one-wave blocks spread the row tiles of all jobs over
-// up to N/32 CUs (k_skinny_sk puts 128 rows, i.e. four copies of x, on one
+// up to N/32 CUs (four-wave blocks on 128 rows put four copies of x on one
 // CU).  Only the job's own chunks are loaded (uniform branches), every load
 // of the wave goes out at once, and the epilogue loads all of its
 // read-modify-write operands in one round after the MFMAs.
@@ -1137,90 +1314,51 @@ __global__ __launch_bounds__(64) void k_skinny_sk1(SkinnyJobs jobs, int MB) {
 #undef SK1_CALL
 }
 
-// Jobs of K <= 32*SK_SMALL_NCH in one pass each, no k-split and no reduce
-// launch: k_skinny_sk1 (one wave per 32 rows; default) or k_skinny_sk (one
-// block per 128 rows, RSV_SKINNY_SK1=0).
+// Jobs of K <= 32*SK_SMALL_NCH in one pass each, no k-split: k_skinny_sk1,
+// one wave per 32 rows, one launch per weight format.
 static int launch_small(rsv_ctx *ctx, SkinnyJobs &jobs, int MB) {
+    const bool i8 = jobs.j[0].fmt == FMT_I8;
+    bool mixed = false;
+    for (int i = 1; i < jobs.n; i++) mixed |= (jobs.j[i].fmt == FMT_I8) != i8;
+    if (mixed) {
+        SkinnyJobs parts[2]{};
+        for (int i = 0; i < jobs.n; i++) {
+            SkinnyJobs &p = parts[jobs.j[i].fmt == FMT_I8 ? 0 : 1];
+            p.j[p.n++] = jobs.j[i];
+        }
+        for (auto &p : parts)
+            if (launch_small(ctx, p, MB)) return -1;
+        return 0;
+    }
     int total = 0;
     for (int i = 0; i < jobs.n; i++) {
         SkinnyJob &J = jobs.j[i];
         J.split = 1;
-        J.nblk = (J.N + 127) / 128;
+        J.nblk = (J.N + 31) / 32;
         jobs.blk_start[i] = total;
         total += J.nblk;
     }
     jobs.blk_start[jobs.n] = total;
-    const bool i8 = jobs.j[0].fmt == FMT_I8;
-    for (int i = 1; i < jobs.n; i++)
-        if ((jobs.j[i].fmt == FMT_I8) != i8) return RSV_FAIL("skinny gemm: mixed formats in one tiled launch");
-    const int one_wave = [] {  // read at each launch, so one process can compare settings
-        const char *e = getenv("RSV_SKINNY_SK1");
-        return e ? atoi(e) : 1;
-    }();
-    if (one_wave) {
-        total = 0;
-        for (int i = 0; i < jobs.n; i++) {
-            SkinnyJob &J = jobs.j[i];
-            J.nblk = (J.N + 31) / 32;
-            jobs.blk_start[i] = total;
-            total += J.nblk;
-        }
-        jobs.blk_start[jobs.n] = total;
-        if (MB <= 32) {
-            if (i8) hipLaunchKernelGGL((k_skinny_sk1<1, true, SK_SMALL_NCH>), dim3(total), dim3(64), 0, ctx->stream, jobs, MB);
-            else hipLaunchKernelGGL((k_skinny_sk1<1, false, SK_SMALL_NCH>), dim3(total), dim3(64), 0, ctx->stream, jobs, MB);
-        } else {
-            if (i8) hipLaunchKernelGGL((k_skinny_sk1<2, true, SK_SMALL_NCH>), dim3(total), dim3(64), 0, ctx->stream, jobs, MB);
-            else hipLaunchKernelGGL((k_skinny_sk1<2, false, SK_SMALL_NCH>), dim3(total), dim3(64), 0, ctx->stream, jobs, MB);
-        }
-        RSV_HIP(hipGetLastError());
-        return 0;
-    }
     if (MB <= 32) {
-        if (i8) hipLaunchKernelGGL((k_skinny_sk<1, true, SK_SMALL_NCH>), dim3(total), dim3(256), 0, ctx->stream, jobs, MB);
-        else hipLaunchKernelGGL((k_skinny_sk<1, false, SK_SMALL_NCH>), dim3(total), dim3(256), 0, ctx->stream, jobs, MB);
+        if (i8) hipLaunchKernelGGL((k_skinny_sk1<1, true, SK_SMALL_NCH>), dim3(total), dim3(64), 0, ctx->stream, jobs, MB);
+        else hipLaunchKernelGGL((k_skinny_sk1<1, false, SK_SMALL_NCH>), dim3(total), dim3(64), 0, ctx->stream, jobs, MB);
     } else {
-        if (i8) hipLaunchKernelGGL((k_skinny_sk<2, true, SK_SMALL_NCH>), dim3(total), dim3(256), 0, ctx->stream, jobs, MB);
-        else hipLaunchKernelGGL((k_skinny_sk<2, false, SK_SMALL_NCH>), dim3(total), dim3(256), 0, ctx->stream, jobs, MB);
+        if (i8) hipLaunchKernelGGL((k_skinny_sk1<2, true, SK_SMALL_NCH>), dim3(total), dim3(64), 0, ctx->stream, jobs, MB);
+        else hipLaunchKernelGGL((k_skinny_sk1<2, false, SK_SMALL_NCH>), dim3(total), dim3(64), 0, ctx->stream, jobs, MB);
     }
     RSV_HIP(hipGetLastError());
     return 0;
 }
 
+// Tiled jobs: small k -> k_skinny_sk1; at least two 128-row groups per CU
+// (the head) -> k_skinny4; k of at most SK8_KMAX chunks, a multiple of 64
+// -> k_skinny8 (one block per 32-row tile over the whole k: its x reads
+// stay within 4x the weight bytes, and no k-slice partials are needed);
+// longer k (ffn.value) -> k_skinny5 with k-slices and the slice reduction.
+constexpr int SK8_KMAX = 80;  // chunks (2560 columns)
 static int launch_slab(rsv_ctx *ctx, SkinnyJobs &jobs, int MB) {
     if (MB <= 0 || MB > 64) return RSV_FAIL("skinny gemm: batch %d outside 1..64", MB);
     if (jobs.n <= 0 || jobs.n > kMaxJobs) return RSV_FAIL("skinny gemm: bad job count %d", jobs.n);
-    const int use_v5 = [] {  // read at each launch, so one process can compare settings
-        const char *e = getenv("RSV_SKINNY_V5");
-        return e ? atoi(e) : 1;
-    }();
-    if (use_v5 && jobs.j[0].tiled) {
-        // jobs with at least two row groups per CU need no k-split: they stay
-        // on the v4 path, whose x window is not bounded by the LDS slab
-        bool big = false;
-        const int cus = ctx->sm_count > 0 ? ctx->sm_count : 256;
-        for (int i = 0; i < jobs.n; i++) big |= (jobs.j[i].N + 127) / 128 >= 2 * cus;
-        bool ok = true;
-        for (int i = 0; i < jobs.n; i++) {
-            const SkinnyJob &J = jobs.j[i];
-            ok &= J.tiled && J.w && J.x && J.y && J.N > 0 && J.K > 0 && J.K % 32 == 0 && J.ldx % 8 == 0 &&
-                  J.ldx >= J.K && (J.fmt != FMT_I8 || (J.K % 128 == 0 && J.sz)) &&
-                  !((J.epi == GE_BIAS || J.epi == GE_WDECAY || J.epi == GE_SIGBIAS || J.epi == GE_VLERP) && !J.bias) &&
-                  !(J.epi == GE_VLERP && !J.aux) && !(J.epi == GE_WDECAY && !J.scale) &&
-                  !(J.y_f16 && (J.epi == GE_ADD || J.epi == GE_VLERP));
-        }
-        bool small = ok;
-        for (int i = 0; i < jobs.n; i++) small &= jobs.j[i].K <= 32 * SK_SMALL_NCH;
-        if (small) return launch_small(ctx, jobs, MB);
-        if (!big && ok) return launch_v5(ctx, jobs, MB);
-    }
-    const int max_split = [] {  // read at each launch, so one process can compare settings
-        const char *e = getenv("RSV_SKINNY_MAX_SPLIT");
-        return e ? atoi(e) : 16;
-    }();
-    const int TB = MB <= 32 ? 32 : 64;
-    int total = 0, red_total = 0;
-    size_t ws_need = 0;
     for (int i = 0; i < jobs.n; i++) {
         SkinnyJob &J = jobs.j[i];
         if (!J.w || !J.x || !J.y) return RSV_FAIL("skinny job %d: null operand", i);
@@ -1233,68 +1371,55 @@ static int launch_slab(rsv_ctx *ctx, SkinnyJobs &jobs, int MB) {
         if (J.epi == GE_WDECAY && !J.scale) return RSV_FAIL("skinny job %d: decay needs scale", i);
         if (J.y_f16 && (J.epi == GE_ADD || J.epi == GE_VLERP)) return RSV_FAIL("skinny job %d: in-place needs fp32 y", i);
         if (J.tiled != jobs.j[0].tiled) return RSV_FAIL("skinny gemm: jobs mix tiled and row-major weights");
-        const int rows_per_block = J.tiled ? 128 : 64;
-        const int rgs = (J.N + rows_per_block - 1) / rows_per_block;
+    }
+    if (jobs.j[0].tiled) {
+        bool small = true, big = false, v8 = true;
+        const int cus = ctx->sm_count > 0 ? ctx->sm_count : 256;
+        for (int i = 0; i < jobs.n; i++) {
+            const SkinnyJob &J = jobs.j[i];
+            small &= J.K <= 32 * SK_SMALL_NCH;
+            big |= (J.N + 127) / 128 >= 2 * cus;
+            v8 &= J.K % 64 == 0 && J.K <= 32 * SK8_KMAX;
+        }
+        if (small) return launch_small(ctx, jobs, MB);
+        if (big) return launch_v4(ctx, jobs, MB);
+        return v8 ? launch_v8(ctx, jobs, MB) : launch_v5(ctx, jobs, MB);
+    }
+    // row-major weights (the C-ABI's untiled form): k_skinny + slice reduce
+    const int TB = MB <= 32 ? 32 : 64;
+    int total = 0, red_total = 0;
+    size_t ws_need = 0;
+    for (int i = 0; i < jobs.n; i++) {
+        SkinnyJob &J = jobs.j[i];
+        const int rgs = (J.N + 63) / 64;
         const int nchunks = J.K / 32;
         int split = 1;
-        if (J.tiled) {
-            // k-slices of whole 4-chunk groups: aim for ~2 blocks per CU with
-            // at least 2 groups per slice
-            const int ngroups = (nchunks + 3) / 4;
-            while (split < max_split && ngroups >= (split + 1) * 2 && rgs * (split + 1) <= 512) split++;
-        } else {
-            // each wave streams at most ~8 chunks (256 columns)
-            while (split < max_split && nchunks > split * 4 * 8 && rgs * split * 2 <= 1024) split++;
-        }
+        // each wave streams at most ~8 chunks (256 columns)
+        while (split < 16 && nchunks > split * 4 * 8 && rgs * split * 2 <= 1024) split++;
         J.split = split;
-        J.ws_slot = (int)(ws_need / ((J.tiled ? 128 : 64) * TB));
+        J.ws_slot = (int)(ws_need / (64 * TB));
         J.nblk = rgs * split;
         jobs.blk_start[i] = total;
         total += J.nblk;
         jobs.red_start[i] = red_total;
         if (split > 1) {
-            ws_need += (size_t)rgs * split * rows_per_block * TB;
-            red_total += rgs * (rows_per_block * TB / 256);
+            ws_need += (size_t)rgs * split * 64 * TB;
+            red_total += rgs * (64 * TB / 256);
         }
     }
     jobs.blk_start[jobs.n] = total;
     jobs.red_start[jobs.n] = red_total;
     if (ws_need > ctx->skinny_ws_cap) return RSV_FAIL("skinny gemm: workspace too small (%zu floats)", ws_need);
-    const bool tiled = jobs.j[0].tiled;
-    if (tiled) {
-        const bool i8 = jobs.j[0].fmt == FMT_I8;
-        for (int i = 1; i < jobs.n; i++)
-            if ((jobs.j[i].fmt == FMT_I8) != i8) return RSV_FAIL("skinny gemm: mixed formats in one tiled launch");
-        if (MB <= 32) {
-            if (i8) hipLaunchKernelGGL((k_skinny4<1, true>), dim3(total), dim3(256), 0, ctx->stream, jobs, MB, ctx->skinny_ws);
-            else hipLaunchKernelGGL((k_skinny4<1, false>), dim3(total), dim3(256), 0, ctx->stream, jobs, MB, ctx->skinny_ws);
-        } else {
-            if (i8) hipLaunchKernelGGL((k_skinny4<2, true>), dim3(total), dim3(256), 0, ctx->stream, jobs, MB, ctx->skinny_ws);
-            else hipLaunchKernelGGL((k_skinny4<2, false>), dim3(total), dim3(256), 0, ctx->stream, jobs, MB, ctx->skinny_ws);
-        }
-    } else {
-        if (MB <= 32)
-            hipLaunchKernelGGL(k_skinny<1>, dim3(total), dim3(256), 0, ctx->stream, jobs, MB, ctx->skinny_ws);
-        else
-            hipLaunchKernelGGL(k_skinny<2>, dim3(total), dim3(256), 0, ctx->stream, jobs, MB, ctx->skinny_ws);
-    }
+    if (MB <= 32)
+        hipLaunchKernelGGL(k_skinny<1>, dim3(total), dim3(256), 0, ctx->stream, jobs, MB, ctx->skinny_ws);
+    else
+        hipLaunchKernelGGL(k_skinny<2>, dim3(total), dim3(256), 0, ctx->stream, jobs, MB, ctx->skinny_ws);
     RSV_HIP(hipGetLastError());
     if (red_total) {
-        if (tiled) {
-            if (MB <= 32)
-                hipLaunchKernelGGL(k_skinny4_reduce<1>, dim3(red_total), dim3(256), 0, ctx->stream, jobs, MB,
-                                   ctx->skinny_ws);
-            else
-                hipLaunchKernelGGL(k_skinny4_reduce<2>, dim3(red_total), dim3(256), 0, ctx->stream, jobs, MB,
-                                   ctx->skinny_ws);
-        } else {
-            if (MB <= 32)
-                hipLaunchKernelGGL(k_skinny_reduce<1>, dim3(red_total), dim3(256), 0, ctx->stream, jobs, MB,
-                                   ctx->skinny_ws);
-            else
-                hipLaunchKernelGGL(k_skinny_reduce<2>, dim3(red_total), dim3(256), 0, ctx->stream, jobs, MB,
-                                   ctx->skinny_ws);
-        }
+        if (MB <= 32)
+            hipLaunchKernelGGL(k_skinny_reduce<1>, dim3(red_total), dim3(256), 0, ctx->stream, jobs, MB, ctx->skinny_ws);
+        else
+            hipLaunchKernelGGL(k_skinny_reduce<2>, dim3(red_total), dim3(256), 0, ctx->stream, jobs, MB, ctx->skinny_ws);
         RSV_HIP(hipGetLastError());
     }
     return 0;

@@ -246,7 +246,7 @@ struct SkinnyJobs {
     SkinnyJob j[kMaxJobs];
     int n;
     int blk_start[kMaxJobs + 1];
-    int red_start[kMaxJobs + 1];  // blocks of the slice-reduction launch
+    int red_start[kMaxJobs + 1];  // blocks of the slice-reduction launch (row-major weights)
 };
 int launch_skinny(rsv_ctx *ctx, SkinnyJobs &jobs, int MB);
 int launch_tile_weights(rsv_ctx *ctx, const void *src, void *dst, int n, int k, int esz);

@@ -434,12 +434,10 @@ def test_prefill_f16_weight_copies_bit_identical(bundles, kind, monkeypatch):
     assert np.array_equal(out["1"][1], out["0"][1])
 
 
-@pytest.mark.parametrize("env", ["RSV_SKINNY_V5=0", "RSV_SKINNY_SK1=0", "RSV_SKINNY_MIXED=0", "RSV_SKINNY_MAX_SPLIT=4",
-                                 "RSV_SKINNY_BLOCKS_PER_CU=1", "RSV_WKV_LORA_MM=0"])
+@pytest.mark.parametrize("env", ["RSV_WKV_LORA_MM=0"])
 def test_batched_alternative_kernels_agree(bundles, env, monkeypatch):
-    """Each selectable alternative of the batched paths (older skinny GEMM
-    forms, split limits, the two-launch LoRA-up +
-    WKV7) gives the default's logits and state to fp32 rounding, on a
+    """Each selectable alternative of the batched paths (the two-launch
+    LoRA-up + WKV7) gives the default's logits and state to fp32 rounding, on a
     prefill of more than 128 packed rows and batched decode steps."""
     b, _ = bundles["i8"]
     B = 20

@@ -592,14 +592,18 @@ def test_gemv_multi_lnmix_and_side_copy(be, batch):
     assert np.array_equal(be.get(ids["dst"], batch * C), be.get(ids["ln"], batch * C))
 
 
-@pytest.mark.parametrize("batch,k", [(16, 1280), (33, 1280), (64, 1280), (100, 1280), (64, 256), (33, 96), (16, 128)])
-def test_gemm_skinny(be, batch, k):
+@pytest.mark.parametrize("batch,k,n", [(16, 1280, 320), (33, 1280, 320), (64, 1280, 320), (100, 1280, 320),
+                                       (64, 256, 320), (33, 96, 320), (16, 128, 320), (64, 10240, 320),
+                                       (64, 2560, 8200), (40, 2560, 8200)])
+def test_gemm_skinny(be, batch, k, n):
     """Batched-decode MFMA GEMM (fp16 x, int8/fp16 W) against float64 with
     the loader's fp16 rounding of the dequantised weights.  k <= 256 takes the
-    one-pass small-K kernel (the LoRA-up chain), larger k the split-K one."""
+    one-pass small-K kernel (the LoRA-up chain), larger k the row-tile kernel:
+    with few row tiles (n = 320) its k-slices meet in the last-arriving block
+    of each row tile, with many (n = 8200, a partial last tile) one block
+    covers the whole k."""
     rsv = _rsv()
     rng = np.random.default_rng(60 + batch + k)
-    n = 320
     ki = k if k % 128 == 0 else 128  # int8 needs whole 128-groups
     idx, sz, W = _int8_weight(rng, n, ki)
     h = be.int8(idx, sz)
