@@ -37,25 +37,30 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def model_path(cache_dir):
+def model_path(cache_dir, kind="i8"):
+    """The configs[3] model file (seed 1), generated once per cache dir:
+    "i8" int8 linears + int8 head, "i8_f16" int8 linears + fp16 embedding
+    and head (the same files the 3B parity tests use)."""
     import synth
-    path = os.path.join(cache_dir, "rsv_3b_i8_seed1.st")
+    name, kw = {"i8": ("rsv_3b_i8_seed1.st", dict(linear="i8", head="i8")),
+                "i8_f16": ("rsv_3b_i8_f16head_seed1.st", dict(linear="i8", head="f16", emb="f16"))}[kind]
+    path = os.path.join(cache_dir, name)
     if not os.path.exists(path):
         t = time.time()
-        tmp = path + ".tmp"
-        synth.write_model(tmp, synth.THREE_B, seed=1, linear="i8", head="i8")
+        tmp = path + ".tmp%d" % os.getpid()
+        synth.write_model(tmp, synth.THREE_B, seed=1, **kw)
         os.replace(tmp, path)
         log(f"generated {path} in {time.time() - t:.1f}s")
     return path
 
 
-def decode_bytes_per_step(cfg, batch):
-    """Algorithmic HBM bytes of one decode step (int8 linears + int8 head,
-    fp16 LoRA, fp32 state and activations)."""
+def decode_bytes_per_step(cfg, batch, head_f16=False):
+    """Algorithmic HBM bytes of one decode step (int8 linears + int8 head or
+    fp16 head, fp16 LoRA, fp32 state and activations)."""
     C, L, F, V = cfg["c"], cfg["n_layer"], cfg["ffn"], cfg["vocab"]
     H, N = cfg["n_head"], cfg["head_size"]
     lin = L * (4 * C * C + 2 * C * F) * (1 + 1 / 32)
-    head = V * C * (1 + 1 / 32)
+    head = V * C * 2 if head_f16 else V * C * (1 + 1 / 32)
     lora = L * 2 * C * (cfg["wm"] + cfg["am"] + cfg["vm"] + cfg["gm"]) * 2
     vec = L * 14 * C * 4
     per_session = L * (2 * H * N * N * 4 + 4 * C * 4) + V * 4
@@ -136,6 +141,192 @@ def kernel_leg(reps=200):
                 timing="HIP events around one replay of a graph of the launches, on the backend stream")
 
 
+
+MFMA_F16_PEAK_TFLOPS = 2500.0   # dense fp16 matrix-core peak of one MI355X
+FP32_PEAK_TFLOPS = 157.3        # fp32 peak of one MI355X (the figure WKV7 T=512 is held to)
+
+
+class _Timer:
+    """Times `reps` enqueues of fn(i) captured as one HIP graph, replayed
+    once untimed, then once between HIP events on the backend's stream."""
+
+    def __init__(self, be):
+        import ctypes
+        import torch
+        import rsv
+        sp = ctypes.c_void_p()
+        rsv.hip_lib().rsv_stream(be.ctx, ctypes.byref(sp))
+        self.stream = torch.cuda.ExternalStream(sp.value, device=torch.device("cuda", 0))
+        self.be = be
+        self.torch = torch
+
+    def us(self, fn, reps):
+        be, torch = self.be, self.torch
+        for i in range(min(reps, 4)):
+            fn(i)
+        be.sync()
+        be.call("rsv_graph_begin")
+        for i in range(reps):
+            fn(i)
+        be.call("rsv_graph_end")
+        be.call("rsv_graph_replay")
+        be.sync()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(self.stream)
+        be.call("rsv_graph_replay")
+        e1.record(self.stream)
+        e1.synchronize()
+        return e0.elapsed_time(e1) * 1000.0 / reps
+
+
+def linear_leg():
+    """the four 3B weight shapes (out x in) in both weight forms
+    (int8 symmetric per-row scale in the reference format from N(0, 0.02^2)
+    masters; fp16 N(0, 0.02^2)) times activations of M rows, fp16 N(0, 1)
+    (the M <= 8 GEMV path takes them as f32 of the same values).  Each call
+    is timed over enough weight copies to exceed the 256 MB MALL.  M <= 8 is
+    held to HBM bandwidth; M >= 32 reports MFMA utilisation against dense
+    fp16 (and its bytes)."""
+    import ctypes
+    import rsv
+    import synth
+    NONE = 0xFFFFFFFF
+    be = rsv.Backend(0)
+    tm = _Timer(be)
+    rng = np.random.default_rng(11)
+    rows = []
+    for (n, k, name) in ((2560, 2560, "2560->2560 (att.*)"), (10240, 2560, "2560->10240 (ffn.key)"),
+                         (2560, 10240, "10240->2560 (ffn.value)"), (65536, 2560, "2560->65536 (head)")):
+        master = (rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02))
+        idx, sz = synth.quantize_rows(master)
+        w16_host = master.astype(np.float16).astype(np.float32)
+        del master
+        for fmt in ("int8", "fp16"):
+            wbytes = n * k * (1 + 4 / 128) if fmt == "int8" else 2 * n * k
+            ncopy = max(1, int(np.ceil(300e6 / wbytes)))
+            base = be.int8(idx, sz) if fmt == "int8" else be.tensor(w16_host, dtype=rsv.F16)
+            copies = [base]
+            for _ in range(ncopy - 1):
+                if fmt == "int8":
+                    h = rsv.Int8Handle(be.tensor(n=n * k // 4, dtype=rsv.U32), be.tensor(n=n * k // 128, dtype=rsv.U32), n, k)
+                    be.call("rsv_copy_device", base.idx, h.idx)
+                    be.call("rsv_copy_device", base.sz, h.sz)
+                    copies.append(h)
+                else:
+                    t = be.tensor(n=n * k, dtype=rsv.F16)
+                    be.call("rsv_copy_device", base, t)
+                    copies.append(t)
+            tiled = None
+            for M in (1, 8, 32, 128, 2048):
+                xh = rng.standard_normal((M, k)).astype(np.float16).astype(np.float32)
+                y = be.tensor(n=M * n)
+                if M <= 8:
+                    x = be.tensor(xh)
+                    if fmt == "int8":
+                        fn = lambda i, x=x, y=y, M=M: be.call("rsv_gemv_int8_plain", ctypes.byref(copies[i % ncopy]), x, y, n, k, M)
+                    else:
+                        fn = lambda i, x=x, y=y, M=M: be.call("rsv_gemv_f16", copies[i % ncopy], x, y, n, k, M)
+                    kern = "k_gemv_os2" if M == 1 else "k_gemv"
+                elif M <= 128:
+                    if tiled is None:
+                        tiled = []
+                        out = ctypes.c_uint32()
+                        for c in copies:
+                            if fmt == "int8":
+                                ht = rsv.Int8Handle(c.idx, c.sz, n, k)
+                                be.call("rsv_tile_weights", c.idx, n, k, 1, ctypes.byref(out))
+                                ht.idx = out.value
+                                be.call("rsv_tile_weights", c.sz, n, k, 4, ctypes.byref(out))
+                                ht.sz = out.value
+                                tiled.append(ht)
+                            else:
+                                be.call("rsv_tile_weights", c, n, k, 2, ctypes.byref(out))
+                                tiled.append(out.value)
+                    x = be.tensor(xh, dtype=rsv.F16)
+                    jobs = [rsv.MmJob(NONE if fmt == "int8" else t, ctypes.pointer(t) if fmt == "int8" else None,
+                                      n, k, x, y, NONE, 0, NONE, NONE, NONE, 1) for t in tiled]
+                    fn = lambda i, jobs=jobs, M=M: be.call("rsv_gemm_skinny", ctypes.byref(jobs[i % ncopy]), 1, M)
+                    kern = "k_skinny4" if n >= 65536 else ("k_skinny8" if k <= 2560 else "k_skinny5")
+                else:
+                    x = be.tensor(xh, dtype=rsv.F16)
+                    if fmt == "int8":
+                        fn = lambda i, x=x, y=y: be.call("rsv_gemm_ex", x, NONE, ctypes.byref(copies[i % ncopy]), y, 2048, n, k, 0, NONE, NONE, NONE)
+                    else:
+                        fn = lambda i, x=x, y=y: be.call("rsv_gemm_ex", x, copies[i % ncopy], None, y, 2048, n, k, 0, NONE, NONE, NONE)
+                    kern = "k_gemm3"
+                reps = max(8, min(200, int(3e-3 / max(wbytes / 5e12, 2 * M * n * k / 1.2e15))))
+                us = tm.us(fn, reps)
+                byts = wbytes + 2 * M * k + 4 * M * n
+                row = dict(shape=name, weights=fmt, M=M, kernel=kern, us=round(us, 3), bytes=int(byts),
+                           gbs=round(byts / us / 1e3, 1), hbm_frac=round(byts / us / 1e3 / HBM_PEAK_GBS, 4))
+                if M >= 32:
+                    tf = 2.0 * M * n * k / us / 1e6
+                    row.update(tflops=round(tf, 1), mfma_frac=round(tf / MFMA_F16_PEAK_TFLOPS, 4))
+                rows.append(row)
+                log(f"linear {name:24s} {fmt:4s} M={M:5d} {kern:10s} {us:9.2f} us {row['gbs']:8.0f} GB/s"
+                    + (f" {row['tflops']:7.1f} TFLOP/s" if M >= 32 else ""))
+            del copies, tiled
+        del idx, sz, w16_host
+    be.close()
+    return rows
+
+
+def wkv_leg():
+    """the fused WKV7 state update (L2-normalised k, DPLR update,
+    y = S r, GroupNorm + bonus) at H=40, N=64, fp32 state, B sessions x T
+    tokens.  T=1 is the decode op (fuse_ka_dplr_norm_batch); T=512 the
+    ragged prefill scan over B segments of 512 tokens.  Inputs as configs[2]
+    (r, v ~ N(0,1); k ~ N(0,1) normalised in the op; w = exp(-0.6065
+    sigmoid(x)); a = sigmoid(N(0,1)); S0 ~ N(0, 0.1^2)), fp32 in HBM.
+    Algorithmic bytes per (session, head): the state read and written once
+    (2 x 16384 B) + T x (5 inputs + 1 output) x 64 x 4 B; flops 36,864 per
+    (session, head, token)."""
+    import rsv
+    NONE = 0xFFFFFFFF
+    be = rsv.Backend(0)
+    tm = _Timer(be)
+    rng = np.random.default_rng(12)
+    H, N = 40, 64
+    C = H * N
+    sig = lambda t: 1.0 / (1.0 + np.exp(-t))
+    consts = dict(kk=be.tensor(np.ones(C, np.float32)), ka=be.tensor(rng.random(C).astype(np.float32)),
+                  rk=be.tensor(rng.standard_normal(C).astype(np.float32) * 0.1),
+                  g=be.tensor(np.ones(C, np.float32)), b=be.tensor(np.zeros(C, np.float32)))
+    rows = []
+    for B in (1, 32, 256):
+        S = be.tensor((rng.standard_normal(B * H * N * N) * 0.1).astype(np.float32))
+        for T in (1, 512):
+            rowsn = B * T
+            vec = lambda: be.tensor(rng.standard_normal(rowsn * C).astype(np.float32))
+            r, k, v = vec(), vec(), vec()
+            w = be.tensor(np.exp(-0.6065 * sig(rng.standard_normal(rowsn * C))).astype(np.float32))
+            a = be.tensor(sig(rng.standard_normal(rowsn * C)).astype(np.float32))
+            yn = be.tensor(n=rowsn * C)
+            if T == 1:
+                fn = lambda i: be.call("rsv_fuse_ka_dplr_norm_batch", S, k, consts["kk"], a, consts["ka"], r, v, w,
+                                       consts["g"], consts["b"], consts["rk"], NONE, NONE, yn, H, N, 1e-12, 64e-5, B)
+                kern = "k_wkv7_decode"
+            else:
+                st = be.tensor(np.arange(B, dtype=np.uint32) * T, dtype=rsv.U32)
+                ln = be.tensor(np.full(B, T, np.uint32), dtype=rsv.U32)
+                sl = be.tensor(np.arange(B, dtype=np.uint32), dtype=rsv.U32)
+                fn = lambda i: be.call("rsv_wkv7_seq_ragged", S, r, w, k, v, a, consts["kk"], consts["ka"], consts["rk"],
+                                       consts["g"], consts["b"], yn, st, ln, sl, B, H, N, 64e-5)
+                kern = "k_wkv7_seq_ragged"
+            reps = 50 if T == 1 else max(2, min(20, 256 // B))
+            us = tm.us(fn, reps)
+            byts = B * H * (2 * 16384 + T * 6 * 64 * 4)
+            fl = 36864.0 * B * H * T
+            gbs, tf = byts / us / 1e3, fl / us / 1e6
+            row = dict(B=B, T=T, kernel=kern, us=round(us, 2), bytes=int(byts), gbs=round(gbs, 1),
+                       hbm_frac=round(gbs / HBM_PEAK_GBS, 4), tflops=round(tf, 2),
+                       fp32_frac=round(tf / FP32_PEAK_TFLOPS, 4),
+                       bound="hbm" if T == 1 else "max(hbm, fp32)")
+            rows.append(row)
+            log(f"wkv7 B={B:3d} T={T:3d} {kern:18s} {us:10.2f} us {gbs:8.0f} GB/s {tf:7.2f} TFLOP/s")
+    be.close()
+    return rows
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -149,7 +340,11 @@ def main():
                     help="tokens sampled per session in the configs[4] ragged-serving leg")
     ap.add_argument("--cpu-tokens", type=int, default=24,
                     help="decode tokens of the CPU-baseline sample (about 14 s of one core; at most 28)")
+    ap.add_argument("--no-legs", action="store_true",
+                    help="skip the configs[1] linear and configs[2] WKV7 microbenchmarks and the fp16 variant")
     ap.add_argument("--cache", default=os.environ.get("RSV_BENCH_CACHE", "/tmp"))
+    ap.add_argument("--legs-only", action="store_true",
+                    help="run only the configs[1] linear and configs[2] WKV7 microbenchmarks")
     ap.add_argument("--kernel-only", action="store_true",
                     help="run only the dominant-kernel leg (for rocprofv3 summaries of that kernel)")
     ap.add_argument("--no-graph", action="store_true",
@@ -161,6 +356,11 @@ def main():
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}).",
               file=sys.stderr)
         sys.exit(2)
+
+    if args.legs_only:
+        lin, wk = linear_leg(), wkv_leg()
+        print(json.dumps({"linear_configs1": lin, "wkv7_configs2": wk}))
+        return
 
     if args.kernel_only:
         kl = kernel_leg()
@@ -184,7 +384,8 @@ def main():
     bundle.reset()
     bundle.infer_seq(prompt[:-1])
     S1 = bundle.create_batch_state(1)
-    S1.load(bundle.state_back())
+    snap1 = bundle.state_back()
+    S1.load(snap1)
     toks, ms = bundle.argmax_selfloop_batch_timed(S1, [int(prompt[-1])], args.steps)
     t0 = time.perf_counter()
     bundle.reset()
@@ -198,18 +399,26 @@ def main():
     bytes1 = decode_bytes_per_step(cfg, 1)
     log(f"B=1: {b1_tps:.1f} tok/s (device), {b1_wall_tps:.1f} tok/s (wall incl. capture), "
         f"{ms / args.steps * 1000:.1f} us/token, {bytes1 / (ms / args.steps / 1000) / 1e9:.0f} GB/s")
+    # ---------------- B = 1 sampling self-loop (configs[4]'s sampler)
+    sp1 = rsv.SamplerParams(temperature=1.0, top_k=0, top_p=0.9)
+    S1.load(snap1)
+    bundle.sample_selfloop_batch(S1, [int(prompt[-1])], 8, sp1)  # warm-up (captures the graph)
+    S1.load(snap1)
+    _, ms_s = bundle.sample_selfloop_batch_timed(S1, [int(prompt[-1])], args.steps, sp1)
+    b1_sample_tps = args.steps / (ms_s / 1000.0)
+    log(f"B=1 sample self-loop (T=1, top_p=0.9): {b1_sample_tps:.1f} tok/s")
     S1.free()
 
     # ---------------- B = 64 argmax self-loop
     B = 64
     S = bundle.create_batch_state(B)
     prompts = [synth.prompt(cfg, 32, seed=100 + i) for i in range(B)]
-    seeds = bundle.forward_seq_batch(S, [p[:-1] for p in prompts])
-    seeds = np.array([int(p[-1]) for p in prompts], np.uint32)
+    bundle.forward_seq_batch(S, [p[:-1] for p in prompts])
+    seeds64 = np.array([int(p[-1]) for p in prompts], np.uint32)
     snap = S.back()
-    bundle.argmax_selfloop_batch(S, seeds, 4)
+    bundle.argmax_selfloop_batch(S, seeds64, 4)
     S.load(snap)
-    _, ms64 = bundle.argmax_selfloop_batch_timed(S, seeds, args.steps_b64)
+    _, ms64 = bundle.argmax_selfloop_batch_timed(S, seeds64, args.steps_b64)
     b64_tps = B * args.steps_b64 / (ms64 / 1000.0)
     bytes64 = decode_bytes_per_step(cfg, B)
     log(f"B=64: {b64_tps:.0f} tok/s, {ms64 / args.steps_b64:.2f} ms/step, "
@@ -268,6 +477,36 @@ def main():
     kl = kernel_leg()
     log(f"kernel: {kl['kernel']}: {kl['avg_us']:.2f} us/launch, {kl['gbs']:.0f} GB/s")
 
+    # ---------------- configs[3] fp16 embedding/head variant, configs[1], configs[2]
+    variant = linear = wkv = None
+    if not args.no_legs:
+        path16 = model_path(args.cache, kind="i8_f16")
+        b16 = rsv.ModelBuilder(path16).build()
+        b16.infer_seq(prompt[:-1])
+        Sv = b16.create_batch_state(1)
+        Sv.load(b16.state_back())
+        snapv = Sv.back()
+        b16.argmax_selfloop_batch(Sv, [int(prompt[-1])], 8)
+        Sv.load(snapv)
+        _, msv = b16.argmax_selfloop_batch_timed(Sv, [int(prompt[-1])], args.steps)
+        Sv.free()
+        Sv = b16.create_batch_state(B)
+        b16.forward_seq_batch(Sv, [p[:-1] for p in prompts])
+        snapv = Sv.back()
+        b16.argmax_selfloop_batch(Sv, seeds64, 4)
+        Sv.load(snapv)
+        _, msv64 = b16.argmax_selfloop_batch_timed(Sv, seeds64, args.steps_b64)
+        Sv.free()
+        b16.close()
+        bytes1v = decode_bytes_per_step(cfg, 1, head_f16=True)
+        variant = dict(model="int8 linears, fp16 embedding and fp16 head (seed 1)",
+                       b1_tok_s=round(args.steps / (msv / 1000.0), 1),
+                       b1_hbm_frac=round(bytes1v / (msv / args.steps / 1000) / 1e9 / HBM_PEAK_GBS, 4),
+                       b64_tok_s=round(B * args.steps_b64 / (msv64 / 1000.0), 1))
+        log(f"fp16 variant: {variant}")
+        linear = linear_leg()
+        wkv = wkv_leg()
+
     # ---------------- CPU baseline (reference CPU fp32 path, restated)
     cpu = None
     if not args.no_cpu:
@@ -316,7 +555,10 @@ def main():
         "extra": {"b1_wall_tok_s": round(b1_wall_tps, 2),
                   "b64_tok_s": round(b64_tps, 1), "b64_ms_per_step": round(ms64 / args.steps_b64, 4),
                   "b64_hbm_frac": round(bytes64 / (ms64 / args.steps_b64 / 1000) / 1e9 / HBM_PEAK_GBS, 4),
-                  "prefill": prefill, "serve_ragged": serve},
+                  "b1_sample_selfloop_tok_s": round(b1_sample_tps, 2),
+                  "fp16_variant": variant,
+                  "prefill": prefill, "serve_ragged": serve,
+                  "linear_configs1": linear, "wkv7_configs2": wkv},
     }
     print(json.dumps(out))
     bundle.close()

@@ -114,6 +114,8 @@ int rsv_serve_ragged(rsv_bundle *b, rsv_state *s, const uint32_t *tokens, const 
  * milliseconds through *ms (hipEvent timing on the context stream). */
 int rsv_argmax_selfloop_batch_timed(rsv_bundle *b, rsv_state *s, const uint32_t *seeds, uint64_t n,
                                     uint32_t *out, float *ms);
+int rsv_sample_selfloop_batch_timed(rsv_bundle *b, rsv_state *s, const uint32_t *seeds, uint64_t n,
+                                    const rsv_sampler_params *sp, uint32_t *out, float *ms);
 
 /* Backend context of a bundle (for harnesses that call librsv_hip.so directly). */
 void *rsv_bundle_ctx(rsv_bundle *b);

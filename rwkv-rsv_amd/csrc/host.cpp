@@ -1774,4 +1774,11 @@ int rsv_sample_selfloop_batch(rsv_bundle *b, rsv_state *s, const uint32_t *seeds
     return selfloop(b, s->s, seeds, n, sp, out, nullptr);
 }
 
+int rsv_sample_selfloop_batch_timed(rsv_bundle *b, rsv_state *s, const uint32_t *seeds, uint64_t n,
+                                    const rsv_sampler_params *sp, uint32_t *out, float *ms) {
+    if (!b || !s || !seeds || !out || !sp || !ms) return herr("null argument");
+    HK(tokens_ok(b, seeds, s->s.batch));
+    return selfloop(b, s->s, seeds, n, sp, out, ms);
+}
+
 }  // extern "C"

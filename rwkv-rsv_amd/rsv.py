@@ -365,6 +365,15 @@ class Bundle:
                                                     ctypes.byref(ms)))
         return out.reshape(state.batch, n), ms.value
 
+    def sample_selfloop_batch_timed(self, state, seeds, n, sp):
+        s = _toks(seeds)
+        out = np.zeros(state.batch * n, np.uint32)
+        c = sp._c()
+        ms = ctypes.c_float()
+        _hchk(_host.rsv_sample_selfloop_batch_timed(self._h, state._h, _u32p(s), ctypes.c_uint64(n), ctypes.byref(c),
+                                                    _u32p(out), ctypes.byref(ms)))
+        return out.reshape(state.batch, n), ms.value
+
     def sample_selfloop_batch(self, state, seeds, n, sp):
         s = _toks(seeds)
         out = np.zeros(state.batch * n, np.uint32)
