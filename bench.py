@@ -159,12 +159,23 @@ class _Timer:
         self.stream = torch.cuda.ExternalStream(sp.value, device=torch.device("cuda", 0))
         self.be = be
         self.torch = torch
+        # --legs-eager: plain enqueues instead of a graph (for per-kernel
+        # traces, where the tracer times every dispatch itself)
+        self.eager = os.environ.get("RSV_BENCH_EAGER") == "1"
 
     def us(self, fn, reps):
         be, torch = self.be, self.torch
         for i in range(min(reps, 4)):
             fn(i)
         be.sync()
+        if self.eager:
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(self.stream)
+            for i in range(reps):
+                fn(i)
+            e1.record(self.stream)
+            e1.synchronize()
+            return e0.elapsed_time(e1) * 1000.0 / reps
         be.call("rsv_graph_begin")
         for i in range(reps):
             fn(i)
@@ -345,6 +356,8 @@ def main():
     ap.add_argument("--cache", default=os.environ.get("RSV_BENCH_CACHE", "/tmp"))
     ap.add_argument("--legs-only", action="store_true",
                     help="run only the configs[1] linear and configs[2] WKV7 microbenchmarks")
+    ap.add_argument("--legs-eager", action="store_true",
+                    help="time the microbenchmarks with plain enqueues instead of graph replays (for traces)")
     ap.add_argument("--kernel-only", action="store_true",
                     help="run only the dominant-kernel leg (for rocprofv3 summaries of that kernel)")
     ap.add_argument("--no-graph", action="store_true",
@@ -357,6 +370,8 @@ def main():
               file=sys.stderr)
         sys.exit(2)
 
+    if args.legs_eager:
+        os.environ["RSV_BENCH_EAGER"] = "1"
     if args.legs_only:
         lin, wk = linear_leg(), wkv_leg()
         print(json.dumps({"linear_configs1": lin, "wkv7_configs2": wk}))
