@@ -264,7 +264,7 @@ def linear_leg():
                         fn = lambda i, x=x, y=y: be.call("rsv_gemm_ex", x, NONE, ctypes.byref(copies[i % ncopy]), y, 2048, n, k, 0, NONE, NONE, NONE)
                     else:
                         fn = lambda i, x=x, y=y: be.call("rsv_gemm_ex", x, copies[i % ncopy], None, y, 2048, n, k, 0, NONE, NONE, NONE)
-                    kern = "k_gemm3"
+                    kern = "k_gemm3" if fmt == "int8" else "k_gemmd"
                 reps = max(8, min(200, int(3e-3 / max(wbytes / 5e12, 2 * M * n * k / 1.2e15))))
                 us = tm.us(fn, reps)
                 byts = wbytes + 2 * M * k + 4 * M * n

@@ -383,6 +383,215 @@ __global__ __launch_bounds__(256, BKT == 64 ? 3 : 2) void k_gemm3_multi(GemmJobs
         gemm3_body<false, BKT, 2>(g, m0, n0, As, Bs);
 }
 
+// Fourth form, for fp16 weights with k a multiple of 64 (the prefill GEMMs
+// on the fp16 weight copies): a large tile per block of 4 waves, one wave
+// per SIMD, and the operand tiles copied global -> LDS by
+// global_load_lds_dwordx4 (no VGPR staging, no LDS stores by the waves).
+//   - A stage is 64 k of the block's BMR activation rows and BNC weight
+//     rows, 128 bytes per row; NS = 3 stages rotate, the copy of stage s+2
+//     in flight while stage s is multiplied out, one barrier per stage.
+//   - Copy instruction i of wave w fills 1 KiB: rows 8g .. 8g+7 of the
+//     stage (g = w*NI + i; A rows first, then B rows), lane l taking row
+//     8g + l/8 and 16-byte piece (l%8) ^ gd_swz(row).  The XOR spreads the
+//     operand reads of 8 (or 16) consecutive rows over all the banks.
+//   - Each wave owns a (MI*32) x (NJ*32) tile of C as MI x NJ 32x32 MFMA
+//     blocks; per 16 k it reads MI + NJ operand pieces (ds_read_b128, in asm:
+//     the compiler cannot see which LDS copy a read waits for and would drain
+//     every copy in flight before it) and issues MI*NJ MFMAs, the reads of
+//     the next 16 k in flight during them.
+//   - The MFMA is the one of k_gemm2/3 (v_mfma_f32_32x32x16_f16, lane l
+//     holding k 8*(l/32) .. +7 of each 16 k, ascending k): every element's
+//     accumulation chain is the same, so the results equal the other forms'
+//     bit for bit (the int8 loader's fp16 rounding included).
+//   - Blocks are spread XCD-aware: the hardware deals consecutive block ids
+//     to the 8 XCDs in turn; block b takes tile (b%8)*(T/8) + b/8 of a
+//     grouped order (4 row tiles x all column tiles per group), so the
+//     blocks that share an XCD's L2 share operand tiles.
+template <int WM, int WN, int MI, int NJ>
+struct GdCfg {
+    static constexpr int BMR = WM * MI * 32, BNC = WN * NJ * 32;
+    static constexpr int ROWS = BMR + BNC;
+    static constexpr int SB = ROWS * 128;     // bytes of one stage
+    static constexpr int NI = ROWS / 8 / 4;   // copy instructions per wave per stage
+    static constexpr int NS = 3;
+    static constexpr int LDS = NS * SB;
+    static_assert(ROWS % 32 == 0, "stage rows must split evenly over 4 waves");
+    static_assert(LDS <= 160 * 1024, "LDS");
+};
+
+// block id -> tile order position: XCD-major when the block count allows
+__device__ __forceinline__ int gd_xcd_order(int bid, int T) {
+    return (T & 7) == 0 ? (bid & 7) * (T >> 3) + (bid >> 3) : bid;
+}
+
+// position t of the grouped order over tm x tn tiles -> (row tile, column tile)
+__device__ __forceinline__ void gd_tile(int t, int tm, int tn, int &mt, int &nt) {
+    constexpr int GM = 4;
+    const int gsz = GM * tn, grp = t / gsz, f = grp * GM, gm = min(GM, tm - f), r = t - grp * gsz;
+    mt = f + r % gm;
+    nt = r / gm;
+}
+
+// Stage row r keeps its logical 16-byte piece p in physical piece
+// p ^ gd_swz(r): any 8 consecutive rows from a multiple of 8 use 8 distinct
+// pieces (8 lanes x 16 bytes meet 32 banks once), and so do the 8 even and
+// the 8 odd rows of 16 consecutive rows (16 lanes over 64 banks: rows r and
+// r+1 sit 128 bytes apart, in the other half of the banks).
+__device__ __forceinline__ int gd_swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+
+// MULTI only separates the instantiations of the two kernels: the host
+// compilation pass cannot check the VGPR asm constraints, and a body it
+// instantiated once (with those errors deferred) is refused to a second
+// caller.
+template <int WM, int WN, int MI, int NJ, bool MULTI>
+__device__ __forceinline__ void gemmd_body(const GemmArgs &g, int m0, int n0, unsigned char *lds) {
+    using C = GdCfg<WM, WN, MI, NJ>;
+    constexpr int NI = C::NI;
+    // the wave index in a scalar register: what derives from it stays scalar
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int wm = (wave / WN) * MI * 32, wn = (wave % WN) * NJ * 32;
+    // Copies go through buffer resources over A ([m, lda]) and B ([n, k]):
+    // a row past the end reads as zeros (its offset is beyond the resource's
+    // size), so partial tiles need no clamping.  Instruction i of this wave
+    // copies row group gi = wave*NI + i: A rows 8*gi .. if gi < BMR/8, else
+    // B rows 8*gi - BMR ..; lane l takes row 8*gi + l/8 and logical piece
+    // (l%8) ^ gd_swz(row).
+    const __amdgpu_buffer_rsrc_t rsA = __builtin_amdgcn_make_buffer_rsrc((void *)g.a, (short)0, g.m * g.lda * 2, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsB = __builtin_amdgcn_make_buffer_rsrc((void *)g.b, (short)0, g.n * g.k * 2, 0x00020000);
+    const int lr = lane >> 3;
+    uint32_t voff[NI];
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+        const int gi = wave * NI + i, r = 8 * gi;
+        const int lp = (lane & 7) ^ gd_swz(r + lr);
+        voff[i] = r < C::BMR ? ((uint32_t)(m0 + r + lr) * (uint32_t)g.lda + lp * 8) * 2u
+                             : ((uint32_t)(n0 + r - C::BMR + lr) * (uint32_t)g.k + lp * 8) * 2u;
+    }
+    const int nA = min(max(C::BMR / 8 - wave * NI, 0), NI);  // this wave's A instructions
+    auto issue = [&](int s, int buf) {
+        unsigned char *dst = lds + buf * C::SB + wave * NI * 1024;
+#pragma unroll
+        for (int i = 0; i < NI; i++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(i < nA ? rsA : rsB, (__attribute__((address_space(3))) void *)(dst + i * 1024),
+                                                     16, voff[i], s * 128, 0, 0);
+    };
+    float16_t acc[MI][NJ];
+#pragma unroll
+    for (int i = 0; i < MI; i++)
+#pragma unroll
+        for (int j = 0; j < NJ; j++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) acc[i][j][e] = 0.0f;
+    // operand read addresses: row (l%32) of the wave's A / B strip, piece
+    // (2*st + l/32) ^ (l%8) of the 64-k stage for the 16-k step st
+    const uint32_t lds0 = (uint32_t)(uintptr_t)lds;
+    const uint32_t rowA = lds0 + (wm + (lane & 31)) * 128, rowB = lds0 + (C::BMR + wn + (lane & 31)) * 128;
+    uint32_t xo[4];
+#pragma unroll
+    for (int st = 0; st < 4; st++) xo[st] = ((2 * st + (lane >> 5)) ^ gd_swz(lane & 31)) * 16;
+    typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+    auto read = [&](u4 (&fa)[MI], u4 (&fb)[NJ], uint32_t boff, int st) {
+        const uint32_t va = rowA + boff + xo[st], vb = rowB + boff + xo[st];
+#pragma unroll
+        for (int i = 0; i < MI; i++) asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(fa[i]) : "v"(va), "i"(i * 4096));
+#pragma unroll
+        for (int j = 0; j < NJ; j++) asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(fb[j]) : "v"(vb), "i"(j * 4096));
+    };
+    auto ready = [&](u4 (&fa)[MI], u4 (&fb)[NJ]) {
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int i = 0; i < MI; i++) asm volatile("" : "+v"(fa[i]));
+#pragma unroll
+        for (int j = 0; j < NJ; j++) asm volatile("" : "+v"(fb[j]));
+    };
+    auto mfmas = [&](const u4 (&fa)[MI], const u4 (&fb)[NJ]) {
+#pragma unroll
+        for (int i = 0; i < MI; i++)
+#pragma unroll
+            for (int j = 0; j < NJ; j++)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8_t, fa[i]),
+                                                                 __builtin_bit_cast(half8_t, fb[j]), acc[i][j], 0, 0, 0);
+    };
+    // Three stage buffers, four operand register sets (one per 16-k step of
+    // a stage).  Step st of stage s: wait for its operands (read during step
+    // st-1), read step st+1's into the set step st-3 used (its MFMAs long
+    // issued: a read into a set the MFMAs just issued would wait for them),
+    // issue step st's MFMAs.  At the last step every wave has its operands of
+    // the stage in registers: after one barrier (which also publishes the
+    // next stage's copies, waited for before it) the stage's buffer takes the
+    // copy of stage s+3, and the next stage's first reads go out behind it.
+    const int nst = g.k / 64;
+    issue(0, 0);
+    if (nst > 1) issue(1, 1);
+    if (nst > 2) issue(2, 2);
+    if (nst > 2) sk_wait_vm(2 * NI);
+    else if (nst > 1) sk_wait_vm(NI);
+    else sk_wait_vm(0);
+    __builtin_amdgcn_s_barrier();
+    u4 fa[4][MI], fb[4][NJ];
+    read(fa[0], fb[0], 0, 0);
+    int buf = 0;
+    for (int s = 0; s < nst; s++) {
+        const int nbuf = buf == 2 ? 0 : buf + 1;
+#pragma unroll
+        for (int st = 0; st < 4; st++) {
+            __builtin_amdgcn_sched_barrier(0);
+            ready(fa[st], fb[st]);
+            if (st < 3) {
+                read(fa[st + 1], fb[st + 1], buf * C::SB, st + 1);
+            } else {
+                if (s + 2 < nst) sk_wait_vm(NI);
+                else sk_wait_vm(0);
+                __builtin_amdgcn_s_barrier();
+                if (s + 3 < nst) issue(s + 3, buf);
+                if (s + 1 < nst) read(fa[0], fb[0], nbuf * C::SB, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            mfmas(fa[st], fb[st]);
+        }
+        buf = nbuf;
+    }
+#define GEMMD_EPI(K) gemm2_epilogue<K, MI, NJ>(g, acc, m0, n0, wm, wn, lane)
+    switch (g.epi) {
+        case GE_BIAS: GEMMD_EPI(GE_BIAS); break;
+        case GE_ADD: GEMMD_EPI(GE_ADD); break;
+        case GE_RELU2: GEMMD_EPI(GE_RELU2); break;
+        case GE_TANH: GEMMD_EPI(GE_TANH); break;
+        case GE_WDECAY: GEMMD_EPI(GE_WDECAY); break;
+        case GE_SIGBIAS: GEMMD_EPI(GE_SIGBIAS); break;
+        case GE_VLERP: GEMMD_EPI(GE_VLERP); break;
+        case GE_SIGMOID: GEMMD_EPI(GE_SIGMOID); break;
+        default: GEMMD_EPI(GE_STORE); break;
+    }
+#undef GEMMD_EPI
+}
+
+template <int WM, int WN, int MI, int NJ>
+__global__ __launch_bounds__(256, 1) void k_gemmd(GemmArgs g) {
+    using C = GdCfg<WM, WN, MI, NJ>;
+    __shared__ __attribute__((aligned(1024))) unsigned char lds[C::LDS];
+    const int tm = (g.m + C::BMR - 1) / C::BMR, tn = (g.n + C::BNC - 1) / C::BNC;
+    int mt, nt;
+    gd_tile(gd_xcd_order(blockIdx.x, gridDim.x), tm, tn, mt, nt);
+    gemmd_body<WM, WN, MI, NJ, false>(g, mt * C::BMR, nt * C::BNC, lds);
+}
+
+template <int WM, int WN, int MI, int NJ>
+__global__ __launch_bounds__(256, 1) void k_gemmd_multi(GemmJobs jobs) {
+    using C = GdCfg<WM, WN, MI, NJ>;
+    __shared__ __attribute__((aligned(1024))) unsigned char lds[C::LDS];
+    const int T = gridDim.x, bid = blockIdx.x;
+    const int t = gd_xcd_order(bid, T);
+    int ji = 0;
+    while (ji + 1 < jobs.n && t >= jobs.blk_start[ji + 1]) ji++;
+    const GemmArgs &g = jobs.j[ji];
+    const int local = t - jobs.blk_start[ji];
+    const int tm = (g.m + C::BMR - 1) / C::BMR, tn = (g.n + C::BNC - 1) / C::BNC;
+    int mt, nt;
+    gd_tile(local, tm, tn, mt, nt);
+    gemmd_body<WM, WN, MI, NJ, true>(g, mt * C::BMR, nt * C::BNC, lds);
+}
+
 // k per stage: 64 (k_gemm3) where every job's k is a multiple of 64, else 32
 // (k_gemm2, double-buffered: the LoRA-up jobs, k = 96 etc.).
 static int gemm_check(const GemmArgs &g) {
@@ -399,6 +608,37 @@ static int gemm_check(const GemmArgs &g) {
     return 0;
 }
 
+// The DMA-tile form (fp16 weights, k % 64 == 0, offsets within 31 bits):
+// one of three tiles, whichever needs the fewest block rounds (one block per
+// CU) times tile area, weighted by the measured per-element cost of each form
+// (256x128 is the cheapest per element, 128x128 the dearest).
+enum GdKind { GD_NONE = 0, GD_256x160, GD_256x128, GD_128x128 };
+
+static bool gd_fits(const GemmArgs &g) {
+    return !g.b_i8 && g.k % 64 == 0 && (uint64_t)(g.m + 256) * g.lda * 2 < (1ull << 31) &&
+           (uint64_t)(g.n + 256) * g.k * 2 < (1ull << 31);
+}
+
+static int gd_tiles(const GemmArgs &g, int kind) {
+    const int bm = kind == GD_128x128 ? 128 : 256, bn = kind == GD_256x160 ? 160 : 128;
+    return ((g.m + bm - 1) / bm) * ((g.n + bn - 1) / bn);
+}
+
+static GdKind gd_pick(const GemmArgs *gs, int n, int cus) {
+    for (int i = 0; i < n; i++)
+        if (!gd_fits(gs[i])) return GD_NONE;
+    static const double area[4] = {0, 256.0 * 160 * 1.0, 256.0 * 128 * 0.86, 128.0 * 128 * 1.07};
+    GdKind best = GD_NONE;
+    double best_cost = 0;
+    for (int kind = GD_256x160; kind <= GD_128x128; kind++) {
+        long tiles = 0;
+        for (int i = 0; i < n; i++) tiles += gd_tiles(gs[i], kind);
+        const double cost = (double)((tiles + cus - 1) / cus) * area[kind];
+        if (best == GD_NONE || cost < best_cost) best = (GdKind)kind, best_cost = cost;
+    }
+    return best;
+}
+
 int launch_gemm_multi(rsv_ctx *ctx, GemmJobs &jobs) {
     if (jobs.n <= 0 || jobs.n > kMaxJobs) return RSV_FAIL("gemm_multi: 1..%d jobs", kMaxJobs);
     int total = 0;
@@ -409,6 +649,20 @@ int launch_gemm_multi(rsv_ctx *ctx, GemmJobs &jobs) {
         total += ((g.n + BN - 1) / BN) * ((g.m + BM - 1) / BM);
     }
     jobs.blk_start[jobs.n] = total;
+    const GdKind gk = gd_pick(jobs.j, jobs.n, ctx->sm_count > 0 ? ctx->sm_count : 256);
+    if (gk != GD_NONE) {
+        total = 0;
+        for (int i = 0; i < jobs.n; i++) {
+            jobs.blk_start[i] = total;
+            total += gd_tiles(jobs.j[i], gk);
+        }
+        jobs.blk_start[jobs.n] = total;
+        if (gk == GD_256x160) hipLaunchKernelGGL((k_gemmd_multi<4, 1, 2, 5>), dim3(total), dim3(256), 0, ctx->stream, jobs);
+        else if (gk == GD_256x128) hipLaunchKernelGGL((k_gemmd_multi<2, 2, 4, 2>), dim3(total), dim3(256), 0, ctx->stream, jobs);
+        else hipLaunchKernelGGL((k_gemmd_multi<2, 2, 2, 2>), dim3(total), dim3(256), 0, ctx->stream, jobs);
+        RSV_HIP(hipGetLastError());
+        return 0;
+    }
     bool k64 = true;
     for (int i = 0; i < jobs.n; i++) k64 &= jobs.j[i].k % 64 == 0;
     if (k64) hipLaunchKernelGGL((k_gemm3_multi<64>), dim3(total), dim3(256), 0, ctx->stream, jobs);
@@ -419,6 +673,15 @@ int launch_gemm_multi(rsv_ctx *ctx, GemmJobs &jobs) {
 
 int launch_gemm(rsv_ctx *ctx, const GemmArgs &g) {
     if (gemm_check(g)) return -1;
+    const GdKind gk = gd_pick(&g, 1, ctx->sm_count > 0 ? ctx->sm_count : 256);
+    if (gk != GD_NONE) {
+        const dim3 gd_grid(gd_tiles(g, gk));
+        if (gk == GD_256x160) hipLaunchKernelGGL((k_gemmd<4, 1, 2, 5>), gd_grid, dim3(256), 0, ctx->stream, g);
+        else if (gk == GD_256x128) hipLaunchKernelGGL((k_gemmd<2, 2, 4, 2>), gd_grid, dim3(256), 0, ctx->stream, g);
+        else hipLaunchKernelGGL((k_gemmd<2, 2, 2, 2>), gd_grid, dim3(256), 0, ctx->stream, g);
+        RSV_HIP(hipGetLastError());
+        return 0;
+    }
     const dim3 grid((g.n + BN - 1) / BN, (g.m + BM - 1) / BM);
     // 128-row tiles: 256-row tiles (one wave per SIMD at 275 registers)
     // measured 1.5x slower on the prefill GEMMs

@@ -769,21 +769,6 @@ __global__ __launch_bounds__(256) void k_skinny4_reduce(SkinnyJobs jobs, int MB,
 #undef SK_RED_CALL
 }
 
-// s_waitcnt vmcnt(n) for n known at compile time after unrolling (the
-// switch folds); other counters left alone.
-#define SK_VM(n) case n: __builtin_amdgcn_s_waitcnt((n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8)); break;
-__device__ __forceinline__ void sk_wait_vm(int n) {
-    switch (n < 63 ? n : 63) {
-        SK_VM(0) SK_VM(1) SK_VM(2) SK_VM(3) SK_VM(4) SK_VM(5) SK_VM(6) SK_VM(7) SK_VM(8) SK_VM(9) SK_VM(10) SK_VM(11)
-        SK_VM(12) SK_VM(13) SK_VM(14) SK_VM(15) SK_VM(16) SK_VM(17) SK_VM(18) SK_VM(19) SK_VM(20) SK_VM(21) SK_VM(22)
-        SK_VM(23) SK_VM(24) SK_VM(25) SK_VM(26) SK_VM(27) SK_VM(28) SK_VM(29) SK_VM(30) SK_VM(31) SK_VM(32) SK_VM(33)
-        SK_VM(34) SK_VM(35) SK_VM(36) SK_VM(37) SK_VM(38) SK_VM(39) SK_VM(40) SK_VM(41) SK_VM(42) SK_VM(43) SK_VM(44)
-        SK_VM(45) SK_VM(46) SK_VM(47) SK_VM(48) SK_VM(49) SK_VM(50) SK_VM(51) SK_VM(52) SK_VM(53) SK_VM(54) SK_VM(55)
-        SK_VM(56) SK_VM(57) SK_VM(58) SK_VM(59) SK_VM(60) SK_VM(61) SK_VM(62)
-        default: __builtin_amdgcn_s_waitcnt((15) | (3 << 14) | (0x7 << 4) | (0xF << 8)); break;
-    }
-}
-#undef SK_VM
 
 // Epilogue of one 32-row x TB-session tile: thread t owns row t % 32 and
 // sessions t/32, t/32 + 8, ...; v[q] holds its TB/8 sums.  Every read

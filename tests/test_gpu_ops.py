@@ -527,6 +527,56 @@ def test_gemm_prefill_shapes(be, m, n, k):
         assert rel_err(got["64"][1].reshape(m, n), np.maximum(acc8, 0) ** 2) < 1e-4
 
 
+@pytest.mark.parametrize("m,n,k", [(4096, 2560, 2560), (2048, 2560, 2560), (1024, 2560, 2560), (3000, 640, 10240),
+                                   (1030, 384, 640)])
+def test_gemm_dma_tiles_equal_int8_loader(be, m, n, k):
+    """The fp16-weight prefill GEMM (operand tiles copied to LDS by DMA, one
+    of three tile shapes picked by the grid size: these shapes take each of
+    them, with partial tiles) on the fp16 copy of an int8 matrix gives the
+    int8 loader's results bit for bit (the same MFMA chain per element), and
+    both match float64 with the loader's fp16 rounding of the weights."""
+    rsv = _rsv()
+    rng = np.random.default_rng(m + 3 * n + k)
+    A = rng.standard_normal((m, k)).astype(np.float16)
+    At = be.tensor(A.astype(np.float32), dtype=rsv.F16)
+    idx, sz, W = _int8_weight(rng, n, k)
+    h = be.int8(idx, sz)
+    W16 = be.tensor(n=n * k, dtype=rsv.F16)
+    be.call("rsv_dequant_int8_to_f16", ctypes.byref(h), W16, n, k)
+    bias = be.tensor(rng.standard_normal(n).astype(np.float32))
+    C8, C16 = be.tensor(n=m * n), be.tensor(n=m * n)
+    be.call("rsv_gemm_ex", At, NONE, ctypes.pointer(h), C8, m, n, k, 1, bias, NONE, NONE)
+    be.call("rsv_gemm_ex", At, W16, None, C16, m, n, k, 1, bias, NONE, NONE)
+    g8, g16 = be.get(C8, m * n), be.get(C16, m * n)
+    assert np.array_equal(g8.view(np.uint32), g16.view(np.uint32))
+    ref = A.astype(np.float64) @ W.astype(np.float16).astype(np.float64).T + be.get(bias, n).astype(np.float64)
+    assert rel_err(g16.reshape(m, n), ref) < 1e-5
+
+
+@pytest.mark.parametrize("m", [1030, 4096])
+def test_gemm_multi_fp16_jobs_equal_single_launches(be, m):
+    """A job list of fp16 weights only (the prefill stage-1 list: r, k, v
+    and the LoRA-down matrices) runs on the DMA-tile GEMM in one launch; each
+    job equals its own launch bit for bit."""
+    rsv = _rsv()
+    rng = np.random.default_rng(m + 5)
+    k = 2560 if m == 4096 else 640
+    x = [be.tensor(rng.standard_normal((m, k)).astype(np.float32), dtype=rsv.F16) for _ in range(3)]
+    ns = [2560, 2560, 96, 64] if m == 4096 else [384, 384, 96, 64]
+    ws = [be.tensor((rng.standard_normal((n, k)) * 0.02).astype(np.float32), dtype=rsv.F16) for n in ns]
+    jobs, outs = [], []
+    for i, (w, n) in enumerate(zip(ws, ns)):
+        epi = 4 if i == 2 else 0
+        ym, ys = be.tensor(n=m * n), be.tensor(n=m * n)
+        jobs.append(rsv.MmJob(w, None, n, k, x[min(i, 2)], ym, NONE, epi, NONE, NONE, NONE, 0))
+        be.call("rsv_gemm_ex", x[min(i, 2)], w, None, ys, m, n, k, epi, NONE, NONE, NONE)
+        outs.append((ym, ys, n))
+    arr = (rsv.MmJob * len(jobs))(*jobs)
+    be.call("rsv_gemm_multi", ctypes.cast(arr, ctypes.c_void_p), len(jobs), m)
+    for ym, ys, n in outs:
+        assert np.array_equal(be.get(ym, m * n).view(np.uint32), be.get(ys, m * n).view(np.uint32)), n
+
+
 def test_gemm_epilogues(be):
     rsv = _rsv()
     rng = np.random.default_rng(8)
