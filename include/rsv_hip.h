@@ -330,6 +330,9 @@ int rsv_gemm_ex(rsv_ctx *ctx, uint32_t a, uint32_t w16, const rsv_int8 *w8, uint
  *   prologue 0: x;  1: x * xmul;  2: sigmoid(x);
  *   3: LN-mix: ln = LN(x)*gamma + beta (eps 1e-5, over k), x' = ln + coef*(prev - ln);
  *      lnout (optional, [batch, k]) receives ln.
+ *   4: GroupNorm-gate, batch 1: x' = ((GN(x)*gamma + beta) + prev) * xmul, GN over each
+ *      64 columns (two-pass, gn_eps inside the sqrt): the att.output operand after the
+ *      split form of rsv_wkv7_lora_decode (x = y, prev = bonus*v, xmul = gate).
  *   epilogue 0: store; 1: relu^2; 2: y += acc; 3: tanh; 4: exp(scale*sigmoid(acc+p0));
  *      5: sigmoid(acc+p0); 6: y + sigmoid(acc+p0)*(p1 - y); 7: store to y and p1.
  * W is F16 (w16) or int8 (w8).  After the launch, side_dst[b, :side_n] =
@@ -345,6 +348,7 @@ typedef struct rsv_gemv_job {
     int prologue, epilogue;
     uint32_t xmul, p0, p1, scale;
     uint32_t gamma, beta, prev, coef, lnout;
+    float gn_eps; /* prologue 4 */
 } rsv_gemv_job;
 int rsv_gemv_multi(rsv_ctx *ctx, const rsv_gemv_job *jobs, uint64_t njobs, uint32_t side_src,
                    uint32_t side_dst, uint64_t side_n, uint64_t batch);
@@ -423,6 +427,12 @@ typedef struct rsv_wkv_lora {
     uint64_t n_head, w_rank, a_rank, v_rank, g_rank;
     float eps, gn_eps;
     int f16_io; /* 1: the four *_mid inputs are F16, g_mid already holds sigmoid(g), and yg is F16 */
+    /* Split form (both set, F32 io): the head's
+     * rows run on 4 blocks, yg receives the raw y = S r, y_bonus the bonus
+     * term times v and y_gate the gate; the GroupNorm and the gate are then
+     * applied by the consumer (rsv_gemv_multi prologue 4).  0xFFFFFFFF: the
+     * one-launch form with the GroupNorm inside. */
+    uint32_t y_bonus, y_gate; /* F32 [batch, C] */
 } rsv_wkv_lora;
 int rsv_wkv7_lora_decode(rsv_ctx *ctx, const rsv_wkv_lora *op, uint64_t batch);
 

@@ -417,6 +417,12 @@ int rsv_wkv7_lora_decode(rsv_ctx *ctx, const rsv_wkv_lora *op, uint64_t batch) {
         if (opnd(ctx, up[m], RSV_F16, C * rk[m], &p, "wkv7_lora up")) return -1;
         a.up[m] = (const _Float16 *)p;
     }
+    if (op->y_bonus != 0xFFFFFFFFu || op->y_gate != 0xFFFFFFFFu) {
+        if (opnd(ctx, op->y_bonus, RSV_F32, B * C, &p, "wkv7_lora y_bonus")) return -1;
+        a.y_bonus = (float *)p;
+        if (opnd(ctx, op->y_gate, RSV_F32, B * C, &p, "wkv7_lora y_gate")) return -1;
+        a.y_gate = (float *)p;
+    }
     if (op->side_src != 0xFFFFFFFFu && op->side_dst != 0xFFFFFFFFu) {
         if (opnd(ctx, op->side_src, RSV_F32, B * C, &p, "wkv7_lora side_src")) return -1;
         a.side_src = (const float *)p;
@@ -1352,7 +1358,12 @@ extern "C" int rsv_gemv_multi(rsv_ctx *ctx, const rsv_gemv_job *jobs, uint64_t n
         if (q.w8 ? job_i8(ctx, g, q.w8, q.m, q.k, "gemv_multi") : job_f16(ctx, g, q.w16, q.m, q.k, "gemv_multi"))
             return -1;
         if (job_xy(ctx, g, q.x, q.y, batch, "gemv_multi")) return -1;
-        if (q.prologue < PRO_NONE || q.prologue > PRO_LNMIX) return RSV_FAIL("gemv_multi: bad prologue %d", q.prologue);
+        if (q.prologue < PRO_NONE || q.prologue > PRO_GNGATE) return RSV_FAIL("gemv_multi: bad prologue %d", q.prologue);
+        if (q.prologue == PRO_GNGATE &&
+            (batch != 1 || q.k % 64 != 0 || q.gamma == 0xFFFFFFFFu || q.beta == 0xFFFFFFFFu ||
+             q.prev == 0xFFFFFFFFu || q.xmul == 0xFFFFFFFFu))
+            return RSV_FAIL("gemv_multi: the GroupNorm-gate prologue needs batch 1, k %% 64 == 0, gamma, beta, prev and xmul");
+        g.eps = q.gn_eps;
         if (q.epilogue < EPI_STORE || q.epilogue > EPI_STORE2) return RSV_FAIL("gemv_multi: bad epilogue %d", q.epilogue);
         g.pro = q.prologue;
         g.epi = q.epilogue;

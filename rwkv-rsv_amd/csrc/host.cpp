@@ -710,7 +710,7 @@ int forward_layer_fused(rsv_bundle *b, uint64_t i, WorkBufs &w, GpuState &s) {
     const rsv_model_info &I = b->info;
     const uint64_t C = I.n_embd, B = w.batch;
     Layer &L = b->layers[i];
-    enum { P_NONE = 0, P_MUL = 1, P_SIG = 2, P_LN = 3 };
+    enum { P_NONE = 0, P_MUL = 1, P_SIG = 2, P_LN = 3, P_GN = 4 };
     enum { E_STORE = 0, E_RELU2 = 1, E_ADD = 2, E_TANH = 3, E_WDECAY = 4, E_SIGB = 5, E_VLERP = 6, E_STORE2 = 7 };
     if (L.rw.i8 != L.kw.i8 || L.rw.i8 != L.vw.i8)
         return herr("layer %llu: receptance/key/value must share one format", (unsigned long long)i);
@@ -747,8 +747,20 @@ int forward_layer_fused(rsv_bundle *b, uint64_t i, WorkBufs &w, GpuState &s) {
         op.eps = L2_EPS;
         op.gn_eps = GN_EPS;
         op.f16_io = 0;
+        // one session: the head's rows over 4 blocks, the GroupNorm and the
+        // gate in the att.output prologue (y raw in yn, bonus*v in a, gate in g)
+        const bool split = B == 1;
+        op.y_bonus = split ? w.a : NONE;
+        op.y_gate = split ? w.g : NONE;
         CK(rsv_wkv7_lora_decode(c, &op, B));
-        rsv_gemv_job j4 = lin_job(L.ow, w.yn, w.x, P_NONE, E_ADD);
+        rsv_gemv_job j4 = lin_job(L.ow, w.yn, w.x, split ? P_GN : P_NONE, E_ADD);
+        if (split) {
+            j4.gamma = L.lnx_w;
+            j4.beta = L.lnx_b;
+            j4.prev = w.a;
+            j4.xmul = w.g;
+            j4.gn_eps = GN_EPS;
+        }
         CK(rsv_gemv_multi(c, &j4, 1, NONE, NONE, 0, B));
     } else {
         rsv_gemv_job j2[4] = {
@@ -931,6 +943,7 @@ int forward_layer_mm(rsv_bundle *b, uint64_t i, WorkBufs &w, GpuState &s) {
         op.eps = L2_EPS;
         op.gn_eps = GN_EPS;
         op.f16_io = 1;
+        op.y_bonus = op.y_gate = NONE;
         CK(rsv_wkv7_lora_decode(c, &op, B));
         rsv_mm_job j4 = mm_job(L.ow, w.yg16, w.x, G_ADD);
         CK(rsv_gemm_skinny(c, &j4, 1, B));

@@ -479,6 +479,7 @@ __device__ __forceinline__ void gemv_os2_body(const GemvJob &J, int rb, float4 *
     const int row0 = (rb * NW + wave) * SLOTS + slot;
     const int row = min(row0, M - 1);
     const bool ln = PV == 2 && J.pro == PRO_LNMIX, mul = PV >= 1 && J.pro == PRO_MUL;
+    const bool gn = PV == 2 && J.pro == PRO_GNGATE;
     // 1. vectors (clamped addresses; lanes past K are zeroed after the loads)
     const float4 *X4 = (const float4 *)J.x;
     float4 xa[Q], ga[PV >= 1 ? Q : 1], ba[PV == 2 ? Q : 1], ca[PV == 2 ? Q : 1], pa[PV == 2 ? Q : 1];
@@ -487,10 +488,10 @@ __device__ __forceinline__ void gemv_os2_body(const GemvJob &J, int rb, float4 *
         const int q = min(tid + NT * i, K4 - 1);
         xa[i] = X4[q];
         if constexpr (PV == 2) {
-            if (ln) {
+            if (ln || gn) {
                 ga[i] = ((const float4 *)J.gamma)[q];
                 ba[i] = ((const float4 *)J.beta)[q];
-                ca[i] = ((const float4 *)J.coef)[q];
+                ca[i] = ((const float4 *)(ln ? J.coef : J.xmul))[q];
                 pa[i] = ((const float4 *)J.prev)[q];
             }
         }
@@ -543,6 +544,24 @@ __device__ __forceinline__ void gemv_os2_body(const GemvJob &J, int rb, float4 *
             xa[i].y = l.y + ca[i].y * (pa[i].y - l.y);
             xa[i].z = l.z + ca[i].z * (pa[i].z - l.z);
             xa[i].w = l.w + ca[i].w * (pa[i].w - l.w);
+        }
+      }
+    }
+    if constexpr (PV == 2) {
+      if (gn) {
+        // GroupNorm over each 64 columns (two-pass, eps inside the sqrt): the
+        // 16 float4 of a group sit in 16 consecutive threads (one DPP row),
+        // then ((d * rstd * gamma + beta) + bonus) * gate (model.rs:803-826)
+#pragma unroll
+        for (int i = 0; i < Q; i++) {
+            const float mu = group_sum_last<16>((xa[i].x + xa[i].y) + (xa[i].z + xa[i].w)) * (1.0f / 64.0f);
+            const float d0 = xa[i].x - mu, d1 = xa[i].y - mu, d2 = xa[i].z - mu, d3 = xa[i].w - mu;
+            const float var = group_sum_last<16>((d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3)) * (1.0f / 64.0f) + J.eps;
+            const float inv = 1.0f / sqrtf(var);
+            xa[i].x = (d0 * inv * ga[i].x + ba[i].x + pa[i].x) * ca[i].x;
+            xa[i].y = (d1 * inv * ga[i].y + ba[i].y + pa[i].y) * ca[i].y;
+            xa[i].z = (d2 * inv * ga[i].z + ba[i].z + pa[i].z) * ca[i].z;
+            xa[i].w = (d3 * inv * ga[i].w + ba[i].w + pa[i].w) * ca[i].w;
         }
       }
     }
@@ -644,7 +663,7 @@ __global__ __launch_bounds__(NT) void k_gemv_os2(GemvJobs jobs) {
 // the 3B decode shapes).  Returns 1 when the jobs do not fit.
 static int launch_os2(rsv_ctx *ctx, GemvJobs &jobs) {
     int cpl_max = 0, kmax = 0;
-    bool lnmix = false, gate = false;
+    bool lnmix = false, gate = false, gngate = false;
     for (int i = 0; i < jobs.n; i++) {
         GemvJob &J = jobs.j[i];
         const int nc = J.K / (J.fmt == FMT_I8 ? 16 : 8);
@@ -654,12 +673,13 @@ static int launch_os2(rsv_ctx *ctx, GemvJobs &jobs) {
         cpl_max = std::max(cpl_max, cpl);
         kmax = std::max(kmax, J.K);
         lnmix |= J.pro == PRO_LNMIX;
+        gngate |= J.pro == PRO_GNGATE;
         gate |= J.pro == PRO_MUL;
     }
     const int nt = (lnmix || kmax > 2560) ? 640 : 320;
     const int qn = (kmax / 4 + nt - 1) / nt;
     const int q = qn <= 1 ? 1 : qn <= 2 ? 2 : qn <= 4 ? 4 : 0;
-    if (!q || (lnmix && q > 2)) return 1;
+    if (!q || ((lnmix || gngate) && q > 2)) return 1;
     int total = 0;
     for (int i = 0; i < jobs.n; i++) {
         GemvJob &J = jobs.j[i];
@@ -672,9 +692,11 @@ static int launch_os2(rsv_ctx *ctx, GemvJobs &jobs) {
     const size_t lds = (size_t)kmax * 4 + (size_t)kmax / 16 * 4;
 #define OS2(C, QQ, N, V) hipLaunchKernelGGL((k_gemv_os2<C, QQ, N, V>), dim3(total), dim3(N), lds, ctx->stream, jobs)
     const bool c5 = cpl_max <= 5;
-    if (lnmix) {
+    if (lnmix || (gngate && nt == 640)) {
         if (q == 1) { if (c5) OS2(5, 1, 640, 2); else OS2(10, 1, 640, 2); }
         else { if (c5) OS2(5, 2, 640, 2); else OS2(10, 2, 640, 2); }
+    } else if (gngate) {  // the GroupNorm-gate operand of att.output: 320-thread blocks as plain k <= 2560
+        if (q == 1) OS2(5, 1, 320, 2); else OS2(5, 2, 320, 2);
     } else if (nt == 320) {  // k <= 2560: at most 5 chunks per lane
         if (q == 1) { if (gate) OS2(5, 1, 320, 1); else OS2(5, 1, 320, 0); }
         else { if (gate) OS2(5, 2, 320, 1); else OS2(5, 2, 320, 0); }
@@ -722,6 +744,8 @@ int launch_gemv_jobs(rsv_ctx *ctx, GemvJobs &jobs, int batch) {
         const int rc = launch_os2(ctx, jobs);
         if (rc <= 0) return rc;
     }
+    for (int i = 0; i < jobs.n; i++)
+        if (jobs.j[i].pro == PRO_GNGATE) return RSV_FAIL("gemv: the GroupNorm-gate prologue runs on the one-session kernel only (k <= 10240)");
     // Lanes per row: a full wave when rows are long, a quarter wave for the
     // short LoRA-up rows (k = rank).  Long rows (ffn.value) keep fewer rows
     // per wave so more waves are resident.

@@ -512,6 +512,171 @@ __global__ __launch_bounds__(256, SB == 4 ? 3 : 2) void k_wkv7_lora_mb(WkvLoraAr
 #undef WKV_MB_LOAD_SESSION
 }
 
+// ------------------------------- fused LoRA-up + decode step, rows split
+// One session's head over four blocks (grid 4H x B, 256 threads), block
+// part p owning state rows 16p .. 16p+15, so that 4H blocks stream the
+// LoRA-up weights and the state instead of H.  Every block forms the head's
+// column vectors (k_hat, b = -k_hat*a, w, k_mod, r) and the two column sums
+// (|kk|^2, bonus) itself, which needs the w and a LoRA-up rows of all 64
+// columns; the v and g rows only for its own 16 rows.  The GroupNorm needs
+// the y of all 64 rows, so it is left to the consumer: the block writes
+// y = S r (raw), bonus * v and the gate g per row, and the att.output GEMV
+// applies ((y - mean) * rstd * gamma + beta + bonus*v) * g in its prologue
+// (gemv prologue PRO_GNGATE).  The four blocks of a head sit on one XCD
+// (consecutive block ids go to the 8 XCDs in turn) so the w/a rows they all
+// read come from one L2.
+//   LoRA dots: w and a as in k_wkv7_lora (column j = tid/4, quarter tid%4,
+//   quad sums); v and g with 16 threads per row (row 16p + tid/16).
+//   State: row 16p + tid/16, columns 4*(tid%16) .. +3; the row sums S k_hat
+//   and S r are 16-lane DPP row sums.
+__device__ __forceinline__ float row16_sum(float v) {
+    v += quad_dpp<0xB1>(v);  // quad_perm 1,0,3,2
+    v += quad_dpp<0x4E>(v);  // quad_perm 2,3,0,1
+    v += quad_dpp<0x141>(v); // row_half_mirror
+    v += quad_dpp<0x140>(v); // row_mirror: every lane of the 16-lane row holds its sum
+    return v;
+}
+
+__global__ __launch_bounds__(256) void k_wkv7_lora_rows(WkvLoraArgs A) {
+    __shared__ float mids[1024];
+    __shared__ float hv[5 * 64];
+    __shared__ float red[8];
+    const int H = A.H, C = H * 64, tid = threadIdx.x, b = blockIdx.y;
+    // block -> (head, part): the 4 parts of a head on one XCD when H % 8 == 0
+    const int bid = blockIdx.x;
+    const int h = (H & 7) == 0 ? (bid & 7) + 8 * (bid >> 5) : bid >> 2;
+    const int p = (H & 7) == 0 ? (bid >> 3) & 3 : bid & 3;
+    const int j = tid >> 2, q = tid & 3, c = h * 64 + j;          // column role
+    const int rr = 16 * p + (tid >> 4), s16 = tid & 15, cr = h * 64 + rr;  // row role
+    const int m0 = A.mid_n[0], m1 = A.mid_n[1], m2 = A.mid_n[2], m3 = A.mid_n[3];
+    const int L4 = m0 + m1 + m2 + m3;
+    // 1. loads: w/a up rows of column j (quarter q), v/g up rows of row rr
+    // (part s16 of 16), then mids, vectors and the 16 state rows
+    uint4 wl[2][8];
+#pragma unroll
+    for (int m = 0; m < 2; m++) {
+        const int mid = A.mid_n[m], np = mid >> 5;
+        const uint4 *wp = (const uint4 *)(A.up[m] + (size_t)c * mid + q * (mid >> 2));
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+            if (e < np) wl[m][e] = wp[e];
+    }
+    // v and g rows: rank/16 halves per thread (2..16), as 2-half pieces
+    uint32_t vl[2][8];
+#pragma unroll
+    for (int m = 0; m < 2; m++) {
+        const int mid = A.mid_n[2 + m], np = mid >> 5;
+        const uint32_t *wp = (const uint32_t *)(A.up[2 + m] + (size_t)cr * mid + s16 * (mid >> 4));
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+            if (e < np) vl[m][e] = wp[e];
+    }
+    for (int e = tid; e < L4; e += 256) {
+        const int m = e < m0 ? 0 : e < m0 + m1 ? 1 : e < m0 + m1 + m2 ? 2 : 3;
+        const int off = m == 0 ? 0 : m == 1 ? m0 : m == 2 ? m0 + m1 : m0 + m1 + m2;
+        const float x = ((const float *)A.mid[m])[(size_t)b * A.mid_n[m] + (e - off)];
+        mids[e] = m == 3 ? sig_f(x) : x;
+    }
+    const size_t vo = (size_t)b * C + c, ro = (size_t)b * C + cr;
+    const float kc = A.k[vo], rc = A.r[vo];
+    const float w0 = A.w0[c], a0 = A.a0[c], kkc = A.kk[c], kac = A.ka[c], rkc = A.rk[c];
+    const float vrow = A.v[ro], vfrow = A.vf[ro], v0row = A.v0[cr], sw = A.scale[0];
+    float4 *srow = (float4 *)(A.S + (((size_t)b * H + h) * 64 + rr) * 64) + s16;
+    const float4 st = *srow;
+    if (h == 0 && p == 0 && A.side_dst)
+        for (int e = tid; e < C; e += 256) A.side_dst[(size_t)b * C + e] = A.side_src[(size_t)b * C + e];
+    __syncthreads();
+    // 2. LoRA dots
+    float acc[2];
+#pragma unroll
+    for (int m = 0; m < 2; m++) {
+        const int mid = A.mid_n[m], np = mid >> 5;
+        const float *xm = mids + (m == 0 ? 0 : m0) + q * (mid >> 2);
+        float sm = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            if (e >= np) break;
+            const uint4 w = wl[m][e];
+            const float4 x0 = *(const float4 *)(xm + 8 * e), x1 = *(const float4 *)(xm + 8 * e + 4);
+            sm = fmaf(x0.x, h2f_w(w.x), sm);
+            sm = fmaf(x0.y, h2f_w(w.x >> 16), sm);
+            sm = fmaf(x0.z, h2f_w(w.y), sm);
+            sm = fmaf(x0.w, h2f_w(w.y >> 16), sm);
+            sm = fmaf(x1.x, h2f_w(w.z), sm);
+            sm = fmaf(x1.y, h2f_w(w.z >> 16), sm);
+            sm = fmaf(x1.z, h2f_w(w.w), sm);
+            sm = fmaf(x1.w, h2f_w(w.w >> 16), sm);
+        }
+        acc[m] = quad_sum(sm);
+    }
+    float racc[2];
+#pragma unroll
+    for (int m = 0; m < 2; m++) {
+        const int mid = A.mid_n[2 + m], np = mid >> 5;
+        const float *xm = mids + (m == 0 ? m0 + m1 : m0 + m1 + m2) + s16 * (mid >> 4);
+        float sm = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            if (e >= np) break;
+            const uint32_t w = vl[m][e];
+            const float2 x0 = *(const float2 *)(xm + 2 * e);
+            sm = fmaf(x0.x, h2f_w(w), sm);
+            sm = fmaf(x0.y, h2f_w(w >> 16), sm);
+        }
+        racc[m] = row16_sum(sm);
+    }
+    const float wd = expf(sig_f(acc[0] + w0) * sw);
+    const float aa = sig_f(acc[1] + a0);
+    const float vv = vrow + sig_f(racc[0] + v0row) * (vfrow - vrow);
+    const float gg = racc[1];
+    // 3. column vectors and the two column sums (as k_wkv7_lora)
+    const float kk = kc * kkc;
+    const float kmod = kc + kac * (kc * aa - kc);
+    const float p_nrm = wave_sum(q == 0 ? kk * kk : 0.0f);
+    const float p_bon = wave_sum(q == 0 ? rc * kmod * rkc : 0.0f);
+    if (q == 0) {
+        hv[j] = kk;
+        hv[64 + j] = aa;
+        hv[128 + j] = wd;
+        hv[192 + j] = kmod;
+        hv[256 + j] = rc;
+    }
+    if ((tid & 63) == 0) {
+        red[tid >> 6] = p_nrm;
+        red[4 + (tid >> 6)] = p_bon;
+    }
+    __syncthreads();
+    float nrm = sqrtf((red[0] + red[1]) + (red[2] + red[3]));
+    nrm = nrm < A.eps ? A.eps : nrm;
+    const float inv = 1.0f / nrm;
+    const float bonus = (red[4] + red[5]) + (red[6] + red[7]);
+    // 4. row rr, columns 4*s16 .. +3: S = S diag(w) + (S k_hat) b^T + v k_mod^T; y = S r
+    float sr[4] = {st.x, st.y, st.z, st.w}, kh[4];
+    float sa = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        kh[e] = hv[4 * s16 + e] * inv;
+        sa = fmaf(sr[e], kh[e], sa);
+    }
+    sa = row16_sum(sa);
+    float y = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const int cc = 4 * s16 + e;
+        const float bb = kh[e] * (-hv[64 + cc]);
+        const float ns = sr[e] * hv[128 + cc] + sa * bb + vv * hv[192 + cc];
+        sr[e] = ns;
+        y = fmaf(ns, hv[256 + cc], y);
+    }
+    y = row16_sum(y);
+    *srow = make_float4(sr[0], sr[1], sr[2], sr[3]);
+    if (s16 == 0) {
+        ((float *)A.yg)[ro] = y;
+        A.y_bonus[ro] = bonus * vv;
+        A.y_gate[ro] = gg;
+    }
+}
+
 int launch_wkv7_lora(rsv_ctx *ctx, const WkvLoraArgs &a, int batch) {
     if (a.H <= 0 || batch <= 0 || batch > 65535) return RSV_FAIL("wkv7_lora: bad h=%d batch=%d", a.H, batch);
     int L4 = 0;
@@ -525,7 +690,11 @@ int launch_wkv7_lora(rsv_ctx *ctx, const WkvLoraArgs &a, int batch) {
     // 512: 4 sessions per block (the head's LoRA-up rows read once per block;
     // 8 or 16 sessions per block measured slower: too few blocks to spread
     // the per-CU traffic)
-    if (a.f16_io && batch >= 16 && L4 <= 512) {
+    if (a.y_bonus || a.y_gate) {
+        if (!a.y_bonus || !a.y_gate || a.f16_io) return RSV_FAIL("wkv7_lora: the split form needs F32 io and both bonus and gate outputs");
+        if ((size_t)4 * a.H > 65535) return RSV_FAIL("wkv7_lora: too many heads for the split form");
+        hipLaunchKernelGGL(k_wkv7_lora_rows, dim3(4 * a.H, batch), dim3(256), 0, ctx->stream, a);
+    } else if (a.f16_io && batch >= 16 && L4 <= 512) {
         hipLaunchKernelGGL(k_wkv7_lora_mb<4>, dim3(a.H, (batch + 3) / 4), dim3(256), 0, ctx->stream, a, batch);
     } else if (a.f16_io) hipLaunchKernelGGL(k_wkv7_lora<true>, dim3(a.H, batch), dim3(256), 0, ctx->stream, a);
     else hipLaunchKernelGGL(k_wkv7_lora<false>, dim3(a.H, batch), dim3(256), 0, ctx->stream, a);

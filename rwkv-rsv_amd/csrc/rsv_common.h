@@ -56,6 +56,7 @@ enum GemvPro {
     PRO_MUL = 1,      // x * xmul
     PRO_SIGMOID = 2,  // sigmoid(x)
     PRO_LNMIX = 3,    // ln = LN(x)*gamma+beta; ln + coef*(prev - ln)   (LN over the K columns)
+    PRO_GNGATE = 4,   // ((GN64(x)*gamma + beta) + prev) * xmul   (GroupNorm over each 64 columns, eps)
 };
 enum GemvEpi {
     EPI_STORE = 0,    // y = acc
@@ -81,6 +82,7 @@ struct GemvJob {
     // coef [K]; lnout [batch, K] receives the plain LN rows when non-null
     const float *gamma, *beta, *prev, *coef;
     float *lnout;
+    float eps;  // PRO_GNGATE
     int M, K;
     int fmt, epi, pro;
     int ldx, ldy;  // batch strides in elements
@@ -272,7 +274,9 @@ struct WkvLoraArgs {
     const float *w0, *a0, *v0;       // [C]
     const float *scale;              // device scalar (decay scale)
     const float *kk, *ka, *rk, *gamma, *beta;  // [C]
-    void *yg;                        // [B, C] out: (GroupNorm(y) + bonus) * g, F32 or (f16_io) F16
+    void *yg;                        // [B, C] out: (GroupNorm(y) + bonus) * g, F32 or (f16_io) F16;
+                                     // with y_bonus/y_gate set, the raw y = S r (split form)
+    float *y_bonus, *y_gate;         // [B, C] split form: bonus * v and the gate g (GroupNorm left to the consumer)
     const float *side_src;           // [B, C] copied to side_dst (optional)
     float *side_dst;
     int H, mid_n[4];

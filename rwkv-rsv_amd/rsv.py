@@ -50,7 +50,7 @@ class GemvJob(ctypes.Structure):
                 ("epilogue", ctypes.c_int), ("xmul", ctypes.c_uint32), ("p0", ctypes.c_uint32),
                 ("p1", ctypes.c_uint32), ("scale", ctypes.c_uint32), ("gamma", ctypes.c_uint32),
                 ("beta", ctypes.c_uint32), ("prev", ctypes.c_uint32), ("coef", ctypes.c_uint32),
-                ("lnout", ctypes.c_uint32)]
+                ("lnout", ctypes.c_uint32), ("gn_eps", ctypes.c_float)]
 
 
 class MmJob(ctypes.Structure):
