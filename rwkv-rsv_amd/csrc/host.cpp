@@ -1308,6 +1308,14 @@ int serve_ragged(rsv_bundle *b, GpuState &s, const uint32_t *tokens, const uint6
     };
     int rc = 0;
     uint64_t nst = 0;
+    // Steps in which every slot decodes one token run the batched decode step
+    // (the kernels of the B-session self-loop) instead of the packed prefill,
+    // captured once as a HIP graph and replayed (RSV_NO_GRAPH=1: enqueued
+    // eagerly); steps with prompt pieces, or with finished slots, take the
+    // packed path.
+    WorkBufs *dw = nullptr;
+    bool dgraph = false;
+    const bool deager = getenv("RSV_NO_GRAPH") && getenv("RSV_NO_GRAPH")[0] && getenv("RSV_NO_GRAPH")[0] != '0';
     do {
         // sampler work rows for up to B segments
         if ((rc = new_tensor(b, V * B, RSV_F32, temp))) break;
@@ -1352,12 +1360,32 @@ int serve_ragged(rsv_bundle *b, GpuState &s, const uint32_t *tokens, const uint6
             if (segs.empty()) break;
             if (nst >= max_steps) { rc = herr("serve_ragged: more than %llu steps", (unsigned long long)max_steps); break; }
             const auto t0 = std::chrono::steady_clock::now();
-            if ((rc = prefill(b, s, segs, nullptr, true))) break;
+            const bool all_decode = npre == 0 && ndec == B;
+            if (all_decode) {
+                if (!dw && (rc = get_bufs(b, B, dw))) break;
+                if (rsv_store_tokens(c, dw->token, one.data(), B)) { rc = herr("store_tokens: %s", rsv_last_error()); break; }
+                if (deager) {
+                    if ((rc = decode_step(b, *dw, s))) break;
+                } else {
+                    if (!dgraph) {
+                        if (rsv_graph_begin(c)) { rc = herr("graph_begin: %s", rsv_last_error()); break; }
+                        const int cap = decode_step(b, *dw, s);
+                        const int end_rc = rsv_graph_end(c);
+                        if (cap) { rc = cap; break; }
+                        if (end_rc) { rc = herr("graph_end: %s", rsv_last_error()); break; }
+                        dgraph = true;
+                    }
+                    if (rsv_graph_replay(c)) { rc = herr("graph_replay: %s", rsv_last_error()); break; }
+                }
+            } else if ((rc = prefill(b, s, segs, nullptr, true))) {
+                break;
+            }
+            const uint32_t logits = all_decode ? dw->logits : b->seq.logits;  // prefill may reallocate its rows
             const uint64_t S = segs.size();
             for (uint64_t g = 0; g < S; g++) seed_row[g] = seeds[seg_slot[g]] + (uint32_t)sl[seg_slot[g]].gen;
             if (rsv_store_sampler_async_batch(c, sampler, 0, sp->temperature, sp->top_k, sp->top_p, seed_row.data(), S,
                                               sp->repetition_penalty, sp->frequency_penalty, sp->presence_penalty, 0) ||
-                rsv_sample_into_host_seeded_batch(c, b->seq.logits, tok, V, temp, NONE, counter, sampler, hist, S) ||
+                rsv_sample_into_host_seeded_batch(c, logits, tok, V, temp, NONE, counter, sampler, hist, S) ||
                 rsv_download_u32(c, tok, drawn.data(), S)) {
                 rc = herr("serve_ragged sampler: %s", rsv_last_error());
                 break;

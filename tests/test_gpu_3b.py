@@ -175,17 +175,19 @@ def test_3b_serve_ragged_greedy_matches_per_session(model3b):
     """configs[4] at the 3B shape, scaled down: six sessions with prompts of
     5..700 tokens served by the ragged scheduler with a 512-token budget
     (prompts split across steps and sharing steps with decode tokens),
-    drawn by the GPU sampler with top_k = 1.  Every token equals the argmax
-    of the logits of that session run alone (prompt as one prefill, then one
-    token at a time): the schedule, the packing and the slot bookkeeping
-    change no session's tokens.  Session 0's prompt logits are also checked
-    against the oracle."""
+    drawn by the GPU sampler with top_k = 1.  Every token is the argmax of
+    the logits of that session run alone (prompt as one prefill, then one
+    token at a time), or, for tokens drawn in the all-decode steps (the
+    batched decode kernels, other roundings), a token whose logit there is
+    within 1e-2 x std (the logits bound) of the maximum: the schedule, the
+    packing and the slot bookkeeping change no session's tokens.  Session
+    0's prompt logits are also checked against the oracle."""
     import rsv
     kind, b, m = model3b
     sp = rsv.SamplerParams(temperature=1.0, top_k=1, top_p=1.0)
 
     def check(q, k, lg, got, seed):
-        return got == int(np.argmax(lg)) or lg[got] == lg.max()
+        return got == int(np.argmax(lg)) or lg[got] >= lg.max() - RMSE_BOUND * float(np.std(lg))
 
     res = _serve_vs_single(b, m, kind, sp, check)
     log(kind, f"serve greedy: packed vs per-session {sum(res)}/{len(res)}")

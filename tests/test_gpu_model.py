@@ -302,7 +302,11 @@ def test_serve_ragged_matches_per_session_runs(bundles):
     steps by a small token budget and interleaved with other slots' decode
     tokens, give the same sampled tokens as serving each session alone (its
     prompt as one prefill, then one token at a time) with the oracle sampler
-    on the GPU logits and the same seed rule (token k of slot q: seeds[q] + k)."""
+    on the GPU logits and the same seed rule (token k of slot q: seeds[q] + k).
+    Steps in which every slot decodes run the batched decode step instead of
+    the packed prefill (other kernels, logits equal to fp32 rounding): a draw
+    there may move to the neighbouring candidate in token order when the
+    sampling threshold falls within that rounding, never further."""
     rsv = _rsv()
     b, _ = bundles["i8"]
     lens = [1, 7, 19, 3, 30]
@@ -319,6 +323,7 @@ def test_serve_ragged_matches_per_session_runs(bundles):
     assert sum(s["sampled"] for s in steps) == len(lens) * D
     assert all(s["prefill_tokens"] + s["decode_tokens"] <= budget for s in steps)
     assert any(s["prefill_tokens"] and s["decode_tokens"] for s in steps), "no step mixed prefill and decode"
+    assert any(s["prefill_tokens"] == 0 and s["decode_tokens"] == len(lens) for s in steps), "no all-decode step"
     # per-session reference
     agree = total = 0
     for q, p in enumerate(prompts):
@@ -329,10 +334,15 @@ def test_serve_ragged_matches_per_session_runs(bundles):
             if k:
                 lg = b.infer_seq([prev])
             want = orc.sample(lg, sp.temperature, sp.top_k, sp.top_p, seeds[q] + k)
-            agree += int(want == toks[q, k])
+            got = int(toks[q, k])
+            if want != got:
+                cand = np.sort(np.argsort(-lg.astype(np.float64), kind="stable")[:512])
+                pos = {int(t): i for i, t in enumerate(cand)}
+                assert got in pos and want in pos and abs(pos[got] - pos[want]) <= 1, (q, k, got, want)
+            agree += int(want == got)
             total += 1
-            prev = int(toks[q, k])
-    assert agree == total, f"{agree}/{total}"
+            prev = got
+    assert agree >= total - 2, f"{agree}/{total}"
 
 
 def test_serve_ragged_errors(bundles):
