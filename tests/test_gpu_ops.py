@@ -418,6 +418,27 @@ def test_sample_matches_oracle(be, params):
     assert mism <= 1, f"{mism}/{trials} draws differ"
 
 
+@pytest.mark.parametrize("n,params", [
+    (70000, dict(temperature=1.0, top_k=0, top_p=0.9)),
+    (70000, dict(temperature=0.8, top_k=50, top_p=0.9)),
+    (1000, dict(temperature=1.0, top_k=0, top_p=0.9)),
+    (1000, dict(temperature=1.0, top_k=0, top_p=1.0)),
+])
+def test_sample_other_row_lengths(be, n, params):
+    """Rows longer than 65,536 take the general sampler kernel (row in global
+    memory), shorter ones the register-resident one: both against the oracle
+    sampler, with the same allowance as above."""
+    rng = np.random.default_rng(n)
+    mism = 0
+    trials = 20
+    for s in range(trials):
+        lg = (rng.standard_normal(n) * 2.0).astype(np.float32)
+        want = orc.sample(lg, params["temperature"], params["top_k"], params["top_p"], 500 + s)
+        got = _sample_gpu(be, lg, params["temperature"], params["top_k"], params["top_p"], 500 + s)
+        mism += want != got
+    assert mism <= 1, f"{mism}/{trials} draws differ"
+
+
 def test_sample_batch_low_temperature_is_argmax(be):
     """backend_cuda.rs:7919-8011 (xorshift32 logits, T=1e-4, top_k=50)."""
     rsv = _rsv()
