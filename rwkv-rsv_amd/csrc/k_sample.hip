@@ -217,7 +217,7 @@ __device__ uint32_t radix_select(const float *t, int n, int R, SampShared &sh) {
     return prefix;
 }
 
-// The same over keys held in registers: kr[0..cnt) of each thread.
+// The same over keys held in registers (kr[0..PER) of each thread, all live).
 template <int PER>
 __device__ uint32_t radix_select_regs(const uint32_t (&kr)[PER], int cnt, int R, SampShared &sh) {
     uint32_t prefix = 0, mask = 0;
@@ -226,7 +226,7 @@ __device__ uint32_t radix_select_regs(const uint32_t (&kr)[PER], int cnt, int R,
         const int shift = 24 - 8 * pass;
         radix_clear(sh);
 #pragma unroll
-        for (int j = 0; j < PER; j++) radix_count(kr[j], j < cnt && (kr[j] & mask) == prefix, shift, pass == 0, sh);
+        for (int j = 0; j < PER; j++) radix_count(kr[j], (kr[j] & mask) == prefix, shift, pass == 0, sh);
         radix_pick(remaining, sh);
         prefix |= sh.sel_bin << shift;
         mask |= 255u << shift;
@@ -261,15 +261,16 @@ __device__ void cand_sort(SampShared &sh) {
 
 // Gathers the R largest keys (ties at the threshold by ascending index) into
 // sh.ckey/cidx sorted by (key desc, index asc), R <= kCand.  Thread t holds
-// the keys of its contiguous elements [lo, lo + cnt) in kr (cnt <= PER).
+// the keys of its contiguous elements [lo, lo + PER) in kr.
 template <int PER>
 __device__ void top_r_keys(const uint32_t (&kr)[PER], int lo, int cnt, int R, SampShared &sh) {
     const uint32_t kthr = radix_select_regs<PER>(kr, cnt, R, sh);
     uint32_t gt = 0, eq = 0;
 #pragma unroll
     for (int j = 0; j < PER; j++) {
-        gt += j < cnt && kr[j] > kthr;
-        eq += j < cnt && kr[j] == kthr;
+        const uint32_t k = kr[j];
+        gt += k > kthr;
+        eq += k == kthr;
     }
     sh.cnt_gt[threadIdx.x] = gt;
     sh.cnt_eq[threadIdx.x] = eq;
@@ -278,7 +279,6 @@ __device__ void top_r_keys(const uint32_t (&kr)[PER], int lo, int cnt, int R, Sa
     uint32_t og = sh.cnt_gt[threadIdx.x], oe = sh.cnt_eq[threadIdx.x];
 #pragma unroll
     for (int j = 0; j < PER; j++) {
-        if (j >= cnt) continue;
         const uint32_t k = kr[j];
         if (k > kthr) {
             sh.ckey[og] = k;
@@ -542,21 +542,21 @@ __global__ __launch_bounds__(kSampBS) void k_sample(const float *__restrict__ lo
     }
 }
 
-// The same pipeline for rows of at most 64 x kSampBS entries with the row in
-// registers: thread t holds the 64 contiguous entries [64t, 64t + 64) (fewer
-// for short rows), so the passes (penalties, 1/T, top-k, max, exp, division,
+// The same pipeline for rows of exactly PER x kSampBS entries (PER a power of
+// two up to 64) with the row in registers: thread t holds the PER contiguous
+// entries [PER t, PER t + PER), so the passes (penalties, 1/T, top-k, max, exp, division,
 // top-p cut, non-zero compaction) run on registers and the radix select on
 // their keys.  Global memory (`temp`) is written only where the
 // reference's summation order must be replayed: the two 112-lane sums, and
 // the full-row CDF scan when more than 512 entries stay non-zero.  The
 // candidates' probabilities are the inverse of their sort keys (exact).
 // Every step computes what k_sample computes, in the same order.
+template <int PER>
 __global__ __launch_bounds__(kSampBS) void k_sample_regs(const float *__restrict__ logits, uint32_t *__restrict__ token,
                                                          int n, float *__restrict__ temp_all,
                                                          uint32_t *__restrict__ counter_all,
                                                          const float *__restrict__ sampler,
                                                          const uint32_t *__restrict__ hist_all, int hist_stride) {
-    constexpr int PER = 64;
     __shared__ SampShared sh;
     const int b = blockIdx.x, tid = threadIdx.x;
     const float *lg = logits + (size_t)b * n;
@@ -571,12 +571,10 @@ __global__ __launch_bounds__(kSampBS) void k_sample_regs(const float *__restrict
     const bool do_topk = top_k > 0u && top_k < (uint32_t)n;
     const int K = do_topk ? (int)top_k : 0;
     const bool fast = K > 0 && K <= 50;
-    const int per = (n + kSampBS - 1) / kSampBS;  // <= PER (launcher)
-    const int lo = tid * per, cnt = max(min(n - lo, per), 0);
-    const bool full = per == PER && cnt == PER;
+    const int lo = tid * PER, cnt = PER;  // n == PER * kSampBS (launcher)
     float v[PER];
     auto load_row = [&](const float *src) {
-        if (full) {
+        if constexpr (PER >= 4) {
             const float4 *s4 = (const float4 *)(src + lo);
 #pragma unroll
             for (int q = 0; q < PER / 4; q++) {
@@ -585,18 +583,17 @@ __global__ __launch_bounds__(kSampBS) void k_sample_regs(const float *__restrict
             }
         } else {
 #pragma unroll
-            for (int j = 0; j < PER; j++) v[j] = j < cnt ? src[lo + j] : 0.0f;
+            for (int j = 0; j < PER; j++) v[j] = src[lo + j];
         }
     };
     auto store_row = [&]() {
-        if (full) {
+        if constexpr (PER >= 4) {
             float4 *d4 = (float4 *)(temp + lo);
 #pragma unroll
             for (int q = 0; q < PER / 4; q++) d4[q] = make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
         } else {
 #pragma unroll
-            for (int j = 0; j < PER; j++)
-                if (j < cnt) temp[lo + j] = v[j];
+            for (int j = 0; j < PER; j++) temp[lo + j] = v[j];
         }
     };
     load_row(lg);
@@ -612,7 +609,6 @@ __global__ __launch_bounds__(kSampBS) void k_sample_regs(const float *__restrict
         __syncthreads();
 #pragma unroll
         for (int j = 0; j < PER; j++) {
-            if (j >= cnt) continue;
             const uint32_t c = counter[lo + j];
             float l = v[j];
             if (c > 0u) {
@@ -628,29 +624,29 @@ __global__ __launch_bounds__(kSampBS) void k_sample_regs(const float *__restrict
 #pragma unroll
     for (int j = 0; j < PER; j++) v[j] *= invT;
 
+    // the selections run on the keys of the row, which replace the values
+    // in the same registers and are turned back after (fkey is a bijection
+    // but for -0, which becomes +0: no comparison or exp sees the difference)
     uint32_t kr[PER];
     if (fast) {
 #pragma unroll
         for (int j = 0; j < PER; j++) kr[j] = fkey(v[j]);
         top_r_keys<PER>(kr, lo, cnt, K, sh);  // sorted top-K list in sh.cidx[0..K)
-        const float thv = fkey_inv(sh.ckey[K - 1]);
+        const uint32_t kth = sh.ckey[K - 1];
 #pragma unroll
-        for (int j = 0; j < PER; j++)
-            if (v[j] < thv) v[j] = -1e30f;
+        for (int j = 0; j < PER; j++) v[j] = kr[j] < kth ? -1e30f : fkey_inv(kr[j]);
     } else if (do_topk) {
 #pragma unroll
         for (int j = 0; j < PER; j++) kr[j] = fkey(v[j]);
         const uint32_t kthr = radix_select_regs<PER>(kr, cnt, K, sh);
 #pragma unroll
-        for (int j = 0; j < PER; j++)
-            if (kr[j] < kthr) v[j] = -1e30f;
+        for (int j = 0; j < PER; j++) v[j] = kr[j] < kthr ? -1e30f : fkey_inv(kr[j]);
     }
 
     // softmax; the total in the reference's 112-lane order from global memory
     float lm = -1e30f;
 #pragma unroll
-    for (int j = 0; j < PER; j++)
-        if (j < cnt) lm = fmaxf(lm, v[j]);
+    for (int j = 0; j < PER; j++) lm = fmaxf(lm, v[j]);
     const float m = block_max(lm, sh);
 #pragma unroll
     for (int j = 0; j < PER; j++) v[j] = expf(v[j] - m);
@@ -681,6 +677,8 @@ __global__ __launch_bounds__(kSampBS) void k_sample_regs(const float *__restrict
 #pragma unroll
             for (int j = 0; j < PER; j++) kr[j] = fkey(v[j]);
             top_r_keys<PER>(kr, lo, cnt, R, sh);
+#pragma unroll
+            for (int j = 0; j < PER; j++) v[j] = fkey_inv(kr[j]);
             for (int c = tid; c < R; c += kSampBS) sh.cval[c] = fkey_inv(sh.ckey[c]);
             __syncthreads();
             if (tid == 0) {
@@ -712,20 +710,19 @@ __global__ __launch_bounds__(kSampBS) void k_sample_regs(const float *__restrict
             // the top-K list in its order from the K-th candidate up, with the
             // cut applied to each probability (recomputed as above)
             const float cut = (top_p > 0.0f && top_p < 1.0f) ? sh.cutoff : -1e30f;
-            float ps[50];
             float tot = 0.0f;
             for (int j = K - 1; j >= 0; j--) {
                 float p = expf(fkey_inv(sh.ckey[j]) - m);
                 if (total > 0.0f) p /= total;
                 if (p < cut) p = 0.0f;
-                ps[j] = p;
+                sh.cval[j] = p;
                 if (p > 0.0f) tot += p;
             }
             const float u = u01_dev(seed) * tot;
             float acc = 0.0f;
             int chosen = sh.cidx[K - 1];
             for (int j = K - 1; j >= 0; j--) {
-                const float p = ps[j];
+                const float p = sh.cval[j];
                 if (p > 0.0f) {
                     acc += p;
                     if (acc > u) { chosen = sh.cidx[j]; break; }
@@ -742,7 +739,7 @@ __global__ __launch_bounds__(kSampBS) void k_sample_regs(const float *__restrict
     const float tot = sum112(temp, n, sh);
     uint32_t nz = 0;
 #pragma unroll
-    for (int j = 0; j < PER; j++) nz += j < cnt && v[j] != 0.0f;
+    for (int j = 0; j < PER; j++) nz += v[j] != 0.0f;
     sh.cnt_gt[tid] = nz;
     const uint32_t NZ = block_exscan(sh.cnt_gt, sh);
     const bool compact = NZ <= (uint32_t)kCand;
@@ -750,7 +747,7 @@ __global__ __launch_bounds__(kSampBS) void k_sample_regs(const float *__restrict
         uint32_t o = sh.cnt_gt[tid];
 #pragma unroll
         for (int j = 0; j < PER; j++)
-            if (j < cnt && v[j] != 0.0f) { sh.cidx[o] = lo + j; sh.cval[o] = v[j]; o++; }
+            if (v[j] != 0.0f) { sh.cidx[o] = lo + j; sh.cval[o] = v[j]; o++; }
     }
     __syncthreads();
     if (tid == 0) {
@@ -825,12 +822,19 @@ uint32_t *sample_scratch(int device) {
 int launch_sample(rsv_ctx *ctx, const float *logits, uint32_t *token, int n, float *temp, uint32_t *counter,
                   const float *sampler, const uint32_t *hist, int hist_stride, int batch) {
     if (n <= 0 || batch <= 0) return RSV_FAIL("sample: bad n=%d batch=%d", n, batch);
-    if (n <= 64 * kSampBS)
-        hipLaunchKernelGGL(k_sample_regs, dim3(batch), dim3(kSampBS), 0, ctx->stream, logits, token, n, temp, counter,
-                           sampler, hist, hist_stride);
-    else
-        hipLaunchKernelGGL(k_sample, dim3(batch), dim3(kSampBS), 0, ctx->stream, logits, token, n, temp, counter, sampler,
-                           hist, hist_stride);
+    // rows of 1024 x 2^j entries (j <= 6: vocabularies 1,024 .. 65,536) in
+    // registers, others on the general kernel
+#define SAMP_REGS(P)                                                                                             \
+    if (n == (P)*kSampBS) {                                                                                        \
+        hipLaunchKernelGGL(k_sample_regs<P>, dim3(batch), dim3(kSampBS), 0, ctx->stream, logits, token, n, temp, \
+                           counter, sampler, hist, hist_stride);                                                  \
+        RSV_HIP(hipGetLastError());                                                                                \
+        return 0;                                                                                                  \
+    }
+    SAMP_REGS(64) SAMP_REGS(32) SAMP_REGS(16) SAMP_REGS(8) SAMP_REGS(4) SAMP_REGS(2) SAMP_REGS(1)
+#undef SAMP_REGS
+    hipLaunchKernelGGL(k_sample, dim3(batch), dim3(kSampBS), 0, ctx->stream, logits, token, n, temp, counter, sampler,
+                       hist, hist_stride);
     RSV_HIP(hipGetLastError());
     return 0;
 }
