@@ -297,6 +297,18 @@ int rsv_wkv7_seq_ragged(rsv_ctx *ctx, uint32_t s, uint32_t r, uint32_t w, uint32
                         uint32_t ln_x_b, uint32_t y_norm, uint32_t seg_start, uint32_t seg_len,
                         uint32_t seg_slot, uint64_t nseg, uint64_t h, uint64_t n, float gn_eps);
 
+/* The same scan leaving the att.output operand yg = (GroupNorm(y) + bonus*v)
+ * * g as F16 [rows, C] (no reference counterpart as one call: the scan,
+ * GroupNorm and the gate multiply of gpu_model.rs's prefill layer,
+ * 2280-2320).  Rows [0, t_rows) of the packed buffers are in use.  y_work
+ * (F32 [t_rows, C]) and bonus_work (F32 [t_rows, h]) are scratch owned by the
+ * caller; their contents on return are unspecified. */
+int rsv_wkv7_seq_ragged_gate(rsv_ctx *ctx, uint32_t s, uint32_t r, uint32_t w, uint32_t k, uint32_t v,
+                             uint32_t a, uint32_t k_k, uint32_t k_a, uint32_t r_k, uint32_t ln_x_w,
+                             uint32_t ln_x_b, uint32_t g, uint32_t y_work, uint32_t bonus_work, uint32_t yg,
+                             uint32_t seg_start, uint32_t seg_len, uint32_t seg_slot, uint64_t nseg, uint64_t t_rows,
+                             uint64_t h, uint64_t n, float gn_eps);
+
 /* ---- prefill building blocks.  These have no one-to-one trait method: they
  * are the pieces the packed (ragged) prefill is built from, replacing the
  * seq_shift, to_f16, gemm_* and elementwise_* chains of gpu_model.rs:2911-3255 with

@@ -1252,6 +1252,40 @@ int rsv_wkv7_seq_ragged(rsv_ctx *ctx, uint32_t s, uint32_t r, uint32_t w, uint32
 
 }  // extern "C"
 
+extern "C" int rsv_wkv7_seq_ragged_gate(rsv_ctx *ctx, uint32_t s, uint32_t r, uint32_t w, uint32_t k, uint32_t v,
+                                        uint32_t a, uint32_t k_k, uint32_t k_a, uint32_t r_k, uint32_t ln_x_w,
+                                        uint32_t ln_x_b, uint32_t g, uint32_t y_work, uint32_t bonus_work, uint32_t yg,
+                                        uint32_t seg_start, uint32_t seg_len, uint32_t seg_slot, uint64_t nseg,
+                                        uint64_t t_rows, uint64_t h, uint64_t n, float gn_eps) {
+    CHECK_CTX();
+    const uint64_t c = h * n;
+    Tensor *ts = get_tensor(ctx, s);
+    if (!ts || c == 0) return RSV_FAIL("wkv7_seq_ragged_gate: unknown tensor");
+    const uint64_t rows = t_rows, slots = ts->len / (h * n * n);
+    OPND(ps, s, RSV_F32, slots * h * n * n, "wkv7_seq s");
+    OPND(pr, r, RSV_F32, rows * c, "wkv7_seq r");
+    OPND(pw, w, RSV_F32, rows * c, "wkv7_seq w");
+    OPND(pk, k, RSV_F32, rows * c, "wkv7_seq k");
+    OPND(pv, v, RSV_F32, rows * c, "wkv7_seq v");
+    OPND(pa, a, RSV_F32, rows * c, "wkv7_seq a");
+    OPND(pkk, k_k, RSV_F32, c, "wkv7_seq k_k");
+    OPND(pka, k_a, RSV_F32, c, "wkv7_seq k_a");
+    OPND(prk, r_k, RSV_F32, c, "wkv7_seq r_k");
+    OPND(pgw, ln_x_w, RSV_F32, c, "wkv7_seq ln_x_w");
+    OPND(pgb, ln_x_b, RSV_F32, c, "wkv7_seq ln_x_b");
+    OPND(pg, g, RSV_F32, rows * c, "wkv7_seq g");
+    OPND(pyw, y_work, RSV_F32, rows * c, "wkv7_seq y_work");
+    OPND(pbw, bonus_work, RSV_F32, rows * h, "wkv7_seq bonus_work");
+    OPND(pyg, yg, RSV_F16, rows * c, "wkv7_seq yg");
+    OPND(pst, seg_start, RSV_U32, nseg, "wkv7_seq seg_start");
+    OPND(pln, seg_len, RSV_U32, nseg, "wkv7_seq seg_len");
+    OPND(psl, seg_slot, RSV_U32, nseg, "wkv7_seq seg_slot");
+    return launch_wkv7_seq_ragged_gate(ctx, F32P(ps), F32P(pr), F32P(pw), F32P(pk), F32P(pv), F32P(pa), F32P(pkk),
+                                       F32P(pka), F32P(prk), F32P(pgw), F32P(pgb), F32P(pg), F32P(pyw), F32P(pbw),
+                                       (_Float16 *)pyg_v, U32P(pst), U32P(pln), U32P(psl), (int)nseg, (int)h, (int)n,
+                                       gn_eps, rows, slots);
+}
+
 // ------------------------------------------------ prefill building blocks
 extern "C" {
 

@@ -284,6 +284,7 @@ struct SeqBufs {
     uint32_t vmid = NONE, wmid = NONE, amid = NONE, gmid = NONE;
     uint32_t row_prev = NONE, seg_start = NONE, seg_len = NONE, seg_slot = NONE, seg_last = NONE, seg_iota = NONE;
     uint32_t xlast = NONE, xnorm = NONE, logits = NONE;
+    uint32_t bonus = NONE;  // [T, H] scratch of the gated scan
 };
 
 }  // namespace
@@ -1018,7 +1019,7 @@ int get_seq(rsv_bundle *b, uint64_t T, uint64_t nseg) {
         struct { uint32_t *id; uint64_t n; int dt; } more[] = {
             {&q.r2, T * I.ffn, RSV_F16}, {&q.vmid, T * I.v_mid, RSV_F16}, {&q.wmid, T * I.w_mid, RSV_F16},
             {&q.amid, T * I.a_mid, RSV_F16}, {&q.gmid, T * I.g_mid, RSV_F16}, {&q.tok, T, RSV_U32},
-            {&q.row_prev, T, RSV_U32}};
+            {&q.row_prev, T, RSV_U32}, {&q.bonus, T * I.n_head, RSV_F32}};
         for (auto &m : more) { if (*m.id != NONE) rsv_tensor_free(b->ctx, *m.id); HK(new_tensor(b, m.n, m.dt, *m.id)); }
         q.cap = T;
     }
@@ -1177,9 +1178,9 @@ int prefill(rsv_bundle *b, GpuState &s, const std::vector<Seg> &segs, float *log
                 j2[2].aux = q.vf;
                 CK(rsv_gemm_multi(c, j2, 4, T));
             }
-            CK(rsv_wkv7_seq_ragged(c, s.rnn[i], q.r, q.w, q.k, q.v, q.a, L.k_k, L.k_a, L.r_k, L.lnx_w, L.lnx_b, q.yn,
-                                   q.seg_start, q.seg_len, q.seg_slot, S, H, N, GN_EPS));
-            CK(rsv_mul_to_f16(c, q.yn, q.g, q.yg, T * C));
+            CK(rsv_wkv7_seq_ragged_gate(c, s.rnn[i], q.r, q.w, q.k, q.v, q.a, L.k_k, L.k_a, L.r_k, L.lnx_w, L.lnx_b,
+                                        q.g, q.yn, q.bonus, q.yg, q.seg_start, q.seg_len, q.seg_slot, S, T, H, N,
+                                        GN_EPS));
             if (small) {
                 rsv_mm_job j4 = mm_job(L.ow, q.yg, q.x, 2);
                 CK(rsv_gemm_skinny(c, &j4, 1, T));

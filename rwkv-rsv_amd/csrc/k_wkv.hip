@@ -764,6 +764,143 @@ int launch_wkv7_seq_ragged(rsv_ctx *ctx, float *s, const float *r, const float *
     return 0;
 }
 
+// ------------------------------------- ragged prefill scan, gated fp16 out
+// Two forms of the same step, both leaving the att.output operand
+// yg = (GroupNorm(y) + bonus*v) * g in fp16:
+//   - k_wkv7_seq_ragged (one wave per head and segment, one lane per state
+//     row, GroupNorm inside) then k_gate_f16 (yn * g);
+//   - k_wkv7_seq_rows4 (four waves per head and segment, four lanes per
+//     state row, 16 columns each) writing the raw y = S r and the head's bonus
+//     sum per token, then k_gn_gate_f16 (GroupNorm + bonus*v, times g).
+// The second has a quarter of the dependent arithmetic per token and lane
+// (each wave forms the head's column vectors itself, in its own LDS copy,
+// so no barrier spans waves), so it runs a long segment about twice as fast;
+// on chunks of many short segments the first keeps more work per wave.
+__global__ __launch_bounds__(256) void k_wkv7_seq_rows4(
+    float *__restrict__ S, const float *__restrict__ r, const float *__restrict__ w, const float *__restrict__ k,
+    const float *__restrict__ v, const float *__restrict__ a, const float *__restrict__ kkc,
+    const float *__restrict__ ka, const float *__restrict__ rk, float *__restrict__ y_out,
+    float *__restrict__ bonus_out, const uint32_t *__restrict__ seg_start, const uint32_t *__restrict__ seg_len,
+    const uint32_t *__restrict__ seg_slot, int H, float eps, uint64_t rows, uint64_t slots) {
+    __shared__ __attribute__((aligned(16))) float hvs[4][2][5 * 64];
+    const int h = blockIdx.x, gi = blockIdx.y, tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63, row = 16 * wave + (lane >> 2), q = lane & 3;
+    const size_t C = (size_t)H * 64;
+    const uint32_t t0 = seg_start[gi], len = seg_len[gi], slot = seg_slot[gi];
+    if (slot >= slots || (uint64_t)t0 + len > rows) return;  // uniform per block
+    float4 *Srow = (float4 *)(S + ((size_t)slot * H + h) * 4096 + (size_t)row * 64) + 4 * q;
+    float s[16];
+#pragma unroll
+    for (int m = 0; m < 4; m++) {
+        const float4 x = Srow[m];
+        s[4 * m] = x.x; s[4 * m + 1] = x.y; s[4 * m + 2] = x.z; s[4 * m + 3] = x.w;
+    }
+    // column role: lane j forms column j's vectors (every wave, for itself)
+    const int j = lane;
+    const float kkc_j = kkc[h * 64 + j], ka_j = ka[h * 64 + j], rk_j = rk[h * 64 + j];
+    size_t vo = (size_t)t0 * C + (size_t)h * 64;
+    float nk = 0.f, na = 0.f, nw = 0.f, nr = 0.f, nv = 0.f;
+    if (len > 0) { nk = k[vo + j]; na = a[vo + j]; nw = w[vo + j]; nr = r[vo + j]; nv = v[vo + row]; }
+    for (uint32_t t = 0; t < len; t++) {
+        const float kc = nk, ac = na, wc = nw, rc = nr, vc = nv;
+        const size_t cur = vo;
+        if (t + 1 < len) {  // the next token's vectors, in flight during this one
+            vo += C;
+            nk = k[vo + j]; na = a[vo + j]; nw = w[vo + j]; nr = r[vo + j]; nv = v[vo + row];
+        }
+        const float kk = kc * kkc_j;
+        float nrm = sqrtf(wave_sum(kk * kk));
+        nrm = nrm < eps ? eps : nrm;
+        const float kh = kk * (1.0f / nrm);
+        const float kmod = kc + ka_j * (kc * ac - kc);
+        const float bonus = wave_sum(rc * kmod * rk_j);
+        // the wave's copy for this token (two copies alternate, so the next
+        // token's writes never meet this token's reads)
+        float *hv = hvs[wave][t & 1];
+        hv[j] = kh; hv[64 + j] = kh * (-ac); hv[128 + j] = wc; hv[192 + j] = kmod; hv[256 + j] = rc;
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the wave's LDS writes done
+        __builtin_amdgcn_wave_barrier();
+        float kv[16], bv[16], wv[16], mv[16], rv[16];
+#pragma unroll
+        for (int m = 0; m < 4; m++) {
+            const float4 a0 = *(const float4 *)(hv + 16 * q + 4 * m), a1 = *(const float4 *)(hv + 64 + 16 * q + 4 * m),
+                         a2 = *(const float4 *)(hv + 128 + 16 * q + 4 * m), a3 = *(const float4 *)(hv + 192 + 16 * q + 4 * m),
+                         a4 = *(const float4 *)(hv + 256 + 16 * q + 4 * m);
+            kv[4 * m] = a0.x; kv[4 * m + 1] = a0.y; kv[4 * m + 2] = a0.z; kv[4 * m + 3] = a0.w;
+            bv[4 * m] = a1.x; bv[4 * m + 1] = a1.y; bv[4 * m + 2] = a1.z; bv[4 * m + 3] = a1.w;
+            wv[4 * m] = a2.x; wv[4 * m + 1] = a2.y; wv[4 * m + 2] = a2.z; wv[4 * m + 3] = a2.w;
+            mv[4 * m] = a3.x; mv[4 * m + 1] = a3.y; mv[4 * m + 2] = a3.z; mv[4 * m + 3] = a3.w;
+            rv[4 * m] = a4.x; rv[4 * m + 1] = a4.y; rv[4 * m + 2] = a4.z; rv[4 * m + 3] = a4.w;
+        }
+        float sa = 0.f;
+#pragma unroll
+        for (int e = 0; e < 16; e++) sa = fmaf(s[e], kv[e], sa);
+        sa = quad_sum(sa);
+        float y = 0.f;
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+            const float ns = s[e] * wv[e] + sa * bv[e] + vc * mv[e];
+            s[e] = ns;
+            y = fmaf(ns, rv[e], y);
+        }
+        y = quad_sum(y);
+        if (q == 0) y_out[cur + row] = y;
+        if (tid == 0) bonus_out[(size_t)(t0 + t) * H + h] = bonus;
+    }
+#pragma unroll
+    for (int m = 0; m < 4; m++) Srow[m] = make_float4(s[4 * m], s[4 * m + 1], s[4 * m + 2], s[4 * m + 3]);
+}
+
+// yg = ((GroupNorm(y) * gamma + beta) + bonus * v) * g in fp16: one wave per
+// (token, head), four per block; the order of k_wkv7_seq_ragged's head_norm.
+__global__ __launch_bounds__(256) void k_gn_gate_f16(const float *__restrict__ y, const float *__restrict__ bonus,
+                                                    const float *__restrict__ v, const float *__restrict__ gamma,
+                                                    const float *__restrict__ beta, const float *__restrict__ g,
+                                                    _Float16 *__restrict__ yg, uint64_t units, int H, float gn_eps) {
+    const uint64_t u = (uint64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (u >= units) return;  // uniform per wave
+    const int i = threadIdx.x & 63, h = (int)(u % H);
+    const size_t o = (size_t)u * 64 + i;  // (token, head) units are consecutive 64-column groups
+    const float yy = y[o];
+    const float mean = wave_sum(yy) * (1.0f / 64.0f);
+    const float d = yy - mean;
+    const float var = wave_sum(d * d) * (1.0f / 64.0f) + gn_eps;
+    const float yn = d * (1.0f / sqrtf(var)) * gamma[h * 64 + i] + beta[h * 64 + i] + bonus[u] * v[o];
+    yg[o] = (_Float16)(yn * g[o]);
+}
+
+// yg = yn * g in fp16 (the one-wave form's gate)
+__global__ void k_gate_f16(const float *__restrict__ yn, const float *__restrict__ g, _Float16 *__restrict__ yg, uint64_t n) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x)
+        yg[i] = (_Float16)(yn[i] * g[i]);
+}
+
+int launch_wkv7_seq_ragged_gate(rsv_ctx *ctx, float *s, const float *r, const float *w, const float *k,
+                                const float *v, const float *a, const float *kk, const float *ka, const float *rk,
+                                const float *gamma, const float *beta, const float *g, float *y_work,
+                                float *bonus_work, _Float16 *yg, const uint32_t *seg_start, const uint32_t *seg_len,
+                                const uint32_t *seg_slot, int nseg, int h, int n, float gn_eps, uint64_t rows,
+                                uint64_t slots) {
+    if (n != 64) return RSV_FAIL("wkv7_seq: head_size must be 64 (got %d)", n);
+    if (nseg <= 0 || rows == 0) return 0;
+    const uint64_t cn = rows * (uint64_t)h * 64;
+    if (nseg <= 40) {  // few (long) segments: the four-lanes-per-row form
+        hipLaunchKernelGGL(k_wkv7_seq_rows4, dim3(h, nseg), dim3(256), 0, ctx->stream, s, r, w, k, v, a, kk, ka, rk,
+                           y_work, bonus_work, seg_start, seg_len, seg_slot, h, 1e-12f, rows, slots);
+        const uint64_t units = rows * (uint64_t)h;
+        hipLaunchKernelGGL(k_gn_gate_f16, dim3((unsigned)((units + 3) / 4)), dim3(256), 0, ctx->stream, y_work,
+                           bonus_work, v, gamma, beta, g, yg, units, h, gn_eps);
+    } else {
+        hipLaunchKernelGGL(k_wkv7_seq_ragged, dim3(h, nseg), dim3(64), 0, ctx->stream, s, r, w, k, v, a, kk, ka, rk,
+                           gamma, beta, y_work, seg_start, seg_len, seg_slot, h, 1e-12f, gn_eps, rows, slots);
+        uint64_t blocks = (cn + 255) / 256;
+        if (blocks > 65535 * 16) blocks = 65535 * 16;
+        hipLaunchKernelGGL(k_gate_f16, dim3((unsigned)blocks), dim3(256), 0, ctx->stream, y_work, g, yg, cn);
+    }
+    RSV_HIP(hipGetLastError());
+    return 0;
+}
+
 // ------------------------------------------- dplr_seq (backend.rs:806, 852)
 // Vectors are precomputed per token: k = k_mod, a = k_hat, b = -k_hat*a.
 // y[t] = S_t r_t.  lens (optional) truncates each slot's token count; the

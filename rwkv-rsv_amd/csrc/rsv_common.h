@@ -192,6 +192,12 @@ int launch_dplr_seq(rsv_ctx *ctx, float *s, const float *r, const float *w, cons
                     int h, int n, int t, int c, int batch);
 int launch_segmean(rsv_ctx *ctx, const float *x, float *out, const uint32_t *lens, int c, int t_pad,
                    int batch);
+int launch_wkv7_seq_ragged_gate(rsv_ctx *ctx, float *s, const float *r, const float *w, const float *k,
+                                const float *v, const float *a, const float *kk, const float *ka, const float *rk,
+                                const float *gamma, const float *beta, const float *g, float *y_work,
+                                float *bonus_work, _Float16 *yg, const uint32_t *seg_start, const uint32_t *seg_len,
+                                const uint32_t *seg_slot, int nseg, int h, int n, float gn_eps, uint64_t rows,
+                                uint64_t slots);
 int launch_wkv7_seq_ragged(rsv_ctx *ctx, float *s, const float *r, const float *w, const float *k,
                            const float *v, const float *a, const float *kk, const float *ka,
                            const float *rk, const float *gamma, const float *beta, float *yn,

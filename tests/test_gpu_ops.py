@@ -314,6 +314,38 @@ def test_wkv7_seq_ragged_matches_decode_loop(be):
         pos += lens[g]
 
 
+@pytest.mark.parametrize("lens", [[300, 212], [8] * 48 + [40]])
+def test_wkv7_seq_ragged_gate_matches_scan_times_gate(be, lens):
+    """rsv_wkv7_seq_ragged_gate leaves (GroupNorm(y) + bonus*v) * g in fp16:
+    with few segments it runs the four-lanes-per-row scan and a separate
+    GroupNorm pass, with many the one-wave scan; both against
+    rsv_wkv7_seq_ragged's yn times g (and its state) to rounding."""
+    rsv = _rsv()
+    H = 40
+    C = H * 64
+    rng = np.random.default_rng(len(lens))
+    T = sum(lens)
+    r, v, k, w, a, _, kk, ka, rk, gam, bet = _wkv_inputs(rng, T, H)
+    g = (1 / (1 + np.exp(-rng.standard_normal((T, C))))).astype(np.float32)
+    n = len(lens)
+    S = (rng.standard_normal((n, H, 64, 64)) * 0.1).astype(np.float32)
+    starts = np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.uint32)
+    st = be.tensor(starts, dtype=rsv.U32)
+    ln = be.tensor(np.array(lens, np.uint32), dtype=rsv.U32)
+    sl = be.tensor(np.arange(n, dtype=np.uint32)[::-1].copy(), dtype=rsv.U32)
+    common = [be.tensor(x) for x in (r, w, k, v, a, kk, ka, rk, gam, bet)]
+    S1, S2 = be.tensor(S), be.tensor(S)
+    yn = be.tensor(n=T * C)
+    be.call("rsv_wkv7_seq_ragged", S1, *common, yn, st, ln, sl, n, H, 64, 64e-5)
+    want = (be.get(yn, T * C) * g.reshape(-1)).astype(np.float16).astype(np.float32)
+    gt, yw, bw = be.tensor(g), be.tensor(n=T * C), be.tensor(n=T * H)
+    yg = be.tensor(n=T * C, dtype=rsv.F16)
+    be.call("rsv_wkv7_seq_ragged_gate", S2, *common, gt, yw, bw, yg, st, ln, sl, n, T, H, 64, 64e-5)
+    got = be.get(yg, T * C)
+    assert rel_err(got, want) < 2e-3
+    assert rel_err(be.get(S2, S.size), be.get(S1, S.size)) < 1e-5
+
+
 # ------------------------------------------------------------- argmax / tokens
 def test_argmax_reference_cases(be):
     rsv = _rsv()
