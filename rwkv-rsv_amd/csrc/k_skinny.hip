@@ -795,6 +795,25 @@ __device__ __forceinline__ void sk8_epilogue(const SkEpi &E, const float (&v)[TB
     }
 }
 
+// Loads this wave issued after its copy of step s, up to the wait of step s,
+// in k_skinny8's two-row-tile form: copies of steps 0..NSX-2 then the weights
+// of steps 0..DW-1 at entry; in iteration t the copy of step t+NSX-1 and the
+// weights of step t+DW.  nx / lw: loads per copy / per weight step.
+template <int FIX, int NSX, int DW>
+__device__ constexpr int sk8p_younger(int s, int nx, int lw) {
+    // position of copy s: entry (s < NSX-1) or iteration s-NSX+1
+    int n = 0;
+    if (s < NSX - 1) {
+        n += (NSX - 2 - s) * nx + DW * lw;  // later entry copies and the entry weights
+        for (int t = 0; t < s; t++) n += (t + NSX - 1 < FIX ? nx : 0) + (t + DW < FIX ? lw : 0);
+    } else {
+        const int t0 = s - NSX + 1;  // iteration that issued copy s
+        n += t0 + DW < FIX ? lw : 0;  // its weights
+        for (int t = t0 + 1; t < s; t++) n += (t + NSX - 1 < FIX ? nx : 0) + (t + DW < FIX ? lw : 0);
+    }
+    return n;
+}
+
 // ------------------------------------------------------------------ v8
 // Batched decode GEMM, one row tile (32 weight rows) per block over the
 // whole k, the k range split over the block's 4 waves (each wave its own
@@ -814,8 +833,14 @@ __device__ __forceinline__ void sk8_epilogue(const SkEpi &E, const float (&v)[TB
 //   - v_mfma_f32_32x32x16_f16 with the lane mapping of k_skinny5.
 // The common k (2560 columns: 10 steps per wave) runs fully unrolled with
 // exact wait counts; other k (a multiple of 64) take a two-deep loop.
-template <int MT, bool I8, int FIX>
-__device__ __forceinline__ void skinny8_body(const SkinnyJob &J, int rt, int MB, unsigned char *xb0, unsigned char *xb1) {
+// With more row tiles than CUs (ffn.key: 320) a block of 8 waves takes two
+// row tiles (RT = 2): the two waves of a k quarter each copy half of the
+// step's x into shared buffers (four per quarter, three steps ahead), one
+// barrier per step, so every x byte read from L2 feeds 64 weight rows.
+// Blocks then number fewer than CUs and each CU reads 491 KiB instead of up
+// to 2 x 409 KiB (ffn.key at B=64: 18.0 -> 15.8 us).
+template <int MT, bool I8, int FIX, int RT>
+__device__ __forceinline__ void skinny8_body(const SkinnyJob &J, int rt0, int MB, unsigned char *xb0, unsigned char *xb1) {
     constexpr int TB = MT * 32;
     constexpr int XB = TB * 128;     // bytes of one x buffer
     constexpr int NX = TB / 8;       // 1 KiB copies per step
@@ -823,31 +848,45 @@ __device__ __forceinline__ void skinny8_body(const SkinnyJob &J, int rt, int MB,
     constexpr int tbytes = I8 ? 1024 : 2048;
     constexpr int DW = FIX > 0 ? 4 : 2;  // weight steps in flight
     constexpr int LW = 2 * WV + (I8 ? 1 : 0);  // weight loads per step
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 5;
+    const int tid = threadIdx.x, lane = tid & 63, g = lane >> 5;
+    // wave -> k quarter (wave % 4) and row tile (wave / 4) of the block
+    const int wave = (tid >> 6) & 3, h = tid >> 8;
+    const int rt = rt0 + h;
+    const bool tile_ok = RT == 1 || rt * 32 < J.N;  // wave-uniform; a masked wave still copies its x share
+    const int rt_ld = tile_ok ? rt : rt0;
     const int nchunks = J.K / 32;
     // chunk pairs per wave (k is a multiple of 64)
     const int q4 = ((nchunks + 3) / 4 + 1) & ~1;
     const int cw0 = min(nchunks, wave * q4), cw1 = min(nchunks, cw0 + q4);
     const int nw = (cw1 - cw0) / 2;  // steps of this wave
-    unsigned char *xbw[2] = {xb0 + wave * XB, xb1 + wave * XB};
-    const uint8_t *wt = (const uint8_t *)J.w + (size_t)rt * nchunks * tbytes + lane * (I8 ? 16 : 32);
-    const uint32_t *szrow = I8 ? J.sz + (size_t)rt * (J.K / 128) * 32 + (lane & 31) : nullptr;
-    // copy source of lane l in instruction i, relative to the step's column
-    const _Float16 *xsrc[NX];
+    // x buffers of this wave's quarter: RT = 1 two (xb0, xb1), RT = 2 NSX in xb0
+    constexpr int NSX = RT == 2 ? 4 : 2;
+    unsigned char *xbw[NSX];
 #pragma unroll
-    for (int i = 0; i < NX; i++) {
+    for (int i = 0; i < NSX; i++) xbw[i] = RT == 2 ? xb0 + (i * 4 + wave) * XB : (i ? xb1 : xb0) + wave * XB;
+    const uint8_t *wt = (const uint8_t *)J.w + (size_t)rt_ld * nchunks * tbytes + lane * (I8 ? 16 : 32);
+    const uint32_t *szrow = I8 ? J.sz + (size_t)rt_ld * (J.K / 128) * 32 + (lane & 31) : nullptr;
+    // copy source of lane l in instruction i, relative to the step's column
+    // (with two row tiles, this wave's share: instructions h*NX/2 ..)
+    constexpr int NXW = NX / RT;
+    const _Float16 *xsrc[NXW];
+#pragma unroll
+    for (int j = 0; j < NXW; j++) {
+        const int i = h * NXW + j;
         const int b = 8 * i + (lane >> 3);
         const int piece = (lane & 7) ^ (b & 7);
-        xsrc[i] = J.x + (size_t)min(b, MB - 1) * J.ldx + piece * 8;
+        xsrc[j] = J.x + (size_t)min(b, MB - 1) * J.ldx + piece * 8;
     }
     sk_u32x4 wr[DW][2][WV];
     uint32_t sr[DW];
     auto issue_x = [&](int slot, int s) {
         const int c = cw0 + 2 * min(s, nw - 1);  // clamped: steps past the end re-read (masked)
         unsigned char *dst = xbw[slot];
+        // with two row tiles the quarter's two waves copy half the sessions each
 #pragma unroll
-        for (int i = 0; i < NX; i++)
-            __builtin_amdgcn_global_load_lds(xsrc[i] + c * 32, (__attribute__((address_space(3))) void *)(dst + i * 1024), 16, 0, 0);
+        for (int j = 0; j < NXW; j++)
+            __builtin_amdgcn_global_load_lds(xsrc[j] + c * 32, (__attribute__((address_space(3))) void *)(dst + (h * NXW + j) * 1024),
+                                             16, 0, 0);
     };
     auto issue_w = [&](int wslot, int s) {
         const int c = cw0 + 2 * min(s, nw - 1);
@@ -920,7 +959,32 @@ __device__ __forceinline__ void skinny8_body(const SkinnyJob &J, int rt, int MB,
             }
         }
     };
-    if (FIX > 0 && nw == FIX) {
+    if constexpr (RT == 2) {
+        // the launcher runs this form with FIX steps only.  x copies go NSX-1
+        // steps ahead through NSX buffers per quarter.  Per step: wait for
+        // this wave's share of the step's copy, a barrier (every share landed
+        // and every wave done with the buffer the next copy refills), the
+        // copy NSX-1 steps ahead, the products, the weights DW steps ahead
+        // (scheduling barriers keep the issue order the wait counts assume)
+#pragma unroll
+        for (int d = 0; d < NSX - 1; d++) {
+            issue_x(d, d);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int d = 0; d < DW; d++) issue_w(d, d);
+#pragma unroll
+        for (int s = 0; s < FIX; s++) {
+            __builtin_amdgcn_sched_barrier(0);
+            sk_wait_vm(sk8p_younger<FIX, NSX, DW>(s, NXW, LW));
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_sched_barrier(0);
+            if (s + NSX - 1 < FIX) issue_x((s + NSX - 1) % NSX, s + NSX - 1);
+            compute(s % NSX, s % DW, s, false);  // a masked wave multiplies its stand-in tile, unstored
+            __builtin_amdgcn_sched_barrier(0);
+            if (s + DW < FIX) issue_w(s % DW, s + DW);
+        }
+    } else if (FIX > 0 && nw == FIX) {
         issue_x(0, 0);
 #pragma unroll
         for (int d = 0; d < DW; d++) issue_w(d, d);
@@ -961,19 +1025,20 @@ __device__ __forceinline__ void skinny8_body(const SkinnyJob &J, int rt, int MB,
     }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();  // x buffers dead: the LDS holds the wave tiles now
-    float (*part)[32][TB + 1] = reinterpret_cast<float (*)[32][TB + 1]>(xb1);
+    float (*part)[32][TB + 1] = reinterpret_cast<float (*)[32][TB + 1]>(RT == 2 ? xb0 : xb1) + 4 * h;
 #pragma unroll
     for (int ct = 0; ct < MT; ct++)
 #pragma unroll
         for (int e = 0; e < 16; e++) part[wave][8 * (e >> 2) + 4 * g + (e & 3)][ct * 32 + (lane & 31)] = acc[ct][e];
     __syncthreads();
-    const int r = tid & 31, b0 = tid >> 5;
+    const int r = tid & 31, b0 = (tid >> 5) & 7;
     float v[TB / 8];
 #pragma unroll
     for (int q = 0; q < TB / 8; q++) {
         const int b = b0 + 8 * q;
         v[q] = ((part[0][r][b] + part[1][r][b]) + part[2][r][b]) + part[3][r][b];
     }
+    if (!tile_ok) return;
     const int n = rt * 32 + r;
     if (n >= J.N) return;
     const SkEpi E = sk_epi_of(J);
@@ -982,20 +1047,24 @@ __device__ __forceinline__ void skinny8_body(const SkinnyJob &J, int rt, int MB,
 #undef SK8_CALL
 }
 
-template <int MT>
-__global__ __launch_bounds__(256) void k_skinny8(SkinnyJobs jobs, int MB) {
-    // 4 waves x TB sessions x 128 bytes per buffer; the second also holds
-    // the 4 x 32 x (TB+1) wave tiles at the end
-    constexpr int XBYTES = 4 * MT * 32 * 128 > 4 * 32 * (MT * 32 + 1) * 4 ? 4 * MT * 32 * 128 : 4 * 32 * (MT * 32 + 1) * 4;
-    __shared__ __attribute__((aligned(16))) unsigned char xb0[4 * MT * 32 * 128];
-    __shared__ __attribute__((aligned(16))) unsigned char xb1[XBYTES];
+// RT row tiles per block (4 waves each); with RT = 2 the two tiles share
+// every x copy, halving the x bytes read from L2 per weight byte.
+template <int MT, int RT>
+__global__ __launch_bounds__(256 * RT) void k_skinny8(SkinnyJobs jobs, int MB) {
+    // 4 quarters x TB sessions x 128 bytes per buffer; the second also holds
+    // the RT x 4 x 32 x (TB+1) wave tiles at the end
+    // (RT = 2: xb0 holds the 4 buffers of each quarter, then the wave tiles)
+    constexpr int XBYTES = 4 * MT * 32 * 128 > RT * 4 * 32 * (MT * 32 + 1) * 4 ? 4 * MT * 32 * 128 : RT * 4 * 32 * (MT * 32 + 1) * 4;
+    __shared__ __attribute__((aligned(16))) unsigned char xb0[(RT == 2 ? 4 : 1) * 4 * MT * 32 * 128];
+    __shared__ __attribute__((aligned(16))) unsigned char xb1[RT == 2 ? 16 : XBYTES];
     const int bid = blockIdx.x;
     int ji = 0;
     while (ji + 1 < jobs.n && bid >= jobs.blk_start[ji + 1]) ji++;
+    const int rt0 = (bid - jobs.blk_start[ji]) * RT;
     if (jobs.j[ji].fmt == FMT_I8)
-        skinny8_body<MT, true, 10>(jobs.j[ji], bid - jobs.blk_start[ji], MB, xb0, xb1);
+        skinny8_body<MT, true, 10, RT>(jobs.j[ji], rt0, MB, xb0, xb1);
     else
-        skinny8_body<MT, false, 10>(jobs.j[ji], bid - jobs.blk_start[ji], MB, xb0, xb1);
+        skinny8_body<MT, false, 10, RT>(jobs.j[ji], rt0, MB, xb0, xb1);
 }
 
 // Tiled copy of a weight matrix [n, k] (int8 bytes or fp16) for k_skinny4;
@@ -1089,8 +1158,27 @@ static int launch_v8(rsv_ctx *ctx, SkinnyJobs &jobs, int MB) {
         total += J.nblk;
     }
     jobs.blk_start[jobs.n] = total;
-    if (MB <= 32) hipLaunchKernelGGL((k_skinny8<1>), dim3(total), dim3(256), 0, ctx->stream, jobs, MB);
-    else hipLaunchKernelGGL((k_skinny8<2>), dim3(total), dim3(256), 0, ctx->stream, jobs, MB);
+    // more row tiles than CUs and every k = 2560: two tiles per block (every
+    // CU one block, each x copy serving 64 rows)
+    const int cus = ctx->sm_count > 0 ? ctx->sm_count : 256;
+    bool pair = total > cus;
+    for (int i = 0; i < jobs.n; i++) pair &= jobs.j[i].K == 32 * 80;
+    if (pair) {
+        total = 0;
+        for (int i = 0; i < jobs.n; i++) {
+            SkinnyJob &J = jobs.j[i];
+            J.nblk = (J.N + 63) / 64;
+            jobs.blk_start[i] = total;
+            total += J.nblk;
+        }
+        jobs.blk_start[jobs.n] = total;
+        if (MB <= 32) hipLaunchKernelGGL((k_skinny8<1, 2>), dim3(total), dim3(512), 0, ctx->stream, jobs, MB);
+        else hipLaunchKernelGGL((k_skinny8<2, 2>), dim3(total), dim3(512), 0, ctx->stream, jobs, MB);
+    } else if (MB <= 32) {
+        hipLaunchKernelGGL((k_skinny8<1, 1>), dim3(total), dim3(256), 0, ctx->stream, jobs, MB);
+    } else {
+        hipLaunchKernelGGL((k_skinny8<2, 1>), dim3(total), dim3(256), 0, ctx->stream, jobs, MB);
+    }
     RSV_HIP(hipGetLastError());
     return 0;
 }
@@ -1411,3 +1499,4 @@ static int launch_slab(rsv_ctx *ctx, SkinnyJobs &jobs, int MB) {
 }
 
 }  // namespace rsv
+
