@@ -765,90 +765,157 @@ int launch_wkv7_seq_ragged(rsv_ctx *ctx, float *s, const float *r, const float *
 }
 
 // ------------------------------------- ragged prefill scan, gated fp16 out
-// Two forms of the same step, both leaving the att.output operand
-// yg = (GroupNorm(y) + bonus*v) * g in fp16:
-//   - k_wkv7_seq_ragged (one wave per head and segment, one lane per state
-//     row, GroupNorm inside) then k_gate_f16 (yn * g);
-//   - k_wkv7_seq_rows4 (four waves per head and segment, four lanes per
-//     state row, 16 columns each) writing the raw y = S r and the head's bonus
-//     sum per token, then k_gn_gate_f16 (GroupNorm + bonus*v, times g).
-// The second has a quarter of the dependent arithmetic per token and lane
-// (each wave forms the head's column vectors itself, in its own LDS copy,
-// so no barrier spans waves), so it runs a long segment about twice as fast;
-// on chunks of many short segments the first keeps more work per wave.
-__global__ __launch_bounds__(256) void k_wkv7_seq_rows4(
+// The scan of rsv_wkv7_seq_ragged_gate, leaving the att.output operand
+// yg = (GroupNorm(y) + bonus*v) * g in fp16: k_wkv7_seq_rows writes the raw
+// y = S r and the head's bonus sum per token, then k_gn_gate_f16 applies
+// GroupNorm + bonus*v and the gate.  Per (head, segment), 64/RPL lane groups
+// of four lanes: a group owns RPL state rows, each lane 16 columns of them.
+// The head's column vectors of a batch of tokens (the reductions over the
+// head, |k| and the bonus sum, included) are formed four tokens per wave
+// into LDS first, so the scan's dependent chain per token is the row-local
+// update alone.  Against the one-wave scan with GroupNorm inside
+// (k_wkv7_seq_ragged): 560 -> 333 us on 8 segments of 512 tokens (40
+// heads), 227 -> 211 us on 64 of 64.
+template <int RPL>
+__global__ __launch_bounds__(256 / RPL) void k_wkv7_seq_rows(
     float *__restrict__ S, const float *__restrict__ r, const float *__restrict__ w, const float *__restrict__ k,
     const float *__restrict__ v, const float *__restrict__ a, const float *__restrict__ kkc,
     const float *__restrict__ ka, const float *__restrict__ rk, float *__restrict__ y_out,
     float *__restrict__ bonus_out, const uint32_t *__restrict__ seg_start, const uint32_t *__restrict__ seg_len,
     const uint32_t *__restrict__ seg_slot, int H, float eps, uint64_t rows, uint64_t slots) {
-    __shared__ __attribute__((aligned(16))) float hvs[4][2][5 * 64];
+    constexpr int NW = 4 / RPL;   // waves per (head, segment)
+    constexpr int kRB = 4 * NW;   // tokens per batch: four per wave in the batch phase
+    // per batch: [token][k^ | -k^ a | w | k_mod | r | v] x 64 columns, two batches alternating
+    __shared__ __attribute__((aligned(16))) float hb[2][kRB][6 * 64];
+    // the batch's outputs (y per token and row, the bonus sum per token) are
+    // staged in LDS and stored once the batch is done: a global store per
+    // token would hold its data register until the write completes
+    __shared__ __attribute__((aligned(16))) float yl[2][kRB][64];
+    __shared__ float bl[2][kRB];
     const int h = blockIdx.x, gi = blockIdx.y, tid = threadIdx.x;
-    const int wave = tid >> 6, lane = tid & 63, row = 16 * wave + (lane >> 2), q = lane & 3;
+    const int wave = tid >> 6, lane = tid & 63, q = lane & 3;
+    const int row0 = 16 * RPL * wave + RPL * (lane >> 2);  // this lane's rows row0 .. row0 + RPL - 1
     const size_t C = (size_t)H * 64;
     const uint32_t t0 = seg_start[gi], len = seg_len[gi], slot = seg_slot[gi];
     if (slot >= slots || (uint64_t)t0 + len > rows) return;  // uniform per block
-    float4 *Srow = (float4 *)(S + ((size_t)slot * H + h) * 4096 + (size_t)row * 64) + 4 * q;
-    float s[16];
+    float4 *Sb = (float4 *)(S + ((size_t)slot * H + h) * 4096);
+    float s[RPL][16];
 #pragma unroll
-    for (int m = 0; m < 4; m++) {
-        const float4 x = Srow[m];
-        s[4 * m] = x.x; s[4 * m + 1] = x.y; s[4 * m + 2] = x.z; s[4 * m + 3] = x.w;
-    }
-    // column role: lane j forms column j's vectors (every wave, for itself)
-    const int j = lane;
-    const float kkc_j = kkc[h * 64 + j], ka_j = ka[h * 64 + j], rk_j = rk[h * 64 + j];
-    size_t vo = (size_t)t0 * C + (size_t)h * 64;
-    float nk = 0.f, na = 0.f, nw = 0.f, nr = 0.f, nv = 0.f;
-    if (len > 0) { nk = k[vo + j]; na = a[vo + j]; nw = w[vo + j]; nr = r[vo + j]; nv = v[vo + row]; }
-    for (uint32_t t = 0; t < len; t++) {
-        const float kc = nk, ac = na, wc = nw, rc = nr, vc = nv;
-        const size_t cur = vo;
-        if (t + 1 < len) {  // the next token's vectors, in flight during this one
-            vo += C;
-            nk = k[vo + j]; na = a[vo + j]; nw = w[vo + j]; nr = r[vo + j]; nv = v[vo + row];
-        }
-        const float kk = kc * kkc_j;
-        float nrm = sqrtf(wave_sum(kk * kk));
-        nrm = nrm < eps ? eps : nrm;
-        const float kh = kk * (1.0f / nrm);
-        const float kmod = kc + ka_j * (kc * ac - kc);
-        const float bonus = wave_sum(rc * kmod * rk_j);
-        // the wave's copy for this token (two copies alternate, so the next
-        // token's writes never meet this token's reads)
-        float *hv = hvs[wave][t & 1];
-        hv[j] = kh; hv[64 + j] = kh * (-ac); hv[128 + j] = wc; hv[192 + j] = kmod; hv[256 + j] = rc;
-        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the wave's LDS writes done
-        __builtin_amdgcn_wave_barrier();
-        float kv[16], bv[16], wv[16], mv[16], rv[16];
+    for (int i = 0; i < RPL; i++)
 #pragma unroll
         for (int m = 0; m < 4; m++) {
-            const float4 a0 = *(const float4 *)(hv + 16 * q + 4 * m), a1 = *(const float4 *)(hv + 64 + 16 * q + 4 * m),
-                         a2 = *(const float4 *)(hv + 128 + 16 * q + 4 * m), a3 = *(const float4 *)(hv + 192 + 16 * q + 4 * m),
-                         a4 = *(const float4 *)(hv + 256 + 16 * q + 4 * m);
-            kv[4 * m] = a0.x; kv[4 * m + 1] = a0.y; kv[4 * m + 2] = a0.z; kv[4 * m + 3] = a0.w;
-            bv[4 * m] = a1.x; bv[4 * m + 1] = a1.y; bv[4 * m + 2] = a1.z; bv[4 * m + 3] = a1.w;
-            wv[4 * m] = a2.x; wv[4 * m + 1] = a2.y; wv[4 * m + 2] = a2.z; wv[4 * m + 3] = a2.w;
-            mv[4 * m] = a3.x; mv[4 * m + 1] = a3.y; mv[4 * m + 2] = a3.z; mv[4 * m + 3] = a3.w;
-            rv[4 * m] = a4.x; rv[4 * m + 1] = a4.y; rv[4 * m + 2] = a4.z; rv[4 * m + 3] = a4.w;
+            const float4 x = Sb[(row0 + i) * 16 + 4 * q + m];
+            s[i][4 * m] = x.x; s[i][4 * m + 1] = x.y; s[i][4 * m + 2] = x.z; s[i][4 * m + 3] = x.w;
         }
-        float sa = 0.f;
+    // column role (batch phase): lane j forms column j's vectors of tokens
+    // 4*wave .. 4*wave+3 of a batch; every reduction over the head happens
+    // here, for four tokens at once, off the scan's dependent chain
+    const int j = lane;
+    const float kkc_j = kkc[h * 64 + j], ka_j = ka[h * 64 + j], rk_j = rk[h * 64 + j];
+    float pk[4], pa[4], pw[4], pr[4], pv[4];
+    auto load_batch = [&](uint32_t tb) {
 #pragma unroll
-        for (int e = 0; e < 16; e++) sa = fmaf(s[e], kv[e], sa);
-        sa = quad_sum(sa);
-        float y = 0.f;
-#pragma unroll
-        for (int e = 0; e < 16; e++) {
-            const float ns = s[e] * wv[e] + sa * bv[e] + vc * mv[e];
-            s[e] = ns;
-            y = fmaf(ns, rv[e], y);
+        for (int i = 0; i < 4; i++) {
+            const uint32_t t = tb + 4 * wave + i;
+            const size_t vo = (size_t)(t0 + (t < len ? t : 0)) * C + (size_t)h * 64 + j;
+            pk[i] = k[vo]; pa[i] = a[vo]; pw[i] = w[vo]; pr[i] = r[vo]; pv[i] = v[vo];
         }
-        y = quad_sum(y);
-        if (q == 0) y_out[cur + row] = y;
-        if (tid == 0) bonus_out[(size_t)(t0 + t) * H + h] = bonus;
+    };
+    auto form_batch = [&](int buf, uint32_t tb) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t t = tb + 4 * wave + i;
+            if (t >= len) break;  // uniform per wave
+            const float kc = pk[i], ac = pa[i], rc = pr[i];
+            const float kk = kc * kkc_j;
+            float nrm = sqrtf(wave_sum(kk * kk));
+            nrm = nrm < eps ? eps : nrm;
+            const float kh = kk * (1.0f / nrm);
+            const float kmod = kc + ka_j * (kc * ac - kc);
+            const float bonus = wave_sum(rc * kmod * rk_j);
+            float *hv = hb[buf][4 * wave + i];
+            hv[j] = kh; hv[64 + j] = kh * (-ac); hv[128 + j] = pw[i]; hv[192 + j] = kmod; hv[256 + j] = rc; hv[320 + j] = pv[i];
+            if (j == 0) bl[buf][4 * wave + i] = bonus;
+        }
+    };
+    auto flush = [&](int buf, uint32_t tb) {
+        // kRB tokens x 64 rows = one float4 per thread (non-temporal: acknowledged sooner)
+        typedef float f4v __attribute__((ext_vector_type(4)));
+        const uint32_t u = tid >> 4, c4 = 4 * (tid & 15);
+        if (tb + u < len) {
+            const float4 yv = *(const float4 *)&yl[buf][u][c4];
+            __builtin_nontemporal_store((f4v){yv.x, yv.y, yv.z, yv.w}, (f4v *)(y_out + (size_t)(t0 + tb + u) * C + (size_t)h * 64 + c4));
+        }
+        if (tid < kRB && tb + tid < len) __builtin_nontemporal_store(bl[buf][tid], bonus_out + (size_t)(t0 + tb + tid) * H + h);
+    };
+    if (len > 0) {
+        load_batch(0);
+        form_batch(0, 0);
+    }
+    for (uint32_t tb = 0; tb < len; tb += kRB) {
+        const int buf = (tb / kRB) & 1;
+        // the batch's vectors are in LDS (lgkmcnt(0), then the barrier); the
+        // other buffer is free
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        __builtin_amdgcn_s_barrier();
+        if (tb > 0) flush(buf ^ 1, tb - kRB);  // the previous batch's outputs
+        const bool more = tb + kRB < len;
+        if (more) load_batch(tb + kRB);  // in flight during the scan below
+        const uint32_t nt = len - tb < (uint32_t)kRB ? len - tb : (uint32_t)kRB;
+        for (uint32_t u = 0; u < nt; u++) {
+            const float *hv = hb[buf][u];
+            float kv[16], bv[16], wv[16], mv[16], rv[16], vc[RPL];
+#pragma unroll
+            for (int m = 0; m < 4; m++) {
+                const float4 a0 = *(const float4 *)(hv + 16 * q + 4 * m), a1 = *(const float4 *)(hv + 64 + 16 * q + 4 * m),
+                             a2 = *(const float4 *)(hv + 128 + 16 * q + 4 * m), a3 = *(const float4 *)(hv + 192 + 16 * q + 4 * m),
+                             a4 = *(const float4 *)(hv + 256 + 16 * q + 4 * m);
+                kv[4 * m] = a0.x; kv[4 * m + 1] = a0.y; kv[4 * m + 2] = a0.z; kv[4 * m + 3] = a0.w;
+                bv[4 * m] = a1.x; bv[4 * m + 1] = a1.y; bv[4 * m + 2] = a1.z; bv[4 * m + 3] = a1.w;
+                wv[4 * m] = a2.x; wv[4 * m + 1] = a2.y; wv[4 * m + 2] = a2.z; wv[4 * m + 3] = a2.w;
+                mv[4 * m] = a3.x; mv[4 * m + 1] = a3.y; mv[4 * m + 2] = a3.z; mv[4 * m + 3] = a3.w;
+                rv[4 * m] = a4.x; rv[4 * m + 1] = a4.y; rv[4 * m + 2] = a4.z; rv[4 * m + 3] = a4.w;
+            }
+#pragma unroll
+            for (int i = 0; i < RPL; i++) vc[i] = hv[320 + row0 + i];
+            float sa[RPL], y[RPL];
+#pragma unroll
+            for (int i = 0; i < RPL; i++) {
+                sa[i] = 0.f;
+#pragma unroll
+                for (int e = 0; e < 16; e++) sa[i] = fmaf(s[i][e], kv[e], sa[i]);
+            }
+#pragma unroll
+            for (int i = 0; i < RPL; i++) sa[i] = quad_sum(sa[i]);
+#pragma unroll
+            for (int i = 0; i < RPL; i++) {
+                y[i] = 0.f;
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    const float ns = s[i][e] * wv[e] + sa[i] * bv[e] + vc[i] * mv[e];
+                    s[i][e] = ns;
+                    y[i] = fmaf(ns, rv[e], y[i]);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < RPL; i++) y[i] = quad_sum(y[i]);
+            if (q == 0)
+#pragma unroll
+                for (int i = 0; i < RPL; i++) yl[buf][u][row0 + i] = y[i];
+        }
+        if (more) form_batch(buf ^ 1, tb + kRB);
+    }
+    if (len > 0) {
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        __builtin_amdgcn_s_barrier();
+        const uint32_t last = (len - 1) / kRB * kRB;
+        flush((last / kRB) & 1, last);
     }
 #pragma unroll
-    for (int m = 0; m < 4; m++) Srow[m] = make_float4(s[4 * m], s[4 * m + 1], s[4 * m + 2], s[4 * m + 3]);
+    for (int i = 0; i < RPL; i++)
+#pragma unroll
+        for (int m = 0; m < 4; m++)
+            Sb[(row0 + i) * 16 + 4 * q + m] = make_float4(s[i][4 * m], s[i][4 * m + 1], s[i][4 * m + 2], s[i][4 * m + 3]);
 }
 
 // yg = ((GroupNorm(y) * gamma + beta) + bonus * v) * g in fp16: one wave per
@@ -869,12 +936,6 @@ __global__ __launch_bounds__(256) void k_gn_gate_f16(const float *__restrict__ y
     yg[o] = (_Float16)(yn * g[o]);
 }
 
-// yg = yn * g in fp16 (the one-wave form's gate)
-__global__ void k_gate_f16(const float *__restrict__ yn, const float *__restrict__ g, _Float16 *__restrict__ yg, uint64_t n) {
-    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x)
-        yg[i] = (_Float16)(yn[i] * g[i]);
-}
-
 int launch_wkv7_seq_ragged_gate(rsv_ctx *ctx, float *s, const float *r, const float *w, const float *k,
                                 const float *v, const float *a, const float *kk, const float *ka, const float *rk,
                                 const float *gamma, const float *beta, const float *g, float *y_work,
@@ -883,19 +944,21 @@ int launch_wkv7_seq_ragged_gate(rsv_ctx *ctx, float *s, const float *r, const fl
                                 uint64_t slots) {
     if (n != 64) return RSV_FAIL("wkv7_seq: head_size must be 64 (got %d)", n);
     if (nseg <= 0 || rows == 0) return 0;
-    const uint64_t cn = rows * (uint64_t)h * 64;
-    if (nseg <= 40) {  // few (long) segments: the four-lanes-per-row form
-        hipLaunchKernelGGL(k_wkv7_seq_rows4, dim3(h, nseg), dim3(256), 0, ctx->stream, s, r, w, k, v, a, kk, ka, rk,
-                           y_work, bonus_work, seg_start, seg_len, seg_slot, h, 1e-12f, rows, slots);
+    {
+        // rows per lane group: 1 (four waves per head and segment) while the
+        // launch has fewer than two such waves per SIMD, else 2 (two waves,
+        // twice the rows per lane, half the LDS vector reads per state
+        // element): the second form measured 5-15% faster on 40-64 segments
+        const int waves1 = nseg * h * 4;
+#define WKV_ROWS_LAUNCH(R)                                                                                            \
+    hipLaunchKernelGGL(k_wkv7_seq_rows<R>, dim3(h, nseg), dim3(256 / (R)), 0, ctx->stream, s, r, w, k, v, a, kk, ka, rk, \
+                       y_work, bonus_work, seg_start, seg_len, seg_slot, h, 1e-12f, rows, slots)
+        if (waves1 >= 2 * 4096) WKV_ROWS_LAUNCH(2);
+        else WKV_ROWS_LAUNCH(1);
+#undef WKV_ROWS_LAUNCH
         const uint64_t units = rows * (uint64_t)h;
         hipLaunchKernelGGL(k_gn_gate_f16, dim3((unsigned)((units + 3) / 4)), dim3(256), 0, ctx->stream, y_work,
                            bonus_work, v, gamma, beta, g, yg, units, h, gn_eps);
-    } else {
-        hipLaunchKernelGGL(k_wkv7_seq_ragged, dim3(h, nseg), dim3(64), 0, ctx->stream, s, r, w, k, v, a, kk, ka, rk,
-                           gamma, beta, y_work, seg_start, seg_len, seg_slot, h, 1e-12f, gn_eps, rows, slots);
-        uint64_t blocks = (cn + 255) / 256;
-        if (blocks > 65535 * 16) blocks = 65535 * 16;
-        hipLaunchKernelGGL(k_gate_f16, dim3((unsigned)blocks), dim3(256), 0, ctx->stream, y_work, g, yg, cn);
     }
     RSV_HIP(hipGetLastError());
     return 0;
