@@ -627,7 +627,7 @@ static int gd_tiles(const GemmArgs &g, int kind) {
 static GdKind gd_pick(const GemmArgs *gs, int n, int cus) {
     for (int i = 0; i < n; i++)
         if (!gd_fits(gs[i])) return GD_NONE;
-    static const double area[4] = {0, 256.0 * 160 * 1.0, 256.0 * 128 * 1.0, 128.0 * 128 * 1.07};
+    static const double area[4] = {0, 256.0 * 160 * 1.0, 256.0 * 128 * 1.0, 128.0 * 128 * 1.2};
     GdKind best = GD_NONE;
     double best_cost = 0;
     for (int kind = GD_256x160; kind <= GD_128x128; kind++) {
