@@ -83,10 +83,12 @@ __device__ __forceinline__ void gemm2_epilogue(const GemmArgs &g, const float16_
                 if (row >= g.m) continue;
                 const size_t o = (size_t)row * g.ldc + col;
                 const float v = gemm_epi_val<EPI>(acc[i][j][e], bias, aux[e], cur[e], scale);
+                // non-temporal stores: acknowledged sooner, so the next
+                // tile's reuse of their data registers waits less
                 if (g.c_f16)
-                    ((_Float16 *)g.c)[o] = (_Float16)v;
+                    __builtin_nontemporal_store((_Float16)v, (_Float16 *)g.c + o);
                 else
-                    ((float *)g.c)[o] = v;
+                    __builtin_nontemporal_store(v, (float *)g.c + o);
             }
         }
     }
