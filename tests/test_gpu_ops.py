@@ -697,14 +697,15 @@ def test_gemv_multi_lnmix_and_side_copy(be, batch):
 
 @pytest.mark.parametrize("batch,k,n", [(16, 1280, 320), (33, 1280, 320), (64, 1280, 320), (100, 1280, 320),
                                        (64, 256, 320), (33, 96, 320), (16, 128, 320), (64, 10240, 320),
-                                       (64, 2560, 8200), (40, 2560, 8200)])
+                                       (64, 2560, 8200), (40, 2560, 8200), (20, 2560, 8200)])
 def test_gemm_skinny(be, batch, k, n):
     """Batched-decode MFMA GEMM (fp16 x, int8/fp16 W) against float64 with
     the loader's fp16 rounding of the dequantised weights.  k <= 256 takes the
-    one-pass small-K kernel (the LoRA-up chain), larger k the row-tile kernel:
-    with few row tiles (n = 320) its k-slices meet in the last-arriving block
-    of each row tile, with many (n = 8200, a partial last tile) one block
-    covers the whole k."""
+    one-pass small-K kernel (the LoRA-up chain); k <= 2560 one block per
+    32-row tile over the whole k, or, with more tiles than CUs (n = 8200: 257
+    tiles, the last partial and its block's second tile masked), two tiles
+    per block sharing the x copies, for 32 and 64 sessions per column tile;
+    longer k (10240) k-slices and the slice-reduction launch."""
     rsv = _rsv()
     rng = np.random.default_rng(60 + batch + k)
     ki = k if k % 128 == 0 else 128  # int8 needs whole 128-groups
