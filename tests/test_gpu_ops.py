@@ -246,7 +246,7 @@ def _wkv_oracle(S, k, kk, a, ka, r, v, w, gam, bet, rk, H):
     return S2, yn, kmod
 
 
-@pytest.mark.parametrize("batch", [1, 32])
+@pytest.mark.parametrize("batch", [1, 32, 256])
 def test_wkv7_decode_config3(be, batch):
     H = 40
     C = H * 64
@@ -344,6 +344,130 @@ def test_wkv7_seq_ragged_gate_matches_scan_times_gate(be, lens):
     got = be.get(yg, T * C)
     assert rel_err(got, want) < 2e-3
     assert rel_err(be.get(S2, S.size), be.get(S1, S.size)) < 1e-5
+
+
+def test_wkv7_seq_config2_b32_t512(be):
+    """configs[2] at B=32 x T=512: 32 segments of 512 tokens (16,384 rows)
+    through rsv_wkv7_seq_ragged, segments written to permuted state slots;
+    three segments checked token by token against the oracle step (y every
+    token, the final state), and the gated fp16 form of the prefill
+    (rsv_wkv7_seq_ragged_gate, the four-lanes-per-row scan at this segment
+    count) against yn * g and the same states."""
+    rsv = _rsv()
+    H, nseg, L = 40, 32, 512
+    C, T = H * 64, 32 * 512
+    rng = np.random.default_rng(2512)
+    f16 = lambda x: x.astype(np.float16).astype(np.float32)
+    r = f16(rng.standard_normal((T, C), dtype=np.float32))
+    v = f16(rng.standard_normal((T, C), dtype=np.float32))
+    k = rng.standard_normal((T, H, 64), dtype=np.float32)
+    k = (k / np.linalg.norm(k, axis=2, keepdims=True)).reshape(T, C).astype(np.float32)
+    w = np.exp(-0.6065 / (1 + np.exp(-rng.standard_normal((T, C), dtype=np.float32)))).astype(np.float32)
+    a = (1 / (1 + np.exp(-rng.standard_normal((T, C), dtype=np.float32)))).astype(np.float32)
+    kk = np.ones(C, np.float32)
+    ka = (rng.random(C) * 0.5).astype(np.float32)
+    rk = (rng.standard_normal(C) * 0.1).astype(np.float32)
+    gam = (1 + rng.standard_normal(C) * 0.1).astype(np.float32)
+    bet = (rng.standard_normal(C) * 0.1).astype(np.float32)
+    g = (1 / (1 + np.exp(-rng.standard_normal((T, C), dtype=np.float32)))).astype(np.float32)
+    S = (rng.standard_normal((nseg, H, 64, 64)) * 0.1).astype(np.float32)
+    slots = rng.permutation(nseg).astype(np.uint32)
+    st = be.tensor(np.arange(nseg, dtype=np.uint32) * L, dtype=rsv.U32)
+    ln = be.tensor(np.full(nseg, L, np.uint32), dtype=rsv.U32)
+    sl = be.tensor(slots, dtype=rsv.U32)
+    common = [be.tensor(x) for x in (r, w, k, v, a, kk, ka, rk, gam, bet)]
+    S1, S2 = be.tensor(S), be.tensor(S)
+    yn = be.tensor(n=T * C)
+    be.call("rsv_wkv7_seq_ragged", S1, *common, yn, st, ln, sl, nseg, H, 64, 64e-5)
+    got_y = be.get(yn, T * C).reshape(T, C)
+    got_S = be.get(S1, S.size).reshape(nseg, -1)
+    for seg in (0, 13, nseg - 1):
+        Sx = S[slots[seg]].reshape(-1).copy()
+        for t in range(seg * L, (seg + 1) * L):
+            Sx, want, _ = _wkv_oracle(Sx, k[t], kk, a[t], ka, r[t], v[t], w[t], gam, bet, rk, H)
+            assert rel_err(got_y[t], want) < 2e-4, (seg, t)
+        assert rel_err(got_S[slots[seg]], Sx) < 2e-4, seg
+    gt, yw, bw = be.tensor(g), be.tensor(n=T * C), be.tensor(n=T * H)
+    yg = be.tensor(n=T * C, dtype=rsv.F16)
+    be.call("rsv_wkv7_seq_ragged_gate", S2, *common, gt, yw, bw, yg, st, ln, sl, nseg, T, H, 64, 64e-5)
+    want_g = (got_y * g).astype(np.float16).astype(np.float32)
+    assert rel_err(be.get(yg, T * C), want_g.reshape(-1)) < 2e-3
+    assert rel_err(be.get(S2, S.size), be.get(S1, S.size)) < 1e-5
+
+
+CONFIG1_SHAPES = [(2560, 2560), (10240, 2560), (2560, 10240)]
+
+
+@pytest.mark.parametrize("M", [1, 8, 32, 128, 2048])
+@pytest.mark.parametrize("fmt", ["int8", "fp16"])
+@pytest.mark.parametrize("n,k", CONFIG1_SHAPES)
+def test_linear_config1_3b_shapes(be, n, k, fmt, M):
+    _linear_config1_case(be, n, k, fmt, M)
+
+
+@pytest.mark.parametrize("M", [1, 32])
+@pytest.mark.parametrize("fmt", ["int8", "fp16"])
+def test_linear_config1_head(be, fmt, M):
+    """configs[1]'s head shape (2560 -> 65536) at M = 1 (GEMV) and 32 (the
+    row-group MFMA form), as test_linear_config1_3b_shapes."""
+    _linear_config1_case(be, 65536, 2560, fmt, M)
+
+
+def _linear_config1_case(be, n, k, fmt, M):
+    """the 3B weight shapes (out x in) in both weight forms
+    through the entry points the model and the bench's linear leg use:
+    M <= 8 the GEMVs (rsv_gemv_int8_plain / rsv_gemv_f16, fp32 x), M = 32
+    and 128 the batched MFMA GEMM on the tiled copy (rsv_gemm_skinny, 128
+    as two 64-row slabs), M = 2048 the prefill GEMM (rsv_gemm_ex: the int8
+    loader, or the DMA-tile form on fp16 weights).  Against float64 with the
+    weights as each form multiplies them (the int8 dequant in fp32 for the
+    GEMVs, rounded to fp16 for the MFMA forms); 2048-row results on 96
+    sampled rows."""
+    rsv = _rsv()
+    rng = np.random.default_rng(n + 7 * k + M + (fmt == "fp16"))
+    if fmt == "int8":
+        idx, sz, W = _int8_weight(rng, n, k)
+        h = be.int8(idx, sz)
+        Wmfma = W.astype(np.float16).astype(np.float64)
+        Wgemv = W.astype(np.float64)
+    else:
+        W16 = (rng.standard_normal((n, k)) * 0.02).astype(np.float16)
+        w16 = be.tensor(W16.astype(np.float32), dtype=rsv.F16)
+        Wmfma = Wgemv = W16.astype(np.float64)
+    x = rng.standard_normal((M, k)).astype(np.float16)
+    y = be.tensor(n=M * n)
+    out = ctypes.c_uint32()
+    if M <= 8:
+        xt = be.tensor(x.astype(np.float32))
+        if fmt == "int8":
+            be.call("rsv_gemv_int8_plain", ctypes.byref(h), xt, y, n, k, M)
+        else:
+            be.call("rsv_gemv_f16", w16, xt, y, n, k, M)
+        rows, Wref, tol = np.arange(M), Wgemv, 5e-5
+    elif M <= 128:
+        xt = be.tensor(x.astype(np.float32), dtype=rsv.F16)
+        if fmt == "int8":
+            ht = rsv.Int8Handle(h.idx, h.sz, h.m, h.k)
+            be.call("rsv_tile_weights", h.idx, n, k, 1, ctypes.byref(out))
+            ht.idx = out.value
+            be.call("rsv_tile_weights", h.sz, n, k, 4, ctypes.byref(out))
+            ht.sz = out.value
+            j = rsv.MmJob(NONE, ctypes.pointer(ht), n, k, xt, y, NONE, 0, NONE, NONE, NONE, 1)
+        else:
+            be.call("rsv_tile_weights", w16, n, k, 2, ctypes.byref(out))
+            j = rsv.MmJob(out.value, None, n, k, xt, y, NONE, 0, NONE, NONE, NONE, 1)
+        be.call("rsv_gemm_skinny", ctypes.byref(j), 1, M)
+        rows, Wref, tol = np.arange(M), Wmfma, 2e-5
+    else:
+        xt = be.tensor(x.astype(np.float32), dtype=rsv.F16)
+        if fmt == "int8":
+            be.call("rsv_gemm_ex", xt, NONE, ctypes.byref(h), y, M, n, k, 0, NONE, NONE, NONE)
+        else:
+            be.call("rsv_gemm_ex", xt, w16, None, y, M, n, k, 0, NONE, NONE, NONE)
+        rows, Wref, tol = np.sort(rng.choice(M, 96, replace=False)), Wmfma, 1e-5
+    got = be.get(y, M * n).reshape(M, n)[rows]
+    want = x[rows].astype(np.float64) @ Wref.T
+    assert rel_err(got, want) < tol
 
 
 # ------------------------------------------------------------- argmax / tokens
