@@ -9,7 +9,7 @@ runs:
   - B=1:  `--steps` tokens (one step = one decoded token)      -> `value`
   - B=64: `--steps-b64` steps of 64 concurrent sessions         -> extra
 and the ragged prefill of configs[4] (64 prompts, lengths U[16, 2048] seed 2,
-packed into chunks of <= 4096 tokens) is timed once               -> extra.
+packed into chunks of <= 12288 tokens) is timed once               -> extra.
 
 Prints ONE JSON line (rank 0).  Inputs are resident in HBM when each timed
 region starts; timings bracket the region with device synchronisation.

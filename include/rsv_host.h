@@ -98,7 +98,7 @@ int rsv_sample_selfloop_batch(rsv_bundle *b, rsv_state *s, const uint32_t *seeds
  * decode_len tokens into out[q*decode_len ...].  Each step is one packed
  * dispatch: a decode token for every generating slot, then prompt chunks
  * (slots in order, split across steps when needed), budget tokens in all
- * (budget >= batch, <= 4096).  The GPU sampler (sp) draws token k of slot q
+ * (budget >= batch, <= 12288).  The GPU sampler (sp) draws token k of slot q
  * with seed seeds[q] + k.  steps (optional, max_steps entries) receives one
  * record per step; *nsteps the step count. */
 typedef struct rsv_serve_step {
