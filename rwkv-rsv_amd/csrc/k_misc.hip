@@ -502,109 +502,164 @@ int launch_segmean(rsv_ctx *ctx, const float *x, float *out, const uint32_t *len
 namespace rsv {
 
 // ------------------------------------------------ packed prefill token mix
-// One block per token row.  LN of the row and of its predecessor (or the
-// slot's token-shift state for the first row of a segment); outputs fp16
-// GEMM operands.  The state itself is written by k_seq_state_store in a
-// separate launch so no block reads a state row another block rewrites.
-__device__ __forceinline__ void row_ln(const float *xr, const float *gamma, const float *beta, int C, float eps,
-                                       float *red, float (&out)[kMaxPer]) {
-    float xv[kMaxPer];
-    float s = 0.0f;
-#pragma unroll
-    for (int m = 0; m < kMaxPer; m++) {
-        const int i = threadIdx.x + 256 * m;
-        xv[m] = i < C ? xr[i] : 0.0f;
-        s += xv[m];
+// One block per token row, thread t owning the eight consecutive columns
+// 8t .. 8t+7 (c % 8 == 0, c <= 8192; blocks of c/8 threads rounded up to a
+// whole wave): 32-byte loads and 16-byte fp16 stores.  LN of the row and of
+// its predecessor (or the slot's token-shift state for the first row of a
+// segment) with the two rows' sums in one pair of block reductions; outputs
+// fp16 GEMM operands.  The state itself is written by k_seq_state_store in a
+// separate launch (so no block reads a state row another block rewrites),
+// with the same arithmetic per row, so a row's LN is the same value whether
+// a later row of its chunk recomputes it or a later chunk reads it back.
+constexpr int kLnVec = 8;
+constexpr int kLnMaxC = 8192;
+
+// Sums of (v.x, v.y) over the block (wave sums, then the waves in order).
+__device__ __forceinline__ float2 block_sum2(float2 v, float2 *red) {
+    v.x = wave_sum_last(v.x);
+    v.y = wave_sum_last(v.y);
+    const int nw = blockDim.x >> 6;
+    if ((threadIdx.x & 63) == 63) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float2 t = red[0];
+    for (int w = 1; w < nw; w++) {
+        t.x += red[w].x;
+        t.y += red[w].y;
     }
-    const float mean = block_sum256(s, red) / (float)C;
-    float q = 0.0f;
+    __syncthreads();  // red is reused by the next call
+    return t;
+}
+
+__device__ __forceinline__ void ld8(const float *p, float (&v)[kLnVec]) {
+    const float4 a = ((const float4 *)p)[0], b = ((const float4 *)p)[1];
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+
+// LayerNorm of two rows at once (a and b; model.rs:402-411), each row's
+// statistics two-pass over its own values; on return a and b hold the
+// normalised rows.  Lanes past c hold zeros and take no part.
+__device__ __forceinline__ void ln_pair(float (&a)[kLnVec], float (&b)[kLnVec], const float (&gm)[kLnVec],
+                                        const float (&bt)[kLnVec], bool live, int C, float eps, float2 *red) {
+    float2 s = make_float2(0.0f, 0.0f);
 #pragma unroll
-    for (int m = 0; m < kMaxPer; m++) {
-        const int i = threadIdx.x + 256 * m;
-        const float d = xv[m] - mean;
-        q += i < C ? d * d : 0.0f;
+    for (int e = 0; e < kLnVec; e++) {
+        s.x += a[e];
+        s.y += b[e];
     }
-    const float var = block_sum256(q, red) / (float)C + eps;
-    const float inv_std = 1.0f / sqrtf(var);
+    s = block_sum2(s, red);
+    const float ma = s.x / (float)C, mb = s.y / (float)C;
+    float2 q = make_float2(0.0f, 0.0f);
+    if (live) {
 #pragma unroll
-    for (int m = 0; m < kMaxPer; m++) {
-        const int i = threadIdx.x + 256 * m;
-        out[m] = i < C ? (xv[m] - mean) * inv_std * gamma[i] + beta[i] : 0.0f;
+        for (int e = 0; e < kLnVec; e++) {
+            const float da = a[e] - ma, db = b[e] - mb;
+            q.x += da * da;
+            q.y += db * db;
+        }
+    }
+    q = block_sum2(q, red);
+    const float ia = 1.0f / sqrtf(q.x / (float)C + eps), ib = 1.0f / sqrtf(q.y / (float)C + eps);
+#pragma unroll
+    for (int e = 0; e < kLnVec; e++) {
+        a[e] = (a[e] - ma) * ia * gm[e] + bt[e];
+        b[e] = (b[e] - mb) * ib * gm[e] + bt[e];
     }
 }
 
 struct HOut6 { _Float16 *p[6]; };
 
-__global__ __launch_bounds__(256) void k_seq_norm_mix(const float *__restrict__ x, const float *__restrict__ state,
-                                                      const float *__restrict__ gamma, const float *__restrict__ beta,
-                                                      Ptr6 coef, HOut6 out, int nout,
-                                                      const uint32_t *__restrict__ row_prev, int C, uint64_t slots,
-                                                      float eps) {
-    __shared__ float red[4];
-    const int t = blockIdx.x;
-    float ln[kMaxPer], pv[kMaxPer];
-    row_ln(x + (size_t)t * C, gamma, beta, C, eps, red, ln);
+__global__ __launch_bounds__(1024) void k_seq_norm_mix(const float *__restrict__ x, const float *__restrict__ state,
+                                                       const float *__restrict__ gamma, const float *__restrict__ beta,
+                                                       Ptr6 coef, HOut6 out, int nout,
+                                                       const uint32_t *__restrict__ row_prev, int C, uint64_t slots,
+                                                       float eps) {
+    __shared__ float2 red[16];
+    const int t = blockIdx.x, c0 = threadIdx.x * kLnVec;
+    const bool live = c0 < C;
     const uint32_t p = row_prev[t];
-    if (p & 0x80000000u) {
-        const uint32_t slot = p & 0x7FFFFFFFu;
+    const bool from_state = (p & 0x80000000u) != 0;
+    const uint32_t slot = p & 0x7FFFFFFFu;
+    // every load first: this row, its predecessor (raw x, or the LN'd state
+    // row), gamma / beta and the mix coefficients
+    float xa[kLnVec] = {}, xb[kLnVec] = {}, gm[kLnVec] = {}, bt[kLnVec] = {}, cf[6][kLnVec];
+    if (live) {
+        ld8(x + (size_t)t * C + c0, xa);
+        if (!from_state) ld8(x + (size_t)p * C + c0, xb);
+        else if (slot < slots) ld8(state + (size_t)slot * C + c0, xb);
+        ld8(gamma + c0, gm);
+        ld8(beta + c0, bt);
 #pragma unroll
-        for (int m = 0; m < kMaxPer; m++) {
-            const int i = threadIdx.x + 256 * m;
-            pv[m] = (i < C && slot < slots) ? state[(size_t)slot * C + i] : 0.0f;
-        }
-    } else {
-        row_ln(x + (size_t)p * C, gamma, beta, C, eps, red, pv);
+        for (int j = 0; j < 6; j++)
+            if (j < nout) ld8(coef.p[j] + c0, cf[j]);
     }
+    float pv[kLnVec];
 #pragma unroll
-    for (int m = 0; m < kMaxPer; m++) {
-        const int i = threadIdx.x + 256 * m;
-        if (i >= C) break;
-        const float d = pv[m] - ln[m];
-        for (int j = 0; j < nout; j++) out.p[j][(size_t)t * C + i] = (_Float16)(ln[m] + coef.p[j][i] * d);
+    for (int e = 0; e < kLnVec; e++) pv[e] = xb[e];
+    ln_pair(xa, xb, gm, bt, live, C, eps, red);  // uniform per block: the barriers inside
+    if (!from_state) {
+#pragma unroll
+        for (int e = 0; e < kLnVec; e++) pv[e] = xb[e];
+    }
+    if (!live) return;
+#pragma unroll
+    for (int j = 0; j < 6; j++) {
+        if (j >= nout) break;
+        typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+        h8 o;
+#pragma unroll
+        for (int e = 0; e < kLnVec; e++) o[e] = (_Float16)(xa[e] + cf[j][e] * (pv[e] - xa[e]));
+        *(h8 *)(out.p[j] + (size_t)t * C + c0) = o;
     }
 }
+
+static int ln_threads(int c) { return ((c / kLnVec + 63) / 64) * 64; }
 
 int launch_seq_norm_mix(rsv_ctx *ctx, const float *x, const float *state, const float *gamma, const float *beta,
                         const float *const *coef, _Float16 *const *out, int nout, const uint32_t *row_prev, int t,
                         int c, uint64_t slots, float eps) {
-    if (c <= 0 || c > 256 * kMaxPer) return RSV_FAIL("seq_norm_mix: c=%d outside 1..%d", c, 256 * kMaxPer);
+    if (c <= 0 || c > kLnMaxC || c % kLnVec) return RSV_FAIL("seq_norm_mix: c=%d must be a multiple of 8 in 8..%d", c, kLnMaxC);
     if (nout < 1 || nout > 6) return RSV_FAIL("seq_norm_mix: nout=%d", nout);
     if (t <= 0) return 0;
     Ptr6 cp{};
     HOut6 op{};
     for (int j = 0; j < nout; j++) { cp.p[j] = coef[j]; op.p[j] = out[j]; }
-    hipLaunchKernelGGL(k_seq_norm_mix, dim3(t), dim3(256), 0, ctx->stream, x, state, gamma, beta, cp, op, nout,
+    hipLaunchKernelGGL(k_seq_norm_mix, dim3(t), dim3(ln_threads(c)), 0, ctx->stream, x, state, gamma, beta, cp, op, nout,
                        row_prev, c, slots, eps);
     RSV_HIP(hipGetLastError());
     return 0;
 }
 
-__global__ __launch_bounds__(256) void k_seq_state_store(const float *__restrict__ x, float *__restrict__ state,
-                                                         const float *__restrict__ gamma,
-                                                         const float *__restrict__ beta,
-                                                         const uint32_t *__restrict__ seg_last,
-                                                         const uint32_t *__restrict__ seg_slot, int C, uint64_t rows,
-                                                         uint64_t slots, float eps) {
-    __shared__ float red[4];
-    const int g = blockIdx.x;
+__global__ __launch_bounds__(1024) void k_seq_state_store(const float *__restrict__ x, float *__restrict__ state,
+                                                          const float *__restrict__ gamma,
+                                                          const float *__restrict__ beta,
+                                                          const uint32_t *__restrict__ seg_last,
+                                                          const uint32_t *__restrict__ seg_slot, int C, uint64_t rows,
+                                                          uint64_t slots, float eps) {
+    __shared__ float2 red[16];
+    const int g = blockIdx.x, c0 = threadIdx.x * kLnVec;
+    const bool live = c0 < C;
     const uint32_t row = seg_last[g], slot = seg_slot[g];
     if (row >= rows || slot >= slots) return;  // uniform per block
-    float ln[kMaxPer];
-    row_ln(x + (size_t)row * C, gamma, beta, C, eps, red, ln);
-#pragma unroll
-    for (int m = 0; m < kMaxPer; m++) {
-        const int i = threadIdx.x + 256 * m;
-        if (i < C) state[(size_t)slot * C + i] = ln[m];
+    float xa[kLnVec] = {}, xb[kLnVec] = {}, gm[kLnVec] = {}, bt[kLnVec] = {};
+    if (live) {
+        ld8(x + (size_t)row * C + c0, xa);
+        ld8(gamma + c0, gm);
+        ld8(beta + c0, bt);
     }
+    ln_pair(xa, xb, gm, bt, live, C, eps, red);
+    if (!live) return;
+    float4 *dst = (float4 *)(state + (size_t)slot * C + c0);
+    dst[0] = make_float4(xa[0], xa[1], xa[2], xa[3]);
+    dst[1] = make_float4(xa[4], xa[5], xa[6], xa[7]);
 }
 
 int launch_seq_state_store(rsv_ctx *ctx, const float *x, float *state, const float *gamma, const float *beta,
                            const uint32_t *seg_last, const uint32_t *seg_slot, int nseg, int c, uint64_t rows,
                            uint64_t slots, float eps) {
-    if (c <= 0 || c > 256 * kMaxPer) return RSV_FAIL("seq_state_store: c=%d", c);
+    if (c <= 0 || c > kLnMaxC || c % kLnVec) return RSV_FAIL("seq_state_store: c=%d must be a multiple of 8 in 8..%d", c, kLnMaxC);
     if (nseg <= 0) return 0;
-    hipLaunchKernelGGL(k_seq_state_store, dim3(nseg), dim3(256), 0, ctx->stream, x, state, gamma, beta, seg_last,
-                       seg_slot, c, rows, slots, eps);
+    hipLaunchKernelGGL(k_seq_state_store, dim3(nseg), dim3(ln_threads(c)), 0, ctx->stream, x, state, gamma, beta,
+                       seg_last, seg_slot, c, rows, slots, eps);
     RSV_HIP(hipGetLastError());
     return 0;
 }
