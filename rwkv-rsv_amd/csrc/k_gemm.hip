@@ -9,6 +9,8 @@
 // Tile: 128x128 per 256-thread block, BK = 32; each wave owns a 64x64
 // quadrant as 2x2 MFMA 32x32 blocks.  The next K-slab is prefetched into
 // registers while the current one is multiplied out of LDS.
+#include <cstdlib>
+
 #include "rsv_common.h"
 
 namespace rsv {
@@ -594,6 +596,153 @@ __global__ __launch_bounds__(256, 1) void k_gemmd_multi(GemmJobs jobs) {
     gemmd_body<WM, WN, MI, NJ, true>(g, mt * C::BMR, nt * C::BNC, lds);
 }
 
+// Epilogue of a wave's 64x64 tile (2x2 MFMA 32x32 tiles at (r0, c0)) through
+// the wave's own 32x36-float LDS tile: each 32x32 tile is written in the
+// MFMA layout and read back as rows, so lane l handles row l/8 (+8, +16,
+// +24) and columns 4*(l%8) .. +3: one 16-byte access per lane, eight whole
+// 128-byte lines per instruction, for the outputs and for the operands an
+// epilogue reads (y in place, aux).  Same per-element values as
+// gemm2_epilogue.  Needs n % 4 == 0 and ldc % 4 == 0.
+template <int EPI>
+__device__ __forceinline__ void shortk_epilogue(const GemmArgs &g, const float16_t (&acc)[2][2], int r0, int c0,
+                                                int lane, float *tl) {
+    constexpr bool need_b = EPI == GE_BIAS || EPI == GE_WDECAY || EPI == GE_SIGBIAS || EPI == GE_VLERP;
+    constexpr bool need_aux = EPI == GE_ADD || EPI == GE_VLERP;
+    constexpr bool need_cur = EPI == GE_VLERP;
+    const float scale = EPI == GE_WDECAY ? g.scale[0] : 0.0f;
+    const int lr = lane >> 3, lc = 4 * (lane & 7);
+    // the read operands of 32x32 tile t = 2j + i (rows r0 + 32i .., columns
+    // c0 + 32j ..): issued one tile ahead of its use
+    float4 aux[2][4], cur[2][4];
+    auto fetch = [&](int t, int b) {
+        const int i = t & 1, j = t >> 1;
+        const int col = c0 + j * 32 + lc;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int row = r0 + i * 32 + lr + 8 * q;
+            const size_t o = (size_t)row * g.ldc + col;
+            const bool ok = col < g.n && row < g.m;
+            aux[b][q] = (need_aux && ok) ? *(const float4 *)(g.aux + o) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            cur[b][q] = (need_cur && ok) ? *(const float4 *)((const float *)g.c + o) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+    };
+    fetch(0, 0);
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const int i = t & 1, j = t >> 1, b = t & 1;
+        if (t + 1 < 4) fetch(t + 1, b ^ 1);
+        const int col = c0 + j * 32 + lc;
+        const bool cok = col < g.n;
+        float4 bias = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (need_b && cok) bias = *(const float4 *)(g.bias + col);
+        // MFMA layout -> LDS rows: element e of lane l is row
+        // 8*(e/4) + 4*(l/32) + e%4, column l%32
+#pragma unroll
+        for (int e = 0; e < 16; e++) tl[(8 * (e >> 2) + 4 * (lane >> 5) + (e & 3)) * 36 + (lane & 31)] = acc[i][j][e];
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int row = r0 + i * 32 + lr + 8 * q;
+            const float4 v = *(const float4 *)(tl + (lr + 8 * q) * 36 + lc);
+            float4 y;
+            y.x = gemm_epi_val<EPI>(v.x, bias.x, aux[b][q].x, cur[b][q].x, scale);
+            y.y = gemm_epi_val<EPI>(v.y, bias.y, aux[b][q].y, cur[b][q].y, scale);
+            y.z = gemm_epi_val<EPI>(v.z, bias.z, aux[b][q].z, cur[b][q].z, scale);
+            y.w = gemm_epi_val<EPI>(v.w, bias.w, aux[b][q].w, cur[b][q].w, scale);
+            if (!cok || row >= g.m) continue;
+            const size_t o = (size_t)row * g.ldc + col;
+            if (g.c_f16) {
+                typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+                const h4 hv = {(_Float16)y.x, (_Float16)y.y, (_Float16)y.z, (_Float16)y.w};
+                __builtin_nontemporal_store(hv, (h4 *)((_Float16 *)g.c + o));
+            } else {
+                typedef float f4 __attribute__((ext_vector_type(4)));
+                const f4 fv = {y.x, y.y, y.z, y.w};
+                __builtin_nontemporal_store(fv, (f4 *)((float *)g.c + o));
+            }
+        }
+        __builtin_amdgcn_wave_barrier();  // the LDS tile is rewritten next
+    }
+}
+
+// Short-k job lists on fp16 weights (the prefill LoRA-up products, k = 64..256):
+// the product is a few MFMA steps and the launch is bound by its epilogue's
+// stores, so the operands skip LDS.  Block = 4 waves on a 128x128 tile as in
+// k_gemm2 (waves 2x2, each 64x64 as 2x2 MFMA 32x32 tiles); every wave loads
+// its own A and B fragments from global straight into registers in the MFMA
+// layout (lane l: row l%32, k 16s + 8*(l/32) .. +7 of step s, one 16-byte
+// load per fragment), KB steps in flight, so waves never wait on each other.
+// The per-element MFMA chain equals k_gemm2's (same k order and lane
+// layout), so the results are bit-identical to it.
+template <int KB>
+__global__ __launch_bounds__(256, 2) void k_gemm_shortk_multi(GemmJobs jobs) {
+    const int bid = blockIdx.x;
+    int ji = 0;
+    while (ji + 1 < jobs.n && bid >= jobs.blk_start[ji + 1]) ji++;
+    const GemmArgs &g = jobs.j[ji];
+    const int local = bid - jobs.blk_start[ji], nt = (g.n + BN - 1) / BN;
+    const int m0 = (local / nt) * BM, n0 = (local % nt) * BN;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+    const int kq = 8 * (lane >> 5);
+    const _Float16 *A = g.a, *B = (const _Float16 *)g.b;
+    int ar[2], br[2];
+    bool aok[2], bok[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        ar[i] = m0 + wm + i * 32 + (lane & 31);
+        aok[i] = ar[i] < g.m;
+        br[i] = n0 + wn + i * 32 + (lane & 31);
+        bok[i] = br[i] < g.n;
+    }
+    float16_t acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) acc[i][j][e] = 0.0f;
+    const int nsteps = g.k / 16;
+    for (int s0 = 0; s0 < nsteps; s0 += KB) {
+        u32x4g fa[KB][2], fb[KB][2];
+#pragma unroll
+        for (int s = 0; s < KB; s++) {
+            const int k0 = 16 * (s0 + s) + kq;
+            const bool kok = s0 + s < nsteps;
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                fa[s][i] = (kok && aok[i]) ? *(const u32x4g *)(A + (size_t)ar[i] * g.lda + k0) : (u32x4g){0u, 0u, 0u, 0u};
+                fb[s][i] = (kok && bok[i]) ? *(const u32x4g *)(B + (size_t)br[i] * g.k + k0) : (u32x4g){0u, 0u, 0u, 0u};
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < KB; s++) {
+            if (s0 + s >= nsteps) break;
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int j = 0; j < 2; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8_t, fa[s][i]),
+                                                                     __builtin_bit_cast(half8_t, fb[s][j]), acc[i][j], 0, 0, 0);
+        }
+    }
+#define SHORTK_EPI(K) shortk_epilogue<K>(g, acc, m0 + wm, n0 + wn, lane, tl)
+    __shared__ float tlds[4][32 * 36];
+    float *tl = tlds[wave];
+    switch (g.epi) {
+        case GE_BIAS: SHORTK_EPI(GE_BIAS); break;
+        case GE_ADD: SHORTK_EPI(GE_ADD); break;
+        case GE_RELU2: SHORTK_EPI(GE_RELU2); break;
+        case GE_TANH: SHORTK_EPI(GE_TANH); break;
+        case GE_WDECAY: SHORTK_EPI(GE_WDECAY); break;
+        case GE_SIGBIAS: SHORTK_EPI(GE_SIGBIAS); break;
+        case GE_VLERP: SHORTK_EPI(GE_VLERP); break;
+        case GE_SIGMOID: SHORTK_EPI(GE_SIGMOID); break;
+        default: SHORTK_EPI(GE_STORE); break;
+    }
+#undef SHORTK_EPI
+}
+
 // k per stage: 64 (k_gemm3) where every job's k is a multiple of 64, else 32
 // (k_gemm2, double-buffered: the LoRA-up jobs, k = 96 etc.).
 static int gemm_check(const GemmArgs &g) {
@@ -665,9 +814,15 @@ int launch_gemm_multi(rsv_ctx *ctx, GemmJobs &jobs) {
         RSV_HIP(hipGetLastError());
         return 0;
     }
-    bool k64 = true;
-    for (int i = 0; i < jobs.n; i++) k64 &= jobs.j[i].k % 64 == 0;
-    if (k64) hipLaunchKernelGGL((k_gemm3_multi<64>), dim3(total), dim3(256), 0, ctx->stream, jobs);
+    // RSV_NO_SHORTK=1 forces the LDS-staged form (the test comparing the two)
+    bool k64 = true, shortk = !getenv("RSV_NO_SHORTK");
+    for (int i = 0; i < jobs.n; i++) {
+        const GemmArgs &g = jobs.j[i];
+        k64 &= g.k % 64 == 0;
+        shortk &= !g.b_i8 && g.k <= 256 && g.k % 16 == 0 && g.lda % 8 == 0 && g.n % 4 == 0 && g.ldc % 4 == 0;
+    }
+    if (shortk) hipLaunchKernelGGL((k_gemm_shortk_multi<4>), dim3(total), dim3(256), 0, ctx->stream, jobs);
+    else if (k64) hipLaunchKernelGGL((k_gemm3_multi<64>), dim3(total), dim3(256), 0, ctx->stream, jobs);
     else hipLaunchKernelGGL((k_gemm2_multi<128>), dim3(total), dim3(256), 0, ctx->stream, jobs);
     RSV_HIP(hipGetLastError());
     return 0;

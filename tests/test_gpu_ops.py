@@ -395,6 +395,49 @@ def test_wkv7_seq_config2_b32_t512(be):
     assert rel_err(be.get(S2, S.size), be.get(S1, S.size)) < 1e-5
 
 
+@pytest.mark.parametrize("m", [1000, 4096])
+def test_gemm_multi_shortk_equals_lds_form(be, m, monkeypatch):
+    """The prefill LoRA-up job list (fp16 weights, k = 96/96/64/256 with the
+    decay, sigmoid+bias, v-lerp and store epilogues) on the short-k kernel
+    (operands straight to registers, LDS-staged 16-byte epilogue) equals the
+    LDS-staged k_gemm2 form (RSV_NO_SHORTK=1) bit for bit, and float64."""
+    rsv = _rsv()
+    rng = np.random.default_rng(77 + m)
+    n = 2560
+    cases = [(96, 5), (96, 6), (64, 7), (256, 0)]
+    ops = []
+    for k, epi in cases:
+        x = rng.standard_normal((m, k)).astype(np.float16)
+        W = (rng.standard_normal((n, k)) * 0.05).astype(np.float16)
+        ops.append(dict(k=k, epi=epi, x=x, W=W, xt=be.tensor(x.astype(np.float32), dtype=rsv.F16),
+                        wt=be.tensor(W.astype(np.float32), dtype=rsv.F16),
+                        y0=rng.standard_normal((m, n)).astype(np.float32),
+                        bias=rng.standard_normal(n).astype(np.float32),
+                        aux=rng.standard_normal((m, n)).astype(np.float32)))
+    sc = be.tensor(np.array([-0.6065], np.float32))
+    res = {}
+    for form in ("shortk", "lds"):
+        if form == "lds":
+            monkeypatch.setenv("RSV_NO_SHORTK", "1")
+        jobs, ys = [], []
+        for o in ops:
+            y = be.tensor(o["y0"])
+            ys.append(y)
+            jobs.append(rsv.MmJob(o["wt"], None, n, o["k"], o["xt"], y, NONE, o["epi"], be.tensor(o["bias"]),
+                                  be.tensor(o["aux"]), sc, 0))
+        arr = (rsv.MmJob * len(jobs))(*jobs)
+        be.call("rsv_gemm_multi", ctypes.cast(arr, ctypes.c_void_p), len(jobs), m)
+        res[form] = [be.get(y, m * n).reshape(m, n) for y in ys]
+    monkeypatch.delenv("RSV_NO_SHORTK", raising=False)
+    sig = lambda t: 1 / (1 + np.exp(-t))
+    for o, a, b in zip(ops, res["shortk"], res["lds"]):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), o["epi"]
+        acc = o["x"].astype(np.float64) @ o["W"].astype(np.float64).T
+        want = {5: np.exp(-0.6065 * sig(acc + o["bias"])), 6: sig(acc + o["bias"]),
+                7: o["y0"] + sig(acc + o["bias"]) * (o["aux"] - o["y0"]), 0: acc}[o["epi"]]
+        assert rel_err(a, want) < 2e-5, o["epi"]
+
+
 CONFIG1_SHAPES = [(2560, 2560), (10240, 2560), (2560, 10240)]
 
 
