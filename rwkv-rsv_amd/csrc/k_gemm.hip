@@ -96,6 +96,76 @@ __device__ __forceinline__ void gemm2_epilogue(const GemmArgs &g, const float16_
     }
 }
 
+// Epilogue of a wave's (32 MI) x (32 NJ) tile (MFMA 32x32 tiles at (r0, c0)) through
+// the wave's own 32x36-float LDS tile: each 32x32 tile is written in the
+// MFMA layout and read back as rows, so lane l handles row l/8 (+8, +16,
+// +24) and columns 4*(l%8) .. +3: one 16-byte access per lane, eight whole
+// 128-byte lines per instruction, for the outputs and for the operands an
+// epilogue reads (y in place, aux).  Same per-element values as
+// gemm2_epilogue.  Needs n % 4 == 0 and ldc % 4 == 0.
+template <int EPI, int MI, int NJ>
+__device__ __forceinline__ void tile_epilogue(const GemmArgs &g, const float16_t (&acc)[MI][NJ], int r0, int c0,
+                                              int lane, float *tl) {
+    constexpr bool need_b = EPI == GE_BIAS || EPI == GE_WDECAY || EPI == GE_SIGBIAS || EPI == GE_VLERP;
+    constexpr bool need_aux = EPI == GE_ADD || EPI == GE_VLERP;
+    constexpr bool need_cur = EPI == GE_VLERP;
+    const float scale = EPI == GE_WDECAY ? g.scale[0] : 0.0f;
+    const int lr = lane >> 3, lc = 4 * (lane & 7);
+    // the read operands of 32x32 tile t = MI*j + i (rows r0 + 32i ..,
+    // columns c0 + 32j ..): issued one tile ahead of its use
+    constexpr int NT = MI * NJ;
+    float4 aux[2][4], cur[2][4];
+    auto fetch = [&](int t, int b) {
+        const int i = t % MI, j = t / MI;
+        const int col = c0 + j * 32 + lc;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int row = r0 + i * 32 + lr + 8 * q;
+            const size_t o = (size_t)row * g.ldc + col;
+            const bool ok = col < g.n && row < g.m;
+            aux[b][q] = (need_aux && ok) ? *(const float4 *)(g.aux + o) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            cur[b][q] = (need_cur && ok) ? *(const float4 *)((const float *)g.c + o) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+    };
+    fetch(0, 0);
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        const int i = t % MI, j = t / MI, b = t & 1;
+        if (t + 1 < NT) fetch(t + 1, b ^ 1);
+        const int col = c0 + j * 32 + lc;
+        const bool cok = col < g.n;
+        float4 bias = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (need_b && cok) bias = *(const float4 *)(g.bias + col);
+        // MFMA layout -> LDS rows: element e of lane l is row
+        // 8*(e/4) + 4*(l/32) + e%4, column l%32
+#pragma unroll
+        for (int e = 0; e < 16; e++) tl[(8 * (e >> 2) + 4 * (lane >> 5) + (e & 3)) * 36 + (lane & 31)] = acc[i][j][e];
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int row = r0 + i * 32 + lr + 8 * q;
+            const float4 v = *(const float4 *)(tl + (lr + 8 * q) * 36 + lc);
+            float4 y;
+            y.x = gemm_epi_val<EPI>(v.x, bias.x, aux[b][q].x, cur[b][q].x, scale);
+            y.y = gemm_epi_val<EPI>(v.y, bias.y, aux[b][q].y, cur[b][q].y, scale);
+            y.z = gemm_epi_val<EPI>(v.z, bias.z, aux[b][q].z, cur[b][q].z, scale);
+            y.w = gemm_epi_val<EPI>(v.w, bias.w, aux[b][q].w, cur[b][q].w, scale);
+            if (!cok || row >= g.m) continue;
+            const size_t o = (size_t)row * g.ldc + col;
+            if (g.c_f16) {
+                typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+                const h4 hv = {(_Float16)y.x, (_Float16)y.y, (_Float16)y.z, (_Float16)y.w};
+                __builtin_nontemporal_store(hv, (h4 *)((_Float16 *)g.c + o));
+            } else {
+                typedef float f4 __attribute__((ext_vector_type(4)));
+                const f4 fv = {y.x, y.y, y.z, y.w};
+                __builtin_nontemporal_store(fv, (f4 *)((float *)g.c + o));
+            }
+        }
+        __builtin_amdgcn_wave_barrier();  // the LDS tile is rewritten next
+    }
+}
+
 // BM2 rows (128 or 256) x 128 columns per block of 4 waves in a 2x2 layout:
 // each wave owns (BM2/2) x 64 as (BM2/64) x 2 MFMA 32x32 tiles.
 template <bool B_I8, int BM2>
@@ -555,7 +625,13 @@ __device__ __forceinline__ void gemmd_body(const GemmArgs &g, int m0, int n0, un
         }
         buf = nbuf;
     }
-#define GEMMD_EPI(K) gemm2_epilogue<K, MI, NJ>(g, acc, m0, n0, wm, wn, lane)
+    // 16-byte epilogue through LDS (the stage buffers are free once every
+    // wave is past its last operand reads): each wave takes 32x36 floats
+    const bool vec = g.n % 4 == 0 && g.ldc % 4 == 0;
+    __syncthreads();
+    float *tl = reinterpret_cast<float *>(lds) + wave * (32 * 36);
+#define GEMMD_EPI(K) do { if (vec) tile_epilogue<K, MI, NJ>(g, acc, m0 + wm, n0 + wn, lane, tl); \
+                          else gemm2_epilogue<K, MI, NJ>(g, acc, m0, n0, wm, wn, lane); } while (0)
     switch (g.epi) {
         case GE_BIAS: GEMMD_EPI(GE_BIAS); break;
         case GE_ADD: GEMMD_EPI(GE_ADD); break;
@@ -594,75 +670,6 @@ __global__ __launch_bounds__(256, 1) void k_gemmd_multi(GemmJobs jobs) {
     int mt, nt;
     gd_tile(local, tm, tn, mt, nt);
     gemmd_body<WM, WN, MI, NJ, true>(g, mt * C::BMR, nt * C::BNC, lds);
-}
-
-// Epilogue of a wave's 64x64 tile (2x2 MFMA 32x32 tiles at (r0, c0)) through
-// the wave's own 32x36-float LDS tile: each 32x32 tile is written in the
-// MFMA layout and read back as rows, so lane l handles row l/8 (+8, +16,
-// +24) and columns 4*(l%8) .. +3: one 16-byte access per lane, eight whole
-// 128-byte lines per instruction, for the outputs and for the operands an
-// epilogue reads (y in place, aux).  Same per-element values as
-// gemm2_epilogue.  Needs n % 4 == 0 and ldc % 4 == 0.
-template <int EPI>
-__device__ __forceinline__ void shortk_epilogue(const GemmArgs &g, const float16_t (&acc)[2][2], int r0, int c0,
-                                                int lane, float *tl) {
-    constexpr bool need_b = EPI == GE_BIAS || EPI == GE_WDECAY || EPI == GE_SIGBIAS || EPI == GE_VLERP;
-    constexpr bool need_aux = EPI == GE_ADD || EPI == GE_VLERP;
-    constexpr bool need_cur = EPI == GE_VLERP;
-    const float scale = EPI == GE_WDECAY ? g.scale[0] : 0.0f;
-    const int lr = lane >> 3, lc = 4 * (lane & 7);
-    // the read operands of 32x32 tile t = 2j + i (rows r0 + 32i .., columns
-    // c0 + 32j ..): issued one tile ahead of its use
-    float4 aux[2][4], cur[2][4];
-    auto fetch = [&](int t, int b) {
-        const int i = t & 1, j = t >> 1;
-        const int col = c0 + j * 32 + lc;
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const int row = r0 + i * 32 + lr + 8 * q;
-            const size_t o = (size_t)row * g.ldc + col;
-            const bool ok = col < g.n && row < g.m;
-            aux[b][q] = (need_aux && ok) ? *(const float4 *)(g.aux + o) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            cur[b][q] = (need_cur && ok) ? *(const float4 *)((const float *)g.c + o) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        }
-    };
-    fetch(0, 0);
-#pragma unroll
-    for (int t = 0; t < 4; t++) {
-        const int i = t & 1, j = t >> 1, b = t & 1;
-        if (t + 1 < 4) fetch(t + 1, b ^ 1);
-        const int col = c0 + j * 32 + lc;
-        const bool cok = col < g.n;
-        float4 bias = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (need_b && cok) bias = *(const float4 *)(g.bias + col);
-        // MFMA layout -> LDS rows: element e of lane l is row
-        // 8*(e/4) + 4*(l/32) + e%4, column l%32
-#pragma unroll
-        for (int e = 0; e < 16; e++) tl[(8 * (e >> 2) + 4 * (lane >> 5) + (e & 3)) * 36 + (lane & 31)] = acc[i][j][e];
-        __builtin_amdgcn_wave_barrier();
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const int row = r0 + i * 32 + lr + 8 * q;
-            const float4 v = *(const float4 *)(tl + (lr + 8 * q) * 36 + lc);
-            float4 y;
-            y.x = gemm_epi_val<EPI>(v.x, bias.x, aux[b][q].x, cur[b][q].x, scale);
-            y.y = gemm_epi_val<EPI>(v.y, bias.y, aux[b][q].y, cur[b][q].y, scale);
-            y.z = gemm_epi_val<EPI>(v.z, bias.z, aux[b][q].z, cur[b][q].z, scale);
-            y.w = gemm_epi_val<EPI>(v.w, bias.w, aux[b][q].w, cur[b][q].w, scale);
-            if (!cok || row >= g.m) continue;
-            const size_t o = (size_t)row * g.ldc + col;
-            if (g.c_f16) {
-                typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-                const h4 hv = {(_Float16)y.x, (_Float16)y.y, (_Float16)y.z, (_Float16)y.w};
-                __builtin_nontemporal_store(hv, (h4 *)((_Float16 *)g.c + o));
-            } else {
-                typedef float f4 __attribute__((ext_vector_type(4)));
-                const f4 fv = {y.x, y.y, y.z, y.w};
-                __builtin_nontemporal_store(fv, (f4 *)((float *)g.c + o));
-            }
-        }
-        __builtin_amdgcn_wave_barrier();  // the LDS tile is rewritten next
-    }
 }
 
 // Short-k job lists on fp16 weights (the prefill LoRA-up products, k = 64..256):
@@ -726,7 +733,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_shortk_multi(GemmJobs jobs) {
                                                                      __builtin_bit_cast(half8_t, fb[s][j]), acc[i][j], 0, 0, 0);
         }
     }
-#define SHORTK_EPI(K) shortk_epilogue<K>(g, acc, m0 + wm, n0 + wn, lane, tl)
+#define SHORTK_EPI(K) tile_epilogue<K, 2, 2>(g, acc, m0 + wm, n0 + wn, lane, tl)
     __shared__ float tlds[4][32 * 36];
     float *tl = tlds[wave];
     switch (g.epi) {
