@@ -918,22 +918,33 @@ __global__ __launch_bounds__(256 / RPL) void k_wkv7_seq_rows(
             Sb[(row0 + i) * 16 + 4 * q + m] = make_float4(s[i][4 * m], s[i][4 * m + 1], s[i][4 * m + 2], s[i][4 * m + 3]);
 }
 
-// yg = ((GroupNorm(y) * gamma + beta) + bonus * v) * g in fp16: one wave per
-// (token, head), four per block; the order of k_wkv7_seq_ragged's head_norm.
+// yg = ((GroupNorm(y) * gamma + beta) + bonus * v) * g in fp16: 16 lanes per
+// (token, head), four columns per lane (16-byte loads, 8-byte stores), four
+// (token, head) units per wave and 16 per block; the two-pass statistics are
+// 16-lane DPP row sums.
 __global__ __launch_bounds__(256) void k_gn_gate_f16(const float *__restrict__ y, const float *__restrict__ bonus,
                                                     const float *__restrict__ v, const float *__restrict__ gamma,
                                                     const float *__restrict__ beta, const float *__restrict__ g,
                                                     _Float16 *__restrict__ yg, uint64_t units, int H, float gn_eps) {
-    const uint64_t u = (uint64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (u >= units) return;  // uniform per wave
-    const int i = threadIdx.x & 63, h = (int)(u % H);
-    const size_t o = (size_t)u * 64 + i;  // (token, head) units are consecutive 64-column groups
-    const float yy = y[o];
-    const float mean = wave_sum(yy) * (1.0f / 64.0f);
-    const float d = yy - mean;
-    const float var = wave_sum(d * d) * (1.0f / 64.0f) + gn_eps;
-    const float yn = d * (1.0f / sqrtf(var)) * gamma[h * 64 + i] + beta[h * 64 + i] + bonus[u] * v[o];
-    yg[o] = (_Float16)(yn * g[o]);
+    const uint64_t u = (uint64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+    const bool live = u < units;  // the row sums below need every lane of the row
+    const int i = 4 * (threadIdx.x & 15), h = live ? (int)(u % H) : 0;
+    const size_t o = (live ? (size_t)u : 0) * 64 + i;  // (token, head) units are consecutive 64-column groups
+    const float4 yy = *(const float4 *)(y + o), vv = *(const float4 *)(v + o), gg = *(const float4 *)(g + o);
+    const float4 gm = *(const float4 *)(gamma + h * 64 + i), bt = *(const float4 *)(beta + h * 64 + i);
+    const float bo = bonus[live ? u : 0];
+    const float mean = row16_sum((yy.x + yy.y) + (yy.z + yy.w)) * (1.0f / 64.0f);
+    const float d0 = yy.x - mean, d1 = yy.y - mean, d2 = yy.z - mean, d3 = yy.w - mean;
+    const float var = row16_sum((d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3)) * (1.0f / 64.0f) + gn_eps;
+    const float inv = 1.0f / sqrtf(var);
+    if (!live) return;
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    h4 out;
+    out[0] = (_Float16)((d0 * inv * gm.x + bt.x + bo * vv.x) * gg.x);
+    out[1] = (_Float16)((d1 * inv * gm.y + bt.y + bo * vv.y) * gg.y);
+    out[2] = (_Float16)((d2 * inv * gm.z + bt.z + bo * vv.z) * gg.z);
+    out[3] = (_Float16)((d3 * inv * gm.w + bt.w + bo * vv.w) * gg.w);
+    *(h4 *)(yg + o) = out;
 }
 
 int launch_wkv7_seq_ragged_gate(rsv_ctx *ctx, float *s, const float *r, const float *w, const float *k,
@@ -957,7 +968,7 @@ int launch_wkv7_seq_ragged_gate(rsv_ctx *ctx, float *s, const float *r, const fl
         else WKV_ROWS_LAUNCH(1);
 #undef WKV_ROWS_LAUNCH
         const uint64_t units = rows * (uint64_t)h;
-        hipLaunchKernelGGL(k_gn_gate_f16, dim3((unsigned)((units + 3) / 4)), dim3(256), 0, ctx->stream, y_work,
+        hipLaunchKernelGGL(k_gn_gate_f16, dim3((unsigned)((units + 15) / 16)), dim3(256), 0, ctx->stream, y_work,
                            bonus_work, v, gamma, beta, g, yg, units, h, gn_eps);
     }
     RSV_HIP(hipGetLastError());
