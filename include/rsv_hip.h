@@ -390,6 +390,15 @@ typedef struct rsv_mm_job {
  * job takes both tiled tensors in its rsv_int8 handle. */
 int rsv_tile_weights(rsv_ctx *ctx, uint32_t src, uint64_t n, uint64_t k, int esz, uint32_t *out);
 int rsv_gemm_skinny(rsv_ctx *ctx, const rsv_mm_job *jobs, uint64_t njobs, uint64_t batch);
+/* rsv_gemm_skinny of one tiled job split into nslice equal k-slices (no
+ * reference counterpart: the batched decode's ffn.value, backend.rs:691-725
+ * runs it as one GEMM).  Slice s writes its partial product
+ * sum_{k in slice s} x[b, k] W[n, k] to y[s, b, n] (y F32 of at least
+ * nslice*batch*n; plain store, no epilogue operands), so no partial sums
+ * pass through a reduction launch: rsv_ln_mix_f16_acc folds them into the
+ * residual row it normalises.  k must be nslice slices of 128-multiples of
+ * 288..2560 columns. */
+int rsv_gemm_skinny_kslices(rsv_ctx *ctx, const rsv_mm_job *job, uint64_t nslice, uint64_t batch);
 
 /* ---- several prefill GEMMs in one launch (no reference counterpart: the
  * reference issues one cuBLAS GEMM per weight, backend.rs:691-725).  Job i
@@ -406,6 +415,14 @@ int rsv_gemm_multi(rsv_ctx *ctx, const rsv_mm_job *jobs, uint64_t njobs, uint64_
 int rsv_ln_mix_f16(rsv_ctx *ctx, uint32_t x, uint32_t state, uint32_t gamma, uint32_t beta,
                    const uint32_t *coef, const uint32_t *out_f16, uint64_t nout, uint64_t c, float eps,
                    uint64_t batch);
+/* rsv_ln_mix_f16 of the row x + ((part[0] + part[1]) + ...) (part F32
+ * [nslice, batch, c], the k-slice sums of rsv_gemm_skinny_kslices, added in
+ * slice order); the summed row is also stored to xout (0xFFFFFFFF: not
+ * stored), which must be another tensor than x.  The residual add of
+ * ffn.value (model.rs:494-496) joined to the next LayerNorm (model.rs:402, 507). */
+int rsv_ln_mix_f16_acc(rsv_ctx *ctx, uint32_t x, uint32_t part, uint64_t nslice, uint32_t xout, uint32_t state,
+                       uint32_t gamma, uint32_t beta, const uint32_t *coef, const uint32_t *out_f16, uint64_t nout,
+                       uint64_t c, float eps, uint64_t batch);
 /* fuse_ka_dplr_norm_batch that also (or only) writes f16(y_norm * g) into
  * yg_f16 (the att.output operand); y_norm may be 0xFFFFFFFF. */
 int rsv_wkv7_decode_ex(rsv_ctx *ctx, uint32_t s, uint32_t k, uint32_t k_k, uint32_t a, uint32_t k_a,

@@ -1424,14 +1424,9 @@ extern "C" int rsv_gemv_multi(rsv_ctx *ctx, const rsv_gemv_job *jobs, uint64_t n
     return launch_gemv_jobs(ctx, J, (int)batch);
 }
 
-extern "C" int rsv_gemm_skinny(rsv_ctx *ctx, const rsv_mm_job *jobs, uint64_t njobs, uint64_t batch) {
-    CHECK_CTX();
-    if (!jobs || njobs == 0 || njobs > (uint64_t)kMaxJobs) return RSV_FAIL("gemm_skinny: 1..%d jobs", kMaxJobs);
-    SkinnyJobs S{};
-    S.n = (int)njobs;
-    for (uint64_t i = 0; i < njobs; i++) {
-        const rsv_mm_job &q = jobs[i];
-        SkinnyJob &J = S.j[i];
+// One rsv_mm_job of rsv_gemm_skinny -> its kernel job (operands checked).
+static int skinny_job_of(rsv_ctx *ctx, const rsv_mm_job &q, uint64_t batch, SkinnyJob &J) {
+    {
         if (q.w8) {
             const uint32_t *idx, *sz;
             if (int8_operands(ctx, q.w8, q.n, q.k, &idx, &sz, "gemm_skinny")) return -1;
@@ -1473,6 +1468,49 @@ extern "C" int rsv_gemm_skinny(rsv_ctx *ctx, const rsv_mm_job *jobs, uint64_t nj
         }
         J.N = (int)q.n;
         J.K = (int)q.k;
+    }
+    return 0;
+}
+
+extern "C" int rsv_gemm_skinny(rsv_ctx *ctx, const rsv_mm_job *jobs, uint64_t njobs, uint64_t batch) {
+    CHECK_CTX();
+    if (!jobs || njobs == 0 || njobs > (uint64_t)kMaxJobs) return RSV_FAIL("gemm_skinny: 1..%d jobs", kMaxJobs);
+    SkinnyJobs S{};
+    S.n = (int)njobs;
+    for (uint64_t i = 0; i < njobs; i++)
+        if (skinny_job_of(ctx, jobs[i], batch, S.j[i])) return -1;
+    return launch_skinny(ctx, S, (int)batch);
+}
+
+extern "C" int rsv_gemm_skinny_kslices(rsv_ctx *ctx, const rsv_mm_job *job, uint64_t nslice, uint64_t batch) {
+    CHECK_CTX();
+    if (!job) return RSV_FAIL("gemm_skinny_kslices: null job");
+    if (nslice == 0 || nslice > (uint64_t)kMaxJobs) return RSV_FAIL("gemm_skinny_kslices: 1..%d slices", kMaxJobs);
+    const rsv_mm_job &q = *job;
+    if (!q.tiled) return RSV_FAIL("gemm_skinny_kslices: takes the tiled weight copy");
+    if (q.epilogue != GE_STORE || q.y2 != 0xFFFFFFFFu || q.bias != 0xFFFFFFFFu || q.aux != 0xFFFFFFFFu ||
+        q.scale != 0xFFFFFFFFu)
+        return RSV_FAIL("gemm_skinny_kslices: partial sums take the plain store (no epilogue operands)");
+    if (q.k % (nslice * 128) != 0) return RSV_FAIL("gemm_skinny_kslices: k=%llu is not %llu slices of 128-multiples",
+                                                   (unsigned long long)q.k, (unsigned long long)nslice);
+    Tensor *ty = get_tensor(ctx, q.y);
+    if (!ty || ty->dtype != RSV_F32 || ty->len < nslice * batch * q.n)
+        return RSV_FAIL("gemm_skinny_kslices: y must be F32 of nslice*batch*n");
+    SkinnyJob J0{};
+    if (skinny_job_of(ctx, q, batch, J0)) return -1;
+    const int ks = (int)(q.k / nslice);
+    const size_t tbytes = J0.fmt == FMT_I8 ? 1024 : 2048;
+    SkinnyJobs S{};
+    S.n = (int)nslice;
+    for (int sl = 0; sl < S.n; sl++) {
+        SkinnyJob &J = S.j[sl];
+        J = J0;
+        J.K = ks;
+        J.wtile_ch = (int)(q.k / 32);
+        J.w = (const uint8_t *)J0.w + (size_t)sl * (ks / 32) * tbytes;
+        if (J0.fmt == FMT_I8) J.sz = J0.sz + (size_t)sl * (ks / 128) * 32;
+        J.x = J0.x + (size_t)sl * ks;
+        J.y = (float *)J0.y + (size_t)sl * batch * q.n;
     }
     return launch_skinny(ctx, S, (int)batch);
 }
@@ -1540,6 +1578,40 @@ extern "C" int rsv_ln_mix_f16(rsv_ctx *ctx, uint32_t x, uint32_t state, uint32_t
         op[j] = (_Float16 *)p;
     }
     return launch_ln_mix_f16(ctx, F32P(px), pst, F32P(pg), F32P(pb), cp, op, (int)nout, (int)c, eps, (int)batch);
+}
+
+extern "C" int rsv_ln_mix_f16_acc(rsv_ctx *ctx, uint32_t x, uint32_t part, uint64_t nslice, uint32_t xout,
+                                  uint32_t state, uint32_t gamma, uint32_t beta, const uint32_t *coef,
+                                  const uint32_t *out_f16, uint64_t nout, uint64_t c, float eps, uint64_t batch) {
+    CHECK_CTX();
+    if ((nout != 1 && nout != 6) || !out_f16) return RSV_FAIL("ln_mix_f16_acc: nout must be 1 or 6");
+    if (nslice == 0 || nslice > 16) return RSV_FAIL("ln_mix_f16_acc: 1..16 slices");
+    OPND(px, x, RSV_F32, c * batch, "ln_mix_f16_acc x");
+    OPND(pp, part, RSV_F32, nslice * c * batch, "ln_mix_f16_acc part");
+    float *pxo = nullptr;
+    if (xout != 0xFFFFFFFFu) {
+        if (xout == x) return RSV_FAIL("ln_mix_f16_acc: xout must not be x (other blocks of a row still read it)");
+        OPND(po, xout, RSV_F32, c * batch, "ln_mix_f16_acc xout");
+        pxo = F32P(po);
+    }
+    OPND(pg, gamma, RSV_F32, c, "ln_mix_f16_acc gamma");
+    OPND(pb, beta, RSV_F32, c, "ln_mix_f16_acc beta");
+    float *pst = nullptr;
+    if (state != 0xFFFFFFFFu) { OPND(ps, state, RSV_F32, c * batch, "ln_mix_f16_acc state"); pst = F32P(ps); }
+    const float *cp[6] = {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
+    _Float16 *op[6];
+    for (uint64_t j = 0; j < nout; j++) {
+        void *p = nullptr;
+        if (coef && coef[j] != 0xFFFFFFFFu) {
+            if (!pst) return RSV_FAIL("ln_mix_f16_acc: a token-shift mix needs the state row");
+            if (opnd(ctx, coef[j], RSV_F32, c, &p, "ln_mix_f16_acc coef")) return -1;
+            cp[j] = (const float *)p;
+        }
+        if (opnd(ctx, out_f16[j], RSV_F16, c * batch, &p, "ln_mix_f16_acc out")) return -1;
+        op[j] = (_Float16 *)p;
+    }
+    return launch_ln_mix_f16(ctx, F32P(px), pst, F32P(pg), F32P(pb), cp, op, (int)nout, (int)c, eps, (int)batch,
+                             F32P(pp), (int)nslice, pxo);
 }
 
 extern "C" int rsv_wkv7_decode_ex(rsv_ctx *ctx, uint32_t s, uint32_t k, uint32_t k_k, uint32_t a, uint32_t k_a,

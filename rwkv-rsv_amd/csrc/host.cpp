@@ -264,6 +264,12 @@ struct GpuState {
     uint32_t v_first = NONE;                    // [batch, C]
 };
 
+// An on/off environment switch (unset: def; "0": off).
+bool getenv_flag(const char *name, bool def) {
+    const char *e = getenv(name);
+    return e && e[0] ? e[0] != '0' : def;
+}
+
 struct WorkBufs {
     uint64_t batch = 0;
     uint32_t x, xr, xw, xk, xv, xa, xg, r, k, v, vmid, wmid, amid, gmid, w, a, g, yn, xb, r2, xnorm, logits, token;
@@ -271,6 +277,13 @@ struct WorkBufs {
     // fp16 operands of the matrix-core path (batch >= kMmBatch)
     bool mm = false;
     uint32_t mix16[6], vmid16, wmid16, amid16, gmid16, yg16, xb16, r216, xn16;
+    // ffn.value as k-slices (matrix-core path): partial sums [fv_nsl, B, C]
+    // that the next LayerNorm adds to the residual row, written to the other
+    // residual buffer (x / xalt); xcur is the buffer holding the row, pend
+    // whether partial sums are still to be added.  Set up per decode step.
+    int fv_nsl = 0;
+    uint32_t fvpart = NONE, xalt = NONE, xcur = NONE;
+    bool pend = false;
 };
 
 constexpr uint64_t kMmBatch = 16;  // sessions from which decode GEMMs run on MFMA
@@ -619,6 +632,14 @@ int get_bufs(rsv_bundle *b, uint64_t B, WorkBufs *&out) {
         HK(new_tensor(b, C * B, RSV_F16, w.xb16));
         HK(new_tensor(b, I.ffn * B, RSV_F16, w.r216));
         HK(new_tensor(b, C * B, RSV_F16, w.xn16));
+        // ffn.value k-slices of at most 2560 columns, each a 128-multiple
+        // above the small-k kernel's 256 (10240 -> 4 x 2560)
+        const uint64_t F = I.ffn, nsl = (F + 2559) / 2560;
+        if (F % (nsl * 128) == 0 && F / nsl > 256 && getenv_flag("RSV_FFNV_KSLICE", true)) {
+            w.fv_nsl = (int)nsl;
+            HK(new_tensor(b, nsl * C * B, RSV_F32, w.fvpart));
+            HK(new_tensor(b, C * B, RSV_F32, w.xalt));
+        }
     }
     out = &(b->bufs[B] = w);
     return 0;
@@ -912,6 +933,20 @@ int tile_model(rsv_bundle *b) {
 // Batched layer (B >= kMmBatch): the same math with fp16 activation
 // operands so every weight product runs on matrix cores, each weight byte
 // streamed once per step for all sessions.
+// ffn.value of the matrix-core layer: k-slice partial sums left for the
+// next LayerNorm (rsv_ln_mix_f16_acc), or one GEMM adding into the row.
+int ffn_value_mm(rsv_bundle *b, Layer &L, WorkBufs &w) {
+    if (w.fv_nsl) {
+        rsv_mm_job j6 = mm_job(L.fv, w.r216, w.fvpart, 0);
+        CK(rsv_gemm_skinny_kslices(b->ctx, &j6, w.fv_nsl, w.batch));
+        w.pend = true;
+        return 0;
+    }
+    rsv_mm_job j6 = mm_job(L.fv, w.r216, w.xcur, 2);
+    CK(rsv_gemm_skinny(b->ctx, &j6, 1, w.batch));
+    return 0;
+}
+
 int forward_layer_mm(rsv_bundle *b, uint64_t i, WorkBufs &w, GpuState &s) {
     rsv_ctx *c = b->ctx;
     const rsv_model_info &I = b->info;
@@ -919,7 +954,16 @@ int forward_layer_mm(rsv_bundle *b, uint64_t i, WorkBufs &w, GpuState &s) {
     Layer &L = b->layers[i];
     enum { G_STORE = 0, G_BIAS = 1, G_ADD = 2, G_RELU2 = 3, G_TANH = 4, G_WDECAY = 5, G_SIGB = 6, G_VLERP = 7, G_SIG = 8 };
     const uint32_t coef6[6] = {L.x_r, L.x_w, L.x_k, L.x_v, L.x_a, L.x_g};
-    CK(rsv_ln_mix_f16(c, w.x, s.tmix_x[i], L.ln1_w, L.ln1_b, coef6, w.mix16, 6, C, LN_EPS, B));
+    if (w.pend) {
+        // the previous layer's ffn.value slices join this LayerNorm
+        const uint32_t dst = w.xcur == w.x ? w.xalt : w.x;
+        CK(rsv_ln_mix_f16_acc(c, w.xcur, w.fvpart, w.fv_nsl, dst, s.tmix_x[i], L.ln1_w, L.ln1_b, coef6, w.mix16, 6, C,
+                              LN_EPS, B));
+        w.xcur = dst;
+        w.pend = false;
+    } else {
+        CK(rsv_ln_mix_f16(c, w.xcur, s.tmix_x[i], L.ln1_w, L.ln1_b, coef6, w.mix16, 6, C, LN_EPS, B));
+    }
     const uint32_t xr = w.mix16[0], xw = w.mix16[1], xk = w.mix16[2], xv = w.mix16[3], xa = w.mix16[4], xg = w.mix16[5];
     rsv_mm_job j1[7] = {
         mm_job(L.rw, xr, w.r, G_STORE), mm_job(L.kw, xk, w.k, G_STORE), mm_job(L.vw, xv, w.v, G_STORE),
@@ -946,14 +990,12 @@ int forward_layer_mm(rsv_bundle *b, uint64_t i, WorkBufs &w, GpuState &s) {
         op.f16_io = 1;
         op.y_bonus = op.y_gate = NONE;
         CK(rsv_wkv7_lora_decode(c, &op, B));
-        rsv_mm_job j4 = mm_job(L.ow, w.yg16, w.x, G_ADD);
+        rsv_mm_job j4 = mm_job(L.ow, w.yg16, w.xcur, G_ADD);
         CK(rsv_gemm_skinny(c, &j4, 1, B));
-        CK(rsv_ln_mix_f16(c, w.x, s.cmix_x[i], L.ln2_w, L.ln2_b, &L.ffn_x_k, &w.xb16, 1, C, LN_EPS, B));
+        CK(rsv_ln_mix_f16(c, w.xcur, s.cmix_x[i], L.ln2_w, L.ln2_b, &L.ffn_x_k, &w.xb16, 1, C, LN_EPS, B));
         rsv_mm_job j5 = mm_job(L.fk, w.xb16, w.r216, G_RELU2);
         CK(rsv_gemm_skinny(c, &j5, 1, B));
-        rsv_mm_job j6 = mm_job(L.fv, w.r216, w.x, G_ADD);
-        CK(rsv_gemm_skinny(c, &j6, 1, B));
-        return 0;
+        return ffn_value_mm(b, L, w);
     }
     rsv_mm_job j2[4] = {
         mm_job(L.lw2, w.wmid16, w.w, G_WDECAY), mm_job(L.la2, w.amid16, w.a, G_SIGB),
@@ -967,14 +1009,12 @@ int forward_layer_mm(rsv_bundle *b, uint64_t i, WorkBufs &w, GpuState &s) {
     CK(rsv_gemm_skinny(c, j2, 4, B));
     CK(rsv_wkv7_decode_ex(c, s.rnn[i], w.k, L.k_k, w.a, L.k_a, w.r, w.v, w.w, L.lnx_w, L.lnx_b, L.r_k, NONE, w.g,
                           w.yg16, I.n_head, I.head_size, L2_EPS, GN_EPS, B));
-    rsv_mm_job j4 = mm_job(L.ow, w.yg16, w.x, G_ADD);
+    rsv_mm_job j4 = mm_job(L.ow, w.yg16, w.xcur, G_ADD);
     CK(rsv_gemm_skinny(c, &j4, 1, B));
-    CK(rsv_ln_mix_f16(c, w.x, s.cmix_x[i], L.ln2_w, L.ln2_b, &L.ffn_x_k, &w.xb16, 1, C, LN_EPS, B));
+    CK(rsv_ln_mix_f16(c, w.xcur, s.cmix_x[i], L.ln2_w, L.ln2_b, &L.ffn_x_k, &w.xb16, 1, C, LN_EPS, B));
     rsv_mm_job j5 = mm_job(L.fk, w.xb16, w.r216, G_RELU2);
     CK(rsv_gemm_skinny(c, &j5, 1, B));
-    rsv_mm_job j6 = mm_job(L.fv, w.r216, w.x, G_ADD);
-    CK(rsv_gemm_skinny(c, &j6, 1, B));
-    return 0;
+    return ffn_value_mm(b, L, w);
 }
 
 bool use_trait_ops() {
@@ -994,9 +1034,17 @@ int decode_step(rsv_bundle *b, WorkBufs &w, GpuState &s) {
     rsv_ctx *c = b->ctx;
     const rsv_model_info &I = b->info;
     CK(rsv_gather_rows_device_f16(c, b->emb_ln, w.x, w.token, I.n_embd, w.batch));
+    w.xcur = w.x;
+    w.pend = false;
     for (uint64_t i = 0; i < I.n_layer; i++) HK(forward_layer(b, i, w, s));
     if (w.mm && !use_trait_ops()) {
-        CK(rsv_ln_mix_f16(c, w.x, NONE, b->ln_out_w, b->ln_out_b, nullptr, &w.xn16, 1, I.n_embd, LN_EPS, w.batch));
+        if (w.pend) {
+            CK(rsv_ln_mix_f16_acc(c, w.xcur, w.fvpart, w.fv_nsl, NONE, NONE, b->ln_out_w, b->ln_out_b, nullptr, &w.xn16,
+                                  1, I.n_embd, LN_EPS, w.batch));
+            w.pend = false;
+        } else {
+            CK(rsv_ln_mix_f16(c, w.xcur, NONE, b->ln_out_w, b->ln_out_b, nullptr, &w.xn16, 1, I.n_embd, LN_EPS, w.batch));
+        }
         rsv_mm_job jh = mm_job(b->head, w.xn16, w.logits, 0);
         CK(rsv_gemm_skinny(c, &jh, 1, w.batch));
         return 0;

@@ -709,7 +709,8 @@ template <int NOUT>
 __global__ __launch_bounds__(1024) void k_ln_mix_f16(const float *__restrict__ x, float *__restrict__ state,
                                                      const float *__restrict__ gamma,
                                                      const float *__restrict__ beta, Ptr6 coef, HOut6 out, int C,
-                                                     float eps) {
+                                                     float eps, const float *__restrict__ part, int nsl,
+                                                     size_t pstride, float *__restrict__ xout) {
     // grid (batch, parts): block (b, y) writes elements [y*plen, (y+1)*plen)
     // of row b (plen <= 1024) and takes the row statistics itself.  Every
     // load of the block (the whole row of x, and gamma/beta/state/coef of its
@@ -727,7 +728,29 @@ __global__ __launch_bounds__(1024) void k_ln_mix_f16(const float *__restrict__ x
         const int e = tid + 1024 * m;
         xv[m] = e < C ? x[(size_t)b * C + e] : 0.0f;
     }
-    const float xi = mine ? x[o] : 0.0f;
+    float xi = mine ? x[o] : 0.0f;
+    if (part) {
+        // x + the k-slice partial sums of the previous GEMM, summed in slice
+        // order; the block owning element i stores the new row to xout
+        // (another buffer: the other blocks of the row still read x)
+#pragma unroll
+        for (int m = 0; m < PER; m++) {
+            const int e = tid + 1024 * m;
+            if (e < C) {
+                const float *pp = part + (size_t)b * C + e;
+                float t = pp[0];
+                for (int q = 1; q < nsl; q++) t += pp[q * pstride];
+                xv[m] += t;
+            }
+        }
+        if (mine) {
+            const float *pp = part + o;
+            float t = pp[0];
+            for (int q = 1; q < nsl; q++) t += pp[q * pstride];
+            xi += t;
+            if (xout) xout[o] = xi;
+        }
+    }
     const float gi = mine ? gamma[i] : 0.0f, bi = mine ? beta[i] : 0.0f;
     const float pi = (mine && state) ? state[o] : 0.0f;
     float ci[NOUT];
@@ -765,8 +788,11 @@ __global__ __launch_bounds__(1024) void k_ln_mix_f16(const float *__restrict__ x
 }
 
 int launch_ln_mix_f16(rsv_ctx *ctx, const float *x, float *state, const float *gamma, const float *beta,
-                      const float *const *coef, _Float16 *const *out, int nout, int c, float eps, int batch) {
+                      const float *const *coef, _Float16 *const *out, int nout, int c, float eps, int batch,
+                      const float *part, int nsl, float *xout) {
     if (c <= 0 || c > 4096) return RSV_FAIL("ln_mix_f16: c=%d outside 1..4096", c);
+    if (part && (nsl < 1 || nsl > 16)) return RSV_FAIL("ln_mix_f16: %d partial slices outside 1..16", nsl);
+    const size_t pstride = (size_t)batch * c;
     if (batch <= 0) return 0;
     Ptr6 cp{};
     HOut6 op{};
@@ -778,8 +804,8 @@ int launch_ln_mix_f16(rsv_ctx *ctx, const float *x, float *state, const float *g
     while ((c + parts - 1) / parts > 1024) parts++;
     const dim3 grid(batch, parts);
     switch (nout) {
-        case 1: hipLaunchKernelGGL(k_ln_mix_f16<1>, grid, dim3(1024), 0, ctx->stream, x, state, gamma, beta, cp, op, c, eps); break;
-        case 6: hipLaunchKernelGGL(k_ln_mix_f16<6>, grid, dim3(1024), 0, ctx->stream, x, state, gamma, beta, cp, op, c, eps); break;
+        case 1: hipLaunchKernelGGL(k_ln_mix_f16<1>, grid, dim3(1024), 0, ctx->stream, x, state, gamma, beta, cp, op, c, eps, part, nsl, pstride, xout); break;
+        case 6: hipLaunchKernelGGL(k_ln_mix_f16<6>, grid, dim3(1024), 0, ctx->stream, x, state, gamma, beta, cp, op, c, eps, part, nsl, pstride, xout); break;
         default: return RSV_FAIL("ln_mix_f16: nout must be 1 or 6 (got %d)", nout);
     }
     RSV_HIP(hipGetLastError());

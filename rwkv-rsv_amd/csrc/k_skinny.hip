@@ -864,8 +864,10 @@ __device__ __forceinline__ void skinny8_body(const SkinnyJob &J, int rt0, int MB
     unsigned char *xbw[NSX];
 #pragma unroll
     for (int i = 0; i < NSX; i++) xbw[i] = RT == 2 ? xb0 + (i * 4 + wave) * XB : (i ? xb1 : xb0) + wave * XB;
-    const uint8_t *wt = (const uint8_t *)J.w + (size_t)rt_ld * nchunks * tbytes + lane * (I8 ? 16 : 32);
-    const uint32_t *szrow = I8 ? J.sz + (size_t)rt_ld * (J.K / 128) * 32 + (lane & 31) : nullptr;
+    // a k-slice job points into a row tile of a wider tiled matrix
+    const int tch = J.wtile_ch ? J.wtile_ch : nchunks;
+    const uint8_t *wt = (const uint8_t *)J.w + (size_t)rt_ld * tch * tbytes + lane * (I8 ? 16 : 32);
+    const uint32_t *szrow = I8 ? J.sz + (size_t)rt_ld * (tch / 4) * 32 + (lane & 31) : nullptr;
     // copy source of lane l in instruction i, relative to the step's column
     // (with two row tiles, this wave's share: instructions h*NX/2 ..)
     constexpr int NXW = NX / RT;
@@ -1454,6 +1456,9 @@ static int launch_slab(rsv_ctx *ctx, SkinnyJobs &jobs, int MB) {
             big |= (J.N + 127) / 128 >= 2 * cus;
             v8 &= J.K % 64 == 0 && J.K <= 32 * SK8_KMAX;
         }
+        bool sliced = false;
+        for (int i = 0; i < jobs.n; i++) sliced |= jobs.j[i].wtile_ch != 0;
+        if (sliced && (small || big || !v8)) return RSV_FAIL("skinny gemm: k-slice jobs need 256 < k <= %d, k %% 64 == 0", 32 * SK8_KMAX);
         if (small) return launch_small(ctx, jobs, MB);
         if (big) return launch_v4(ctx, jobs, MB);
         return v8 ? launch_v8(ctx, jobs, MB) : launch_v5(ctx, jobs, MB);

@@ -249,6 +249,7 @@ struct SkinnyJob {
     int split, ws_slot;  // k-slices per row group; first workspace tile
     int kslice;                    // k-chunks (of 32) per slice
     int tiled;                   // weights are the MFMA-tiled copy
+    int wtile_ch;                // k-chunks per row tile of the tiled copy when the job is a k-slice of it (0: K/32)
 };
 struct SkinnyJobs {
     SkinnyJob j[kMaxJobs];
@@ -260,7 +261,8 @@ int launch_skinny(rsv_ctx *ctx, SkinnyJobs &jobs, int MB);
 int launch_tile_weights(rsv_ctx *ctx, const void *src, void *dst, int n, int k, int esz);
 // LayerNorm rows + up to 6 token-shift mixes, fp16 outputs (state optional).
 int launch_ln_mix_f16(rsv_ctx *ctx, const float *x, float *state, const float *gamma, const float *beta,
-                      const float *const *coef, _Float16 *const *out, int nout, int c, float eps, int batch);
+                      const float *const *coef, _Float16 *const *out, int nout, int c, float eps, int batch,
+                      const float *part = nullptr, int nsl = 0, float *xout = nullptr);
 int launch_seq_norm_mix(rsv_ctx *ctx, const float *x, const float *state, const float *gamma, const float *beta,
                         const float *const *coef, _Float16 *const *out, int nout, const uint32_t *row_prev, int t,
                         int c, uint64_t slots, float eps);

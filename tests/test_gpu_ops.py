@@ -971,6 +971,77 @@ def test_gemm_skinny_mixed_formats(be, batch):
             assert rel_err(be.get(y, batch * n).reshape(batch, n), mixed[i]) < 1e-6, i
 
 
+@pytest.mark.parametrize("fmt", ["i8", "f16"])
+@pytest.mark.parametrize("n,k,nsl,batch", [(2560, 10240, 4, 64), (2560, 10240, 4, 16), (320, 1536, 3, 80)])
+def test_gemm_skinny_kslices_and_ln_acc(be, fmt, n, k, nsl, batch):
+    """The batched ffn.value as k-slices (rsv_gemm_skinny_kslices): slice s
+    of the tiled weights writes sum over its k range of x W^T to part[s];
+    each slice matches float64 of the loader's fp16 weights.  The next
+    LayerNorm (rsv_ln_mix_f16_acc) adds the slices to the residual row in
+    slice order: the stored row equals x + sum of the slices as float64
+    within fp32 rounding, its LN + token-shift mixes the oracle's LN of that
+    row, and the row agrees with the one-launch in-place GEMM (epilogue add)
+    within fp32 summation-order differences.  Batch 80 runs as two slabs."""
+    rsv = _rsv()
+    rng = np.random.default_rng(n + k + batch + (fmt == "f16"))
+    out = ctypes.c_uint32()
+    if fmt == "i8":
+        idx, sz, W = _int8_weight(rng, n, k)
+        h = be.int8(idx, sz)
+        ht = rsv.Int8Handle(h.idx, h.sz, h.m, h.k)
+        be.call("rsv_tile_weights", h.idx, n, k, 1, ctypes.byref(out))
+        ht.idx = out.value
+        be.call("rsv_tile_weights", h.sz, n, k, 4, ctypes.byref(out))
+        ht.sz = out.value
+        w8, w16, Wm = ctypes.pointer(ht), NONE, W.astype(np.float16).astype(np.float64)
+    else:
+        W16 = (rng.standard_normal((n, k)) * 0.02).astype(np.float16)
+        wt = be.tensor(W16.astype(np.float32), dtype=rsv.F16)
+        be.call("rsv_tile_weights", wt, n, k, 2, ctypes.byref(out))
+        w8, w16, Wm = None, out.value, W16.astype(np.float64)
+    x16 = rng.standard_normal((batch, k)).astype(np.float16)
+    xt = be.tensor(x16.astype(np.float32), dtype=rsv.F16)
+    X = x16.astype(np.float64)
+    part = be.tensor(n=nsl * batch * n)
+    j = rsv.MmJob(w16, w8, n, k, xt, part, NONE, 0, NONE, NONE, NONE, 1)
+    be.call("rsv_gemm_skinny_kslices", ctypes.byref(j), nsl, batch)
+    P = be.get(part, nsl * batch * n).reshape(nsl, batch, n)
+    ks = k // nsl
+    for q in range(nsl):
+        want = X[:, q * ks:(q + 1) * ks] @ Wm[:, q * ks:(q + 1) * ks].T
+        assert rel_err(P[q], want) < 2e-5, q
+    # residual row + slices through the LayerNorm
+    res = (rng.standard_normal((batch, n)) * 2).astype(np.float32)
+    st = rng.standard_normal((batch, n)).astype(np.float32)
+    gam, bet = rng.standard_normal(n).astype(np.float32), rng.standard_normal(n).astype(np.float32)
+    coef = rng.random(n).astype(np.float32)
+    rt, xo, stt = be.tensor(res), be.tensor(n=batch * n), be.tensor(st)
+    gt, btt, ct = be.tensor(gam), be.tensor(bet), be.tensor(coef)
+    o16 = be.tensor(n=batch * n, dtype=rsv.F16)
+    U = lambda a: np.array(a, np.uint32).ctypes.data_as(ctypes.POINTER(ctypes.c_uint32))
+    cids, oids = np.array([ct], np.uint32), np.array([o16], np.uint32)
+    be.call("rsv_ln_mix_f16_acc", rt, part, nsl, xo, stt, gt, btt, U(cids), U(oids), 1, n, 1e-5, batch)
+    xn = be.get(xo, batch * n).reshape(batch, n)
+    want_row = res.astype(np.float64) + P.astype(np.float64).sum(0)
+    assert rel_err(xn, want_row) < 1e-6
+    got16 = be.get(o16, batch * n).reshape(batch, n)
+    for b in range(0, batch, 7):
+        ln = orc.layer_norm(xn[b], gam, bet)
+        want = (ln + coef * (st[b] - ln)).astype(np.float16).astype(np.float32)
+        assert np.max(np.abs(got16[b] - want)) <= 2e-3 * np.max(np.abs(want)), b
+        assert rel_err(be.get(stt, batch * n).reshape(batch, n)[b], ln) < 1e-5
+    # against the one-launch GEMM that adds into the row in place
+    yt = be.tensor(res)
+    j1 = rsv.MmJob(w16, w8, n, k, xt, yt, NONE, 2, NONE, NONE, NONE, 1)
+    be.call("rsv_gemm_skinny", ctypes.byref(j1), 1, batch)
+    assert rel_err(be.get(yt, batch * n).reshape(batch, n), xn) < 1e-5
+    # xout must be another tensor than x; slice counts are checked
+    with pytest.raises(RuntimeError):
+        be.call("rsv_ln_mix_f16_acc", rt, part, nsl, rt, stt, gt, btt, U(cids), U(oids), 1, n, 1e-5, batch)
+    with pytest.raises(RuntimeError):
+        be.call("rsv_gemm_skinny_kslices", ctypes.byref(j), 7, batch)
+
+
 def test_ln_mix_f16_and_wkv_yg(be):
     rsv = _rsv()
     rng = np.random.default_rng(70)
