@@ -283,7 +283,7 @@ struct WorkBufs {
     // whether partial sums are still to be added.  Set up per decode step.
     int fv_nsl = 0;
     uint32_t fvpart = NONE, xalt = NONE, xcur = NONE;
-    bool pend = false;
+    int pend = 0;  // k-slices in fvpart still to be added (0: none)
 };
 
 constexpr uint64_t kMmBatch = 16;  // sessions from which decode GEMMs run on MFMA
@@ -933,17 +933,36 @@ int tile_model(rsv_bundle *b) {
 // Batched layer (B >= kMmBatch): the same math with fp16 activation
 // operands so every weight product runs on matrix cores, each weight byte
 // streamed once per step for all sessions.
-// ffn.value of the matrix-core layer: k-slice partial sums left for the
-// next LayerNorm (rsv_ln_mix_f16_acc), or one GEMM adding into the row.
-int ffn_value_mm(rsv_bundle *b, Layer &L, WorkBufs &w) {
-    if (w.fv_nsl) {
-        rsv_mm_job j6 = mm_job(L.fv, w.r216, w.fvpart, 0);
-        CK(rsv_gemm_skinny_kslices(b->ctx, &j6, w.fv_nsl, w.batch));
-        w.pend = true;
+// A weight product added to the residual row on the matrix-core path: as
+// nsl k-slice partial sums left in fvpart for the next LayerNorm
+// (ln_mix_mm), or, with nsl = 0, one GEMM adding into the row.
+int resid_gemm_mm(rsv_bundle *b, const Linear &L, uint32_t xin, WorkBufs &w, int nsl) {
+    if (nsl) {
+        rsv_mm_job j = mm_job(L, xin, w.fvpart, 0);
+        CK(rsv_gemm_skinny_kslices(b->ctx, &j, nsl, w.batch));
+        w.pend = nsl;
         return 0;
     }
-    rsv_mm_job j6 = mm_job(L.fv, w.r216, w.xcur, 2);
-    CK(rsv_gemm_skinny(b->ctx, &j6, 1, w.batch));
+    rsv_mm_job j = mm_job(L, xin, w.xcur, 2);
+    CK(rsv_gemm_skinny(b->ctx, &j, 1, w.batch));
+    return 0;
+}
+
+// rsv_ln_mix_f16 of the residual row, first adding pending k-slice sums
+// (the summed row goes to the other residual buffer, which becomes xcur).
+int ln_mix_mm(rsv_bundle *b, WorkBufs &w, uint32_t state, uint32_t gamma, uint32_t beta, const uint32_t *coef,
+              const uint32_t *out, uint64_t nout, bool keep_row = true) {
+    rsv_ctx *c = b->ctx;
+    const uint64_t C = b->info.n_embd;
+    if (w.pend) {
+        const uint32_t dst = !keep_row ? NONE : w.xcur == w.x ? w.xalt : w.x;
+        CK(rsv_ln_mix_f16_acc(c, w.xcur, w.fvpart, w.pend, dst, state, gamma, beta, coef, out, nout, C, LN_EPS,
+                              w.batch));
+        if (keep_row) w.xcur = dst;
+        w.pend = 0;
+        return 0;
+    }
+    CK(rsv_ln_mix_f16(c, w.xcur, state, gamma, beta, coef, out, nout, C, LN_EPS, w.batch));
     return 0;
 }
 
@@ -954,16 +973,7 @@ int forward_layer_mm(rsv_bundle *b, uint64_t i, WorkBufs &w, GpuState &s) {
     Layer &L = b->layers[i];
     enum { G_STORE = 0, G_BIAS = 1, G_ADD = 2, G_RELU2 = 3, G_TANH = 4, G_WDECAY = 5, G_SIGB = 6, G_VLERP = 7, G_SIG = 8 };
     const uint32_t coef6[6] = {L.x_r, L.x_w, L.x_k, L.x_v, L.x_a, L.x_g};
-    if (w.pend) {
-        // the previous layer's ffn.value slices join this LayerNorm
-        const uint32_t dst = w.xcur == w.x ? w.xalt : w.x;
-        CK(rsv_ln_mix_f16_acc(c, w.xcur, w.fvpart, w.fv_nsl, dst, s.tmix_x[i], L.ln1_w, L.ln1_b, coef6, w.mix16, 6, C,
-                              LN_EPS, B));
-        w.xcur = dst;
-        w.pend = false;
-    } else {
-        CK(rsv_ln_mix_f16(c, w.xcur, s.tmix_x[i], L.ln1_w, L.ln1_b, coef6, w.mix16, 6, C, LN_EPS, B));
-    }
+    HK(ln_mix_mm(b, w, s.tmix_x[i], L.ln1_w, L.ln1_b, coef6, w.mix16, 6));
     const uint32_t xr = w.mix16[0], xw = w.mix16[1], xk = w.mix16[2], xv = w.mix16[3], xa = w.mix16[4], xg = w.mix16[5];
     rsv_mm_job j1[7] = {
         mm_job(L.rw, xr, w.r, G_STORE), mm_job(L.kw, xk, w.k, G_STORE), mm_job(L.vw, xv, w.v, G_STORE),
@@ -990,12 +1000,11 @@ int forward_layer_mm(rsv_bundle *b, uint64_t i, WorkBufs &w, GpuState &s) {
         op.f16_io = 1;
         op.y_bonus = op.y_gate = NONE;
         CK(rsv_wkv7_lora_decode(c, &op, B));
-        rsv_mm_job j4 = mm_job(L.ow, w.yg16, w.xcur, G_ADD);
-        CK(rsv_gemm_skinny(c, &j4, 1, B));
-        CK(rsv_ln_mix_f16(c, w.xcur, s.cmix_x[i], L.ln2_w, L.ln2_b, &L.ffn_x_k, &w.xb16, 1, C, LN_EPS, B));
+        HK(resid_gemm_mm(b, L.ow, w.yg16, w, 0));
+        HK(ln_mix_mm(b, w, s.cmix_x[i], L.ln2_w, L.ln2_b, &L.ffn_x_k, &w.xb16, 1));
         rsv_mm_job j5 = mm_job(L.fk, w.xb16, w.r216, G_RELU2);
         CK(rsv_gemm_skinny(c, &j5, 1, B));
-        return ffn_value_mm(b, L, w);
+        return resid_gemm_mm(b, L.fv, w.r216, w, w.fv_nsl);
     }
     rsv_mm_job j2[4] = {
         mm_job(L.lw2, w.wmid16, w.w, G_WDECAY), mm_job(L.la2, w.amid16, w.a, G_SIGB),
@@ -1009,12 +1018,11 @@ int forward_layer_mm(rsv_bundle *b, uint64_t i, WorkBufs &w, GpuState &s) {
     CK(rsv_gemm_skinny(c, j2, 4, B));
     CK(rsv_wkv7_decode_ex(c, s.rnn[i], w.k, L.k_k, w.a, L.k_a, w.r, w.v, w.w, L.lnx_w, L.lnx_b, L.r_k, NONE, w.g,
                           w.yg16, I.n_head, I.head_size, L2_EPS, GN_EPS, B));
-    rsv_mm_job j4 = mm_job(L.ow, w.yg16, w.xcur, G_ADD);
-    CK(rsv_gemm_skinny(c, &j4, 1, B));
-    CK(rsv_ln_mix_f16(c, w.xcur, s.cmix_x[i], L.ln2_w, L.ln2_b, &L.ffn_x_k, &w.xb16, 1, C, LN_EPS, B));
+    HK(resid_gemm_mm(b, L.ow, w.yg16, w, 0));
+    HK(ln_mix_mm(b, w, s.cmix_x[i], L.ln2_w, L.ln2_b, &L.ffn_x_k, &w.xb16, 1));
     rsv_mm_job j5 = mm_job(L.fk, w.xb16, w.r216, G_RELU2);
     CK(rsv_gemm_skinny(c, &j5, 1, B));
-    return ffn_value_mm(b, L, w);
+    return resid_gemm_mm(b, L.fv, w.r216, w, w.fv_nsl);
 }
 
 bool use_trait_ops() {
@@ -1035,16 +1043,10 @@ int decode_step(rsv_bundle *b, WorkBufs &w, GpuState &s) {
     const rsv_model_info &I = b->info;
     CK(rsv_gather_rows_device_f16(c, b->emb_ln, w.x, w.token, I.n_embd, w.batch));
     w.xcur = w.x;
-    w.pend = false;
+    w.pend = 0;
     for (uint64_t i = 0; i < I.n_layer; i++) HK(forward_layer(b, i, w, s));
     if (w.mm && !use_trait_ops()) {
-        if (w.pend) {
-            CK(rsv_ln_mix_f16_acc(c, w.xcur, w.fvpart, w.fv_nsl, NONE, NONE, b->ln_out_w, b->ln_out_b, nullptr, &w.xn16,
-                                  1, I.n_embd, LN_EPS, w.batch));
-            w.pend = false;
-        } else {
-            CK(rsv_ln_mix_f16(c, w.xcur, NONE, b->ln_out_w, b->ln_out_b, nullptr, &w.xn16, 1, I.n_embd, LN_EPS, w.batch));
-        }
+        HK(ln_mix_mm(b, w, NONE, b->ln_out_w, b->ln_out_b, nullptr, &w.xn16, 1, false));
         rsv_mm_job jh = mm_job(b->head, w.xn16, w.logits, 0);
         CK(rsv_gemm_skinny(c, &jh, 1, w.batch));
         return 0;
