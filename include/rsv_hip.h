@@ -416,7 +416,7 @@ int rsv_ln_mix_f16(rsv_ctx *ctx, uint32_t x, uint32_t state, uint32_t gamma, uin
                    const uint32_t *coef, const uint32_t *out_f16, uint64_t nout, uint64_t c, float eps,
                    uint64_t batch);
 /* rsv_ln_mix_f16 of the row x + ((part[0] + part[1]) + ...) (part F32
- * [nslice, batch, c], the k-slice sums of rsv_gemm_skinny_kslices, added in
+ * [nslice, batch, c], nslice 1..4, the k-slice sums of rsv_gemm_skinny_kslices, added in
  * slice order); the summed row is also stored to xout (0xFFFFFFFF: not
  * stored), which must be another tensor than x.  The residual add of
  * ffn.value (model.rs:494-496) joined to the next LayerNorm (model.rs:402, 507). */

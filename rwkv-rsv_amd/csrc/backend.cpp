@@ -1585,7 +1585,7 @@ extern "C" int rsv_ln_mix_f16_acc(rsv_ctx *ctx, uint32_t x, uint32_t part, uint6
                                   const uint32_t *out_f16, uint64_t nout, uint64_t c, float eps, uint64_t batch) {
     CHECK_CTX();
     if ((nout != 1 && nout != 6) || !out_f16) return RSV_FAIL("ln_mix_f16_acc: nout must be 1 or 6");
-    if (nslice == 0 || nslice > 16) return RSV_FAIL("ln_mix_f16_acc: 1..16 slices");
+    if (nslice == 0 || nslice > 4) return RSV_FAIL("ln_mix_f16_acc: 1..4 slices");
     OPND(px, x, RSV_F32, c * batch, "ln_mix_f16_acc x");
     OPND(pp, part, RSV_F32, nslice * c * batch, "ln_mix_f16_acc part");
     float *pxo = nullptr;

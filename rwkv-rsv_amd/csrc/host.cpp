@@ -635,7 +635,7 @@ int get_bufs(rsv_bundle *b, uint64_t B, WorkBufs *&out) {
         // ffn.value k-slices of at most 2560 columns, each a 128-multiple
         // above the small-k kernel's 256 (10240 -> 4 x 2560)
         const uint64_t F = I.ffn, nsl = (F + 2559) / 2560;
-        if (F % (nsl * 128) == 0 && F / nsl > 256 && getenv_flag("RSV_FFNV_KSLICE", true)) {
+        if (nsl <= 4 && F % (nsl * 128) == 0 && F / nsl > 256 && getenv_flag("RSV_FFNV_KSLICE", true)) {
             w.fv_nsl = (int)nsl;
             HK(new_tensor(b, nsl * C * B, RSV_F32, w.fvpart));
             HK(new_tensor(b, C * B, RSV_F32, w.xalt));

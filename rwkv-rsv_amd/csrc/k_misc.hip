@@ -730,26 +730,24 @@ __global__ __launch_bounds__(1024) void k_ln_mix_f16(const float *__restrict__ x
     }
     float xi = mine ? x[o] : 0.0f;
     if (part) {
-        // x + the k-slice partial sums of the previous GEMM, summed in slice
-        // order; the block owning element i stores the new row to xout
-        // (another buffer: the other blocks of the row still read x)
+        // x + the k-slice partial sums of the previous GEMM (at most 4),
+        // summed in slice order (missing slices read as 0, which adds
+        // nothing); every load is issued before the first sum.  The block
+        // owning element i stores the new row to xout (another buffer: the
+        // other blocks of the row still read x)
+        float pv[PER + 1][4];
 #pragma unroll
-        for (int m = 0; m < PER; m++) {
-            const int e = tid + 1024 * m;
-            if (e < C) {
-                const float *pp = part + (size_t)b * C + e;
-                float t = pp[0];
-                for (int q = 1; q < nsl; q++) t += pp[q * pstride];
-                xv[m] += t;
-            }
+        for (int m = 0; m <= PER; m++) {
+            const int e = m < PER ? tid + 1024 * m : i;
+            const bool ok = m < PER ? e < C : mine;
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+                pv[m][q] = ok && q < nsl ? part[(size_t)b * C + e + q * pstride] : 0.0f;
         }
-        if (mine) {
-            const float *pp = part + o;
-            float t = pp[0];
-            for (int q = 1; q < nsl; q++) t += pp[q * pstride];
-            xi += t;
-            if (xout) xout[o] = xi;
-        }
+#pragma unroll
+        for (int m = 0; m < PER; m++) xv[m] += ((pv[m][0] + pv[m][1]) + pv[m][2]) + pv[m][3];
+        xi += ((pv[PER][0] + pv[PER][1]) + pv[PER][2]) + pv[PER][3];
+        if (mine && xout) xout[o] = xi;
     }
     const float gi = mine ? gamma[i] : 0.0f, bi = mine ? beta[i] : 0.0f;
     const float pi = (mine && state) ? state[o] : 0.0f;
@@ -791,7 +789,7 @@ int launch_ln_mix_f16(rsv_ctx *ctx, const float *x, float *state, const float *g
                       const float *const *coef, _Float16 *const *out, int nout, int c, float eps, int batch,
                       const float *part, int nsl, float *xout) {
     if (c <= 0 || c > 4096) return RSV_FAIL("ln_mix_f16: c=%d outside 1..4096", c);
-    if (part && (nsl < 1 || nsl > 16)) return RSV_FAIL("ln_mix_f16: %d partial slices outside 1..16", nsl);
+    if (part && (nsl < 1 || nsl > 4)) return RSV_FAIL("ln_mix_f16: %d partial slices outside 1..4", nsl);
     const size_t pstride = (size_t)batch * c;
     if (batch <= 0) return 0;
     Ptr6 cp{};
