@@ -966,6 +966,16 @@ int ln_mix_mm(rsv_bundle *b, WorkBufs &w, uint32_t state, uint32_t gamma, uint32
     return 0;
 }
 
+// att.output k-slices on the matrix-core path (its 2560 rows are only 80
+// row tiles: two slices spread them over twice the CUs, the slice sums
+// going to LN2).  RSV_ATTO_KSLICE=0 keeps one GEMM adding into the row.
+int atto_nsl(const Linear &L) {
+    const char *e = getenv("RSV_ATTO_KSLICE");
+    const int n = e && e[0] ? atoi(e) : 2;
+    if (n <= 1 || n > 4 || L.k % (uint64_t)(n * 128) != 0 || L.k / n <= 256 || L.k / n > 2560 || (L.k / n) % 64) return 0;
+    return n;
+}
+
 int forward_layer_mm(rsv_bundle *b, uint64_t i, WorkBufs &w, GpuState &s) {
     rsv_ctx *c = b->ctx;
     const rsv_model_info &I = b->info;
@@ -1000,7 +1010,7 @@ int forward_layer_mm(rsv_bundle *b, uint64_t i, WorkBufs &w, GpuState &s) {
         op.f16_io = 1;
         op.y_bonus = op.y_gate = NONE;
         CK(rsv_wkv7_lora_decode(c, &op, B));
-        HK(resid_gemm_mm(b, L.ow, w.yg16, w, 0));
+        HK(resid_gemm_mm(b, L.ow, w.yg16, w, w.fv_nsl ? atto_nsl(L.ow) : 0));
         HK(ln_mix_mm(b, w, s.cmix_x[i], L.ln2_w, L.ln2_b, &L.ffn_x_k, &w.xb16, 1));
         rsv_mm_job j5 = mm_job(L.fk, w.xb16, w.r216, G_RELU2);
         CK(rsv_gemm_skinny(c, &j5, 1, B));
@@ -1018,7 +1028,7 @@ int forward_layer_mm(rsv_bundle *b, uint64_t i, WorkBufs &w, GpuState &s) {
     CK(rsv_gemm_skinny(c, j2, 4, B));
     CK(rsv_wkv7_decode_ex(c, s.rnn[i], w.k, L.k_k, w.a, L.k_a, w.r, w.v, w.w, L.lnx_w, L.lnx_b, L.r_k, NONE, w.g,
                           w.yg16, I.n_head, I.head_size, L2_EPS, GN_EPS, B));
-    HK(resid_gemm_mm(b, L.ow, w.yg16, w, 0));
+    HK(resid_gemm_mm(b, L.ow, w.yg16, w, w.fv_nsl ? atto_nsl(L.ow) : 0));
     HK(ln_mix_mm(b, w, s.cmix_x[i], L.ln2_w, L.ln2_b, &L.ffn_x_k, &w.xb16, 1));
     rsv_mm_job j5 = mm_job(L.fk, w.xb16, w.r216, G_RELU2);
     CK(rsv_gemm_skinny(c, &j5, 1, B));

@@ -1063,10 +1063,15 @@ __global__ __launch_bounds__(256 * RT) void k_skinny8(SkinnyJobs jobs, int MB) {
     int ji = 0;
     while (ji + 1 < jobs.n && bid >= jobs.blk_start[ji + 1]) ji++;
     const int rt0 = (bid - jobs.blk_start[ji]) * RT;
-    if (jobs.j[ji].fmt == FMT_I8)
-        skinny8_body<MT, true, 10, RT>(jobs.j[ji], rt0, MB, xb0, xb1);
-    else
-        skinny8_body<MT, false, 10, RT>(jobs.j[ji], rt0, MB, xb0, xb1);
+    // k = 1280 (a half-k slice) runs its 5 steps per wave unrolled too
+    const bool k1280 = RT == 1 && jobs.j[ji].K == 32 * 40;
+    if (jobs.j[ji].fmt == FMT_I8) {
+        if (k1280) skinny8_body<MT, true, 5, RT>(jobs.j[ji], rt0, MB, xb0, xb1);
+        else skinny8_body<MT, true, 10, RT>(jobs.j[ji], rt0, MB, xb0, xb1);
+    } else {
+        if (k1280) skinny8_body<MT, false, 5, RT>(jobs.j[ji], rt0, MB, xb0, xb1);
+        else skinny8_body<MT, false, 10, RT>(jobs.j[ji], rt0, MB, xb0, xb1);
+    }
 }
 
 // Tiled copy of a weight matrix [n, k] (int8 bytes or fp16) for k_skinny4;

@@ -972,7 +972,7 @@ def test_gemm_skinny_mixed_formats(be, batch):
 
 
 @pytest.mark.parametrize("fmt", ["i8", "f16"])
-@pytest.mark.parametrize("n,k,nsl,batch", [(2560, 10240, 4, 64), (2560, 10240, 4, 16), (320, 1536, 3, 80)])
+@pytest.mark.parametrize("n,k,nsl,batch", [(2560, 10240, 4, 64), (2560, 10240, 4, 16), (2560, 2560, 2, 64), (2560, 2560, 2, 20), (320, 1536, 3, 80)])
 def test_gemm_skinny_kslices_and_ln_acc(be, fmt, n, k, nsl, batch):
     """The batched ffn.value as k-slices (rsv_gemm_skinny_kslices): slice s
     of the tiled weights writes sum over its k range of x W^T to part[s];
