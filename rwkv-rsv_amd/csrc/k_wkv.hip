@@ -956,16 +956,15 @@ int launch_wkv7_seq_ragged_gate(rsv_ctx *ctx, float *s, const float *r, const fl
     if (n != 64) return RSV_FAIL("wkv7_seq: head_size must be 64 (got %d)", n);
     if (nseg <= 0 || rows == 0) return 0;
     {
-        // rows per lane group: 1 (four waves per head and segment) while the
-        // launch has fewer than two such waves per SIMD, else 2 (two waves,
-        // twice the rows per lane, half the LDS vector reads per state
-        // element): the second form measured 5-15% faster on 40-64 segments
-        const int waves1 = nseg * h * 4;
+        // two rows per lane group (two waves per head and segment, half the
+        // LDS vector reads per state element): faster than one row (four
+        // waves) at every chunk shape of a 64-session ragged prefill, including
+        // chunks of few long segments (115.5k against 114.9k tok/s when one
+        // row per group was used below 51 segments)
 #define WKV_ROWS_LAUNCH(R)                                                                                            \
     hipLaunchKernelGGL(k_wkv7_seq_rows<R>, dim3(h, nseg), dim3(256 / (R)), 0, ctx->stream, s, r, w, k, v, a, kk, ka, rk, \
                        y_work, bonus_work, seg_start, seg_len, seg_slot, h, 1e-12f, rows, slots)
-        if (waves1 >= 2 * 4096) WKV_ROWS_LAUNCH(2);
-        else WKV_ROWS_LAUNCH(1);
+        WKV_ROWS_LAUNCH(2);
 #undef WKV_ROWS_LAUNCH
         const uint64_t units = rows * (uint64_t)h;
         hipLaunchKernelGGL(k_gn_gate_f16, dim3((unsigned)((units + 15) / 16)), dim3(256), 0, ctx->stream, y_work,
