@@ -447,7 +447,9 @@ def main():
         lens = rng.integers(16, 2049, size=64)
         pr = [synth.prompt(cfg, int(n), seed=1000 + i) for i, n in enumerate(lens)]
         SP = bundle.create_batch_state(64)
-        bundle.forward_seq_batch(SP, [p[:16] for p in pr])  # warm-up
+        # warm-up: the same pass once, so that the timed pass finds its work
+        # buffers (sized by the largest chunk) allocated, as a serving process does
+        bundle.forward_seq_batch(SP, pr)
         SP.reset()
         rsv.hip_lib().rsv_synchronize(bundle.ctx())
         t0 = time.perf_counter()
@@ -467,7 +469,9 @@ def main():
         SV = bundle.create_batch_state(64)
         sp = rsv.SamplerParams(temperature=1.0, top_k=0, top_p=0.9)
         seeds = np.arange(64, dtype=np.uint32) * 7919 + 2
-        bundle.serve_ragged(SV, [p[:16] for p in pr], 2, sp, seeds, budget=4096)  # warm-up
+        # warm-up: 64 x 64 prompt tokens fill a whole 4096-row step, so the
+        # timed run finds its work buffers allocated
+        bundle.serve_ragged(SV, [p[:64] for p in pr], 2, sp, seeds, budget=4096)
         SV.reset()
         t0 = time.perf_counter()
         toks, steps = bundle.serve_ragged(SV, pr, args.serve_decode, sp, seeds, budget=4096)
