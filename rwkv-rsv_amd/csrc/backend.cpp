@@ -129,15 +129,6 @@ int rsv_create(int device, rsv_ctx **out) {
         delete ctx;
         return RSV_FAIL("rsv_create: %s", why.c_str());
     }
-    ctx->sparse_cnt_cap = 1 << 16;
-    if (hipMalloc(&ctx->sparse_cnt, ctx->sparse_cnt_cap * 4) != hipSuccess ||
-        hipMemset(ctx->sparse_cnt, 0, ctx->sparse_cnt_cap * 4) != hipSuccess) {
-        if (ctx->sparse_cnt) hipFree(ctx->sparse_cnt);
-        hipFree(ctx->skinny_ws);
-        hipStreamDestroy(ctx->stream);
-        delete ctx;
-        return RSV_FAIL("rsv_create: counter allocation failed");
-    }
     *out = ctx;
     return 0;
 }
@@ -153,7 +144,6 @@ int rsv_destroy(rsv_ctx *ctx) {
     if (ctx->hist_dev) hipFree(ctx->hist_dev);
     if (ctx->sample_work) hipFree(ctx->sample_work);
     if (ctx->skinny_ws) hipFree(ctx->skinny_ws);
-    if (ctx->sparse_cnt) hipFree(ctx->sparse_cnt);
     hipStreamDestroy(ctx->stream);
     delete ctx;
     return 0;

@@ -5,12 +5,12 @@
 // [f/128][c/256][f%128][c%256], so a non-zero f is one contiguous 512-byte
 // row of 256 outputs.
 //
-// Grid (C/256 column blocks, F-ranges, sessions), one launch.  A block loads
-// the r2 of its whole F-range, compacts the non-zero f with wave ballots and
-// streams those rows with eight loads in flight per thread; thread t owns
-// output column t of the block.  The F-range partials meet in a workspace and
-// the last block of each column block adds them to x in range order, so the
-// result does not depend on scheduling (the reference adds with atomics).
+// Grid (C/256 column blocks, F-ranges, sessions).  A block loads the r2 of
+// its whole F-range, compacts the non-zero f with wave ballots and streams
+// those rows with four loads in flight per thread; thread t owns output
+// column t of the block.  The F-range partials meet in a workspace and a
+// second launch adds them to x in range order, so the result does not depend
+// on scheduling (the reference adds with atomics).
 #include "rsv_common.h"
 #include <algorithm>
 
@@ -47,28 +47,20 @@ __global__ void k_tile_ffn_value(const uint8_t *__restrict__ idx, const uint32_t
 
 constexpr int kSpMaxF = 2048;  // f values one block compacts (its share of fh)
 
-__device__ __forceinline__ float ld_sc1(const float *base, unsigned bytes, int i) {
-    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(base), (short)0, (int)bytes, 0x00020000);
-    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, i * 4, 0, 0x10));
-}
-__device__ __forceinline__ void st_sc1(float *base, unsigned bytes, int i, float v) {
-    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(base, (short)0, (int)bytes, 0x00020000);
-    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, i * 4, 0, 0x10);
-}
-
 // grid (c/256, S, batch).  Block (cb, s, b) handles f in [s*per, (s+1)*per)
-// for output columns cb*256 .. +255 of session b.  With S > 1 the partials
-// go to ws through coherent (sc1) stores; the last block of (b, cb) to
-// finish, counted on cnt[b*cbn + cb], sums them in s order and adds to x.
+// for output columns cb*256 .. +255 of session b.  With S == 1 the block adds
+// its sum to x; with S > 1 it stores its partial to ws[b][s][col] and the
+// second launch, k_ffn_sparse_reduce, adds the S partials in s order.  The
+// kernel boundary between the two launches orders the partial stores before
+// their loads on every XCD (a launch ends with its writes flushed to the
+// device-coherent level), so no in-kernel cross-block handshake is needed.
 __global__ __launch_bounds__(256) void k_ffn_sparse(const float *__restrict__ r2, const _Float16 *__restrict__ vt,
-                                                    float *__restrict__ x, float *__restrict__ ws,
-                                                    unsigned *__restrict__ cnt, unsigned ws_bytes, int c, int fh,
+                                                    float *__restrict__ x, float *__restrict__ ws, int c, int fh,
                                                     int per) {
     __shared__ float rs[kSpMaxF];
     __shared__ short ids[kSpMaxF];
     __shared__ int wcnt[4];
     __shared__ int base_n;
-    __shared__ int last;
     const int c_block = blockIdx.x, s = blockIdx.y, b = blockIdx.z, S = gridDim.y, cbn = gridDim.x;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int f0 = s * per, f1 = min(fh, f0 + per);
@@ -138,27 +130,27 @@ __global__ __launch_bounds__(256) void k_ffn_sparse(const float *__restrict__ r2
         xb[col] += acc;
         return;
     }
-    // 3. partial out; the last block of (b, c_block) adds the S partials in order
-    st_sc1(ws, ws_bytes, ((b * S + s) * c) + col, acc);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (tid == 0) {
-        unsigned *cp = cnt + b * cbn + c_block;
-        const unsigned old = __hip_atomic_fetch_add(cp, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        last = old == (unsigned)(S - 1);
-        if (last) __hip_atomic_store(cp, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __syncthreads();
-    if (!last) return;
+    ws[((size_t)(b * S + s)) * c + col] = acc;
+}
+
+// x[b][col] += ((ws[b][0][col] + ws[b][1][col]) + ...) in s order: the same
+// sum for every scheduling of the partial launch.
+__global__ __launch_bounds__(256) void k_ffn_sparse_reduce(const float *__restrict__ ws, float *__restrict__ x, int c,
+                                                           int S, int batch) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= c * batch) return;
+    const int b = i / c, col = i - b * c;
+    const float *p = ws + (size_t)b * S * c + col;
     float sum = 0.0f;
     for (int q0 = 0; q0 < S; q0 += 8) {
         float pv[8];
 #pragma unroll
-        for (int q = 0; q < 8; q++) pv[q] = q0 + q < S ? ld_sc1(ws, ws_bytes, ((b * S + q0 + q) * c) + col) : 0.0f;
+        for (int q = 0; q < 8; q++) pv[q] = q0 + q < S ? p[(size_t)(q0 + q) * c] : 0.0f;
 #pragma unroll
-        for (int q = 0; q < 8; q++) sum += pv[q];
+        for (int q = 0; q < 8; q++)
+            if (q0 + q < S) sum += pv[q];
     }
-    xb[col] += sum;
+    x[i] += sum;
 }
 
 }  // namespace
@@ -183,11 +175,16 @@ int launch_ffn_sparse(rsv_ctx *ctx, const float *r2, const _Float16 *vt, float *
     const int per = (fh + S - 1) / S;
     S = (fh + per - 1) / per;
     const size_t need = (size_t)S * batch * c;
-    if (S > 1 && (need > ctx->skinny_ws_cap || (size_t)batch * cbn > ctx->sparse_cnt_cap))
+    if (S > 1 && need > ctx->skinny_ws_cap)
         return RSV_FAIL("ffn_value_sparse_add: workspace too small for batch %d", batch);
-    hipLaunchKernelGGL(k_ffn_sparse, dim3(cbn, S, batch), dim3(256), 0, ctx->stream, r2, vt, x, ctx->skinny_ws,
-                       ctx->sparse_cnt, (unsigned)std::min(need * 4, (size_t)0xFFFFFFF0u), c, fh, per);
+    hipLaunchKernelGGL(k_ffn_sparse, dim3(cbn, S, batch), dim3(256), 0, ctx->stream, r2, vt, x, ctx->skinny_ws, c, fh,
+                       per);
     RSV_HIP(hipGetLastError());
+    if (S > 1) {
+        hipLaunchKernelGGL(k_ffn_sparse_reduce, dim3((c * batch + 255) / 256), dim3(256), 0, ctx->stream,
+                           (const float *)ctx->skinny_ws, x, c, S, batch);
+        RSV_HIP(hipGetLastError());
+    }
     return 0;
 }
 

@@ -346,17 +346,18 @@ def test_wkv7_seq_ragged_gate_matches_scan_times_gate(be, lens):
     assert rel_err(be.get(S2, S.size), be.get(S1, S.size)) < 1e-5
 
 
-def test_wkv7_seq_config2_b32_t512(be):
-    """configs[2] at B=32 x T=512: 32 segments of 512 tokens (16,384 rows)
+@pytest.mark.parametrize("nseg", [32, 256])
+def test_wkv7_seq_config2_t512(be, nseg):
+    """configs[2] at B=32 and B=256 x T=512: nseg segments of 512 tokens
     through rsv_wkv7_seq_ragged, segments written to permuted state slots;
     three segments checked token by token against the oracle step (y every
     token, the final state), and the gated fp16 form of the prefill
     (rsv_wkv7_seq_ragged_gate, the four-lanes-per-row scan at this segment
     count) against yn * g and the same states."""
     rsv = _rsv()
-    H, nseg, L = 40, 32, 512
-    C, T = H * 64, 32 * 512
-    rng = np.random.default_rng(2512)
+    H, L = 40, 512
+    C, T = H * 64, nseg * 512
+    rng = np.random.default_rng(2512 + nseg)
     f16 = lambda x: x.astype(np.float16).astype(np.float32)
     r = f16(rng.standard_normal((T, C), dtype=np.float32))
     v = f16(rng.standard_normal((T, C), dtype=np.float32))
@@ -448,11 +449,12 @@ def test_linear_config1_3b_shapes(be, n, k, fmt, M):
     _linear_config1_case(be, n, k, fmt, M)
 
 
-@pytest.mark.parametrize("M", [1, 32])
+@pytest.mark.parametrize("M", [1, 8, 32, 128, 2048])
 @pytest.mark.parametrize("fmt", ["int8", "fp16"])
 def test_linear_config1_head(be, fmt, M):
-    """configs[1]'s head shape (2560 -> 65536) at M = 1 (GEMV) and 32 (the
-    row-group MFMA form), as test_linear_config1_3b_shapes."""
+    """configs[1]'s head shape (2560 -> 65536) at every M of the config:
+    1 and 8 on the GEMVs, 32 and 128 on the MFMA skinny forms, 2048 on the
+    prefill GEMM, as test_linear_config1_3b_shapes."""
     _linear_config1_case(be, 65536, 2560, fmt, M)
 
 
