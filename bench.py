@@ -7,7 +7,7 @@ head in the reference's int8 format.  Each session is seeded with a 32-token
 uniform random prompt (prefilled untimed), then the argmax decode self-loop
 runs:
   - B=1:  `--steps` tokens (one step = one decoded token)      -> `value`
-  - B=64: `--steps-b64` steps of 64 concurrent sessions         -> extra
+  - B=8 and B=64: `--steps-b64` steps of 8 / 64 concurrent sessions -> extra
 and the ragged prefill of configs[4] (64 prompts, lengths U[16, 2048] seed 2,
 packed into chunks of <= 12288 tokens) is timed once               -> extra.
 
@@ -194,10 +194,13 @@ def linear_leg():
     """the four 3B weight shapes (out x in) in both weight forms
     (int8 symmetric per-row scale in the reference format from N(0, 0.02^2)
     masters; fp16 N(0, 0.02^2)) times activations of M rows, fp16 N(0, 1)
-    (the M <= 8 GEMV path takes them as f32 of the same values).  Each call
-    is timed over enough weight copies to exceed the 256 MB MALL.  M <= 8 is
-    held to HBM bandwidth; M >= 32 reports MFMA utilisation against dense
-    fp16 (and its bytes)."""
+    (the row-major GEMVs take them as f32 of the same values).  Each call
+    is timed over enough weight copies to exceed the 256 MB MALL.  M = 1 is
+    the B=1 GEMV; M = 8 .. 128 the batched-decode MFMA form on the tiled
+    weight copy (what the model runs for 2 <= B < prefill chunks), with the
+    trait-op GEMV on the row-major weights beside it at M = 8; M = 2048 the
+    prefill GEMM.  M <= 8 is held to HBM bandwidth; M >= 32 also reports
+    MFMA utilisation against dense fp16."""
     import ctypes
     import rsv
     import synth
@@ -231,14 +234,19 @@ def linear_leg():
             for M in (1, 8, 32, 128, 2048):
                 xh = rng.standard_normal((M, k)).astype(np.float16).astype(np.float32)
                 y = be.tensor(n=M * n)
+                rowmajor_us = None
                 if M <= 8:
+                    # the trait-op GEMV on the row-major weights (B=1: k_gemv_os2, 2..16: k_gemv_mb)
                     x = be.tensor(xh)
                     if fmt == "int8":
                         fn = lambda i, x=x, y=y, M=M: be.call("rsv_gemv_int8_plain", ctypes.byref(copies[i % ncopy]), x, y, n, k, M)
                     else:
                         fn = lambda i, x=x, y=y, M=M: be.call("rsv_gemv_f16", copies[i % ncopy], x, y, n, k, M)
-                    kern = "k_gemv_os2" if M == 1 else "k_gemv"
-                elif M <= 128:
+                    kern = "k_gemv_os2" if M == 1 else "k_gemv_mb"
+                    if M > 1:
+                        rowmajor_us = tm.us(fn, max(8, min(200, int(3e-3 / (wbytes / 5e12)))))
+                if 1 < M <= 128:
+                    # the model's batched-decode form: MFMA on the tiled weight copy
                     if tiled is None:
                         tiled = []
                         out = ctypes.c_uint32()
@@ -258,7 +266,7 @@ def linear_leg():
                                       n, k, x, y, NONE, 0, NONE, NONE, NONE, 1) for t in tiled]
                     fn = lambda i, jobs=jobs, M=M: be.call("rsv_gemm_skinny", ctypes.byref(jobs[i % ncopy]), 1, M)
                     kern = "k_skinny4" if n >= 65536 else ("k_skinny8" if k <= 2560 else "k_skinny5")
-                else:
+                elif M > 128:
                     x = be.tensor(xh, dtype=rsv.F16)
                     if fmt == "int8":
                         fn = lambda i, x=x, y=y: be.call("rsv_gemm_ex", x, NONE, ctypes.byref(copies[i % ncopy]), y, 2048, n, k, 0, NONE, NONE, NONE)
@@ -270,12 +278,16 @@ def linear_leg():
                 byts = wbytes + 2 * M * k + 4 * M * n
                 row = dict(shape=name, weights=fmt, M=M, kernel=kern, us=round(us, 3), bytes=int(byts),
                            gbs=round(byts / us / 1e3, 1), hbm_frac=round(byts / us / 1e3 / HBM_PEAK_GBS, 4))
+                if rowmajor_us is not None:
+                    row.update(rowmajor_kernel="k_gemv_mb", rowmajor_us=round(rowmajor_us, 3),
+                               rowmajor_hbm_frac=round(byts / rowmajor_us / 1e3 / HBM_PEAK_GBS, 4))
                 if M >= 32:
                     tf = 2.0 * M * n * k / us / 1e6
                     row.update(tflops=round(tf, 1), mfma_frac=round(tf / MFMA_F16_PEAK_TFLOPS, 4))
                 rows.append(row)
                 log(f"linear {name:24s} {fmt:4s} M={M:5d} {kern:10s} {us:9.2f} us {row['gbs']:8.0f} GB/s"
-                    + (f" {row['tflops']:7.1f} TFLOP/s" if M >= 32 else ""))
+                    + (f" {row['tflops']:7.1f} TFLOP/s" if M >= 32 else "")
+                    + (f"  (row-major k_gemv_mb {rowmajor_us:.2f} us)" if rowmajor_us is not None else ""))
             del copies, tiled
         del idx, sz, w16_host
     be.close()
@@ -423,6 +435,22 @@ def main():
     b1_sample_tps = args.steps / (ms_s / 1000.0)
     log(f"B=1 sample self-loop (T=1, top_p=0.9): {b1_sample_tps:.1f} tok/s")
     S1.free()
+
+    # ---------------- B = 8 argmax self-loop (small-batch decode, HBM-bound)
+    B8 = 8
+    S8 = bundle.create_batch_state(B8)
+    prompts8 = [synth.prompt(cfg, 32, seed=200 + i) for i in range(B8)]
+    bundle.forward_seq_batch(S8, [p[:-1] for p in prompts8])
+    seeds8 = np.array([int(p[-1]) for p in prompts8], np.uint32)
+    snap8 = S8.back()
+    bundle.argmax_selfloop_batch(S8, seeds8, 4)
+    S8.load(snap8)
+    _, ms8 = bundle.argmax_selfloop_batch_timed(S8, seeds8, args.steps_b64)
+    b8_tps = B8 * args.steps_b64 / (ms8 / 1000.0)
+    bytes8 = decode_bytes_per_step(cfg, B8)
+    log(f"B=8: {b8_tps:.0f} tok/s, {ms8 / args.steps_b64:.3f} ms/step, "
+        f"{bytes8 / (ms8 / args.steps_b64 / 1000) / 1e9:.0f} GB/s, {b8_tps / b1_tps:.2f}x B=1")
+    S8.free()
 
     # ---------------- B = 64 argmax self-loop
     B = 64
@@ -572,6 +600,9 @@ def main():
                      "step_frac": round(bytes1 / (ms / args.steps / 1000) / 1e9 / HBM_PEAK_GBS, 4)},
         "cpu_baseline": cpu,
         "extra": {"b1_wall_tok_s": round(b1_wall_tps, 2),
+                  "b8_tok_s": round(b8_tps, 1), "b8_ms_per_step": round(ms8 / args.steps_b64, 4),
+                  "b8_hbm_frac": round(bytes8 / (ms8 / args.steps_b64 / 1000) / 1e9 / HBM_PEAK_GBS, 4),
+                  "b8_over_b1": round(b8_tps / b1_tps, 3),
                   "b64_tok_s": round(b64_tps, 1), "b64_ms_per_step": round(ms64 / args.steps_b64, 4),
                   "b64_hbm_frac": round(bytes64 / (ms64 / args.steps_b64 / 1000) / 1e9 / HBM_PEAK_GBS, 4),
                   "b1_sample_selfloop_tok_s": round(b1_sample_tps, 2),

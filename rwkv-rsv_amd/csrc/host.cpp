@@ -286,7 +286,11 @@ struct WorkBufs {
     int pend = 0;  // k-slices in fvpart still to be added (0: none)
 };
 
-constexpr uint64_t kMmBatch = 16;  // sessions from which decode GEMMs run on MFMA
+constexpr uint64_t kMmBatch = 2;  // sessions from which decode GEMMs run on MFMA
+uint64_t mm_batch() {
+    const char *e = getenv("RSV_MM_BATCH");
+    return e ? (uint64_t)atoi(e) : kMmBatch;
+}
 constexpr uint64_t kSmallPrefill = 128;  // packed prefill rows that still take the decode MFMA kernel
 
 struct SeqBufs {
@@ -620,7 +624,7 @@ int get_bufs(rsv_bundle *b, uint64_t B, WorkBufs *&out) {
     HK(new_tensor(b, I.ffn * B, RSV_F32, w.r2));
     HK(new_tensor(b, I.vocab * B, RSV_F32, w.logits));
     HK(new_tensor(b, B, RSV_U32, w.token));
-    w.mm = B >= kMmBatch;
+    w.mm = B >= mm_batch();
     if (w.mm) {
         HK(tile_model(b));
         for (auto &m : w.mix16) HK(new_tensor(b, C * B, RSV_F16, m));

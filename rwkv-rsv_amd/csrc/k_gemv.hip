@@ -446,6 +446,397 @@ static int launch_t(rsv_ctx *ctx, GemvJobs &jobs, int batch) {
     return 0;
 }
 
+// ---------------------------------------------------------------- 2 <= B <= 16
+// Batched decode GEMV that streams every weight byte once for up to 16
+// sessions (the reference's gemv_variant_mb streams it once per 4 sessions,
+// backend_cuda.rs:3381-3554).  With B sessions a VALU dot product costs B/2
+// v_dot2 per weight pair, about the HBM time of the weights at B = 8; the
+// products therefore run on v_mfma_f32_16x16x32_f16 with the sessions as the
+// 16 rows of A (x, fp16) and 16 weight rows as the columns of B, and the
+// kernel stays bound by the weight stream at every B <= 16.
+//
+//   - A block owns a range of rows of one job and one k-slice (<= kMfKS
+//     columns).  It stages x of all sessions for the slice into LDS as fp16
+//     (the job's prologue applied on the way; session-major rows padded by
+//     16 bytes so the 16 session rows fall in different banks).
+//   - A unit is 16 rows x 64 bytes of weights (64 int8 or 32 fp16 columns),
+//     one 16-byte load per lane: lane (n = l%16, g = l/16) loads row n,
+//     bytes 16g..16g+15 of the unit.  int8 pairs become the exact fp16
+//     values 1024 + q (one v_perm each); the A operand of lane (m = l%16, g)
+//     is x of session m at the same columns, so A and B pair up on the same
+//     k.  D[session 4g+i][row n] lands in the lane that loaded row n.
+//   - int8 (model.rs:234-252): a unit lies inside one 128-column group, so
+//     s*sum(x*q) + z*sum(x) = s*D + (z - 1024*s)*dx with D the unit's MFMA
+//     sum and dx the sum of the unit's fp16 x of the session (staged).
+//   - Each wave streams its units through a kMfRing-deep register ring.
+//     With >= 4 row tiles in the block a wave owns whole tiles; with fewer,
+//     the four waves split the slice's units and their partial tiles meet in
+//     LDS in wave order.
+//   - Rows longer than kMfKS split into k-slices whose partial sums go to a
+//     workspace; k_gemv_mb_reduce adds them in slice order and applies the
+//     epilogue.
+constexpr int kMfNT = 512;
+constexpr int kMfKS = 2560;
+constexpr int kMfXS = kMfKS + 8;  // LDS row stride of one session's x (halves)
+constexpr int kMfRing = 8;
+constexpr int kMfSlots = 4;  // row tiles one wave may touch (bounds the rows per block)
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
+
+// int8 bytes 2i, 2i+1 of w -> fp16 pair (1024 + q_lo, 1024 + q_hi)
+__device__ __forceinline__ uint32_t q2h(uint32_t w, int pair) {
+    return __builtin_amdgcn_perm(0x64646464u, w, pair ? 0x04030402u : 0x04010400u);
+}
+
+// Stages x[b, k0 .. k0+KS) for b < nb into LDS rows xs + b*kMfXS as fp16
+// after the job's prologue; int8 jobs also get dx[unit*16 + b], the sum of
+// the session's fp16 x over each 64-column unit.
+template <int BT>
+__device__ __forceinline__ void stage_x_mf(const GemvJob &J, int k0, int KS, int nb, bool wr_ln, _Float16 *xs,
+                                           float *dx, float (*red)[4]) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const bool i8 = J.fmt == FMT_I8;
+    const int NO = KS / 8;  // octets in the slice
+    constexpr int UO = (kMfKS / 8 + kMfNT - 1) / kMfNT;
+    const bool ln = J.pro == PRO_LNMIX;
+    float4 g0[UO], g1[UO], e0[UO], e1[UO], c0[UO], c1[UO];
+    if (ln) {
+#pragma unroll
+        for (int j = 0; j < UO; j++) {
+            const int u = min(tid + kMfNT * j, NO - 1);
+            const float4 *gp = (const float4 *)(J.gamma + 8 * u), *bp = (const float4 *)(J.beta + 8 * u),
+                         *cp = (const float4 *)(J.coef + 8 * u);
+            g0[j] = gp[0]; g1[j] = gp[1]; e0[j] = bp[0]; e1[j] = bp[1]; c0[j] = cp[0]; c1[j] = cp[1];
+        }
+    }
+    // sessions in fours: every load of a group first, then its statistics
+    constexpr int SG = 4;
+    for (int b2 = 0; b2 < nb; b2 += SG) {
+        float v[SG][UO][8], pv[SG][UO][8];
+#pragma unroll
+        for (int q = 0; q < SG; q++) {
+            const int b = min(b2 + q, nb - 1);
+            const size_t ro = (size_t)b * J.ldx + k0;
+#pragma unroll
+            for (int j = 0; j < UO; j++) {
+                const int uc = min(tid + kMfNT * j, NO - 1);
+                const float4 *xp = (const float4 *)(J.x + ro + 8 * uc);
+                float4 a0 = xp[0], a1 = xp[1], m0 = make_float4(0.f, 0.f, 0.f, 0.f), m1 = m0;
+                if (ln) {
+                    const float4 *pp = (const float4 *)(J.prev + ro + 8 * uc);
+                    m0 = pp[0]; m1 = pp[1];
+                } else if (J.pro == PRO_MUL) {
+                    const float4 *pp = (const float4 *)(J.xmul + ro + 8 * uc);
+                    m0 = pp[0]; m1 = pp[1];
+                }
+                v[q][j][0] = a0.x; v[q][j][1] = a0.y; v[q][j][2] = a0.z; v[q][j][3] = a0.w;
+                v[q][j][4] = a1.x; v[q][j][5] = a1.y; v[q][j][6] = a1.z; v[q][j][7] = a1.w;
+                pv[q][j][0] = m0.x; pv[q][j][1] = m0.y; pv[q][j][2] = m0.z; pv[q][j][3] = m0.w;
+                pv[q][j][4] = m1.x; pv[q][j][5] = m1.y; pv[q][j][6] = m1.z; pv[q][j][7] = m1.w;
+            }
+        }
+        if (ln) {
+            // LayerNorm of each session row (two-pass, model.rs:625-635)
+            float mu[SG], inv[SG];
+#pragma unroll
+            for (int q = 0; q < SG; q++) {
+                float s = 0.0f;
+#pragma unroll
+                for (int j = 0; j < UO; j++) {
+                    if (tid + kMfNT * j >= NO) continue;
+#pragma unroll
+                    for (int e = 0; e < 8; e++) s += v[q][j][e];
+                }
+                s = group_sum_last<64>(s);
+                if (lane == 63) red[wave][q] = s;
+            }
+            __syncthreads();
+#pragma unroll
+            for (int q = 0; q < SG; q++) {
+                float t = 0.0f;
+#pragma unroll
+                for (int w = 0; w < kMfNT / 64; w++) t += red[w][q];
+                mu[q] = t / (float)J.K;
+            }
+            __syncthreads();
+#pragma unroll
+            for (int q = 0; q < SG; q++) {
+                float s = 0.0f;
+#pragma unroll
+                for (int j = 0; j < UO; j++) {
+                    if (tid + kMfNT * j >= NO) continue;
+#pragma unroll
+                    for (int e = 0; e < 8; e++) { const float d = v[q][j][e] - mu[q]; s += d * d; }
+                }
+                s = group_sum_last<64>(s);
+                if (lane == 63) red[wave][q] = s;
+            }
+            __syncthreads();
+#pragma unroll
+            for (int q = 0; q < SG; q++) {
+                float t = 0.0f;
+#pragma unroll
+                for (int w = 0; w < kMfNT / 64; w++) t += red[w][q];
+                inv[q] = 1.0f / sqrtf(t / (float)J.K + 1.0e-5f);
+            }
+            __syncthreads();
+#pragma unroll
+            for (int q = 0; q < SG; q++) {
+                const int b = b2 + q;
+#pragma unroll
+                for (int j = 0; j < UO; j++) {
+                    const int u = tid + kMfNT * j;
+                    const float gm[8] = {g0[j].x, g0[j].y, g0[j].z, g0[j].w, g1[j].x, g1[j].y, g1[j].z, g1[j].w};
+                    const float bt[8] = {e0[j].x, e0[j].y, e0[j].z, e0[j].w, e1[j].x, e1[j].y, e1[j].z, e1[j].w};
+                    const float cf[8] = {c0[j].x, c0[j].y, c0[j].z, c0[j].w, c1[j].x, c1[j].y, c1[j].z, c1[j].w};
+                    float l[8];
+#pragma unroll
+                    for (int e = 0; e < 8; e++) l[e] = (v[q][j][e] - mu[q]) * inv[q] * gm[e] + bt[e];
+                    if (wr_ln && b < nb && u < NO) {
+                        float4 *lp = (float4 *)(J.lnout + (size_t)b * J.ldx + 8 * u);
+                        lp[0] = make_float4(l[0], l[1], l[2], l[3]);
+                        lp[1] = make_float4(l[4], l[5], l[6], l[7]);
+                    }
+#pragma unroll
+                    for (int e = 0; e < 8; e++) v[q][j][e] = l[e] + cf[e] * (pv[q][j][e] - l[e]);
+                }
+            }
+        } else if (J.pro == PRO_MUL) {
+#pragma unroll
+            for (int q = 0; q < SG; q++)
+#pragma unroll
+                for (int j = 0; j < UO; j++)
+#pragma unroll
+                    for (int e = 0; e < 8; e++) v[q][j][e] *= pv[q][j][e];
+        } else if (J.pro == PRO_SIGMOID) {
+#pragma unroll
+            for (int q = 0; q < SG; q++)
+#pragma unroll
+                for (int j = 0; j < UO; j++)
+#pragma unroll
+                    for (int e = 0; e < 8; e++) v[q][j][e] = sigmoid_f(v[q][j][e]);
+        }
+        // fp16 rows into LDS; int8 unit sums over the 8 octets of each unit
+        // (8 consecutive lanes: quad sums, then the other quad by row_half_mirror)
+#pragma unroll
+        for (int q = 0; q < SG; q++) {
+            const int b = b2 + q;
+#pragma unroll
+            for (int j = 0; j < UO; j++) {
+                const int u = tid + kMfNT * j;
+                h8_t h;
+                float s = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    h[e] = (_Float16)v[q][j][e];
+                    s += (float)h[e];
+                }
+                if (b < nb && u < NO) *(h8_t *)(xs + b * kMfXS + 8 * u) = h;
+                if (i8) {
+                    s += gdpp<0xB1>(s);   // quad_perm 1,0,3,2
+                    s += gdpp<0x4E>(s);   // quad_perm 2,3,0,1
+                    s += gdpp<0x141>(s);  // row_half_mirror: the other quad of the 8
+                    if (b < nb && u < NO && !(u & 7)) dx[(u >> 3) * 16 + b] = s;
+                }
+            }
+        }
+    }
+}
+
+template <int FMT, int BT>
+__device__ __forceinline__ void gemv_mf_body(const GemvJob &J, int q, int batch, float *ws, _Float16 *xs, float *dx,
+                                             float *part, float (*red)[4]) {
+    constexpr int NW = kMfNT / 64;
+    const int nks = J.ks, nbs = J.nblk / nks, ks = q / nbs, rb = q - ks * nbs;
+    const int KS = J.K / nks, k0 = ks * KS, NS = KS * (FMT == FMT_I8 ? 1 : 2) / 64;  // units per row tile
+    const int rbeg = rb * J.rpb, rend = min(J.M, rbeg + J.rpb), TB = (rend - rbeg + 15) / 16;
+    const int tid = threadIdx.x, lane = tid & 63, n = lane & 15, g = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: the loop control stays scalar
+    // the wave's units: an even share of the block's TB*NS units, tile-major
+    const int U = TB * NS, ua = wave * U / NW, ub = (wave + 1) * U / NW, ta = ua / NS;
+    const size_t rowb = (size_t)J.K * (FMT == FMT_I8 ? 1 : 2);  // bytes per weight row
+    const unsigned char *W = (const unsigned char *)J.w + (size_t)k0 * (FMT == FMT_I8 ? 1 : 2) + 16 * g;
+    const int KG = J.K / 128;
+    // issue cursor: rows past the block's end (and units past the wave's end)
+    // re-read the last valid ones, so every load is unconditional
+    int it = ta, is = ua - ta * NS, iu = ua;
+    const unsigned char *wp = W + (size_t)min(rbeg + 16 * it + n, rend - 1) * rowb;
+    const uint32_t *sp = J.sz + (size_t)min(rbeg + 16 * it + n, rend - 1) * KG + k0 / 128;
+    auto issue = [&](u32x4 &wv, uint32_t &sv) {
+        wv = __builtin_nontemporal_load((const u32x4 *)(wp + 64 * is));
+        if (FMT == FMT_I8) sv = sp[is >> 1];
+        if (iu + 1 < ub) {
+            iu++;
+            if (++is == NS) {
+                is = 0;
+                it++;
+                const int row = min(rbeg + 16 * it + n, rend - 1);
+                wp = W + (size_t)row * rowb;
+                if (FMT == FMT_I8) sp = J.sz + (size_t)row * KG + k0 / 128;
+            }
+        }
+    };
+    u32x4 ring[kMfRing];
+    uint32_t szr[kMfRing];
+#pragma unroll
+    for (int p = 0; p < kMfRing; p++) issue(ring[p], szr[p]);
+    stage_x_mf<BT>(J, k0, KS, batch, J.lnout && q == 0, xs, dx, red);
+    __syncthreads();
+    const int xm = min(n, batch - 1);  // A row of lane: session n (rows past the batch repeat the last one)
+    const _Float16 *xrow = xs + xm * kMfXS + (FMT == FMT_I8 ? 16 : 8) * g;
+    int ct = ta, cs = ua - ta * NS, slot = 0;
+    f4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int u0 = ua; u0 < ub; u0 += kMfRing) {
+#pragma unroll
+        for (int p = 0; p < kMfRing; p++) {
+            const int u = u0 + p;
+            if (u >= ub) break;
+            const u32x4 w = ring[p];
+            if (FMT == FMT_I8) {
+                const h8_t xa = *(const h8_t *)(xrow + 64 * cs), xb = *(const h8_t *)(xrow + 64 * cs + 8);
+                const uint32_t s = szr[p];
+                const h8_t wa = __builtin_bit_cast(h8_t, (u32x4){q2h(w[0], 0), q2h(w[0], 1), q2h(w[1], 0), q2h(w[1], 1)});
+                const h8_t wb = __builtin_bit_cast(h8_t, (u32x4){q2h(w[2], 0), q2h(w[2], 1), q2h(w[3], 0), q2h(w[3], 1)});
+                f4_t d = {0.0f, 0.0f, 0.0f, 0.0f};
+                d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, wa, d, 0, 0, 0);
+                d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xb, wb, d, 0, 0, 0);
+                const f4_t dxv = *(const f4_t *)(dx + cs * 16 + 4 * g);
+                const float sc = h2f(s), zc = h2f(s >> 16) - 1024.0f * sc;
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc[i] = fmaf(sc, d[i], fmaf(zc, dxv[i], acc[i]));
+            } else {
+                const h8_t xa = *(const h8_t *)(xrow + 32 * cs);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, __builtin_bit_cast(h8_t, w), acc, 0, 0, 0);
+            }
+            issue(ring[p], szr[p]);
+            if (++cs == NS || u == ub - 1) {
+                // the wave's sum over tile ct (all of it or its share): D[session 4g+i][row n]
+                *(f4_t *)(part + ((wave * kMfSlots + slot) * 16 + n) * 16 + 4 * g) = acc;
+                acc = (f4_t){0.0f, 0.0f, 0.0f, 0.0f};
+                slot++;
+                if (cs == NS) { cs = 0; ct++; }
+            }
+        }
+    }
+    // every tile: the sums of the waves that cover it, in wave order
+    __syncthreads();
+    float *wsp = nks > 1 ? ws + J.wso + (size_t)ks * batch * J.M : nullptr;
+    for (int e = tid; e < TB * 256; e += kMfNT) {
+        const int t = e >> 8, nn = (e >> 4) & 15, b = e & 15, row = rbeg + 16 * t + nn;
+        if (b >= batch || row >= rend) continue;
+        int w = min(NW - 1, t * NS * NW / U);
+        while (w > 0 && (w * U / NW) > t * NS) w--;  // first wave with a unit of tile t
+        float v = 0.0f;
+        bool any = false;
+        for (; w < NW; w++) {
+            const int wa = w * U / NW, wb = (w + 1) * U / NW;
+            if (wa >= (t + 1) * NS) break;
+            if (wb <= t * NS || wa >= wb) continue;
+            const float pv = part[((w * kMfSlots + (t - wa / NS)) * 16 + nn) * 16 + b];
+            v = any ? v + pv : pv;
+            any = true;
+        }
+        if (wsp) wsp[(size_t)b * J.M + row] = v;
+        else apply_epi(J, row, b, v);
+    }
+}
+
+template <int BT>
+__global__ __launch_bounds__(kMfNT) void k_gemv_mb(GemvJobs jobs, int batch, float *ws) {
+    __shared__ __attribute__((aligned(16))) _Float16 xs[BT * kMfXS];
+    __shared__ __attribute__((aligned(16))) float dx[kMfKS / 64 * 16];
+    __shared__ __attribute__((aligned(16))) float part[kMfNT / 64 * kMfSlots * 256];
+    __shared__ float red[kMfNT / 64][4];
+    const int bid = blockIdx.x;
+    if (bid == 0 && jobs.side.src)
+        for (int i = threadIdx.x; i < batch * jobs.side.n; i += kMfNT) jobs.side.dst[i] = jobs.side.src[i];
+    int ji = 0;
+    while (ji + 1 < jobs.n && bid >= jobs.blk_start[ji + 1]) ji++;
+    const GemvJob &J = jobs.j[ji];
+    const int q = bid - jobs.blk_start[ji];
+    if (J.fmt == FMT_I8)
+        gemv_mf_body<FMT_I8, BT>(J, q, batch, ws, xs, dx, part, red);
+    else
+        gemv_mf_body<FMT_F16, BT>(J, q, batch, ws, xs, dx, part, red);
+}
+
+// y[b, row] (epilogue) of the k-sliced jobs: the slices' partial sums added
+// in slice order.
+__global__ __launch_bounds__(256) void k_gemv_mb_reduce(GemvJobs jobs, int batch, const float *ws) {
+    int ji = 0;
+    while (ji + 1 < jobs.n && (int)blockIdx.x >= jobs.blk_start[ji + 1]) ji++;
+    const GemvJob &J = jobs.j[ji];
+    const int i = (blockIdx.x - jobs.blk_start[ji]) * 256 + threadIdx.x;
+    if (J.ks <= 1 || i >= J.M * batch) return;
+    const int b = i / J.M, row = i - b * J.M;
+    const float *p = ws + J.wso + i;
+    float s = p[0];
+    for (int k = 1; k < J.ks; k++) s += p[(size_t)k * batch * J.M];
+    apply_epi(J, row, b, s);
+}
+
+static bool mb_disabled() {
+    const char *e = getenv("RSV_GEMV_MB");
+    return e && e[0] == '0';
+}
+
+// 2 <= batch <= 16 on k_gemv_mb.  Returns 1 when a job does not fit it.
+static int launch_mb(rsv_ctx *ctx, GemvJobs &jobs, int batch) {
+    if (batch > 16) return 1;
+    double total = 0.0;
+    double bytes[kMaxJobs];
+    for (int i = 0; i < jobs.n; i++) {
+        GemvJob &J = jobs.j[i];
+        const int nks = (J.K + kMfKS - 1) / kMfKS;
+        const int KS = J.K / nks;
+        if (J.K % nks || KS % (J.fmt == FMT_I8 ? 128 : 32) || J.pro == PRO_GNGATE || (J.pro == PRO_LNMIX && nks > 1))
+            return 1;
+        J.ks = nks;
+        bytes[i] = (double)J.M * J.K * (J.fmt == FMT_I8 ? 1.03125 : 2.0);
+        total += bytes[i];
+    }
+    const int cus = ctx->sm_count > 0 ? ctx->sm_count : 256;
+    const int target = cus;
+    int nblk = 0;
+    size_t wso = 0;
+    for (int i = 0; i < jobs.n; i++) {
+        GemvJob &J = jobs.j[i];
+        int per = (int)(target * bytes[i] / total / J.ks + 0.5);
+        per = std::max(1, std::min((J.M + 15) / 16, per));
+        // a wave covers TB/8 tiles + 1 boundary tile: at most kMfSlots
+        per = std::max(per, (J.M + 16 * 8 * (kMfSlots - 1) - 1) / (16 * 8 * (kMfSlots - 1)));
+        J.rpb = (J.M + per - 1) / per;
+        per = (J.M + J.rpb - 1) / J.rpb;
+        J.nblk = per * J.ks;
+        jobs.blk_start[i] = nblk;
+        nblk += J.nblk;
+        J.wso = wso;
+        if (J.ks > 1) wso += (size_t)J.ks * batch * J.M;
+    }
+    jobs.blk_start[jobs.n] = nblk;
+    if (wso > ctx->skinny_ws_cap) return RSV_FAIL("gemv: k-slice workspace too small (%zu floats)", wso);
+    const int bt = batch <= 2 ? 2 : batch <= 4 ? 4 : batch <= 8 ? 8 : 16;
+#define MB(BT) hipLaunchKernelGGL((k_gemv_mb<BT>), dim3(nblk), dim3(kMfNT), 0, ctx->stream, jobs, batch, ctx->skinny_ws)
+    if (bt == 2) MB(2);
+    else if (bt == 4) MB(4);
+    else if (bt == 8) MB(8);
+    else MB(16);
+#undef MB
+    RSV_HIP(hipGetLastError());
+    if (wso) {
+        GemvJobs rj = jobs;
+        int rb = 0;
+        for (int i = 0; i < rj.n; i++) {
+            rj.blk_start[i] = rb;
+            rb += rj.j[i].ks > 1 ? (rj.j[i].M * batch + 255) / 256 : 0;
+        }
+        rj.blk_start[rj.n] = rb;
+        hipLaunchKernelGGL(k_gemv_mb_reduce, dim3(rb), dim3(256), 0, ctx->stream, rj, batch, (const float *)ctx->skinny_ws);
+        RSV_HIP(hipGetLastError());
+    }
+    return 0;
+}
+
 // ---------------------------------------------------------------- B = 1
 // One-shot GEMV for one session: NT threads per block (NT/64 waves x 64/LPR
 // rows each).  Every vector load of the block (x and, for the LN-mix
@@ -742,6 +1133,10 @@ int launch_gemv_jobs(rsv_ctx *ctx, GemvJobs &jobs, int batch) {
     // B=1: the one-shot kernel (prologues inside it) where the jobs fit it
     if (batch == 1) {
         const int rc = launch_os2(ctx, jobs);
+        if (rc <= 0) return rc;
+    }
+    if (batch >= 2 && !mb_disabled()) {
+        const int rc = launch_mb(ctx, jobs, batch);
         if (rc <= 0) return rc;
     }
     for (int i = 0; i < jobs.n; i++)

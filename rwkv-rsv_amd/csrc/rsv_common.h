@@ -89,6 +89,8 @@ struct GemvJob {
     int nblk;      // blocks along M (filled by the launcher)
     int ks;        // k-slices per row (register-resident B=1 kernel; filled by the launcher)
     int lpr;       // lanes per row (one-shot B=1 kernel; filled by the launcher)
+    int rpb;       // rows per block (batched kernel; filled by the launcher)
+    size_t wso;    // offset of the job's k-slice partial sums in the workspace (batched kernel)
 };
 constexpr int kMaxJobs = 8;
 // A side copy done by the first block column of a launch: dst[b, :n] =
@@ -130,9 +132,6 @@ struct rsv_ctx {
     // with the context so that graph capture never allocates)
     float *skinny_ws = nullptr;
     size_t skinny_ws_cap = 0;
-    // arrival counters of the sparse ffn.value reduction (zeroed at create; each launch leaves them zero)
-    unsigned *sparse_cnt = nullptr;
-    size_t sparse_cnt_cap = 0;
 };
 
 namespace rsv {

@@ -122,28 +122,32 @@ def test_state_roundtrip_bit_exact(bundles):
 
 
 def test_batch_prefill_and_decode_match_single(bundles):
-    """forward_seq_batch over ragged prompts == per-session infer_seq; batch
-    argmax self-loop == per-session self-loops; slot back/load."""
-    b, _ = bundles["i8"]
+    """forward_seq_batch over ragged prompts against per-session infer_seq
+    (the batch's last-token rows run on the fp16-activation MFMA path, the
+    single session's on the fp32 GEMVs: 1e-3 apart), the batched argmax
+    self-loop against the oracle teacher-forced along it, slot back/load."""
+    b, m = bundles["i8"]
     lens = [5, 17, 1, 33]
     prompts = [_prompt(l, 10 + i) for i, l in enumerate(lens)]
     S = b.create_batch_state(len(lens))
     seeds, lg = b.forward_seq_batch(S, prompts, want_logits=True)
     assert list(seeds) == [int(p[-1]) for p in prompts]
-    singles = []
     for i, p in enumerate(prompts):
         b.reset()
         lg1 = b.infer_seq(p)
-        singles.append(b.state_back())
-        assert rel_rmse(lg[i], lg1) <= 1e-5
-        assert rel_rmse(S.slot_back(i), singles[-1]) <= 1e-5
-    n = 12
+        assert rel_rmse(lg[i], lg1) <= 1e-3
+        assert rel_rmse(S.slot_back(i), b.state_back()) <= 1e-3
+    n = 40
     out = b.argmax_selfloop_batch(S, seeds, n)
+    agree = 0
     for i, p in enumerate(prompts):
-        b.reset()
-        b.state_load(singles[i])
-        one = b.infer_argmax_selfloop(int(seeds[i]), n)
-        assert np.array_equal(out[i], one), i
+        st = m.init_state()
+        m.forward(p[:-1], st)
+        prev = int(seeds[i])
+        for t in range(n):
+            agree += orc.argmax(m.forward([prev], st)) == out[i, t]
+            prev = int(out[i, t])
+    assert agree / (n * len(prompts)) >= 0.98
     # slot round trip and bounds
     data = S.slot_back(2)
     S.slot_load(0, data)
@@ -262,27 +266,27 @@ def test_fused_decode_matches_trait_op_sequence(bundles, kind, monkeypatch):
     assert rel_rmse(s_fused, s_ops) <= 1e-5
 
 
-@pytest.mark.parametrize("kind,bar", [("f32", 0.98), ("i8", 0.98)])
-def test_batch_matrix_core_decode(bundles, kind, bar):
-    """B >= 16 runs the decode GEMMs on MFMA with fp16 activations: logits and
+@pytest.mark.parametrize("kind,bar,B", [("f32", 0.98, 20), ("i8", 0.98, 20), ("i8", 0.98, 2), ("f32", 0.98, 5),
+                                        ("i8", 0.98, 8), ("i8", 0.98, 15)])
+def test_batch_matrix_core_decode(bundles, kind, bar, B):
+    """B >= 2 runs the decode GEMMs on MFMA with fp16 activations: logits and
     states meet the RMSE bound against the oracle, and the batched argmax
     self-loop agrees teacher-forced with the oracle."""
     b, m = bundles[kind]
-    B = 20
     S = b.create_batch_state(B)
     prompts = [_prompt(3 + (i % 5), 40 + i) for i in range(B)]
     seeds = b.forward_seq_batch(S, prompts)
     snap = S.back()
     toks = np.array([(7 * i + 3) % SMALL["vocab"] for i in range(B)], np.uint32)
     lg = b.forward_tokens_batch(S, toks)
-    for i in range(0, B, 7):
+    for i in sorted(set(range(0, B, 7)) | {B - 1}):
         st = m.init_state()
         m.forward(prompts[i], st)
         want = m.forward([int(toks[i])], st)
         assert rel_rmse(lg[i], want) <= RMSE_BOUND
         assert rel_rmse(S.slot_back(i), st) <= RMSE_BOUND
     S.load(snap)
-    n = 12
+    n = max(12, 240 // B)  # about 240 teacher-forced tokens per case
     out = b.argmax_selfloop_batch(S, seeds, n)
     agree = total = 0
     for i in range(B):

@@ -57,6 +57,14 @@ def test_dequant_bit_exact(be):
 
 
 # ------------------------------------------------------------- GEMV
+def _act(batch):
+    """Activations as the batched GEMV multiplies them: 2..16 sessions run on
+    fp16 activations (MFMA), 1 and >= 17 on the fp32 values."""
+    if 2 <= batch <= 16:
+        return lambda a: np.asarray(a, np.float32).astype(np.float16).astype(np.float64)
+    return lambda a: np.asarray(a, np.float64)
+
+
 def _int8_weight(rng, m, k):
     import synth
     w = rng.standard_normal((m, k)).astype(np.float32) * 0.02
@@ -94,14 +102,19 @@ def test_gemv_epilogues_and_batch_tails(be, batch):
     xt, gt = be.tensor(x), be.tensor(g)
     Wd = W.astype(np.float64)
     Wh = W16.astype(np.float64)
+    # 2..16 sessions run the MFMA GEMV on fp16 activations (the reference's
+    # GEMVs also take x in fp16): the reference product uses x (or x*g)
+    # rounded to fp16, 1 and >= 17 sessions the fp32 x
+    r16 = (lambda a: a.astype(np.float16).astype(np.float64)) if 2 <= batch <= 16 else (lambda a: a)
+    xr, xg = r16(x), r16(x * g)
     cases = [
-        ("rsv_gemv_int8_relu2", (ctypes.byref(h), xt), lambda: np.maximum(x @ Wd.T, 0) ** 2, None),
-        ("rsv_gemv_int8_add", (ctypes.byref(h), xt), lambda: y0 + x @ Wd.T, y0),
-        ("rsv_gemv_int8_mul_add", (ctypes.byref(h), xt, gt), lambda: y0 + (x * g) @ Wd.T, y0),
-        ("rsv_gemv_f16", (w16, xt), lambda: x @ Wh.T, None),
-        ("rsv_gemv_f16_relu2", (w16, xt), lambda: np.maximum(x @ Wh.T, 0) ** 2, None),
-        ("rsv_gemv_f16_add", (w16, xt), lambda: y0 + x @ Wh.T, y0),
-        ("rsv_gemv_f16_mul_add", (w16, xt, gt), lambda: y0 + (x * g) @ Wh.T, y0),
+        ("rsv_gemv_int8_relu2", (ctypes.byref(h), xt), lambda: np.maximum(xr @ Wd.T, 0) ** 2, None),
+        ("rsv_gemv_int8_add", (ctypes.byref(h), xt), lambda: y0 + xr @ Wd.T, y0),
+        ("rsv_gemv_int8_mul_add", (ctypes.byref(h), xt, gt), lambda: y0 + xg @ Wd.T, y0),
+        ("rsv_gemv_f16", (w16, xt), lambda: xr @ Wh.T, None),
+        ("rsv_gemv_f16_relu2", (w16, xt), lambda: np.maximum(xr @ Wh.T, 0) ** 2, None),
+        ("rsv_gemv_f16_add", (w16, xt), lambda: y0 + xr @ Wh.T, y0),
+        ("rsv_gemv_f16_mul_add", (w16, xt, gt), lambda: y0 + xg @ Wh.T, y0),
     ]
     for name, args, ref, init in cases:
         yt = be.tensor(init if init is not None else np.zeros((batch, m), np.float32))
@@ -146,7 +159,8 @@ def test_stage1_and_chain4(be, batch):
     be.call("rsv_gemv_int8_rkv_stage1_batch", ctypes.byref(hs[0]), ctypes.byref(hs[1]), ctypes.byref(hs[2]),
             t1["v"], t1["w"], t1["a"], t1["g"], xt["r"], xt["k"], xt["v"], xt["w"], xt["a"], xt["g"],
             out["r"], out["k"], out["v"], mids["v"], mids["w"], mids["a"], mids["g"], C, vm, wm, am, gm, batch)
-    X = {n: a.astype(np.float64) for n, a in xs.items()}
+    act = _act(batch)
+    X = {n: act(a) for n, a in xs.items()}
     for j, n in enumerate("rkv"):
         assert rel_err(be.get(out[n], batch * C).reshape(batch, C), X[n] @ Ws[j][2].astype(np.float64).T) < 5e-5
     M = {}
@@ -170,11 +184,11 @@ def test_stage1_and_chain4(be, batch):
             C, wm, am, vm, gm, batch)
     sig = lambda t: 1 / (1 + np.exp(-t))
     P = lambda n: L2[n].astype(np.float64).T
-    want_w = np.exp(sc * sig(M["w"] @ P("w") + w0))
-    want_a = sig(M["a"] @ P("a") + a0)
-    gate = sig(M["v"] @ P("v") + v0)
+    want_w = np.exp(sc * sig(act(M["w"]) @ P("w") + w0))
+    want_a = sig(act(M["a"]) @ P("a") + a0)
+    gate = sig(act(M["v"]) @ P("v") + v0)
     want_v = v_in + gate * (vfirst - v_in)
-    want_g = sig(M["g"]) @ P("g")
+    want_g = act(sig(M["g"])) @ P("g")
     for n, want in (("w", want_w), ("a", want_a), ("g", want_g)):
         assert rel_err(be.get(ids[n], batch * C).reshape(batch, C), want) < 5e-5, n
     assert rel_err(be.get(out["v"], batch * C).reshape(batch, C), want_v) < 5e-5
@@ -854,7 +868,7 @@ def test_gemv_multi_lnmix_and_side_copy(be, batch):
     for q in range(batch):
         ln = orc.layer_norm(x[q], gam, bet)
         mix = ln + coef * (prev[q] - ln)
-        assert rel_err(got[q], mix.astype(np.float64) @ W.astype(np.float64).T) < 5e-5
+        assert rel_err(got[q], _act(batch)(mix) @ W.astype(np.float64).T) < 5e-5
         assert rel_err(be.get(ids["ln"], batch * C).reshape(batch, C)[q], ln) < 1e-5
     assert np.array_equal(be.get(ids["y2"], batch * M), be.get(ids["y"], batch * M))
     # the side copy moves the previous launch's LN rows (the state write is
