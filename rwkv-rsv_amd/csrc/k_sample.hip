@@ -1,5 +1,8 @@
 // On-GPU sampler: penalties -> 1/T -> top-k -> softmax -> top-p -> seeded
-// draw, one 1024-thread block per session row.
+// draw.  Rows without top-k and with 0 < top_p < 1 (the serving case) run on
+// three launches spread over the chip (k_samp_scale / k_samp_exp /
+// k_samp_pick, below); every other row runs the whole pipeline on one
+// 1024-thread block.
 //
 // Observable behaviour follows backend_cuda.rs:3690-4009:
 //  - sampler row [T, top_k bits, top_p, seed bits, rep, freq, pres, hist_len bits]
@@ -333,13 +336,12 @@ __device__ __forceinline__ float fkey_inv(uint32_t k) {
     return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
 }
 
-__global__ __launch_bounds__(kSampBS) void k_sample(const float *__restrict__ logits, uint32_t *__restrict__ token,
-                                                    int n, float *__restrict__ temp_all,
-                                                    uint32_t *__restrict__ counter_all,
-                                                    const float *__restrict__ sampler,
-                                                    const uint32_t *__restrict__ hist_all, int hist_stride) {
-    __shared__ SampShared sh;
-    const int b = blockIdx.x, tid = threadIdx.x;
+// The whole pipeline for row b of any length, on the row in global memory.
+__device__ void sample_row_general(int b, const float *__restrict__ logits, uint32_t *__restrict__ token, int n,
+                                   float *__restrict__ temp_all, uint32_t *__restrict__ counter_all,
+                                   const float *__restrict__ sampler, const uint32_t *__restrict__ hist_all,
+                                   int hist_stride, SampShared &sh) {
+    const int tid = threadIdx.x;
     const float *lg = logits + (size_t)b * n;
     float *temp = temp_all + (size_t)b * n;
     const float *sp = sampler + (size_t)b * 8;
@@ -552,13 +554,11 @@ __global__ __launch_bounds__(kSampBS) void k_sample(const float *__restrict__ lo
 // candidates' probabilities are the inverse of their sort keys (exact).
 // Every step computes what k_sample computes, in the same order.
 template <int PER>
-__global__ __launch_bounds__(kSampBS) void k_sample_regs(const float *__restrict__ logits, uint32_t *__restrict__ token,
-                                                         int n, float *__restrict__ temp_all,
-                                                         uint32_t *__restrict__ counter_all,
-                                                         const float *__restrict__ sampler,
-                                                         const uint32_t *__restrict__ hist_all, int hist_stride) {
-    __shared__ SampShared sh;
-    const int b = blockIdx.x, tid = threadIdx.x;
+__device__ void sample_row_regs(int b, const float *__restrict__ logits, uint32_t *__restrict__ token, int n,
+                                float *__restrict__ temp_all, uint32_t *__restrict__ counter_all,
+                                const float *__restrict__ sampler, const uint32_t *__restrict__ hist_all,
+                                int hist_stride, SampShared &sh) {
+    const int tid = threadIdx.x;
     const float *lg = logits + (size_t)b * n;
     float *temp = temp_all + (size_t)b * n;
     const float *sp = sampler + (size_t)b * 8;
@@ -787,6 +787,609 @@ __global__ __launch_bounds__(kSampBS) void k_sample_regs(const float *__restrict
     }
 }
 
+__global__ __launch_bounds__(kSampBS) void k_sample(const float *__restrict__ logits, uint32_t *__restrict__ token,
+                                                    int n, float *__restrict__ temp_all,
+                                                    uint32_t *__restrict__ counter_all,
+                                                    const float *__restrict__ sampler,
+                                                    const uint32_t *__restrict__ hist_all, int hist_stride) {
+    __shared__ SampShared sh;
+    sample_row_general(blockIdx.x, logits, token, n, temp_all, counter_all, sampler, hist_all, hist_stride, sh);
+}
+
+template <int PER>
+__global__ __launch_bounds__(kSampBS) void k_sample_regs(const float *__restrict__ logits, uint32_t *__restrict__ token,
+                                                         int n, float *__restrict__ temp_all,
+                                                         uint32_t *__restrict__ counter_all,
+                                                         const float *__restrict__ sampler,
+                                                         const uint32_t *__restrict__ hist_all, int hist_stride) {
+    __shared__ SampShared sh;
+    sample_row_regs<PER>(blockIdx.x, logits, token, n, temp_all, counter_all, sampler, hist_all, hist_stride, sh);
+}
+
+// ------------------------------------------------ multi-CU top-p sampling
+// The configs' serving case (no top-k, 0 < top_p < 1) spread over the chip,
+// in three launches per batch of rows; the draws are the ones the
+// one-block pipeline makes (the same operations in the same order):
+//   k_samp_scale (n/1024 blocks per row): penalties, 1/T -> temp; block maxima;
+//   k_samp_exp   (n/1024 blocks per row): m = the row maximum, e = exp(l - m)
+//                -> temp; a 4096-bin histogram of the keys of e (their top
+//                12 bits) in global memory;
+//   k_samp_pick  (one block per row): the bin holding the 512-th largest e;
+//                one pass over e that takes the softmax total in the
+//                112-lane order (backend_cuda.rs:3880-3921) and gathers the
+//                elements of that bin and above (and the bin below, which
+//                holds any element whose probability can round to a tie
+//                with the 512-th); p = e / total for those only; the 512
+//                largest p by radix select + rank sort, the sequential top-p
+//                accumulation, the kept set in index order, its 112-lane sum
+//                (zero entries add nothing) and the CDF draw.
+// A row outside this case (top-k, top_p outside (0, 1)), or with more than
+// kPickMax gathered candidates, runs the one-block pipeline from its logits
+// inside k_samp_pick.
+constexpr int kPickMax = 4096;
+constexpr int kSampHistBins = 4096;
+constexpr int kSampMinN = kSampHistBins + 64 + 1024;  // rows long enough for the work words carved below
+
+// per-row work words inside `counter_all` (n u32 per row): block maxima [64..], histogram [4096]
+__device__ __forceinline__ uint32_t *samp_hist(uint32_t *counter_all, int b, int n) { return counter_all + (size_t)b * n; }
+__device__ __forceinline__ float *samp_pmax(uint32_t *counter_all, int b, int n) {
+    return (float *)(counter_all + (size_t)b * n + kSampHistBins);
+}
+
+__device__ __forceinline__ bool samp_multi_case(const float *sp, int n) {
+    const uint32_t top_k = __float_as_uint(sp[1]);
+    const float top_p = sp[2];
+    return (top_k == 0u || top_k >= (uint32_t)n) && top_p > 0.0f && top_p < 1.0f;
+}
+
+__global__ __launch_bounds__(1024) void k_samp_scale(const float *__restrict__ logits, int n, float *__restrict__ temp_all,
+                                                     uint32_t *__restrict__ counter_all,
+                                                     const float *__restrict__ sampler,
+                                                     const uint32_t *__restrict__ hist_all, int hist_stride) {
+    __shared__ uint32_t cnt[1024];
+    __shared__ float red[16];
+    const int b = blockIdx.y, blk = blockIdx.x, tid = threadIdx.x;
+    const float *sp = sampler + (size_t)b * 8;
+    if (!samp_multi_case(sp, n)) return;
+    const int base = blk * 1024, i = base + tid;
+    const float temperature = sp[0];
+    const float rep = sp[4], freq = sp[5], pres = sp[6];
+    const uint32_t hist_len = min(__float_as_uint(sp[7]), (uint32_t)max(hist_stride, 0));
+    float l = i < n ? logits[(size_t)b * n + i] : -1e30f;
+    if (blk == 0) {  // the row's histogram, filled by the next launch
+        uint32_t *h = samp_hist(counter_all, b, n);
+        for (int q = tid; q < kSampHistBins; q += 1024) h[q] = 0u;
+    }
+    if (hist_len > 0u && hist_all && (rep != 1.0f || freq != 0.0f || pres != 0.0f)) {
+        // occurrences of this block's tokens in the history (the counter of backend_cuda.rs:3700-3720)
+        cnt[tid] = 0u;
+        __syncthreads();
+        const uint32_t *hist = hist_all + (size_t)b * hist_stride;
+        for (uint32_t h = tid; h < hist_len; h += 1024) {
+            const uint32_t tk = hist[h];
+            if (tk >= (uint32_t)base && tk < (uint32_t)min(n, base + 1024)) atomicAdd(&cnt[tk - base], 1u);
+        }
+        __syncthreads();
+        const uint32_t c = cnt[tid];
+        if (c > 0u) {
+            if (rep != 1.0f) l = l > 0.0f ? l / rep : l * rep;
+            if (pres != 0.0f) l -= pres;
+        }
+        if (freq != 0.0f) l -= freq * (float)c;
+    }
+    float invT = 1.0f / temperature;
+    if (!(temperature > 0.0f)) invT = 1.0f;
+    l *= invT;
+    if (i < n) temp_all[(size_t)b * n + i] = l;
+    float m = wave_max_last(i < n ? l : -1e30f);
+    if ((tid & 63) == 63) red[tid >> 6] = m;
+    __syncthreads();
+    if (tid == 0) {
+        float mm = red[0];
+        for (int w = 1; w < 16; w++) mm = fmaxf(mm, red[w]);
+        samp_pmax(counter_all, b, n)[blk] = mm;
+    }
+}
+
+__global__ __launch_bounds__(1024) void k_samp_exp(int n, float *__restrict__ temp_all, uint32_t *__restrict__ counter_all,
+                                                   const float *__restrict__ sampler) {
+    __shared__ uint32_t hb[kSampHistBins];
+    __shared__ float mrow;
+    const int b = blockIdx.y, blk = blockIdx.x, tid = threadIdx.x, nb = gridDim.x;
+    if (!samp_multi_case(sampler + (size_t)b * 8, n)) return;
+    for (int q = tid; q < kSampHistBins; q += 1024) hb[q] = 0u;
+    if (tid < 64) {
+        const float *pm = samp_pmax(counter_all, b, n);
+        float m = -1e30f;
+        for (int q = tid; q < nb; q += 64) m = fmaxf(m, pm[q]);
+        m = wave_max_last(m);
+        if (tid == 63) mrow = m;
+    }
+    __syncthreads();
+    const int i = blk * 1024 + tid;
+    if (i < n) {
+        float *t = temp_all + (size_t)b * n;
+        const float e = expf(t[i] - mrow);
+        t[i] = e;
+        atomicAdd(&hb[fkey(e) >> 20], 1u);
+    }
+    __syncthreads();
+    uint32_t *h = samp_hist(counter_all, b, n);
+    for (int q = tid; q < kSampHistBins; q += 1024)
+        if (hb[q]) atomicAdd(&h[q], hb[q]);
+}
+
+struct PickShared {
+    union {
+        float chunk[16384];  // one streamed piece of e
+        SampShared sh;       // the radix select / fallback pipeline
+        struct {
+            uint32_t bits[8192];  // kept-set bitmap (rows up to 262,144)
+            uint32_t wpre[8192];  // kept entries before each word
+        } bm;
+    };
+    uint64_t comp[kCand];    // the R largest: key << 32 | ~index
+    float psort[kCand];      // their p, sorted (p desc, index asc)
+    uint32_t sh_scan[1024];
+    double dred[1024];
+    uint32_t lcnt[112], loff[112], lcur[112];
+    double dtot;
+    int flat, chosen;
+    float ce[kPickMax];      // gathered candidates: e, then p; at the end the kept set in index order
+    int ci[kPickMax];
+    union {
+        uint32_t fh[8192];   // fine histogram of the boundary bins
+        struct {
+            float kp[kPickMax];  // the kept set (p >= cut) as found
+            int ki[kPickMax];
+        };
+    };
+    float part[112];
+    uint32_t bsum[1024];
+    uint32_t ncand, ndef, ngt, neq, nsel, nkeep, bin;
+    int overflow;
+    float total, cut, tot2;
+};
+
+template <int PER>
+__global__ __launch_bounds__(1024) void k_samp_pick(const float *__restrict__ logits, uint32_t *__restrict__ token,
+                                                    int n, float *__restrict__ temp_all,
+                                                    uint32_t *__restrict__ counter_all,
+                                                    const float *__restrict__ sampler,
+                                                    const uint32_t *__restrict__ hist_all, int hist_stride) {
+    __shared__ PickShared ps;
+    const int b = blockIdx.x, tid = threadIdx.x;
+    const float *sp = sampler + (size_t)b * 8;
+    auto fallback = [&]() {
+        if constexpr (PER > 0)
+            sample_row_regs<PER>(b, logits, token, n, temp_all, counter_all, sampler, hist_all, hist_stride, ps.sh);
+        else
+            sample_row_general(b, logits, token, n, temp_all, counter_all, sampler, hist_all, hist_stride, ps.sh);
+    };
+    if (!samp_multi_case(sp, n)) {
+        fallback();
+        return;
+    }
+    const float top_p = sp[2];
+    const uint32_t seed = __float_as_uint(sp[3]);
+    const int R = n < kCand ? n : kCand;
+    const float *e_row = temp_all + (size_t)b * n;
+    // 1. the bin of the R-th largest key: bins from the top, 4 per thread
+    {
+        const uint32_t *h = samp_hist(counter_all, b, n);
+        const int q0 = kSampHistBins - 4 - 4 * tid;  // thread 0 holds the top bins
+        uint32_t hv[4], s = 0;
+#pragma unroll
+        for (int e = 0; e < 4; e++) { hv[e] = h[q0 + e]; s += hv[e]; }
+        ps.sh.cnt_gt[tid] = s;
+        __syncthreads();
+        block_exscan(ps.sh.cnt_gt, ps.sh);
+        uint32_t above = ps.sh.cnt_gt[tid];
+#pragma unroll
+        for (int e = 3; e >= 0; e--) {
+            if (above < (uint32_t)R && above + hv[e] >= (uint32_t)R) ps.bin = (uint32_t)(q0 + e);
+            above += hv[e];
+        }
+        if (tid == 0) { ps.ncand = 0u; ps.ndef = 0u; ps.overflow = 0; }
+        __syncthreads();
+    }
+    // 2. pass 1 over e: the 112-lane sums, the elements of the bins above
+    // the boundary (fewer than R: all of them are taken), and a histogram of
+    // the next 12 key bits of the elements in the boundary bin and the one
+    // below it
+    const uint32_t bin = ps.bin, lowbin = bin > 0u ? bin - 1u : 0u;
+    for (int q = tid; q < 8192; q += 1024) ps.fh[q] = 0u;
+    float s112 = 0.0f;
+    float4 cur[4];
+    auto load_piece = [&](int c0) {
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int i = c0 + 4096 * q + 4 * tid;
+            if (i + 3 < n) {
+                cur[q] = *(const float4 *)(e_row + i);
+            } else {
+                cur[q].x = i < n ? e_row[i] : 0.0f;
+                cur[q].y = i + 1 < n ? e_row[i + 1] : 0.0f;
+                cur[q].z = i + 2 < n ? e_row[i + 2] : 0.0f;
+                cur[q].w = i + 3 < n ? e_row[i + 3] : 0.0f;
+            }
+        }
+    };
+    auto take = [&](float ev, int i) {
+        const uint32_t slot = atomicAdd(&ps.ncand, 1u);
+        if (slot < (uint32_t)kPickMax) { ps.ce[slot] = ev; ps.ci[slot] = i; }
+    };
+    load_piece(0);
+    for (int c0 = 0; c0 < n; c0 += 16384) {
+        __syncthreads();  // the previous piece's sums are done with ps.chunk
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            *(float4 *)(ps.chunk + 4096 * q + 4 * tid) = cur[q];
+            const float ev[4] = {cur[q].x, cur[q].y, cur[q].z, cur[q].w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int i = c0 + 4096 * q + 4 * tid + e;
+                const uint32_t kk = fkey(ev[e]), cb = kk >> 20;
+                if (i >= n || cb < lowbin) continue;
+                take(ev[e], i);
+                if (cb > bin) atomicAdd(&ps.ndef, 1u);
+                else atomicAdd(&ps.fh[((cb - lowbin) << 12) | ((kk >> 8) & 0xFFFu)], 1u);
+            }
+        }
+        __syncthreads();
+        if (c0 + 16384 < n) load_piece(c0 + 16384);  // in flight while the lanes add
+        if (tid < 112) {
+            const int hi = min(n, c0 + 16384);
+            int i = c0 + (((tid - c0) % 112) + 112) % 112;
+            for (; i + 7 * 112 < hi; i += 8 * 112) {
+                float v[8];
+#pragma unroll
+                for (int e = 0; e < 8; e++) v[e] = ps.chunk[i + 112 * e - c0];
+#pragma unroll
+                for (int e = 0; e < 8; e++) s112 += v[e];
+            }
+            for (; i < hi; i += 112) s112 += ps.chunk[i - c0];
+        }
+    }
+    if (tid < 112) ps.part[tid] = s112;
+    __syncthreads();
+    if (tid == 0) {
+        for (int q = 0; q < 48; q++) ps.part[q] += ps.part[q + 64];
+        for (int step = 32; step > 0; step >>= 1)
+            for (int q = 0; q < step; q++) ps.part[q] += ps.part[q + step];
+        ps.total = ps.part[0];
+    }
+    // 3. the fine bin of the R-th largest: R - (taken so far) from the top of
+    // the 8192 fine bins, 8 per thread
+    {
+        const uint32_t need = (uint32_t)R - ps.ndef;
+        const int q0 = 8192 - 8 - 8 * tid;
+        uint32_t hv[8], s = 0;
+#pragma unroll
+        for (int e = 0; e < 8; e++) { hv[e] = ps.fh[q0 + e]; s += hv[e]; }
+        ps.sh.cnt_gt[tid] = s;
+        __syncthreads();
+        block_exscan(ps.sh.cnt_gt, ps.sh);
+        uint32_t above = ps.sh.cnt_gt[tid];
+#pragma unroll
+        for (int e = 7; e >= 0; e--) {
+            if (above < need && above + hv[e] >= need) ps.bin = (uint32_t)(q0 + e);
+            above += hv[e];
+        }
+        __syncthreads();
+    }
+    // 4. the candidates: the elements above the boundary bin and those of
+    // the fine bin of the R-th largest and above (and of the fine bin below,
+    // which holds any element whose probability can round to a tie with the
+    // R-th).  Pass 1 gathered both boundary bins whole: pruned in place when
+    // they fit, else gathered again by a second pass over e.
+    const uint32_t k24lo = (lowbin << 12) + (ps.bin > 0u ? ps.bin - 1u : 0u), k24hi = ((bin + 1u) << 12);
+    auto wanted = [&](float ev) {
+        const uint32_t kk = fkey(ev);
+        return (kk >> 20) > bin || ((kk >> 8) >= k24lo && (kk >> 8) < k24hi);
+    };
+    if (ps.ncand <= (uint32_t)kPickMax) {
+        constexpr int KPT = kPickMax / 1024;
+        const int C0 = (int)ps.ncand;
+        float pe[KPT];
+        int pi[KPT];
+#pragma unroll
+        for (int m = 0; m < KPT; m++) {
+            const int c = tid + 1024 * m;
+            pe[m] = c < C0 ? ps.ce[c] : 0.0f;
+            pi[m] = c < C0 ? ps.ci[c] : -1;
+        }
+        __syncthreads();
+        if (tid == 0) ps.ncand = 0u;
+        __syncthreads();
+#pragma unroll
+        for (int m = 0; m < KPT; m++)
+            if (pi[m] >= 0 && wanted(pe[m])) take(pe[m], pi[m]);
+    } else {
+        __syncthreads();
+        if (tid == 0) ps.ncand = 0u;
+        __syncthreads();
+        for (int c0 = 0; c0 < n; c0 += 16384) {
+            load_piece(c0);
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const float ev[4] = {cur[q].x, cur[q].y, cur[q].z, cur[q].w};
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int i = c0 + 4096 * q + 4 * tid + e;
+                    if (i < n && wanted(ev[e])) take(ev[e], i);
+                }
+            }
+        }
+    }
+    __syncthreads();
+    if (tid == 0) ps.overflow = ps.ncand > (uint32_t)kPickMax;
+    __syncthreads();
+    if (ps.overflow) {
+        fallback();
+        return;
+    }
+    const float total = ps.total;
+    const int C = (int)ps.ncand;
+    // 3. p of the candidates and the key of the R-th largest (radix select)
+    for (int c = tid; c < C; c += 1024) {
+        float p = ps.ce[c];
+        if (total > 0.0f) p /= total;
+        ps.ce[c] = p;
+    }
+    __syncthreads();
+    uint32_t prefix = 0, mask = 0, remaining = (uint32_t)R;
+    for (int pass = 0; pass < 4; pass++) {
+        const int shift = 24 - 8 * pass;
+        radix_clear(ps.sh);
+        for (int c0 = 0; c0 < C; c0 += 1024) {
+            const int c = c0 + tid;
+            const uint32_t kk = c < C ? fkey(ps.ce[c]) : 0u;
+            radix_count(kk, c < C && (kk & mask) == prefix, shift, pass == 0, ps.sh);
+        }
+        radix_pick(remaining, ps.sh);
+        prefix |= ps.sh.sel_bin << shift;
+        mask |= 255u << shift;
+        remaining = ps.sh.sel_rem;
+        __syncthreads();
+    }
+    const uint32_t kthr = prefix;
+    // 4. top-p's cut.  The sum of the R largest p in double (the ties at
+    // the threshold all have its p): when it is below top_p by more than the
+    // sequential fp32 rounding can move it, the sequential pass over the
+    // sorted list never stops early and its cut is the R-th largest p, with
+    // no sort.  Otherwise the R largest are sorted (composite keys key << 32
+    // | ~index, ranked) and the pass runs as written.
+    {
+        double ds = 0.0;
+        uint32_t g = 0;
+        for (int c = tid; c < C; c += 1024) {
+            const uint32_t kk = fkey(ps.ce[c]);
+            if (kk > kthr) { ds += (double)ps.ce[c]; g++; }
+        }
+        ps.dred[tid] = ds;
+        ps.sh_scan[tid] = g;
+        __syncthreads();
+        if (tid < 64) {
+            double t = 0.0;
+            uint32_t gg = 0;
+            for (int q = tid; q < 1024; q += 64) { t += ps.dred[q]; gg += ps.sh_scan[q]; }
+            for (int d = 32; d > 0; d >>= 1) {
+                t += __shfl_xor(t, d);
+                gg += __shfl_xor(gg, d);
+            }
+            if (tid == 0) {
+                const double pr = (double)fkey_inv(kthr);
+                ps.dtot = t + (double)(R - (int)gg) * pr;
+                ps.flat = ps.dtot < (double)top_p - 1e-4;
+                ps.cut = fkey_inv(kthr);
+            }
+        }
+        __syncthreads();
+    }
+    if (!ps.flat) {
+        if (tid == 0) { ps.ngt = 0u; ps.neq = 0u; ps.nsel = 0u; }
+        __syncthreads();
+        for (int c = tid; c < C; c += 1024) {
+            const uint32_t kk = fkey(ps.ce[c]);
+            if (kk > kthr) ps.comp[atomicAdd(&ps.ngt, 1u)] = ((uint64_t)kk << 32) | (uint32_t)~ps.ci[c];
+            else if (kk == kthr) ps.ki[atomicAdd(&ps.neq, 1u)] = ps.ci[c];
+        }
+        __syncthreads();
+        {
+            const int G = (int)ps.ngt, T = (int)ps.neq, take = R - G;
+            for (int t = tid; t < T; t += 1024) {
+                const int ii = ps.ki[t];
+                int before = 0;  // ties with a smaller index
+                if (take < T)
+                    for (int j = 0; j < T; j++) before += ps.ki[j] < ii;
+                if (before < take) ps.comp[G + atomicAdd(&ps.nsel, 1u)] = ((uint64_t)kthr << 32) | (uint32_t)~ii;
+            }
+        }
+        __syncthreads();
+        for (int r = tid; r < R; r += 1024) {
+            const uint64_t cv = ps.comp[r];
+            int rank = 0;
+            for (int j0 = 0; j0 < R; j0 += 16) {
+                uint64_t w[16];
+#pragma unroll
+                for (int e = 0; e < 16; e++) w[e] = j0 + e < R ? ps.comp[j0 + e] : 0ull;
+#pragma unroll
+                for (int e = 0; e < 16; e++) rank += w[e] > cv;
+            }
+            ps.psort[rank] = fkey_inv((uint32_t)(cv >> 32));
+        }
+        __syncthreads();
+        // the sequential pass on wave 0 (values broadcast by readlane)
+        if (tid < 64) {
+            float vals[kCand / 64];
+#pragma unroll
+            for (int m = 0; m < kCand / 64; m++) vals[m] = tid + 64 * m < R ? ps.psort[tid + 64 * m] : 0.0f;
+            float cum = 0.0f, cut = 0.0f;
+#pragma unroll
+            for (int m = 0; m < kCand / 64; m++) {
+                const int cnt = min(64, R - 64 * m);
+                for (int q = 0; q < cnt && cum < top_p; q++) {
+                    const float v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(vals[m]), q));
+                    cum += v;
+                    cut = v;
+                }
+            }
+            if (tid == 0) ps.cut = cut;
+        }
+    }
+    // 6. the kept entries (p >= cut; every one is a candidate) in index
+    // order: a bitmap over the row, word prefix counts, each entry's place
+    const int NWD = (n + 31) / 32;
+    for (int w = tid; w < NWD; w += 1024) ps.bm.bits[w] = 0u;
+    __syncthreads();
+    const float cut = ps.cut;
+    for (int c = tid; c < C; c += 1024)
+        if (ps.ce[c] >= cut) atomicOr(&ps.bm.bits[ps.ci[c] >> 5], 1u << (ps.ci[c] & 31));
+    __syncthreads();
+    {
+        const int per = (NWD + 1023) / 1024, w0 = tid * per;
+        uint32_t s = 0;
+        for (int w = w0; w < min(NWD, w0 + per); w++) s += __popc(ps.bm.bits[w]);
+        ps.sh_scan[tid] = s;
+        __syncthreads();
+        if (tid < 64) {
+            // exclusive scan of the 1024 thread sums on one wave, 16 per lane
+            uint32_t v[16], t = 0;
+#pragma unroll
+            for (int e = 0; e < 16; e++) { v[e] = ps.sh_scan[16 * tid + e]; t += v[e]; }
+            uint32_t x = t;
+#pragma unroll
+            for (int d = 1; d < 64; d <<= 1) {
+                const uint32_t y = __shfl_up(x, d);
+                if (tid >= d) x += y;
+            }
+            uint32_t off = x - t;
+#pragma unroll
+            for (int e = 0; e < 16; e++) { ps.sh_scan[16 * tid + e] = off; off += v[e]; }
+            if (tid == 63) ps.nkeep = x;
+        }
+        __syncthreads();
+        uint32_t o = ps.sh_scan[tid];
+        for (int w = w0; w < min(NWD, w0 + per); w++) {
+            ps.bm.wpre[w] = o;
+            o += __popc(ps.bm.bits[w]);
+        }
+    }
+    __syncthreads();
+    for (int c = tid; c < C; c += 1024) {
+        const float p = ps.ce[c];
+        if (p >= cut) {
+            const int i = ps.ci[c];
+            const uint32_t pos = ps.bm.wpre[i >> 5] + __popc(ps.bm.bits[i >> 5] & ((1u << (i & 31)) - 1u));
+            ps.kp[pos] = p;
+            ps.ki[pos] = i;
+        }
+    }
+    if (tid < 112) ps.lcnt[tid] = 0u;
+    __syncthreads();
+    const int NK = (int)ps.nkeep;
+    // 7. the kept probabilities' sum in the 112-lane order: lane t adds the
+    // kept entries of index = t mod 112 in ascending index.  The entries go
+    // into per-lane lists (counting sort by lane; each list then sorted by
+    // its few indices), then each lane adds its list in order.
+    for (int j = tid; j < NK; j += 1024) atomicAdd(&ps.lcnt[ps.ki[j] % 112], 1u);
+    __syncthreads();
+    if (tid == 0) {
+        uint32_t o = 0;
+        for (int l = 0; l < 112; l++) { ps.loff[l] = o; ps.lcur[l] = o; o += ps.lcnt[l]; }
+    }
+    __syncthreads();
+    uint32_t *lidx = ps.bm.wpre;  // free again after the scatter
+    for (int j = tid; j < NK; j += 1024) lidx[atomicAdd(&ps.lcur[ps.ki[j] % 112], 1u)] = (uint32_t)j;
+    __syncthreads();
+    if (tid < 112) {
+        const int o = (int)ps.loff[tid], cnt = (int)ps.lcnt[tid];
+        for (int a2 = 1; a2 < cnt; a2++) {  // insertion sort of the lane's list by position (= index order)
+            const uint32_t v = lidx[o + a2];
+            int q = a2 - 1;
+            while (q >= 0 && lidx[o + q] > v) { lidx[o + q + 1] = lidx[o + q]; q--; }
+            lidx[o + q + 1] = v;
+        }
+        float s = 0.0f;
+        for (int q = 0; q < cnt; q++) s += ps.kp[lidx[o + q]];
+        ps.part[tid] = s;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        for (int q = 0; q < 48; q++) ps.part[q] += ps.part[q + 64];
+        for (int step = 32; step > 0; step >>= 1)
+            for (int q = 0; q < step; q++) ps.part[q] += ps.part[q + step];
+        ps.tot2 = ps.part[0];
+        ps.chosen = -1;
+    }
+    __syncthreads();
+    // 8. the CDF draw: the first kept entry (index order) whose sequential
+    // fp32 running sum exceeds u.  Exact prefix sums (double, in parallel)
+    // place the crossing; when u is further from both neighbouring prefix
+    // sums than the sequential fp32 sum can stray (each prefix within
+    // NK * 2^-24 of the total), the sequential crossing is that entry.
+    // Otherwise the sequential scan runs as written.
+    const float u = u01_dev(seed) * ps.tot2;
+    {
+        double *dpre = (double *)ps.bm.bits;  // 4096 doubles (bits is free)
+        const int per = (NK + 1023) / 1024, j0 = tid * per, j1 = min(NK, j0 + per);
+        double loc = 0.0;
+        for (int j = j0; j < j1; j++) loc += (double)ps.kp[j];
+        ps.dred[tid] = loc;
+        __syncthreads();
+        if (tid < 64) {
+            double v[16], t = 0.0;
+#pragma unroll
+            for (int e = 0; e < 16; e++) { v[e] = ps.dred[16 * tid + e]; t += v[e]; }
+            double x = t;
+#pragma unroll
+            for (int d = 1; d < 64; d <<= 1) {
+                const double y = __shfl_up(x, d);
+                if (tid >= d) x += y;
+            }
+            double off = x - t;
+#pragma unroll
+            for (int e = 0; e < 16; e++) { ps.dred[16 * tid + e] = off; off += v[e]; }
+        }
+        __syncthreads();
+        double run = ps.dred[tid];
+        for (int j = j0; j < j1; j++) { run += (double)ps.kp[j]; dpre[j] = run; }
+        __syncthreads();
+        const double bound = (double)(NK + 2) * 1.1920928955078125e-07 * (double)fmaxf(ps.tot2, u) + 1e-30;
+        for (int j = j0; j < j1; j++) {
+            const double prev = j > 0 ? dpre[j - 1] : 0.0;
+            if (dpre[j] > (double)u && prev <= (double)u)
+                ps.chosen = (dpre[j] - (double)u > bound && (double)u - prev > bound) ? j : -2;
+        }
+        if (tid == 0 && NK > 0 && dpre[NK - 1] <= (double)u)
+            ps.chosen = (double)u - dpre[NK - 1] > bound ? NK : -2;  // no crossing: the default token
+        __syncthreads();
+    }
+    if (ps.chosen >= 0) {
+        if (tid == 0) token[b] = ps.chosen < NK ? (uint32_t)ps.ki[ps.chosen] : (uint32_t)(n - 1);
+        return;
+    }
+    if (tid < 64) {
+        float acc = 0.0f;
+        int chosen = n - 1;
+        bool found = false;
+        for (int j0 = 0; j0 < NK && !found; j0 += 64) {
+            const float pv = j0 + tid < NK ? ps.kp[j0 + tid] : 0.0f;
+            const int cnt = min(64, NK - j0);
+            for (int q = 0; q < cnt; q++) {
+                acc += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pv), q));
+                if (acc > u) {
+                    chosen = ps.ki[j0 + q];
+                    found = true;
+                    break;
+                }
+            }
+        }
+        if (tid == 0) token[b] = (uint32_t)chosen;
+    }
+}
+
 // ------------------------------------------------ allocation-free sampling
 // Work area of rsv_sample_noalloc: temp [n] f32, counter [n] u32 and one
 // sampler row [8], for n up to kNoAllocMaxN.  One copy per device, held
@@ -822,6 +1425,24 @@ uint32_t *sample_scratch(int device) {
 int launch_sample(rsv_ctx *ctx, const float *logits, uint32_t *token, int n, float *temp, uint32_t *counter,
                   const float *sampler, const uint32_t *hist, int hist_stride, int batch) {
     if (n <= 0 || batch <= 0) return RSV_FAIL("sample: bad n=%d batch=%d", n, batch);
+    if (n >= kSampMinN && n <= 262144 && batch <= 65535) {
+        // the multi-CU top-p path (each row falls back to the one-block pipeline inside the last launch)
+        const dim3 g((n + 1023) / 1024, batch);
+        hipLaunchKernelGGL(k_samp_scale, g, dim3(1024), 0, ctx->stream, logits, n, temp, counter, sampler, hist,
+                           hist_stride);
+        RSV_HIP(hipGetLastError());
+        hipLaunchKernelGGL(k_samp_exp, g, dim3(1024), 0, ctx->stream, n, temp, counter, sampler);
+        RSV_HIP(hipGetLastError());
+#define SAMP_PICK(P)                                                                                          \
+    if (P == 0 || n == (P)*kSampBS) {                                                                           \
+        hipLaunchKernelGGL(k_samp_pick<P>, dim3(batch), dim3(1024), 0, ctx->stream, logits, token, n, temp, counter, \
+                           sampler, hist, hist_stride);                                                          \
+        RSV_HIP(hipGetLastError());                                                                             \
+        return 0;                                                                                               \
+    }
+        SAMP_PICK(64) SAMP_PICK(32) SAMP_PICK(16) SAMP_PICK(8) SAMP_PICK(0)
+#undef SAMP_PICK
+    }
     // rows of 1024 x 2^j entries (j <= 6: vocabularies 1,024 .. 65,536) in
     // registers, others on the general kernel
 #define SAMP_REGS(P)                                                                                             \
