@@ -236,8 +236,10 @@ int rsv_sample_into_host_seeded_batch(rsv_ctx *ctx, uint32_t logits, uint32_t to
  * token ids (ignored when hist_len is 0) instead of a host array.  The work
  * area (temp, counter, sampler row) is one static device array per GPU of
  * 2*262144+64 words (2 MiB), held until the process ends: n above 262144 is
- * rejected.  Calls that overlap on one GPU (several contexts or threads on
- * the same device) race on that array; calls in one stream do not. */
+ * rejected.  The first context on a device to call it owns the array until
+ * rsv_destroy; calls from another context on that device fail (their streams
+ * could overlap).  Calls from several host threads on the owning context's
+ * one stream are ordered by that stream. */
 int rsv_sample_noalloc(rsv_ctx *ctx, uint32_t logits, uint32_t token, uint64_t n, float temperature,
                        uint32_t top_k, float top_p, uint32_t seed, float repetition_penalty,
                        float frequency_penalty, float presence_penalty, uint32_t hist, uint64_t hist_len);

@@ -108,6 +108,13 @@ typedef struct rsv_serve_step {
 int rsv_serve_ragged(rsv_bundle *b, rsv_state *s, const uint32_t *tokens, const uint64_t *lens, uint64_t decode_len,
                      const rsv_sampler_params *sp, const uint32_t *seeds, uint64_t budget, uint32_t *out,
                      rsv_serve_step *steps, uint64_t max_steps, uint64_t *nsteps);
+/* rsv_serve_ragged that also copies, for each draw, the logits row it was
+ * drawn from into sampled_logits[batch][decode_len][vocab] (host memory;
+ * for checking the sampler and the batched logits separately). */
+int rsv_serve_ragged_logits(rsv_bundle *b, rsv_state *s, const uint32_t *tokens, const uint64_t *lens,
+                            uint64_t decode_len, const rsv_sampler_params *sp, const uint32_t *seeds, uint64_t budget,
+                            uint32_t *out, rsv_serve_step *steps, uint64_t max_steps, uint64_t *nsteps,
+                            float *sampled_logits);
 
 /* Timed variants for benchmarks: run the self-loop with the graph already
  * captured, synchronising before and after, and report device-side elapsed

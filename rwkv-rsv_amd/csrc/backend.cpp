@@ -144,6 +144,7 @@ int rsv_destroy(rsv_ctx *ctx) {
     if (ctx->hist_dev) hipFree(ctx->hist_dev);
     if (ctx->sample_work) hipFree(ctx->sample_work);
     if (ctx->skinny_ws) hipFree(ctx->skinny_ws);
+    sample_scratch_release(ctx->device, ctx);
     hipStreamDestroy(ctx->stream);
     delete ctx;
     return 0;
@@ -982,6 +983,7 @@ int rsv_sample_noalloc(rsv_ctx *ctx, uint32_t logits, uint32_t token, uint64_t n
         OPND(hh, hist, RSV_U32, hist_len, "sample_noalloc history");
         hp = U32P(hh);
     }
+    if (sample_scratch_claim(ctx->device, ctx)) return -1;
     uint32_t *work = sample_scratch(ctx->device);
     if (!work) return RSV_FAIL("sample_noalloc: no work area on device %d", ctx->device);
     // temp [n] f32, counter [n] u32, sampler row [8]: every word the kernel

@@ -265,10 +265,6 @@ struct GpuState {
 };
 
 // An on/off environment switch (unset: def; "0": off).
-bool getenv_flag(const char *name, bool def) {
-    const char *e = getenv(name);
-    return e && e[0] ? e[0] != '0' : def;
-}
 
 struct WorkBufs {
     uint64_t batch = 0;
@@ -287,10 +283,6 @@ struct WorkBufs {
 };
 
 constexpr uint64_t kMmBatch = 2;  // sessions from which decode GEMMs run on MFMA
-uint64_t mm_batch() {
-    const char *e = getenv("RSV_MM_BATCH");
-    return e ? (uint64_t)atoi(e) : kMmBatch;
-}
 constexpr uint64_t kSmallPrefill = 128;  // packed prefill rows that still take the decode MFMA kernel
 
 struct SeqBufs {
@@ -624,7 +616,7 @@ int get_bufs(rsv_bundle *b, uint64_t B, WorkBufs *&out) {
     HK(new_tensor(b, I.ffn * B, RSV_F32, w.r2));
     HK(new_tensor(b, I.vocab * B, RSV_F32, w.logits));
     HK(new_tensor(b, B, RSV_U32, w.token));
-    w.mm = B >= mm_batch();
+    w.mm = B >= kMmBatch;
     if (w.mm) {
         HK(tile_model(b));
         for (auto &m : w.mix16) HK(new_tensor(b, C * B, RSV_F16, m));
@@ -639,9 +631,10 @@ int get_bufs(rsv_bundle *b, uint64_t B, WorkBufs *&out) {
         // ffn.value k-slices of at most 2560 columns, each a 128-multiple
         // above the small-k kernel's 256 (10240 -> 4 x 2560)
         const uint64_t F = I.ffn, nsl = (F + 2559) / 2560;
-        if (nsl <= 4 && F % (nsl * 128) == 0 && F / nsl > 256 && getenv_flag("RSV_FFNV_KSLICE", true)) {
+        if (nsl <= 4 && F % (nsl * 128) == 0 && F / nsl > 256) {
             w.fv_nsl = (int)nsl;
-            HK(new_tensor(b, nsl * C * B, RSV_F32, w.fvpart));
+            // also holds att.output's k-slices (atto_nsl: at most 4)
+            HK(new_tensor(b, std::max<uint64_t>(nsl, 4) * C * B, RSV_F32, w.fvpart));
             HK(new_tensor(b, C * B, RSV_F32, w.xalt));
         }
     }
@@ -972,11 +965,10 @@ int ln_mix_mm(rsv_bundle *b, WorkBufs &w, uint32_t state, uint32_t gamma, uint32
 
 // att.output k-slices on the matrix-core path (its 2560 rows are only 80
 // row tiles: two slices spread them over twice the CUs, the slice sums
-// going to LN2).  RSV_ATTO_KSLICE=0 keeps one GEMM adding into the row.
+// going to LN2).
 int atto_nsl(const Linear &L) {
-    const char *e = getenv("RSV_ATTO_KSLICE");
-    const int n = e && e[0] ? atoi(e) : 2;
-    if (n <= 1 || n > 4 || L.k % (uint64_t)(n * 128) != 0 || L.k / n <= 256 || L.k / n > 2560 || (L.k / n) % 64) return 0;
+    const int n = 2;
+    if ( L.k % (uint64_t)(n * 128) != 0 || L.k / n <= 256 || L.k / n > 2560 || (L.k / n) % 64) return 0;
     return n;
 }
 
@@ -1354,7 +1346,7 @@ struct ServeSlot {
 
 int serve_ragged(rsv_bundle *b, GpuState &s, const uint32_t *tokens, const uint64_t *lens, uint64_t decode_len,
                  const rsv_sampler_params *sp, const uint32_t *seeds, uint64_t budget, uint32_t *out,
-                 rsv_serve_step *steps, uint64_t max_steps, uint64_t *nsteps) {
+                 rsv_serve_step *steps, uint64_t max_steps, uint64_t *nsteps, float *sampled_logits) {
     rsv_ctx *c = b->ctx;
     const rsv_model_info &I = b->info;
     const uint64_t B = s.batch, V = I.vocab;
@@ -1461,6 +1453,14 @@ int serve_ragged(rsv_bundle *b, GpuState &s, const uint32_t *tokens, const uint6
                 break;
             }
             const auto t1 = std::chrono::steady_clock::now();
+            if (sampled_logits) {  // the logits row each draw was made from (checks)
+                std::vector<float> rows(S * V);
+                if (rsv_download(c, logits, rows.data(), S * V)) { rc = herr("serve_ragged logits: %s", rsv_last_error()); break; }
+                for (uint64_t g = 0; g < S; g++)
+                    if (samples[g])
+                        memcpy(sampled_logits + (seg_slot[g] * decode_len + sl[seg_slot[g]].gen) * V, rows.data() + g * V,
+                               V * sizeof(float));
+            }
             for (uint64_t g = 0; g < S; g++) {
                 if (!samples[g]) continue;
                 ServeSlot &z = sl[seg_slot[g]];
@@ -1875,7 +1875,15 @@ int rsv_serve_ragged(rsv_bundle *b, rsv_state *s, const uint32_t *tokens, const 
                      const rsv_sampler_params *sp, const uint32_t *seeds, uint64_t budget, uint32_t *out,
                      rsv_serve_step *steps, uint64_t max_steps, uint64_t *nsteps) {
     if (!b || !s || !tokens || !lens || !sp || !seeds || !out) return herr("null argument");
-    return serve_ragged(b, s->s, tokens, lens, decode_len, sp, seeds, budget, out, steps, max_steps, nsteps);
+    return serve_ragged(b, s->s, tokens, lens, decode_len, sp, seeds, budget, out, steps, max_steps, nsteps, nullptr);
+}
+
+int rsv_serve_ragged_logits(rsv_bundle *b, rsv_state *s, const uint32_t *tokens, const uint64_t *lens,
+                            uint64_t decode_len, const rsv_sampler_params *sp, const uint32_t *seeds, uint64_t budget,
+                            uint32_t *out, rsv_serve_step *steps, uint64_t max_steps, uint64_t *nsteps,
+                            float *sampled_logits) {
+    if (!b || !s || !tokens || !lens || !sp || !seeds || !out) return herr("null argument");
+    return serve_ragged(b, s->s, tokens, lens, decode_len, sp, seeds, budget, out, steps, max_steps, nsteps, sampled_logits);
 }
 
 int rsv_sample_selfloop_batch(rsv_bundle *b, rsv_state *s, const uint32_t *seeds, uint64_t n,

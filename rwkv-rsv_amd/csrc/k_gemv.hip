@@ -775,11 +775,6 @@ __global__ __launch_bounds__(256) void k_gemv_mb_reduce(GemvJobs jobs, int batch
     apply_epi(J, row, b, s);
 }
 
-static bool mb_disabled() {
-    const char *e = getenv("RSV_GEMV_MB");
-    return e && e[0] == '0';
-}
-
 // 2 <= batch <= 16 on k_gemv_mb.  Returns 1 when a job does not fit it.
 static int launch_mb(rsv_ctx *ctx, GemvJobs &jobs, int batch) {
     if (batch > 16) return 1;
@@ -1135,7 +1130,7 @@ int launch_gemv_jobs(rsv_ctx *ctx, GemvJobs &jobs, int batch) {
         const int rc = launch_os2(ctx, jobs);
         if (rc <= 0) return rc;
     }
-    if (batch >= 2 && !mb_disabled()) {
+    if (batch >= 2) {
         const int rc = launch_mb(ctx, jobs, batch);
         if (rc <= 0) return rc;
     }

@@ -1422,6 +1422,27 @@ uint32_t *sample_scratch(int device) {
     return (uint32_t *)g_scratch_ptr[device];
 }
 
+// One context per device may use the work area: the first to call
+// rsv_sample_noalloc owns it until it is destroyed, and calls from any other
+// context on that device are refused (their streams could overlap).
+static const void *g_scratch_owner[kMaxDevices];
+
+int sample_scratch_claim(int device, const void *ctx) {
+    if (device < 0 || device >= kMaxDevices) return RSV_FAIL("sample scratch: device %d out of range", device);
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_owner[device]) g_scratch_owner[device] = ctx;
+    if (g_scratch_owner[device] != ctx)
+        return RSV_FAIL("sample_noalloc: the work area of device %d belongs to another context (one context per "
+                        "device may use it, until that context is destroyed)", device);
+    return 0;
+}
+
+void sample_scratch_release(int device, const void *ctx) {
+    if (device < 0 || device >= kMaxDevices) return;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (g_scratch_owner[device] == ctx) g_scratch_owner[device] = nullptr;
+}
+
 int launch_sample(rsv_ctx *ctx, const float *logits, uint32_t *token, int n, float *temp, uint32_t *counter,
                   const float *sampler, const uint32_t *hist, int hist_stride, int batch) {
     if (n <= 0 || batch <= 0) return RSV_FAIL("sample: bad n=%d batch=%d", n, batch);

@@ -169,6 +169,8 @@ constexpr uint64_t kNoAllocWords = 2 * kNoAllocMaxN + 64;
 constexpr int kMaxDevices = 64;
 int sample_scratch_init(int device);
 uint32_t *sample_scratch(int device);
+int sample_scratch_claim(int device, const void *ctx);
+void sample_scratch_release(int device, const void *ctx);
 int launch_sample(rsv_ctx *ctx, const float *logits, uint32_t *token, int n, float *temp,
                   uint32_t *counter, const float *sampler, const uint32_t *hist, int hist_stride,
                   int batch);

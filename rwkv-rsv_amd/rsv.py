@@ -383,11 +383,12 @@ class Bundle:
         return out.reshape(state.batch, n)
 
 
-    def serve_ragged(self, state, prompts, decode_len, sp, seeds, budget=4096, max_steps=None):
+    def serve_ragged(self, state, prompts, decode_len, sp, seeds, budget=4096, max_steps=None, want_logits=False):
         """Ragged continuous batching over the slots of `state`: slot q
         prefills prompts[q] and samples `decode_len` tokens; every step is one
         packed dispatch of decode tokens plus prompt chunks (`budget` tokens).
-        Returns (tokens [batch, decode_len], list of per-step dicts)."""
+        Returns (tokens [batch, decode_len], list of per-step dicts), and with
+        want_logits the logits row of every draw [batch, decode_len, vocab]."""
         if len(prompts) != state.batch:
             raise RsvError(f"serve_ragged: {len(prompts)} prompts for {state.batch} slots")
         lens = np.array([len(p) for p in prompts], np.uint64)
@@ -399,12 +400,19 @@ class Bundle:
         steps = (ServeStep * max_steps)()
         n = ctypes.c_uint64()
         c = sp._c()
-        _hchk(_host.rsv_serve_ragged(self._h, state._h, _u32p(flat), _u64p(lens), ctypes.c_uint64(decode_len),
-                                     ctypes.byref(c), _u32p(sd), ctypes.c_uint64(budget), _u32p(out),
-                                     ctypes.cast(steps, ctypes.c_void_p), ctypes.c_uint64(max_steps),
-                                     ctypes.byref(n)))
+        args = (self._h, state._h, _u32p(flat), _u64p(lens), ctypes.c_uint64(decode_len), ctypes.byref(c), _u32p(sd),
+                ctypes.c_uint64(budget), _u32p(out), ctypes.cast(steps, ctypes.c_void_p), ctypes.c_uint64(max_steps),
+                ctypes.byref(n))
+        lg = None
+        if want_logits:
+            lg = np.zeros((state.batch, decode_len, self.vocab), np.float32)
+            _hchk(_host.rsv_serve_ragged_logits(*args, lg.ctypes.data_as(ctypes.POINTER(ctypes.c_float))))
+        else:
+            _hchk(_host.rsv_serve_ragged(*args))
         recs = [dict(prefill_tokens=steps[i].prefill_tokens, decode_tokens=steps[i].decode_tokens,
                      sampled=steps[i].sampled, ms=steps[i].ms) for i in range(n.value)]
+        if want_logits:
+            return out.reshape(state.batch, decode_len), recs, lg
         return out.reshape(state.batch, decode_len), recs
 
 

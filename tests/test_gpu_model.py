@@ -304,13 +304,11 @@ def test_batch_matrix_core_decode(bundles, kind, bar, B):
 def test_serve_ragged_matches_per_session_runs(bundles):
     """Ragged continuous batching: prompts of mixed lengths, split across
     steps by a small token budget and interleaved with other slots' decode
-    tokens, give the same sampled tokens as serving each session alone (its
-    prompt as one prefill, then one token at a time) with the oracle sampler
-    on the GPU logits and the same seed rule (token k of slot q: seeds[q] + k).
-    Steps in which every slot decodes run the batched decode step instead of
-    the packed prefill (other kernels, logits equal to fp32 rounding): a draw
-    there may move to the neighbouring candidate in token order when the
-    sampling threshold falls within that rounding, never further."""
+    tokens.  Two separate checks per draw: the served token is exactly the
+    oracle sampler's draw (seed rule: token k of slot q takes seeds[q] + k) on
+    the logits row it was drawn from, and that row (packed prefill, or the
+    batched decode step when every slot decodes) is within 1e-3 of the same
+    session served alone along the same tokens."""
     rsv = _rsv()
     b, _ = bundles["i8"]
     lens = [1, 7, 19, 3, 30]
@@ -319,7 +317,7 @@ def test_serve_ragged_matches_per_session_runs(bundles):
     sp = rsv.SamplerParams(temperature=1.0, top_k=0, top_p=0.9)
     D, budget = 6, 16
     S = b.create_batch_state(len(lens))
-    toks, steps = b.serve_ragged(S, prompts, D, sp, seeds, budget=budget)
+    toks, steps, slg = b.serve_ragged(S, prompts, D, sp, seeds, budget=budget, want_logits=True)
     S.free()
     # schedule accounting
     assert sum(s["prefill_tokens"] for s in steps) == sum(lens)
@@ -328,25 +326,15 @@ def test_serve_ragged_matches_per_session_runs(bundles):
     assert all(s["prefill_tokens"] + s["decode_tokens"] <= budget for s in steps)
     assert any(s["prefill_tokens"] and s["decode_tokens"] for s in steps), "no step mixed prefill and decode"
     assert any(s["prefill_tokens"] == 0 and s["decode_tokens"] == len(lens) for s in steps), "no all-decode step"
-    # per-session reference
-    agree = total = 0
     for q, p in enumerate(prompts):
         b.reset()
         lg = b.infer_seq(p)
-        prev = None
         for k in range(D):
             if k:
-                lg = b.infer_seq([prev])
-            want = orc.sample(lg, sp.temperature, sp.top_k, sp.top_p, seeds[q] + k)
-            got = int(toks[q, k])
-            if want != got:
-                cand = np.sort(np.argsort(-lg.astype(np.float64), kind="stable")[:512])
-                pos = {int(t): i for i, t in enumerate(cand)}
-                assert got in pos and want in pos and abs(pos[got] - pos[want]) <= 1, (q, k, got, want)
-            agree += int(want == got)
-            total += 1
-            prev = got
-    assert agree >= total - 2, f"{agree}/{total}"
+                lg = b.infer_seq([int(toks[q, k - 1])])
+            assert rel_rmse(slg[q, k], lg) <= 1e-3, (q, k)
+            want = orc.sample(slg[q, k], sp.temperature, sp.top_k, sp.top_p, seeds[q] + k)
+            assert int(toks[q, k]) == want, (q, k)
 
 
 def test_serve_ragged_errors(bundles):

@@ -37,7 +37,9 @@ def _pair(be, logits, temperature, top_k, top_p, seed, rep=1.0, freq=0.0, pres=0
 @pytest.mark.parametrize("top_k,top_p", [(0, 0.9), (40, 0.8), (0, 1.0), (300, 0.95)])
 def test_sample_noalloc_matches_sample(be, top_k, top_p):
     rng = np.random.default_rng(7 + top_k)
-    for n, seed in ((65536, 11), (4096, 12)):  # second call smaller than the first
+    # second call smaller than the first; 65529 and 3000 are not multiples
+    # of 1024 (the general kernels), 65536 and 4096 the register-resident ones
+    for n, seed in ((65536, 11), (4096, 12), (65529, 13), (3000, 14)):
         lg = rng.standard_normal(n).astype(np.float32) * 2.0
         a, b = _pair(be, lg, 1.0, top_k, top_p, seed)
         assert a == b, (n, a, b)
@@ -55,3 +57,23 @@ def test_sample_noalloc_limits(be):
     short = be.tensor(np.zeros(3, np.uint32), dtype=rsv.U32)
     with pytest.raises(rsv.RsvError):
         be.call("rsv_sample_noalloc", lt, tok, 1000, 1.0, 0, 0.9, 1, 1.1, 0.0, 0.0, short, 5)
+
+
+def test_sample_noalloc_one_context_per_device(be):
+    """A second context on the device is refused while the owner lives (the
+    work area is per device); it may use it once the owner is destroyed."""
+    import rsv
+    lg = np.random.default_rng(3).standard_normal(4096).astype(np.float32)
+    lt, tok = be.tensor(lg), be.tensor(n=1, dtype=rsv.U32)
+    be.call("rsv_sample_noalloc", lt, tok, 4096, 1.0, 0, 0.9, 5, 1.0, 0.0, 0.0, NONE, 0)
+    other = rsv.Backend(0)
+    try:
+        lt2, tok2 = other.tensor(lg), other.tensor(n=1, dtype=rsv.U32)
+        with pytest.raises(rsv.RsvError, match="another context"):
+            other.call("rsv_sample_noalloc", lt2, tok2, 4096, 1.0, 0, 0.9, 5, 1.0, 0.0, 0.0, NONE, 0)
+        first = rsv.Backend(0)
+        first.close()  # destroying a non-owner leaves the owner in place
+        with pytest.raises(rsv.RsvError, match="another context"):
+            other.call("rsv_sample_noalloc", lt2, tok2, 4096, 1.0, 0, 0.9, 5, 1.0, 0.0, 0.0, NONE, 0)
+    finally:
+        other.close()
