@@ -116,6 +116,11 @@ int rsv_serve_ragged_logits(rsv_bundle *b, rsv_state *s, const uint32_t *tokens,
                             uint32_t *out, rsv_serve_step *steps, uint64_t max_steps, uint64_t *nsteps,
                             float *sampled_logits);
 
+/* Rows per packed prefill chunk of infer_seq / forward_seq_batch (1..12288,
+ * default 12288).  BASELINE configs[4] packs ragged batches of <= 4096
+ * tokens; larger chunks fill more GEMM tile rounds per launch. */
+int rsv_set_prefill_chunk(rsv_bundle *b, uint64_t rows);
+
 /* Timed variants for benchmarks: run the self-loop with the graph already
  * captured, synchronising before and after, and report device-side elapsed
  * milliseconds through *ms (hipEvent timing on the context stream). */

@@ -304,6 +304,7 @@ struct rsv_state {
 
 struct rsv_bundle {
     rsv_ctx *ctx = nullptr;
+    uint64_t prefill_chunk = 12288;  // packed prefill rows per chunk (rsv_set_prefill_chunk)
     rsv_model_info info{};
     uint32_t emb_ln = NONE, ln_out_w = NONE, ln_out_b = NONE, scale_w = NONE;
     Linear head;
@@ -1315,11 +1316,12 @@ static uint64_t water_fill(const std::vector<uint64_t> &rem, uint64_t cap) {
     return lo;
 }
 
-// Single-session prefill in chunks of at most kMaxChunk tokens.
+// Single-session prefill in chunks of at most prefill_chunk tokens.
 int seq_single(rsv_bundle *b, GpuState &s, uint64_t slot, const uint32_t *tokens, uint64_t n, float *logits) {
     if (n == 0) return herr("infer_seq: empty token list");
-    for (uint64_t off = 0; off < n; off += kMaxChunk) {
-        const uint64_t len = n - off < kMaxChunk ? n - off : kMaxChunk;
+    const uint64_t ch = b->prefill_chunk;
+    for (uint64_t off = 0; off < n; off += ch) {
+        const uint64_t len = n - off < ch ? n - off : ch;
         std::vector<Seg> segs{{tokens + off, len, slot}};
         HK(prefill(b, s, segs, off + len == n ? logits : nullptr));
     }
@@ -1806,7 +1808,7 @@ int rsv_forward_seq_batch(rsv_bundle *b, rsv_state *s, const uint32_t *tokens, c
         off += lens[q];
         T += lens[q];
     }
-    // Packed chunks of at most kMaxChunk tokens, filled breadth-first: every
+    // Packed chunks of at most prefill_chunk tokens, filled breadth-first: every
     // unfinished prompt contributes its next piece of at most L tokens, with
     // L the largest length whose pieces still fit one chunk (water filling).
     // A prompt's pieces go through consecutive chunks in order, its state
@@ -1830,10 +1832,11 @@ int rsv_forward_seq_batch(rsv_bundle *b, rsv_state *s, const uint32_t *tokens, c
         std::vector<uint64_t> rem(segs.size());
         for (size_t i = 0; i < segs.size(); i++) rem[i] = segs[i].len - done[i];
         if (rem.empty() || *std::max_element(rem.begin(), rem.end()) == 0) break;
-        const uint64_t L = std::max<uint64_t>(1, water_fill(rem, kMaxChunk));
+        const uint64_t ch = b->prefill_chunk;
+        const uint64_t L = std::max<uint64_t>(1, water_fill(rem, ch));
         uint64_t used = 0;
         for (size_t i = 0; i < segs.size(); i++) {
-            const uint64_t take = std::min({segs[i].len - done[i], L, kMaxChunk - used});
+            const uint64_t take = std::min({segs[i].len - done[i], L, ch - used});
             if (take == 0) continue;
             pending.push_back({segs[i].tok + done[i], take, segs[i].slot});
             done[i] += take;
@@ -1869,6 +1872,13 @@ int rsv_argmax_selfloop_batch_timed(rsv_bundle *b, rsv_state *s, const uint32_t 
     if (!b || !s || !seeds || !out || !ms) return herr("null argument");
     HK(tokens_ok(b, seeds, s->s.batch));
     return selfloop(b, s->s, seeds, n, nullptr, out, ms);
+}
+
+int rsv_set_prefill_chunk(rsv_bundle *b, uint64_t rows) {
+    if (!b) return herr("null argument");
+    if (rows == 0 || rows > kMaxChunk) return herr("set_prefill_chunk: rows must be 1..%llu", (unsigned long long)kMaxChunk);
+    b->prefill_chunk = rows;
+    return 0;
 }
 
 int rsv_serve_ragged(rsv_bundle *b, rsv_state *s, const uint32_t *tokens, const uint64_t *lens, uint64_t decode_len,

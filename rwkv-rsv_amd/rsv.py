@@ -336,6 +336,10 @@ class Bundle:
         _hchk(_host.rsv_create_batch_state(self._h, ctypes.c_uint64(batch), ctypes.byref(h)))
         return State(self, h, batch)
 
+    def set_prefill_chunk(self, rows):
+        """Rows per packed prefill chunk (1..12288; configs[4] packs <= 4096)."""
+        _hchk(_host.rsv_set_prefill_chunk(self._h, ctypes.c_uint64(rows)))
+
     def forward_seq_batch(self, state, prompts, want_logits=False):
         lens = np.array([len(p) for p in prompts], dtype=np.uint64)
         flat = _toks(np.concatenate([np.asarray(p, dtype=np.uint32) for p in prompts]))
