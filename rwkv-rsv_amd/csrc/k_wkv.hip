@@ -918,6 +918,135 @@ __global__ __launch_bounds__(256 / RPL) void k_wkv7_seq_rows(
             Sb[(row0 + i) * 16 + 4 * q + m] = make_float4(s[i][4 * m], s[i][4 * m + 1], s[i][4 * m + 2], s[i][4 * m + 3]);
 }
 
+// The scan for latency-bound launches (few segments: a long prompt of one
+// session, or a handful): one state row per lane group of G lanes, each lane
+// 64/G columns, G waves per (head, segment).  The dependent chain per token
+// is 64/G multiply-adds and a log2(G)-step DPP sum instead of 16 and two, at
+// G times the threads of k_wkv7_seq_rows<1>.  The head's column vectors of
+// a batch of tokens are formed into LDS one token per wave (16 per batch).
+template <int G>
+__device__ __forceinline__ float group_allsum(float v) {
+    v += quad_dpp<0xB1>(v);  // quad_perm 1,0,3,2
+    v += quad_dpp<0x4E>(v);  // quad_perm 2,3,0,1
+    if (G >= 8) v += quad_dpp<0x141>(v);   // row_half_mirror: the 8-lane sum in every lane of the 8
+    if (G >= 16) v += quad_dpp<0x140>(v);  // row_mirror: the 16-lane sum in every lane of the row
+    return v;
+}
+
+template <int G>
+__global__ __launch_bounds__(64 * G) void k_wkv7_seq_cols(
+    float *__restrict__ S, const float *__restrict__ r, const float *__restrict__ w, const float *__restrict__ k,
+    const float *__restrict__ v, const float *__restrict__ a, const float *__restrict__ kkc,
+    const float *__restrict__ ka, const float *__restrict__ rk, float *__restrict__ y_out,
+    float *__restrict__ bonus_out, const uint32_t *__restrict__ seg_start, const uint32_t *__restrict__ seg_len,
+    const uint32_t *__restrict__ seg_slot, int H, float eps, uint64_t rows, uint64_t slots) {
+    constexpr int NW = G;           // waves per (head, segment)
+    constexpr int CPL = 64 / G;     // columns per lane
+    constexpr int TPW = G >= 4 ? 1 : 4 / G;
+    constexpr int kRB = NW * TPW;   // tokens per batch
+    __shared__ __attribute__((aligned(16))) float hb[2][kRB][6 * 64];
+    __shared__ __attribute__((aligned(16))) float yl[2][kRB][64];
+    __shared__ float bl[2][kRB];
+    const int h = blockIdx.x, gi = blockIdx.y, tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63, q = lane % G;
+    const int row = (64 / G) * wave + lane / G;
+    const size_t C = (size_t)H * 64;
+    const uint32_t t0 = seg_start[gi], len = seg_len[gi], slot = seg_slot[gi];
+    if (slot >= slots || (uint64_t)t0 + len > rows) return;  // uniform per block
+    float *Sr = S + ((size_t)slot * H + h) * 4096 + (size_t)row * 64 + q * CPL;
+    float s[CPL];
+#pragma unroll
+    for (int m = 0; m < CPL / 4; m++) {
+        const float4 x = ((const float4 *)Sr)[m];
+        s[4 * m] = x.x; s[4 * m + 1] = x.y; s[4 * m + 2] = x.z; s[4 * m + 3] = x.w;
+    }
+    const int j = lane;
+    const float kkc_j = kkc[h * 64 + j], ka_j = ka[h * 64 + j], rk_j = rk[h * 64 + j];
+    float pk[TPW], pa[TPW], pw[TPW], pr[TPW], pv[TPW];
+    auto load_batch = [&](uint32_t tb) {
+#pragma unroll
+        for (int i = 0; i < TPW; i++) {
+            const uint32_t t = tb + TPW * wave + i;
+            const size_t vo = (size_t)(t0 + (t < len ? t : 0)) * C + (size_t)h * 64 + j;
+            pk[i] = k[vo]; pa[i] = a[vo]; pw[i] = w[vo]; pr[i] = r[vo]; pv[i] = v[vo];
+        }
+    };
+    auto form_batch = [&](int buf, uint32_t tb) {
+#pragma unroll
+        for (int i = 0; i < TPW; i++) {
+            const uint32_t t = tb + TPW * wave + i;
+            if (t >= len) break;  // uniform per wave
+            const float kc = pk[i], ac = pa[i], rc = pr[i];
+            const float kk = kc * kkc_j;
+            float nrm = sqrtf(wave_sum(kk * kk));
+            nrm = nrm < eps ? eps : nrm;
+            const float kh = kk * (1.0f / nrm);
+            const float kmod = kc + ka_j * (kc * ac - kc);
+            const float bonus = wave_sum(rc * kmod * rk_j);
+            float *hv = hb[buf][TPW * wave + i];
+            hv[j] = kh; hv[64 + j] = kh * (-ac); hv[128 + j] = pw[i]; hv[192 + j] = kmod; hv[256 + j] = rc; hv[320 + j] = pv[i];
+            if (j == 0) bl[buf][TPW * wave + i] = bonus;
+        }
+    };
+    auto flush = [&](int buf, uint32_t tb) {
+        for (int e = tid; e < kRB * 64; e += 64 * G) {
+            const uint32_t u = e >> 6;
+            if (tb + u < len) __builtin_nontemporal_store(yl[buf][u][e & 63], y_out + (size_t)(t0 + tb + u) * C + (size_t)h * 64 + (e & 63));
+        }
+        if (tid < kRB && tb + tid < len) __builtin_nontemporal_store(bl[buf][tid], bonus_out + (size_t)(t0 + tb + tid) * H + h);
+    };
+    if (len > 0) {
+        load_batch(0);
+        form_batch(0, 0);
+    }
+    for (uint32_t tb = 0; tb < len; tb += kRB) {
+        const int buf = (tb / kRB) & 1;
+        __syncthreads();
+        if (tb > 0) flush(buf ^ 1, tb - kRB);
+        const bool more = tb + kRB < len;
+        if (more) load_batch(tb + kRB);
+        const uint32_t nt = len - tb < (uint32_t)kRB ? len - tb : (uint32_t)kRB;
+        for (uint32_t u = 0; u < nt; u++) {
+            const float *hv = hb[buf][u] + q * CPL;
+            float kv[CPL], bv[CPL], wv[CPL], mv[CPL], rv[CPL];
+#pragma unroll
+            for (int m = 0; m < CPL / 4; m++) {
+                const float4 a0 = *(const float4 *)(hv + 4 * m), a1 = *(const float4 *)(hv + 64 + 4 * m),
+                             a2 = *(const float4 *)(hv + 128 + 4 * m), a3 = *(const float4 *)(hv + 192 + 4 * m),
+                             a4 = *(const float4 *)(hv + 256 + 4 * m);
+                kv[4 * m] = a0.x; kv[4 * m + 1] = a0.y; kv[4 * m + 2] = a0.z; kv[4 * m + 3] = a0.w;
+                bv[4 * m] = a1.x; bv[4 * m + 1] = a1.y; bv[4 * m + 2] = a1.z; bv[4 * m + 3] = a1.w;
+                wv[4 * m] = a2.x; wv[4 * m + 1] = a2.y; wv[4 * m + 2] = a2.z; wv[4 * m + 3] = a2.w;
+                mv[4 * m] = a3.x; mv[4 * m + 1] = a3.y; mv[4 * m + 2] = a3.z; mv[4 * m + 3] = a3.w;
+                rv[4 * m] = a4.x; rv[4 * m + 1] = a4.y; rv[4 * m + 2] = a4.z; rv[4 * m + 3] = a4.w;
+            }
+            const float vc = hb[buf][u][320 + row];
+            float sa = 0.f;
+#pragma unroll
+            for (int e = 0; e < CPL; e++) sa = fmaf(s[e], kv[e], sa);
+            sa = group_allsum<G>(sa);
+            float y = 0.f;
+#pragma unroll
+            for (int e = 0; e < CPL; e++) {
+                const float ns = s[e] * wv[e] + sa * bv[e] + vc * mv[e];
+                s[e] = ns;
+                y = fmaf(ns, rv[e], y);
+            }
+            y = group_allsum<G>(y);
+            if (q == 0) yl[buf][u][row] = y;
+        }
+        if (more) form_batch(buf ^ 1, tb + kRB);
+    }
+    if (len > 0) {
+        __syncthreads();
+        const uint32_t last = (len - 1) / kRB * kRB;
+        flush((last / kRB) & 1, last);
+    }
+#pragma unroll
+    for (int m = 0; m < CPL / 4; m++)
+        ((float4 *)Sr)[m] = make_float4(s[4 * m], s[4 * m + 1], s[4 * m + 2], s[4 * m + 3]);
+}
+
 // yg = ((GroupNorm(y) * gamma + beta) + bonus * v) * g in fp16: 16 lanes per
 // (token, head), four columns per lane (16-byte loads, 8-byte stores), four
 // (token, head) units per wave and 16 per block; the two-pass statistics are
@@ -964,7 +1093,18 @@ int launch_wkv7_seq_ragged_gate(rsv_ctx *ctx, float *s, const float *r, const fl
 #define WKV_ROWS_LAUNCH(R)                                                                                            \
     hipLaunchKernelGGL(k_wkv7_seq_rows<R>, dim3(h, nseg), dim3(256 / (R)), 0, ctx->stream, s, r, w, k, v, a, kk, ka, rk, \
                        y_work, bonus_work, seg_start, seg_len, seg_slot, h, 1e-12f, rows, slots)
-        WKV_ROWS_LAUNCH(2);
+#define WKV_COLS_LAUNCH(G)                                                                                            \
+    hipLaunchKernelGGL(k_wkv7_seq_cols<G>, dim3(h, nseg), dim3(64 * (G)), 0, ctx->stream, s, r, w, k, v, a, kk, ka, rk, \
+                       y_work, bonus_work, seg_start, seg_len, seg_slot, h, 1e-12f, rows, slots)
+        // (head, segment) blocks: with fewer than one per CU the launch is
+        // the longest segment's dependent chain, shortened by more lanes per row
+        const int blocks = h * nseg, cus = ctx->sm_count > 0 ? ctx->sm_count : 256;
+        const char *e = getenv("RSV_SCAN_G");
+        const int gsel = e ? atoi(e) : (blocks * 4 <= cus ? 16 : blocks <= cus ? 8 : 0);
+        if (gsel == 16) WKV_COLS_LAUNCH(16);
+        else if (gsel == 8) WKV_COLS_LAUNCH(8);
+        else WKV_ROWS_LAUNCH(2);
+#undef WKV_COLS_LAUNCH
 #undef WKV_ROWS_LAUNCH
         const uint64_t units = rows * (uint64_t)h;
         hipLaunchKernelGGL(k_gn_gate_f16, dim3((unsigned)((units + 15) / 16)), dim3(256), 0, ctx->stream, y_work,

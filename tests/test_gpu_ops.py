@@ -328,13 +328,18 @@ def test_wkv7_seq_ragged_matches_decode_loop(be):
         pos += lens[g]
 
 
-@pytest.mark.parametrize("lens", [[300, 212], [8] * 48 + [40]])
-def test_wkv7_seq_ragged_gate_matches_scan_times_gate(be, lens):
+@pytest.mark.parametrize("scan_g", ["", "16", "8", "0"])
+@pytest.mark.parametrize("lens", [[300, 212], [8] * 48 + [40], [512]])
+def test_wkv7_seq_ragged_gate_matches_scan_times_gate(be, lens, scan_g, monkeypatch):
     """rsv_wkv7_seq_ragged_gate leaves (GroupNorm(y) + bonus*v) * g in fp16:
     with few segments it runs the four-lanes-per-row scan and a separate
     GroupNorm pass, with many the one-wave scan; both against
-    rsv_wkv7_seq_ragged's yn times g (and its state) to rounding."""
+    rsv_wkv7_seq_ragged's yn times g (and its state) to rounding.  scan_g
+    forces the scan form (16 or 8 lanes per state row, 0 the two-rows-per-
+    group form; empty: chosen by the block count)."""
     rsv = _rsv()
+    if scan_g:
+        monkeypatch.setenv("RSV_SCAN_G", scan_g)
     H = 40
     C = H * 64
     rng = np.random.default_rng(len(lens))
