@@ -117,7 +117,7 @@ int rsv_serve_ragged_logits(rsv_bundle *b, rsv_state *s, const uint32_t *tokens,
                             float *sampled_logits);
 
 /* Rows per packed prefill chunk of infer_seq / forward_seq_batch (1..12288,
- * default 12288).  BASELINE configs[4] packs ragged batches of <= 4096
+ * default 12288).  The reference packs ragged serving batches of <= 4096
  * tokens; larger chunks fill more GEMM tile rounds per launch. */
 int rsv_set_prefill_chunk(rsv_bundle *b, uint64_t rows);
 

@@ -659,6 +659,38 @@ def test_sample_other_row_lengths(be, n, params):
     assert mism <= 1, f"{mism}/{trials} draws differ"
 
 
+def _samp_rows(kind, n, rng):
+    if kind == "normal":
+        return (rng.standard_normal(n) * 2.0).astype(np.float32)
+    if kind == "flat":  # thousands of candidates inside the boundary bin
+        return (rng.standard_normal(n) * 1e-3).astype(np.float32)
+    if kind == "ties":  # many exactly equal values at the 512-th place
+        return np.round(rng.standard_normal(n) * 2.0).astype(np.float32)
+    return (rng.standard_normal(n) * 8.0).astype(np.float32)  # peaked
+
+
+@pytest.mark.parametrize("kind,n,T,top_p", [
+    ("normal", 65536, 1.0, 0.05), ("normal", 65536, 0.7, 0.99), ("flat", 65536, 1.0, 0.9),
+    ("ties", 65536, 1.0, 0.9), ("peaked", 65536, 1.0, 0.9), ("normal", 65529, 1.0, 0.9),
+    ("flat", 5184, 1.0, 0.5), ("ties", 131072, 1.3, 0.8),
+])
+def test_sample_multi_cu_rows(be, kind, n, T, top_p):
+    """Rows with no top-k and 0 < top_p < 1 of 5184..262,144 entries run the
+    multi-CU sampler (scale / exp / pick launches): against the oracle
+    sampler (backend_cuda.rs:3690-4009) on rows that exercise the candidate
+    gather (flat rows overflow the coarse bin, tied rows put equal values at
+    the 512-th place, peaked rows keep few candidates)."""
+    rng = np.random.default_rng(n + len(kind))
+    mism = 0
+    trials = 12
+    for s in range(trials):
+        lg = _samp_rows(kind, n, rng)
+        want = orc.sample(lg, T, 0, top_p, 77 + s)
+        got = _sample_gpu(be, lg, T, 0, top_p, 77 + s)
+        mism += want != got
+    assert mism <= 1, f"{mism}/{trials} draws differ"
+
+
 def test_sample_batch_low_temperature_is_argmax(be):
     """backend_cuda.rs:7919-8011 (xorshift32 logits, T=1e-4, top_k=50)."""
     rsv = _rsv()
