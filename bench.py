@@ -344,9 +344,9 @@ def wkv_leg():
                                        N, 64e-5)
                 # the scan form follows the block count (H x B): 16 lanes per
                 # state row below a quarter of the CUs, two rows per group of
-                # four lanes from one block per CU up
+                # four lanes from one block per CU up, four rows from 16 per CU
                 kern = ("k_wkv7_seq_cols<16>" if H * B * 4 <= 256 else "k_wkv7_seq_cols<8>" if H * B <= 256
-                        else "k_wkv7_seq_rows<2>") + "+k_gn_gate_f16"
+                        else "k_wkv7_seq_rows<4>" if H * B >= 16 * 256 else "k_wkv7_seq_rows<2>") + "+k_gn_gate_f16"
             reps = 50 if T == 1 else max(2, min(20, 256 // B))
             us = tm.us(fn, reps)
             byts = B * H * (2 * 16384 + T * 6 * 64 * 4)

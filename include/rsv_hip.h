@@ -471,6 +471,21 @@ int rsv_wkv7_lora_decode(rsv_ctx *ctx, const rsv_wkv_lora *op, uint64_t batch);
 int rsv_clear_kernel_prof(rsv_ctx *ctx);
 int rsv_dump_kernel_prof(rsv_ctx *ctx);
 
+/* ---- prefill lanes.  No counterpart in the reference (its prefill runs on
+ * one stream); for the host layer's pipelined prefill, which overlaps
+ * consecutive packed chunks.  rsv_lane_select makes lane 0 (the context's
+ * own stream) or lane 1 (a second stream of the context, made on first use,
+ * default priority) the stream every later launch, copy and synchronisation
+ * of ctx uses; refused during graph capture.  rsv_lane_record records event
+ * ev (0..255) of the current lane; rsv_lane_wait makes the current lane wait
+ * for the last recording of event ev of `lane`.  Work buffers a caller hands
+ * to launches on both lanes must not overlap while both are in flight (the
+ * batched-decode GEMM and the sampler use context-wide work areas: keep them
+ * on one lane at a time). */
+int rsv_lane_select(rsv_ctx *ctx, int lane);
+int rsv_lane_record(rsv_ctx *ctx, int ev);
+int rsv_lane_wait(rsv_ctx *ctx, int lane, int ev);
+
 /* ---- raw access for harnesses: device pointer and stream of a tensor/ctx */
 int rsv_tensor_ptr(rsv_ctx *ctx, uint32_t id, void **ptr);
 int rsv_stream(rsv_ctx *ctx, void **stream);

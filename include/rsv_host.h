@@ -121,6 +121,14 @@ int rsv_serve_ragged_logits(rsv_bundle *b, rsv_state *s, const uint32_t *tokens,
  * tokens; larger chunks fill more GEMM tile rounds per launch. */
 int rsv_set_prefill_chunk(rsv_bundle *b, uint64_t rows);
 
+/* Streams a multi-chunk prefill uses (1 or 2, default 2).  With 2, consecutive
+ * packed chunks of infer_seq / forward_seq_batch (without logits) run on two
+ * streams of the context, each chunk waiting per layer only for the state its
+ * predecessor leaves (token-shift rows, WKV state), so one chunk's scan
+ * overlaps the other's GEMMs.  Results are bit-identical to 1.  No
+ * counterpart in the reference (one stream). */
+int rsv_set_prefill_lanes(rsv_bundle *b, int lanes);
+
 /* Timed variants for benchmarks: run the self-loop with the graph already
  * captured, synchronising before and after, and report device-side elapsed
  * milliseconds through *ms (hipEvent timing on the context stream). */

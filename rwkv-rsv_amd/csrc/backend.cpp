@@ -136,6 +136,13 @@ int rsv_create(int device, rsv_ctx **out) {
 int rsv_destroy(rsv_ctx *ctx) {
     if (!ctx) return 0;
     hipSetDevice(ctx->device);
+    if (ctx->lane[0]) ctx->stream = ctx->lane[0];
+    if (ctx->lane[1]) {
+        hipStreamSynchronize(ctx->lane[1]);
+        hipStreamDestroy(ctx->lane[1]);
+    }
+    for (auto &v : ctx->lane_ev)
+        for (hipEvent_t e : v) hipEventDestroy(e);
     hipStreamSynchronize(ctx->stream);
     if (ctx->graph_exec) hipGraphExecDestroy(ctx->graph_exec);
     if (ctx->graph) hipGraphDestroy(ctx->graph);
@@ -161,6 +168,49 @@ int rsv_device_name(rsv_ctx *ctx, char *buf, size_t len) {
 int rsv_synchronize(rsv_ctx *ctx) {
     CHECK_CTX();
     RSV_HIP(hipStreamSynchronize(ctx->stream));
+    return 0;
+}
+
+// ------------------------------------------------------------ prefill lanes
+constexpr int kLaneEvents = 256;
+
+static int lane_make(rsv_ctx *ctx, int lane) {
+    if (!ctx->lane[0]) ctx->lane[0] = ctx->stream;
+    if (lane == 1 && !ctx->lane[1]) {
+        RSV_HIP(hipSetDevice(ctx->device));
+        RSV_HIP(hipStreamCreateWithFlags(&ctx->lane[1], hipStreamNonBlocking));  // default priority
+    }
+    if (ctx->lane_ev[lane].empty()) {
+        ctx->lane_ev[lane].assign(kLaneEvents, nullptr);
+        for (auto &e : ctx->lane_ev[lane]) RSV_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+    }
+    return 0;
+}
+
+int rsv_lane_select(rsv_ctx *ctx, int lane) {
+    CHECK_CTX();
+    if (lane < 0 || lane > 1) return RSV_FAIL("lane_select: lane %d is not 0 or 1", lane);
+    if (ctx->capturing || ctx->prefill_capturing) return RSV_FAIL("lane_select: not during graph capture");
+    if (lane_make(ctx, lane)) return -1;
+    ctx->stream = ctx->lane[lane];
+    return 0;
+}
+
+int rsv_lane_record(rsv_ctx *ctx, int ev) {
+    CHECK_CTX();
+    if (ev < 0 || ev >= kLaneEvents) return RSV_FAIL("lane_record: event %d out of 0..%d", ev, kLaneEvents - 1);
+    const int lane = ctx->lane[1] && ctx->stream == ctx->lane[1] ? 1 : 0;
+    if (lane_make(ctx, lane)) return -1;
+    RSV_HIP(hipEventRecord(ctx->lane_ev[lane][ev], ctx->stream));
+    return 0;
+}
+
+int rsv_lane_wait(rsv_ctx *ctx, int lane, int ev) {
+    CHECK_CTX();
+    if (lane < 0 || lane > 1) return RSV_FAIL("lane_wait: lane %d is not 0 or 1", lane);
+    if (ev < 0 || ev >= kLaneEvents) return RSV_FAIL("lane_wait: event %d out of 0..%d", ev, kLaneEvents - 1);
+    if (lane_make(ctx, lane)) return -1;
+    RSV_HIP(hipStreamWaitEvent(ctx->stream, ctx->lane_ev[lane][ev], 0));
     return 0;
 }
 

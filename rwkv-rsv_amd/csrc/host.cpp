@@ -312,6 +312,8 @@ struct rsv_bundle {
     rsv_state *state = nullptr;  // the bundle's own session
     std::map<uint64_t, WorkBufs> bufs;
     SeqBufs seq;
+    SeqBufs seq2;          // the second lane's buffers of the pipelined prefill
+    int prefill_lanes = 2; // rsv_set_prefill_lanes
     std::vector<uint32_t> owned;  // every tensor the bundle created
     bool tiled = false;           // MFMA-tiled weight copies made (tile_model)
     bool p16 = false;             // fp16 prefill copies of the int8 linears made (prefill_weights)
@@ -1064,8 +1066,7 @@ int decode_step(rsv_bundle *b, WorkBufs &w, GpuState &s) {
 }
 
 // ------------------------------------------------------------ prefill
-int get_seq(rsv_bundle *b, uint64_t T, uint64_t nseg) {
-    SeqBufs &q = b->seq;
+int get_seq(rsv_bundle *b, uint64_t T, uint64_t nseg, SeqBufs &q) {
     const rsv_model_info &I = b->info;
     const uint64_t C = I.n_embd;
     if (T > q.cap) {
@@ -1137,7 +1138,25 @@ bool prefill_graph_on() {
 // Packed prefill of non-empty segments into state slots; logits (optional)
 // receives nseg*vocab floats (last token of each segment).  With head set
 // and no host buffer the logits stay on the device in b->seq.logits.
-int prefill(rsv_bundle *b, GpuState &s, const std::vector<Seg> &segs, float *logits, bool head = false) {
+// Pipelined prefill (prefill_chunks): consecutive packed chunks on
+// alternating lanes (streams) of the context, each lane with its own
+// buffers.  Chunk c depends on chunk c-1 only through the state it carries:
+// per layer i, the LN1 token-shift rows (tmix_x), the WKV state (rnn) and the
+// LN2 token-shift rows (cmix_x).  So chunk c waits, per layer, for the
+// previous chunk's event after the op that leaves each of them (events 3i,
+// 3i+1, 3i+2), and everything else of the two chunks overlaps: the scan of
+// one chunk (VALU and LDS bound) runs beside the LN, LoRA-up and GEMM
+// launches of the other.  Event kLaneTail closes a chunk.
+struct LaneHooks {
+    int lane = 0;             // lane this chunk runs on
+    int prev_lane = 0;        // lane of the previous chunk
+    bool prev_layers = false; // wait for the previous chunk's per-layer events
+    bool other_tail = false;  // first wait for the other lane's last chunk to end
+};
+constexpr int kLaneTail = 255;
+
+int prefill(rsv_bundle *b, GpuState &s, const std::vector<Seg> &segs, float *logits, bool head = false,
+            const LaneHooks *lh = nullptr) {
     rsv_ctx *c = b->ctx;
     const rsv_model_info &I = b->info;
     const uint64_t C = I.n_embd, H = I.n_head, N = I.head_size;
@@ -1158,8 +1177,8 @@ int prefill(rsv_bundle *b, GpuState &s, const std::vector<Seg> &segs, float *log
     // which decode needs next) come from tile_model on both paths
     HK(tile_model(b));
     if (!small) HK(prefill_weights(b));
-    HK(get_seq(b, T, S));
-    SeqBufs &q = b->seq;
+    SeqBufs &q = lh && lh->lane == 1 ? b->seq2 : b->seq;
+    HK(get_seq(b, T, S, q));
     std::vector<uint32_t> tok(T), prev(T), st(S), ln(S), sl(S), last(S);
     uint64_t pos = 0;
     for (uint64_t g = 0; g < S; g++) {
@@ -1187,13 +1206,25 @@ int prefill(rsv_bundle *b, GpuState &s, const std::vector<Seg> &segs, float *log
     // (gpu_model.rs:2440-2507); the uploads above and the logits download
     // below stay outside the graph.
     const bool want_head = logits || head;
+    // the lane hooks: wait for the previous chunk's event k, record ours
+    auto wait_prev = [&](int k) -> int {
+        if (lh && lh->prev_layers) CK(rsv_lane_wait(c, lh->prev_lane, k));
+        return 0;
+    };
+    auto record = [&](int k) -> int {
+        if (lh) CK(rsv_lane_record(c, k));
+        return 0;
+    };
     auto enqueue = [&]() -> int {
+        if (lh && lh->other_tail) CK(rsv_lane_wait(c, 1 - lh->lane, kLaneTail));
         CK(rsv_gather_rows_device_f16(c, b->emb_ln, q.x, q.tok, C, T));
         for (uint64_t i = 0; i < I.n_layer; i++) {
             Layer &L = b->layers[i];
             const uint32_t coef6[6] = {L.x_r, L.x_w, L.x_k, L.x_v, L.x_a, L.x_g};
+            HK(wait_prev((int)(3 * i)));
             CK(rsv_seq_norm_mix(c, q.x, s.tmix_x[i], L.ln1_w, L.ln1_b, coef6, q.mix, 6, q.row_prev, T, C, LN_EPS));
             CK(rsv_seq_state_store(c, q.x, s.tmix_x[i], L.ln1_w, L.ln1_b, q.seg_last, q.seg_slot, S, C, LN_EPS));
+            HK(record((int)(3 * i)));
             const uint32_t xr = q.mix[0], xw = q.mix[1], xk = q.mix[2], xv = q.mix[3], xa = q.mix[4], xg = q.mix[5];
             if (small) {
                 rsv_mm_job j1[7] = {
@@ -1211,10 +1242,7 @@ int prefill(rsv_bundle *b, GpuState &s, const std::vector<Seg> &segs, float *log
                 };
                 CK(rsv_gemm_multi(c, j1, 7, T));
             }
-            if (i == 0) {
-                CK(rsv_copy_device(c, q.v, q.vf));
-                CK(rsv_copy_rows(c, q.v, s.v_first, q.seg_last, q.seg_slot, S, C));
-            }
+            if (i == 0) CK(rsv_copy_device(c, q.v, q.vf));
             if (small) {
                 rsv_mm_job j2[4] = {mm_job(L.lw2, q.wmid, q.w, 5), mm_job(L.la2, q.amid, q.a, 6),
                                     mm_job(L.lv2, q.vmid, q.v, 7), mm_job(L.lg2, q.gmid, q.g, 0)};
@@ -1235,9 +1263,14 @@ int prefill(rsv_bundle *b, GpuState &s, const std::vector<Seg> &segs, float *log
                 j2[2].aux = q.vf;
                 CK(rsv_gemm_multi(c, j2, 4, T));
             }
+            HK(wait_prev((int)(3 * i + 1)));
+            // each segment's layer-0 v of its last token is the slot's v_first
+            // (written here, after the previous chunk's write to the same slot)
+            if (i == 0) CK(rsv_copy_rows(c, q.vf, s.v_first, q.seg_last, q.seg_slot, S, C));
             CK(rsv_wkv7_seq_ragged_gate(c, s.rnn[i], q.r, q.w, q.k, q.v, q.a, L.k_k, L.k_a, L.r_k, L.lnx_w, L.lnx_b,
                                         q.g, q.yn, q.bonus, q.yg, q.seg_start, q.seg_len, q.seg_slot, S, T, H, N,
                                         GN_EPS));
+            HK(record((int)(3 * i + 1)));
             if (small) {
                 rsv_mm_job j4 = mm_job(L.ow, q.yg, q.x, 2);
                 CK(rsv_gemm_skinny(c, &j4, 1, T));
@@ -1245,8 +1278,10 @@ int prefill(rsv_bundle *b, GpuState &s, const std::vector<Seg> &segs, float *log
                 HK(gemm_lin(b, L.ow, q.yg, q.x, T, 2));
             }
             const uint32_t coef1[1] = {L.ffn_x_k};
+            HK(wait_prev((int)(3 * i + 2)));
             CK(rsv_seq_norm_mix(c, q.x, s.cmix_x[i], L.ln2_w, L.ln2_b, coef1, &q.xb, 1, q.row_prev, T, C, LN_EPS));
             CK(rsv_seq_state_store(c, q.x, s.cmix_x[i], L.ln2_w, L.ln2_b, q.seg_last, q.seg_slot, S, C, LN_EPS));
+            HK(record((int)(3 * i + 2)));
             if (small) {
                 rsv_mm_job j5 = mm_job(L.fk, q.xb, q.r2, 3);
                 CK(rsv_gemm_skinny(c, &j5, 1, T));
@@ -1263,9 +1298,10 @@ int prefill(rsv_bundle *b, GpuState &s, const std::vector<Seg> &segs, float *log
             CK(rsv_norm(c, q.xlast, b->ln_out_w, b->ln_out_b, q.xnorm, C, 1, LN_EPS, S));
             HK(gemv_lin(b, b->head, q.xnorm, q.logits, S, 0));
         }
+        HK(record(kLaneTail));
         return 0;
     };
-    if (prefill_graph_on()) {
+    if (prefill_graph_on() && !lh) {
         const uint64_t key = T | (S << 24) | ((uint64_t)want_head << 47) | ((s.serial & 0xFFFF) << 48);
         int valid = 0;
         CK(rsv_prefill_graph_valid(c, key, &valid));
@@ -1283,7 +1319,66 @@ int prefill(rsv_bundle *b, GpuState &s, const std::vector<Seg> &segs, float *log
         HK(enqueue());
     }
     if (logits) CK(rsv_download(c, q.logits, logits, S * I.vocab));
-    else if (!head) CK(rsv_synchronize(c));
+    else if (!head && !lh) CK(rsv_synchronize(c));
+    return 0;
+}
+
+// Runs packed chunks in order (the state carried from each to the next),
+// pipelined over two lanes when there are several; logits (optional) gets
+// the head's rows of the last chunk's segments.  Chunks of at most
+// kSmallPrefill rows, and the head's GEMV, run kernels that share one
+// context-wide split-K work area: such a chunk stays on its predecessor's
+// lane and first waits for the other lane's last chunk to end, so that no
+// two of them are ever in flight.
+int prefill_chunks(rsv_bundle *b, GpuState &s, const std::vector<std::vector<Seg>> &chunks, float *logits) {
+    rsv_ctx *c = b->ctx;
+    const bool lanes = b->prefill_lanes > 1 && chunks.size() > 1 && !prefill_graph_on() &&
+                       3 * b->info.n_layer <= (uint64_t)kLaneTail;
+    if (!lanes) {
+        for (size_t k = 0; k < chunks.size(); k++) HK(prefill(b, s, chunks[k], k + 1 == chunks.size() ? logits : nullptr));
+        return 0;
+    }
+    // every buffer at its final size before anything is in flight (a
+    // reallocation would free memory the other lane still uses)
+    uint64_t maxT = 0, maxS = 0;
+    for (auto &ch : chunks) {
+        uint64_t T = 0;
+        for (auto &g : ch) T += g.len;
+        maxT = std::max(maxT, T);
+        maxS = std::max<uint64_t>(maxS, ch.size());
+    }
+    HK(tile_model(b));
+    if (maxT > kSmallPrefill) HK(prefill_weights(b));
+    HK(get_seq(b, maxT, maxS, b->seq));
+    HK(get_seq(b, maxT, maxS, b->seq2));
+    bool used[2] = {false, false};
+    int rc = 0, prev_lane = -1;
+    for (size_t k = 0; k < chunks.size() && !rc; k++) {
+        uint64_t T = 0;
+        for (auto &g : chunks[k]) T += g.len;
+        const bool last = k + 1 == chunks.size();
+        const bool shared_ws = T <= kSmallPrefill || (last && logits);
+        LaneHooks h;
+        h.lane = prev_lane < 0 ? 0 : T <= kSmallPrefill ? prev_lane : 1 - prev_lane;
+        h.prev_lane = prev_lane < 0 ? 0 : prev_lane;
+        h.prev_layers = prev_lane >= 0 && prev_lane != h.lane;
+        h.other_tail = shared_ws && used[1 - h.lane];
+        if (rsv_lane_select(c, h.lane)) {
+            rc = herr("prefill lanes: %s", rsv_last_error());
+            break;
+        }
+        used[h.lane] = true;
+        rc = prefill(b, s, chunks[k], last ? logits : nullptr, false, &h);
+        prev_lane = h.lane;
+    }
+    // join: launches go to lane 0 again, after lane 1's last chunk (also after
+    // a failure, so that nothing of this call is left in flight)
+    // (rc set: the host error text is already set by the failing call)
+    int rb = rsv_lane_select(c, 0);
+    if (!rb && used[1]) rb = rsv_lane_wait(c, 1, kLaneTail);
+    if (!rb) rb = rsv_synchronize(c);
+    if (rc) return -1;
+    if (rb) return herr("prefill lanes: %s", rsv_last_error());
     return 0;
 }
 
@@ -1320,12 +1415,12 @@ static uint64_t water_fill(const std::vector<uint64_t> &rem, uint64_t cap) {
 int seq_single(rsv_bundle *b, GpuState &s, uint64_t slot, const uint32_t *tokens, uint64_t n, float *logits) {
     if (n == 0) return herr("infer_seq: empty token list");
     const uint64_t ch = b->prefill_chunk;
+    std::vector<std::vector<Seg>> chunks;
     for (uint64_t off = 0; off < n; off += ch) {
         const uint64_t len = n - off < ch ? n - off : ch;
-        std::vector<Seg> segs{{tokens + off, len, slot}};
-        HK(prefill(b, s, segs, off + len == n ? logits : nullptr));
+        chunks.push_back({{tokens + off, len, slot}});
     }
-    return 0;
+    return prefill_chunks(b, s, chunks, logits);
 }
 
 // ------------------------------------------------------------ ragged serving
@@ -1828,6 +1923,7 @@ int rsv_forward_seq_batch(rsv_bundle *b, rsv_state *s, const uint32_t *tokens, c
         return 0;
     };
     std::vector<uint64_t> done(segs.size(), 0);
+    std::vector<std::vector<Seg>> chunks;
     for (;;) {
         std::vector<uint64_t> rem(segs.size());
         for (size_t i = 0; i < segs.size(); i++) rem[i] = segs[i].len - done[i];
@@ -1842,8 +1938,14 @@ int rsv_forward_seq_batch(rsv_bundle *b, rsv_state *s, const uint32_t *tokens, c
             done[i] += take;
             used += take;
         }
-        HK(flush());
+        if (logits) {
+            HK(flush());  // every chunk's last rows feed the logits
+        } else {
+            chunks.push_back(std::move(pending));
+            pending.clear();
+        }
     }
+    if (!logits) return prefill_chunks(b, s->s, chunks, nullptr);
     HK(flush());
     return 0;
 }
@@ -1872,6 +1974,13 @@ int rsv_argmax_selfloop_batch_timed(rsv_bundle *b, rsv_state *s, const uint32_t 
     if (!b || !s || !seeds || !out || !ms) return herr("null argument");
     HK(tokens_ok(b, seeds, s->s.batch));
     return selfloop(b, s->s, seeds, n, nullptr, out, ms);
+}
+
+int rsv_set_prefill_lanes(rsv_bundle *b, int lanes) {
+    if (!b) return herr("null argument");
+    if (lanes != 1 && lanes != 2) return herr("set_prefill_lanes: lanes must be 1 or 2");
+    b->prefill_lanes = lanes;
+    return 0;
 }
 
 int rsv_set_prefill_chunk(rsv_bundle *b, uint64_t rows) {

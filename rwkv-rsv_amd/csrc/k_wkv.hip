@@ -1100,9 +1100,15 @@ int launch_wkv7_seq_ragged_gate(rsv_ctx *ctx, float *s, const float *r, const fl
         // the longest segment's dependent chain, shortened by more lanes per row
         const int blocks = h * nseg, cus = ctx->sm_count > 0 ? ctx->sm_count : 256;
         const char *e = getenv("RSV_SCAN_G");
-        const int gsel = e ? atoi(e) : (blocks * 4 <= cus ? 16 : blocks <= cus ? 8 : 0);
+        // From 16 blocks per CU (e.g. 256 sessions x 40 heads) four rows per
+        // group (one wave per block, half the LDS vector reads per state
+        // element again) keeps every SIMD busy: B=256 x T=512 5.09 -> 4.68 ms;
+        // below that it leaves SIMDs idle (64 x 64 tokens: 192 -> 208 us)
+        const int gsel = e ? atoi(e)
+                           : (blocks * 4 <= cus ? 16 : blocks <= cus ? 8 : blocks >= 16 * cus ? -4 : 0);
         if (gsel == 16) WKV_COLS_LAUNCH(16);
         else if (gsel == 8) WKV_COLS_LAUNCH(8);
+        else if (gsel == -4) WKV_ROWS_LAUNCH(4);
         else WKV_ROWS_LAUNCH(2);
 #undef WKV_COLS_LAUNCH
 #undef WKV_ROWS_LAUNCH

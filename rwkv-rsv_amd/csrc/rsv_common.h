@@ -132,6 +132,10 @@ struct rsv_ctx {
     // with the context so that graph capture never allocates)
     float *skinny_ws = nullptr;
     size_t skinny_ws_cap = 0;
+    // prefill lanes: lane 0 is the context's own stream, lane 1 a second
+    // stream made on first use; `stream` is the lane launches go to
+    hipStream_t lane[2] = {nullptr, nullptr};
+    std::vector<hipEvent_t> lane_ev[2];
 };
 
 namespace rsv {

@@ -340,6 +340,11 @@ class Bundle:
         """Rows per packed prefill chunk (1..12288; configs[4] packs <= 4096)."""
         _hchk(_host.rsv_set_prefill_chunk(self._h, ctypes.c_uint64(rows)))
 
+    def set_prefill_lanes(self, lanes):
+        """Streams of a multi-chunk prefill (1 or 2; 2 overlaps consecutive
+        chunks, bit-identical results)."""
+        _hchk(_host.rsv_set_prefill_lanes(self._h, ctypes.c_int(lanes)))
+
     def forward_seq_batch(self, state, prompts, want_logits=False):
         lens = np.array([len(p) for p in prompts], dtype=np.uint64)
         flat = _toks(np.concatenate([np.asarray(p, dtype=np.uint32) for p in prompts]))

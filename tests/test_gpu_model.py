@@ -158,6 +158,41 @@ def test_batch_prefill_and_decode_match_single(bundles):
     S.free()
 
 
+@pytest.mark.parametrize("chunk", [200, 96])
+def test_prefill_lanes_bit_identical(bundles, chunk):
+    """The pipelined prefill (consecutive packed chunks on two streams, each
+    waiting per layer only for the state its predecessor leaves) against the
+    one-stream prefill: every slot's state bit for bit, for batch prefill
+    over many chunks (chunk 200: large chunks and a small last one; 96: all
+    chunks on the batched-decode kernels) and for one long single-session
+    prompt, then the next decode step's logits bit for bit."""
+    b, m = bundles["i8"]
+    lens = [300, 17, 1, 233, 90]
+    prompts = [_prompt(l, 40 + i) for i, l in enumerate(lens)]
+    b.set_prefill_chunk(chunk)
+    try:
+        got = {}
+        for lanes in (1, 2):
+            b.set_prefill_lanes(lanes)
+            S = b.create_batch_state(len(lens))
+            seeds = b.forward_seq_batch(S, prompts)
+            states = [S.slot_back(i).view(np.uint32).copy() for i in range(len(lens))]
+            lg = b.forward_tokens_batch(S, np.asarray(seeds, np.uint32))
+            S.free()
+            b.reset()
+            lg1 = b.infer_seq(_prompt(700, 77))
+            got[lanes] = (states, np.asarray(lg).view(np.uint32).copy(), lg1.view(np.uint32).copy(),
+                          b.state_back().view(np.uint32).copy())
+        for i in range(len(lens)):
+            assert np.array_equal(got[1][0][i], got[2][0][i]), f"slot {i} state"
+        for k in (1, 2, 3):
+            assert np.array_equal(got[1][k], got[2][k])
+    finally:
+        b.set_prefill_lanes(2)
+        b.set_prefill_chunk(12288)
+        b.reset()
+
+
 def test_forward_tokens_batch_matches_single(bundles):
     b, m = bundles["f32"]
     S = b.create_batch_state(3)

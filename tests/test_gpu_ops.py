@@ -328,7 +328,7 @@ def test_wkv7_seq_ragged_matches_decode_loop(be):
         pos += lens[g]
 
 
-@pytest.mark.parametrize("scan_g", ["", "16", "8", "0"])
+@pytest.mark.parametrize("scan_g", ["", "16", "8", "0", "-4"])
 @pytest.mark.parametrize("lens", [[300, 212], [8] * 48 + [40], [512]])
 def test_wkv7_seq_ragged_gate_matches_scan_times_gate(be, lens, scan_g, monkeypatch):
     """rsv_wkv7_seq_ragged_gate leaves (GroupNorm(y) + bonus*v) * g in fp16:
@@ -336,7 +336,7 @@ def test_wkv7_seq_ragged_gate_matches_scan_times_gate(be, lens, scan_g, monkeypa
     GroupNorm pass, with many the one-wave scan; both against
     rsv_wkv7_seq_ragged's yn times g (and its state) to rounding.  scan_g
     forces the scan form (16 or 8 lanes per state row, 0 the two-rows-per-
-    group form; empty: chosen by the block count)."""
+    group form, -4 four rows per group; empty: chosen by the block count)."""
     rsv = _rsv()
     if scan_g:
         monkeypatch.setenv("RSV_SCAN_G", scan_g)
