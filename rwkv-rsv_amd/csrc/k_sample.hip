@@ -996,62 +996,66 @@ __global__ __launch_bounds__(1024) void k_samp_pick(const float *__restrict__ lo
     // 2. pass 1 over e: the 112-lane sums, the elements of the bins above
     // the boundary (fewer than R: all of them are taken), and a histogram of
     // the next 12 key bits of the elements in the boundary bin and the one
-    // below it
+    // below it.  Waves 0-1 form the sums (lane t < 112 adds e[t], e[t+112],
+    // ... in that order) straight from global memory with 32 loads in flight
+    // per lane, while the other 14 waves gather and count: the sums are a
+    // dependent chain of n/112 adds, which staged through LDS pieces with the
+    // other waves waiting at barriers took most of this kernel's time
     const uint32_t bin = ps.bin, lowbin = bin > 0u ? bin - 1u : 0u;
     for (int q = tid; q < 8192; q += 1024) ps.fh[q] = 0u;
-    float s112 = 0.0f;
-    float4 cur[4];
-    auto load_piece = [&](int c0) {
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const int i = c0 + 4096 * q + 4 * tid;
-            if (i + 3 < n) {
-                cur[q] = *(const float4 *)(e_row + i);
-            } else {
-                cur[q].x = i < n ? e_row[i] : 0.0f;
-                cur[q].y = i + 1 < n ? e_row[i + 1] : 0.0f;
-                cur[q].z = i + 2 < n ? e_row[i + 2] : 0.0f;
-                cur[q].w = i + 3 < n ? e_row[i + 3] : 0.0f;
-            }
-        }
-    };
+    __syncthreads();
     auto take = [&](float ev, int i) {
         const uint32_t slot = atomicAdd(&ps.ncand, 1u);
         if (slot < (uint32_t)kPickMax) { ps.ce[slot] = ev; ps.ci[slot] = i; }
     };
-    load_piece(0);
-    for (int c0 = 0; c0 < n; c0 += 16384) {
-        __syncthreads();  // the previous piece's sums are done with ps.chunk
+    if (tid < 128) {
+        if (tid < 112) {
+            constexpr int D = 32;
+            const int nj = (n - tid + 111) / 112;  // this lane's elements: tid + 112 j < n
+            const float *er = e_row + tid;
+            float r[D];
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-            *(float4 *)(ps.chunk + 4096 * q + 4 * tid) = cur[q];
-            const float ev[4] = {cur[q].x, cur[q].y, cur[q].z, cur[q].w};
+            for (int k = 0; k < D; k++) r[k] = k < nj ? er[112 * k] : 0.0f;
+            float s112 = 0.0f;
+            int j = 0;
+            // (unconditional refills while two windows remain: a conditional
+            // load per element becomes a branch, and the waits at the joins
+            // drain the loads in flight)
+            for (; j + 2 * D <= nj; j += D) {
+#pragma unroll
+                for (int k = 0; k < D; k++) {
+                    s112 += r[k];
+                    r[k] = er[(size_t)112 * (j + D + k)];
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < D; k++)
+                if (j + k < nj) s112 += r[k];
+            for (int jj = j + D; jj < nj; jj++) s112 += er[(size_t)112 * jj];
+            ps.part[tid] = s112;
+        }
+    } else {
+        for (int i = 4 * (tid - 128); i < n; i += 4 * 896) {
+            float4 c;
+            if (i + 3 < n) {
+                c = *(const float4 *)(e_row + i);
+            } else {
+                c.x = e_row[i];
+                c.y = i + 1 < n ? e_row[i + 1] : 0.0f;
+                c.z = i + 2 < n ? e_row[i + 2] : 0.0f;
+                c.w = i + 3 < n ? e_row[i + 3] : 0.0f;
+            }
+            const float ev[4] = {c.x, c.y, c.z, c.w};
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                const int i = c0 + 4096 * q + 4 * tid + e;
                 const uint32_t kk = fkey(ev[e]), cb = kk >> 20;
-                if (i >= n || cb < lowbin) continue;
-                take(ev[e], i);
+                if (i + e >= n || cb < lowbin) continue;
+                take(ev[e], i + e);
                 if (cb > bin) atomicAdd(&ps.ndef, 1u);
                 else atomicAdd(&ps.fh[((cb - lowbin) << 12) | ((kk >> 8) & 0xFFFu)], 1u);
             }
         }
-        __syncthreads();
-        if (c0 + 16384 < n) load_piece(c0 + 16384);  // in flight while the lanes add
-        if (tid < 112) {
-            const int hi = min(n, c0 + 16384);
-            int i = c0 + (((tid - c0) % 112) + 112) % 112;
-            for (; i + 7 * 112 < hi; i += 8 * 112) {
-                float v[8];
-#pragma unroll
-                for (int e = 0; e < 8; e++) v[e] = ps.chunk[i + 112 * e - c0];
-#pragma unroll
-                for (int e = 0; e < 8; e++) s112 += v[e];
-            }
-            for (; i < hi; i += 112) s112 += ps.chunk[i - c0];
-        }
     }
-    if (tid < 112) ps.part[tid] = s112;
     __syncthreads();
     if (tid == 0) {
         for (int q = 0; q < 48; q++) ps.part[q] += ps.part[q + 64];
@@ -1109,17 +1113,20 @@ __global__ __launch_bounds__(1024) void k_samp_pick(const float *__restrict__ lo
         __syncthreads();
         if (tid == 0) ps.ncand = 0u;
         __syncthreads();
-        for (int c0 = 0; c0 < n; c0 += 16384) {
-            load_piece(c0);
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const float ev[4] = {cur[q].x, cur[q].y, cur[q].z, cur[q].w};
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const int i = c0 + 4096 * q + 4 * tid + e;
-                    if (i < n && wanted(ev[e])) take(ev[e], i);
-                }
+        for (int i = 4 * tid; i < n; i += 4 * 1024) {
+            float4 c;
+            if (i + 3 < n) {
+                c = *(const float4 *)(e_row + i);
+            } else {
+                c.x = e_row[i];
+                c.y = i + 1 < n ? e_row[i + 1] : 0.0f;
+                c.z = i + 2 < n ? e_row[i + 2] : 0.0f;
+                c.w = i + 3 < n ? e_row[i + 3] : 0.0f;
             }
+            const float ev[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                if (i + e < n && wanted(ev[e])) take(ev[e], i + e);
         }
     }
     __syncthreads();
