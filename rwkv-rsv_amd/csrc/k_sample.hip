@@ -240,6 +240,9 @@ __device__ uint32_t radix_select_regs(const uint32_t (&kr)[PER], int cnt, int R,
 }
 
 // Bitonic sort of sh.ckey/cidx[0..kCand): descending by key, ascending by index.
+// A stage of stride < 64 pairs elements of one wave's 64 (thread i handles
+// i and i ^ stride), so it needs only the wave's own LDS order, not a block
+// barrier: 6 block barriers for 512 entries instead of 45.
 __device__ void cand_sort(SampShared &sh) {
     for (int size = 2; size <= kCand; size <<= 1) {
         for (int stride = size >> 1; stride > 0; stride >>= 1) {
@@ -257,9 +260,19 @@ __device__ void cand_sort(SampShared &sh) {
                     }
                 }
             }
-            __syncthreads();
+            // the next stage's pairs stay in the wave only if its stride is
+            // below 64 too
+            if (stride > 64) {
+                __syncthreads();
+            } else if (stride == 64 || (stride == 1 && size < kCand && 2 * size > 64)) {
+                __syncthreads();
+            } else {
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                __builtin_amdgcn_wave_barrier();
+            }
         }
     }
+    __syncthreads();
 }
 
 // Gathers the R largest keys (ties at the threshold by ascending index) into
@@ -934,7 +947,7 @@ struct PickShared {
     double dred[1024];
     uint32_t lcnt[112], loff[112], lcur[112];
     double dtot;
-    int flat, chosen;
+    int flat, chosen, cutok;
     float ce[kPickMax];      // gathered candidates: e, then p; at the end the kept set in index order
     int ci[kPickMax];
     union {
@@ -1214,35 +1227,71 @@ __global__ __launch_bounds__(1024) void k_samp_pick(const float *__restrict__ lo
             }
         }
         __syncthreads();
-        for (int r = tid; r < R; r += 1024) {
-            const uint64_t cv = ps.comp[r];
-            int rank = 0;
-            for (int j0 = 0; j0 < R; j0 += 16) {
-                uint64_t w[16];
-#pragma unroll
-                for (int e = 0; e < 16; e++) w[e] = j0 + e < R ? ps.comp[j0 + e] : 0ull;
-#pragma unroll
-                for (int e = 0; e < 16; e++) rank += w[e] > cv;
-            }
-            ps.psort[rank] = fkey_inv((uint32_t)(cv >> 32));
+        // sorted order: bitonic sort of the R keys (key desc, index asc) in
+        // the pipeline's candidate area, free once the radix select is done
+        // (a rank count over all keys per thread cost 15-24 us per row)
+        for (int r = tid; r < kCand; r += 1024) {
+            const uint64_t cv = r < R ? ps.comp[r] : 0ull;
+            ps.sh.ckey[r] = r < R ? (uint32_t)(cv >> 32) : 0u;
+            ps.sh.cidx[r] = r < R ? (int)~(uint32_t)cv : 0x7FFFFFFF;
         }
         __syncthreads();
-        // the sequential pass on wave 0 (values broadcast by readlane)
-        if (tid < 64) {
-            float vals[kCand / 64];
+        cand_sort(ps.sh);
+        for (int r = tid; r < R; r += 1024) ps.psort[r] = fkey_inv(ps.sh.ckey[r]);
+        __syncthreads();
+        // The sequential fp32 pass adds entry q while the sum of entries
+        // 0..q-1 is below top_p and cuts at the last one added.  Its sums
+        // differ from the exact ones by at most (q+1) 2^-24 of them, so where
+        // the double prefix sums clear top_p by (q+2) 2^-23 max(sum, top_p)
+        // on both sides of their crossing, the pass stops at that crossing
+        // too; otherwise it runs below as written
+        {
+            // inclusive double prefix: a scan per wave, then the waves' totals
+            double v = tid < R ? (double)ps.psort[tid] : 0.0;
+            const int ln = tid & 63;
 #pragma unroll
-            for (int m = 0; m < kCand / 64; m++) vals[m] = tid + 64 * m < R ? ps.psort[tid + 64 * m] : 0.0f;
+            for (int d = 1; d < 64; d <<= 1) {
+                const double t = __shfl_up(v, d);
+                if (ln >= d) v += t;
+            }
+            if (ln == 63) ps.dred[1008 + (tid >> 6)] = v;
+            if (tid == 0) ps.cutok = 0;
+            __syncthreads();
+            double off = 0.0;
+            for (int w = 0; w < (tid >> 6); w++) off += ps.dred[1008 + w];
+            __syncthreads();
+            ps.dred[tid] = v + off;
+            __syncthreads();
+        }
+        if (tid < R) {
+            const double tp = (double)top_p, c = ps.dred[tid], cp = tid ? ps.dred[tid - 1] : 0.0;
+            const double mc = (tid + 2) * 0x1p-23 * fmax(c, tp), mp = (tid + 1) * 0x1p-23 * fmax(cp, tp);
+            if (c >= tp && cp < tp && c >= tp + mc && (tid == 0 || cp < tp - mp)) {
+                ps.cut = ps.psort[tid];
+                ps.cutok = 1;
+            }
+            if (tid == R - 1 && c < tp - mc) {
+                ps.cut = ps.psort[R - 1];
+                ps.cutok = 1;
+            }
+        }
+        __syncthreads();
+        // otherwise the sequential pass itself, on one lane (16 values read
+        // per batch, then added in order)
+        if (!ps.cutok && tid == 0) {
             float cum = 0.0f, cut = 0.0f;
+            for (int q0 = 0; q0 < R; q0 += 16) {
+                float v[16];
 #pragma unroll
-            for (int m = 0; m < kCand / 64; m++) {
-                const int cnt = min(64, R - 64 * m);
-                for (int q = 0; q < cnt && cum < top_p; q++) {
-                    const float v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(vals[m]), q));
-                    cum += v;
-                    cut = v;
+                for (int e = 0; e < 16; e++) v[e] = q0 + e < R ? ps.psort[q0 + e] : 0.0f;
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    const bool go = q0 + e < R && cum < top_p;
+                    cut = go ? v[e] : cut;
+                    cum = go ? cum + v[e] : cum;
                 }
             }
-            if (tid == 0) ps.cut = cut;
+            ps.cut = cut;
         }
     }
     // 6. the kept entries (p >= cut; every one is a candidate) in index
