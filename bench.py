@@ -505,7 +505,7 @@ def main():
         # 12,288-row chunks (fuller GEMM tile rounds) are reported beside it
         dt = timed_prefill(4096)
         dt12 = timed_prefill(12288)
-        bundle.set_prefill_chunk(12288)
+        bundle.set_prefill_chunk(4096)
         prefill = dict(tokens=int(lens.sum()), chunk_rows=4096, seconds=dt, tok_s=float(lens.sum() / dt),
                        tok_s_12288_row_chunks=float(lens.sum() / dt12),
                        note="tok_s packs <= 4096-token ragged batches as configs[4]; the 12,288-row figure "

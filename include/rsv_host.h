@@ -117,8 +117,9 @@ int rsv_serve_ragged_logits(rsv_bundle *b, rsv_state *s, const uint32_t *tokens,
                             float *sampled_logits);
 
 /* Rows per packed prefill chunk of infer_seq / forward_seq_batch (1..12288,
- * default 12288).  The reference packs ragged serving batches of <= 4096
- * tokens; larger chunks fill more GEMM tile rounds per launch. */
+ * default 4096, the reference's packing bound for ragged batches).  Larger
+ * chunks fill more GEMM tile rounds per launch; with consecutive chunks
+ * overlapped on two streams (rsv_set_prefill_lanes) 4096 is the faster. */
 int rsv_set_prefill_chunk(rsv_bundle *b, uint64_t rows);
 
 /* Streams a multi-chunk prefill uses (1 or 2, default 2).  With 2, consecutive

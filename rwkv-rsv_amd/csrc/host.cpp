@@ -304,7 +304,7 @@ struct rsv_state {
 
 struct rsv_bundle {
     rsv_ctx *ctx = nullptr;
-    uint64_t prefill_chunk = 12288;  // packed prefill rows per chunk (rsv_set_prefill_chunk)
+    uint64_t prefill_chunk = 4096;   // packed prefill rows per chunk (rsv_set_prefill_chunk)
     rsv_model_info info{};
     uint32_t emb_ln = NONE, ln_out_w = NONE, ln_out_b = NONE, scale_w = NONE;
     Linear head;

@@ -337,7 +337,7 @@ class Bundle:
         return State(self, h, batch)
 
     def set_prefill_chunk(self, rows):
-        """Rows per packed prefill chunk (1..12288; configs[4] packs <= 4096)."""
+        """Rows per packed prefill chunk (1..12288, default 4096: the reference's packing bound)."""
         _hchk(_host.rsv_set_prefill_chunk(self._h, ctypes.c_uint64(rows)))
 
     def set_prefill_lanes(self, lanes):

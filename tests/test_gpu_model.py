@@ -189,7 +189,7 @@ def test_prefill_lanes_bit_identical(bundles, chunk):
             assert np.array_equal(got[1][k], got[2][k])
     finally:
         b.set_prefill_lanes(2)
-        b.set_prefill_chunk(12288)
+        b.set_prefill_chunk(4096)
         b.reset()
 
 
