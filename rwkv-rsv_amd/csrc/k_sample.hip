@@ -1015,6 +1015,7 @@ __global__ __launch_bounds__(1024) void k_samp_pick(const float *__restrict__ lo
     // dependent chain of n/112 adds, which staged through LDS pieces with the
     // other waves waiting at barriers took most of this kernel's time
     const uint32_t bin = ps.bin, lowbin = bin > 0u ? bin - 1u : 0u;
+    const float elo = lowbin > 0u ? fkey_inv(lowbin << 20) : -1.0f;  // the smallest value of bin lowbin
     for (int q = tid; q < 8192; q += 1024) ps.fh[q] = 0u;
     __syncthreads();
     auto take = [&](float ev, int i) {
@@ -1022,7 +1023,25 @@ __global__ __launch_bounds__(1024) void k_samp_pick(const float *__restrict__ lo
         if (slot < (uint32_t)kPickMax) { ps.ce[slot] = ev; ps.ci[slot] = i; }
     };
     if (tid < 128) {
-        if (tid < 112) {
+        if (PER > 0 && tid < 112) {
+            // n = PER * kSampBS is known here: the chain is unrolled whole, so
+            // that the load of element j + D goes out right after the add of
+            // element j with an exact wait for each add (a loop's back edge
+            // makes the compiler wait for every load in flight at its head)
+            constexpr int NN = PER * kSampBS, NJ0 = NN / 112, D = 32;
+            const float *er = e_row + tid;
+            float r[D];
+#pragma unroll
+            for (int k = 0; k < D; k++) r[k] = er[112 * k];
+            float s112 = 0.0f;
+#pragma unroll
+            for (int j = 0; j < NJ0; j++) {
+                s112 += r[j % D];
+                if (j + D < NJ0) r[j % D] = er[112 * (j + D)];
+            }
+            if (tid < NN - 112 * NJ0) s112 += er[112 * NJ0];
+            ps.part[tid] = s112;
+        } else if (tid < 112) {
             constexpr int D = 32;
             const int nj = (n - tid + 111) / 112;  // this lane's elements: tid + 112 j < n
             const float *er = e_row + tid;
@@ -1047,6 +1066,35 @@ __global__ __launch_bounds__(1024) void k_samp_pick(const float *__restrict__ lo
             for (int jj = j + D; jj < nj; jj++) s112 += er[(size_t)112 * jj];
             ps.part[tid] = s112;
         }
+    } else if (PER > 0) {
+        // the loads of 8 float4 per lane go out before any is used (a loop
+        // with one load per trip waits for it at every trip's head)
+        constexpr int NN = PER * kSampBS, ITS = (NN + 4 * 896 - 1) / (4 * 896), BT = 8;
+#pragma unroll
+        for (int i0 = 0; i0 < ITS; i0 += BT) {
+            float4 cv[BT];
+#pragma unroll
+            for (int u = 0; u < BT; u++) {
+                const int i = 4 * (tid - 128) + (i0 + u) * 4 * 896;
+                cv[u] = i0 + u < ITS && i < NN ? *(const float4 *)(e_row + i) : make_float4(-1.0f, -1.0f, -1.0f, -1.0f);
+            }
+#pragma unroll
+            for (int u = 0; u < BT; u++) {
+                const int i = 4 * (tid - 128) + (i0 + u) * 4 * 896;
+                const float4 c = cv[u];
+                if (i0 + u >= ITS || i >= NN) continue;
+                if (fmaxf(fmaxf(c.x, c.y), fmaxf(c.z, c.w)) < elo) continue;
+                const float ev[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const uint32_t kk = fkey(ev[e]), cb = kk >> 20;
+                    if (cb < lowbin) continue;
+                    take(ev[e], i + e);
+                    if (cb > bin) atomicAdd(&ps.ndef, 1u);
+                    else atomicAdd(&ps.fh[((cb - lowbin) << 12) | ((kk >> 8) & 0xFFFu)], 1u);
+                }
+            }
+        }
     } else {
         for (int i = 4 * (tid - 128); i < n; i += 4 * 896) {
             float4 c;
@@ -1058,6 +1106,9 @@ __global__ __launch_bounds__(1024) void k_samp_pick(const float *__restrict__ lo
                 c.z = i + 2 < n ? e_row[i + 2] : 0.0f;
                 c.w = i + 3 < n ? e_row[i + 3] : 0.0f;
             }
+            // e >= 0, so key order is float order: one compare rejects the
+            // elements below the candidate bins (most of the row)
+            if (fmaxf(fmaxf(c.x, c.y), fmaxf(c.z, c.w)) < elo) continue;
             const float ev[4] = {c.x, c.y, c.z, c.w};
 #pragma unroll
             for (int e = 0; e < 4; e++) {
