@@ -389,22 +389,27 @@ __global__ __launch_bounds__(256, SB == 4 ? 3 : 2) void k_wkv7_lora_mb(WkvLoraAr
             wl[e] = *((const uint4 *)(up + (size_t)(h * 64 + wave * 16 + li) * mid + (k - off)) + g);
         }
     }
-    // 1b. the block's LoRA inputs, session-major, 16-byte pieces
+    // 1b. the block's LoRA inputs, session-major, 16-byte pieces (at most
+    // NP per thread: SB * L4 / 8 <= SB * 64), held in registers until the
+    // state loads below are issued, so that the HBM stream of the state
+    // starts at entry
+    constexpr int NP = (SB * 64 + 255) / 256;
     const int ppr = L4 >> 3;  // pieces per session
-    for (int e = tid; e < SB * ppr; e += 256) {
-        const int sl = e / ppr, k = (e - sl * ppr) * 8, b = b0 + sl;
-        const int m = (k >= moff[1]) + (k >= moff[2]) + (k >= moff[3]);
-        const _Float16 *src = (const _Float16 *)(m == 0 ? A.mid[0] : m == 1 ? A.mid[1] : m == 2 ? A.mid[2] : A.mid[3]);
-        const int mid = m == 0 ? A.mid_n[0] : m == 1 ? A.mid_n[1] : m == 2 ? A.mid_n[2] : A.mid_n[3];
-        const int off = m == 0 ? 0 : m == 1 ? moff[1] : m == 2 ? moff[2] : moff[3];
-        uint4 v = make_uint4(0u, 0u, 0u, 0u);
-        if (b < batch) v = *(const uint4 *)(src + (size_t)b * mid + (k - off));
-        *(uint4 *)&xs[sl * XS + k] = v;
+    uint4 xv[NP];
+#pragma unroll
+    for (int q = 0; q < NP; q++) {
+        const int e = tid + 256 * q, sl = e / ppr, k = (e - sl * ppr) * 8;
+        xv[q] = make_uint4(0u, 0u, 0u, 0u);
+        if (e < SB * ppr && b0 + sl < batch) {
+            const int m = (k >= moff[1]) + (k >= moff[2]) + (k >= moff[3]);
+            const _Float16 *src = (const _Float16 *)(m == 0 ? A.mid[0] : m == 1 ? A.mid[1] : m == 2 ? A.mid[2] : A.mid[3]);
+            const int mid = m == 0 ? A.mid_n[0] : m == 1 ? A.mid_n[1] : m == 2 ? A.mid_n[2] : A.mid_n[3];
+            const int off = m == 0 ? 0 : m == 1 ? moff[1] : m == 2 ? moff[2] : moff[3];
+            xv[q] = *(const uint4 *)(src + (size_t)(b0 + sl) * mid + (k - off));
+        }
     }
     // 1c. the first session's state rows and vectors of this wave
     const int c = h * 64 + lane;
-    const float w0 = A.w0[c], a0 = A.a0[c], v0 = A.v0[c], kkc = A.kk[c], kac = A.ka[c], rkc = A.rk[c];
-    const float gam = A.gamma[c], bet = A.beta[c], sw = A.scale[0];
     float4 st[16];
     float nk = 0.0f, nr = 0.0f, nv = 0.0f, nvf = 0.0f;
     // (a session index past the batch reads session b0, which always exists;
@@ -417,8 +422,15 @@ __global__ __launch_bounds__(256, SB == 4 ? 3 : 2) void k_wkv7_lora_mb(WkvLoraAr
         const size_t vq = (size_t)bq * C + c;                                              \
         nk = A.k[vq]; nr = A.r[vq]; nv = A.v[vq]; nvf = A.vf[vq];                          \
     }
+    __builtin_amdgcn_sched_barrier(0);
     WKV_MB_LOAD_SESSION(wave)
-    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int q = 0; q < NP; q++) {
+        const int e = tid + 256 * q, sl = e / ppr, k = (e - sl * ppr) * 8;
+        if (e < SB * ppr) *(uint4 *)&xs[sl * XS + k] = xv[q];
+    }
+    __syncthreads();  // (the state loads stay in flight through the dots)
 
     // 1d. LoRA-up dots: rows 16*wave + 4g + q (q = 0..3) for session li; one
     // accumulator, flushed to LDS where the matrix changes (uniform branch)
@@ -449,11 +461,15 @@ __global__ __launch_bounds__(256, SB == 4 ? 3 : 2) void k_wkv7_lora_mb(WkvLoraAr
         }
         flush(mcur);
     }
-    if (h == 0 && A.side_dst)
-        for (int e = tid; e < SB * C; e += 256) {
-            const int b = b0 + e / C;
-            if (b < batch) A.side_dst[(size_t)b * C + e % C] = A.side_src[(size_t)b * C + e % C];
-        }
+    // the channel constants of phase 2, loaded only now: with the weight
+    // ring and the state both in registers they would be spilled
+    const float w0 = A.w0[c], a0 = A.a0[c], v0 = A.v0[c], kkc = A.kk[c], kac = A.ka[c], rkc = A.rk[c];
+    const float gam = A.gamma[c], bet = A.beta[c], sw = A.scale[0];
+    // side copy: this block's sessions x the head's 64 channels
+    for (int e = tid; e < SB * 64; e += 256) {
+        const int b = b0 + (e >> 6);
+        if (A.side_dst && b < batch) A.side_dst[(size_t)b * C + c - lane + (e & 63)] = A.side_src[(size_t)b * C + c - lane + (e & 63)];
+    }
     __syncthreads();
 
     // 2. WKV7 step of sessions wave, wave + 4, ... (model.rs:445-473, 716-826)
