@@ -345,11 +345,19 @@ __global__ __launch_bounds__(256) void k_wkv7_lora(WkvLoraArgs A) {
 //      inputs staged in LDS, fp32 accumulation).  A 16-byte piece of lane
 //      (i = l%16, g = l/16) covers k = 32e + 8g .. +7 of both operands and
 //      feeds two MFMAs, so A and B pair up on the same k;
-//   2. the dots pass through LDS to the WKV7 step, where wave w runs sessions
-//      w, w+4, ... with the lane-per-row layout of k_wkv7_decode (its state
-//      transpose tile and head vectors private to the wave, so the step needs
-//      no block barrier); the next session's state and vectors are loaded
-//      while the current one is computed.
+//   2. the dots pass through LDS to the WKV7 step, where wave w runs session
+//      w on the state as loaded (16 lanes per row, no transpose; its head
+//      vectors private to the wave, so the step needs no block barrier).
+// Sum over a 16-lane DPP row; every lane of the row gets the same value
+// (each step adds a lane's value and its partner's, commutatively).
+__device__ __forceinline__ float row16_sum(float v) {
+    v += quad_dpp<0xB1>(v);  // quad_perm 1,0,3,2
+    v += quad_dpp<0x4E>(v);  // quad_perm 2,3,0,1
+    v += quad_dpp<0x141>(v); // row_half_mirror
+    v += quad_dpp<0x140>(v); // row_mirror: every lane of the 16-lane row holds its sum
+    return v;
+}
+
 typedef _Float16 wk_h4 __attribute__((ext_vector_type(4)));
 typedef float wk_f4 __attribute__((ext_vector_type(4)));
 
@@ -358,8 +366,9 @@ __global__ __launch_bounds__(256, SB == 4 ? 3 : 2) void k_wkv7_lora_mb(WkvLoraAr
     constexpr int XS = 512 + 8;  // LDS row stride (halves) of one session's inputs (ranks sum <= 512)
     __shared__ __attribute__((aligned(16))) _Float16 xs[SB * XS];
     __shared__ float dots[4][64][SB + 1];
-    __shared__ float tile[4][32 * 65];
-    __shared__ HeadVecs hvs[4];
+    __shared__ __attribute__((aligned(16))) HeadVecs hvs[4];
+    __shared__ __attribute__((aligned(16))) float rowv[4][64];
+    static_assert(SB <= 4, "one session per wave");
     const int h = blockIdx.x, b0 = blockIdx.y * SB, tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int li = lane & 15, g = lane >> 4;
@@ -472,58 +481,64 @@ __global__ __launch_bounds__(256, SB == 4 ? 3 : 2) void k_wkv7_lora_mb(WkvLoraAr
     }
     __syncthreads();
 
-    // 2. WKV7 step of sessions wave, wave + 4, ... (model.rs:445-473, 716-826)
-    float *tl = tile[wave];
+    // 2. WKV7 step of session wave (model.rs:445-473, 716-826).  The state
+    // stays in the layout it was loaded in: lane l holds columns
+    // 4(l%16) .. +3 of rows 4m + l/16 (m = 0..15), so each row lies in one
+    // 16-lane DPP row and its dot products are 4-column partials summed
+    // over that row.  Per-column vectors are formed lane-per-column as in
+    // k_wkv7_decode and read back as the lane's four columns.
     HeadVecs &hv = hvs[wave];
-    for (int sl = wave; sl < SB && b0 + sl < batch; sl += 4) {
-        const int b = b0 + sl;
-        const float kc = nk, rc = nr, vc = nv, vfc = nvf;
-        float s[64];
-#pragma unroll
-        for (int half = 0; half < 2; half++) {
-#pragma unroll
-            for (int m = 8 * half; m < 8 * half + 8; m++) {
-                const int e = (m * 64 + lane) * 4, row = (e >> 6) - 32 * half, col = e & 63;
-                tl[row * 65 + col + 0] = st[m].x;
-                tl[row * 65 + col + 1] = st[m].y;
-                tl[row * 65 + col + 2] = st[m].z;
-                tl[row * 65 + col + 3] = st[m].w;
-            }
-            __builtin_amdgcn_wave_barrier();
-            if ((lane >> 5) == half) {
-#pragma unroll
-                for (int j = 0; j < 64; j++) s[j] = tl[(lane & 31) * 65 + j];
-            }
-            __builtin_amdgcn_wave_barrier();
-        }
-        if (sl + 4 < SB) WKV_MB_LOAD_SESSION(sl + 4)  // in flight during this session's step
+    float *vr = rowv[wave];  // v by row group: [l%4][l/4] for row l; then y by row
+    if (wave < SB && b0 + wave < batch) {
+        const int b = b0 + wave, sl = wave;
+        const int rg = lane >> 4, cq = lane & 15;
         const float wd = expf(sig_f(dots[0][lane][sl] + w0) * sw);
         const float aa = sig_f(dots[1][lane][sl] + a0);
-        const float vv = vc + sig_f(dots[2][lane][sl] + v0) * (vfc - vc);
+        const float vv = nv + sig_f(dots[2][lane][sl] + v0) * (nvf - nv);
         const float gg = dots[3][lane][sl];
         float kmod;
-        head_vectors(hv, lane, kc, kkc, aa, kac, rc, wd, A.eps, kmod);
+        head_vectors(hv, lane, nk, kkc, aa, kac, nr, wd, A.eps, kmod);
+        vr[(lane & 3) * 16 + (lane >> 2)] = vv;
         __builtin_amdgcn_wave_barrier();
-        const float y = row_update(s, hv, vv);
-        const float yn = head_norm(y, gam, bet, rc * kmod * rkc, vv, A.gn_eps);
-        ((_Float16 *)A.yg)[(size_t)b * C + c] = (_Float16)(yn * gg);
+        const float4 kh4 = *(const float4 *)&hv.kh[4 * cq], bv4 = *(const float4 *)&hv.bv[4 * cq];
+        const float4 wv4 = *(const float4 *)&hv.wv[4 * cq], km4 = *(const float4 *)&hv.km[4 * cq];
+        const float4 rv4 = *(const float4 *)&hv.rv[4 * cq];
+        float vrow[16];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const float4 t = *(const float4 *)&vr[rg * 16 + 4 * q];
+            vrow[4 * q] = t.x; vrow[4 * q + 1] = t.y; vrow[4 * q + 2] = t.z; vrow[4 * q + 3] = t.w;
+        }
+        float ymine = 0.0f;  // y of row 4 cq + rg
+#pragma unroll
+        for (int m = 0; m < 16; m++) {
+            float4 &q = st[m];
+            float sa = q.x * kh4.x;
+            sa = fmaf(q.y, kh4.y, sa);
+            sa = fmaf(q.z, kh4.z, sa);
+            sa = fmaf(q.w, kh4.w, sa);
+            sa = row16_sum(sa);
+            const float vi = vrow[m];
+            q.x = q.x * wv4.x + sa * bv4.x + vi * km4.x;
+            q.y = q.y * wv4.y + sa * bv4.y + vi * km4.y;
+            q.z = q.z * wv4.z + sa * bv4.z + vi * km4.z;
+            q.w = q.w * wv4.w + sa * bv4.w + vi * km4.w;
+            float y = q.x * rv4.x;
+            y = fmaf(q.y, rv4.y, y);
+            y = fmaf(q.z, rv4.z, y);
+            y = fmaf(q.w, rv4.w, y);
+            y = row16_sum(y);
+            ymine = cq == m ? y : ymine;
+        }
         float4 *Sg = (float4 *)(A.S + ((size_t)b * H + h) * 4096);
 #pragma unroll
-        for (int half = 0; half < 2; half++) {
-            __builtin_amdgcn_wave_barrier();
-            if ((lane >> 5) == half) {
-#pragma unroll
-                for (int j = 0; j < 64; j++) tl[(lane & 31) * 65 + j] = s[j];
-            }
-            __builtin_amdgcn_wave_barrier();
-#pragma unroll
-            for (int m = 8 * half; m < 8 * half + 8; m++) {
-                const int e = (m * 64 + lane) * 4, row = (e >> 6) - 32 * half, col = e & 63;
-                Sg[m * 64 + lane] = make_float4(tl[row * 65 + col], tl[row * 65 + col + 1], tl[row * 65 + col + 2],
-                                                tl[row * 65 + col + 3]);
-            }
-        }
+        for (int m = 0; m < 16; m++) Sg[m * 64 + lane] = st[m];
         __builtin_amdgcn_wave_barrier();
+        vr[4 * cq + rg] = ymine;  // (every lane has read its v rows above)
+        __builtin_amdgcn_wave_barrier();
+        const float y = vr[lane];
+        const float yn = head_norm(y, gam, bet, nr * kmod * rkc, vv, A.gn_eps);
+        ((_Float16 *)A.yg)[(size_t)b * C + c] = (_Float16)(yn * gg);
     }
 #undef WKV_MB_LOAD_SESSION
 }
@@ -545,13 +560,6 @@ __global__ __launch_bounds__(256, SB == 4 ? 3 : 2) void k_wkv7_lora_mb(WkvLoraAr
 //   quad sums); v and g with 16 threads per row (row 16p + tid/16).
 //   State: row 16p + tid/16, columns 4*(tid%16) .. +3; the row sums S k_hat
 //   and S r are 16-lane DPP row sums.
-__device__ __forceinline__ float row16_sum(float v) {
-    v += quad_dpp<0xB1>(v);  // quad_perm 1,0,3,2
-    v += quad_dpp<0x4E>(v);  // quad_perm 2,3,0,1
-    v += quad_dpp<0x141>(v); // row_half_mirror
-    v += quad_dpp<0x140>(v); // row_mirror: every lane of the 16-lane row holds its sum
-    return v;
-}
 
 __global__ __launch_bounds__(256) void k_wkv7_lora_rows(WkvLoraArgs A) {
     __shared__ float mids[1024];
