@@ -839,8 +839,15 @@ __device__ constexpr int sk8p_younger(int s, int nx, int lw) {
 // barrier per step, so every x byte read from L2 feeds 64 weight rows.
 // Blocks then number fewer than CUs and each CU reads 491 KiB instead of up
 // to 2 x 409 KiB (ffn.key at B=64: 18.0 -> 15.8 us).
+// x buffers per k quarter: copies NSX-1 steps ahead (one row tile: 3 buffers,
+// B=8 4.21k -> 4.26k tok/s against 2; 4 buffers measured no better at B=64)
+#ifndef SK8_NS1
+#define SK8_NS1 3
+#endif
+__host__ __device__ constexpr int sk8_nsx(int rt) { return rt == 2 ? 4 : SK8_NS1; }
+
 template <int MT, bool I8, int FIX, int RT, int XC>
-__device__ __forceinline__ void skinny8_body(const SkinnyJob &J, int rt0, int MB, unsigned char *xb0, unsigned char *xb1) {
+__device__ __forceinline__ void skinny8_body(const SkinnyJob &J, int rt0, int MB, unsigned char *xb0) {
     constexpr int TB = MT * 32;
     constexpr int XB = TB * 128;     // bytes of one x buffer
     // 1 KiB copies per step: XC of the TB / 8 (a batch of at most 8 * XC
@@ -864,11 +871,12 @@ __device__ __forceinline__ void skinny8_body(const SkinnyJob &J, int rt0, int MB
     const int q4 = ((nchunks + 3) / 4 + 1) & ~1;
     const int cw0 = min(nchunks, wave * q4), cw1 = min(nchunks, cw0 + q4);
     const int nw = (cw1 - cw0) / 2;  // steps of this wave
-    // x buffers of this wave's quarter: RT = 1 two (xb0, xb1), RT = 2 NSX in xb0
-    constexpr int NSX = RT == 2 ? 4 : 2;
+    // NSX x buffers per k quarter (wave-private with one row tile, shared by
+    // the quarter's two waves with two), copies NSX-1 steps ahead
+    constexpr int NSX = sk8_nsx(RT);
     unsigned char *xbw[NSX];
 #pragma unroll
-    for (int i = 0; i < NSX; i++) xbw[i] = RT == 2 ? xb0 + (i * 4 + wave) * XB : (i ? xb1 : xb0) + wave * XB;
+    for (int i = 0; i < NSX; i++) xbw[i] = xb0 + (i * 4 + wave) * XB;
     // a k-slice job points into a row tile of a wider tiled matrix
     const int tch = J.wtile_ch ? J.wtile_ch : nchunks;
     const uint8_t *wt = (const uint8_t *)J.w + (size_t)rt_ld * tch * tbytes + lane * (I8 ? 16 : 32);
@@ -994,23 +1002,23 @@ __device__ __forceinline__ void skinny8_body(const SkinnyJob &J, int rt0, int MB
             if (s + DW < FIX) issue_w(s % DW, s + DW);
         }
     } else if (FIX > 0 && nw == FIX) {
-        issue_x(0, 0);
+        // one row tile: the same issue order as above without the barrier
+        // (the buffers are the wave's own; the slot a copy refills was last
+        // read by the previous step, whose reads completed before its MFMAs)
+#pragma unroll
+        for (int d = 0; d < NSX - 1; d++) {
+            issue_x(d, d);
+            __builtin_amdgcn_sched_barrier(0);
+        }
 #pragma unroll
         for (int d = 0; d < DW; d++) issue_w(d, d);
 #pragma unroll
         for (int s = 0; s < FIX; s++) {
-            // order per step: the next step's x copy, this step's products,
-            // then the weights DW steps ahead into the slot just consumed.
-            // Scheduling barriers keep that order: otherwise the scheduler
-            // sinks the weight loads next to their use (register pressure
-            // first) and the ring degenerates to one step
             __builtin_amdgcn_sched_barrier(0);
-            if (s + 1 < FIX) issue_x((s + 1) & 1, s + 1);
-            // loads younger than x(s): the weights issued after it (at the end
-            // of step s-1, or the whole prologue ring for s = 0) and x(s+1)
-            const int younger = (s == 0 ? DW * LW : (s - 1 + DW < FIX ? LW : 0)) + (s + 1 < FIX ? NX : 0);
-            sk_wait_vm(younger);
-            compute(s & 1, s % DW, s, false);
+            sk_wait_vm(sk8p_younger<FIX, NSX, DW>(s, NX, LW));
+            __builtin_amdgcn_sched_barrier(0);
+            if (s + NSX - 1 < FIX) issue_x((s + NSX - 1) % NSX, s + NSX - 1);
+            compute(s % NSX, s % DW, s, false);
             __builtin_amdgcn_sched_barrier(0);
             if (s + DW < FIX) issue_w(s % DW, s + DW);
         }
@@ -1034,7 +1042,7 @@ __device__ __forceinline__ void skinny8_body(const SkinnyJob &J, int rt0, int MB
     }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();  // x buffers dead: the LDS holds the wave tiles now
-    float (*part)[32][TB + 1] = reinterpret_cast<float (*)[32][TB + 1]>(RT == 2 ? xb0 : xb1) + 4 * h;
+    float (*part)[32][TB + 1] = reinterpret_cast<float (*)[32][TB + 1]>(xb0) + 4 * h;
 #pragma unroll
     for (int ct = 0; ct < MT; ct++)
 #pragma unroll
@@ -1060,12 +1068,11 @@ __device__ __forceinline__ void skinny8_body(const SkinnyJob &J, int rt0, int MB
 // every x copy, halving the x bytes read from L2 per weight byte.
 template <int MT, int RT, int XC>
 __global__ __launch_bounds__(256 * RT) void k_skinny8(SkinnyJobs jobs, int MB) {
-    // 4 quarters x TB sessions x 128 bytes per buffer; the second also holds
-    // the RT x 4 x 32 x (TB+1) wave tiles at the end
-    // (RT = 2: xb0 holds the 4 buffers of each quarter, then the wave tiles)
-    constexpr int XBYTES = 4 * MT * 32 * 128 > RT * 4 * 32 * (MT * 32 + 1) * 4 ? 4 * MT * 32 * 128 : RT * 4 * 32 * (MT * 32 + 1) * 4;
-    __shared__ __attribute__((aligned(16))) unsigned char xb0[(RT == 2 ? 4 : 1) * 4 * MT * 32 * 128];
-    __shared__ __attribute__((aligned(16))) unsigned char xb1[RT == 2 ? 16 : XBYTES];
+    // NSX buffers per k quarter of TB sessions x 128 bytes, then the wave
+    // tiles of the partial sums in the same bytes
+    constexpr int XBYTES = sk8_nsx(RT) * 4 * MT * 32 * 128;
+    static_assert(RT * 4 * 32 * (MT * 32 + 1) * 4 <= XBYTES, "partial tiles fit the x buffers");
+    __shared__ __attribute__((aligned(16))) unsigned char xb0[XBYTES];
     const int bid = blockIdx.x;
     int ji = 0;
     while (ji + 1 < jobs.n && bid >= jobs.blk_start[ji + 1]) ji++;
@@ -1073,11 +1080,11 @@ __global__ __launch_bounds__(256 * RT) void k_skinny8(SkinnyJobs jobs, int MB) {
     // k = 1280 (a half-k slice) runs its 5 steps per wave unrolled too
     const bool k1280 = RT == 1 && jobs.j[ji].K == 32 * 40;
     if (jobs.j[ji].fmt == FMT_I8) {
-        if (k1280) skinny8_body<MT, true, 5, RT, XC>(jobs.j[ji], rt0, MB, xb0, xb1);
-        else skinny8_body<MT, true, 10, RT, XC>(jobs.j[ji], rt0, MB, xb0, xb1);
+        if (k1280) skinny8_body<MT, true, 5, RT, XC>(jobs.j[ji], rt0, MB, xb0);
+        else skinny8_body<MT, true, 10, RT, XC>(jobs.j[ji], rt0, MB, xb0);
     } else {
-        if (k1280) skinny8_body<MT, false, 5, RT, XC>(jobs.j[ji], rt0, MB, xb0, xb1);
-        else skinny8_body<MT, false, 10, RT, XC>(jobs.j[ji], rt0, MB, xb0, xb1);
+        if (k1280) skinny8_body<MT, false, 5, RT, XC>(jobs.j[ji], rt0, MB, xb0);
+        else skinny8_body<MT, false, 10, RT, XC>(jobs.j[ji], rt0, MB, xb0);
     }
 }
 
