@@ -361,6 +361,47 @@ def wkv_leg():
     be.close()
     return rows
 
+def gemm_compare_leg(reps=20):
+    """The prefill GEMMs of a 4096-row chunk (fp16 weight copies, fp32
+    out) on `k_gemmd` (rsv_gemm_ex) and on hipBLASLt through torch.matmul
+    (fp16 out), same shapes, HIP events around `reps` launches each on the
+    stream each is enqueued on.  Operands: N(0,1) activations, N(0, 0.02^2)
+    weights; the weights rotate over copies so that they are not L2-resident."""
+    import torch
+    import rsv
+    be = rsv.Backend(0)
+    tm = _Timer(be)
+    rng = np.random.default_rng(1)
+    rows = []
+    for (M, N, K, nm) in ((4096, 10240, 2560, "ffn.key"), (4096, 2560, 10240, "ffn.value"),
+                          (4096, 2560, 2560, "att.output"), (4096, 7680, 2560, "r/k/v")):
+        ncopy = max(1, int(np.ceil(300e6 / (2 * N * K))))
+        w = [be.tensor((rng.standard_normal(N * K) * 0.02).astype(np.float32), dtype=rsv.F16) for _ in range(ncopy)]
+        x = be.tensor(rng.standard_normal(M * K).astype(np.float32), dtype=rsv.F16)
+        y = be.tensor(n=M * N)
+        us = tm.us(lambda i: be.call("rsv_gemm_ex", x, w[i % ncopy], None, y, M, N, K, 0, NONE, NONE, NONE), reps)
+        a = torch.randn(M, K, device="cuda", dtype=torch.float16)
+        bt = [torch.randn(N, K, device="cuda", dtype=torch.float16) * 0.02 for _ in range(ncopy)]
+        for i in range(4):
+            c = a @ bt[i % ncopy].t()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(reps):
+            c = a @ bt[i % ncopy].t()
+        e1.record()
+        e1.synchronize()
+        ub = e0.elapsed_time(e1) * 1000.0 / reps
+        fl = 2.0 * M * N * K
+        rows.append(dict(gemm=nm, m=M, n=N, k=K, k_gemmd_us=round(us, 1), hipblaslt_us=round(ub, 1),
+                         k_gemmd_tflops=round(fl / us / 1e6, 1), hipblaslt_tflops=round(fl / ub / 1e6, 1)))
+        log(f"gemm {nm:10s} {M}x{N}x{K}: k_gemmd {us:7.1f} us ({fl / us / 1e6:6.1f} TFLOP/s), "
+            f"hipBLASLt {ub:7.1f} us ({fl / ub / 1e6:6.1f} TFLOP/s)")
+        del w, x, y, bt, a, c
+    be.close()
+    return rows
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -385,6 +426,8 @@ def main():
                     help="run only the dominant-kernel leg (for rocprofv3 summaries of that kernel)")
     ap.add_argument("--no-graph", action="store_true",
                     help="enqueue self-loop steps eagerly instead of replaying a HIP graph (profiling)")
+    ap.add_argument("--gemm-compare", action="store_true",
+                    help="run only the prefill GEMM shapes on k_gemmd and on hipBLASLt (torch.matmul)")
     args = ap.parse_args()
     if args.no_graph:
         os.environ["RSV_NO_GRAPH"] = "1"
@@ -398,6 +441,10 @@ def main():
     if args.legs_only:
         lin, wk = linear_leg(), wkv_leg()
         print(json.dumps({"linear_configs1": lin, "wkv7_configs2": wk}))
+        return
+
+    if args.gemm_compare:
+        print(json.dumps({"gemm_compare": gemm_compare_leg()}))
         return
 
     if args.kernel_only:
