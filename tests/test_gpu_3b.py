@@ -12,7 +12,9 @@ COMPARE_LOGITS checks (main.rs):
 - teacher-forced top-1 agreement >= 98% for int8 linears + int8 head, and
   >= 99% for the fp16 embedding/head variant.  Teacher forcing: the oracle
   is fed the tokens the GPU chose, and its argmax at every step is compared
-  with the GPU's choice.
+  with the GPU's choice.  In the B=64 check a differing token counts as
+  agreeing when the oracle's gap between its argmax and the GPU's token is
+  below the logits tolerance (a near tie), with strict agreement >= 95%.
 
 The oracle splits its matvec columns over threads (bit-identical to one
 thread) so that the 3B checks take seconds per token, not half a second.
@@ -113,8 +115,16 @@ def test_3b_b1_prefill_and_selfloop(model3b):
 def test_3b_b64_prefill_and_selfloop(model3b):
     """B=64: 64 sessions prefilled as one packed batch (512 rows: the prefill
     GEMM path), then a 24-step batched argmax self-loop (the B>=16 MFMA
-    decode the bench times).  Sessions 0, 31 and 63 are checked against the
-    oracle: prompt logits and teacher-forced top-1."""
+    decode the bench times, graph-replayed).  The same 24 steps are replayed
+    eagerly from the saved state with forward_tokens_batch, which returns
+    every step's logits: its argmax must equal the self-loop's token.
+    Sessions 0, 15, 31, 47 and 63 are checked against the oracle along the
+    same tokens: prompt logits and every decode step's logits within the
+    RMSE bound, and teacher-forced top-1 over the 120 steps.  A step whose
+    token differs from the oracle's argmax counts as agreeing only when the
+    oracle's own gap between the two is below the logits tolerance
+    (1e-2 x its logit std: a near tie that the logits bound cannot order);
+    each such step is logged, and strict agreement must still be >= 95%."""
     kind, b, m = model3b
     B, plen, n = 64, 8, 24
     prompts = [_prompt(plen, 100 + i) for i in range(B)]
@@ -122,21 +132,49 @@ def test_3b_b64_prefill_and_selfloop(model3b):
     try:
         seeds, lg = b.forward_seq_batch(S, [q[:-1] for q in prompts], want_logits=True)
         seeds = np.array([int(q[-1]) for q in prompts], np.uint32)
+        snap = S.back()
         out = b.argmax_selfloop_batch(S, seeds, n)
+        S.load(snap)
+        glog = {}
+        prev = seeds
+        for i in range(n):
+            L = b.forward_tokens_batch(S, prev)
+            for s in range(B):
+                t = int(out[s][i])
+                assert int(np.argmax(L[s])) == t or L[s][t] == L[s].max(), (s, i)
+            for s in (0, 15, 31, 47, 63):
+                glog[(s, i)] = L[s].copy()
+            prev = np.ascontiguousarray(out[:, i])
     finally:
         S.free()
-    agree = total = 0
-    for s in (0, 31, 63):
+    agree = strict = total = 0
+    worst = 0.0
+    for s in (0, 15, 31, 47, 63):
         st = m.init_state()
         want = m.forward(prompts[s][:-1], st)
         e = rel_rmse(lg[s], want)
         log(kind, f"B=64 session {s}: prompt logits rel rmse {e:.2e}")
         assert e <= RMSE_BOUND, s
         olg = _teacher_forced(m, st, seeds[s], out[s])
-        a = sum(int(orc.argmax(o) == out[s][i]) for i, o in enumerate(olg))
-        log(kind, f"B=64 session {s}: teacher-forced top-1 {a}/{n}")
-        agree += a
-        total += n
+        for i, o in enumerate(olg):
+            o = np.asarray(o)
+            e = rel_rmse(glog[(s, i)], o)
+            worst = max(worst, e)
+            assert e <= RMSE_BOUND, (s, i, e)
+            t, top = int(out[s][i]), int(orc.argmax(o))
+            total += 1
+            if top == t:
+                strict += 1
+                agree += 1
+            elif o[top] - o[t] <= RMSE_BOUND * o.std():
+                agree += 1
+                log(kind, f"  session {s} step {i}: near tie, oracle top {top} at {o[top]:.4f}, GPU token {t} at "
+                          f"{o[t]:.4f} (oracle logit std {o.std():.3f})")
+            else:
+                log(kind, f"  session {s} step {i}: oracle top {top} at {o[top]:.4f}, GPU token {t} at {o[t]:.4f}")
+    log(kind, f"B=64 decode: worst per-step logits rel rmse {worst:.2e}; top-1 {strict}/{total} strict, "
+              f"{agree}/{total} with near ties")
+    assert strict / total >= 0.95, f"strict top-1 agreement {strict}/{total}"
     assert agree / total >= BAR[kind], f"top-1 agreement {agree}/{total}"
 
 
