@@ -222,13 +222,24 @@ __global__ __launch_bounds__(256) void k_wkv7_lora(WkvLoraArgs A) {
         for (int e = 0; e < kUp; e++)
             if (e < np) wl[m][e] = wp[e];
     }
-    for (int e = tid; e < L4; e += 256) {
+    // the LoRA inputs (L4 <= 1024: at most 4 per thread) stay in registers
+    // until the state and vector loads below are issued: stored to LDS
+    // first, they would hold those loads back until the weights had landed
+    uint32_t mv[4];  // raw bits, converted when stored (an index past L4 reloads the last input)
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int e = min(tid + 256 * u, L4 - 1);
         const int m = e < m0 ? 0 : e < m0 + m1 ? 1 : e < m0 + m1 + m2 ? 2 : 3;
         const int off = m == 0 ? 0 : m == 1 ? m0 : m == 2 ? m0 + m1 : m0 + m1 + m2;
-        const size_t mi = (size_t)b * A.mid_n[m] + (e - off);
-        if (F16IO) mids[e] = (float)((const _Float16 *)A.mid[m])[mi];  // g input already through its sigmoid
-        else mids[e] = m == 3 ? sig_f(((const float *)A.mid[m])[mi]) : ((const float *)A.mid[m])[mi];
+        // selects, not an indexed kernel-argument array (which is read
+        // through memory, one more wait before the loads below)
+        const int mid = m == 0 ? m0 : m == 1 ? m1 : m == 2 ? m2 : m3;
+        const void *src = m == 0 ? A.mid[0] : m == 1 ? A.mid[1] : m == 2 ? A.mid[2] : A.mid[3];
+        const size_t mi = (size_t)b * mid + (e - off);
+        if (F16IO) mv[u] = ((const uint16_t *)src)[mi];  // g input already through its sigmoid
+        else mv[u] = ((const uint32_t *)src)[mi];
     }
+    __builtin_amdgcn_sched_barrier(0);
     const float kc = A.k[vo], rc = A.r[vo], vc = A.v[vo], vfc = A.vf[vo];
     const float w0 = A.w0[c], a0 = A.a0[c], v0 = A.v0[c], kkc = A.kk[c], kac = A.ka[c], rkc = A.rk[c];
     const float gam = A.gamma[c], bet = A.beta[c], sw = A.scale[0];
@@ -236,6 +247,15 @@ __global__ __launch_bounds__(256) void k_wkv7_lora(WkvLoraArgs A) {
     float4 st4[4];
 #pragma unroll
     for (int m = 0; m < 4; m++) st4[m] = srow[m];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int e = tid + 256 * u;
+        if (e < L4) {
+            const float f = F16IO ? h2f_w(mv[u]) : __uint_as_float(mv[u]);
+            mids[e] = (!F16IO && e >= m0 + m1 + m2) ? sig_f(f) : f;
+        }
+    }
     if (h == 0 && A.side_dst)
         for (int e = tid; e < C; e += 256) A.side_dst[(size_t)b * C + e] = A.side_src[(size_t)b * C + e];
     __syncthreads();
