@@ -1029,8 +1029,6 @@ __global__ __launch_bounds__(NT) void k_gemv_os2(GemvJobs jobs) {
     extern __shared__ float4 xs4[];
     __shared__ float red[NT / 64];
     const int bid = blockIdx.x;
-    if (bid == 0 && jobs.side.src)
-        for (int i = threadIdx.x; i < jobs.side.n; i += NT) jobs.side.dst[i] = jobs.side.src[i];
     int ji = 0;
     while (ji + 1 < jobs.n && bid >= jobs.blk_start[ji + 1]) ji++;
     const GemvJob &J = jobs.j[ji];
@@ -1041,6 +1039,14 @@ __global__ __launch_bounds__(NT) void k_gemv_os2(GemvJobs jobs) {
     } else {
         if (J.lpr == 32) gemv_os2_body<FMT_F16, 32, CPL, Q, NT, PV>(J, rb, xs4, red);
         else gemv_os2_body<FMT_F16, 64, CPL, Q, NT, PV>(J, rb, xs4, red);
+    }
+    // side copy, a share per block after the block's own rows (one block
+    // copying the whole vector up front chained its round trips ahead of
+    // that block's weight stream)
+    if (jobs.side.src) {
+        const int per = (jobs.side.n + (int)gridDim.x - 1) / (int)gridDim.x;
+        const int end = min(jobs.side.n, (bid + 1) * per);
+        for (int i = bid * per + (int)threadIdx.x; i < end; i += NT) jobs.side.dst[i] = jobs.side.src[i];
     }
 }
 

@@ -184,8 +184,8 @@ int launch_wkv7_decode(rsv_ctx *ctx, float *s, const float *k, const float *kk, 
 // channel 64h+j: it takes quarter q of each LoRA-up dot (the inputs staged in
 // LDS, the weights loaded into registers at kernel entry, ranks <= 256) and
 // columns 16q..16q+15 of state row j.  Quad sums run on DPP.  The output is
-// y_norm * g, the att.output operand.  Blocks with h == 0 also copy
-// side_src -> side_dst for their session (the token-shift state row).
+// y_norm * g, the att.output operand.  Each block also copies its head's 64
+// channels of side_src -> side_dst for its session (the token-shift state row).
 template <int CTRL>
 __device__ __forceinline__ float quad_dpp(float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
@@ -256,8 +256,6 @@ __global__ __launch_bounds__(256) void k_wkv7_lora(WkvLoraArgs A) {
             mids[e] = (!F16IO && e >= m0 + m1 + m2) ? sig_f(f) : f;
         }
     }
-    if (h == 0 && A.side_dst)
-        for (int e = tid; e < C; e += 256) A.side_dst[(size_t)b * C + e] = A.side_src[(size_t)b * C + e];
     __syncthreads();
     // LoRA-up dots, reduced over the quad
     float acc[4];
@@ -353,6 +351,11 @@ __global__ __launch_bounds__(256) void k_wkv7_lora(WkvLoraArgs A) {
     if (q == 0) {
         if (F16IO) ((_Float16 *)A.yg)[vo] = (_Float16)(yn * gg);
         else ((float *)A.yg)[vo] = yn * gg;
+    }
+    // side copy (the token-shift state row): the head's 64 channels
+    if (A.side_dst && tid < 64) {
+        const size_t e = (size_t)b * C + (size_t)h * 64 + tid;
+        A.side_dst[e] = A.side_src[e];
     }
 }
 
@@ -615,20 +618,33 @@ __global__ __launch_bounds__(256) void k_wkv7_lora_rows(WkvLoraArgs A) {
         for (int e = 0; e < 8; e++)
             if (e < np) vl[m][e] = wp[e];
     }
-    for (int e = tid; e < L4; e += 256) {
+    // the LoRA inputs (L4 <= 1024: at most 4 per thread; an index past L4
+    // reloads the last one) stay in registers until the vector and state
+    // loads below are issued; kernel-argument arrays are selected, not
+    // indexed (an indexed one is read through memory, one more wait)
+    float mv[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int e = min(tid + 256 * u, L4 - 1);
         const int m = e < m0 ? 0 : e < m0 + m1 ? 1 : e < m0 + m1 + m2 ? 2 : 3;
         const int off = m == 0 ? 0 : m == 1 ? m0 : m == 2 ? m0 + m1 : m0 + m1 + m2;
-        const float x = ((const float *)A.mid[m])[(size_t)b * A.mid_n[m] + (e - off)];
-        mids[e] = m == 3 ? sig_f(x) : x;
+        const int mid = m == 0 ? m0 : m == 1 ? m1 : m == 2 ? m2 : m3;
+        const float *src = (const float *)(m == 0 ? A.mid[0] : m == 1 ? A.mid[1] : m == 2 ? A.mid[2] : A.mid[3]);
+        mv[u] = src[(size_t)b * mid + (e - off)];
     }
+    __builtin_amdgcn_sched_barrier(0);
     const size_t vo = (size_t)b * C + c, ro = (size_t)b * C + cr;
     const float kc = A.k[vo], rc = A.r[vo];
     const float w0 = A.w0[c], a0 = A.a0[c], kkc = A.kk[c], kac = A.ka[c], rkc = A.rk[c];
     const float vrow = A.v[ro], vfrow = A.vf[ro], v0row = A.v0[cr], sw = A.scale[0];
     float4 *srow = (float4 *)(A.S + (((size_t)b * H + h) * 64 + rr) * 64) + s16;
     const float4 st = *srow;
-    if (h == 0 && p == 0 && A.side_dst)
-        for (int e = tid; e < C; e += 256) A.side_dst[(size_t)b * C + e] = A.side_src[(size_t)b * C + e];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int e = tid + 256 * u;
+        if (e < L4) mids[e] = e >= m0 + m1 + m2 ? sig_f(mv[u]) : mv[u];
+    }
     __syncthreads();
     // 2. LoRA dots
     float acc[2];
@@ -718,6 +734,12 @@ __global__ __launch_bounds__(256) void k_wkv7_lora_rows(WkvLoraArgs A) {
         ((float *)A.yg)[ro] = y;
         A.y_bonus[ro] = bonus * vv;
         A.y_gate[ro] = gg;
+    }
+    // side copy (the token-shift state row), 16 elements per block at the
+    // end: one block copying the whole row would chain its round trips
+    if (A.side_dst && tid < 16) {
+        const size_t e = (size_t)b * C + (size_t)(h * 4 + p) * 16 + tid;
+        A.side_dst[e] = A.side_src[e];
     }
 }
 
