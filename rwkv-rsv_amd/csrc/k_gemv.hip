@@ -407,11 +407,14 @@ __global__ __launch_bounds__(256) void k_gemv(GemvJobs jobs, int batch) {
     extern __shared__ float4 smem4[];
     __shared__ float red[4];
     const int bid = blockIdx.x;
-    if (bid == 0 && jobs.side.src) {
+    if (jobs.side.src) {
+        // side copy of this batch tile's rows, a share per block (one block
+        // copying all of it would chain its round trips ahead of its rows)
         const int b0 = blockIdx.y * BT, nb = min(BT, batch - b0);
-        for (int b = 0; b < nb; b++)
-            for (int i = threadIdx.x; i < jobs.side.n; i += 256)
-                jobs.side.dst[(size_t)(b0 + b) * jobs.side.n + i] = jobs.side.src[(size_t)(b0 + b) * jobs.side.n + i];
+        const int tot = nb * jobs.side.n, per = (tot + (int)gridDim.x - 1) / (int)gridDim.x;
+        const int end = min(tot, (bid + 1) * per);
+        for (int i = bid * per + (int)threadIdx.x; i < end; i += 256)
+            jobs.side.dst[(size_t)b0 * jobs.side.n + i] = jobs.side.src[(size_t)b0 * jobs.side.n + i];
     }
     int ji = 0;
     while (ji + 1 < jobs.n && bid >= jobs.blk_start[ji + 1]) ji++;
@@ -748,8 +751,12 @@ __global__ __launch_bounds__(kMfNT) void k_gemv_mb(GemvJobs jobs, int batch, flo
     __shared__ __attribute__((aligned(16))) float part[kMfNT / 64 * kMfSlots * 256];
     __shared__ float red[kMfNT / 64][4];
     const int bid = blockIdx.x;
-    if (bid == 0 && jobs.side.src)
-        for (int i = threadIdx.x; i < batch * jobs.side.n; i += kMfNT) jobs.side.dst[i] = jobs.side.src[i];
+    if (jobs.side.src) {
+        // side copy, a share per block (see k_gemv)
+        const int tot = batch * jobs.side.n, per = (tot + (int)gridDim.x - 1) / (int)gridDim.x;
+        const int end = min(tot, (bid + 1) * per);
+        for (int i = bid * per + (int)threadIdx.x; i < end; i += kMfNT) jobs.side.dst[i] = jobs.side.src[i];
+    }
     int ji = 0;
     while (ji + 1 < jobs.n && bid >= jobs.blk_start[ji + 1]) ji++;
     const GemvJob &J = jobs.j[ji];
