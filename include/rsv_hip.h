@@ -219,6 +219,13 @@ int rsv_dequant_int8_to_f16(rsv_ctx *ctx, const rsv_int8 *a, uint32_t out, uint6
 int rsv_argmax(rsv_ctx *ctx, uint32_t logits, uint32_t token, uint64_t n);
 int rsv_argmax_into_host(rsv_ctx *ctx, uint32_t logits, uint32_t token, uint64_t n);
 int rsv_argmax_batch(rsv_ctx *ctx, uint32_t logits, uint32_t token, uint64_t n, uint64_t batch);
+/* One greedy self-loop round's tail in one launch: rsv_argmax_batch, then
+ * rsv_record_tokens (backend.rs:621) of the chosen tokens, then
+ * rsv_gather_rows_device_f16 (backend.rs:449) of their rows of `emb` into x
+ * for the next step; the same results as the three calls in that order. */
+int rsv_argmax_record_gather_batch(rsv_ctx *ctx, uint32_t logits, uint32_t token, uint64_t n,
+                                   uint32_t out_seq, uint32_t cnt, uint64_t stride, uint32_t emb,
+                                   uint32_t x, uint64_t c, uint64_t batch);
 int rsv_sample(rsv_ctx *ctx, uint32_t logits, uint32_t token, uint64_t n, float temperature,
                uint32_t top_k, float top_p, uint32_t seed, float repetition_penalty,
                float frequency_penalty, float presence_penalty, const uint32_t *history,

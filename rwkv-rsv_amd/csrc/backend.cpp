@@ -953,6 +953,22 @@ int rsv_argmax_batch(rsv_ctx *ctx, uint32_t logits, uint32_t token, uint64_t n, 
     OPND(t, token, RSV_U32, batch, "argmax token");
     return launch_argmax(ctx, F32P(l), U32P(t), (int)n, (int)batch);
 }
+int rsv_argmax_record_gather_batch(rsv_ctx *ctx, uint32_t logits, uint32_t token, uint64_t n, uint32_t out_seq,
+                                   uint32_t cnt, uint64_t stride, uint32_t emb, uint32_t x, uint64_t c,
+                                   uint64_t batch) {
+    CHECK_CTX();
+    OPND(l, logits, RSV_F32, n * batch, "argmax_record_gather logits");
+    OPND(t, token, RSV_U32, batch, "argmax_record_gather token");
+    OPND(os, out_seq, RSV_U32, stride * batch, "argmax_record_gather out_seq");
+    OPND(cn, cnt, RSV_U32, batch, "argmax_record_gather cnt");
+    OPND(xd, x, RSV_F32, c * batch, "argmax_record_gather x");
+    Tensor *e = get_tensor(ctx, emb);
+    if (!e) return RSV_FAIL("argmax_record_gather: unknown emb");
+    if (e->dtype == RSV_U32) return RSV_FAIL("argmax_record_gather: emb must be F16 or F32");
+    if (c == 0 || stride == 0) return RSV_FAIL("argmax_record_gather: c and stride must be > 0");
+    return launch_argmax_next(ctx, F32P(l), U32P(t), (int)n, U32P(os), U32P(cn), (int)stride, e->ptr,
+                              e->dtype == RSV_F16, e->len / c, F32P(xd), (int)c, (int)batch);
+}
 int rsv_argmax(rsv_ctx *ctx, uint32_t logits, uint32_t token, uint64_t n) {
     return rsv_argmax_batch(ctx, logits, token, n, 1);
 }

@@ -1047,10 +1047,12 @@ int forward_layer(rsv_bundle *b, uint64_t i, WorkBufs &w, GpuState &s) {
 
 // gather -> layers -> ln_out -> head (gpu_model.rs:1879-1913 minus the
 // sampler).
-int decode_step(rsv_bundle *b, WorkBufs &w, GpuState &s) {
+// gather = false: x already holds the tokens' embedding rows (the greedy
+// self-loop's fused argmax / record / gather launch wrote them).
+int decode_step(rsv_bundle *b, WorkBufs &w, GpuState &s, bool gather = true) {
     rsv_ctx *c = b->ctx;
     const rsv_model_info &I = b->info;
-    CK(rsv_gather_rows_device_f16(c, b->emb_ln, w.x, w.token, I.n_embd, w.batch));
+    if (gather) CK(rsv_gather_rows_device_f16(c, b->emb_ln, w.x, w.token, I.n_embd, w.batch));
     w.xcur = w.x;
     w.pend = 0;
     for (uint64_t i = 0; i < I.n_layer; i++) HK(forward_layer(b, i, w, s));
@@ -1613,15 +1615,26 @@ int selfloop(rsv_bundle *b, GpuState &s, const uint32_t *seeds, uint64_t n, cons
         // enqueues the same kernels eagerly every round instead (the
         // reference's SKIP_GRAPH debugging path, gpu_model.rs:1698-1721).
         const bool eager = getenv("RSV_NO_GRAPH") && getenv("RSV_NO_GRAPH")[0] && getenv("RSV_NO_GRAPH")[0] != '0';
+        // Greedy rounds end with one launch that takes the argmax, records
+        // it and gathers its embedding row for the next round, so a round
+        // starts at the layers; the first round's rows are gathered here.
+        if (!sp && rsv_gather_rows_device_f16(c, b->emb_ln, w->x, w->token, I.n_embd, B)) {
+            rc = herr("gather: %s", rsv_last_error());
+            break;
+        }
         auto step = [&]() -> int {
-            int e = decode_step(b, *w, s);
-            if (!e) {
-                if (sp) e = rsv_sample_into_host_seeded_batch(c, w->logits, w->token, I.vocab, temp, NONE, counter,
-                                                             sampler, seq, B);
-                else e = rsv_argmax_batch(c, w->logits, w->token, I.vocab, B);
-                if (e) herr("sampler: %s", rsv_last_error());
+            int e = decode_step(b, *w, s, sp != nullptr);
+            if (!e && sp) {
+                if (rsv_sample_into_host_seeded_batch(c, w->logits, w->token, I.vocab, temp, NONE, counter, sampler,
+                                                      seq, B))
+                    e = herr("sampler: %s", rsv_last_error());
+                else if (rsv_record_tokens(c, w->token, seq, cnt, n, B))
+                    e = herr("record: %s", rsv_last_error());
+            } else if (!e) {
+                if (rsv_argmax_record_gather_batch(c, w->logits, w->token, I.vocab, seq, cnt, n, b->emb_ln, w->x,
+                                                   I.n_embd, B))
+                    e = herr("argmax: %s", rsv_last_error());
             }
-            if (!e && rsv_record_tokens(c, w->token, seq, cnt, n, B)) e = herr("record: %s", rsv_last_error());
             return e;
         };
         if (!eager) {

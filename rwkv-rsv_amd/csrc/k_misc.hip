@@ -196,12 +196,9 @@ int launch_gather_rows(rsv_ctx *ctx, const void *src, int src_f16, uint64_t src_
 // ------------------------------------------------------------------ argmax
 // Ties go to the smaller index (backend_cuda.rs:3640-3680); the scan starts
 // from -1e30 at index 0 like the reference.  grid (batch), block 1024.
-__global__ __launch_bounds__(1024) void k_argmax(const float *__restrict__ logits, uint32_t *__restrict__ tok,
-                                                 int n) {
-    __shared__ float sv[16];
-    __shared__ int si[16];
-    const int b = blockIdx.x, tid = threadIdx.x;
-    const float *lg = logits + (size_t)b * n;
+// Argmax of one row by a 1024-thread block; the index is valid in thread 0.
+__device__ __forceinline__ int argmax_block(const float *__restrict__ lg, int n, float *sv, int *si) {
+    const int tid = threadIdx.x;
     float bv = -1e30f;
     int bi = 0;
     if ((n & 3) == 0) {
@@ -235,13 +232,61 @@ __global__ __launch_bounds__(1024) void k_argmax(const float *__restrict__ logit
     wave_argmax_last(bv, bi);
     if ((tid & 63) == 63) { sv[tid >> 6] = bv; si[tid >> 6] = bi; }
     __syncthreads();
+    int ix = 0;
     if (tid == 0) {
         float v = sv[0];
-        int ix = si[0];
+        ix = si[0];
         for (int w = 1; w < 16; w++)
             if (sv[w] > v || (sv[w] == v && si[w] < ix)) { v = sv[w]; ix = si[w]; }
-        tok[b] = (uint32_t)ix;
     }
+    return ix;
+}
+
+__global__ __launch_bounds__(1024) void k_argmax(const float *__restrict__ logits, uint32_t *__restrict__ tok,
+                                                 int n) {
+    __shared__ float sv[16];
+    __shared__ int si[16];
+    const int b = blockIdx.x;
+    const int ix = argmax_block(logits + (size_t)b * n, n, sv, si);
+    if (threadIdx.x == 0) tok[b] = (uint32_t)ix;
+}
+
+// argmax, then the token's record (k_record_tokens) and the gather of its
+// embedding row into x for the next step (k_gather_rows), in one launch:
+// the three steps of a greedy self-loop round, with the same results.
+__global__ __launch_bounds__(1024) void k_argmax_next(const float *__restrict__ logits, uint32_t *__restrict__ tok,
+                                                      int n, uint32_t *__restrict__ out_seq,
+                                                      uint32_t *__restrict__ cnt, int stride,
+                                                      const void *__restrict__ emb, int emb_f16, uint64_t emb_rows,
+                                                      float *__restrict__ x, int c) {
+    __shared__ float sv[16];
+    __shared__ int si[16];
+    __shared__ uint32_t stok;
+    const int b = blockIdx.x, tid = threadIdx.x;
+    const int ix = argmax_block(logits + (size_t)b * n, n, sv, si);
+    if (tid == 0) {
+        tok[b] = (uint32_t)ix;
+        const uint32_t i = cnt[b];
+        if (i < (uint32_t)stride) out_seq[(size_t)b * stride + i] = (uint32_t)ix;
+        cnt[b] = i + 1u;
+        stok = (uint32_t)ix;
+    }
+    __syncthreads();
+    const size_t row = stok;
+    for (int i = tid; i < c; i += 1024) {
+        float v = 0.0f;
+        if (row < emb_rows) v = emb_f16 ? (float)((const _Float16 *)emb)[row * c + i] : ((const float *)emb)[row * c + i];
+        x[(size_t)b * c + i] = v;
+    }
+}
+
+int launch_argmax_next(rsv_ctx *ctx, const float *logits, uint32_t *tok, int n, uint32_t *out_seq, uint32_t *cnt,
+                       int stride, const void *emb, int emb_f16, uint64_t emb_rows, float *x, int c, int batch) {
+    if (n <= 0 || batch <= 0 || c <= 0) return RSV_FAIL("argmax_next: bad n=%d c=%d batch=%d", n, c, batch);
+    hipLaunchKernelGGL(k_argmax_next, dim3(batch), dim3(1024), 0, ctx->stream, logits, tok, n, out_seq, cnt, stride,
+                       emb, emb_f16, emb_rows, x, c);
+    RSV_HIP(hipGetLastError());
+    return 0;
 }
 
 int launch_argmax(rsv_ctx *ctx, const float *logits, uint32_t *tok, int n, int batch) {

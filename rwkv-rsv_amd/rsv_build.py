@@ -16,6 +16,7 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 COMMON = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-I", INC, "-I", CSRC,
           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-Wno-unused-result", "-Wno-unused-value"]
+COMMON += os.environ.get("RSV_EXTRA_FLAGS", "").split()
 
 BACKEND_SRCS = ["backend.cpp", "k_gemv.hip", "k_wkv.hip", "k_misc.hip", "k_sample.hip", "k_gemm.hip",
                 "k_skinny.hip", "k_sparse.hip"]
@@ -48,12 +49,13 @@ def build(force=False, jobs=8):
         objs = list(ex.map(lambda s: _compile(s, force), BACKEND_SRCS + HOST_SRCS))
     back = objs[: len(BACKEND_SRCS)]
     host = objs[len(BACKEND_SRCS):]
-    lib = os.path.join(OUT, "librsv_hip.so")
+    out = os.environ.get("RSV_BUILD_OUT")  # another directory for the libraries (experiments)
+    lib = os.path.join(out or OUT, "librsv_hip.so")
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", lib] + back
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed: {' '.join(cmd)}\n{r.stderr}")
-    hlib = os.path.join(OUT, "librsv_host.so")
+    hlib = os.path.join(out or OUT, "librsv_host.so")
     cmd = [HIPCC, "-shared", "-fPIC", "-o", hlib] + host + ["-L", OUT, "-lrsv_hip", "-Wl,-rpath,$ORIGIN"]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:

@@ -589,6 +589,43 @@ def test_gather_rows(be):
         assert np.all(got[3] == 0)
 
 
+def test_argmax_record_gather_equals_three_ops(be):
+    """The fused greedy round tail (argmax, record, embedding gather) against
+    rsv_argmax_batch + rsv_record_tokens + rsv_gather_rows_device_f16 on the
+    same rows: equal tokens, records, counters and gathered rows, bit for
+    bit; rows with ties (smallest index wins) and a token past the table
+    (zero row); F32 and F16 tables; the round past the row length records
+    nothing."""
+    rsv = _rsv()
+    rng = np.random.default_rng(21)
+    B, n, c, rows, stride = 5, 4096, 320, 3000, 3
+    for dt in (rsv.F32, rsv.F16):
+        tab = be.tensor(rng.standard_normal((rows, c)).astype(np.float32), dtype=dt)
+        bufs = {f: (be.tensor(n=B, dtype=rsv.U32), be.tensor(np.zeros(B * stride, np.uint32), dtype=rsv.U32),
+                    be.tensor(np.zeros(B, np.uint32), dtype=rsv.U32), be.tensor(n=B * c)) for f in (False, True)}
+        for r in range(stride + 1):
+            lg = rng.standard_normal((B, n)).astype(np.float32)
+            lg[1, [17, 2900]] = 9.0  # tie: index 17
+            lg[2, 3500] = 9.0        # argmax past the table: zero row
+            L = be.tensor(lg)
+            outs = []
+            for fused in (False, True):
+                tok, seq, cnt, x = bufs[fused]
+                if fused:
+                    be.call("rsv_argmax_record_gather_batch", L, tok, n, seq, cnt, stride, tab, x, c, B)
+                else:
+                    be.call("rsv_argmax_batch", L, tok, n, B)
+                    be.call("rsv_record_tokens", tok, seq, cnt, stride, B)
+                    be.call("rsv_gather_rows_device_f16", tab, x, tok, c, B)
+                outs.append([be.get(tok, B, rsv.U32), be.get(seq, B * stride, rsv.U32), be.get(cnt, B, rsv.U32),
+                             be.get(x, B * c)])
+            for u, v in zip(*outs):
+                assert np.array_equal(u, v)
+            assert outs[1][0][1] == 17 and outs[1][0][2] == 3500
+            assert np.all(outs[1][3].reshape(B, c)[2] == 0)
+            assert list(outs[1][2]) == [r + 1] * B
+
+
 # ------------------------------------------------------------- sampler
 def _sample_gpu(be, logits, temperature, top_k, top_p, seed, rep=1.0, freq=0.0, pres=0.0, hist=()):
     rsv = _rsv()
