@@ -253,6 +253,11 @@ int rsv_sample_noalloc(rsv_ctx *ctx, uint32_t logits, uint32_t token, uint64_t n
 int rsv_record_token(rsv_ctx *ctx, uint32_t in_tok, uint32_t out_seq, uint32_t cnt);
 int rsv_record_tokens(rsv_ctx *ctx, uint32_t in_tok, uint32_t out_seq, uint32_t cnt, uint64_t stride,
                       uint64_t batch);
+/* rsv_record_tokens (backend.rs:621) and rsv_gather_rows_device_f16
+ * (backend.rs:449) of the same tokens in one launch: the tail of a sampled
+ * self-loop round; the same results as the two calls in that order. */
+int rsv_record_gather_batch(rsv_ctx *ctx, uint32_t in_tok, uint32_t out_seq, uint32_t cnt, uint64_t stride,
+                            uint32_t emb, uint32_t x, uint64_t c, uint64_t batch);
 
 /* ---- sequence (prefill) ops (backend.rs:681-939) */
 int rsv_copy_token(rsv_ctx *ctx, uint32_t x, uint32_t y, uint64_t c, uint64_t stride, uint64_t token);

@@ -1071,6 +1071,21 @@ int rsv_record_tokens(rsv_ctx *ctx, uint32_t in_tok, uint32_t out_seq, uint32_t 
     return launch_record_tokens(ctx, U32P(it), U32P(os), U32P(cn), (int)stride, (int)batch);
 }
 
+int rsv_record_gather_batch(rsv_ctx *ctx, uint32_t in_tok, uint32_t out_seq, uint32_t cnt, uint64_t stride,
+                            uint32_t emb, uint32_t x, uint64_t c, uint64_t batch) {
+    CHECK_CTX();
+    OPND(it, in_tok, RSV_U32, batch, "record_gather in_tok");
+    OPND(os, out_seq, RSV_U32, stride * batch, "record_gather out_seq");
+    OPND(cn, cnt, RSV_U32, batch, "record_gather cnt");
+    OPND(xd, x, RSV_F32, c * batch, "record_gather x");
+    Tensor *e = get_tensor(ctx, emb);
+    if (!e) return RSV_FAIL("record_gather: unknown emb");
+    if (e->dtype == RSV_U32) return RSV_FAIL("record_gather: emb must be F16 or F32");
+    if (c == 0 || stride == 0) return RSV_FAIL("record_gather: c and stride must be > 0");
+    return launch_record_gather(ctx, U32P(it), U32P(os), U32P(cn), (int)stride, e->ptr, e->dtype == RSV_F16,
+                                e->len / c, F32P(xd), (int)c, (int)batch);
+}
+
 int rsv_record_token(rsv_ctx *ctx, uint32_t in_tok, uint32_t out_seq, uint32_t cnt) {
     CHECK_CTX();
     Tensor *o = get_tensor(ctx, out_seq);

@@ -1615,20 +1615,21 @@ int selfloop(rsv_bundle *b, GpuState &s, const uint32_t *seeds, uint64_t n, cons
         // enqueues the same kernels eagerly every round instead (the
         // reference's SKIP_GRAPH debugging path, gpu_model.rs:1698-1721).
         const bool eager = getenv("RSV_NO_GRAPH") && getenv("RSV_NO_GRAPH")[0] && getenv("RSV_NO_GRAPH")[0] != '0';
-        // Greedy rounds end with one launch that takes the argmax, records
-        // it and gathers its embedding row for the next round, so a round
-        // starts at the layers; the first round's rows are gathered here.
-        if (!sp && rsv_gather_rows_device_f16(c, b->emb_ln, w->x, w->token, I.n_embd, B)) {
+        // A round ends with the token's record and the gather of its
+        // embedding row for the next round (one launch with the argmax when
+        // greedy, one after the sampler otherwise), so a round starts at the
+        // layers; the first round's rows are gathered here.
+        if (rsv_gather_rows_device_f16(c, b->emb_ln, w->x, w->token, I.n_embd, B)) {
             rc = herr("gather: %s", rsv_last_error());
             break;
         }
         auto step = [&]() -> int {
-            int e = decode_step(b, *w, s, sp != nullptr);
+            int e = decode_step(b, *w, s, false);
             if (!e && sp) {
                 if (rsv_sample_into_host_seeded_batch(c, w->logits, w->token, I.vocab, temp, NONE, counter, sampler,
                                                       seq, B))
                     e = herr("sampler: %s", rsv_last_error());
-                else if (rsv_record_tokens(c, w->token, seq, cnt, n, B))
+                else if (rsv_record_gather_batch(c, w->token, seq, cnt, n, b->emb_ln, w->x, I.n_embd, B))
                     e = herr("record: %s", rsv_last_error());
             } else if (!e) {
                 if (rsv_argmax_record_gather_batch(c, w->logits, w->token, I.vocab, seq, cnt, n, b->emb_ln, w->x,

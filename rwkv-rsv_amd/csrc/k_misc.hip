@@ -308,6 +308,34 @@ __global__ void k_record_tokens(const uint32_t *__restrict__ in_tok, uint32_t *_
     cnt[b] = i + 1u;
 }
 
+// k_record_tokens and k_gather_rows of the same tokens in one launch (grid
+// (ceil(c/256), batch)): the tail of a sampled self-loop round.
+__global__ void k_record_gather(const uint32_t *__restrict__ in_tok, uint32_t *__restrict__ out_seq,
+                                uint32_t *__restrict__ cnt, int stride, const void *__restrict__ emb, int emb_f16,
+                                uint64_t emb_rows, float *__restrict__ x, int c) {
+    const int b = blockIdx.y, i = blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t t = in_tok[b];
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        const uint32_t k = cnt[b];
+        if (k < (uint32_t)stride) out_seq[(size_t)b * stride + k] = t;
+        cnt[b] = k + 1u;
+    }
+    if (i >= c) return;
+    const size_t row = t;
+    float v = 0.0f;
+    if (row < emb_rows) v = emb_f16 ? (float)((const _Float16 *)emb)[row * c + i] : ((const float *)emb)[row * c + i];
+    x[(size_t)b * c + i] = v;
+}
+
+int launch_record_gather(rsv_ctx *ctx, const uint32_t *in_tok, uint32_t *out_seq, uint32_t *cnt, int stride,
+                         const void *emb, int emb_f16, uint64_t emb_rows, float *x, int c, int batch) {
+    if (c <= 0 || batch <= 0) return RSV_FAIL("record_gather: bad c=%d batch=%d", c, batch);
+    hipLaunchKernelGGL(k_record_gather, dim3((c + 255) / 256, batch), dim3(256), 0, ctx->stream, in_tok, out_seq,
+                       cnt, stride, emb, emb_f16, emb_rows, x, c);
+    RSV_HIP(hipGetLastError());
+    return 0;
+}
+
 int launch_record_tokens(rsv_ctx *ctx, const uint32_t *in_tok, uint32_t *out_seq, uint32_t *cnt, int stride,
                          int batch) {
     hipLaunchKernelGGL(k_record_tokens, dim3((batch + 255) / 256), dim3(256), 0, ctx->stream, in_tok, out_seq,

@@ -160,6 +160,8 @@ int launch_wkv7_decode(rsv_ctx *ctx, float *s, const float *k, const float *kk, 
 int launch_gather_rows(rsv_ctx *ctx, const void *src, int src_f16, uint64_t src_rows, float *dst,
                        const uint32_t *tok, int c, int batch);
 int launch_argmax(rsv_ctx *ctx, const float *logits, uint32_t *tok, int n, int batch);
+int launch_record_gather(rsv_ctx *ctx, const uint32_t *in_tok, uint32_t *out_seq, uint32_t *cnt, int stride,
+                         const void *emb, int emb_f16, uint64_t emb_rows, float *x, int c, int batch);
 int launch_argmax_next(rsv_ctx *ctx, const float *logits, uint32_t *tok, int n, uint32_t *out_seq, uint32_t *cnt,
                        int stride, const void *emb, int emb_f16, uint64_t emb_rows, float *x, int c, int batch);
 int launch_record_tokens(rsv_ctx *ctx, const uint32_t *in_tok, uint32_t *out_seq, uint32_t *cnt,

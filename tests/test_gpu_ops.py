@@ -626,6 +626,33 @@ def test_argmax_record_gather_equals_three_ops(be):
             assert list(outs[1][2]) == [r + 1] * B
 
 
+def test_record_gather_equals_two_ops(be):
+    """rsv_record_gather_batch against rsv_record_tokens +
+    rsv_gather_rows_device_f16 on the same tokens (one past the table: zero
+    row), F32 and F16 tables, over more rounds than the record row holds."""
+    rsv = _rsv()
+    rng = np.random.default_rng(22)
+    B, c, rows, stride = 4, 2560, 500, 2
+    for dt in (rsv.F32, rsv.F16):
+        tab = be.tensor(rng.standard_normal((rows, c)).astype(np.float32), dtype=dt)
+        bufs = {f: (be.tensor(np.zeros(B * stride, np.uint32), dtype=rsv.U32),
+                    be.tensor(np.zeros(B, np.uint32), dtype=rsv.U32), be.tensor(n=B * c)) for f in (False, True)}
+        for r in range(stride + 1):
+            tok = be.tensor(np.array([r, 499, 500 + r, 7 * r], np.uint32), dtype=rsv.U32)
+            outs = []
+            for fused in (False, True):
+                seq, cnt, x = bufs[fused]
+                if fused:
+                    be.call("rsv_record_gather_batch", tok, seq, cnt, stride, tab, x, c, B)
+                else:
+                    be.call("rsv_record_tokens", tok, seq, cnt, stride, B)
+                    be.call("rsv_gather_rows_device_f16", tab, x, tok, c, B)
+                outs.append([be.get(seq, B * stride, rsv.U32), be.get(cnt, B, rsv.U32), be.get(x, B * c)])
+            for u, v in zip(*outs):
+                assert np.array_equal(u, v)
+            assert np.all(outs[1][2].reshape(B, c)[2] == 0)
+
+
 # ------------------------------------------------------------- sampler
 def _sample_gpu(be, logits, temperature, top_k, top_p, seed, rep=1.0, freq=0.0, pres=0.0, hist=()):
     rsv = _rsv()
