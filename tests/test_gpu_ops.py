@@ -981,7 +981,9 @@ def test_gemv_multi_lnmix_and_side_copy(be, batch):
 
 @pytest.mark.parametrize("batch,k,n", [(16, 1280, 320), (33, 1280, 320), (64, 1280, 320), (100, 1280, 320),
                                        (64, 256, 320), (33, 96, 320), (16, 128, 320), (64, 10240, 320),
-                                       (64, 2560, 8200), (40, 2560, 8200), (20, 2560, 8200)])
+                                       (64, 2560, 8200), (40, 2560, 8200), (20, 2560, 8200),
+                                       (2, 2560, 8200), (12, 2560, 8200), (5, 2560, 320), (9, 1280, 320),
+                                       (8, 2560, 2560)])
 def test_gemm_skinny(be, batch, k, n):
     """Batched-decode MFMA GEMM (fp16 x, int8/fp16 W) against float64 with
     the loader's fp16 rounding of the dequantised weights.  k <= 256 takes the
@@ -989,7 +991,9 @@ def test_gemm_skinny(be, batch, k, n):
     32-row tile over the whole k, or, with more tiles than CUs (n = 8200: 257
     tiles, the last partial and its block's second tile masked), two tiles
     per block sharing the x copies, for 32 and 64 sessions per column tile;
-    longer k (10240) k-slices and the slice-reduction launch."""
+    below 32 sessions only 8*ceil(B/8) sessions' x pieces are copied (B = 2,
+    5, 8, 9, 12, 20); longer k (10240) k-slices and the slice-reduction
+    launch."""
     rsv = _rsv()
     rng = np.random.default_rng(60 + batch + k)
     ki = k if k % 128 == 0 else 128  # int8 needs whole 128-groups
