@@ -266,7 +266,7 @@ def linear_leg():
                     jobs = [rsv.MmJob(NONE if fmt == "int8" else t, ctypes.pointer(t) if fmt == "int8" else None,
                                       n, k, x, y, NONE, 0, NONE, NONE, NONE, 1) for t in tiled]
                     fn = lambda i, jobs=jobs, M=M: be.call("rsv_gemm_skinny", ctypes.byref(jobs[i % ncopy]), 1, M)
-                    kern = "k_skinny4" if n >= 65536 else ("k_skinny8" if k <= 2560 else "k_skinny5")
+                    kern = "k_skinny8" if k <= 2560 else "k_skinny5"
                 elif M > 128:
                     x = be.tensor(xh, dtype=rsv.F16)
                     if fmt == "int8":

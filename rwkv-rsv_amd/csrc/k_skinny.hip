@@ -393,168 +393,6 @@ __global__ __launch_bounds__(256) void k_skinny_reduce(SkinnyJobs jobs, int MB, 
     }
 }
 
-// ------------------------------------------------------------------ v4
-// Same contract with the weights in the MFMA-tiled copy made by
-// launch_tile_weights: a 32-row x 32-column tile is 1 KiB (int8) / 2 KiB
-// (fp16) contiguous, lane l's 16 (32) bytes = row l%32, columns
-// 16*(l/32) .. +15, tiles ordered [row tile][k chunk].  A wave's weight load
-// is one fully contiguous 1 KiB burst per chunk.
-//
-// Block = 4 waves = 4 row tiles (128 rows) on one k-slice; the x slab of a
-// 4-chunk group (batch x 128 columns, fp16) is staged once per block in LDS
-// (double buffered) and shared by the 4 waves.
-template <int MT, bool I8>
-__global__ __launch_bounds__(256) void k_skinny4(SkinnyJobs jobs, int MB, float *__restrict__ ws) {
-    constexpr int TB = MT * 32;
-    constexpr int G = 4;              // chunks per group
-    constexpr int D = I8 ? 3 : 2;     // weight groups in flight per wave
-    constexpr int WV = I8 ? 1 : 2;    // 16-byte loads per lane per chunk
-    constexpr int XS = G * 32 + 8;    // LDS row stride (halves) of the x slab
-    // the x slab double buffer and the output tile are never live together
-    __shared__ __attribute__((aligned(16))) unsigned char smem[2 * TB * XS * 2 > 128 * (TB + 1) * 4
-                                                                  ? 2 * TB * XS * 2 : 128 * (TB + 1) * 4];
-    _Float16 (*xs)[TB][XS] = reinterpret_cast<_Float16 (*)[TB][XS]>(smem);
-    float (*tile)[TB + 1] = reinterpret_cast<float (*)[TB + 1]>(smem);
-    const int bid = blockIdx.x;
-    int ji = 0;
-    while (ji + 1 < jobs.n && bid >= jobs.blk_start[ji + 1]) ji++;
-    const SkinnyJob &J = jobs.j[ji];
-    const int local = bid - jobs.blk_start[ji];
-    const int rg = local / J.split, sl = local - (local / J.split) * J.split;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 5;
-    const int nchunks = J.K / 32;
-    const int ngroups = (nchunks + G - 1) / G;
-    const int per = (ngroups + J.split - 1) / J.split;
-    const int g_lo = sl * per, g_hi = min(ngroups, g_lo + per);
-    const int rt_glob = rg * 4 + wave;  // this wave's row tile
-    const int row = rt_glob * 32 + (lane & 31);
-    constexpr int tbytes = I8 ? 1024 : 2048;
-    const uint8_t *wt = (const uint8_t *)J.w + ((size_t)rt_glob * nchunks) * tbytes + lane * (I8 ? 16 : 32);
-    const bool row_ok = row < J.N;
-    // tiled scale/zero: [row tile][group][32 rows]
-    const uint32_t *szrow = I8 ? J.sz + (size_t)rt_glob * (J.K / 128) * 32 + (lane & 31) : nullptr;
-
-    sk_f16x acc[MT];
-#pragma unroll
-    for (int ct = 0; ct < MT; ct++)
-#pragma unroll
-        for (int e = 0; e < 16; e++) acc[ct][e] = 0.0f;
-
-    sk_u32x4 wr[D][G][WV];
-    uint32_t sr[D][G];
-    sk_u32x4 xr[4];  // x staging: thread t -> session t/4, 32 halves at (t%4)*32
-    const int xb = tid >> 2, xk = (tid & 3) * 32;
-
-    auto load_w = [&](int grp, sk_u32x4 (&w)[G][WV], uint32_t (&sz)[G]) {
-#pragma unroll
-        for (int q = 0; q < G; q++) {
-            const int c = grp * G + q;
-            if (grp < g_hi && c < nchunks && row_ok) {
-                const sk_u32x4 *p = (const sk_u32x4 *)(wt + (size_t)c * tbytes);
-#pragma unroll
-                for (int v = 0; v < WV; v++) w[q][v] = __builtin_nontemporal_load(p + v);
-                if (I8) sz[q] = szrow[(size_t)(c >> 2) * 32];
-            } else {
-#pragma unroll
-                for (int v = 0; v < WV; v++) w[q][v] = (sk_u32x4){0u, 0u, 0u, 0u};
-                sz[q] = 0u;
-            }
-        }
-    };
-    auto load_x = [&](int grp) {
-        const int k0 = grp * G * 32 + xk;
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-            if (xb < MB && k0 + 8 * q < J.K)
-                xr[q] = *(const sk_u32x4 *)(J.x + (size_t)xb * J.ldx + k0 + 8 * q);
-            else
-                xr[q] = (sk_u32x4){0u, 0u, 0u, 0u};
-        }
-    };
-    auto store_x = [&](int buf) {
-        if (xb < TB) {
-#pragma unroll
-            for (int q = 0; q < 4; q++) *(sk_u32x4 *)&xs[buf][xb][xk + 8 * q] = xr[q];
-        }
-    };
-    auto compute = [&](const sk_u32x4 (&w)[G][WV], const uint32_t (&sz)[G], int buf) {
-#pragma unroll
-        for (int q = 0; q < G; q++) {
-            uint32_t wh[8];
-            if (I8) {
-                const float s = sk_h2f(sz[q]), z = sk_h2f(sz[q] >> 16);
-#pragma unroll
-                for (int h = 0; h < 4; h++) {
-                    const uint32_t u = w[q][0][h];
-                    wh[2 * h] = sk_deq2(s, (float)(u & 0xFFu), (float)((u >> 8) & 0xFFu), z);
-                    wh[2 * h + 1] = sk_deq2(s, (float)((u >> 16) & 0xFFu), (float)(u >> 24), z);
-                }
-            } else {
-#pragma unroll
-                for (int h = 0; h < 4; h++) {
-                    wh[h] = w[q][0][h];
-                    wh[4 + h] = w[q][WV - 1][h];
-                }
-            }
-#pragma unroll
-            for (int ct = 0; ct < MT; ct++) {
-                const _Float16 *xp = &xs[buf][ct * 32 + (lane & 31)][q * 32 + 16 * g];
-                const sk_u32x4 x0 = *(const sk_u32x4 *)xp, x1 = *(const sk_u32x4 *)(xp + 8);
-#pragma unroll
-                for (int s2 = 0; s2 < 4; s2++) {
-                    const sk_half4 a = __builtin_bit_cast(sk_half4, (unsigned long long)wh[2 * s2] |
-                                                                        ((unsigned long long)wh[2 * s2 + 1] << 32));
-                    const sk_u32x4 &xx = s2 < 2 ? x0 : x1;
-                    const uint32_t lo = xx[(s2 & 1) * 2], hi = xx[(s2 & 1) * 2 + 1];
-                    const sk_half4 bv =
-                        __builtin_bit_cast(sk_half4, (unsigned long long)lo | ((unsigned long long)hi << 32));
-                    acc[ct] = __builtin_amdgcn_mfma_f32_32x32x8f16(a, bv, acc[ct], 0, 0, 0);
-                }
-            }
-        }
-    };
-
-#pragma unroll
-    for (int d = 0; d < D; d++) load_w(g_lo + d, wr[d], sr[d]);
-    if (g_lo < g_hi) {
-        load_x(g_lo);
-        store_x(0);
-    }
-    __syncthreads();
-    for (int base = g_lo; base < g_hi; base += D) {
-#pragma unroll
-        for (int d = 0; d < D; d++) {
-            const int grp = base + d;
-            if (grp < g_hi) {  // uniform across the block
-                const int buf = (grp - g_lo) & 1;
-                const bool more = grp + 1 < g_hi;
-                if (more) load_x(grp + 1);
-                compute(wr[d], sr[d], buf);
-                load_w(grp + D, wr[d], sr[d]);
-                if (more) store_x(buf ^ 1);
-                __syncthreads();
-            }
-        }
-    }
-
-    // wave w owns tile rows 32w .. 32w+31: acc[ct][e] -> (row 32w + 8*(e/4) + 4g + e%4, col ct*32 + lane%32)
-#pragma unroll
-    for (int ct = 0; ct < MT; ct++)
-#pragma unroll
-        for (int e = 0; e < 16; e++) tile[wave * 32 + 8 * (e >> 2) + 4 * g + (e & 3)][ct * 32 + (lane & 31)] = acc[ct][e];
-    __syncthreads();
-    const int n0 = rg * 128;
-    if (J.split > 1) {
-        float4 *wsp = (float4 *)(ws + ((size_t)J.ws_slot + (size_t)rg * J.split + sl) * 128 * TB);
-        for (int o4 = tid; o4 < 32 * TB; o4 += 256) {
-            const int r = (4 * o4) & 127, b = (4 * o4) >> 7;
-            sk_st4(wsp + o4, make_float4(tile[r][b], tile[r + 1][b], tile[r + 2][b], tile[r + 3][b]));
-        }
-        return;
-    }
-    sk_store_tile<TB>(sk_epi_of(J), tile, n0, MB);
-}
-
 // ------------------------------------------------------------------ v5
 // Batched decode GEMM, weights in the MFMA-tiled copy (see v4).  Block = 4
 // waves = 4 row tiles (128 rows) on one k-slice of J.kslice chunks:
@@ -1088,7 +926,7 @@ __global__ __launch_bounds__(256 * RT) void k_skinny8(SkinnyJobs jobs, int MB) {
     }
 }
 
-// Tiled copy of a weight matrix [n, k] (int8 bytes or fp16) for k_skinny4;
+// Tiled copy of a weight matrix [n, k] (int8 bytes or fp16) for the tiled kernels;
 // rows beyond n (up to the next multiple of 32) are zero.  One thread per
 // 16-byte lane slice.
 __global__ void k_tile_weights(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst, int n, int k, int esz) {
@@ -1111,7 +949,7 @@ __global__ void k_tile_weights(const uint8_t *__restrict__ src, uint8_t *__restr
     }
 }
 
-// Tiled copy of an int8 scale/zero array [n, k/128] for k_skinny4/5:
+// Tiled copy of an int8 scale/zero array [n, k/128] for the tiled kernels:
 // [row tile][group][32 rows], so the 32 rows of a tile read one 128-byte
 // line per group.  Rows beyond n are zero.
 __global__ void k_tile_sz(const uint32_t *__restrict__ src, uint32_t *__restrict__ dst, int n, int groups) {
@@ -1281,31 +1119,6 @@ static int launch_v5(rsv_ctx *ctx, SkinnyJobs &jobs, int MB) {
     return 0;
 }
 
-// k_skinny4 for jobs with at least two 128-row groups per CU (the head):
-// one block per row group over the whole k, no split.
-static int launch_v4(rsv_ctx *ctx, SkinnyJobs &jobs, int MB) {
-    const bool i8 = jobs.j[0].fmt == FMT_I8;
-    int total = 0;
-    for (int i = 0; i < jobs.n; i++) {
-        SkinnyJob &J = jobs.j[i];
-        if ((J.fmt == FMT_I8) != i8) return RSV_FAIL("skinny gemm: mixed formats in one large-job launch");
-        J.split = 1;
-        J.nblk = (J.N + 127) / 128;
-        jobs.blk_start[i] = total;
-        total += J.nblk;
-    }
-    jobs.blk_start[jobs.n] = total;
-    if (MB <= 32) {
-        if (i8) hipLaunchKernelGGL((k_skinny4<1, true>), dim3(total), dim3(256), 0, ctx->stream, jobs, MB, ctx->skinny_ws);
-        else hipLaunchKernelGGL((k_skinny4<1, false>), dim3(total), dim3(256), 0, ctx->stream, jobs, MB, ctx->skinny_ws);
-    } else {
-        if (i8) hipLaunchKernelGGL((k_skinny4<2, true>), dim3(total), dim3(256), 0, ctx->stream, jobs, MB, ctx->skinny_ws);
-        else hipLaunchKernelGGL((k_skinny4<2, false>), dim3(total), dim3(256), 0, ctx->stream, jobs, MB, ctx->skinny_ws);
-    }
-    RSV_HIP(hipGetLastError());
-    return 0;
-}
-
 // Epilogue of k_skinny_sk1 for one epilogue kind: every read operand of the
 // thread's sessions is loaded in one round, then the values are stored.
 template <int EPI, int TB>
@@ -1455,8 +1268,7 @@ static int launch_small(rsv_ctx *ctx, SkinnyJobs &jobs, int MB) {
     return 0;
 }
 
-// Tiled jobs: small k -> k_skinny_sk1; at least two 128-row groups per CU
-// (the head) -> k_skinny4; k of at most SK8_KMAX chunks, a multiple of 64
+// Tiled jobs: small k -> k_skinny_sk1; k of at most SK8_KMAX chunks, a multiple of 64
 // -> k_skinny8 (one block per 32-row tile over the whole k: its x reads
 // stay within 4x the weight bytes, and no k-slice partials are needed);
 // longer k (ffn.value) -> k_skinny5 with k-slices and the slice reduction.
@@ -1478,19 +1290,18 @@ static int launch_slab(rsv_ctx *ctx, SkinnyJobs &jobs, int MB) {
         if (J.tiled != jobs.j[0].tiled) return RSV_FAIL("skinny gemm: jobs mix tiled and row-major weights");
     }
     if (jobs.j[0].tiled) {
-        bool small = true, big = false, v8 = true;
-        const int cus = ctx->sm_count > 0 ? ctx->sm_count : 256;
+        // (the head, 65,536 rows, also runs on k_skinny8: B=8 4.31k -> 4.35k
+        // tok/s against the 128-row-group kernel it had before)
+        bool small = true, v8 = true;
         for (int i = 0; i < jobs.n; i++) {
             const SkinnyJob &J = jobs.j[i];
             small &= J.K <= 32 * SK_SMALL_NCH;
-            big |= (J.N + 127) / 128 >= 2 * cus;
             v8 &= J.K % 64 == 0 && J.K <= 32 * SK8_KMAX;
         }
         bool sliced = false;
         for (int i = 0; i < jobs.n; i++) sliced |= jobs.j[i].wtile_ch != 0;
-        if (sliced && (small || big || !v8)) return RSV_FAIL("skinny gemm: k-slice jobs need 256 < k <= %d, k %% 64 == 0", 32 * SK8_KMAX);
+        if (sliced && (small || !v8)) return RSV_FAIL("skinny gemm: k-slice jobs need 256 < k <= %d, k %% 64 == 0", 32 * SK8_KMAX);
         if (small) return launch_small(ctx, jobs, MB);
-        if (big) return launch_v4(ctx, jobs, MB);
         return v8 ? launch_v8(ctx, jobs, MB) : launch_v5(ctx, jobs, MB);
     }
     // row-major weights (the C-ABI's untiled form): k_skinny + slice reduce
